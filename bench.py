@@ -1,0 +1,191 @@
+#!/usr/bin/env python3
+"""GDN forward + VJP throughput on one MI355X.
+
+A step is one forward of the delta-rule recurrence over a batch of synthetic input plus its full VJP (dq, dk,
+dv, dg, dbeta, dS0), with every input already resident in HBM.  Prints ONE JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+
+Workloads (one GPU; the default is the T=4096 configuration the metric is quoted on):
+  bf16_b4_t4096   B=4, T=4096, Hk=16, Hv=32, D=128, bf16 q/k/v/dO, fp32 state and gates, chunk 64
+  fp32_b1_t4096   B=1, T=4096, same heads, fp32
+  fp32_b1_t2048   B=1, T=2048, fp32, S0 ~ N(0, 0.02), full dS0
+  ckpt_b1_t16384  B=1, T=16384, fp32, snapshots every 256 tokens, peak HBM reported
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "moe-stream-mac_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "GDN fwd+VJP tokens/sec at T=4096 (1 GPU) + % of HBM/MFMA roofline"
+PEAK_HBM_GBS = 8000.0
+PEAK_FP32_TFLOPS = 157.3
+
+WORKLOADS = {
+    "bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0),
+    "fp32_b1_t4096": dict(B=1, T=4096, Hk=16, Hv=32, D=128, dtype="fp32", chunk=64, s0_std=0.0),
+    "fp32_b1_t2048": dict(B=1, T=2048, Hk=16, Hv=32, D=128, dtype="fp32", chunk=64, s0_std=0.02),
+    "ckpt_b1_t16384": dict(B=1, T=16384, Hk=16, Hv=32, D=128, dtype="fp32", chunk=256, s0_std=0.0),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_inputs(w, dev, seed=0):
+    """Synthetic inputs with the measured distributions, generated on the device (seeded)."""
+    import torch
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    B, T, Hk, Hv, D = w["B"], w["T"], w["Hk"], w["Hv"], w["D"]
+    dt = torch.bfloat16 if w["dtype"] == "bf16" else torch.float32
+    n = lambda *s: torch.randn(*s, device=dev, generator=gen)
+    q, k = n(B, T, Hk, D), n(B, T, Hk, D)
+    q = q * (D ** -0.5) * torch.rsqrt((q * q).sum(-1, keepdim=True) + 1e-6)
+    k = k * torch.rsqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+    v = n(B, T, Hv, D)
+    beta = torch.sigmoid(n(B, T, Hv))
+    A_log = torch.empty(Hv, device=dev).uniform_(0.0, float(torch.log(torch.tensor(16.0))), generator=gen)
+    a = n(B, T, Hv)
+    g_log = -torch.exp(A_log) * torch.nn.functional.softplus(a)
+    state = n(B, Hv, D, D) * w["s0_std"] if w["s0_std"] > 0 else torch.zeros(B, Hv, D, D, device=dev)
+    dy = n(B, T, Hv, D)
+    return dict(q=q.to(dt), k=k.to(dt), v=v.to(dt), g_log=g_log.contiguous(), beta=beta.contiguous(),
+                state=state.contiguous(), dy=dy.to(dt))
+
+
+def cpu_info():
+    info = {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "machine": platform.machine()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                info["model"] = line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
+        if os.environ.get(var):
+            info[var] = os.environ[var]
+    return info
+
+
+def cpu_baseline(T_sample=256):
+    """The NumPy oracle (restating tools/gdn_vjp.py _forward + _backward, impl="staged") on a bounded
+    sample: B=1, T_sample tokens, Hk=16, Hv=32, D=128, fp32, chunk 64; median of 3 after one warm-up."""
+    import numpy as np
+    from oracle import gdn_oracle as O
+    d = O.make_inputs(1, T_sample, 16, 32, 128, seed=0)
+    run = lambda: O.gated_delta_chunked_vjp(d["q"], d["k"], d["v"], d["decay"], d["beta"], d["state"], None,
+                                            d["dy"], None, chunk=64)
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    info = cpu_info()
+    return {"value": T_sample / med, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle fwd+VJP, B=1 T={T_sample} Hk=16 Hv=32 D=128 fp32 chunk 64, "
+                      f"median of 3 ({med:.2f} s) after 1 warm-up; elementwise numpy is single-threaded",
+            "host": info}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="bf16_b4_t4096", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=256)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the GDN path here is "
+              "single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import gdn_engine
+    import gdn_lib
+
+    w = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    gdn_lib.load()
+    log(f"bench: workload {args.workload} {w}")
+    x = make_inputs(w, dev)
+    B, T, Hk, Hv, D = w["B"], w["T"], w["Hk"], w["Hv"], w["D"]
+    out_dtype = x["q"].dtype
+    leaves = [x[n].requires_grad_(True) for n in ("q", "k", "v", "g_log", "beta", "state")]
+
+    def step():
+        y, S = gdn_engine.recurrence(x["q"], x["k"], x["v"], x["g_log"], x["beta"], x["state"], None,
+                                     chunk=w["chunk"], log_gate=True, output_dtype=out_dtype)
+        return torch.autograd.grad([y], leaves, [x["dy"]])
+
+    for i in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log("bench: warmup done")
+    torch.cuda.reset_peak_memory_stats(dev)
+    gdn_lib.profile_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    gdn_lib.profile_enable(False)
+    kt = gdn_lib.profile_collect()
+    peak_gib = torch.cuda.max_memory_allocated(dev) / 2 ** 30
+    log(f"bench: timed {args.steps} steps in {elapsed:.3f} s; kernels {kt}")
+
+    tokens = B * T
+    value = tokens * args.steps / elapsed
+    # Dominant kernel: the one with the largest total time.  Algorithmic flops per head-token per state
+    # element: forward 7 (decay, S k, update, S q), backward 20 (the adjoint of tools/gdn_vjp.py:8-21 plus
+    # the residual); recompute is not counted.
+    flops_per_elem = {"rec_fwd": 7, "rec_bwd": 20}
+    dom = max(kt, key=lambda n: kt[n][0])
+    ms, cnt = kt[dom]
+    avg_ms = ms / cnt
+    per_launch = flops_per_elem.get(dom, 0) * B * T * Hv * D * D
+    achieved = per_launch / (avg_ms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None, "kernel": dom,
+                "avg_launch_ms": round(avg_ms, 4),
+                "note": "fp32 VALU arithmetic (packed fp32 disabled); peak is MI355X fp32 157.3 TFLOP/s",
+                "kernels_ms_per_step": {n: round(v[0] / max(v[1], 1) * v[1] / args.steps, 4)
+                                        for n, v in kt.items()}}
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": args.workload, "B": B, "T": T, "Hk": Hk, "Hv": Hv, "Dk": D, "Dv": D,
+                   "chunk": w["chunk"], "inputs": w["dtype"], "state": "fp32", "form": "recurrent",
+                   "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
+        "peak_hbm_gib": round(peak_gib, 3),
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        log("bench: cpu baseline")
+        cb = cpu_baseline(args.cpu_sample)
+        line["cpu_baseline"] = cb
+        line["gpu_over_cpu"] = round(value / cb["value"], 1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

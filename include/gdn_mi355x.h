@@ -1,0 +1,111 @@
+/* gdn_mi355x.h: C ABI of the MI355X (gfx950) Gated DeltaNet forward + VJP engine.
+ *
+ * One delta-rule step per value head h (value head h reads key head h / (Hv/Hk)):
+ *   A = S * decay;  r = v - A k;  delta = beta r;  S~ = A + delta (x) k;  y = S~ q;
+ *   S_next = mask ? S~ : S            (y always reads the candidate S~)
+ * with S the [Dv][Dk] state of one head.  This is the arithmetic of the reference's
+ * tools/gdn_vjp.py:3-25 (_step_parts :238-256) and engine/include/gdn.h:217-226.
+ *
+ * Layouts (all row-major, contiguous):
+ *   q, k    [B][T][Hk][Dk]          dtype in_dtype (GDN_F32 / GDN_BF16 / GDN_F16)
+ *   v       [B][T][Hv][Dv]          dtype in_dtype
+ *   g       [B][T][Hv]   (GDN_GATE_DECAY, GDN_GATE_LOG)   or [B][T][Hv][Dk] (GDN_GATE_DECAY_VEC), fp32
+ *   beta    [B][T][Hv]              fp32
+ *   state   [B][Hv][Dv][Dk]         fp32 (initial state S0; NULL means zeros)
+ *   mask    [B][T]                  uint8, nonzero keeps the candidate state; NULL means all ones
+ *   y, dy   [B][T][Hv][Dv]          dtype out_dtype / dy_dtype
+ * Every pointer is a device pointer owned by the caller; nothing is freed or retained.  Calls are
+ * asynchronous on `stream` (a hipStream_t, NULL = default stream) and never synchronise the host,
+ * except when the environment variable GDN_DEBUG_SYNC=1 asks for a synchronise after every launch.
+ *
+ * Return codes: 0 ok, negative on error; gdn_last_error() returns a message for the calling thread.
+ * This follows the 0 / negative convention of the reference's C API (engine/include/qengine.h:13-14).
+ */
+#ifndef GDN_MI355X_H
+#define GDN_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum gdn_status {
+    GDN_OK = 0,
+    GDN_ERR_INVALID = -1,      /* bad shape, chunk, pointer or enum (reference: ValueError) */
+    GDN_ERR_UNSUPPORTED = -2,  /* valid request this build does not implement (e.g. Dk > 256) */
+    GDN_ERR_WORKSPACE = -3,    /* workspace smaller than gdn_bwd_workspace_bytes() */
+    GDN_ERR_LAUNCH = -4        /* a HIP launch or runtime call failed */
+};
+
+enum gdn_dtype { GDN_F32 = 0, GDN_BF16 = 1, GDN_F16 = 2 };
+
+enum gdn_gate {
+    GDN_GATE_DECAY = 0,      /* g is the multiplicative decay, [B][T][Hv] (reference convention) */
+    GDN_GATE_DECAY_VEC = 1,  /* g is a decay per key channel, [B][T][Hv][Dk] (tools/gdn_vjp.py:174-179) */
+    GDN_GATE_LOG = 2         /* g is the log decay, [B][T][Hv]; dg is returned w.r.t. the log decay */
+};
+
+enum gdn_form {
+    GDN_FORM_AUTO = 0,       /* the engine chooses */
+    GDN_FORM_RECURRENT = 1   /* token-sequential recurrence, state resident in VGPRs */
+};
+
+/* Library version, (major << 16) | minor. */
+int gdn_version(void);
+
+/* Message for the last non-zero status returned on the calling thread ("" if none). */
+const char *gdn_last_error(void);
+
+/* Benchmark support, no counterpart in the reference (which has no kernel-level timing): while enabled,
+ * every launch is bracketed by two HIP events recorded on the launch's stream.  gdn_profile_collect waits
+ * for the recorded events, writes up to max_entries distinct kernel names (name_len bytes each), their
+ * summed milliseconds and launch counts, clears the records and returns the number of entries (< 0 on
+ * error). */
+int gdn_profile_enable(int on);
+int gdn_profile_collect(int max_entries, char *names, int name_len, double *total_ms, int *counts);
+
+/* Number of chunk snapshots gdn_fwd writes: ceil(T / chunk) - 1 states of [B][Hv][Dv][Dk] fp32, the states
+ * at token chunk, 2*chunk, ... (the reference keeps the same boundaries, tools/gdn_vjp.py:205-235; the first
+ * one, S0, is the caller's input and the last one is the returned final state). */
+int64_t gdn_num_snapshots(int T, int chunk);
+
+/* Forward.  Replaces the forward of gated_delta_chunked (tools/gdn_vjp.py:503-528 via _forward :205-235)
+ * and of gated_delta_ops_checkpointed (tools/gdn_checkpoint.py:53-95).
+ * Writes y (out_dtype), state_T (fp32; may be NULL) and, when snapshots is not NULL, the
+ * gdn_num_snapshots(T, chunk) chunk-boundary states.  With snapshots == NULL this is the forward-only path
+ * of frozen layers (tools/frozen_gdn.py:19-25, mlx-lm gated_delta_kernel). */
+int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
+            const float *state0, const uint8_t *mask,
+            void *y, float *state_T, float *snapshots,
+            int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk,
+            int in_dtype, int out_dtype, int gate_kind, int form, void *stream);
+
+/* Device workspace gdn_bwd needs, in bytes (256-byte aligned base expected). */
+size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind,
+                               int form);
+
+/* Backward (VJP).  Replaces _backward / _chunk_vjp / the Metal kernel gdn_chunk_backward
+ * (tools/gdn_vjp.py:273-320, :341-423, :426-474) and the mx.checkpoint recompute of
+ * tools/gdn_checkpoint.py:39-50.  Reads the snapshots written by gdn_fwd with the same chunk, recomputes
+ * the states inside each chunk, and writes
+ *   dq, dk [B][T][Hk][Dk] (grad_dtype; summed over the value heads of each key head, tools/gdn_vjp.py:266-270)
+ *   dv     [B][T][Hv][Dv] (grad_dtype)
+ *   dg     shaped like g, fp32 (w.r.t. the log decay for GDN_GATE_LOG)
+ *   dbeta  [B][T][Hv] fp32
+ *   dstate0 [B][Hv][Dv][Dk] fp32 (may be NULL)
+ * dy has dy_dtype; dstate_T may be NULL (zero cotangent).  Results are deterministic (no atomics). */
+int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
+            const float *state0, const uint8_t *mask, const float *snapshots,
+            const void *dy, const float *dstate_T,
+            void *dq, void *dk, void *dv, float *dg, float *dbeta, float *dstate0,
+            void *workspace, size_t workspace_bytes,
+            int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk,
+            int in_dtype, int dy_dtype, int grad_dtype, int gate_kind, int form, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

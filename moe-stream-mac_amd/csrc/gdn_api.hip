@@ -1,0 +1,260 @@
+// C ABI of the GDN engine (declared in include/gdn_mi355x.h): argument checks, workspace layout, dispatch.
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "gdn_common.h"
+#include "gdn_internal.h"
+#include "../../include/gdn_mi355x.h"
+
+namespace gdn {
+
+static thread_local char g_err[512];
+
+static int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+static bool debug_sync() {
+    static const int on = [] {
+        const char *s = getenv("GDN_DEBUG_SYNC");
+        return s && s[0] == '1';
+    }();
+    return on != 0;
+}
+
+// After a launch: report launch errors, and in debug mode synchronise and report execution errors.
+static int check_launch(hipStream_t st, const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+    if (debug_sync()) {
+        e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "%s: execution failed: %s", what, hipGetErrorString(e));
+    }
+    return GDN_OK;
+}
+
+// Opt-in launch timing (gdn_profile_enable): each launch is bracketed by two HIP events recorded on the
+// launch's own stream.  Off by default; the normal path records nothing.
+struct ProfRec {
+    const char *name;
+    hipEvent_t start, stop;
+};
+static std::mutex g_prof_mu;
+static std::vector<ProfRec> g_prof;
+static bool g_prof_on = false;
+
+struct Timed {
+    const char *name;
+    hipStream_t st;
+    hipEvent_t start = nullptr, stop = nullptr;
+    Timed(const char *n, hipStream_t s) : name(n), st(s) {
+        if (!g_prof_on) return;
+        if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess) {
+            start = stop = nullptr;
+            return;
+        }
+        (void)hipEventRecord(start, st);
+    }
+    ~Timed() {
+        if (!start) return;
+        (void)hipEventRecord(stop, st);
+        std::lock_guard<std::mutex> lk(g_prof_mu);
+        g_prof.push_back({name, start, stop});
+    }
+};
+
+__global__ void copy_or_zero_kernel(float *dst, const float *src, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = src ? src[i] : 0.f;
+}
+
+void launch_copy_or_zero(float *dst, const float *src, size_t n, hipStream_t st) {
+    if (dst && n) hipLaunchKernelGGL(copy_or_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                                     dst, src, n);
+}
+
+static bool dtype_ok(int dt) { return dt == DT_F32 || dt == DT_BF16 || dt == DT_F16; }
+
+static int check_shape(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate, int form) {
+    if (chunk <= 0) return fail(GDN_ERR_INVALID, "chunk must be a positive integer");
+    if (B < 0 || T < 0) return fail(GDN_ERR_INVALID, "batch and timesteps must be non-negative");
+    if (Hk <= 0 || Hv <= 0 || Dk <= 0 || Dv <= 0)
+        return fail(GDN_ERR_INVALID, "head counts and head dims must be positive");
+    if (Hv % Hk != 0) return fail(GDN_ERR_INVALID, "q/k head count must divide the value head count");
+    if (gate != GATE_DECAY && gate != GATE_DECAY_VEC && gate != GATE_LOG)
+        return fail(GDN_ERR_INVALID, "Unsupported gating kind %d", gate);
+    if (form != GDN_FORM_AUTO && form != GDN_FORM_RECURRENT)
+        return fail(GDN_ERR_INVALID, "unknown form %d", form);
+    if (pick_lane_width(Dk) == 0) return fail(GDN_ERR_UNSUPPORTED, "key_dim %d > 256 is not supported", Dk);
+    if (Hv > 65535 || B > 65535) return fail(GDN_ERR_UNSUPPORTED, "batch and value heads must be <= 65535");
+    return GDN_OK;
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct BwdLayout {
+    size_t sub, part_qk, part_gb, part_gv, total;
+};
+
+static BwdLayout bwd_layout(int B, int T, int Hv, int Dk, int Dv, int chunk, int gate) {
+    const size_t nrb = (size_t)rec_num_row_blocks(Dv);
+    const size_t toks = (size_t)B * T * Hv;
+    BwdLayout L;
+    size_t off = 0;
+    L.sub = off;
+    off += align256(rec_sub_floats(B, Hv, Dk, Dv, T, chunk) * sizeof(float));
+    L.part_qk = off;
+    off += align256(nrb * toks * 2 * Dk * sizeof(float));
+    L.part_gb = off;
+    off += align256(nrb * toks * 2 * sizeof(float));
+    L.part_gv = off;
+    if (gate == GATE_DECAY_VEC) off += align256(nrb * toks * Dk * sizeof(float));
+    L.total = off;
+    return L;
+}
+
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" {
+
+int gdn_version(void) { return (1 << 16) | 0; }
+
+int gdn_profile_enable(int on) {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    g_prof_on = on != 0;
+    return GDN_OK;
+}
+
+int gdn_profile_collect(int max_entries, char *names, int name_len, double *total_ms, int *counts) {
+    std::vector<ProfRec> recs;
+    {
+        std::lock_guard<std::mutex> lk(g_prof_mu);
+        recs.swap(g_prof);
+    }
+    std::map<std::string, std::pair<double, int>> agg;
+    int rc = GDN_OK;
+    for (auto &r : recs) {
+        float ms = 0.f;
+        if (hipEventSynchronize(r.stop) == hipSuccess && hipEventElapsedTime(&ms, r.start, r.stop) == hipSuccess) {
+            auto &e = agg[r.name];
+            e.first += ms;
+            e.second += 1;
+        } else {
+            rc = fail(GDN_ERR_LAUNCH, "profiling event failed");
+        }
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+    }
+    if (rc) return rc;
+    int n = 0;
+    for (auto &kv : agg) {
+        if (n >= max_entries) break;
+        snprintf(names + (size_t)n * name_len, name_len, "%s", kv.first.c_str());
+        total_ms[n] = kv.second.first;
+        counts[n] = kv.second.second;
+        ++n;
+    }
+    return n;
+}
+
+const char *gdn_last_error(void) { return g_err; }
+
+int64_t gdn_num_snapshots(int T, int chunk) {
+    if (chunk <= 0 || T <= 0) return 0;
+    return (int64_t)((T + chunk - 1) / chunk) - 1;
+}
+
+int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
+            const float *state0, const uint8_t *mask, void *y, float *state_T, float *snapshots, int B, int T,
+            int Hk, int Hv, int Dk, int Dv, int chunk, int in_dtype, int out_dtype, int gate_kind, int form,
+            void *stream) {
+    g_err[0] = 0;
+    int rc = check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form);
+    if (rc) return rc;
+    if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (B == 0) return GDN_OK;
+    if (T == 0) {
+        launch_copy_or_zero(state_T, state0, (size_t)B * Hv * Dv * Dk, st);
+        return check_launch(st, "gdn_fwd(T=0)");
+    }
+    if (!q || !k || !v || !g || !beta || !y) return fail(GDN_ERR_INVALID, "null input or output pointer");
+    RecFwdArgs a{q, k, v, g, beta, state0, mask, y, state_T, snapshots,
+                 B, T, Hk, Hv, Dk, Dv, chunk, in_dtype, out_dtype, gate_kind};
+    {
+        Timed tm("rec_fwd", st);
+        launch_rec_fwd(a, st);
+    }
+    return check_launch(st, "gdn_fwd");
+}
+
+size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind,
+                               int form) {
+    if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
+    return bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind).total;
+}
+
+int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
+            const float *state0, const uint8_t *mask, const float *snapshots, const void *dy,
+            const float *dstate_T, void *dq, void *dk, void *dv, float *dg, float *dbeta, float *dstate0,
+            void *workspace, size_t workspace_bytes, int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk,
+            int in_dtype, int dy_dtype, int grad_dtype, int gate_kind, int form, void *stream) {
+    g_err[0] = 0;
+    int rc = check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form);
+    if (rc) return rc;
+    if (!dtype_ok(in_dtype) || !dtype_ok(dy_dtype) || !dtype_ok(grad_dtype))
+        return fail(GDN_ERR_INVALID, "unknown dtype code");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (B == 0) return GDN_OK;
+    if (T == 0) {
+        launch_copy_or_zero(dstate0, dstate_T, (size_t)B * Hv * Dv * Dk, st);
+        return check_launch(st, "gdn_bwd(T=0)");
+    }
+    if (!q || !k || !v || !g || !beta || !dy || !dq || !dk || !dv || !dg || !dbeta)
+        return fail(GDN_ERR_INVALID, "null input or output pointer");
+    if (gdn_num_snapshots(T, chunk) > 0 && !snapshots)
+        return fail(GDN_ERR_INVALID, "snapshots from gdn_fwd are required when T > chunk");
+    const BwdLayout L = bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind);
+    if (workspace_bytes < L.total || (L.total && !workspace))
+        return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
+                    workspace_bytes, L.total);
+    char *ws = static_cast<char *>(workspace);
+    RecBwdArgs a{};
+    a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.state0 = state0; a.mask = mask;
+    a.snaps = snapshots; a.dy = dy; a.dstate_T = dstate_T;
+    a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dstate0 = dstate0;
+    a.ws_sub = reinterpret_cast<float *>(ws + L.sub);
+    a.part_qk = reinterpret_cast<float *>(ws + L.part_qk);
+    a.part_gb = reinterpret_cast<float *>(ws + L.part_gb);
+    a.part_gv = reinterpret_cast<float *>(ws + L.part_gv);
+    a.B = B; a.T = T; a.Hk = Hk; a.Hv = Hv; a.Dk = Dk; a.Dv = Dv; a.chunk = chunk;
+    a.in_dt = in_dtype; a.dy_dt = dy_dtype; a.grad_dt = grad_dtype; a.gate = gate_kind;
+    a.nrb = rec_num_row_blocks(Dv);
+    a.max_sub = rec_max_sub(T, chunk);
+    {
+        Timed tm("rec_bwd", st);
+        launch_rec_bwd(a, st);
+    }
+    rc = check_launch(st, "gdn_bwd");
+    if (rc) return rc;
+    {
+        Timed tm("rec_bwd_reduce", st);
+        launch_rec_bwd_reduce(a, st);
+    }
+    return check_launch(st, "gdn_bwd_reduce");
+}
+
+}  // extern "C"

@@ -1,0 +1,61 @@
+// Device helpers shared by the GDN kernels: dtype conversion and wavefront reductions for gfx950.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace gdn {
+
+enum : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
+enum : int { GATE_DECAY = 0, GATE_DECAY_VEC = 1, GATE_LOG = 2 };
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// Round-to-nearest-even float -> bfloat16 (NaN stays a quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// Load element i of a buffer of dtype dt as float.  dt is uniform across the wave.
+__device__ __forceinline__ float load_as_f32(const void *p, size_t i, int dt) {
+    if (dt == DT_F32) return static_cast<const float *>(p)[i];
+    if (dt == DT_BF16) return bf16_to_f32(static_cast<const uint16_t *>(p)[i]);
+    return __half2float(static_cast<const __half *>(p)[i]);
+}
+
+__device__ __forceinline__ void store_from_f32(void *p, size_t i, float x, int dt) {
+    if (dt == DT_F32) {
+        static_cast<float *>(p)[i] = x;
+    } else if (dt == DT_BF16) {
+        static_cast<uint16_t *>(p)[i] = f32_to_bf16(x);
+    } else {
+        static_cast<__half *>(p)[i] = __float2half(x);
+    }
+}
+
+// DPP lane moves inside a row of 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_QUAD_1032 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_2301 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+
+// Sum over the 16 lanes of a DPP row; every lane of the row receives the same (bitwise) total.
+__device__ __forceinline__ float row16_allreduce(float x) {
+    x += dpp_mov<DPP_QUAD_1032>(x);
+    x += dpp_mov<DPP_QUAD_2301>(x);
+    x += dpp_mov<DPP_ROW_HALF_MIRROR>(x);
+    x += dpp_mov<DPP_ROW_MIRROR>(x);
+    return x;
+}
+
+__device__ __forceinline__ float shfl_xor(float x, int mask) { return __shfl_xor(x, mask, 64); }
+
+}  // namespace gdn

@@ -1,0 +1,524 @@
+// Token-sequential ("recurrent") form of the Gated DeltaNet forward and VJP for gfx950.
+//
+// Work split.  The rows of the [Dv][Dk] state are independent in the forward (engine/include/gdn.h:226), so a
+// workgroup owns one (batch, value head, block of 16 value rows).  Each row lives in the VGPRs of one DPP row
+// of 16 lanes, E = Dk/16 key channels per lane; row dot products (S k, S q, dS~ k) are 4-step DPP all-reduces
+// with no LDS traffic and no barriers.  Per-token inputs are staged through LDS in tiles.
+//
+// Backward.  Reverse-time adjoint of tools/gdn_vjp.py:8-21 (_chunk_vjp :273-320).  The states inside a chunk
+// are never stored: for each chunk the workgroup reloads the chunk-start snapshot written by the forward,
+// replays the chunk once to write sub-chunk starts (every CS tokens) to a small workspace, then for each
+// sub-chunk in reverse replays CS steps keeping S_{t-1} of its rows in VGPRs (fully unrolled), and walks them
+// backward.  Cross-row sums (dq, dk, dg, dbeta) are reduced in-wave (xor shuffles), across the 4 waves in LDS,
+// and across row blocks and the GQA head group by a second, deterministic kernel — no atomics.
+#include "gdn_common.h"
+#include "gdn_internal.h"
+
+namespace gdn {
+
+constexpr int ROWS = 16;      // value rows per workgroup (16 DPP rows of 16 lanes)
+constexpr int THREADS = 256;  // 4 wave64
+constexpr int FWD_TT = 16;    // tokens per LDS tile in the forward
+constexpr int BWD_CS = 8;     // tokens per register-resident sub-chunk in the backward
+
+template <int E, bool VEC, int TT>
+struct StageBuf {
+    static constexpr int DKP = 16 * E;
+    float k[TT][DKP];
+    float q[TT][DKP];
+    float g[TT][VEC ? DKP : 1];
+    float v[TT][ROWS];
+    float dy[TT][ROWS];
+    float beta[TT];
+    float m[TT];
+};
+
+// Stage tokens [t0, t0+n) of head (b, hv), rows [rb*16, rb*16+16) into LDS as fp32.  Slots past n and
+// channels past Dk are zero (decay 1), so padded lanes carry exact zeros through every step.
+template <int E, bool VEC, int TT, bool WITH_DY>
+__device__ __forceinline__ void stage_tokens(StageBuf<E, VEC, TT> &sb, const void *q, const void *k,
+                                             const void *v, const float *g, const float *beta,
+                                             const uint8_t *mask, const void *dy, int b, int hv, int hk,
+                                             int rb, int t0, int n, int T, int Hk, int Hv, int Dk, int Dv,
+                                             int in_dt, int dy_dt, int gate) {
+    constexpr int DKP = 16 * E;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < TT * DKP; i += THREADS) {
+        const int tt = i / DKP, j = i - tt * DKP;
+        float kv = 0.f, qv = 0.f, gv = 1.f;
+        if (tt < n && j < Dk) {
+            const size_t idx = (((size_t)b * T + t0 + tt) * Hk + hk) * Dk + j;
+            kv = load_as_f32(k, idx, in_dt);
+            qv = load_as_f32(q, idx, in_dt);
+            if (VEC) gv = g[(((size_t)b * T + t0 + tt) * Hv + hv) * Dk + j];
+        }
+        sb.k[tt][j] = kv;
+        sb.q[tt][j] = qv;
+        if (VEC) sb.g[tt][j] = gv;
+    }
+    for (int i = tid; i < TT * ROWS; i += THREADS) {
+        const int tt = i / ROWS, r = i - tt * ROWS, rr = rb * ROWS + r;
+        float vv = 0.f, dd = 0.f;
+        if (tt < n && rr < Dv) {
+            const size_t idx = (((size_t)b * T + t0 + tt) * Hv + hv) * Dv + rr;
+            vv = load_as_f32(v, idx, in_dt);
+            if (WITH_DY) dd = load_as_f32(dy, idx, dy_dt);
+        }
+        sb.v[tt][r] = vv;
+        if (WITH_DY) sb.dy[tt][r] = dd;
+    }
+    if (tid < TT) {
+        const int tt = tid;
+        float bt = 0.f, gt = 1.f, mt = 1.f;
+        if (tt < n) {
+            const size_t gi = ((size_t)b * T + t0 + tt) * Hv + hv;
+            bt = beta[gi];
+            if (!VEC) {
+                gt = g[gi];
+                if (gate == GATE_LOG) gt = expf(gt);
+            }
+            if (mask) mt = mask[(size_t)b * T + t0 + tt] ? 1.f : 0.f;
+        }
+        sb.beta[tt] = bt;
+        if (!VEC) sb.g[tt][0] = gt;
+        sb.m[tt] = mt;
+    }
+}
+
+template <int E>
+__device__ __forceinline__ void lds_vec(float (&dst)[E], const float *src) {
+    if constexpr (E % 4 == 0) {
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+            const float4 x = *reinterpret_cast<const float4 *>(src + e);
+            dst[e] = x.x; dst[e + 1] = x.y; dst[e + 2] = x.z; dst[e + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) dst[e] = src[e];
+    }
+}
+
+// One forward step of one state row held as E channels per lane.  Returns the residual r = v - A k and
+// leaves the candidate S~ in cand.
+template <int E, bool VEC, int TT>
+__device__ __forceinline__ float row_step(const StageBuf<E, VEC, TT> &sb, int tt, int grp, int c,
+                                          const float (&S)[E], float (&cand)[E], float (&kk)[E],
+                                          float &delta) {
+    float dec[E];
+    lds_vec<E>(kk, &sb.k[tt][c * E]);
+    if (VEC) {
+        lds_vec<E>(dec, &sb.g[tt][c * E]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) dec[e] = sb.g[tt][0];
+    }
+    float A[E];
+    float kv = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        A[e] = S[e] * dec[e];
+        kv = fmaf(A[e], kk[e], kv);
+    }
+    kv = row16_allreduce(kv);
+    const float r = sb.v[tt][grp] - kv;
+    delta = r * sb.beta[tt];
+#pragma unroll
+    for (int e = 0; e < E; ++e) cand[e] = fmaf(delta, kk[e], A[e]);
+    return r;
+}
+
+// ---------------------------------------------------------------------------------------------------- forward
+
+template <int E, bool VEC>
+__global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
+    __shared__ __align__(16) StageBuf<E, VEC, FWD_TT> sb;
+    __shared__ float s_y[FWD_TT][ROWS];
+
+    const int rb = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, grp = tid >> 4, c = tid & 15;
+    const int row = rb * ROWS + grp;
+    const bool row_ok = row < a.Dv;
+    const int hk = hv / (a.Hv / a.Hk);
+    const int T = a.T, Dk = a.Dk, Dv = a.Dv;
+    const size_t state_elems = (size_t)a.B * a.Hv * Dv * Dk;
+    const size_t row_off = (((size_t)b * a.Hv + hv) * Dv + row) * Dk;
+
+    float S[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int j = c * E + e;
+        S[e] = (a.state0 && row_ok && j < Dk) ? a.state0[row_off + j] : 0.f;
+    }
+    int until_snap = a.chunk;  // tokens left before the next chunk boundary
+    for (int t0 = 0; t0 < T; t0 += FWD_TT) {
+        const int n = min(FWD_TT, T - t0);
+        __syncthreads();
+        stage_tokens<E, VEC, FWD_TT, false>(sb, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb,
+                                            t0, n, T, a.Hk, a.Hv, Dk, Dv, a.in_dt, 0, a.gate);
+        __syncthreads();
+        for (int tt = 0; tt < n; ++tt) {
+            float cand[E], kk[E], qq[E], delta;
+            row_step<E, VEC, FWD_TT>(sb, tt, grp, c, S, cand, kk, delta);
+            lds_vec<E>(qq, &sb.q[tt][c * E]);
+            float y = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) y = fmaf(cand[e], qq[e], y);
+            y = row16_allreduce(y);
+            if (sb.m[tt] != 0.f) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) S[e] = cand[e];
+            }
+            if (c == 0) s_y[tt][grp] = y;
+            if (--until_snap == 0) {
+                until_snap = a.chunk;
+                const int t = t0 + tt;
+                if (a.snaps && t + 1 < T && row_ok) {
+                    float *dst = a.snaps + (size_t)((t + 1) / a.chunk - 1) * state_elems + row_off;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        const int j = c * E + e;
+                        if (j < Dk) dst[j] = S[e];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        for (int i = tid; i < n * ROWS; i += THREADS) {
+            const int tt = i / ROWS, r = i - tt * ROWS, rr = rb * ROWS + r;
+            if (rr < Dv)
+                store_from_f32(a.y, (((size_t)b * T + t0 + tt) * a.Hv + hv) * Dv + rr, s_y[tt][r], a.out_dt);
+        }
+    }
+    if (a.state_T && row_ok) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int j = c * E + e;
+            if (j < Dk) a.state_T[row_off + j] = S[e];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------- backward
+
+template <int E, bool VEC>
+__global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
+    constexpr int CS = BWD_CS;
+    constexpr int DKP = 16 * E;
+    constexpr int NQ = VEC ? 3 : 2;
+    __shared__ __align__(16) StageBuf<E, VEC, CS> sb;
+    __shared__ float s_red[CS][4][NQ * DKP];  // per-wave sums over its 4 rows: dq | dk | (dg per channel)
+    __shared__ float s_row[CS][ROWS][3];      // per row: dv, dbeta, dg (scalar gate)
+
+    const int rb = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, grp = tid >> 4, c = tid & 15, wave = tid >> 6, gw = grp & 3;
+    const int row = rb * ROWS + grp;
+    const bool row_ok = row < a.Dv;
+    const int hk = hv / (a.Hv / a.Hk);
+    const int T = a.T, Dk = a.Dk, Dv = a.Dv, B = a.B, Hv = a.Hv;
+    const size_t state_elems = (size_t)B * Hv * Dv * Dk;
+    const size_t row_off = (((size_t)b * Hv + hv) * Dv + row) * Dk;
+    float *ws = a.ws_sub + ((((size_t)b * Hv + hv) * a.nrb + rb) * a.max_sub) * ROWS * DKP + grp * DKP + c * E;
+
+    float dS[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int j = c * E + e;
+        dS[e] = (a.dstate_T && row_ok && j < Dk) ? a.dstate_T[row_off + j] : 0.f;
+    }
+    const int nch = (T + a.chunk - 1) / a.chunk;
+    for (int ci = nch - 1; ci >= 0; --ci) {
+        const int cs = ci * a.chunk, ce = min(T, cs + a.chunk);
+        const int nsub = (ce - cs + CS - 1) / CS;
+        const float *start = ci == 0 ? a.state0 : a.snaps + (size_t)(ci - 1) * state_elems;
+        float S[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int j = c * E + e;
+            S[e] = (start && row_ok && j < Dk) ? start[row_off + j] : 0.f;
+        }
+        // Replay the chunk once, recording the state at each sub-chunk start (1 .. nsub-1).
+        for (int si = 0; si < nsub - 1; ++si) {
+            __syncthreads();
+            stage_tokens<E, VEC, CS, false>(sb, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb,
+                                            cs + si * CS, CS, T, a.Hk, Hv, Dk, Dv, a.in_dt, 0, a.gate);
+            __syncthreads();
+#pragma unroll
+            for (int s = 0; s < CS; ++s) {
+                float cand[E], kk[E], delta;
+                row_step<E, VEC, CS>(sb, s, grp, c, S, cand, kk, delta);
+                if (sb.m[s] != 0.f) {
+#pragma unroll
+                    for (int e = 0; e < E; ++e) S[e] = cand[e];
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < E; ++e) ws[(size_t)si * ROWS * DKP + e] = S[e];
+        }
+        // Sub-chunks in reverse.
+        for (int si = nsub - 1; si >= 0; --si) {
+            const int ss = cs + si * CS, n = min(CS, ce - ss);
+            if (si == 0) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int j = c * E + e;
+                    S[e] = (start && row_ok && j < Dk) ? start[row_off + j] : 0.f;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) S[e] = ws[(size_t)(si - 1) * ROWS * DKP + e];
+            }
+            __syncthreads();
+            stage_tokens<E, VEC, CS, true>(sb, a.q, a.k, a.v, a.g, a.beta, a.mask, a.dy, b, hv, hk, rb, ss, n,
+                                           T, a.Hk, Hv, Dk, Dv, a.in_dt, a.dy_dt, a.gate);
+            __syncthreads();
+            float hist[CS][E];
+            float rh[CS];
+#pragma unroll
+            for (int s = 0; s < CS; ++s) {
+                if (s < n) {
+                    float cand[E], kk[E], delta;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) hist[s][e] = S[e];
+                    rh[s] = row_step<E, VEC, CS>(sb, s, grp, c, S, cand, kk, delta);
+                    if (sb.m[s] != 0.f) {
+#pragma unroll
+                        for (int e = 0; e < E; ++e) S[e] = cand[e];
+                    }
+                }
+            }
+#pragma unroll
+            for (int s = CS - 1; s >= 0; --s) {
+                if (s < n) {
+                    float kk[E], qq[E], dec[E];
+                    lds_vec<E>(kk, &sb.k[s][c * E]);
+                    lds_vec<E>(qq, &sb.q[s][c * E]);
+                    if (VEC) {
+                        lds_vec<E>(dec, &sb.g[s][c * E]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < E; ++e) dec[e] = sb.g[s][0];
+                    }
+                    const float dyr = sb.dy[s][grp], bt = sb.beta[s], r = rh[s], delta = r * bt;
+                    const bool keep = sb.m[s] != 0.f;
+                    float dSc[E];
+                    float u = 0.f;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        dSc[e] = fmaf(dyr, qq[e], keep ? dS[e] : 0.f);
+                        u = fmaf(dSc[e], kk[e], u);
+                    }
+                    u = row16_allreduce(u);
+                    const float ev = bt * u;
+                    float pq[E], pk[E], pg[E];
+                    float dgl = 0.f;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        const float A = hist[s][e] * dec[e];
+                        const float cand = fmaf(delta, kk[e], A);
+                        pq[e] = dyr * cand;
+                        pk[e] = fmaf(dSc[e], delta, -ev * A);
+                        const float dA = fmaf(-ev, kk[e], dSc[e]);
+                        if (VEC) pg[e] = dA * hist[s][e];
+                        else dgl = fmaf(dA, hist[s][e], dgl);
+                        dS[e] = fmaf(dA, dec[e], keep ? 0.f : dS[e]);
+                    }
+                    if (!VEC) dgl = row16_allreduce(dgl);
+                    if (c == 0) {
+                        s_row[s][grp][0] = ev;
+                        s_row[s][grp][1] = u * r;
+                        s_row[s][grp][2] = dgl;
+                    }
+                    // Sum dq / dk over the 4 rows of this wave: halve the vector at each exchange so every
+                    // lane ends with E/2 fully reduced values.
+                    const int h = gw & 1;
+                    float W[E];
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        const float mine = h ? pk[e] : pq[e];
+                        const float other = h ? pq[e] : pk[e];
+                        W[e] = mine + shfl_xor(other, 16);
+                    }
+                    if constexpr (E >= 2) {
+                        constexpr int H = E / 2;
+                        const int h2 = gw >> 1;
+#pragma unroll
+                        for (int e = 0; e < H; ++e) {
+                            const float mine = h2 ? W[H + e] : W[e];
+                            const float other = h2 ? W[e] : W[H + e];
+                            s_red[s][wave][h * DKP + c * E + h2 * H + e] = mine + shfl_xor(other, 32);
+                        }
+                    } else {
+                        const float x = W[0] + shfl_xor(W[0], 32);
+                        if ((gw >> 1) == 0) s_red[s][wave][h * DKP + c] = x;
+                    }
+                    if constexpr (VEC) {
+#pragma unroll
+                        for (int e = 0; e < E; ++e) {
+                            float x = pg[e] + shfl_xor(pg[e], 16);
+                            x += shfl_xor(x, 32);
+                            if (gw == 0) s_red[s][wave][2 * DKP + c * E + e] = x;
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            // Write this workgroup's partial sums for tokens [ss, ss+n).
+            for (int i = tid; i < n * NQ * Dk; i += THREADS) {
+                const int s = i / (NQ * Dk), rem = i - s * NQ * Dk, which = rem / Dk, j = rem - which * Dk;
+                const float sum = (s_red[s][0][which * DKP + j] + s_red[s][1][which * DKP + j]) +
+                                  (s_red[s][2][which * DKP + j] + s_red[s][3][which * DKP + j]);
+                const size_t tok = (((size_t)rb * B + b) * T + ss + s) * Hv + hv;
+                if (which < 2) a.part_qk[tok * 2 * Dk + which * Dk + j] = sum;
+                else a.part_gv[tok * Dk + j] = sum;
+            }
+            for (int i = tid; i < n * ROWS; i += THREADS) {
+                const int s = i / ROWS, r = i - s * ROWS, rr = rb * ROWS + r;
+                if (rr < Dv)
+                    store_from_f32(a.dv, (((size_t)b * T + ss + s) * Hv + hv) * Dv + rr, s_row[s][r][0],
+                                   a.grad_dt);
+            }
+            if (tid < n) {
+                const int s = tid;
+                float db = 0.f, dg = 0.f;
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) {
+                    db += s_row[s][r][1];
+                    dg += s_row[s][r][2];
+                }
+                const size_t tok = (((size_t)rb * B + b) * T + ss + s) * Hv + hv;
+                a.part_gb[tok * 2 + 0] = db;
+                a.part_gb[tok * 2 + 1] = dg;
+            }
+        }
+    }
+    if (a.dstate0 && row_ok) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int j = c * E + e;
+            if (j < Dk) a.dstate0[row_off + j] = dS[e];
+        }
+    }
+}
+
+// Sum the per-row-block partials over row blocks and over the value heads of each key head.
+__global__ __launch_bounds__(256) void rec_bwd_reduce_qk(RecBwdArgs a) {
+    const size_t total = (size_t)a.B * a.T * a.Hk * a.Dk;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const int j = (int)(i % a.Dk);
+    const size_t bth = i / a.Dk;
+    const int hk = (int)(bth % a.Hk);
+    const size_t bt = bth / a.Hk;
+    const int rep = a.Hv / a.Hk;
+    const size_t BT = (size_t)a.B * a.T;
+    float sq = 0.f, sk = 0.f;
+    for (int rb = 0; rb < a.nrb; ++rb) {
+        for (int r = 0; r < rep; ++r) {
+            const size_t tok = ((size_t)rb * BT + bt) * a.Hv + hk * rep + r;
+            sq += a.part_qk[tok * 2 * a.Dk + j];
+            sk += a.part_qk[tok * 2 * a.Dk + a.Dk + j];
+        }
+    }
+    store_from_f32(a.dq, i, sq, a.grad_dt);
+    store_from_f32(a.dk, i, sk, a.grad_dt);
+}
+
+__global__ __launch_bounds__(256) void rec_bwd_reduce_gates(RecBwdArgs a) {
+    const size_t BT = (size_t)a.B * a.T;
+    const size_t total = BT * a.Hv * (a.gate == GATE_DECAY_VEC ? a.Dk : 1);
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    if (a.gate == GATE_DECAY_VEC) {
+        float s = 0.f;
+        for (int rb = 0; rb < a.nrb; ++rb) s += a.part_gv[(size_t)rb * BT * a.Hv * a.Dk + i];
+        a.dg[i] = s;
+        if (i % a.Dk == 0) {
+            const size_t tok = i / a.Dk;
+            float db = 0.f;
+            for (int rb = 0; rb < a.nrb; ++rb) db += a.part_gb[((size_t)rb * BT * a.Hv + tok) * 2];
+            a.dbeta[tok] = db;
+        }
+        return;
+    }
+    float db = 0.f, dg = 0.f;
+    for (int rb = 0; rb < a.nrb; ++rb) {
+        const size_t tok = (size_t)rb * BT * a.Hv + i;
+        db += a.part_gb[tok * 2 + 0];
+        dg += a.part_gb[tok * 2 + 1];
+    }
+    if (a.gate == GATE_LOG) dg *= expf(a.g[i]);
+    a.dbeta[i] = db;
+    a.dg[i] = dg;
+}
+
+// ---------------------------------------------------------------------------------------------------- dispatch
+
+int pick_lane_width(int Dk) {
+    if (Dk <= 16) return 1;
+    if (Dk <= 32) return 2;
+    if (Dk <= 64) return 4;
+    if (Dk <= 128) return 8;
+    if (Dk <= 256) return 16;
+    return 0;
+}
+
+int rec_num_row_blocks(int Dv) { return (Dv + ROWS - 1) / ROWS; }
+
+int rec_max_sub(int T, int chunk) {
+    const int span = chunk < T ? chunk : T;
+    const int ns = (span + BWD_CS - 1) / BWD_CS - 1;
+    return ns > 0 ? ns : 0;
+}
+
+size_t rec_sub_floats(int B, int Hv, int Dk, int Dv, int T, int chunk) {
+    const int E = pick_lane_width(Dk);
+    return (size_t)B * Hv * rec_num_row_blocks(Dv) * rec_max_sub(T, chunk) * ROWS * 16 * E;
+}
+
+template <int E>
+static void launch_fwd_e(const RecFwdArgs &a, hipStream_t st) {
+    dim3 grid(rec_num_row_blocks(a.Dv), a.Hv, a.B);
+    if (a.gate == GATE_DECAY_VEC)
+        hipLaunchKernelGGL((rec_fwd_kernel<E, true>), grid, dim3(THREADS), 0, st, a);
+    else
+        hipLaunchKernelGGL((rec_fwd_kernel<E, false>), grid, dim3(THREADS), 0, st, a);
+}
+
+void launch_rec_fwd(const RecFwdArgs &a, hipStream_t st) {
+    switch (pick_lane_width(a.Dk)) {
+        case 1: launch_fwd_e<1>(a, st); break;
+        case 2: launch_fwd_e<2>(a, st); break;
+        case 4: launch_fwd_e<4>(a, st); break;
+        case 8: launch_fwd_e<8>(a, st); break;
+        default: launch_fwd_e<16>(a, st); break;
+    }
+}
+
+template <int E>
+static void launch_bwd_e(const RecBwdArgs &a, hipStream_t st) {
+    dim3 grid(rec_num_row_blocks(a.Dv), a.Hv, a.B);
+    if (a.gate == GATE_DECAY_VEC)
+        hipLaunchKernelGGL((rec_bwd_kernel<E, true>), grid, dim3(THREADS), 0, st, a);
+    else
+        hipLaunchKernelGGL((rec_bwd_kernel<E, false>), grid, dim3(THREADS), 0, st, a);
+}
+
+void launch_rec_bwd(const RecBwdArgs &a, hipStream_t st) {
+    switch (pick_lane_width(a.Dk)) {
+        case 1: launch_bwd_e<1>(a, st); break;
+        case 2: launch_bwd_e<2>(a, st); break;
+        case 4: launch_bwd_e<4>(a, st); break;
+        case 8: launch_bwd_e<8>(a, st); break;
+        default: launch_bwd_e<16>(a, st); break;
+    }
+}
+
+void launch_rec_bwd_reduce(const RecBwdArgs &a, hipStream_t st) {
+    const size_t nqk = (size_t)a.B * a.T * a.Hk * a.Dk;
+    const size_t ng = (size_t)a.B * a.T * a.Hv * (a.gate == GATE_DECAY_VEC ? a.Dk : 1);
+    if (nqk) hipLaunchKernelGGL(rec_bwd_reduce_qk, dim3((unsigned)((nqk + 255) / 256)), dim3(256), 0, st, a);
+    if (ng) hipLaunchKernelGGL(rec_bwd_reduce_gates, dim3((unsigned)((ng + 255) / 256)), dim3(256), 0, st, a);
+}
+
+}  // namespace gdn

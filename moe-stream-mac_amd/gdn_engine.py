@@ -1,0 +1,169 @@
+"""torch.autograd bridge to the HIP engine: one Function whose forward runs ``gdn_fwd`` (saving chunk
+snapshots) and whose backward runs ``gdn_bwd``.
+
+This is the device-side replacement of the reference's ``mx.custom_function`` pair
+(``tools/gdn_vjp.py:477-500``): the forward keeps ceil(T/chunk)-1 boundary states (the reference keeps
+ceil(T/chunk)+1 including S0 and S_T, ``:205-235``), and the backward recomputes every state inside a
+chunk from its boundary, like ``_chunk_vjp`` (``:273-320``) and ``mx.checkpoint`` in
+``tools/gdn_checkpoint.py:39-50``.  Tensors must live on a ROCm device; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+import gdn_lib as L
+
+
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError("the GDN engine runs on a ROCm GPU only; got tensors on " + str(dev))
+    for t in tensors:
+        if t is not None and t.device != dev:
+            raise ValueError("all GDN inputs must be on the same device")
+    return dev
+
+
+def gate_kind_for(g: torch.Tensor, log_gate: bool) -> int:
+    if g.dim() == 3:
+        return L.GATE_LOG if log_gate else L.GATE_DECAY
+    if g.dim() == 4:
+        if log_gate:
+            raise ValueError("log-space gates must be scalar per head, [B,T,Hv]")
+        return L.GATE_DECAY_VEC
+    raise ValueError(f"Unsupported gating shape {tuple(g.shape)}")
+
+
+class _GDNRecurrence(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, state, mask, chunk, log_gate, out_dtype, need_snapshots):
+        dev = _require_device(q, k, v, g, beta, state)
+        B, T, Hk, Dk = q.shape
+        Hv, Dv = v.shape[2], v.shape[3]
+        in_dtype = q.dtype
+        gate = gate_kind_for(g, log_gate)
+        y = torch.empty((B, T, Hv, Dv), device=dev, dtype=out_dtype)
+        state_T = torch.empty((B, Hv, Dv, Dk), device=dev, dtype=torch.float32)
+        lib = L.load()
+        n_snap = int(lib.gdn_num_snapshots(T, chunk)) if need_snapshots else 0
+        snaps = torch.empty((max(n_snap, 0), B, Hv, Dv, Dk), device=dev, dtype=torch.float32)
+        L.check(lib.gdn_fwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), L.ptr(state),
+                            L.ptr(mask), L.ptr(y), L.ptr(state_T), L.ptr(snaps) if n_snap else None,
+                            B, T, Hk, Hv, Dk, Dv, chunk, L.DTYPE_CODE[in_dtype], L.DTYPE_CODE[out_dtype],
+                            gate, L.FORM_AUTO, L.stream_handle(dev)))
+        ctx.save_for_backward(q, k, v, g, beta, state, mask, snaps)
+        ctx.meta = (chunk, gate)
+        ctx.mark_non_differentiable()
+        return y, state_T
+
+    @staticmethod
+    def backward(ctx, dy, dstate_T):
+        q, k, v, g, beta, state, mask, snaps = ctx.saved_tensors
+        chunk, gate = ctx.meta
+        dev = q.device
+        B, T, Hk, Dk = q.shape
+        Hv, Dv = v.shape[2], v.shape[3]
+        lib = L.load()
+        if dy is None:
+            dy = torch.zeros((B, T, Hv, Dv), device=dev, dtype=torch.float32)
+        dy = dy.contiguous()
+        if dy.dtype not in L.DTYPE_CODE:
+            dy = dy.float()
+        dstate_T = None if dstate_T is None else dstate_T.contiguous().float()
+        grad_dtype = q.dtype
+        dq = torch.empty((B, T, Hk, Dk), device=dev, dtype=grad_dtype)
+        dk = torch.empty_like(dq)
+        dv = torch.empty((B, T, Hv, Dv), device=dev, dtype=grad_dtype)
+        dg = torch.empty(g.shape, device=dev, dtype=torch.float32)
+        dbeta = torch.empty((B, T, Hv), device=dev, dtype=torch.float32)
+        dS0 = torch.empty((B, Hv, Dv, Dk), device=dev, dtype=torch.float32)
+        ws_bytes = int(lib.gdn_bwd_workspace_bytes(B, T, Hk, Hv, Dk, Dv, chunk, gate, L.FORM_AUTO))
+        ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+        L.check(lib.gdn_bwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), L.ptr(state), L.ptr(mask),
+                            L.ptr(snaps) if snaps.numel() else None, L.ptr(dy), L.ptr(dstate_T),
+                            L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(dg), L.ptr(dbeta), L.ptr(dS0),
+                            L.ptr(ws), ws_bytes, B, T, Hk, Hv, Dk, Dv, chunk,
+                            L.DTYPE_CODE[q.dtype], L.DTYPE_CODE[dy.dtype], L.DTYPE_CODE[grad_dtype], gate,
+                            L.FORM_AUTO, L.stream_handle(dev)))
+        return dq, dk, dv, dg, dbeta, dS0, None, None, None, None, None
+
+
+def _prep(q, k, v, g, beta, state, mask):
+    common = torch.promote_types(torch.promote_types(q.dtype, k.dtype), v.dtype)
+    if common not in L.DTYPE_CODE:
+        common = torch.float32
+    q, k, v = (x.to(common).contiguous() for x in (q, k, v))
+    g = g.to(torch.float32).contiguous()
+    beta = beta.to(torch.float32).contiguous()
+    state = state.to(torch.float32).contiguous()
+    if mask is not None:
+        mask = mask.to(device=q.device, dtype=torch.uint8).contiguous()
+    return q, k, v, g, beta, state, mask
+
+
+def check_shapes(q, k, v, g, beta, state, mask) -> None:
+    """Shape checks raising the reference's exception types."""
+    if q.dim() != 4 or k.shape != q.shape:
+        raise ValueError("q and k must both be [B, T, Hk, Dk]")
+    B, T, Hk, Dk = q.shape
+    if v.dim() != 4 or v.shape[:2] != (B, T):
+        raise ValueError("v must be [B, T, Hv, Dv]")
+    Hv, Dv = v.shape[2], v.shape[3]
+    if Hv % Hk:
+        raise ValueError("q/k head count must divide the value head count")
+    if g.dim() not in (3, 4):
+        raise ValueError(f"Unsupported gating shape {tuple(g.shape)}")
+    want_g = (B, T, Hv) if g.dim() == 3 else (B, T, Hv, Dk)
+    if tuple(g.shape) != want_g:
+        raise ValueError(f"Unsupported gating shape {tuple(g.shape)}")
+    if tuple(beta.shape) != (B, T, Hv):
+        raise ValueError("beta must be [B, T, Hv]")
+    if tuple(state.shape) != (B, Hv, Dv, Dk):
+        raise ValueError("state must be [B, Hv, Dv, Dk]")
+    if mask is not None and tuple(mask.shape) != (B, T):
+        raise ValueError("mask must be [B, T]")
+
+
+def recurrence(q, k, v, g, beta, state, mask=None, chunk: int = 64, log_gate: bool = False,
+               output_dtype: Optional[torch.dtype] = None, need_grad: Optional[bool] = None):
+    """(y, final_state) of the delta-rule recurrence with a HIP forward and VJP.
+
+    ``g`` is the multiplicative decay ([B,T,Hv] or [B,T,Hv,Dk]) or, with ``log_gate``, the log decay.
+    ``y`` defaults to the dtype the reference's arithmetic promotes to (fp32 with an fp32 state).
+    ``need_grad=False`` runs the forward-only path (no snapshots, no autograd graph).
+    """
+    if chunk <= 0:
+        raise ValueError("chunk must be a positive integer")
+    check_shapes(q, k, v, g, beta, state, mask)
+    _require_device(q, k, v, g, beta, state)
+    out_dtype = output_dtype
+    if out_dtype is None:
+        out_dtype = q.dtype
+        for t in (k, v, g, beta, state):
+            out_dtype = torch.promote_types(out_dtype, t.dtype)
+        if out_dtype not in L.DTYPE_CODE:
+            out_dtype = torch.float32
+    grads_wanted = torch.is_grad_enabled() and any(
+        t.requires_grad for t in (q, k, v, g, beta, state))
+    if need_grad is None:
+        need_grad = grads_wanted
+    pq, pk, pv, pg, pb, ps, pm = _prep(q, k, v, g, beta, state, mask)
+    if not (need_grad and grads_wanted):
+        with torch.no_grad():
+            return _GDNRecurrence.forward(_NoCtx(), pq, pk, pv, pg, pb, ps, pm, chunk, log_gate, out_dtype,
+                                          False)
+    y, state_T = _GDNRecurrence.apply(pq, pk, pv, pg, pb, ps, pm, chunk, log_gate, out_dtype, True)
+    return y, state_T
+
+
+class _NoCtx:
+    """Stand-in ctx for calling the forward without building an autograd node."""
+
+    def save_for_backward(self, *args):
+        pass
+
+    def mark_non_differentiable(self, *args):
+        pass

@@ -1,0 +1,224 @@
+"""Torch Qwen3.5 model pieces around the GDN hot path: the module whose global ``gated_delta_update`` the
+``install()`` functions rebind, exactly as the reference rebinds ``mlx_lm.models.qwen3_5.gated_delta_update``
+(``tools/gdn_vjp.py:566-574``, ``tools/gdn_checkpoint.py:145-153``, ``tools/frozen_gdn.py:54-62``).
+
+``GatedDeltaNet`` follows the order of one GDN block in ``engine/include/gdn_layer.h:31-43``: in-projections
+-> causal depthwise conv1d + SiLU -> split q/k/v -> q/k L2 norm -> gates -> recurrence -> gated RMSNorm *
+SiLU(z) -> out-projection.  The recurrence call resolves ``gated_delta_update`` from this module's globals
+at call time with ``use_kernel=not self.training`` (the mlx-lm call site, ``qwen3_5.py:183-193``).
+
+``TextModel`` / ``Model`` are small decoder stacks (GDN or causal attention mixer + SwiGLU MLP) used to
+exercise install()/frozen-layer dispatch and LoRA gradients; the MoE and full-attention details of the real
+model are outside the GDN path and are not modelled.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from gated_delta import gated_delta_update, normalize_qk  # noqa: F401  (rebound by install())
+
+Array = torch.Tensor
+
+
+@dataclass
+class ModelArgs:
+    hidden_size: int = 64
+    intermediate_size: int = 128
+    num_hidden_layers: int = 4
+    num_attention_heads: int = 4
+    vocab_size: int = 1000
+    rms_norm_eps: float = 1e-6
+    linear_num_value_heads: int = 4
+    linear_num_key_heads: int = 2
+    linear_key_head_dim: int = 8
+    linear_value_head_dim: int = 8
+    linear_conv_kernel_dim: int = 4
+    full_attention_interval: int = 2
+    layer_types: list = field(default_factory=list)
+
+    def __post_init__(self):
+        if not self.layer_types:
+            self.layer_types = [
+                "full_attention" if (i + 1) % self.full_attention_interval == 0 else "linear_attention"
+                for i in range(self.num_hidden_layers)]
+
+
+class RMSNormGated(nn.Module):
+    """rmsnorm(y) * w * silu(z) over the value head dim, eps 1e-6 (engine/src/gdn_layer.c:47-55)."""
+
+    def __init__(self, dim: int, eps: float = 1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, y: Array, z: Array) -> Array:
+        yf = y.float()
+        n = yf * torch.rsqrt((yf * yf).mean(-1, keepdim=True) + self.eps)
+        return (n * self.weight.float() * F.silu(z.float())).to(y.dtype)
+
+
+class GatedDeltaNet(nn.Module):
+    def __init__(self, args: ModelArgs):
+        super().__init__()
+        self.Hk, self.Hv = args.linear_num_key_heads, args.linear_num_value_heads
+        self.Dk, self.Dv = args.linear_key_head_dim, args.linear_value_head_dim
+        self.key_dim, self.value_dim = self.Hk * self.Dk, self.Hv * self.Dv
+        self.conv_dim = 2 * self.key_dim + self.value_dim
+        self.K = args.linear_conv_kernel_dim
+        h = args.hidden_size
+        self.in_proj_qkv = nn.Linear(h, self.conv_dim, bias=False)
+        self.in_proj_z = nn.Linear(h, self.value_dim, bias=False)
+        self.in_proj_b = nn.Linear(h, self.Hv, bias=False)
+        self.in_proj_a = nn.Linear(h, self.Hv, bias=False)
+        self.conv1d = nn.Conv1d(self.conv_dim, self.conv_dim, self.K, groups=self.conv_dim, bias=False,
+                                padding=self.K - 1)
+        self.A_log = nn.Parameter(torch.log(torch.empty(self.Hv).uniform_(1.0, 16.0)))
+        self.dt_bias = nn.Parameter(torch.zeros(self.Hv))
+        self.norm = RMSNormGated(self.Dv, args.rms_norm_eps)
+        self.out_proj = nn.Linear(self.value_dim, h, bias=False)
+
+    def forward(self, x: Array, mask: Optional[Array] = None, state: Optional[Array] = None) -> Array:
+        B, T, _ = x.shape
+        qkv = self.in_proj_qkv(x)
+        z = self.in_proj_z(x).reshape(B, T, self.Hv, self.Dv)
+        b = self.in_proj_b(x)
+        a = self.in_proj_a(x)
+        if mask is not None:
+            qkv = qkv * mask[..., None].to(qkv.dtype)
+        conv = F.silu(self.conv1d(qkv.transpose(1, 2))[..., :T]).transpose(1, 2)
+        q, k, v = torch.split(conv, [self.key_dim, self.key_dim, self.value_dim], dim=-1)
+        q = q.reshape(B, T, self.Hk, self.Dk)
+        k = k.reshape(B, T, self.Hk, self.Dk)
+        v = v.reshape(B, T, self.Hv, self.Dv)
+        q, k = normalize_qk(q, k, self.Dk ** -0.5, 1e-6)
+        update = globals()["gated_delta_update"]
+        out, _ = update(q, k, v, a, b, self.A_log, self.dt_bias, state, mask, use_kernel=not self.training)
+        out = self.norm(out.to(z.dtype), z)
+        return self.out_proj(out.reshape(B, T, -1))
+
+
+class Attention(nn.Module):
+    """Plain causal softmax attention standing in for the full-attention layers."""
+
+    def __init__(self, args: ModelArgs):
+        super().__init__()
+        h = args.hidden_size
+        self.nh = args.num_attention_heads
+        self.qkv = nn.Linear(h, 3 * h, bias=False)
+        self.o_proj = nn.Linear(h, h, bias=False)
+
+    def forward(self, x: Array, mask: Optional[Array] = None, state: Optional[Array] = None) -> Array:
+        B, T, H = x.shape
+        q, k, v = self.qkv(x).float().reshape(B, T, 3, self.nh, H // self.nh).unbind(2)
+        att = torch.einsum("bqhd,bkhd->bhqk", q, k) / math.sqrt(H // self.nh)
+        causal = torch.ones(T, T, dtype=torch.bool, device=x.device).tril()
+        att = att.masked_fill(~causal, float("-inf")).softmax(-1)
+        out = torch.einsum("bhqk,bkhd->bqhd", att, v).reshape(B, T, H).to(x.dtype)
+        return self.o_proj(out)
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, x: Array) -> Array:
+        xf = x.float()
+        return (xf * torch.rsqrt((xf * xf).mean(-1, keepdim=True) + self.eps) * self.weight).to(x.dtype)
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, args: ModelArgs, layer_type: str):
+        super().__init__()
+        self.is_linear = layer_type == "linear_attention"
+        if self.is_linear:
+            self.linear_attn = GatedDeltaNet(args)
+        else:
+            self.self_attn = Attention(args)
+        h = args.hidden_size
+        self.input_layernorm = RMSNorm(h, args.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(h, args.rms_norm_eps)
+        self.gate_up = nn.Linear(h, 2 * args.intermediate_size, bias=False)
+        self.down = nn.Linear(args.intermediate_size, h, bias=False)
+
+    def forward(self, x: Array, mask: Optional[Array] = None) -> Array:
+        mixer = self.linear_attn if self.is_linear else self.self_attn
+        x = x + mixer(self.input_layernorm(x), mask)
+        gate, up = self.gate_up(self.post_attention_layernorm(x)).chunk(2, dim=-1)
+        return x + self.down(F.silu(gate) * up)
+
+
+class TextModel(nn.Module):
+    def __init__(self, args: ModelArgs):
+        super().__init__()
+        self.args = args
+        self.embed_tokens = nn.Embedding(args.vocab_size, args.hidden_size)
+        self.layers = nn.ModuleList(DecoderLayer(args, t) for t in args.layer_types)
+        self.norm = RMSNorm(args.hidden_size, args.rms_norm_eps)
+
+    def forward(self, tokens: Array, mask: Optional[Array] = None) -> Array:
+        x = self.embed_tokens(tokens)
+        for layer in self.layers:
+            x = layer(x, mask)
+        return self.norm(x)
+
+
+class Model(nn.Module):
+    def __init__(self, args: ModelArgs):
+        super().__init__()
+        self.model = TextModel(args)
+        self.lm_head = nn.Linear(args.hidden_size, args.vocab_size, bias=False)
+
+    @property
+    def layers(self):
+        return self.model.layers
+
+    def forward(self, tokens: Array, mask: Optional[Array] = None) -> Array:
+        return self.lm_head(self.model(tokens, mask))
+
+
+Qwen3_5TextModel = TextModel
+
+
+class LoRALinear(nn.Module):
+    """y = W x + scale * B(A x) with A ~ N(0, std), B = 0; W frozen."""
+
+    def __init__(self, base: nn.Linear, rank: int, scale: float, std: float = 0.02):
+        super().__init__()
+        self.base = base
+        self.base.weight.requires_grad_(False)
+        self.lora_a = nn.Parameter(torch.randn(rank, base.in_features) * std)
+        self.lora_b = nn.Parameter(torch.zeros(base.out_features, rank))
+        self.scale = scale
+
+    @property
+    def weight(self):
+        return self.base.weight
+
+    def forward(self, x: Array) -> Array:
+        return self.base(x) + self.scale * F.linear(F.linear(x, self.lora_a.to(x.dtype)),
+                                                    self.lora_b.to(x.dtype))
+
+
+def freeze(module: nn.Module) -> None:
+    for p in module.parameters():
+        p.requires_grad_(False)
+
+
+def linear_to_lora_layers(model: Model, num_layers: int, rank: int = 2, scale: float = 2.0) -> None:
+    """Freeze the model and put LoRA adapters on every Linear of the last ``num_layers`` decoder layers
+    (the convention of mlx_lm.tuner.utils.linear_to_lora_layers used by the reference tests)."""
+    freeze(model)
+    for layer in list(model.layers)[-num_layers:]:
+        for name, mod in list(layer.named_modules()):
+            for child_name, child in list(mod.named_children()):
+                if isinstance(child, nn.Linear):
+                    setattr(mod, child_name, LoRALinear(child, rank, scale))

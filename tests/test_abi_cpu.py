@@ -1,0 +1,115 @@
+"""CPU-side checks of the C ABI and the host logic (no kernel launches)."""
+
+import ctypes
+
+import pytest
+import torch
+
+import gdn_lib
+
+
+def test_library_exports_every_declared_symbol():
+    lib = gdn_lib.load()
+    declared = gdn_lib.header_functions()
+    assert {"gdn_fwd", "gdn_bwd", "gdn_bwd_workspace_bytes", "gdn_last_error", "gdn_num_snapshots",
+            "gdn_version"} <= set(declared)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.gdn_version() >> 16 == 1
+
+
+def test_snapshot_count_matches_reference_boundaries():
+    lib = gdn_lib.load()
+    # the reference keeps ceil(T/chunk)+1 boundaries including S0 and S_T (tools/gdn_vjp.py:205-235)
+    for T, chunk in [(1, 64), (64, 64), (65, 64), (200, 16), (4096, 64), (16384, 256), (0, 64)]:
+        ref_boundaries = -(-T // chunk) + 1 if T else 1
+        expect = max(ref_boundaries - 2, 0)
+        assert lib.gdn_num_snapshots(T, chunk) == expect
+
+
+def test_abi_rejects_bad_arguments_without_launching():
+    lib = gdn_lib.load()
+    null = None
+    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 2, 3, 8, 8, 0, 0, 0, 0, 0, null)
+    assert rc == gdn_lib.GDN_ERR_INVALID
+    assert b"chunk must be a positive integer" in lib.gdn_last_error()
+    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 2, 3, 8, 8, 64, 0, 0, 0, 0, null)
+    assert rc == gdn_lib.GDN_ERR_INVALID and b"head count must divide" in lib.gdn_last_error()
+    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 1, 1, 300, 8, 64, 0, 0, 0, 0, null)
+    assert rc == gdn_lib.GDN_ERR_UNSUPPORTED
+    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 1, 1, 8, 8, 64, 7, 0, 0, 0, null)
+    assert rc == gdn_lib.GDN_ERR_INVALID and b"dtype" in lib.gdn_last_error()
+    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 1, 1, 8, 8, 64, 0, 0, 9, 0, null)
+    assert rc == gdn_lib.GDN_ERR_INVALID
+    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0, null)
+    assert rc == gdn_lib.GDN_ERR_INVALID and b"null" in lib.gdn_last_error()
+    need = lib.gdn_bwd_workspace_bytes(1, 4, 1, 1, 8, 8, 64, 0, 0)
+    assert need > 0 and lib.gdn_bwd_workspace_bytes(1, 4, 1, 1, 8, 8, 0, 0, 0) == 0
+    fake = ctypes.c_void_p(256)   # never dereferenced: the size check fails first
+    args = [fake] * 17
+    rc = lib.gdn_bwd(*args, need - 1, 1, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0, 0, null)
+    assert rc == gdn_lib.GDN_ERR_WORKSPACE
+    # B == 0 is a no-op
+    assert lib.gdn_fwd(*([null] * 10), 0, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0, null) == 0
+
+
+def test_workspace_scales_with_row_blocks_and_tokens():
+    lib = gdn_lib.load()
+    a = lib.gdn_bwd_workspace_bytes(1, 4096, 16, 32, 128, 128, 64, 0, 0)
+    b = lib.gdn_bwd_workspace_bytes(1, 8192, 16, 32, 128, 128, 64, 0, 0)
+    assert 1.9 < b / a < 2.1
+
+
+def test_python_wrapper_errors_on_cpu_tensors():
+    import gdn_vjp
+    q = torch.zeros(1, 4, 1, 8)
+    v = torch.zeros(1, 4, 2, 8)
+    g = torch.ones(1, 4, 2)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        gdn_vjp.gated_delta_chunked(q, q, v, g, g)
+    with pytest.raises(ValueError, match="chunk must be a positive integer"):
+        gdn_vjp.gated_delta_chunked(q, q, v, g, g, chunk=-1)
+    with pytest.raises(ValueError, match="impl must be"):
+        gdn_vjp.gated_delta_chunked(q, q, v, g, g, impl="nope")
+
+
+def test_install_rebinds_and_delegates_use_kernel(monkeypatch):
+    """tools/test_gdn_vjp.py:177-193 and tools/test_gdn_checkpoint.py:223-241, on the torch module."""
+    import gdn_checkpoint
+    import gdn_vjp
+    import qwen3_5
+    for mod, fn in ((gdn_vjp, "_vjp_update"), (gdn_checkpoint, "_checkpointed_update")):
+        calls = []
+        sentinel = object()
+
+        def spy(*args, **kwargs):
+            calls.append(kwargs.get("use_kernel"))
+            return sentinel
+
+        monkeypatch.setattr(mod, "_ORIGINAL_UPDATE", None)
+        monkeypatch.setattr(qwen3_5, "gated_delta_update", spy)
+        mod.install()
+        assert qwen3_5.gated_delta_update is getattr(mod, fn)
+        mod.install()   # idempotent
+        assert mod._ORIGINAL_UPDATE is spy
+        values = [torch.tensor(0.0) for _ in range(7)]
+        assert qwen3_5.gated_delta_update(*values, use_kernel=True) is sentinel
+        assert calls == [True]
+
+
+def test_update_without_install_raises(monkeypatch):
+    import gdn_vjp
+    monkeypatch.setattr(gdn_vjp, "_ORIGINAL_UPDATE", None)
+    with pytest.raises(RuntimeError, match="install\\(\\) has not been called"):
+        gdn_vjp._vjp_update(*[torch.tensor(0.0)] * 7, use_kernel=True)
+
+
+def test_frozen_gdn_install_errors():
+    import frozen_gdn
+    import qwen3_5
+    with pytest.raises(TypeError, match="qwen3_5-family"):
+        frozen_gdn.install(torch.nn.Linear(2, 2))
+    model = qwen3_5.Model(qwen3_5.ModelArgs(full_attention_interval=3))
+    qwen3_5.freeze(model)
+    with pytest.raises(ValueError, match="trainable parameter"):
+        frozen_gdn.install(model)
