@@ -111,6 +111,8 @@ def main():
     ap.add_argument("--workload", default="bf16_b4_t4096", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=256)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="run one plain device copy of MIB MiB first (scales rocprof FETCH/WRITE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the GDN path here is "
@@ -124,6 +126,15 @@ def main():
     w = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     gdn_lib.load()
+    if args.copy_calibration:
+        n = args.copy_calibration * 2 ** 20 // 4
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: calibration copy of {args.copy_calibration} MiB done")
+        del src, dst
     log(f"bench: workload {args.workload} {w}")
     x = make_inputs(w, dev)
     B, T, Hk, Hv, D = w["B"], w["T"], w["Hk"], w["Hv"], w["D"]
