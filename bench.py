@@ -31,6 +31,37 @@ sys.path.insert(0, str(ROOT))
 METRIC = "GDN fwd+VJP tokens/sec at T=4096 (1 GPU) + % of HBM/MFMA roofline"
 PEAK_HBM_GBS = 8000.0
 PEAK_FP32_TFLOPS = 157.3
+PEAK_BF16_TFLOPS = 2500.0
+CK_C = 64
+
+
+def kernel_model(name, B, T, Hk, Hv, D, in_b):
+    """Algorithmic (flops, HBM bytes) of one launch of a kernel, from what the kernel must read and write
+    and the products it must form (recompute and padding excluded).  Chunk kernels: per (head, 64-token
+    chunk); recurrent kernels: per head-token state element."""
+    nc = -(-T // CK_C)
+    ch = B * Hv * nc            # chunk-heads
+    tokh = B * T * Hv           # head-tokens
+    C = CK_C
+    cd, cc, dd = C * D, C * C, D * D
+    if name == "ck_prep":
+        return ch * 4 * 2 * cd * C, ch * (3 * cd * in_b + 2 * C * 4 + 2 * cd * 4 + 2 * cc * 4 + C * 8)
+    if name == "ck_fwd":
+        return ch * (3 * 2 * cd * D + 2 * cc * D), ch * (2 * cd * 4 + cc * 4 + 2 * cd * in_b + C * 8
+                                                         + dd * 4 + cd * 4 + cd * in_b)
+    if name == "ck_bwd_seq":
+        return ch * (3 * 2 * cd * D + 2 * cc * D), ch * (cc * 4 + cd * 4 + 3 * cd * in_b + C * 8
+                                                         + dd * 4 + cd * 4)
+    if name == "ck_bwd_local":
+        f = ch * (3 * 2 * cd * D + 10 * 2 * cc * D + 2 * 2 * cc * C)
+        by = ch * (2 * dd * 4 + 2 * cd * 4 + 2 * cc * 4 + C * 8 + 4 * cd * in_b + C * 4
+                   + 2 * cd * 4 + cd * in_b + 2 * C * 4)
+        return f, by
+    if name == "rec_fwd":
+        return 7 * tokh * D * D, B * T * (2 * Hk * D * in_b + Hv * D * in_b * 2 + 2 * Hv * 4)
+    if name == "rec_bwd":
+        return 20 * tokh * D * D, B * T * (2 * Hk * D * in_b + 3 * Hv * D * in_b + 2 * Hv * 4)
+    return 0, 0
 
 WORKLOADS = {
     "bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0),
@@ -165,27 +196,34 @@ def main():
 
     tokens = B * T
     value = tokens * args.steps / elapsed
-    # Dominant kernel: the one with the largest total time.  Algorithmic flops per head-token per state
-    # element: forward 7 (decay, S k, update, S q), backward 20 (the adjoint of tools/gdn_vjp.py:8-21 plus
-    # the residual); recompute is not counted.
-    flops_per_elem = {"rec_fwd": 7, "rec_bwd": 20}
     dom = max(kt, key=lambda n: kt[n][0])
     ms, cnt = kt[dom]
     avg_ms = ms / cnt
-    per_launch = flops_per_elem.get(dom, 0) * B * T * Hv * D * D
-    achieved = per_launch / (avg_ms * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None, "kernel": dom,
-                "avg_launch_ms": round(avg_ms, 4),
-                "note": "fp32 VALU arithmetic (packed fp32 disabled); peak is MI355X fp32 157.3 TFLOP/s",
-                "kernels_ms_per_step": {n: round(v[0] / max(v[1], 1) * v[1] / args.steps, 4)
-                                        for n, v in kt.items()}}
+    in_b = 2 if w["dtype"] == "bf16" else 4
+    flops, nbytes = kernel_model(dom, B, T, Hk, Hv, D, in_b)
+    t_s = avg_ms * 1e-3
+    peak_flops = PEAK_BF16_TFLOPS if (w["dtype"] == "bf16" and dom.startswith("ck_")) else PEAK_FP32_TFLOPS
+    f_frac = flops / t_s / 1e12 / peak_flops
+    b_frac = nbytes / t_s / 1e9 / PEAK_HBM_GBS
+    if b_frac >= f_frac:
+        roofline = {"bound": "hbm", "achieved": round(nbytes / t_s / 1e9, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(b_frac, 4)}
+    else:
+        roofline = {"bound": "mfma", "achieved": round(flops / t_s / 1e12, 3), "peak": peak_flops,
+                    "unit": "TFLOP/s", "frac": round(f_frac, 4)}
+    roofline.update({
+        "traffic": None, "kernel": dom, "avg_launch_ms": round(avg_ms, 4),
+        "algo_flops_per_launch": flops, "algo_bytes_per_launch": nbytes,
+        "other_roof_frac": round(min(f_frac, b_frac), 4),
+        "kernels_ms_per_step": {n: round(v[0] / args.steps, 4) for n, v in kt.items()}})
+    form = "chunk" if any(n.startswith("ck_") for n in kt) else "recurrent"
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if (w["dtype"] == "bf16" and form == "chunk") else "fp32", "data": "synthetic",
         "config": {"workload": args.workload, "B": B, "T": T, "Hk": Hk, "Hv": Hv, "Dk": D, "Dv": D,
-                   "chunk": w["chunk"], "inputs": w["dtype"], "state": "fp32", "form": "recurrent",
+                   "chunk": w["chunk"], "inputs": w["dtype"], "state": "fp32", "form": form,
                    "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
         "peak_hbm_gib": round(peak_gib, 3),
         "roofline": roofline,

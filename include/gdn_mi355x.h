@@ -48,8 +48,9 @@ enum gdn_gate {
 };
 
 enum gdn_form {
-    GDN_FORM_AUTO = 0,       /* the engine chooses */
-    GDN_FORM_RECURRENT = 1   /* token-sequential recurrence, state resident in VGPRs */
+    GDN_FORM_AUTO = 0,       /* the chunked form when eligible, else the recurrent form */
+    GDN_FORM_RECURRENT = 1,  /* token-sequential recurrence, state rows resident in VGPRs; any shape */
+    GDN_FORM_CHUNK = 2       /* chunked WY/UT form on MFMA (chunk 64); Dk = Dv = 128, no mask, scalar gate */
 };
 
 /* Library version, (major << 16) | minor. */
@@ -66,29 +67,39 @@ const char *gdn_last_error(void);
 int gdn_profile_enable(int on);
 int gdn_profile_collect(int max_entries, char *names, int name_len, double *total_ms, int *counts);
 
-/* Number of chunk snapshots gdn_fwd writes: ceil(T / chunk) - 1 states of [B][Hv][Dv][Dk] fp32, the states
- * at token chunk, 2*chunk, ... (the reference keeps the same boundaries, tools/gdn_vjp.py:205-235; the first
- * one, S0, is the caller's input and the last one is the returned final state). */
+/* Number of chunk snapshots the recurrent form keeps: ceil(T / chunk) - 1 states of [B][Hv][Dv][Dk] fp32, the
+ * states at token chunk, 2*chunk, ... (the reference keeps the same boundaries, tools/gdn_vjp.py:205-235; the
+ * first, S0, is the caller's input and the last is the returned final state). */
 int64_t gdn_num_snapshots(int T, int chunk);
+
+/* The form a call with these arguments runs in (GDN_FORM_RECURRENT or GDN_FORM_CHUNK), or < 0 when the
+ * requested form cannot run them.  gdn_fwd and gdn_bwd resolve the form the same way. */
+int gdn_select_form(int Dk, int Dv, int has_mask, int gate_kind, int form);
+
+/* Size of the buffer gdn_fwd fills for gdn_bwd (the "saved" activations).  Recurrent form: the chunk
+ * snapshots.  Chunked form: per 64-token chunk, the entry state, the cumulative log decays, T = (I+A)^-1, the
+ * intra-chunk output matrix, W, U and Delta (all recomputable from the inputs; kept because HBM is ample). */
+size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind, int has_mask,
+                       int form);
 
 /* Forward.  Replaces the forward of gated_delta_chunked (tools/gdn_vjp.py:503-528 via _forward :205-235)
  * and of gated_delta_ops_checkpointed (tools/gdn_checkpoint.py:53-95).
- * Writes y (out_dtype), state_T (fp32; may be NULL) and, when snapshots is not NULL, the
- * gdn_num_snapshots(T, chunk) chunk-boundary states.  With snapshots == NULL this is the forward-only path
- * of frozen layers (tools/frozen_gdn.py:19-25, mlx-lm gated_delta_kernel). */
+ * Writes y (out_dtype), state_T (fp32; may be NULL) and, when saved is not NULL, the gdn_saved_bytes()
+ * buffer gdn_bwd reads.  In the recurrent form saved may be NULL: the forward-only path of frozen layers
+ * (tools/frozen_gdn.py:19-25, mlx-lm gated_delta_kernel); the chunked form always needs it. */
 int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
             const float *state0, const uint8_t *mask,
-            void *y, float *state_T, float *snapshots,
+            void *y, float *state_T, void *saved, size_t saved_bytes,
             int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk,
             int in_dtype, int out_dtype, int gate_kind, int form, void *stream);
 
 /* Device workspace gdn_bwd needs, in bytes (256-byte aligned base expected). */
 size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind,
-                               int form);
+                               int has_mask, int form);
 
 /* Backward (VJP).  Replaces _backward / _chunk_vjp / the Metal kernel gdn_chunk_backward
  * (tools/gdn_vjp.py:273-320, :341-423, :426-474) and the mx.checkpoint recompute of
- * tools/gdn_checkpoint.py:39-50.  Reads the snapshots written by gdn_fwd with the same chunk, recomputes
+ * tools/gdn_checkpoint.py:39-50.  Reads the saved buffer gdn_fwd wrote with the same arguments, recomputes
  * the states inside each chunk, and writes
  *   dq, dk [B][T][Hk][Dk] (grad_dtype; summed over the value heads of each key head, tools/gdn_vjp.py:266-270)
  *   dv     [B][T][Hv][Dv] (grad_dtype)
@@ -97,7 +108,7 @@ size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int
  *   dstate0 [B][Hv][Dv][Dk] fp32 (may be NULL)
  * dy has dy_dtype; dstate_T may be NULL (zero cotangent).  Results are deterministic (no atomics). */
 int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
-            const float *state0, const uint8_t *mask, const float *snapshots,
+            const float *state0, const uint8_t *mask, const void *saved, size_t saved_bytes,
             const void *dy, const float *dstate_T,
             void *dq, void *dk, void *dv, float *dg, float *dbeta, float *dstate0,
             void *workspace, size_t workspace_bytes,

@@ -94,12 +94,28 @@ static int check_shape(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, 
     if (Hv % Hk != 0) return fail(GDN_ERR_INVALID, "q/k head count must divide the value head count");
     if (gate != GATE_DECAY && gate != GATE_DECAY_VEC && gate != GATE_LOG)
         return fail(GDN_ERR_INVALID, "Unsupported gating kind %d", gate);
-    if (form != GDN_FORM_AUTO && form != GDN_FORM_RECURRENT)
+    if (form != GDN_FORM_AUTO && form != GDN_FORM_RECURRENT && form != GDN_FORM_CHUNK)
         return fail(GDN_ERR_INVALID, "unknown form %d", form);
     if (pick_lane_width(Dk) == 0) return fail(GDN_ERR_UNSUPPORTED, "key_dim %d > 256 is not supported", Dk);
     if (Hv > 65535 || B > 65535) return fail(GDN_ERR_UNSUPPORTED, "batch and value heads must be <= 65535");
     return GDN_OK;
 }
+
+static bool chunk_eligible(int Dk, int Dv, int has_mask, int gate) {
+    return Dk == 128 && Dv == 128 && !has_mask && (gate == GATE_DECAY || gate == GATE_LOG);
+}
+
+// The form a (shape, mask, gate, requested form) resolves to, or < 0 when a requested form cannot run.
+static int resolve_form(int Dk, int Dv, int has_mask, int gate, int form) {
+    if (form == GDN_FORM_RECURRENT) return GDN_FORM_RECURRENT;
+    const bool ok = chunk_eligible(Dk, Dv, has_mask, gate);
+    if (form == GDN_FORM_CHUNK)
+        return ok ? GDN_FORM_CHUNK
+                  : fail(GDN_ERR_UNSUPPORTED, "the chunked form needs Dk = Dv = 128, no mask and a scalar gate");
+    return ok ? GDN_FORM_CHUNK : GDN_FORM_RECURRENT;
+}
+
+static bool misaligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -122,6 +138,11 @@ static BwdLayout bwd_layout(int B, int T, int Hv, int Dk, int Dv, int chunk, int
     if (gate == GATE_DECAY_VEC) off += align256(nrb * toks * Dk * sizeof(float));
     L.total = off;
     return L;
+}
+
+static size_t rec_saved_bytes(int B, int T, int Hv, int Dk, int Dv, int chunk) {
+    const int64_t ns = T > 0 ? (int64_t)((T + chunk - 1) / chunk) - 1 : 0;
+    return (size_t)(ns > 0 ? ns : 0) * B * Hv * Dv * Dk * sizeof(float);
 }
 
 }  // namespace gdn
@@ -177,14 +198,30 @@ int64_t gdn_num_snapshots(int T, int chunk) {
     return (int64_t)((T + chunk - 1) / chunk) - 1;
 }
 
+int gdn_select_form(int Dk, int Dv, int has_mask, int gate_kind, int form) {
+    g_err[0] = 0;
+    return resolve_form(Dk, Dv, has_mask, gate_kind, form);
+}
+
+size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind, int has_mask,
+                       int form) {
+    if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
+    const int f = resolve_form(Dk, Dv, has_mask, gate_kind, form);
+    if (f < 0 || B == 0 || T == 0) return 0;
+    if (f == GDN_FORM_CHUNK) return chunk_sizes(B, T, Hv).saved;
+    return rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
+}
+
 int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
-            const float *state0, const uint8_t *mask, void *y, float *state_T, float *snapshots, int B, int T,
-            int Hk, int Hv, int Dk, int Dv, int chunk, int in_dtype, int out_dtype, int gate_kind, int form,
-            void *stream) {
+            const float *state0, const uint8_t *mask, void *y, float *state_T, void *saved, size_t saved_bytes,
+            int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int in_dtype, int out_dtype, int gate_kind,
+            int form, void *stream) {
     g_err[0] = 0;
     int rc = check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form);
     if (rc) return rc;
     if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    const int f = resolve_form(Dk, Dv, mask != nullptr, gate_kind, form);
+    if (f < 0) return f;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (B == 0) return GDN_OK;
     if (T == 0) {
@@ -192,7 +229,39 @@ int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const f
         return check_launch(st, "gdn_fwd(T=0)");
     }
     if (!q || !k || !v || !g || !beta || !y) return fail(GDN_ERR_INVALID, "null input or output pointer");
-    RecFwdArgs a{q, k, v, g, beta, state0, mask, y, state_T, snapshots,
+    if (f == GDN_FORM_CHUNK) {
+        if (misaligned16(q) || misaligned16(k) || misaligned16(v))
+            return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned q, k and v");
+        // the chunked form always needs its per-chunk buffers, also for a forward-only call
+        const size_t need = chunk_sizes(B, T, Hv).saved;
+        if (!saved || saved_bytes < need)
+            return fail(GDN_ERR_WORKSPACE, "saved buffer of %zu bytes is smaller than the %zu bytes required",
+                        saved_bytes, need);
+        ChunkCall cc{};
+        cc.q = q; cc.k = k; cc.v = v; cc.g = g; cc.beta = beta; cc.state0 = state0;
+        cc.y = y; cc.state_T = state_T; cc.saved = saved;
+        cc.B = B; cc.T = T; cc.Hk = Hk; cc.Hv = Hv; cc.in_dt = in_dtype; cc.out_dt = out_dtype; cc.gate = gate_kind;
+        {
+            Timed tm("ck_prep", st);
+            launch_chunk_stage(cc, "prep", st);
+        }
+        rc = check_launch(st, "gdn_fwd(ck_prep)");
+        if (rc) return rc;
+        {
+            Timed tm("ck_fwd", st);
+            launch_chunk_stage(cc, "fwd", st);
+        }
+        return check_launch(st, "gdn_fwd(ck_fwd)");
+    }
+    const size_t need = rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
+    float *snaps = nullptr;
+    if (saved) {
+        if (saved_bytes < need)
+            return fail(GDN_ERR_WORKSPACE, "saved buffer of %zu bytes is smaller than the %zu bytes required",
+                        saved_bytes, need);
+        snaps = static_cast<float *>(saved);
+    }
+    RecFwdArgs a{q, k, v, g, beta, state0, mask, y, state_T, snaps,
                  B, T, Hk, Hv, Dk, Dv, chunk, in_dtype, out_dtype, gate_kind};
     {
         Timed tm("rec_fwd", st);
@@ -202,13 +271,16 @@ int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const f
 }
 
 size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind,
-                               int form) {
+                               int has_mask, int form) {
     if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
+    const int f = resolve_form(Dk, Dv, has_mask, gate_kind, form);
+    if (f < 0) return 0;
+    if (f == GDN_FORM_CHUNK) return chunk_sizes(B, T, Hv).work;
     return bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind).total;
 }
 
 int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
-            const float *state0, const uint8_t *mask, const float *snapshots, const void *dy,
+            const float *state0, const uint8_t *mask, const void *saved, size_t saved_bytes, const void *dy,
             const float *dstate_T, void *dq, void *dk, void *dv, float *dg, float *dbeta, float *dstate0,
             void *workspace, size_t workspace_bytes, int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk,
             int in_dtype, int dy_dtype, int grad_dtype, int gate_kind, int form, void *stream) {
@@ -217,6 +289,8 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
     if (rc) return rc;
     if (!dtype_ok(in_dtype) || !dtype_ok(dy_dtype) || !dtype_ok(grad_dtype))
         return fail(GDN_ERR_INVALID, "unknown dtype code");
+    const int f = resolve_form(Dk, Dv, mask != nullptr, gate_kind, form);
+    if (f < 0) return f;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (B == 0) return GDN_OK;
     if (T == 0) {
@@ -225,23 +299,55 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
     }
     if (!q || !k || !v || !g || !beta || !dy || !dq || !dk || !dv || !dg || !dbeta)
         return fail(GDN_ERR_INVALID, "null input or output pointer");
-    if (gdn_num_snapshots(T, chunk) > 0 && !snapshots)
-        return fail(GDN_ERR_INVALID, "snapshots from gdn_fwd are required when T > chunk");
-    const BwdLayout L = bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind);
-    if (workspace_bytes < L.total || (L.total && !workspace))
+    const size_t need_saved = f == GDN_FORM_CHUNK ? chunk_sizes(B, T, Hv).saved : rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
+    if (need_saved && (!saved || saved_bytes < need_saved))
+        return fail(GDN_ERR_INVALID, "the saved buffer written by gdn_fwd (%zu bytes) is required", need_saved);
+    const size_t need_ws = f == GDN_FORM_CHUNK ? chunk_sizes(B, T, Hv).work
+                                               : bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind).total;
+    if (workspace_bytes < need_ws || (need_ws && !workspace))
         return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
-                    workspace_bytes, L.total);
-    char *ws = static_cast<char *>(workspace);
+                    workspace_bytes, need_ws);
     RecBwdArgs a{};
     a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.state0 = state0; a.mask = mask;
-    a.snaps = snapshots; a.dy = dy; a.dstate_T = dstate_T;
+    a.snaps = static_cast<const float *>(saved); a.dy = dy; a.dstate_T = dstate_T;
     a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dstate0 = dstate0;
+    a.B = B; a.T = T; a.Hk = Hk; a.Hv = Hv; a.Dk = Dk; a.Dv = Dv; a.chunk = chunk;
+    a.in_dt = in_dtype; a.dy_dt = dy_dtype; a.grad_dt = grad_dtype; a.gate = gate_kind;
+    if (f == GDN_FORM_CHUNK) {
+        if (misaligned16(q) || misaligned16(k) || misaligned16(v) || misaligned16(dy))
+            return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned q, k, v and dy");
+        ChunkCall cc{};
+        cc.q = q; cc.k = k; cc.v = v; cc.g = g; cc.beta = beta; cc.state0 = state0;
+        cc.dy = dy; cc.dstate_T = dstate_T; cc.dv = dv; cc.dg = dg; cc.dbeta = dbeta; cc.dstate0 = dstate0;
+        cc.saved = const_cast<void *>(saved); cc.work = workspace;
+        cc.B = B; cc.T = T; cc.Hk = Hk; cc.Hv = Hv; cc.in_dt = in_dtype; cc.dy_dt = dy_dtype;
+        cc.grad_dt = grad_dtype; cc.gate = gate_kind;
+        {
+            Timed tm("ck_bwd_seq", st);
+            launch_chunk_stage(cc, "seq", st);
+        }
+        rc = check_launch(st, "gdn_bwd(ck_bwd_seq)");
+        if (rc) return rc;
+        {
+            Timed tm("ck_bwd_local", st);
+            launch_chunk_stage(cc, "local", st);
+        }
+        rc = check_launch(st, "gdn_bwd(ck_bwd_local)");
+        if (rc) return rc;
+        a.part_qk = reinterpret_cast<float *>(static_cast<char *>(workspace) + chunk_sizes(B, T, Hv).part);
+        a.nrb = 1;
+        {
+            Timed tm("reduce_qk", st);
+            launch_reduce_qk(a, st);
+        }
+        return check_launch(st, "gdn_bwd(reduce_qk)");
+    }
+    const BwdLayout L = bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind);
+    char *ws = static_cast<char *>(workspace);
     a.ws_sub = reinterpret_cast<float *>(ws + L.sub);
     a.part_qk = reinterpret_cast<float *>(ws + L.part_qk);
     a.part_gb = reinterpret_cast<float *>(ws + L.part_gb);
     a.part_gv = reinterpret_cast<float *>(ws + L.part_gv);
-    a.B = B; a.T = T; a.Hk = Hk; a.Hv = Hv; a.Dk = Dk; a.Dv = Dv; a.chunk = chunk;
-    a.in_dt = in_dtype; a.dy_dt = dy_dtype; a.grad_dt = grad_dtype; a.gate = gate_kind;
     a.nrb = rec_num_row_blocks(Dv);
     a.max_sub = rec_max_sub(T, chunk);
     {

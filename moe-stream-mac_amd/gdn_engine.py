@@ -10,6 +10,7 @@ chunk from its boundary, like ``_chunk_vjp`` (``:273-320``) and ``mx.checkpoint`
 
 from __future__ import annotations
 
+import os
 from typing import Optional
 
 import torch
@@ -37,41 +38,51 @@ def gate_kind_for(g: torch.Tensor, log_gate: bool) -> int:
     raise ValueError(f"Unsupported gating shape {tuple(g.shape)}")
 
 
+def _saved_bytes(lib, B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form) -> int:
+    return int(lib.gdn_saved_bytes(B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form))
+
+
 class _GDNRecurrence(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, g, beta, state, mask, chunk, log_gate, out_dtype, need_snapshots):
+    def forward(ctx, q, k, v, g, beta, state, mask, chunk, log_gate, out_dtype, need_saved, form):
         dev = _require_device(q, k, v, g, beta, state)
         B, T, Hk, Dk = q.shape
         Hv, Dv = v.shape[2], v.shape[3]
         in_dtype = q.dtype
         gate = gate_kind_for(g, log_gate)
+        lib = L.load()
+        has_mask = int(mask is not None)
+        resolved = int(lib.gdn_select_form(Dk, Dv, has_mask, gate, form))
+        if resolved < 0:
+            L.check(resolved)
         y = torch.empty((B, T, Hv, Dv), device=dev, dtype=out_dtype)
         state_T = torch.empty((B, Hv, Dv, Dk), device=dev, dtype=torch.float32)
-        lib = L.load()
-        n_snap = int(lib.gdn_num_snapshots(T, chunk)) if need_snapshots else 0
-        snaps = torch.empty((max(n_snap, 0), B, Hv, Dv, Dk), device=dev, dtype=torch.float32)
+        keep = need_saved or resolved == L.FORM_CHUNK
+        n_saved = _saved_bytes(lib, B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form) if keep else 0
+        saved = torch.empty((n_saved,), device=dev, dtype=torch.uint8)
         L.check(lib.gdn_fwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), L.ptr(state),
-                            L.ptr(mask), L.ptr(y), L.ptr(state_T), L.ptr(snaps) if n_snap else None,
+                            L.ptr(mask), L.ptr(y), L.ptr(state_T), L.ptr(saved) if n_saved else None, n_saved,
                             B, T, Hk, Hv, Dk, Dv, chunk, L.DTYPE_CODE[in_dtype], L.DTYPE_CODE[out_dtype],
-                            gate, L.FORM_AUTO, L.stream_handle(dev)))
-        ctx.save_for_backward(q, k, v, g, beta, state, mask, snaps)
-        ctx.meta = (chunk, gate)
-        ctx.mark_non_differentiable()
+                            gate, form, L.stream_handle(dev)))
+        ctx.save_for_backward(q, k, v, g, beta, state, mask, saved)
+        ctx.meta = (chunk, gate, form)
         return y, state_T
 
     @staticmethod
     def backward(ctx, dy, dstate_T):
-        q, k, v, g, beta, state, mask, snaps = ctx.saved_tensors
-        chunk, gate = ctx.meta
+        q, k, v, g, beta, state, mask, saved = ctx.saved_tensors
+        chunk, gate, form = ctx.meta
         dev = q.device
         B, T, Hk, Dk = q.shape
         Hv, Dv = v.shape[2], v.shape[3]
         lib = L.load()
+        has_mask = int(mask is not None)
         if dy is None:
             dy = torch.zeros((B, T, Hv, Dv), device=dev, dtype=torch.float32)
         dy = dy.contiguous()
         if dy.dtype not in L.DTYPE_CODE:
             dy = dy.float()
+        dy = _aligned(dy)
         dstate_T = None if dstate_T is None else dstate_T.contiguous().float()
         grad_dtype = q.dtype
         dq = torch.empty((B, T, Hk, Dk), device=dev, dtype=grad_dtype)
@@ -80,22 +91,27 @@ class _GDNRecurrence(torch.autograd.Function):
         dg = torch.empty(g.shape, device=dev, dtype=torch.float32)
         dbeta = torch.empty((B, T, Hv), device=dev, dtype=torch.float32)
         dS0 = torch.empty((B, Hv, Dv, Dk), device=dev, dtype=torch.float32)
-        ws_bytes = int(lib.gdn_bwd_workspace_bytes(B, T, Hk, Hv, Dk, Dv, chunk, gate, L.FORM_AUTO))
+        ws_bytes = int(lib.gdn_bwd_workspace_bytes(B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form))
         ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
         L.check(lib.gdn_bwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), L.ptr(state), L.ptr(mask),
-                            L.ptr(snaps) if snaps.numel() else None, L.ptr(dy), L.ptr(dstate_T),
-                            L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(dg), L.ptr(dbeta), L.ptr(dS0),
-                            L.ptr(ws), ws_bytes, B, T, Hk, Hv, Dk, Dv, chunk,
+                            L.ptr(saved) if saved.numel() else None, saved.numel(), L.ptr(dy),
+                            L.ptr(dstate_T), L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(dg), L.ptr(dbeta),
+                            L.ptr(dS0), L.ptr(ws), ws_bytes, B, T, Hk, Hv, Dk, Dv, chunk,
                             L.DTYPE_CODE[q.dtype], L.DTYPE_CODE[dy.dtype], L.DTYPE_CODE[grad_dtype], gate,
-                            L.FORM_AUTO, L.stream_handle(dev)))
-        return dq, dk, dv, dg, dbeta, dS0, None, None, None, None, None
+                            form, L.stream_handle(dev)))
+        return dq, dk, dv, dg, dbeta, dS0, None, None, None, None, None, None
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """The kernels read rows with 16-byte loads: a contiguous view at an unaligned offset is copied."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 def _prep(q, k, v, g, beta, state, mask):
     common = torch.promote_types(torch.promote_types(q.dtype, k.dtype), v.dtype)
     if common not in L.DTYPE_CODE:
         common = torch.float32
-    q, k, v = (x.to(common).contiguous() for x in (q, k, v))
+    q, k, v = (_aligned(x.to(common).contiguous()) for x in (q, k, v))
     g = g.to(torch.float32).contiguous()
     beta = beta.to(torch.float32).contiguous()
     state = state.to(torch.float32).contiguous()
@@ -127,13 +143,23 @@ def check_shapes(q, k, v, g, beta, state, mask) -> None:
         raise ValueError("mask must be [B, T]")
 
 
+def default_form() -> int:
+    """Form requested by default: GDN_FORM=auto|recurrent|chunk in the environment, else auto."""
+    name = os.environ.get("GDN_FORM", "auto").strip().lower()
+    if name not in L.FORMS:
+        raise ValueError(f"GDN_FORM must be one of {sorted(L.FORMS)}, got {name!r}")
+    return L.FORMS[name]
+
+
 def recurrence(q, k, v, g, beta, state, mask=None, chunk: int = 64, log_gate: bool = False,
-               output_dtype: Optional[torch.dtype] = None, need_grad: Optional[bool] = None):
+               output_dtype: Optional[torch.dtype] = None, need_grad: Optional[bool] = None,
+               form: Optional[str] = None):
     """(y, final_state) of the delta-rule recurrence with a HIP forward and VJP.
 
     ``g`` is the multiplicative decay ([B,T,Hv] or [B,T,Hv,Dk]) or, with ``log_gate``, the log decay.
     ``y`` defaults to the dtype the reference's arithmetic promotes to (fp32 with an fp32 state).
-    ``need_grad=False`` runs the forward-only path (no snapshots, no autograd graph).
+    ``need_grad=False`` runs the forward-only path (no autograd graph).  ``form`` is "auto" (default, or the
+    GDN_FORM environment variable), "recurrent" or "chunk".
     """
     if chunk <= 0:
         raise ValueError("chunk must be a positive integer")
@@ -150,12 +176,13 @@ def recurrence(q, k, v, g, beta, state, mask=None, chunk: int = 64, log_gate: bo
         t.requires_grad for t in (q, k, v, g, beta, state))
     if need_grad is None:
         need_grad = grads_wanted
+    form_code = default_form() if form is None else L.FORMS[form]
     pq, pk, pv, pg, pb, ps, pm = _prep(q, k, v, g, beta, state, mask)
     if not (need_grad and grads_wanted):
         with torch.no_grad():
             return _GDNRecurrence.forward(_NoCtx(), pq, pk, pv, pg, pb, ps, pm, chunk, log_gate, out_dtype,
-                                          False)
-    y, state_T = _GDNRecurrence.apply(pq, pk, pv, pg, pb, ps, pm, chunk, log_gate, out_dtype, True)
+                                          False, form_code)
+    y, state_T = _GDNRecurrence.apply(pq, pk, pv, pg, pb, ps, pm, chunk, log_gate, out_dtype, True, form_code)
     return y, state_T
 
 
@@ -165,5 +192,3 @@ class _NoCtx:
     def save_for_backward(self, *args):
         pass
 
-    def mark_non_differentiable(self, *args):
-        pass

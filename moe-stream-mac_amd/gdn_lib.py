@@ -20,7 +20,8 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "gdn_mi355x.h"
 GDN_OK, GDN_ERR_INVALID, GDN_ERR_UNSUPPORTED, GDN_ERR_WORKSPACE, GDN_ERR_LAUNCH = 0, -1, -2, -3, -4
 F32, BF16, F16 = 0, 1, 2
 GATE_DECAY, GATE_DECAY_VEC, GATE_LOG = 0, 1, 2
-FORM_AUTO, FORM_RECURRENT = 0, 1
+FORM_AUTO, FORM_RECURRENT, FORM_CHUNK = 0, 1, 2
+FORMS = {"auto": FORM_AUTO, "recurrent": FORM_RECURRENT, "chunk": FORM_CHUNK}
 
 DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -30,9 +31,11 @@ _SIGS = {
     "gdn_version": ([], _i),
     "gdn_last_error": ([], ctypes.c_char_p),
     "gdn_num_snapshots": ([_i, _i], ctypes.c_int64),
-    "gdn_fwd": ([_vp] * 10 + [_i] * 11 + [_vp], _i),
-    "gdn_bwd_workspace_bytes": ([_i] * 9, ctypes.c_size_t),
-    "gdn_bwd": ([_vp] * 17 + [ctypes.c_size_t] + [_i] * 12 + [_vp], _i),
+    "gdn_select_form": ([_i] * 5, _i),
+    "gdn_saved_bytes": ([_i] * 10, ctypes.c_size_t),
+    "gdn_fwd": ([_vp] * 10 + [ctypes.c_size_t] + [_i] * 11 + [_vp], _i),
+    "gdn_bwd_workspace_bytes": ([_i] * 10, ctypes.c_size_t),
+    "gdn_bwd": ([_vp] * 8 + [ctypes.c_size_t] + [_vp] * 9 + [ctypes.c_size_t] + [_i] * 12 + [_vp], _i),
     "gdn_profile_enable": ([_i], _i),
     "gdn_profile_collect": ([_i, ctypes.c_char_p, _i, ctypes.POINTER(ctypes.c_double),
                              ctypes.POINTER(_i)], _i),

@@ -12,7 +12,8 @@ def test_library_exports_every_declared_symbol():
     lib = gdn_lib.load()
     declared = gdn_lib.header_functions()
     assert {"gdn_fwd", "gdn_bwd", "gdn_bwd_workspace_bytes", "gdn_last_error", "gdn_num_snapshots",
-            "gdn_version"} <= set(declared)
+            "gdn_version", "gdn_saved_bytes", "gdn_select_form", "gdn_profile_enable",
+            "gdn_profile_collect"} <= set(declared)
     for name in declared:
         assert hasattr(lib, name), name
     assert lib.gdn_version() >> 16 == 1
@@ -30,33 +31,51 @@ def test_snapshot_count_matches_reference_boundaries():
 def test_abi_rejects_bad_arguments_without_launching():
     lib = gdn_lib.load()
     null = None
-    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 2, 3, 8, 8, 0, 0, 0, 0, 0, null)
+    fwd = lambda *ints: lib.gdn_fwd(*([null] * 10), 0, *ints, null)
+    rc = fwd(1, 4, 2, 3, 8, 8, 0, 0, 0, 0, 0)
     assert rc == gdn_lib.GDN_ERR_INVALID
     assert b"chunk must be a positive integer" in lib.gdn_last_error()
-    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 2, 3, 8, 8, 64, 0, 0, 0, 0, null)
+    rc = fwd(1, 4, 2, 3, 8, 8, 64, 0, 0, 0, 0)
     assert rc == gdn_lib.GDN_ERR_INVALID and b"head count must divide" in lib.gdn_last_error()
-    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 1, 1, 300, 8, 64, 0, 0, 0, 0, null)
+    rc = fwd(1, 4, 1, 1, 300, 8, 64, 0, 0, 0, 0)
     assert rc == gdn_lib.GDN_ERR_UNSUPPORTED
-    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 1, 1, 8, 8, 64, 7, 0, 0, 0, null)
+    rc = fwd(1, 4, 1, 1, 8, 8, 64, 7, 0, 0, 0)
     assert rc == gdn_lib.GDN_ERR_INVALID and b"dtype" in lib.gdn_last_error()
-    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 1, 1, 8, 8, 64, 0, 0, 9, 0, null)
+    rc = fwd(1, 4, 1, 1, 8, 8, 64, 0, 0, 9, 0)
     assert rc == gdn_lib.GDN_ERR_INVALID
-    rc = lib.gdn_fwd(*([null] * 10), 1, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0, null)
+    rc = fwd(1, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0)
     assert rc == gdn_lib.GDN_ERR_INVALID and b"null" in lib.gdn_last_error()
-    need = lib.gdn_bwd_workspace_bytes(1, 4, 1, 1, 8, 8, 64, 0, 0)
-    assert need > 0 and lib.gdn_bwd_workspace_bytes(1, 4, 1, 1, 8, 8, 0, 0, 0) == 0
-    fake = ctypes.c_void_p(256)   # never dereferenced: the size check fails first
-    args = [fake] * 17
-    rc = lib.gdn_bwd(*args, need - 1, 1, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0, 0, null)
+    # the chunked form cannot run a vector gate, and says so
+    rc = fwd(1, 4, 1, 1, 128, 128, 64, 0, 0, gdn_lib.GATE_DECAY_VEC, gdn_lib.FORM_CHUNK)
+    assert rc == gdn_lib.GDN_ERR_UNSUPPORTED and b"chunked form" in lib.gdn_last_error()
+    # the chunked form needs its saved buffer even for a forward-only call
+    fake = ctypes.c_void_p(256)   # never dereferenced: the size checks fail first
+    rc = lib.gdn_fwd(*([fake] * 6), null, fake, fake, null, 0, 1, 4, 1, 1, 128, 128, 64, 0, 0, 2, 0, null)
+    assert rc == gdn_lib.GDN_ERR_WORKSPACE
+    need = lib.gdn_bwd_workspace_bytes(1, 4, 1, 1, 8, 8, 64, 0, 0, 0)
+    assert need > 0 and lib.gdn_bwd_workspace_bytes(1, 4, 1, 1, 8, 8, 0, 0, 0, 0) == 0
+    rc = lib.gdn_bwd(*([fake] * 8), 0, *([fake] * 9), need - 1, 1, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0, 0, null)
     assert rc == gdn_lib.GDN_ERR_WORKSPACE
     # B == 0 is a no-op
-    assert lib.gdn_fwd(*([null] * 10), 0, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0, null) == 0
+    assert fwd(0, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0) == 0
+
+
+def test_saved_sizes_by_form():
+    lib = gdn_lib.load()
+    L = gdn_lib
+    rec = lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_RECURRENT)
+    assert rec == 63 * 32 * 128 * 128 * 4
+    ck = lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_AUTO)
+    assert ck == lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_CHUNK) > rec
+    assert lib.gdn_select_form(128, 128, 0, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK
+    assert lib.gdn_select_form(128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(8, 8, 0, L.GATE_DECAY, L.FORM_AUTO) == L.FORM_RECURRENT
 
 
 def test_workspace_scales_with_row_blocks_and_tokens():
     lib = gdn_lib.load()
-    a = lib.gdn_bwd_workspace_bytes(1, 4096, 16, 32, 128, 128, 64, 0, 0)
-    b = lib.gdn_bwd_workspace_bytes(1, 8192, 16, 32, 128, 128, 64, 0, 0)
+    a = lib.gdn_bwd_workspace_bytes(1, 4096, 16, 32, 128, 128, 64, 0, 0, 1)
+    b = lib.gdn_bwd_workspace_bytes(1, 8192, 16, 32, 128, 128, 64, 0, 0, 1)
     assert 1.9 < b / a < 2.1
 
 

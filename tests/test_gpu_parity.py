@@ -212,8 +212,9 @@ def test_bf16_inputs_fp32_state(dev):
             assert nerr(a, b) <= 1e-2, (hk, n, nerr(a, b))
 
 
-def test_chunk_invariance_long(dev):
-    """The snapshot interval is an implementation detail: chunk 64 vs 256 vs 1000 agree at T=1500."""
+def test_chunk_invariance_long(dev, monkeypatch):
+    """The recurrent form's snapshot interval is an implementation detail: chunk 64 vs 256 vs 1000 agree."""
+    monkeypatch.setenv("GDN_FORM", "recurrent")
     c = _workload(1500, s0_std=0.02, seed=4)
     base = run_gpu(c, dev, 64)
     for chunk in (256, 1000):
