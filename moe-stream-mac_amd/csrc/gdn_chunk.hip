@@ -68,31 +68,74 @@ __device__ __forceinline__ void mma16(f4 &acc, const float *A, int asr, int asc,
     }
 }
 
+// A 16-row strip of NTILES output tiles sharing one A operand: acc[t] += A(16 x K) * B_t(K x 16), where B_t
+// starts at B + t * btile.  Each A fragment is loaded (and converted / split) once per k-step for all tiles.
+template <int MT, int K, int NTILES, bool SA = false, bool SB = false>
+__device__ __forceinline__ void mma_strip(f4 (&acc)[NTILES], const float *A, int asr, int asc, const float *B,
+                                          int bsr, int bsc, int btile) {
+    const int l = threadIdx.x & 63, li = l & 15, lg = l >> 4;
+    if constexpr (MT == 0) {
+#pragma unroll 4
+        for (int k0 = 0; k0 < K; k0 += 4) {
+            const float av = A[li * asr + (k0 + lg) * asc];
+#pragma unroll
+            for (int t = 0; t < NTILES; ++t) {
+                const float bv = B[t * btile + (k0 + lg) * bsr + li * bsc];
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[t], 0, 0, 0);
+            }
+        }
+    } else {
+#pragma unroll 1
+        for (int k0 = 0; k0 < K; k0 += 32) {
+            bf8 ah, al;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x = A[li * asr + (k0 + 8 * lg + i) * asc];
+                ah[i] = (__bf16)x;
+                if constexpr (SA) al[i] = (__bf16)(x - (float)ah[i]);
+            }
+#pragma unroll
+            for (int t = 0; t < NTILES; ++t) {
+                bf8 bh, bl;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float y = B[t * btile + (k0 + 8 * lg + i) * bsr + li * bsc];
+                    bh[i] = (__bf16)y;
+                    if constexpr (SB) bl[i] = (__bf16)(y - (float)bh[i]);
+                }
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc[t], 0, 0, 0);
+                if constexpr (SA) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc[t], 0, 0, 0);
+                if constexpr (SB) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc[t], 0, 0, 0);
+            }
+        }
+    }
+}
+
 // Copy a [ROWS][COLS] tile (rows strided by src_stride elements, dtype dt) into LDS as fp32 with row stride
 // lds_stride, multiplying row r by scale[r] when scale is given.  Rows >= n are zero.  Every load is 16 bytes
 // and all of a thread's loads are issued before the first LDS store, so the tile costs one memory latency.
-template <int ROWS, int COLS>
+template <int ROWS, int COLS, int NTH = NT>
 __device__ __forceinline__ void load_tile(float *dst, int lds_stride, const void *src, size_t src_stride, int n,
                                           int dt, const float *scale = nullptr) {
     const int tid = threadIdx.x;
     constexpr int BATCH = 8;  // 16-byte loads in flight per thread
     if (dt == DT_F32) {
         constexpr int VPR = COLS / 4;
-        constexpr int PER = ROWS * VPR / NT;
-        static_assert(PER * NT == ROWS * VPR, "tile must split evenly");
+        constexpr int PER = ROWS * VPR / NTH;
+        static_assert(PER * NTH == ROWS * VPR, "tile must split evenly");
 #pragma unroll
         for (int p0 = 0; p0 < PER; p0 += BATCH) {
             constexpr int NB = PER < BATCH ? PER : BATCH;
             float4 buf[NB];
 #pragma unroll
             for (int p = 0; p < NB; ++p) {
-                const int v = tid + (p0 + p) * NT, r = v / VPR, c4 = (v - r * VPR) * 4;
+                const int v = tid + (p0 + p) * NTH, r = v / VPR, c4 = (v - r * VPR) * 4;
                 buf[p] = r < n ? *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + r * src_stride + c4)
                                : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (int p = 0; p < NB; ++p) {
-                const int v = tid + (p0 + p) * NT, r = v / VPR, c4 = (v - r * VPR) * 4;
+                const int v = tid + (p0 + p) * NTH, r = v / VPR, c4 = (v - r * VPR) * 4;
                 const float sc = scale ? scale[r] : 1.f;
                 float *d = dst + r * lds_stride + c4;
                 d[0] = buf[p].x * sc; d[1] = buf[p].y * sc; d[2] = buf[p].z * sc; d[3] = buf[p].w * sc;
@@ -100,21 +143,21 @@ __device__ __forceinline__ void load_tile(float *dst, int lds_stride, const void
         }
     } else {
         constexpr int VPR = COLS / 8;
-        constexpr int PER = ROWS * VPR / NT;
-        static_assert(PER * NT == ROWS * VPR, "tile must split evenly");
+        constexpr int PER = ROWS * VPR / NTH;
+        static_assert(PER * NTH == ROWS * VPR, "tile must split evenly");
 #pragma unroll
         for (int p0 = 0; p0 < PER; p0 += BATCH) {
             constexpr int NB = PER < BATCH ? PER : BATCH;
             uint4 buf[NB];
 #pragma unroll
             for (int p = 0; p < NB; ++p) {
-                const int v = tid + (p0 + p) * NT, r = v / VPR, c8 = (v - r * VPR) * 8;
+                const int v = tid + (p0 + p) * NTH, r = v / VPR, c8 = (v - r * VPR) * 8;
                 buf[p] = r < n ? *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(src) + r * src_stride + c8)
                                : make_uint4(0u, 0u, 0u, 0u);
             }
 #pragma unroll
             for (int p = 0; p < NB; ++p) {
-                const int v = tid + (p0 + p) * NT, r = v / VPR, c8 = (v - r * VPR) * 8;
+                const int v = tid + (p0 + p) * NTH, r = v / VPR, c8 = (v - r * VPR) * 8;
                 const float sc = scale ? scale[r] : 1.f;
                 float *d = dst + r * lds_stride + c8;
                 const uint32_t w4[4] = {buf[p].x, buf[p].y, buf[p].z, buf[p].w};
@@ -136,18 +179,89 @@ __device__ __forceinline__ void load_tile(float *dst, int lds_stride, const void
     }
 }
 
+// Register staging for prefetch: a [ROWS][COLS] tile fetched as raw 16-byte quads (fp32: 4 elements, 16-bit
+// dtypes: 8), later written to LDS as fp32.  Rows >= n read as zero.
+template <int ROWS, int COLS, int NTH>
+struct TileRegs {
+    static constexpr int TOTAL_F32 = ROWS * COLS / 4;
+    static constexpr int MAXQ = (TOTAL_F32 + NTH - 1) / NTH;
+    uint4 q[MAXQ];
+};
+
+template <int ROWS, int COLS, int NTH>
+__device__ __forceinline__ void tile_fetch(TileRegs<ROWS, COLS, NTH> &R, const void *src, size_t src_stride, int n,
+                                           int dt) {
+    const int tid = threadIdx.x;
+    const int epq = dt == DT_F32 ? 4 : 8;               // elements per quad
+    const int vpr = COLS / epq, total = ROWS * vpr;
+    const int esz = dt == DT_F32 ? 4 : 2;
+#pragma unroll
+    for (int p = 0; p < TileRegs<ROWS, COLS, NTH>::MAXQ; ++p) {
+        const int v = tid + p * NTH, r = v / vpr, c = (v - r * vpr) * epq;
+        R.q[p] = (v < total && r < n)
+                     ? *reinterpret_cast<const uint4 *>(static_cast<const char *>(src) + (r * src_stride + c) * esz)
+                     : make_uint4(0u, 0u, 0u, 0u);
+    }
+}
+
+__device__ __forceinline__ void unpack16(uint32_t w, int dt, float &lo, float &hi) {
+    if (dt == DT_BF16) {
+        lo = __uint_as_float(w << 16);
+        hi = __uint_as_float(w & 0xffff0000u);
+    } else {
+        lo = __half2float(__ushort_as_half((unsigned short)(w & 0xffffu)));
+        hi = __half2float(__ushort_as_half((unsigned short)(w >> 16)));
+    }
+}
+
+// Write a fetched tile to LDS (row stride lds_stride), row r multiplied by scale(r) when given.
+template <int ROWS, int COLS, int NTH, typename Scale>
+__device__ __forceinline__ void tile_store(float *dst, int lds_stride, const TileRegs<ROWS, COLS, NTH> &R, int dt,
+                                           Scale scale) {
+    const int tid = threadIdx.x;
+    const int epq = dt == DT_F32 ? 4 : 8;
+    const int vpr = COLS / epq, total = ROWS * vpr;
+#pragma unroll
+    for (int p = 0; p < TileRegs<ROWS, COLS, NTH>::MAXQ; ++p) {
+        const int v = tid + p * NTH, r = v / vpr, c = (v - r * vpr) * epq;
+        if (v < total) {
+            const float sc = scale(r);
+            float *d = dst + r * lds_stride + c;
+            if (dt == DT_F32) {
+                d[0] = __uint_as_float(R.q[p].x) * sc;
+                d[1] = __uint_as_float(R.q[p].y) * sc;
+                d[2] = __uint_as_float(R.q[p].z) * sc;
+                d[3] = __uint_as_float(R.q[p].w) * sc;
+            } else {
+                const uint32_t w4[4] = {R.q[p].x, R.q[p].y, R.q[p].z, R.q[p].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    float lo, hi;
+                    unpack16(w4[k], dt, lo, hi);
+                    d[2 * k] = lo * sc;
+                    d[2 * k + 1] = hi * sc;
+                }
+            }
+        }
+    }
+}
+
+struct NoScale {
+    __device__ float operator()(int) const { return 1.f; }
+};
+
 __device__ __forceinline__ const void *elem_ptr(const void *p, size_t idx, int dt) {
     return static_cast<const char *>(p) + idx * (dt == DT_F32 ? 4 : 2);
 }
 
 // Write the [D][D] state slab [i0, i0+VS) x [0, D) from its LDS copy sH ([j][ii], stride LV) to global in the
 // reference layout S[i][j], one contiguous row of S per pass (coalesced along j).
-template <int VS, int LV>
+template <int VS, int LV, int NTH>
 __device__ __forceinline__ void store_state_slice(float *dst, const float *sH, int i0) {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int p = 0; p < VS * D / NT; ++p) {
-        const int v = tid + p * NT, ii = v / D, j = v - ii * D;
+    for (int p = 0; p < VS * D / NTH; ++p) {
+        const int v = tid + p * NTH, ii = v / D, j = v - ii * D;
         dst[(size_t)(i0 + ii) * D + j] = sH[j * LV + ii];
     }
 }
@@ -312,198 +426,253 @@ __global__ __launch_bounds__(NT) void ck_prep_kernel(Args a) {
 
 // ---------------------------------------------------------------------------------------------- ck_fwd
 
+constexpr int NTS = 512;  // sequential kernels: 8 waves
+
+// Row scalings read the chunk's cumulative log decays from LDS: gamma_r = exp(G_r), rc_r = exp(G_{C-1} - G_r).
+struct GamScale {
+    const double *G;
+    __device__ float operator()(int r) const { return expf((float)G[r]); }
+};
+struct RcScale {
+    const double *G;
+    __device__ float operator()(int r) const { return expf((float)(G[C - 1] - G[r])); }
+};
+
 template <int MT, int VS>
-__global__ __launch_bounds__(NT) void ck_fwd_kernel(Args a) {
+__global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
     constexpr int LV = VS + 4;
-    constexpr int NTN = VS / 16;
+    constexpr int NTN = VS / 16;                 // value tiles of the slice
+    constexpr int DN = NTN >= 2 ? NTN / 2 : 1;   // value tiles per wave for [C][VS] products
     __shared__ __align__(16) float sW[C * LD];  // W, then P (stride LDC)
-    __shared__ __align__(16) float sQ[C * LD];  // gamma Q, then K diag(gamma_C / gamma)
+    __shared__ __align__(16) float sQ[C * LD];  // Q, then K diag(gamma_C / gamma)
     __shared__ __align__(16) float sU[C * LV];
     __shared__ __align__(16) float sH[D * LV];  // h slice, [j][i]
     __shared__ __align__(16) float sD[C * LV];  // Delta slice
     __shared__ double sG[C];
-    __shared__ float sGam[C], sRc[C];
 
     const int i0 = blockIdx.x * VS, hv = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
     const size_t head = (size_t)b * a.Hv + hv;
+    const size_t qk_row = (size_t)a.Hk * D;
+    const int mrow = 16 * (w & 3);                              // rows of this wave's [C][VS] tiles
+    const bool cwave = NTN >= 2 || w < 4;                       // waves that own [C][VS] tiles
+    const int nt0 = NTN >= 2 ? (w >> 2) * DN : 0;               // first value tile of those
 
-    f4 h[2][NTN];
+    f4 h[NTN];  // rows j = 16w.., value tiles 0..NTN-1
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int t = 0; t < NTN; ++t)
 #pragma unroll
-        for (int nt = 0; nt < NTN; ++nt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = 16 * (2 * w + mi) + 4 * lg + e, i = i0 + 16 * nt + li;
-                h[mi][nt][e] = a.state0 ? a.state0[(head * D + i) * D + j] : 0.f;
-            }
+        for (int e = 0; e < 4; ++e) {
+            const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
+            h[t][e] = a.state0 ? a.state0[(head * D + i) * D + j] : 0.f;
+        }
+    TileRegs<C, D, NTS> rW, rQ, rK;
+    TileRegs<C, VS, NTS> rU;
+    TileRegs<C, C, NTS> rP;
+    double rG = 0.0;
+    auto fetchA = [&](int c) {
+        const size_t ci = head * a.NC + c;
+        const size_t qk0 = (((size_t)b * T + c * C) * a.Hk + hk) * D;
+        const int n = min(C, T - c * C);
+        tile_fetch(rW, a.w.W + ci * C * D, D, C, DT_F32);
+        tile_fetch(rU, a.w.U + ci * C * D + i0, D, C, DT_F32);
+        tile_fetch(rQ, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
+        if (tid < C) rG = a.w.G[ci * C + tid];
+    };
+    auto fetchB = [&](int c) {
+        const size_t ci = head * a.NC + c;
+        const size_t qk0 = (((size_t)b * T + c * C) * a.Hk + hk) * D;
+        const int n = min(C, T - c * C);
+        tile_fetch(rP, a.w.P + ci * C * C, C, C, DT_F32);
+        tile_fetch(rK, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
+    };
+    fetchA(0);
+    fetchB(0);
     for (int c = 0; c < a.NC; ++c) {
         const int t0 = c * C, n = min(C, T - t0);
         const size_t ci = head * a.NC + c;
         __syncthreads();
-        const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int t = 0; t < NTN; ++t)
 #pragma unroll
-            for (int nt = 0; nt < NTN; ++nt)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sH[(16 * (2 * w + mi) + 4 * lg + e) * LV + 16 * nt + li] = h[mi][nt][e];
-        if (tid < C) sG[tid] = a.w.G[ci * C + tid];
+            for (int e = 0; e < 4; ++e) sH[(16 * w + 4 * lg + e) * LV + 16 * t + li] = h[t][e];
+        tile_store(sW, LD, rW, DT_F32, NoScale{});
+        tile_store(sU, LV, rU, DT_F32, NoScale{});
+        tile_store(sQ, LD, rQ, a.in_dt, NoScale{});
+        if (tid < C) sG[tid] = rG;
         __syncthreads();
-        if (tid < C) {
-            sGam[tid] = expf((float)sG[tid]);
-            sRc[tid] = expf((float)(sG[C - 1] - sG[tid]));
-        }
-        store_state_slice<VS, LV>(a.w.H + ci * D * D, sH, i0);
-        load_tile<C, D>(sW, LD, a.w.W + ci * C * D, D, C, DT_F32);
-        load_tile<C, VS>(sU, LV, a.w.U + ci * C * D + i0, D, C, DT_F32);
-        __syncthreads();
-        load_tile<C, D>(sQ, LD, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt, sGam);
-        __syncthreads();
-        f4 yi[NTN];
+        if (c + 1 < a.NC) fetchA(c + 1);
+        store_state_slice<VS, LV, NTS>(a.w.H + ci * D * D, sH, i0);
+        // Delta = U - W h ; Yi = Q h
+        f4 wh[DN], yi[DN];
 #pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) {
-            f4 wh = zero4();
-            yi[nt] = zero4();
-            mma16<MT, D>(wh, sW + 16 * w * LD, LD, 1, sH + 16 * nt, LV, 1);
-            mma16<MT, D, true, true>(yi[nt], sQ + 16 * w * LD, LD, 1, sH + 16 * nt, LV, 1);
+        for (int t = 0; t < DN; ++t) wh[t] = yi[t] = zero4();
+        if (cwave) {
+            mma_strip<MT, D, DN>(wh, sW + mrow * LD, LD, 1, sH + 16 * nt0, LV, 1, 16);
+            mma_strip<MT, D, DN, false, true>(yi, sQ + mrow * LD, LD, 1, sH + 16 * nt0, LV, 1, 16);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = 16 * w + 4 * lg + e, ii = 16 * nt + li;
-                const float dl = sU[r * LV + ii] - wh[e];
-                sD[r * LV + ii] = dl;
-                a.w.Dl[ci * C * D + r * D + i0 + ii] = dl;
-            }
+            for (int t = 0; t < DN; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = mrow + 4 * lg + e, ii = 16 * (nt0 + t) + li;
+                    const float dl = sU[r * LV + ii] - wh[t][e];
+                    sD[r * LV + ii] = dl;
+                    a.w.Dl[ci * C * D + r * D + i0 + ii] = dl;
+                }
         }
         __syncthreads();
-        load_tile<C, C>(sW, LDC, a.w.P + ci * C * C, C, C, DT_F32);
-        load_tile<C, D>(sQ, LD, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt, sRc);
+        tile_store(sW, LDC, rP, DT_F32, NoScale{});
+        tile_store(sQ, LD, rK, a.in_dt, RcScale{sG});
         __syncthreads();
+        if (c + 1 < a.NC) fetchB(c + 1);
+        if (cwave) {
+            // Y = diag(gamma) Q h + P Delta
 #pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) {
-            mma16<MT, C, true, true>(yi[nt], sW + 16 * w * LDC, LDC, 1, sD + 16 * nt, LV, 1);
+            for (int t = 0; t < DN; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = 16 * w + 4 * lg + e, ii = 16 * nt + li;
-                if (r < n)
-                    store_from_f32(a.y, (((size_t)b * T + t0 + r) * a.Hv + hv) * D + i0 + ii, yi[nt][e], a.out_dt);
-            }
+                for (int e = 0; e < 4; ++e) yi[t][e] *= expf((float)sG[mrow + 4 * lg + e]);
+            mma_strip<MT, C, DN, true, true>(yi, sW + mrow * LDC, LDC, 1, sD + 16 * nt0, LV, 1, 16);
+#pragma unroll
+            for (int t = 0; t < DN; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = mrow + 4 * lg + e, ii = 16 * (nt0 + t) + li;
+                    if (r < n)
+                        store_from_f32(a.y, (((size_t)b * T + t0 + r) * a.Hv + hv) * D + i0 + ii, yi[t][e],
+                                       a.out_dt);
+                }
         }
-        const float gC = sGam[C - 1];
+        // h = gamma_C h + Ktilde^T Delta
+        const float gC = expf((float)sG[C - 1]);
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int nt = 0; nt < NTN; ++nt) {
-                h[mi][nt] *= gC;
-                mma16<MT, C>(h[mi][nt], sQ + 16 * (2 * w + mi), 1, LD, sD + 16 * nt, LV, 1);
-            }
+        for (int t = 0; t < NTN; ++t) h[t] *= gC;
+        mma_strip<MT, C, NTN>(h, sQ + 16 * w, 1, LD, sD, LV, 1, 16);
     }
     if (a.state_T) {
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int t = 0; t < NTN; ++t)
 #pragma unroll
-            for (int nt = 0; nt < NTN; ++nt)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int j = 16 * (2 * w + mi) + 4 * lg + e, i = i0 + 16 * nt + li;
-                    a.state_T[(head * D + i) * D + j] = h[mi][nt][e];
-                }
+            for (int e = 0; e < 4; ++e) {
+                const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
+                a.state_T[(head * D + i) * D + j] = h[t][e];
+            }
     }
 }
 
 // ---------------------------------------------------------------------------------------------- ck_bwd_seq
 
 template <int MT, int VS>
-__global__ __launch_bounds__(NT) void ck_bwd_seq_kernel(Args a) {
+__global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
     constexpr int LV = VS + 4;
     constexpr int NTN = VS / 16;
-    __shared__ __align__(16) float sW[C * LD];  // P (stride LDC), then W
-    __shared__ __align__(16) float sQ[C * LD];  // K diag(gamma_C / gamma), then gamma Q
-    __shared__ __align__(16) float sY[C * LV];  // dY slice
-    __shared__ __align__(16) float sH[D * LV];  // dh slice, [j][i]
-    __shared__ __align__(16) float sD[C * LV];  // dDelta slice
+    constexpr int DN = NTN >= 2 ? NTN / 2 : 1;
+    __shared__ __align__(16) float sW[C * LD];   // P (stride LDC), then W
+    __shared__ __align__(16) float sQ[C * LD];   // K, then Q
+    __shared__ __align__(16) float sY[C * LV];   // dY slice
+    __shared__ __align__(16) float sYg[C * LV];  // diag(gamma) dY slice
+    __shared__ __align__(16) float sH[D * LV];   // dh slice, [j][i]
+    __shared__ __align__(16) float sD[C * LV];   // dDelta slice
     __shared__ double sG[C];
-    __shared__ float sGam[C], sRc[C];
 
     const int i0 = blockIdx.x * VS, hv = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
     const size_t head = (size_t)b * a.Hv + hv;
+    const size_t qk_row = (size_t)a.Hk * D, v_row = (size_t)a.Hv * D;
+    const int mrow = 16 * (w & 3);
+    const bool cwave = NTN >= 2 || w < 4;
+    const int nt0 = NTN >= 2 ? (w >> 2) * DN : 0;
 
-    f4 dh[2][NTN];
+    f4 dh[NTN];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int t = 0; t < NTN; ++t)
 #pragma unroll
-        for (int nt = 0; nt < NTN; ++nt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = 16 * (2 * w + mi) + 4 * lg + e, i = i0 + 16 * nt + li;
-                dh[mi][nt][e] = a.dstate_T ? a.dstate_T[(head * D + i) * D + j] : 0.f;
-            }
+        for (int e = 0; e < 4; ++e) {
+            const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
+            dh[t][e] = a.dstate_T ? a.dstate_T[(head * D + i) * D + j] : 0.f;
+        }
+    TileRegs<C, C, NTS> rP;
+    TileRegs<C, D, NTS> rK, rW, rQ;
+    TileRegs<C, VS, NTS> rY;
+    double rG = 0.0;
+    auto fetchA = [&](int c) {
+        const size_t ci = head * a.NC + c;
+        const size_t qk0 = (((size_t)b * T + c * C) * a.Hk + hk) * D;
+        const size_t v0 = (((size_t)b * T + c * C) * a.Hv + hv) * D;
+        const int n = min(C, T - c * C);
+        tile_fetch(rP, a.w.P + ci * C * C, C, C, DT_F32);
+        tile_fetch(rK, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
+        tile_fetch(rY, elem_ptr(a.dy, v0 + i0, a.dy_dt), v_row, n, a.dy_dt);
+        if (tid < C) rG = a.w.G[ci * C + tid];
+    };
+    auto fetchB = [&](int c) {
+        const size_t ci = head * a.NC + c;
+        const size_t qk0 = (((size_t)b * T + c * C) * a.Hk + hk) * D;
+        const int n = min(C, T - c * C);
+        tile_fetch(rW, a.w.W + ci * C * D, D, C, DT_F32);
+        tile_fetch(rQ, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
+    };
+    fetchA(a.NC - 1);
+    fetchB(a.NC - 1);
     for (int c = a.NC - 1; c >= 0; --c) {
-        const int t0 = c * C, n = min(C, T - t0);
         const size_t ci = head * a.NC + c;
         __syncthreads();
-        const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
-        const size_t v0 = (((size_t)b * T + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int t = 0; t < NTN; ++t)
 #pragma unroll
-            for (int nt = 0; nt < NTN; ++nt)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sH[(16 * (2 * w + mi) + 4 * lg + e) * LV + 16 * nt + li] = dh[mi][nt][e];
-        if (tid < C) sG[tid] = a.w.G[ci * C + tid];
+            for (int e = 0; e < 4; ++e) sH[(16 * w + 4 * lg + e) * LV + 16 * t + li] = dh[t][e];
+        tile_store(sW, LDC, rP, DT_F32, NoScale{});
+        tile_store(sQ, LD, rK, a.in_dt, NoScale{});
+        tile_store(sY, LV, rY, a.dy_dt, NoScale{});
+        if (tid < C) sG[tid] = rG;
         __syncthreads();
-        if (tid < C) {
-            sGam[tid] = expf((float)sG[tid]);
-            sRc[tid] = expf((float)(sG[C - 1] - sG[tid]));
-        }
-        store_state_slice<VS, LV>(a.w.dH + ci * D * D, sH, i0);
-        load_tile<C, C>(sW, LDC, a.w.P + ci * C * C, C, C, DT_F32);
-        load_tile<C, VS>(sY, LV, elem_ptr(a.dy, v0 + i0, a.dy_dt), v_row, n, a.dy_dt);
-        __syncthreads();
-        load_tile<C, D>(sQ, LD, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt, sRc);
-        __syncthreads();
+        tile_store(sYg, LV, rY, a.dy_dt, GamScale{sG});   // before rY is refilled
+        if (c > 0) fetchA(c - 1);
+        store_state_slice<VS, LV, NTS>(a.w.dH + ci * D * D, sH, i0);
+        // dDelta = diag(gamma_C / gamma) K dh' + P^T dY
+        if (cwave) {
+            f4 kd[DN], pd[DN];
 #pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) {
-            f4 dd = zero4();
-            mma16<MT, D, true, true>(dd, sQ + 16 * w * LD, LD, 1, sH + 16 * nt, LV, 1);
-            mma16<MT, C, true, false>(dd, sW + 16 * w, 1, LDC, sY + 16 * nt, LV, 1);
+            for (int t = 0; t < DN; ++t) kd[t] = pd[t] = zero4();
+            mma_strip<MT, D, DN, false, true>(kd, sQ + mrow * LD, LD, 1, sH + 16 * nt0, LV, 1, 16);
+            mma_strip<MT, C, DN, true, false>(pd, sW + mrow, 1, LDC, sY + 16 * nt0, LV, 1, 16);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = 16 * w + 4 * lg + e, ii = 16 * nt + li;
-                sD[r * LV + ii] = dd[e];
-                a.w.dDl[ci * C * D + r * D + i0 + ii] = dd[e];
-            }
+            for (int t = 0; t < DN; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = mrow + 4 * lg + e, ii = 16 * (nt0 + t) + li;
+                    const float dd = kd[t][e] * expf((float)(sG[C - 1] - sG[r])) + pd[t][e];
+                    sD[r * LV + ii] = dd;
+                    a.w.dDl[ci * C * D + r * D + i0 + ii] = dd;
+                }
         }
         __syncthreads();
-        load_tile<C, D>(sW, LD, a.w.W + ci * C * D, D, C, DT_F32);
-        load_tile<C, D>(sQ, LD, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt, sGam);
+        tile_store(sW, LD, rW, DT_F32, NoScale{});
+        tile_store(sQ, LD, rQ, a.in_dt, NoScale{});
         __syncthreads();
-        const float gC = sGam[C - 1];
+        if (c > 0) fetchB(c - 1);
+        // dh = gamma_C dh' + Q^T diag(gamma) dY - W^T dDelta
+        const float gC = expf((float)sG[C - 1]);
+        f4 wd[NTN];
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int t = 0; t < NTN; ++t) {
+            dh[t] *= gC;
+            wd[t] = zero4();
+        }
+        mma_strip<MT, C, NTN, false, true>(dh, sQ + 16 * w, 1, LD, sYg, LV, 1, 16);
+        mma_strip<MT, C, NTN>(wd, sW + 16 * w, 1, LD, sD, LV, 1, 16);
 #pragma unroll
-            for (int nt = 0; nt < NTN; ++nt) {
-                f4 wd = zero4();
-                dh[mi][nt] *= gC;
-                mma16<MT, C, true, false>(dh[mi][nt], sQ + 16 * (2 * w + mi), 1, LD, sY + 16 * nt, LV, 1);
-                mma16<MT, C>(wd, sW + 16 * (2 * w + mi), 1, LD, sD + 16 * nt, LV, 1);
-                dh[mi][nt] -= wd;
-            }
+        for (int t = 0; t < NTN; ++t) dh[t] -= wd[t];
     }
     if (a.dstate0) {
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int t = 0; t < NTN; ++t)
 #pragma unroll
-            for (int nt = 0; nt < NTN; ++nt)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int j = 16 * (2 * w + mi) + 4 * lg + e, i = i0 + 16 * nt + li;
-                    a.dstate0[(head * D + i) * D + j] = dh[mi][nt][e];
-                }
+            for (int e = 0; e < 4; ++e) {
+                const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
+                a.dstate0[(head * D + i) * D + j] = dh[t][e];
+            }
     }
 }
 
@@ -520,18 +689,22 @@ __device__ __forceinline__ float wave_sum(float x) {
 // dG_s'.  The gradient of the per-token log decay g_u is then the sum of the pair terms whose span straddles
 // u:  dg_u = sum_{r >= u} sum_{s' < u} E[r][s'].  Summing only straddling terms (each carrying the factor
 // exp(g_u)) keeps dg accurate for tiny decays, where a reverse cumulative sum of dG would cancel.
+constexpr int NTB = 512;  // ck_bwd_local: 8 waves; waves w and w+4 share the 16-row strip w%4 (column halves)
+
 template <int MT>
-__global__ __launch_bounds__(NT) void ck_bwd_local_kernel(Args a) {
+__global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     __shared__ __align__(16) float R1[D * LD];       // h / dh' ([i][j]); then K at R1, Q / dW at R1 + C*LD
     __shared__ __align__(16) float R2[C * LD];       // dY, then dDelta, then the pair matrix E
     __shared__ __align__(16) float RX[2 * C * LDC];  // V ([C][LD] fits), then R3 = RX (Y1), R4 = RX + C*LDC
     __shared__ __align__(16) float R5[C * LDC];      // T
     __shared__ double sG[C];
     __shared__ float sGam[C], sRc[C], sB[C], sEb[C], sT2[C], sDg[C];
-    __shared__ float sLast[4];
+    __shared__ float sRow[3][2][C];                  // per column half: chunk-start pair terms, t2 terms, dbeta
+    __shared__ float sLast[8];
 
     const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
+    const int r0 = 16 * (w & 3), ch = w >> 2;  // this wave's rows r0..r0+15 and column half
     const int T = a.T, hk = hv / (a.Hv / a.Hk), t0 = c * C, n = min(C, T - t0);
     const size_t ci = chunk_index(a, b, hv, c);
     float *const sKm = R1;
@@ -542,6 +715,8 @@ __global__ __launch_bounds__(NT) void ck_bwd_local_kernel(Args a) {
     const float *dHc = a.w.dH + ci * D * D;
     const float *Dc = a.w.Dl + ci * C * D;
     const float *dDc = a.w.dDl + ci * C * D;
+    const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
+    const size_t v0 = (((size_t)b * T + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
     // dW of this chunk is parked in its rows of the dq|dk output buffer until it is needed (rows >= n of dW
     // are zero: padded tokens have k = 0, so their dDelta vanishes)
     float *const dWpark = a.w.part + ((size_t)b * T + t0) * a.Hv * 2 * D + (size_t)hv * 2 * D;
@@ -554,10 +729,8 @@ __global__ __launch_bounds__(NT) void ck_bwd_local_kernel(Args a) {
         if (tid < n) bt = a.beta[((size_t)b * T + t0 + tid) * a.Hv + hv];
         sB[tid] = bt;
     }
-    const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
-    const size_t v0 = (((size_t)b * T + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
-    load_tile<D, D>(R1, LD, Hc, D, D, DT_F32);
-    load_tile<C, D>(R2, LD, elem_ptr(a.dy, v0, a.dy_dt), v_row, n, a.dy_dt);
+    load_tile<D, D, NTB>(R1, LD, Hc, D, D, DT_F32);
+    load_tile<C, D, NTB>(R2, LD, elem_ptr(a.dy, v0, a.dy_dt), v_row, n, a.dy_dt);
     __syncthreads();
     if (tid < C) {
         sGam[tid] = expf((float)sG[tid]);
@@ -565,203 +738,203 @@ __global__ __launch_bounds__(NT) void ck_bwd_local_kernel(Args a) {
     }
     __syncthreads();
     const float gC = sGam[C - 1];
-    float bnd[4] = {0.f, 0.f, 0.f, 0.f};   // pair terms (r, chunk start) of rows 16w+4lg+e, this lane's columns
+    float bnd[4] = {0.f, 0.f, 0.f, 0.f};   // pair terms (r, chunk start) of rows r0+4lg+e, this lane's columns
     float rowB[4] = {0.f, 0.f, 0.f, 0.f};  // dbeta partials
+    float tl[4] = {0.f, 0.f, 0.f, 0.f};    // pair terms (C-1, r)
     float lastp = 0.f;                     // pair (C-1, chunk start): gamma_C <dh', h>
-
-    // <dh', h>: h is in R1, dh' streams from global in 16-byte loads, all issued up front
     {
-        constexpr int PER = D * D / 4 / NT;
+        constexpr int PER = D * D / 4 / NTB;
+        float4 dv4[PER];
 #pragma unroll
-        for (int p0 = 0; p0 < PER; p0 += 8) {
-            float4 dv4[8];
+        for (int p = 0; p < PER; ++p) dv4[p] = reinterpret_cast<const float4 *>(dHc)[tid + p * NTB];
 #pragma unroll
-            for (int p = 0; p < 8; ++p) dv4[p] = reinterpret_cast<const float4 *>(dHc)[tid + (p0 + p) * NT];
-#pragma unroll
-            for (int p = 0; p < 8; ++p) {
-                const int v = tid + (p0 + p) * NT, i = v / (D / 4), j = (v - i * (D / 4)) * 4;
-                const float *hh = R1 + i * LD + j;
-                lastp += dv4[p].x * hh[0] + dv4[p].y * hh[1] + dv4[p].z * hh[2] + dv4[p].w * hh[3];
-            }
+        for (int p = 0; p < PER; ++p) {
+            const int v = tid + p * NTB, i = v / (D / 4), j = (v - i * (D / 4)) * 4;
+            const float *hh = R1 + i * LD + j;
+            lastp += dv4[p].x * hh[0] + dv4[p].y * hh[1] + dv4[p].z * hh[2] + dv4[p].w * hh[3];
         }
     }
     lastp *= gC;
 
-    // ---- phase 1: dQ = diag(gamma) dY h^T ; dW = -dDelta h^T (parked in global)
-    f4 dQ[8], dK[8];
+    // ---- phase 1: dQ = diag(gamma) dY h^T ; dW = -dDelta h^T (parked)
+    f4 dQ[4], dK[4];
+    {
+        f4 dw[4];
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-        f4 dw = zero4();
-        dQ[nt] = zero4();
-        mma16<MT, D>(dQ[nt], R2 + 16 * w * LD, LD, 1, R1 + 16 * nt, LD, 1);
-        mma16<MT, D>(dw, dDc + 16 * w * D, D, 1, R1 + 16 * nt, LD, 1);
+        for (int t = 0; t < 4; ++t) dQ[t] = dw[t] = zero4();
+        mma_strip<MT, D, 4>(dQ, R2 + r0 * LD, LD, 1, R1 + 64 * ch, LD, 1, 16);
+        mma_strip<MT, D, 4>(dw, dDc + r0 * D, D, 1, R1 + 64 * ch, LD, 1, 16);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = 16 * w + 4 * lg + e, j = 16 * nt + li;
-            dQ[nt][e] *= sGam[r];
-            if (r < n) dWpark[r * park_row + j] = -dw[e];
-        }
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+                dQ[t][e] *= sGam[r];
+                if (r < n) dWpark[r * park_row + j] = -dw[t][e];
+            }
     }
     __syncthreads();
     // ---- phase 2: dK = diag(gamma_C/gamma) Delta dh'^T ; dP = lower(dY Delta^T)
-    load_tile<D, D>(R1, LD, dHc, D, D, DT_F32);
+    load_tile<D, D, NTB>(R1, LD, dHc, D, D, DT_F32);
     __syncthreads();
-    float tl[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-        dK[nt] = zero4();
-        mma16<MT, D, true, true>(dK[nt], Dc + 16 * w * D, D, 1, R1 + 16 * nt, LD, 1);
+    for (int t = 0; t < 4; ++t) dK[t] = zero4();
+    mma_strip<MT, D, 4, true, true>(dK, Dc + r0 * D, D, 1, R1 + 64 * ch, LD, 1, 16);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            dK[nt][e] *= sRc[16 * w + 4 * lg + e];
-        }
-    }
-    f4 dPG[4], Ep[4];
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-        f4 dp = zero4();
-        mma16<MT, D, false, true>(dp, R2 + 16 * w * LD, LD, 1, Dc + 16 * nt * D, 1, D);
+        for (int e = 0; e < 4; ++e) dK[t][e] *= sRc[r0 + 4 * lg + e];
+    f4 dPG[2], Ep[2];
+    {
+        f4 dp[2] = {zero4(), zero4()};
+        mma_strip<MT, D, 2, false, true>(dp, R2 + r0 * LD, LD, 1, Dc + 32 * ch * D, 1, D, 16 * D);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = 16 * w + 4 * lg + e, s = 16 * nt + li;
-            const float pv = s <= r ? dp[e] : 0.f;
-            Ep[nt][e] = s < r ? pv * a.w.P[ci * C * C + r * C + s] : 0.f;
-            dPG[nt][e] = s <= r ? pv * expf((float)(sG[r] - sG[s])) : 0.f;
-        }
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
+                const float pv = s2 <= r ? dp[t][e] : 0.f;
+                Ep[t][e] = s2 < r ? pv * a.w.P[ci * C * C + r * C + s2] : 0.f;
+                dPG[t][e] = s2 <= r ? pv * expf((float)(sG[r] - sG[s2])) : 0.f;
+            }
     }
     __syncthreads();
     // ---- phase 3: dQ += dPG K ; dK += dPG^T Q
-    load_tile<C, D>(sKm, LD, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
-    load_tile<C, D>(sQm, LD, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
+    load_tile<C, D, NTB>(sKm, LD, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
+    load_tile<C, D, NTB>(sQm, LD, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) R4[(16 * w + 4 * lg + e) * LDC + 16 * nt + li] = dPG[nt][e];
+        for (int e = 0; e < 4; ++e) R4[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = dPG[t][e];
     __syncthreads();
-    // pair terms of the state-entry and state-exit factors, from the dQ / dK parts computed so far
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int r = 16 * w + 4 * lg + e, j = 16 * nt + li;
-            bnd[e] += sQm[r * LD + j] * dQ[nt][e];
-            tl[e] += sKm[r * LD + j] * dK[nt][e];
+            const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+            bnd[e] += sQm[r * LD + j] * dQ[t][e];
+            tl[e] += sKm[r * LD + j] * dK[t][e];
         }
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-        mma16<MT, C, true, false>(dQ[nt], R4 + 16 * w * LDC, LDC, 1, sKm + 16 * nt, LD, 1);
-        mma16<MT, C, true, false>(dK[nt], R4 + 16 * w, 1, LDC, sQm + 16 * nt, LD, 1);
-    }
+    mma_strip<MT, C, 4, true, false>(dQ, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16);
+    mma_strip<MT, C, 4, true, false>(dK, R4 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16);
     __syncthreads();
     // ---- phase 4: through T.  R1b <- dW, R2 <- dDelta, RX <- V, R5 <- T
-    load_tile<C, D>(sQm, LD, dWpark, park_row, n, DT_F32);
-    load_tile<C, D>(R2, LD, dDc, D, C, DT_F32);
-    load_tile<C, D>(RX, LD, elem_ptr(a.v, v0, a.in_dt), v_row, n, a.in_dt);
-    load_tile<C, C>(R5, LDC, a.w.T + ci * C * C, C, C, DT_F32);
+    load_tile<C, D, NTB>(sQm, LD, dWpark, park_row, n, DT_F32);
+    load_tile<C, D, NTB>(R2, LD, dDc, D, C, DT_F32);
+    load_tile<C, D, NTB>(RX, LD, elem_ptr(a.v, v0, a.in_dt), v_row, n, a.in_dt);
+    load_tile<C, C, NTB>(R5, LDC, a.w.T + ci * C * C, C, C, DT_F32);
+    __syncthreads();
+    {
+        f4 tdw[4], tdd[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) tdw[t] = tdd[t] = zero4();
+        mma_strip<MT, C, 4>(tdw, R5 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16);
+        mma_strip<MT, C, 4, true, true>(tdd, R5 + r0, 1, LDC, R2 + 64 * ch, LD, 1, 16);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+                const float bg = sB[r] * sGam[r];
+                dK[t][e] += bg * tdw[t][e];
+                const float s4 = tdw[t][e] * sKm[r * LD + j];
+                rowB[e] += sGam[r] * s4;
+                bnd[e] += bg * s4;
+                rowB[e] += RX[r * LD + j] * tdd[t][e];
+                if (r < n) store_from_f32(a.dv, v0 + (size_t)r * v_row + j, sB[r] * tdd[t][e], a.grad_dt);
+            }
+    }
+    f4 dT[2];
+    {
+        f4 t1[2] = {zero4(), zero4()}, t2[2] = {zero4(), zero4()};
+        mma_strip<MT, D, 2>(t1, R2 + r0 * LD, LD, 1, RX + 32 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<MT, D, 2>(t2, sQm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int s2 = 32 * ch + 16 * t + li;
+                dT[t][e] = sB[s2] * (t1[t][e] + sGam[s2] * t2[t][e]);
+            }
+    }
     __syncthreads();
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-        f4 tdw = zero4(), tdd = zero4();
-        mma16<MT, C>(tdw, R5 + 16 * w, 1, LDC, sQm + 16 * nt, LD, 1);
-        mma16<MT, C, true, true>(tdd, R5 + 16 * w, 1, LDC, R2 + 16 * nt, LD, 1);
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = 16 * w + 4 * lg + e, j = 16 * nt + li;
-            const float bg = sB[r] * sGam[r];
-            dK[nt][e] += bg * tdw[e];
-            const float s4 = tdw[e] * sKm[r * LD + j];
-            rowB[e] += sGam[r] * s4;
-            bnd[e] += bg * s4;
-            rowB[e] += RX[r * LD + j] * tdd[e];
-            if (r < n)
-                store_from_f32(a.dv, (((size_t)b * T + t0 + r) * a.Hv + hv) * D + j, sB[r] * tdd[e], a.grad_dt);
-        }
-    }
-    f4 dT[4];
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-        f4 t1 = zero4(), t2 = zero4();
-        mma16<MT, D>(t1, R2 + 16 * w * LD, LD, 1, RX + 16 * nt * LD, 1, LD);
-        mma16<MT, D>(t2, sQm + 16 * w * LD, LD, 1, sKm + 16 * nt * LD, 1, LD);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int s = 16 * nt + li;
-            dT[nt][e] = sB[s] * (t1[e] + sGam[s] * t2[e]);
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) R4[(16 * w + 4 * lg + e) * LDC + 16 * nt + li] = dT[nt][e];
+        for (int e = 0; e < 4; ++e) R4[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = dT[t][e];
     __syncthreads();
     // ---- phase 5: dA = -T^T dT T^T ; K K^T ; M = diag(beta) dA * Gam
+    {
+        f4 y1[2] = {zero4(), zero4()};
+        mma_strip<MT, C, 2>(y1, R4 + r0 * LDC, LDC, 1, R5 + 32 * ch * LDC, 1, LDC, 16 * LDC);
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-        f4 y1 = zero4();
-        mma16<MT, C>(y1, R4 + 16 * w * LDC, LDC, 1, R5 + 16 * nt * LDC, 1, LDC);
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) R3[(16 * w + 4 * lg + e) * LDC + 16 * nt + li] = y1[e];
+            for (int e = 0; e < 4; ++e) R3[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = y1[t][e];
     }
     __syncthreads();
-    f4 Mt[4];
+    f4 Mt[2];
+    {
+        f4 da[2] = {zero4(), zero4()}, kk[2] = {zero4(), zero4()};
+        mma_strip<MT, C, 2>(da, R5 + r0, 1, LDC, R3 + 32 * ch, LDC, 1, 16);
+        mma_strip<MT, D, 2>(kk, sKm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD);
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-        f4 da = zero4(), kk = zero4();
-        mma16<MT, C>(da, R5 + 16 * w, 1, LDC, R3 + 16 * nt, LDC, 1);
-        mma16<MT, D>(kk, sKm + 16 * w * LD, LD, 1, sKm + 16 * nt * LD, 1, LD);
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = 16 * w + 4 * lg + e, s = 16 * nt + li;
-            const float gam = s < r ? expf((float)(sG[r] - sG[s])) : 0.f;
-            const float dav = s < r ? -da[e] : 0.f;
-            const float kg = kk[e] * gam;
-            rowB[e] += dav * kg;
-            Ep[nt][e] += dav * sB[r] * kg;
-            Mt[nt][e] = sB[r] * dav * gam;
-        }
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
+                const float gam = s2 < r ? expf((float)(sG[r] - sG[s2])) : 0.f;
+                const float dav = s2 < r ? -da[t][e] : 0.f;
+                const float kg = kk[t][e] * gam;
+                rowB[e] += dav * kg;
+                Ep[t][e] += dav * sB[r] * kg;
+                Mt[t][e] = sB[r] * dav * gam;
+            }
     }
     __syncthreads();
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) R4[(16 * w + 4 * lg + e) * LDC + 16 * nt + li] = Mt[nt][e];
+        for (int e = 0; e < 4; ++e) R4[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = Mt[t][e];
     __syncthreads();
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-        mma16<MT, C>(dK[nt], R4 + 16 * w * LDC, LDC, 1, sKm + 16 * nt, LD, 1);
-        mma16<MT, C>(dK[nt], R4 + 16 * w, 1, LDC, sKm + 16 * nt, LD, 1);
-    }
+    mma_strip<MT, C, 4>(dK, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16);
+    mma_strip<MT, C, 4>(dK, R4 + r0, 1, LDC, sKm + 64 * ch, LD, 1, 16);
     // ---- phase 6: straddle sums for dg, dbeta, outputs.  R2 (dDelta) is free: E goes there.
     float *const sE = R2;
     lastp = wave_sum(lastp);
     if (l == 0) sLast[w] = lastp;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sE[(16 * w + 4 * lg + e) * LDC + 16 * nt + li] = Ep[nt][e];
+        for (int e = 0; e < 4; ++e) sE[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = Ep[t][e];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const float bsum = row16_allreduce(bnd[e]);
         const float t2 = row16_allreduce(tl[e]);
         const float rbv = row16_allreduce(rowB[e]);
-        const int r = 16 * w + 4 * lg + e;
+        const int r = r0 + 4 * lg + e;
         if (li == 0) {
-            sEb[r] = bsum;
-            sT2[r] = r < C - 1 ? t2 : 0.f;   // pair (C-1, r); r = C-1 contributes nothing
-            if (r < n) a.dbeta[((size_t)b * T + t0 + r) * a.Hv + hv] = rbv;
+            sRow[0][ch][r] = bsum;
+            sRow[1][ch][r] = t2;
+            sRow[2][ch][r] = rbv;
         }
     }
     __syncthreads();
     if (tid < C) {
-        // row prefix sums of E over s' = 0 .. r-1, in place
+        const int r = tid;
+        float eb = sRow[0][0][r] + sRow[0][1][r];
+        if (r == C - 1)
+            for (int i = 0; i < 8; ++i) eb += sLast[i];
+        sEb[r] = eb;
+        sT2[r] = r < C - 1 ? sRow[1][0][r] + sRow[1][1][r] : 0.f;  // pair (C-1, r)
+        if (r < n) a.dbeta[((size_t)b * T + t0 + r) * a.Hv + hv] = sRow[2][0][r] + sRow[2][1][r];
+        // row prefix sums of E over s' = 0 .. r-1, in place: sE[r][s2] <- sum_{s' < s2} E[r][s']
         float acc = 0.f;
         for (int s2 = 0; s2 < C; ++s2) {
-            const float x = sE[tid * LDC + s2];
-            sE[tid * LDC + s2] = acc;   // = sum_{s' < s2} E[tid][s']
-            acc += s2 < tid ? x : 0.f;
+            const float x = sE[r * LDC + s2];
+            sE[r * LDC + s2] = acc;
+            acc += s2 < r ? x : 0.f;
         }
-        if (tid == C - 1) sEb[tid] += sLast[0] + sLast[1] + sLast[2] + sLast[3];
     }
     __syncthreads();
     if (tid < C) {
@@ -782,14 +955,14 @@ __global__ __launch_bounds__(NT) void ck_bwd_local_kernel(Args a) {
         a.dg[gi] = dgv;
     }
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int r = 16 * w + 4 * lg + e, j = 16 * nt + li;
+            const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
             if (r < n) {
                 const size_t tok = ((size_t)b * T + t0 + r) * a.Hv + hv;
-                a.w.part[tok * 2 * D + j] = dQ[nt][e];
-                a.w.part[tok * 2 * D + D + j] = dK[nt][e];
+                a.w.part[tok * 2 * D + j] = dQ[t][e];
+                a.w.part[tok * 2 * D + D + j] = dK[t][e];
             }
         }
 }
@@ -849,22 +1022,40 @@ static ck::Args make_args(const ChunkCall &cc) {
     return a;
 }
 
-constexpr int CK_VS = 32;
+// Value-slice width of the sequential kernels: the widest slice that still gives about one workgroup per CU
+// (256 CUs), so fewer workgroups re-read the chunk's shared W / Q / K / P tiles.
+static int slice_width(int heads) { return heads >= 128 ? 64 : heads >= 64 ? 32 : 16; }
+
+template <int MT, int VS>
+static void seq_launch(const ck::Args &a, hipStream_t st, bool fwd) {
+    const dim3 grid(CK_D / VS, a.Hv, a.B);
+    if (fwd) hipLaunchKernelGGL((ck::ck_fwd_kernel<MT, VS>), grid, dim3(ck::NTS), 0, st, a);
+    else hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<MT, VS>), grid, dim3(ck::NTS), 0, st, a);
+}
+
+template <int MT>
+static void seq_dispatch(const ck::Args &a, hipStream_t st, bool fwd) {
+    switch (slice_width(a.B * a.Hv)) {
+        case 64: seq_launch<MT, 64>(a, st, fwd); break;
+        case 32: seq_launch<MT, 32>(a, st, fwd); break;
+        default: seq_launch<MT, 16>(a, st, fwd); break;
+    }
+}
 
 template <int MT>
 static void ck_fwd_launch(const ck::Args &a, hipStream_t st, const char *stage) {
     if (stage[0] == 'p')
         hipLaunchKernelGGL((ck::ck_prep_kernel<MT>), dim3(a.NC, a.Hv, a.B), dim3(ck::NT), 0, st, a);
     else
-        hipLaunchKernelGGL((ck::ck_fwd_kernel<MT, CK_VS>), dim3(CK_D / CK_VS, a.Hv, a.B), dim3(ck::NT), 0, st, a);
+        seq_dispatch<MT>(a, st, true);
 }
 
 template <int MT>
 static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) {
     if (stage[0] == 's')
-        hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<MT, CK_VS>), dim3(CK_D / CK_VS, a.Hv, a.B), dim3(ck::NT), 0, st, a);
+        seq_dispatch<MT>(a, st, false);
     else
-        hipLaunchKernelGGL((ck::ck_bwd_local_kernel<MT>), dim3(a.NC, a.Hv, a.B), dim3(ck::NT), 0, st, a);
+        hipLaunchKernelGGL((ck::ck_bwd_local_kernel<MT>), dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
 }
 
 static int mma_kind(int in_dt) { return in_dt == DT_BF16 ? 1 : 0; }

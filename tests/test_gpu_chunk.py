@@ -162,6 +162,20 @@ def test_chunk_matches_recurrent_full_heads(dev, dtype):
         assert nerr(x, y) <= tol, (n, nerr(x, y))
 
 
+@pytest.mark.parametrize("B", [2, 4])
+def test_chunk_matches_recurrent_wide_slices(dev, B):
+    """B*Hv = 64 / 128 heads select value slices of 32 / 64 in the sequential kernels."""
+    d = _inputs(B, 130, 16, 32, seed=B, s0_std=0.02)
+    a = _gpu(d, dev, "chunk", dtype=torch.bfloat16)
+    b = _gpu(d, dev, "recurrent", dtype=torch.bfloat16)
+    for n, x, y in zip(NAMES, a, b):
+        assert nerr(x, y) <= 1e-2, (n, nerr(x, y))
+    a = _gpu(d, dev, "chunk")
+    b = _gpu(d, dev, "recurrent")
+    for n, x, y in zip(NAMES, a, b):
+        assert nerr(x, y) <= 1e-4, (n, nerr(x, y))
+
+
 def test_auto_form_selection(dev):
     import gdn_lib as L
     lib = L.load()
