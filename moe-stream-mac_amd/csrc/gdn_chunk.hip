@@ -305,9 +305,10 @@ __device__ __forceinline__ size_t chunk_index(const Args &a, int b, int hv, int 
 // (I + A)^-1 of a unit lower-triangular 64x64 matrix, A strictly lower in sA.  Diagonal 16x16 blocks by
 // column-parallel forward substitution, then off-diagonal blocks by distance:
 // T_ij = -T_ii sum_{u=j}^{i-1} A_iu T_uj.
+template <int NTH>
 __device__ void unit_lower_inverse(const float *sA, float *sT, float *scratch) {
     const int tid = threadIdx.x;
-    for (int i = tid; i < C * C; i += NT) {
+    for (int i = tid; i < C * C; i += NTH) {
         const int r = i / C, s = i - r * C;
         if ((s >> 4) > (r >> 4)) sT[r * LDC + s] = 0.f;
     }
@@ -327,14 +328,14 @@ __device__ void unit_lower_inverse(const float *sA, float *sT, float *scratch) {
     __syncthreads();
     for (int d = 1; d < 4; ++d) {
         const int nb = 4 - d;
-        for (int e = tid; e < nb * 256; e += NT) {
+        for (int e = tid; e < nb * 256; e += NTH) {
             const int blk = e >> 8, bi = blk + d, bj = blk, r = (e >> 4) & 15, cc = e & 15;
             float x = 0.f;
             for (int u = 16 * bj; u < 16 * bi; ++u) x = fmaf(sA[(16 * bi + r) * LDC + u], sT[u * LDC + 16 * bj + cc], x);
             scratch[e] = x;
         }
         __syncthreads();
-        for (int e = tid; e < nb * 256; e += NT) {
+        for (int e = tid; e < nb * 256; e += NTH) {
             const int blk = e >> 8, bi = blk + d, bj = blk, r = (e >> 4) & 15, cc = e & 15;
             float t = 0.f;
 #pragma unroll
@@ -347,80 +348,93 @@ __device__ void unit_lower_inverse(const float *sA, float *sT, float *scratch) {
 
 // ---------------------------------------------------------------------------------------------- ck_prep
 
+constexpr int NTP = 512;  // ck_prep: 8 waves
+
 template <int MT>
-__global__ __launch_bounds__(NT) void ck_prep_kernel(Args a) {
+__global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
     __shared__ __align__(16) float sK[C * LD];
     __shared__ __align__(16) float sX[C * LD];
     __shared__ __align__(16) float sA[C * LDC];
     __shared__ __align__(16) float sT[C * LDC];
     __shared__ float scratch[3 * 256];
     __shared__ double sG[C];
-    __shared__ float sGl[C], sB[C], sGam[C];
+    __shared__ float sB[C], sGam[C];
 
     const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk), t0 = c * C, n = min(C, T - t0);
     const size_t ci = chunk_index(a, b, hv, c);
-
     const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
     const size_t v0 = (((size_t)b * T + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
-    load_tile<C, D>(sK, LD, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
-    load_tile<C, D>(sX, LD, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
+
+    TileRegs<C, D, NTP> rV;  // V is needed only after the inverse: fetch it now, store it later
+    tile_fetch(rV, elem_ptr(a.v, v0, a.in_dt), v_row, n, a.in_dt);
+    load_tile<C, D, NTP>(sK, LD, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
+    load_tile<C, D, NTP>(sX, LD, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
     if (tid < C) {
+        // inclusive prefix sum of the log decays in fp64 across wave 0
         float bt = 0.f, gl = 0.f;
         if (tid < n) {
             const size_t gi = ((size_t)b * T + t0 + tid) * a.Hv + hv;
             bt = a.beta[gi];
             gl = gate_log(a.g[gi], a.gate);
         }
+        double x = gl;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const double y = __shfl_up(x, d, 64);
+            if (tid >= d) x += y;
+        }
         sB[tid] = bt;
-        sGl[tid] = gl;
+        sG[tid] = x;
+        sGam[tid] = expf((float)x);
     }
     __syncthreads();
-    if (tid == 0) {
-        double s = 0.0;
-        for (int r = 0; r < C; ++r) {
-            s += (double)sGl[r];
-            sG[r] = s;
-        }
-    }
-    __syncthreads();
-    if (tid < C) sGam[tid] = expf((float)sG[tid]);
-    // K K^T and Q K^T: wave w owns rows 16w..16w+15
+    // K K^T (waves 0-3) and Q K^T (waves 4-7): each wave a 16-row strip of 4 tiles
+    {
+        const int r0 = 16 * (w & 3);
+        const bool isq = w >= 4;
+        f4 acc[4];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-        f4 kk = zero4(), qk = zero4();
-        mma16<MT, D>(kk, sK + 16 * w * LD, LD, 1, sK + 16 * nt * LD, 1, LD);
-        mma16<MT, D>(qk, sX + 16 * w * LD, LD, 1, sK + 16 * nt * LD, 1, LD);
+        for (int t = 0; t < 4; ++t) acc[t] = zero4();
+        mma_strip<MT, D, 4>(acc, (isq ? sX : sK) + r0 * LD, LD, 1, sK, 1, LD, 16 * LD);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = 16 * w + 4 * lg + e, s = 16 * nt + li;
-            const float gam = s <= r ? expf((float)(sG[r] - sG[s])) : 0.f;
-            sA[r * LDC + s] = s < r ? sB[r] * kk[e] * gam : 0.f;
-            a.w.P[ci * C * C + r * C + s] = qk[e] * gam;
-        }
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, s2 = 16 * t + li;
+                const float gam = s2 <= r ? expf((float)(sG[r] - sG[s2])) : 0.f;
+                if (isq) a.w.P[ci * C * C + r * C + s2] = acc[t][e] * gam;
+                else sA[r * LDC + s2] = s2 < r ? sB[r] * acc[t][e] * gam : 0.f;
+            }
     }
     __syncthreads();
-    unit_lower_inverse(sA, sT, scratch);
-    for (int i = tid; i < C * D; i += NT) {
+    unit_lower_inverse<NTP>(sA, sT, scratch);
+    for (int i = tid; i < C * D; i += NTP) {
         const int r = i / D, j = i - r * D;
         sK[r * LD + j] *= sB[r] * sGam[r];
     }
-    load_tile<C, D>(sX, LD, elem_ptr(a.v, v0, a.in_dt), v_row, n, a.in_dt, sB);
-    __syncthreads();
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-        f4 wa = zero4(), ua = zero4();
-        mma16<MT, C>(wa, sT + 16 * w * LDC, LDC, 1, sK + 16 * nt, LD, 1);
-        mma16<MT, C, true, true>(ua, sT + 16 * w * LDC, LDC, 1, sX + 16 * nt, LD, 1);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = 16 * w + 4 * lg + e, col = 16 * nt + li;
-            a.w.W[ci * C * D + r * D + col] = wa[e];
-            a.w.U[ci * C * D + r * D + col] = ua[e];
-        }
+    {
+        const float *bp = sB;
+        tile_store(sX, LD, rV, a.in_dt, [bp](int r) { return bp[r]; });
     }
-    for (int i = tid; i < C * C; i += NT) a.w.T[ci * C * C + i] = sT[(i / C) * LDC + (i % C)];
+    __syncthreads();
+    // W = T diag(beta gamma) K (waves 0-3) and U = T diag(beta) V (waves 4-7), 16-row strips of 8 tiles
+    {
+        const int r0 = 16 * (w & 3);
+        const bool isu = w >= 4;
+        f4 acc[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[t] = zero4();
+        if (isu) mma_strip<MT, C, 8, true, true>(acc, sT + r0 * LDC, LDC, 1, sX, LD, 1, 16);
+        else mma_strip<MT, C, 8>(acc, sT + r0 * LDC, LDC, 1, sK, LD, 1, 16);
+        float *out = isu ? a.w.U : a.w.W;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = acc[t][e];
+    }
+    for (int i = tid; i < C * C; i += NTP) a.w.T[ci * C * C + i] = sT[(i / C) * LDC + (i % C)];
     if (tid < C) a.w.G[ci * C + tid] = sG[tid];
 }
 
@@ -1045,7 +1059,7 @@ static void seq_dispatch(const ck::Args &a, hipStream_t st, bool fwd) {
 template <int MT>
 static void ck_fwd_launch(const ck::Args &a, hipStream_t st, const char *stage) {
     if (stage[0] == 'p')
-        hipLaunchKernelGGL((ck::ck_prep_kernel<MT>), dim3(a.NC, a.Hv, a.B), dim3(ck::NT), 0, st, a);
+        hipLaunchKernelGGL((ck::ck_prep_kernel<MT>), dim3(a.NC, a.Hv, a.B), dim3(ck::NTP), 0, st, a);
     else
         seq_dispatch<MT>(a, st, true);
 }
