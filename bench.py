@@ -211,8 +211,15 @@ def main():
     else:
         roofline = {"bound": "mfma", "achieved": round(flops / t_s / 1e12, 3), "peak": peak_flops,
                     "unit": "TFLOP/s", "frac": round(f_frac, 4)}
+    traffic = None
+    tj = ROOT / "profiles" / "traffic.json"
+    if tj.exists():
+        rec = json.loads(tj.read_text()).get(args.workload, {}).get(dom)
+        if rec:
+            traffic = rec["read_bytes"] + rec["write_bytes"]
     roofline.update({
-        "traffic": None, "kernel": dom, "avg_launch_ms": round(avg_ms, 4),
+        "traffic": traffic, "traffic_source": "profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE)"
+        if traffic else None, "kernel": dom, "avg_launch_ms": round(avg_ms, 4),
         "algo_flops_per_launch": flops, "algo_bytes_per_launch": nbytes,
         "other_roof_frac": round(min(f_frac, b_frac), 4),
         "kernels_ms_per_step": {n: round(v[0] / args.steps, 4) for n, v in kt.items()}})
