@@ -115,6 +115,72 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
             int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk,
             int in_dtype, int dy_dtype, int grad_dtype, int gate_kind, int form, void *stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * Block ops around the recurrence: the steps of one GDN block (engine/src/gdn_layer.c:29-55) over a whole
+ * sequence, each with its backward.  Tensors are contiguous; `tokens` = B*T.  Parameter gradients are reduced
+ * deterministically (no atomics) through a caller workspace of the size the matching *_workspace_bytes call
+ * returns.  Kernels use 8/16-byte vector loads when every tensor is 16-byte aligned and the row length allows,
+ * and element loads otherwise; results do not depend on which path runs beyond fp32 rounding.
+ * --------------------------------------------------------------------------------------------------------- */
+
+/* Gates, replacing gdn_gates (engine/include/gdn.h:20-25) over all tokens:
+ *   a, b [tokens][Hv] (in_dtype);  A_log, dt_bias [Hv] fp32;  g, beta [tokens][Hv] fp32 outputs
+ *   log decay  l = -exp(A_log[h]) * softplus(a + dt_bias[h]),  softplus(t) = t > 20 ? t : log1p(exp(t))
+ *   g = log_space ? l : exp(l)          (log_space = the log-decay convention of GDN_GATE_LOG)
+ *   beta = s / (1 + exp(-b)),  s = 2 when allow_neg_eigval (mlx-lm gated_delta_update), else 1
+ * Hv <= 256. */
+int gdn_gates_fwd(const void *a, const void *b, const float *A_log, const float *dt_bias, float *g, float *beta,
+                  int64_t tokens, int Hv, int in_dtype, int log_space, int allow_neg_eigval, void *stream);
+
+size_t gdn_gates_bwd_workspace_bytes(int64_t tokens, int Hv);
+
+/* Backward of gdn_gates_fwd.  g is the forward output; dg is the cotangent of g (w.r.t. the decay, or the log
+ * decay when log_space); dbeta of beta.  Writes da, db [tokens][Hv] (grad_dtype) and dA_log, ddt_bias [Hv]
+ * fp32 (summed over tokens). */
+int gdn_gates_bwd(const void *a, const void *b, const float *A_log, const float *dt_bias, const float *g,
+                  const float *dg, const float *dbeta, void *da, void *db, float *dA_log, float *ddt_bias,
+                  void *workspace, size_t workspace_bytes, int64_t tokens, int Hv, int in_dtype, int grad_dtype,
+                  int log_space, int allow_neg_eigval, void *stream);
+
+/* Per-row L2 norm, replacing gdn_l2norm (engine/include/gdn.h:17-18; applied per head with scale
+ * 1/sqrt(Dk) for q and 1 for k, engine/src/gdn_layer.c:35-39):
+ *   y = scale * x / sqrt(sum x^2 + eps)  over rows of D elements;  x, y [rows][D] (dtype); y may equal x. */
+int gdn_l2norm_fwd(const void *x, void *y, int64_t rows, int D, float eps, float scale, int dtype, void *stream);
+
+/* dx = scale/n (dy - x (x.dy)/n^2), n = sqrt(sum x^2 + eps);  dx has dtype, dy has dy_dtype. */
+int gdn_l2norm_bwd(const void *x, const void *dy, void *dx, int64_t rows, int D, float eps, float scale, int dtype,
+                   int dy_dtype, void *stream);
+
+/* Causal depthwise conv + SiLU over a whole sequence, replacing T calls of gdn_conv_step
+ * (engine/include/gdn.h:7-15):
+ *   x, out [B][T][C] (dtype);  w [C][K] fp32 (w[c*K + K-1] multiplies the current input);  2 <= K <= 8
+ *   out[b,t,c] = silu( sum_j w[c*K + j] * x[b, t-(K-1)+j, c] ),  x before t = 0 taken from state_in
+ *   state_in  [B][K-1][C] fp32, oldest input first, or NULL for zeros (a fresh state)
+ *   state_out [B][K-1][C] fp32, the last K-1 inputs after the sequence, or NULL; must not alias state_in. */
+int gdn_conv_silu_fwd(const void *x, const float *w, const float *state_in, void *out, float *state_out, int B,
+                      int T, int C, int K, int dtype, void *stream);
+
+size_t gdn_conv_silu_bwd_workspace_bytes(int B, int T, int C, int K);
+
+/* Backward of gdn_conv_silu_fwd (no gradient w.r.t. state_in): dx [B][T][C] (dtype), dw [C][K] fp32. */
+int gdn_conv_silu_bwd(const void *x, const float *w, const float *state_in, const void *dout, void *dx, float *dw,
+                      void *workspace, size_t workspace_bytes, int B, int T, int C, int K, int dtype, int dout_dtype,
+                      void *stream);
+
+/* Gated RMSNorm, replacing op_rmsnorm + op_silu_mul per value head (engine/include/ops.h:7-11,
+ * engine/src/gdn_layer.c:47-55):
+ *   out = y / sqrt(mean(y^2) + eps) * w * silu(z)   over rows of D;  y, out [rows][D] (dtype), z (z_dtype),
+ *   w [D] fp32. */
+int gdn_gated_rmsnorm_fwd(const void *y, const void *z, const float *w, void *out, int64_t rows, int D, float eps,
+                          int dtype, int z_dtype, void *stream);
+
+size_t gdn_gated_rmsnorm_bwd_workspace_bytes(int64_t rows, int D);
+
+/* Backward: dy (dtype), dz (z_dtype), dw [D] fp32 (summed over rows); D <= 4096. */
+int gdn_gated_rmsnorm_bwd(const void *y, const void *z, const float *w, const void *dout, void *dy, void *dz,
+                          float *dw, void *workspace, size_t workspace_bytes, int64_t rows, int D, float eps,
+                          int dtype, int z_dtype, int dout_dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

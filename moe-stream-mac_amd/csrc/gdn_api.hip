@@ -363,4 +363,189 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
     return check_launch(st, "gdn_bwd_reduce");
 }
 
+// ------------------------------------------------------------------------------------------- block ops
+
+static bool all_aligned16(std::initializer_list<const void *> ps) {
+    for (const void *p : ps)
+        if (p && misaligned16(p)) return false;
+    return true;
+}
+
+static size_t floats_bytes(size_t n) { return align256(n * sizeof(float)); }
+
+int gdn_gates_fwd(const void *a, const void *b, const float *A_log, const float *dt_bias, float *g, float *beta,
+                  int64_t tokens, int Hv, int in_dtype, int log_space, int allow_neg_eigval, void *stream) {
+    g_err[0] = 0;
+    if (tokens < 0 || Hv <= 0) return fail(GDN_ERR_INVALID, "tokens must be >= 0 and Hv > 0");
+    if (Hv > gates_max_heads()) return fail(GDN_ERR_UNSUPPORTED, "Hv > %d is not supported", gates_max_heads());
+    if (!dtype_ok(in_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    if (tokens == 0) return GDN_OK;
+    if (!a || !b || !A_log || !dt_bias || !g || !beta) return fail(GDN_ERR_INVALID, "null pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    {
+        Timed tm("gates_fwd", st);
+        launch_gates_fwd(a, b, A_log, dt_bias, g, beta, (size_t)tokens, Hv, in_dtype, log_space != 0,
+                         allow_neg_eigval ? 2.f : 1.f, st);
+    }
+    return check_launch(st, "gdn_gates_fwd");
+}
+
+size_t gdn_gates_bwd_workspace_bytes(int64_t tokens, int Hv) {
+    if (tokens < 0 || Hv <= 0) return 0;
+    return floats_bytes(gates_bwd_work_floats((size_t)tokens, Hv));
+}
+
+int gdn_gates_bwd(const void *a, const void *b, const float *A_log, const float *dt_bias, const float *g,
+                  const float *dg, const float *dbeta, void *da, void *db, float *dA_log, float *ddt_bias,
+                  void *workspace, size_t workspace_bytes, int64_t tokens, int Hv, int in_dtype, int grad_dtype,
+                  int log_space, int allow_neg_eigval, void *stream) {
+    g_err[0] = 0;
+    if (tokens < 0 || Hv <= 0) return fail(GDN_ERR_INVALID, "tokens must be >= 0 and Hv > 0");
+    if (Hv > gates_max_heads()) return fail(GDN_ERR_UNSUPPORTED, "Hv > %d is not supported", gates_max_heads());
+    if (!dtype_ok(in_dtype) || !dtype_ok(grad_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    if (!A_log || !dt_bias || !dA_log || !ddt_bias) return fail(GDN_ERR_INVALID, "null pointer");
+    if (tokens > 0 && (!a || !b || !g || !dg || !dbeta || !da || !db)) return fail(GDN_ERR_INVALID, "null pointer");
+    const size_t need = gdn_gates_bwd_workspace_bytes(tokens, Hv);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
+                    workspace_bytes, need);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    {
+        Timed tm("gates_bwd", st);
+        launch_gates_bwd(a, b, A_log, dt_bias, g, dg, dbeta, da, db, dA_log, ddt_bias, static_cast<float *>(workspace),
+                         (size_t)tokens, Hv, in_dtype, grad_dtype, log_space != 0, allow_neg_eigval ? 2.f : 1.f, st);
+    }
+    return check_launch(st, "gdn_gates_bwd");
+}
+
+int gdn_l2norm_fwd(const void *x, void *y, int64_t rows, int D, float eps, float scale, int dtype, void *stream) {
+    g_err[0] = 0;
+    if (rows < 0 || D <= 0) return fail(GDN_ERR_INVALID, "rows must be >= 0 and D > 0");
+    if (!dtype_ok(dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    if (rows == 0) return GDN_OK;
+    if (!x || !y) return fail(GDN_ERR_INVALID, "null pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    {
+        Timed tm("l2norm_fwd", st);
+        launch_l2norm_fwd(x, y, (size_t)rows, D, eps, scale, dtype, all_aligned16({x, y}), st);
+    }
+    return check_launch(st, "gdn_l2norm_fwd");
+}
+
+int gdn_l2norm_bwd(const void *x, const void *dy, void *dx, int64_t rows, int D, float eps, float scale, int dtype,
+                   int dy_dtype, void *stream) {
+    g_err[0] = 0;
+    if (rows < 0 || D <= 0) return fail(GDN_ERR_INVALID, "rows must be >= 0 and D > 0");
+    if (!dtype_ok(dtype) || !dtype_ok(dy_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    if (rows == 0) return GDN_OK;
+    if (!x || !dy || !dx) return fail(GDN_ERR_INVALID, "null pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    {
+        Timed tm("l2norm_bwd", st);
+        launch_l2norm_bwd(x, dy, dx, (size_t)rows, D, eps, scale, dtype, dy_dtype, all_aligned16({x, dy, dx}), st);
+    }
+    return check_launch(st, "gdn_l2norm_bwd");
+}
+
+static int check_conv(int B, int T, int C, int K, int dtype) {
+    if (B < 0 || T < 0 || C < 0) return fail(GDN_ERR_INVALID, "B, T and C must be >= 0");
+    if (K < 2) return fail(GDN_ERR_INVALID, "the conv kernel size K must be >= 2");
+    if (K > conv_kmax()) return fail(GDN_ERR_UNSUPPORTED, "conv kernel size K > %d is not supported", conv_kmax());
+    if (!dtype_ok(dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    return GDN_OK;
+}
+
+int gdn_conv_silu_fwd(const void *x, const float *w, const float *state_in, void *out, float *state_out, int B,
+                      int T, int C, int K, int dtype, void *stream) {
+    g_err[0] = 0;
+    int rc = check_conv(B, T, C, K, dtype);
+    if (rc) return rc;
+    if (B == 0 || C == 0) return GDN_OK;
+    if (!w || (T > 0 && (!x || !out))) return fail(GDN_ERR_INVALID, "null pointer");
+    if (state_out && state_out == state_in) return fail(GDN_ERR_INVALID, "state_out must not alias state_in");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    {
+        Timed tm("conv_fwd", st);
+        launch_conv_fwd(x, w, state_in, out, state_out, B, T, C, K, dtype, C % 4 == 0 && all_aligned16({x, out}),
+                        st);
+    }
+    return check_launch(st, "gdn_conv_silu_fwd");
+}
+
+size_t gdn_conv_silu_bwd_workspace_bytes(int B, int T, int C, int K) {
+    if (B < 0 || T < 0 || C < 0 || K < 2) return 0;
+    return floats_bytes(conv_bwd_work_floats(B, T, C, K));
+}
+
+int gdn_conv_silu_bwd(const void *x, const float *w, const float *state_in, const void *dout, void *dx, float *dw,
+                      void *workspace, size_t workspace_bytes, int B, int T, int C, int K, int dtype, int dout_dtype,
+                      void *stream) {
+    g_err[0] = 0;
+    int rc = check_conv(B, T, C, K, dtype);
+    if (rc) return rc;
+    if (!dtype_ok(dout_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    if (C == 0) return GDN_OK;
+    if (!w || !dw || (B > 0 && T > 0 && (!x || !dout || !dx))) return fail(GDN_ERR_INVALID, "null pointer");
+    const size_t need = gdn_conv_silu_bwd_workspace_bytes(B, T, C, K);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
+                    workspace_bytes, need);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    {
+        Timed tm("conv_bwd", st);
+        launch_conv_bwd(x, w, state_in, dout, dx, dw, static_cast<float *>(workspace), B, T, C, K, dtype, dout_dtype,
+                        C % 4 == 0 && all_aligned16({x, dout, dx}), st);
+    }
+    return check_launch(st, "gdn_conv_silu_bwd");
+}
+
+static int check_grms(int64_t rows, int D, int dtype, int z_dtype, bool bwd) {
+    if (rows < 0 || D <= 0) return fail(GDN_ERR_INVALID, "rows must be >= 0 and D > 0");
+    if (bwd && D > grms_dmax())
+        return fail(GDN_ERR_UNSUPPORTED, "gated RMSNorm backward of rows longer than %d", grms_dmax());
+    if (!dtype_ok(dtype) || !dtype_ok(z_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    return GDN_OK;
+}
+
+int gdn_gated_rmsnorm_fwd(const void *y, const void *z, const float *w, void *out, int64_t rows, int D, float eps,
+                          int dtype, int z_dtype, void *stream) {
+    g_err[0] = 0;
+    int rc = check_grms(rows, D, dtype, z_dtype, false);
+    if (rc) return rc;
+    if (rows == 0) return GDN_OK;
+    if (!y || !z || !w || !out) return fail(GDN_ERR_INVALID, "null pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    {
+        Timed tm("grms_fwd", st);
+        launch_grms_fwd(y, z, w, out, (size_t)rows, D, eps, dtype, z_dtype, all_aligned16({y, z, w, out}), st);
+    }
+    return check_launch(st, "gdn_gated_rmsnorm_fwd");
+}
+
+size_t gdn_gated_rmsnorm_bwd_workspace_bytes(int64_t rows, int D) {
+    if (rows < 0 || D <= 0) return 0;
+    return floats_bytes(grms_bwd_work_floats((size_t)rows, D));
+}
+
+int gdn_gated_rmsnorm_bwd(const void *y, const void *z, const float *w, const void *dout, void *dy, void *dz,
+                          float *dw, void *workspace, size_t workspace_bytes, int64_t rows, int D, float eps,
+                          int dtype, int z_dtype, int dout_dtype, void *stream) {
+    g_err[0] = 0;
+    int rc = check_grms(rows, D, dtype, z_dtype, true);
+    if (rc) return rc;
+    if (!dtype_ok(dout_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    if (!w || !dw || (rows > 0 && (!y || !z || !dout || !dy || !dz))) return fail(GDN_ERR_INVALID, "null pointer");
+    const size_t need = gdn_gated_rmsnorm_bwd_workspace_bytes(rows, D);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
+                    workspace_bytes, need);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    {
+        Timed tm("grms_bwd", st);
+        launch_grms_bwd(y, z, w, dout, dy, dz, dw, static_cast<float *>(workspace), (size_t)rows, D, eps, dtype,
+                        z_dtype, dout_dtype, all_aligned16({y, z, w, dout, dy, dz}), st);
+    }
+    return check_launch(st, "gdn_gated_rmsnorm_bwd");
+}
+
 }  // extern "C"

@@ -1,0 +1,802 @@
+// Streaming kernels that surround the GDN recurrence inside one block, for gfx950:
+//   gates (log decay + beta), q/k L2 norm, causal depthwise conv1d + SiLU, gated RMSNorm * SiLU(z),
+// each with its backward.  All of them are HBM-bound elementwise/row work:
+//   * every input element is read once with 8- or 16-byte vector loads, every output written once;
+//   * per-row reductions (L2 norm, RMS) stay inside a group of L lanes of one wavefront (xor shuffles);
+//   * parameter gradients (dA_log, ddt_bias, conv weights, norm weight) are reduced deterministically:
+//     per-workgroup partials in a fixed order, then a fixed-order column sum.  No atomics.
+//
+// Specs: engine/include/gdn.h:7-25 (conv step, l2norm, gates), engine/include/ops.h:7-11 and
+// engine/src/gdn_layer.c:35-55 (per-head L2 norm scales, gated RMSNorm).
+#include "gdn_common.h"
+#include "gdn_internal.h"
+
+namespace gdn {
+namespace ops {
+
+constexpr int NT = 256;
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+
+// softplus(t) = t > 20 ? t : log1p(exp(t))   (engine/include/gdn.h:23-24)
+__device__ __forceinline__ float softplus_(float t) { return t > 20.f ? t : log1pf(expf(t)); }
+
+template <int L>
+__device__ __forceinline__ float group_sum(float x) {
+#pragma unroll
+    for (int m = L / 2; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+    return x;
+}
+
+__device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
+    return __half2float(__ushort_as_half((unsigned short)(h & 0xffffu)));
+}
+
+// V consecutive elements starting at element i (i % V == 0, buffer base 16-byte aligned).
+template <int V>
+__device__ __forceinline__ void loadv(const void *p, size_t i, int dt, float (&o)[V]) {
+    if constexpr (V == 1) {
+        o[0] = load_as_f32(p, i, dt);
+    } else if constexpr (V == 4) {
+        if (dt == DT_F32) {
+            const float4 a = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
+            o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+        } else {
+            const uint2 u = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(p) + i);
+            const uint32_t w[2] = {u.x, u.y};
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (dt == DT_BF16) {
+                    o[2 * j] = __uint_as_float(w[j] << 16);
+                    o[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+                } else {
+                    o[2 * j] = half_bits_to_f32(w[j]);
+                    o[2 * j + 1] = half_bits_to_f32(w[j] >> 16);
+                }
+            }
+        }
+    } else {
+        static_assert(V == 8, "V is 1, 4 or 8");
+        if (dt == DT_F32) {
+            const float4 a = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
+            const float4 b = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i + 4);
+            o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+            o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+        } else {
+            const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (dt == DT_BF16) {
+                    o[2 * j] = __uint_as_float(w[j] << 16);
+                    o[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+                } else {
+                    o[2 * j] = half_bits_to_f32(w[j]);
+                    o[2 * j + 1] = half_bits_to_f32(w[j] >> 16);
+                }
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t pack2(float a, float b, int dt) {
+    if (dt == DT_BF16) return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+    return (uint32_t)__half_as_ushort(__float2half(a)) | ((uint32_t)__half_as_ushort(__float2half(b)) << 16);
+}
+
+template <int V>
+__device__ __forceinline__ void storev(void *p, size_t i, int dt, const float (&o)[V]) {
+    if constexpr (V == 1) {
+        store_from_f32(p, i, o[0], dt);
+    } else if constexpr (V == 4) {
+        if (dt == DT_F32) {
+            *reinterpret_cast<float4 *>(static_cast<float *>(p) + i) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(p) + i) =
+                make_uint2(pack2(o[0], o[1], dt), pack2(o[2], o[3], dt));
+        }
+    } else {
+        static_assert(V == 8, "V is 1, 4 or 8");
+        if (dt == DT_F32) {
+            *reinterpret_cast<float4 *>(static_cast<float *>(p) + i) = make_float4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<float4 *>(static_cast<float *>(p) + i + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        } else {
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(p) + i) =
+                make_uint4(pack2(o[0], o[1], dt), pack2(o[2], o[3], dt), pack2(o[4], o[5], dt),
+                           pack2(o[6], o[7], dt));
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------- column sums
+
+// s_j = sum_r part[r * ncols + j] (r ascending), written to out[j] for j < split and out2[j - split] after.
+__device__ __forceinline__ void put_col(float *out, float *out2, int split, int j, float s) {
+    if (j < split)
+        out[j] = s;
+    else
+        out2[j - split] = s;
+}
+
+// One thread per column: for few partial rows.
+__global__ void colsum_thread_kernel(const float *part, int nrows, int ncols, float *out, float *out2, int split) {
+    const int j = blockIdx.x * NT + threadIdx.x;
+    if (j >= ncols) return;
+    float s = 0.f;
+    for (int r = 0; r < nrows; ++r) s += part[(size_t)r * ncols + j];
+    put_col(out, out2, split, j, s);
+}
+
+// One workgroup per column: thread t sums rows t, t+NT, ... in order, then a fixed tree over the threads.
+__global__ __launch_bounds__(NT) void colsum_block_kernel(const float *part, int nrows, int ncols, float *out,
+                                                          float *out2, int split) {
+    __shared__ float red[NT];
+    const int j = blockIdx.x, tid = threadIdx.x;
+    float s = 0.f;
+    for (int r = tid; r < nrows; r += NT) s += part[(size_t)r * ncols + j];
+    red[tid] = s;
+    __syncthreads();
+#pragma unroll
+    for (int h = NT / 2; h >= 1; h >>= 1) {
+        if (tid < h) red[tid] += red[tid + h];
+        __syncthreads();
+    }
+    if (tid == 0) put_col(out, out2, split, j, red[0]);
+}
+
+// ------------------------------------------------------------------------------------------------ gates
+
+// g = -exp(A_log[h]) softplus(a + dt_bias[h]) as log decay (log_space) or decay exp(g); beta = s sigmoid(b)
+__global__ __launch_bounds__(NT) void gates_fwd_kernel(const void *a, const void *b, const float *A_log,
+                                                       const float *dt_bias, float *g, float *beta, size_t n,
+                                                       int Hv, int in_dt, int log_space, float beta_scale) {
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= n) return;
+    const int h = (int)(i % Hv);
+    const float x = load_as_f32(a, i, in_dt) + dt_bias[h];
+    const float gl = -expf(A_log[h]) * softplus_(x);
+    g[i] = log_space ? gl : expf(gl);
+    beta[i] = beta_scale * sigmoidf_(load_as_f32(b, i, in_dt));
+}
+
+// da, db elementwise and per-workgroup partials of dA_log / ddt_bias.  A workgroup owns GATE_TOK tokens x
+// all Hv heads (Hv <= NT); thread tid handles head tid % Hv for tokens slot, slot + nslot, ...
+constexpr int GATE_TOK = 256;
+__global__ __launch_bounds__(NT) void gates_bwd_kernel(const void *a, const void *b, const float *A_log,
+                                                       const float *dt_bias, const float *g, const float *dg,
+                                                       const float *dbeta, void *da, void *db, float *part,
+                                                       size_t tokens, int Hv, int in_dt, int grad_dt, int log_space,
+                                                       float beta_scale) {
+    __shared__ float sA[NT], sT[NT];
+    const int tid = threadIdx.x;
+    const size_t tok0 = (size_t)blockIdx.x * GATE_TOK;
+    const int ntok = (int)min((size_t)GATE_TOK, tokens - tok0);
+    const int nslot = NT / Hv;
+    const int h = tid % Hv, slot = tid / Hv;
+    float accA = 0.f, accT = 0.f;
+    if (slot < nslot) {
+        const float e = expf(A_log[h]), bias = dt_bias[h];
+        for (int t = slot; t < ntok; t += nslot) {
+            const size_t i = (tok0 + t) * Hv + h;
+            const float x = load_as_f32(a, i, in_dt) + bias;
+            const float gv = g[i];
+            const float gl = log_space ? gv : -e * softplus_(x);
+            const float dgl = log_space ? dg[i] : dg[i] * gv;  // gradient w.r.t. the log decay
+            const float dx = dgl * -e * (x > 20.f ? 1.f : sigmoidf_(x));
+            store_from_f32(da, i, dx, grad_dt);
+            accA = fmaf(dgl, gl, accA);  // d(log decay)/dA_log = log decay
+            accT += dx;
+            const float sb = sigmoidf_(load_as_f32(b, i, in_dt));
+            store_from_f32(db, i, dbeta[i] * beta_scale * sb * (1.f - sb), grad_dt);
+        }
+    }
+    sA[tid] = accA;
+    sT[tid] = accT;
+    __syncthreads();
+    if (tid < Hv) {
+        float s1 = 0.f, s2 = 0.f;
+        for (int s = 0; s < nslot; ++s) {
+            s1 += sA[s * Hv + tid];
+            s2 += sT[s * Hv + tid];
+        }
+        part[(size_t)blockIdx.x * 2 * Hv + tid] = s1;
+        part[(size_t)blockIdx.x * 2 * Hv + Hv + tid] = s2;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ l2 norm
+
+// L lanes per row, 8 elements per lane (D = 8L); NT / L rows per workgroup.
+// y = scale * x / sqrt(sum x^2 + eps)
+template <int L>
+__global__ __launch_bounds__(NT) void l2norm_fwd_vec(const void *x, void *y, size_t rows, float eps, float scale,
+                                                     int dt) {
+    const size_t row = (size_t)blockIdx.x * (NT / L) + threadIdx.x / L;
+    if (row >= rows) return;
+    const size_t base = row * (8 * L) + (threadIdx.x % L) * 8;
+    float v[8];
+    loadv<8>(x, base, dt, v);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
+    const float inv = scale * rsqrtf(group_sum<L>(ss) + eps);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] *= inv;
+    storev<8>(y, base, dt, v);
+}
+
+// dx = s/n (dy - x (x . dy) / n^2),  n = sqrt(sum x^2 + eps)
+template <int L>
+__global__ __launch_bounds__(NT) void l2norm_bwd_vec(const void *x, const void *dy, void *dx, size_t rows, float eps,
+                                                     float scale, int dt, int dy_dt) {
+    const size_t row = (size_t)blockIdx.x * (NT / L) + threadIdx.x / L;
+    if (row >= rows) return;
+    const size_t base = row * (8 * L) + (threadIdx.x % L) * 8;
+    float v[8], d[8];
+    loadv<8>(x, base, dt, v);
+    loadv<8>(dy, base, dy_dt, d);
+    float ss = 0.f, xd = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        ss = fmaf(v[j], v[j], ss);
+        xd = fmaf(v[j], d[j], xd);
+    }
+    const float n2 = group_sum<L>(ss) + eps, dot = group_sum<L>(xd);
+    const float c1 = scale * rsqrtf(n2), c2 = c1 * dot / n2;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) d[j] = c1 * d[j] - c2 * v[j];
+    storev<8>(dx, base, dt, d);
+}
+
+// Any D: one wavefront per row.
+__global__ __launch_bounds__(NT) void l2norm_fwd_any(const void *x, void *y, size_t rows, int D, float eps,
+                                                     float scale, int dt) {
+    const size_t row = (size_t)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+    const int l = threadIdx.x & 63;
+    if (row >= rows) return;
+    const size_t base = row * D;
+    float ss = 0.f;
+    for (int j = l; j < D; j += 64) {
+        const float v = load_as_f32(x, base + j, dt);
+        ss = fmaf(v, v, ss);
+    }
+    const float inv = scale * rsqrtf(group_sum<64>(ss) + eps);
+    for (int j = l; j < D; j += 64) store_from_f32(y, base + j, load_as_f32(x, base + j, dt) * inv, dt);
+}
+
+__global__ __launch_bounds__(NT) void l2norm_bwd_any(const void *x, const void *dy, void *dx, size_t rows, int D,
+                                                     float eps, float scale, int dt, int dy_dt) {
+    const size_t row = (size_t)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+    const int l = threadIdx.x & 63;
+    if (row >= rows) return;
+    const size_t base = row * D;
+    float ss = 0.f, xd = 0.f;
+    for (int j = l; j < D; j += 64) {
+        const float v = load_as_f32(x, base + j, dt), d = load_as_f32(dy, base + j, dy_dt);
+        ss = fmaf(v, v, ss);
+        xd = fmaf(v, d, xd);
+    }
+    const float n2 = group_sum<64>(ss) + eps, dot = group_sum<64>(xd);
+    const float c1 = scale * rsqrtf(n2), c2 = c1 * dot / n2;
+    for (int j = l; j < D; j += 64) {
+        const float v = load_as_f32(x, base + j, dt), d = load_as_f32(dy, base + j, dy_dt);
+        store_from_f32(dx, base + j, c1 * d - c2 * v, dt);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ conv1d + SiLU
+
+// A workgroup is 4 wavefronts stacked in time: wavefront s covers tokens [t0 + s*CONV_TT, +CONV_TT) and every
+// lane V consecutive channels.  Each thread walks its tokens in order keeping the last K-1 inputs in
+// registers, so an input is read once (plus a K-1 token halo per CONV_TT tokens).
+constexpr int CONV_TT = 64;
+constexpr int CONV_SLICES = NT / 64;
+constexpr int CONV_U = 4;  // tokens loaded ahead per step
+
+// x at token t (t < 0: the carried conv state, zero when absent; t >= T: zero)
+template <int K, int V>
+__device__ __forceinline__ void conv_x(const void *x, const float *state_in, int b, int t, int T, int C, int c0,
+                                       int dt, float (&o)[V]) {
+    if (t >= 0 && t < T) {
+        loadv<V>(x, ((size_t)b * T + t) * C + c0, dt, o);
+    } else if (t < 0 && state_in) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) o[v] = state_in[((size_t)b * (K - 1) + (t + K - 1)) * C + c0 + v];
+    } else {
+#pragma unroll
+        for (int v = 0; v < V; ++v) o[v] = 0.f;
+    }
+}
+
+// out[t, c] = silu(sum_j w[c*K + j] x[t - (K-1) + j, c])   (engine/include/gdn.h:7-15 over a whole sequence)
+template <int K, int V>
+__global__ __launch_bounds__(NT) void conv_fwd_kernel(const void *x, const float *w, const float *state_in,
+                                                      void *out, int T, int C, int dt) {
+    const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
+    const int c0 = (blockIdx.x * 64 + lane) * V;
+    const int t0 = (blockIdx.y * CONV_SLICES + slice) * CONV_TT, b = blockIdx.z;
+    if (c0 >= C || t0 >= T) return;
+    float wk[K][V], hist[K - 1][V];
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+#pragma unroll
+        for (int j = 0; j < K; ++j) wk[j][v] = w[(size_t)(c0 + v) * K + j];
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j) conv_x<K, V>(x, state_in, b, t0 - (K - 1) + j, T, C, c0, dt, hist[j]);
+    const int t1 = min(T, t0 + CONV_TT);
+    for (int t = t0; t < t1; t += CONV_U) {
+        float xs[CONV_U][V];
+#pragma unroll
+        for (int u = 0; u < CONV_U; ++u) conv_x<K, V>(x, nullptr, b, t + u < t1 ? t + u : T, T, C, c0, dt, xs[u]);
+#pragma unroll
+        for (int u = 0; u < CONV_U; ++u) {
+            if (t + u >= t1) break;
+            float o[V];
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+                float pre = wk[K - 1][v] * xs[u][v];
+#pragma unroll
+                for (int j = 0; j < K - 1; ++j) pre = fmaf(wk[j][v], hist[j][v], pre);
+#pragma unroll
+                for (int j = 0; j + 1 < K - 1; ++j) hist[j][v] = hist[j + 1][v];
+                hist[K - 2][v] = xs[u][v];
+                o[v] = pre * sigmoidf_(pre);
+            }
+            storev<V>(out, ((size_t)b * T + t + u) * C + c0, dt, o);
+        }
+    }
+}
+
+// The last K-1 inputs after the sequence, oldest first: state_out[b][j][c] = x at T-(K-1)+j (from state_in when
+// that is before the sequence).  state_out must not alias state_in.
+__global__ void conv_state_kernel(const void *x, const float *state_in, float *state_out, int B, int T, int C, int K,
+                                  int dt) {
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= (size_t)B * (K - 1) * C) return;
+    const int c = (int)(i % C), j = (int)((i / C) % (K - 1)), b = (int)(i / ((size_t)C * (K - 1)));
+    const int t = T - (K - 1) + j;
+    float val = 0.f;
+    if (t >= 0)
+        val = load_as_f32(x, ((size_t)b * T + t) * C + c, dt);
+    else if (state_in)
+        val = state_in[((size_t)b * (K - 1) + (t + K - 1)) * C + c];
+    state_out[i] = val;
+}
+
+// silu'(p) dout with p the pre-activation from the window xs[0..K-1] = x[t-(K-1) .. t]
+template <int K, int V>
+__device__ __forceinline__ void conv_dpre(const float (&wk)[K][V], const float (*xs)[V], const float (&go)[V],
+                                          float (&dp)[V]) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        float pre = 0.f;
+#pragma unroll
+        for (int j = 0; j < K; ++j) pre = fmaf(wk[j][v], xs[j][v], pre);
+        const float s = sigmoidf_(pre);
+        dp[v] = go[v] * s * (1.f + pre * (1.f - s));
+    }
+}
+
+// Backward: dpre = dout silu'(pre);  dx[t] = sum_j w[j] dpre[t + K-1-j];  dw[j] = sum_t dpre[t] x[t-(K-1)+j].
+// Same grid as the forward.  dw partials of the workgroup (its 4 time slices summed in order) go to
+// part[(b * gridDim.y + blockIdx.y) * C*K + c*K + j].
+template <int K, int V>
+__global__ __launch_bounds__(NT) void conv_bwd_kernel(const void *x, const float *w, const float *state_in,
+                                                      const void *dout, void *dx, float *part, int T, int C, int dt,
+                                                      int dout_dt) {
+    __shared__ float red[CONV_SLICES][64 * V * K];
+    const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
+    const int c0 = (blockIdx.x * 64 + lane) * V;
+    const int t0 = (blockIdx.y * CONV_SLICES + slice) * CONV_TT, b = blockIdx.z;
+    const bool active = c0 < C && t0 < T;
+    float dwp[K][V];
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+#pragma unroll
+        for (int v = 0; v < V; ++v) dwp[j][v] = 0.f;
+    if (active) {
+        float wk[K][V];
+#pragma unroll
+        for (int v = 0; v < V; ++v)
+#pragma unroll
+            for (int j = 0; j < K; ++j) wk[j][v] = w[(size_t)(c0 + v) * K + j];
+        float xw[2 * K - 1][V];  // x[t-(K-1) .. t+K-1]
+        float dp[K][V];          // dpre[t .. t+K-1]
+#pragma unroll
+        for (int j = 0; j < 2 * K - 1; ++j) conv_x<K, V>(x, state_in, b, t0 - (K - 1) + j, T, C, c0, dt, xw[j]);
+#pragma unroll
+        for (int m = 0; m < K; ++m) {
+            float go[V];
+            conv_x<K, V>(dout, nullptr, b, t0 + m, T, C, c0, dout_dt, go);
+            conv_dpre<K, V>(wk, xw + m, go, dp[m]);
+        }
+        const int t1 = min(T, t0 + CONV_TT);
+        for (int t = t0; t < t1; t += CONV_U) {
+            float xn[CONV_U][V], gn[CONV_U][V];  // x and dout at t + K + u
+#pragma unroll
+            for (int u = 0; u < CONV_U; ++u) {
+                const int tn = t + K + u < T ? t + K + u : T;
+                conv_x<K, V>(x, nullptr, b, tn, T, C, c0, dt, xn[u]);
+                conv_x<K, V>(dout, nullptr, b, tn, T, C, c0, dout_dt, gn[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < CONV_U; ++u) {
+                if (t + u >= t1) break;
+                float o[V];
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+                    float s = 0.f;
+#pragma unroll
+                    for (int j = 0; j < K; ++j) s = fmaf(wk[j][v], dp[K - 1 - j][v], s);
+                    o[v] = s;
+#pragma unroll
+                    for (int j = 0; j < K; ++j) dwp[j][v] = fmaf(dp[0][v], xw[j][v], dwp[j][v]);
+                }
+                storev<V>(dx, ((size_t)b * T + t + u) * C + c0, dt, o);
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+#pragma unroll
+                    for (int j = 0; j + 1 < 2 * K - 1; ++j) xw[j][v] = xw[j + 1][v];
+                    xw[2 * K - 2][v] = xn[u][v];
+#pragma unroll
+                    for (int m = 0; m + 1 < K; ++m) dp[m][v] = dp[m + 1][v];
+                }
+                conv_dpre<K, V>(wk, xw + (K - 1), gn[u], dp[K - 1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+#pragma unroll
+        for (int v = 0; v < V; ++v) red[slice][(lane * V + v) * K + j] = dwp[j][v];
+    __syncthreads();
+    const size_t prow = ((size_t)b * gridDim.y + blockIdx.y) * C * K;
+    const int cbase = blockIdx.x * 64 * V;
+    for (int e = threadIdx.x; e < 64 * V * K; e += NT) {
+        if (cbase * K + e >= C * K) break;
+        float s = 0.f;
+#pragma unroll
+        for (int sl = 0; sl < CONV_SLICES; ++sl) s += red[sl][e];
+        part[prow + (size_t)cbase * K + e] = s;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ gated RMSNorm
+
+// out = y / sqrt(mean(y^2) + eps) * w * silu(z) per row of D = 8L   (engine/src/gdn_layer.c:47-55)
+template <int L>
+__global__ __launch_bounds__(NT) void grms_fwd_vec(const void *y, const void *z, const float *w, void *out,
+                                                   size_t rows, float eps, int dt, int z_dt) {
+    constexpr int D = 8 * L;
+    const size_t row = (size_t)blockIdx.x * (NT / L) + threadIdx.x / L;
+    if (row >= rows) return;
+    const int col = (threadIdx.x % L) * 8;
+    const size_t base = row * D + col;
+    float v[8], zv[8], wv[8];
+    loadv<8>(y, base, dt, v);
+    loadv<8>(z, base, z_dt, zv);
+    loadv<8>(w, col, DT_F32, wv);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
+    const float r = rsqrtf(group_sum<L>(ss) * (1.f / D) + eps);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = v[j] * r * wv[j] * (zv[j] * sigmoidf_(zv[j]));
+    storev<8>(out, base, dt, v);
+}
+
+// n = y r;  dn = dout w silu(z);  dy = r (dn - n mean(dn n));  dz = dout n w silu'(z);  dw += dout n silu(z).
+// A workgroup walks GRMS_ROWS rows; each lane keeps dw for its 8 columns, the NT/L row groups are summed in
+// order into part[blockIdx.x][D].
+constexpr int GRMS_ROWS = 512;
+template <int L>
+__global__ __launch_bounds__(NT) void grms_bwd_vec(const void *y, const void *z, const float *w, const void *dout,
+                                                   void *dy, void *dz, float *part, size_t rows, float eps, int dt,
+                                                   int z_dt, int dout_dt) {
+    constexpr int D = 8 * L, G = NT / L;
+    __shared__ float red[G][D];
+    const int grp = threadIdx.x / L, col = (threadIdx.x % L) * 8;
+    float wv[8], dw[8];
+    loadv<8>(w, col, DT_F32, wv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dw[j] = 0.f;
+    const size_t r0 = (size_t)blockIdx.x * GRMS_ROWS;
+    for (int rr = grp; rr < GRMS_ROWS; rr += G) {
+        const size_t row = r0 + rr;
+        if (row >= rows) break;  // uniform across the L lanes of a row group
+        const size_t base = row * D + col;
+        float v[8], zv[8], go[8];
+        loadv<8>(y, base, dt, v);
+        loadv<8>(z, base, z_dt, zv);
+        loadv<8>(dout, base, dout_dt, go);
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
+        const float r = rsqrtf(group_sum<L>(ss) * (1.f / D) + eps);
+        float dn[8], sg[8], dnn = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            sg[j] = sigmoidf_(zv[j]);
+            v[j] *= r;  // n
+            dn[j] = go[j] * wv[j] * zv[j] * sg[j];
+            dnn = fmaf(dn[j], v[j], dnn);
+        }
+        const float mean = group_sum<L>(dnn) * (1.f / D);
+        float oy[8], oz[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            oy[j] = r * (dn[j] - v[j] * mean);
+            oz[j] = go[j] * v[j] * wv[j] * sg[j] * (1.f + zv[j] * (1.f - sg[j]));
+            dw[j] = fmaf(go[j] * v[j], zv[j] * sg[j], dw[j]);
+        }
+        storev<8>(dy, base, dt, oy);
+        storev<8>(dz, base, z_dt, oz);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) red[grp][col + j] = dw[j];
+    __syncthreads();
+    for (int j = threadIdx.x; j < D; j += NT) {
+        float s = 0.f;
+        for (int g = 0; g < G; ++g) s += red[g][j];
+        part[(size_t)blockIdx.x * D + j] = s;
+    }
+}
+
+// Any D: one wavefront per row (the backward keeps per-wavefront dw in LDS, so D <= GRMS_DMAX there).
+constexpr int GRMS_DMAX = 4096;
+__global__ __launch_bounds__(NT) void grms_fwd_any(const void *y, const void *z, const float *w, void *out,
+                                                   size_t rows, int D, float eps, int dt, int z_dt) {
+    const size_t row = (size_t)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+    const int l = threadIdx.x & 63;
+    if (row >= rows) return;
+    const size_t base = row * D;
+    float ss = 0.f;
+    for (int j = l; j < D; j += 64) {
+        const float v = load_as_f32(y, base + j, dt);
+        ss = fmaf(v, v, ss);
+    }
+    const float r = rsqrtf(group_sum<64>(ss) / D + eps);
+    for (int j = l; j < D; j += 64) {
+        const float zv = load_as_f32(z, base + j, z_dt);
+        store_from_f32(out, base + j, load_as_f32(y, base + j, dt) * r * w[j] * (zv * sigmoidf_(zv)), dt);
+    }
+}
+
+__global__ __launch_bounds__(NT) void grms_bwd_any(const void *y, const void *z, const float *w, const void *dout,
+                                                   void *dy, void *dz, float *part, size_t rows, int D, float eps,
+                                                   int dt, int z_dt, int dout_dt) {
+    __shared__ float sdw[NT / 64][GRMS_DMAX];
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    for (int j = l; j < D; j += 64) sdw[wv][j] = 0.f;
+    const size_t r0 = (size_t)blockIdx.x * GRMS_ROWS;
+    for (int rr = wv; rr < GRMS_ROWS; rr += NT / 64) {
+        const size_t row = r0 + rr;
+        if (row >= rows) break;
+        const size_t base = row * D;
+        float ss = 0.f;
+        for (int j = l; j < D; j += 64) {
+            const float v = load_as_f32(y, base + j, dt);
+            ss = fmaf(v, v, ss);
+        }
+        const float r = rsqrtf(group_sum<64>(ss) / D + eps);
+        float dnn = 0.f;
+        for (int j = l; j < D; j += 64) {
+            const float zv = load_as_f32(z, base + j, z_dt), go = load_as_f32(dout, base + j, dout_dt);
+            dnn = fmaf(go * w[j] * zv * sigmoidf_(zv), load_as_f32(y, base + j, dt) * r, dnn);
+        }
+        const float mean = group_sum<64>(dnn) / D;
+        for (int j = l; j < D; j += 64) {
+            const float zv = load_as_f32(z, base + j, z_dt), go = load_as_f32(dout, base + j, dout_dt);
+            const float s = sigmoidf_(zv), n = load_as_f32(y, base + j, dt) * r;
+            const float dn = go * w[j] * zv * s;
+            store_from_f32(dy, base + j, r * (dn - n * mean), dt);
+            store_from_f32(dz, base + j, go * n * w[j] * s * (1.f + zv * (1.f - s)), z_dt);
+            sdw[wv][j] += go * n * zv * s;  // column j belongs to this lane within its wavefront
+        }
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < D; j += NT) {
+        float s = 0.f;
+        for (int g = 0; g < NT / 64; ++g) s += sdw[g][j];
+        part[(size_t)blockIdx.x * D + j] = s;
+    }
+}
+
+}  // namespace ops
+
+// ------------------------------------------------------------------------------------------------ launchers
+
+static unsigned nblocks(size_t n, size_t per) { return (unsigned)((n + per - 1) / per); }
+
+static void launch_colsum(const float *part, int nrows, int ncols, float *out, float *out2, int split,
+                          hipStream_t st) {
+    if (ncols <= 0) return;
+    if (nrows <= 128)
+        hipLaunchKernelGGL(ops::colsum_thread_kernel, dim3(nblocks(ncols, ops::NT)), dim3(ops::NT), 0, st, part, nrows,
+                           ncols, out, out2, split);
+    else
+        hipLaunchKernelGGL(ops::colsum_block_kernel, dim3(ncols), dim3(ops::NT), 0, st, part, nrows, ncols, out, out2,
+                           split);
+}
+
+// Lanes per row for the vector row kernels: D = 8L with L a power of two in [4, 64]; 0 = generic path.
+int row_lanes(int D) {
+    if (D % 8) return 0;
+    const int L = D / 8;
+    return (L >= 4 && L <= 64 && (L & (L - 1)) == 0) ? L : 0;
+}
+
+void launch_gates_fwd(const void *a, const void *b, const float *A_log, const float *dt_bias, float *g, float *beta,
+                      size_t tokens, int Hv, int in_dt, int log_space, float beta_scale, hipStream_t st) {
+    const size_t n = tokens * Hv;
+    if (n)
+        hipLaunchKernelGGL(ops::gates_fwd_kernel, dim3(nblocks(n, ops::NT)), dim3(ops::NT), 0, st, a, b, A_log, dt_bias,
+                           g, beta, n, Hv, in_dt, log_space, beta_scale);
+}
+
+int gates_max_heads() { return ops::NT; }
+
+size_t gates_bwd_work_floats(size_t tokens, int Hv) { return (size_t)nblocks(tokens, ops::GATE_TOK) * Hv * 2; }
+
+void launch_gates_bwd(const void *a, const void *b, const float *A_log, const float *dt_bias, const float *g,
+                      const float *dg, const float *dbeta, void *da, void *db, float *dA_log, float *ddt_bias,
+                      float *work, size_t tokens, int Hv, int in_dt, int grad_dt, int log_space, float beta_scale,
+                      hipStream_t st) {
+    const unsigned nblk = nblocks(tokens, ops::GATE_TOK);
+    if (nblk)
+        hipLaunchKernelGGL(ops::gates_bwd_kernel, dim3(nblk), dim3(ops::NT), 0, st, a, b, A_log, dt_bias, g, dg, dbeta,
+                           da, db, work, tokens, Hv, in_dt, grad_dt, log_space, beta_scale);
+    launch_colsum(work, (int)nblk, 2 * Hv, dA_log, ddt_bias, Hv, st);  // partial rows are [dA_log | ddt_bias]
+}
+
+void launch_l2norm_fwd(const void *x, void *y, size_t rows, int D, float eps, float scale, int dt, bool vec,
+                       hipStream_t st) {
+    if (!rows) return;
+    const int L = vec ? row_lanes(D) : 0;
+    switch (L) {
+#define GDN_L2F(LL)                                                                                                   \
+    case LL:                                                                                                          \
+        hipLaunchKernelGGL(ops::l2norm_fwd_vec<LL>, dim3(nblocks(rows, ops::NT / LL)), dim3(ops::NT), 0, st, x, y,   \
+                           rows, eps, scale, dt);                                                                     \
+        break;
+        GDN_L2F(4) GDN_L2F(8) GDN_L2F(16) GDN_L2F(32) GDN_L2F(64)
+#undef GDN_L2F
+    default:
+        hipLaunchKernelGGL(ops::l2norm_fwd_any, dim3(nblocks(rows, ops::NT / 64)), dim3(ops::NT), 0, st, x, y, rows,
+                           D, eps, scale, dt);
+    }
+}
+
+void launch_l2norm_bwd(const void *x, const void *dy, void *dx, size_t rows, int D, float eps, float scale, int dt,
+                       int dy_dt, bool vec, hipStream_t st) {
+    if (!rows) return;
+    const int L = vec ? row_lanes(D) : 0;
+    switch (L) {
+#define GDN_L2B(LL)                                                                                                   \
+    case LL:                                                                                                          \
+        hipLaunchKernelGGL(ops::l2norm_bwd_vec<LL>, dim3(nblocks(rows, ops::NT / LL)), dim3(ops::NT), 0, st, x, dy,  \
+                           dx, rows, eps, scale, dt, dy_dt);                                                          \
+        break;
+        GDN_L2B(4) GDN_L2B(8) GDN_L2B(16) GDN_L2B(32) GDN_L2B(64)
+#undef GDN_L2B
+    default:
+        hipLaunchKernelGGL(ops::l2norm_bwd_any, dim3(nblocks(rows, ops::NT / 64)), dim3(ops::NT), 0, st, x, dy, dx,
+                           rows, D, eps, scale, dt, dy_dt);
+    }
+}
+
+int conv_kmax() { return 8; }
+
+static dim3 conv_grid(int B, int T, int C, int V) {
+    return dim3(nblocks(C, 64 * V), nblocks(T, ops::CONV_SLICES * ops::CONV_TT), B);
+}
+
+template <int K>
+static void conv_fwd_k(const void *x, const float *w, const float *state_in, void *out, int B, int T, int C, int dt,
+                       bool vec, hipStream_t st) {
+    if (vec)
+        hipLaunchKernelGGL((ops::conv_fwd_kernel<K, 4>), conv_grid(B, T, C, 4), dim3(ops::NT), 0, st, x, w, state_in,
+                           out, T, C, dt);
+    else
+        hipLaunchKernelGGL((ops::conv_fwd_kernel<K, 1>), conv_grid(B, T, C, 1), dim3(ops::NT), 0, st, x, w, state_in,
+                           out, T, C, dt);
+}
+
+void launch_conv_fwd(const void *x, const float *w, const float *state_in, void *out, float *state_out, int B, int T,
+                     int C, int K, int dt, bool vec, hipStream_t st) {
+    if (B && T && C) {
+        switch (K) {
+        case 2: conv_fwd_k<2>(x, w, state_in, out, B, T, C, dt, vec, st); break;
+        case 3: conv_fwd_k<3>(x, w, state_in, out, B, T, C, dt, vec, st); break;
+        case 4: conv_fwd_k<4>(x, w, state_in, out, B, T, C, dt, vec, st); break;
+        case 5: conv_fwd_k<5>(x, w, state_in, out, B, T, C, dt, vec, st); break;
+        case 6: conv_fwd_k<6>(x, w, state_in, out, B, T, C, dt, vec, st); break;
+        case 7: conv_fwd_k<7>(x, w, state_in, out, B, T, C, dt, vec, st); break;
+        case 8: conv_fwd_k<8>(x, w, state_in, out, B, T, C, dt, vec, st); break;
+        default: break;
+        }
+    }
+    if (state_out && B && C)
+        hipLaunchKernelGGL(ops::conv_state_kernel, dim3(nblocks((size_t)B * (K - 1) * C, ops::NT)), dim3(ops::NT), 0,
+                           st, x, state_in, state_out, B, T, C, K, dt);
+}
+
+size_t conv_bwd_work_floats(int B, int T, int C, int K) {
+    return (size_t)B * nblocks(T, ops::CONV_SLICES * ops::CONV_TT) * C * K;
+}
+
+template <int K>
+static void conv_bwd_k(const void *x, const float *w, const float *state_in, const void *dout, void *dx, float *work,
+                       int B, int T, int C, int dt, int dout_dt, bool vec, hipStream_t st) {
+    if (vec)
+        hipLaunchKernelGGL((ops::conv_bwd_kernel<K, 4>), conv_grid(B, T, C, 4), dim3(ops::NT), 0, st, x, w, state_in,
+                           dout, dx, work, T, C, dt, dout_dt);
+    else
+        hipLaunchKernelGGL((ops::conv_bwd_kernel<K, 1>), conv_grid(B, T, C, 1), dim3(ops::NT), 0, st, x, w, state_in,
+                           dout, dx, work, T, C, dt, dout_dt);
+}
+
+void launch_conv_bwd(const void *x, const float *w, const float *state_in, const void *dout, void *dx, float *dw,
+                     float *work, int B, int T, int C, int K, int dt, int dout_dt, bool vec, hipStream_t st) {
+    if (!C) return;
+    const int nparts = (B && T) ? (int)(B * nblocks(T, ops::CONV_SLICES * ops::CONV_TT)) : 0;
+    if (nparts) {
+        switch (K) {
+        case 2: conv_bwd_k<2>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
+        case 3: conv_bwd_k<3>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
+        case 4: conv_bwd_k<4>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
+        case 5: conv_bwd_k<5>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
+        case 6: conv_bwd_k<6>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
+        case 7: conv_bwd_k<7>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
+        case 8: conv_bwd_k<8>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
+        default: return;
+        }
+    }
+    launch_colsum(work, nparts, C * K, dw, dw, C * K, st);  // with no tokens: dw = 0
+}
+
+int grms_dmax() { return ops::GRMS_DMAX; }
+
+void launch_grms_fwd(const void *y, const void *z, const float *w, void *out, size_t rows, int D, float eps, int dt,
+                     int z_dt, bool vec, hipStream_t st) {
+    if (!rows) return;
+    const int L = vec ? row_lanes(D) : 0;
+    switch (L) {
+#define GDN_GF(LL)                                                                                                    \
+    case LL:                                                                                                          \
+        hipLaunchKernelGGL(ops::grms_fwd_vec<LL>, dim3(nblocks(rows, ops::NT / LL)), dim3(ops::NT), 0, st, y, z, w,  \
+                           out, rows, eps, dt, z_dt);                                                                 \
+        break;
+        GDN_GF(4) GDN_GF(8) GDN_GF(16) GDN_GF(32) GDN_GF(64)
+#undef GDN_GF
+    default:
+        hipLaunchKernelGGL(ops::grms_fwd_any, dim3(nblocks(rows, ops::NT / 64)), dim3(ops::NT), 0, st, y, z, w, out,
+                           rows, D, eps, dt, z_dt);
+    }
+}
+
+size_t grms_bwd_work_floats(size_t rows, int D) { return (size_t)nblocks(rows, ops::GRMS_ROWS) * D; }
+
+void launch_grms_bwd(const void *y, const void *z, const float *w, const void *dout, void *dy, void *dz, float *dw,
+                     float *work, size_t rows, int D, float eps, int dt, int z_dt, int dout_dt, bool vec,
+                     hipStream_t st) {
+    const unsigned nblk = nblocks(rows, ops::GRMS_ROWS);
+    const int L = vec ? row_lanes(D) : 0;
+    if (nblk) {
+        switch (L) {
+#define GDN_GB(LL)                                                                                                    \
+    case LL:                                                                                                          \
+        hipLaunchKernelGGL(ops::grms_bwd_vec<LL>, dim3(nblk), dim3(ops::NT), 0, st, y, z, w, dout, dy, dz, work,     \
+                           rows, eps, dt, z_dt, dout_dt);                                                             \
+        break;
+            GDN_GB(4) GDN_GB(8) GDN_GB(16) GDN_GB(32) GDN_GB(64)
+#undef GDN_GB
+        default:
+            hipLaunchKernelGGL(ops::grms_bwd_any, dim3(nblk), dim3(ops::NT), 0, st, y, z, w, dout, dy, dz, work, rows,
+                               D, eps, dt, z_dt, dout_dt);
+        }
+    }
+    launch_colsum(work, (int)nblk, D, dw, dw, D, st);  // with no rows: dw = 0
+}
+
+}  // namespace gdn

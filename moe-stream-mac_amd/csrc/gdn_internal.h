@@ -63,4 +63,33 @@ void launch_rec_bwd_reduce(const RecBwdArgs &a, hipStream_t st);
 void launch_reduce_qk(const RecBwdArgs &a, hipStream_t st);
 void launch_copy_or_zero(float *dst, const float *src, size_t n, hipStream_t st);
 
+// Block ops around the recurrence (gdn_block_ops.hip).  `vec` selects the vector-load kernels; the caller
+// checks alignment and shape for them.
+int row_lanes(int D);
+int gates_max_heads();
+int conv_kmax();
+int grms_dmax();
+size_t gates_bwd_work_floats(size_t tokens, int Hv);
+size_t conv_bwd_work_floats(int B, int T, int C, int K);
+size_t grms_bwd_work_floats(size_t rows, int D);
+void launch_gates_fwd(const void *a, const void *b, const float *A_log, const float *dt_bias, float *g, float *beta,
+                      size_t tokens, int Hv, int in_dt, int log_space, float beta_scale, hipStream_t st);
+void launch_gates_bwd(const void *a, const void *b, const float *A_log, const float *dt_bias, const float *g,
+                      const float *dg, const float *dbeta, void *da, void *db, float *dA_log, float *ddt_bias,
+                      float *work, size_t tokens, int Hv, int in_dt, int grad_dt, int log_space, float beta_scale,
+                      hipStream_t st);
+void launch_l2norm_fwd(const void *x, void *y, size_t rows, int D, float eps, float scale, int dt, bool vec,
+                       hipStream_t st);
+void launch_l2norm_bwd(const void *x, const void *dy, void *dx, size_t rows, int D, float eps, float scale, int dt,
+                       int dy_dt, bool vec, hipStream_t st);
+void launch_conv_fwd(const void *x, const float *w, const float *state_in, void *out, float *state_out, int B, int T,
+                     int C, int K, int dt, bool vec, hipStream_t st);
+void launch_conv_bwd(const void *x, const float *w, const float *state_in, const void *dout, void *dx, float *dw,
+                     float *work, int B, int T, int C, int K, int dt, int dout_dt, bool vec, hipStream_t st);
+void launch_grms_fwd(const void *y, const void *z, const float *w, void *out, size_t rows, int D, float eps, int dt,
+                     int z_dt, bool vec, hipStream_t st);
+void launch_grms_bwd(const void *y, const void *z, const float *w, const void *dout, void *dy, void *dz, float *dw,
+                     float *work, size_t rows, int D, float eps, int dt, int z_dt, int dout_dt, bool vec,
+                     hipStream_t st);
+
 }  // namespace gdn

@@ -13,25 +13,32 @@ import math
 from typing import Optional
 
 import torch
-import torch.nn.functional as F
 
+import gdn_block
 import gdn_engine
 
 Array = torch.Tensor
 
 
 def compute_g(A_log: Array, a: Array, dt_bias: Array) -> Array:
-    """Multiplicative decay exp(-exp(A_log) * softplus(a + dt_bias)) (engine/include/gdn.h:20-25)."""
-    return torch.exp(-torch.exp(A_log.float()) * F.softplus((a + dt_bias).float()))
+    """Multiplicative decay exp(-exp(A_log) * softplus(a + dt_bias)) (engine/include/gdn.h:20-25), float32,
+    on the fused gates kernel."""
+    return gdn_block.gates(a, a, A_log, dt_bias)[0]
+
+
+def gates(a: Array, b: Array, A_log: Array, dt_bias: Array, allow_neg_eigval: bool = False,
+          lower_bound: float | None = None) -> tuple[Array, Array]:
+    """(decay, beta) of the update functions (tools/gdn_vjp.py:554-558): beta = sigmoid(b), x2 when
+    allow_neg_eigval; decay = compute_g(A_log, a, dt_bias).  One fused HIP kernel forward and backward."""
+    if lower_bound is not None:
+        raise NotImplementedError("lower_bound gates are not supported by this engine")
+    return gdn_block.gates(a, b, A_log, dt_bias, allow_neg_eigval=allow_neg_eigval)
 
 
 def normalize_qk(q: Array, k: Array, inv_scale: float, eps: float = 1e-6) -> tuple[Array, Array]:
     """q <- inv_scale * q / sqrt(sum q^2 + eps), k <- k / sqrt(sum k^2 + eps) (engine/include/gdn.h:17-18,
-    engine/src/gdn_layer.c:35-39)."""
-    qf, kf = q.float(), k.float()
-    qn = qf * (inv_scale * torch.rsqrt((qf * qf).sum(-1, keepdim=True) + eps))
-    kn = kf * torch.rsqrt((kf * kf).sum(-1, keepdim=True) + eps)
-    return qn.to(q.dtype), kn.to(k.dtype)
+    engine/src/gdn_layer.c:35-39), on the L2-norm kernel."""
+    return gdn_block.normalize_qk(q, k, inv_scale, eps)
 
 
 def _default_state(q: Array, v: Array, state: Optional[Array]) -> Array:
@@ -71,12 +78,7 @@ def gated_delta_update(
     allow_neg_eigval: bool = False,
 ) -> tuple[Array, Array]:
     """Gates from (a, b, A_log, dt_bias), then the recurrence (mlx-lm ``gated_delta_update`` contract)."""
-    beta = torch.sigmoid(b)
-    if allow_neg_eigval:
-        beta = beta * 2.0
-    if lower_bound is not None:
-        raise NotImplementedError("lower_bound gates are not supported by this engine")
-    g = compute_g(A_log, a, dt_bias)
+    g, beta = gates(a, b, A_log, dt_bias, allow_neg_eigval, lower_bound)
     if use_kernel:
         return gated_delta_kernel(q, k, v, g, beta, state, mask)
     return gated_delta_ops(q, k, v, g, beta, state, mask)

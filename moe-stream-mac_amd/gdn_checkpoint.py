@@ -71,12 +71,7 @@ def _checkpointed_update(
             q, k, v, a, b, A_log, dt_bias, state, mask,
             use_kernel=use_kernel, lower_bound=lower_bound, allow_neg_eigval=allow_neg_eigval,
         )
-    beta = torch.sigmoid(b)
-    if allow_neg_eigval:
-        beta = beta * 2.0
-    if lower_bound is not None:
-        raise NotImplementedError("lower_bound gates are not supported by this engine")
-    g = gated_delta.compute_g(A_log, a, dt_bias)
+    g, beta = gated_delta.gates(a, b, A_log, dt_bias, allow_neg_eigval, lower_bound)
     if state is None:
         batch, _, _, key_dim = q.shape
         value_heads, value_dim = v.shape[-2:]

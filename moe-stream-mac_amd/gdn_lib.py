@@ -27,7 +27,21 @@ DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
 _SIGS = {
+    "gdn_gates_fwd": ([_vp] * 6 + [_i64, _i, _i, _i, _i, _vp], _i),
+    "gdn_gates_bwd_workspace_bytes": ([_i64, _i], _sz),
+    "gdn_gates_bwd": ([_vp] * 12 + [_sz, _i64, _i, _i, _i, _i, _i, _vp], _i),
+    "gdn_l2norm_fwd": ([_vp, _vp, _i64, _i, _f, _f, _i, _vp], _i),
+    "gdn_l2norm_bwd": ([_vp, _vp, _vp, _i64, _i, _f, _f, _i, _i, _vp], _i),
+    "gdn_conv_silu_fwd": ([_vp] * 5 + [_i] * 5 + [_vp], _i),
+    "gdn_conv_silu_bwd_workspace_bytes": ([_i] * 4, _sz),
+    "gdn_conv_silu_bwd": ([_vp] * 7 + [_sz] + [_i] * 6 + [_vp], _i),
+    "gdn_gated_rmsnorm_fwd": ([_vp] * 4 + [_i64, _i, _f, _i, _i, _vp], _i),
+    "gdn_gated_rmsnorm_bwd_workspace_bytes": ([_i64, _i], _sz),
+    "gdn_gated_rmsnorm_bwd": ([_vp] * 8 + [_sz, _i64, _i, _f, _i, _i, _i, _vp], _i),
     "gdn_version": ([], _i),
     "gdn_last_error": ([], ctypes.c_char_p),
     "gdn_num_snapshots": ([_i, _i], ctypes.c_int64),

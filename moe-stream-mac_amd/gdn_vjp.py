@@ -91,12 +91,7 @@ def _vjp_update(
             use_kernel=use_kernel, lower_bound=lower_bound,
             allow_neg_eigval=allow_neg_eigval
         )
-    beta = torch.sigmoid(b)
-    if allow_neg_eigval:
-        beta = beta * 2.0
-    if lower_bound is not None:
-        raise NotImplementedError("lower_bound gates are not supported by this engine")
-    g = gated_delta.compute_g(A_log, a, dt_bias)
+    g, beta = gated_delta.gates(a, b, A_log, dt_bias, allow_neg_eigval, lower_bound)
     impl = "kernel" if q.shape[-1] % 32 == 0 and q.dtype == k.dtype == v.dtype else "staged"
     return gated_delta_chunked(q, k, v, g, beta, state, mask, impl=impl)
 

@@ -22,6 +22,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+import gdn_block
 from gated_delta import gated_delta_update, normalize_qk  # noqa: F401  (rebound by install())
 
 Array = torch.Tensor
@@ -59,9 +60,7 @@ class RMSNormGated(nn.Module):
         self.eps = eps
 
     def forward(self, y: Array, z: Array) -> Array:
-        yf = y.float()
-        n = yf * torch.rsqrt((yf * yf).mean(-1, keepdim=True) + self.eps)
-        return (n * self.weight.float() * F.silu(z.float())).to(y.dtype)
+        return gdn_block.gated_rmsnorm(y, z, self.weight, self.eps)
 
 
 class GatedDeltaNet(nn.Module):
@@ -92,7 +91,7 @@ class GatedDeltaNet(nn.Module):
         a = self.in_proj_a(x)
         if mask is not None:
             qkv = qkv * mask[..., None].to(qkv.dtype)
-        conv = F.silu(self.conv1d(qkv.transpose(1, 2))[..., :T]).transpose(1, 2)
+        conv = gdn_block.conv_silu(qkv, self.conv1d.weight)
         q, k, v = torch.split(conv, [self.key_dim, self.key_dim, self.value_dim], dim=-1)
         q = q.reshape(B, T, self.Hk, self.Dk)
         k = k.reshape(B, T, self.Hk, self.Dk)

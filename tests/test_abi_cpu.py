@@ -60,6 +60,56 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert fwd(0, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0) == 0
 
 
+def test_block_op_abi_rejects_bad_arguments_without_launching():
+    lib = gdn_lib.load()
+    L = gdn_lib
+    null, fake = None, ctypes.c_void_p(256)   # never dereferenced: every call below fails its checks first
+    assert lib.gdn_gates_fwd(*([fake] * 6), 10, 257, 0, 0, 0, null) == L.GDN_ERR_UNSUPPORTED
+    assert lib.gdn_gates_fwd(*([fake] * 6), -1, 4, 0, 0, 0, null) == L.GDN_ERR_INVALID
+    assert lib.gdn_gates_fwd(*([fake] * 6), 10, 4, 5, 0, 0, null) == L.GDN_ERR_INVALID
+    assert lib.gdn_gates_fwd(*([null] * 6), 10, 4, 0, 0, 0, null) == L.GDN_ERR_INVALID
+    assert b"null" in lib.gdn_last_error()
+    assert lib.gdn_gates_fwd(*([null] * 6), 0, 4, 0, 0, 0, null) == 0   # no tokens: nothing to do
+    need = lib.gdn_gates_bwd_workspace_bytes(1000, 32)
+    assert need >= 4 * 2 * 32 * 4 and need % 256 == 0
+    rc = lib.gdn_gates_bwd(*([fake] * 12), need - 1, 1000, 32, 0, 0, 0, 0, null)
+    assert rc == L.GDN_ERR_WORKSPACE
+    assert lib.gdn_l2norm_fwd(fake, fake, 4, 0, 1e-6, 1.0, 0, null) == L.GDN_ERR_INVALID
+    assert lib.gdn_l2norm_bwd(null, null, null, 4, 128, 1e-6, 1.0, 0, 0, null) == L.GDN_ERR_INVALID
+    assert lib.gdn_l2norm_fwd(null, null, 0, 128, 1e-6, 1.0, 0, null) == 0
+    conv = lambda B, T, C, K, dt=0, s_in=null, s_out=null: lib.gdn_conv_silu_fwd(fake, fake, s_in, fake, s_out,
+                                                                                 B, T, C, K, dt, null)
+    assert conv(1, 4, 8, 1) == L.GDN_ERR_INVALID and b"K must be >= 2" in lib.gdn_last_error()
+    assert conv(1, 4, 8, 9) == L.GDN_ERR_UNSUPPORTED
+    assert conv(1, 4, 8, 4, dt=3) == L.GDN_ERR_INVALID
+    assert conv(1, 4, 8, 4, s_in=fake, s_out=fake) == L.GDN_ERR_INVALID
+    assert b"alias" in lib.gdn_last_error()
+    ws = lib.gdn_conv_silu_bwd_workspace_bytes(2, 8192, 8192, 4)
+    assert ws == 2 * 32 * 8192 * 4 * 4   # one partial per (batch, 256 tokens) x C x K floats
+    rc = lib.gdn_conv_silu_bwd(*([fake] * 7), ws - 1, 2, 8192, 8192, 4, 1, 1, null)
+    assert rc == L.GDN_ERR_WORKSPACE
+    assert lib.gdn_gated_rmsnorm_fwd(fake, fake, fake, fake, 4, 0, 1e-6, 0, 0, null) == L.GDN_ERR_INVALID
+    rc = lib.gdn_gated_rmsnorm_bwd(*([fake] * 8), 1 << 20, 4, 4097, 1e-6, 0, 0, 0, null)
+    assert rc == L.GDN_ERR_UNSUPPORTED and b"4096" in lib.gdn_last_error()
+    ws = lib.gdn_gated_rmsnorm_bwd_workspace_bytes(2 * 8192 * 32, 128)
+    assert ws == 2 * 8192 * 32 // 512 * 128 * 4
+    rc = lib.gdn_gated_rmsnorm_bwd(*([fake] * 8), ws - 1, 2 * 8192 * 32, 128, 1e-6, 1, 1, 1, null)
+    assert rc == L.GDN_ERR_WORKSPACE
+
+
+def test_block_wrappers_error_on_cpu_tensors():
+    import gdn_block
+    x = torch.zeros(2, 4, 8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        gdn_block.conv_silu(x, torch.zeros(8, 4))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        gdn_block.l2norm(x)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        gdn_block.gated_rmsnorm(x, x, torch.ones(8))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        gdn_block.gates(x, x, torch.zeros(8), torch.zeros(8))
+
+
 def test_saved_sizes_by_form():
     lib = gdn_lib.load()
     L = gdn_lib
