@@ -11,6 +11,10 @@ Workloads (one GPU; the default is the T=4096 configuration the metric is quoted
   fp32_b1_t4096   B=1, T=4096, same heads, fp32
   fp32_b1_t2048   B=1, T=2048, fp32, S0 ~ N(0, 0.02), full dS0
   ckpt_b1_t16384  B=1, T=16384, fp32, snapshots every 256 tokens, peak HBM reported
+  block_bf16_b2_t8192
+                  one whole GDN block (projections with LoRA rank 16, conv1d K=4 + SiLU, q/k L2 norm, gates,
+                  recurrence, gated RMSNorm * SiLU(z), out-projection), B=2, T=8192, hidden 2048, bf16 weights
+                  and activations; a step is forward + backward to the LoRA parameters and the input
 """
 
 from __future__ import annotations
@@ -61,6 +65,24 @@ def kernel_model(name, B, T, Hk, Hv, D, in_b):
         return 7 * tokh * D * D, B * T * (2 * Hk * D * in_b + Hv * D * in_b * 2 + 2 * Hv * 4)
     if name == "rec_bwd":
         return 20 * tokh * D * D, B * T * (2 * Hk * D * in_b + 3 * Hv * D * in_b + 2 * Hv * 4)
+    # block ops (per launch): conv over C = 2*Hk*D + Hv*D channels; the L2 norm runs once for q and once for k
+    C = 2 * Hk * D + Hv * D
+    if name == "conv_fwd":
+        return 0, B * T * C * 2 * in_b
+    if name == "conv_bwd":
+        return 0, B * T * C * 3 * in_b
+    if name == "l2norm_fwd":
+        return 0, B * T * Hk * D * 2 * in_b
+    if name == "l2norm_bwd":
+        return 0, B * T * Hk * D * 3 * in_b
+    if name == "gates_fwd":
+        return 0, tokh * (2 * in_b + 8)
+    if name == "gates_bwd":
+        return 0, tokh * (4 * in_b + 12)
+    if name == "grms_fwd":
+        return 0, tokh * D * 3 * in_b
+    if name == "grms_bwd":
+        return 0, tokh * D * 5 * in_b
     return 0, 0
 
 WORKLOADS = {
@@ -68,6 +90,8 @@ WORKLOADS = {
     "fp32_b1_t4096": dict(B=1, T=4096, Hk=16, Hv=32, D=128, dtype="fp32", chunk=64, s0_std=0.0),
     "fp32_b1_t2048": dict(B=1, T=2048, Hk=16, Hv=32, D=128, dtype="fp32", chunk=64, s0_std=0.02),
     "ckpt_b1_t16384": dict(B=1, T=16384, Hk=16, Hv=32, D=128, dtype="fp32", chunk=256, s0_std=0.0),
+    "block_bf16_b2_t8192": dict(B=2, T=8192, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
+                                block=dict(hidden=2048, K=4, rank=16, lora_scale=20.0)),
 }
 
 
@@ -95,6 +119,32 @@ def make_inputs(w, dev, seed=0):
     dy = n(B, T, Hv, D)
     return dict(q=q.to(dt), k=k.to(dt), v=v.to(dt), g_log=g_log.contiguous(), beta=beta.contiguous(),
                 state=state.contiguous(), dy=dy.to(dt))
+
+
+def make_block(w, dev, seed=0):
+    """One GDN block with LoRA adapters on its five projections (base frozen), bf16, plus input and output
+    cotangent: projection weights ~ N(0, 0.02), LoRA A ~ N(0, 0.02), B = 0; conv, A_log, dt_bias and norm weight
+    at the module's initialisation."""
+    import torch
+    import qwen3_5 as Q
+    torch.manual_seed(seed)
+    bw = w["block"]
+    args = Q.ModelArgs(hidden_size=bw["hidden"], linear_num_key_heads=w["Hk"], linear_num_value_heads=w["Hv"],
+                       linear_key_head_dim=w["D"], linear_value_head_dim=w["D"], linear_conv_kernel_dim=bw["K"])
+    blk = Q.GatedDeltaNet(args)
+    with torch.no_grad():
+        for m in (blk.in_proj_qkv, blk.in_proj_z, blk.in_proj_b, blk.in_proj_a, blk.out_proj):
+            m.weight.normal_(0.0, 0.02)
+    Q.freeze(blk)
+    for n in ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a", "out_proj"):
+        setattr(blk, n, Q.LoRALinear(getattr(blk, n), bw["rank"], bw["lora_scale"]))
+    blk = blk.to(device=dev, dtype=torch.bfloat16).train()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    shape = (w["B"], w["T"], bw["hidden"])
+    x = torch.randn(shape, device=dev, generator=gen).to(torch.bfloat16).requires_grad_(True)
+    dout = torch.randn(shape, device=dev, generator=gen).to(torch.bfloat16)
+    return blk, x, dout
 
 
 def cpu_info():
@@ -167,15 +217,22 @@ def main():
         log(f"bench: calibration copy of {args.copy_calibration} MiB done")
         del src, dst
     log(f"bench: workload {args.workload} {w}")
-    x = make_inputs(w, dev)
     B, T, Hk, Hv, D = w["B"], w["T"], w["Hk"], w["Hv"], w["D"]
-    out_dtype = x["q"].dtype
-    leaves = [x[n].requires_grad_(True) for n in ("q", "k", "v", "g_log", "beta", "state")]
+    if "block" in w:
+        blk, xb, dout = make_block(w, dev)
+        leaves = [xb] + [p for p in blk.parameters() if p.requires_grad]
 
-    def step():
-        y, S = gdn_engine.recurrence(x["q"], x["k"], x["v"], x["g_log"], x["beta"], x["state"], None,
-                                     chunk=w["chunk"], log_gate=True, output_dtype=out_dtype)
-        return torch.autograd.grad([y], leaves, [x["dy"]])
+        def step():
+            return torch.autograd.grad(blk(xb), leaves, dout)
+    else:
+        x = make_inputs(w, dev)
+        out_dtype = x["q"].dtype
+        leaves = [x[n].requires_grad_(True) for n in ("q", "k", "v", "g_log", "beta", "state")]
+
+        def step():
+            y, S = gdn_engine.recurrence(x["q"], x["k"], x["v"], x["g_log"], x["beta"], x["state"], None,
+                                         chunk=w["chunk"], log_gate=True, output_dtype=out_dtype)
+            return torch.autograd.grad([y], leaves, [x["dy"]])
 
     for i in range(args.warmup):
         step()
@@ -223,6 +280,9 @@ def main():
         "algo_flops_per_launch": flops, "algo_bytes_per_launch": nbytes,
         "other_roof_frac": round(min(f_frac, b_frac), 4),
         "kernels_ms_per_step": {n: round(v[0] / args.steps, 4) for n, v in kt.items()}})
+    if "block" in w:
+        lib_ms = sum(v[0] for v in kt.values()) / args.steps
+        roofline["outside_library_ms_per_step"] = round(elapsed / args.steps * 1e3 - lib_ms, 4)
     form = "chunk" if any(n.startswith("ck_") for n in kt) else "recurrent"
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -231,7 +291,7 @@ def main():
         "dtype": "bf16" if (w["dtype"] == "bf16" and form == "chunk") else "fp32", "data": "synthetic",
         "config": {"workload": args.workload, "B": B, "T": T, "Hk": Hk, "Hv": Hv, "Dk": D, "Dv": D,
                    "chunk": w["chunk"], "inputs": w["dtype"], "state": "fp32", "form": form,
-                   "global_batch": B, "seq_len": T, "parallelism": "single-gpu"},
+                   "global_batch": B, "seq_len": T, "parallelism": "single-gpu", **w.get("block", {})},
         "peak_hbm_gib": round(peak_gib, 3),
         "roofline": roofline,
     }

@@ -40,3 +40,38 @@ def vjp(q, k, v, g, beta, state, mask, dy, dstate):
     grads = torch.autograd.grad(loss, xs, allow_unused=True)
     grads = [torch.zeros_like(x) if gr is None else gr for x, gr in zip(xs, grads)]
     return [t.detach().numpy() for t in (y, S, *grads)]
+
+
+def gdn_block(x, P, Hk, Hv, Dk, Dv, eps=1e-6):
+    """One GDN block over a sequence in float64 torch ops, written from engine/src/gdn_layer.c:18-58:
+    projections (W + scale B A when a LoRA adapter is present), causal depthwise conv + SiLU, per-head L2 norm
+    (q scaled by Dk^-1/2), gates, the recurrence from a zero state, rmsnorm(y) * w * silu(z), out-projection.
+    P maps names to float64 tensors (those requiring grad are differentiated by the caller)."""
+    import torch.nn.functional as F
+
+    def W(n):
+        w = P["W_" + n]
+        if ("A_" + n) in P:
+            w = w + P["lora_scale"] * P["B_" + n] @ P["A_" + n]
+        return w
+
+    B, T, _ = x.shape
+    qkv, z, b, a = (F.linear(x, W(n)) for n in ("qkv", "z", "b", "a"))
+    K = P["conv_w"].shape[1]
+    pre = F.conv1d(qkv.transpose(1, 2), P["conv_w"][:, None, :], padding=K - 1, groups=qkv.shape[-1])[..., :T]
+    c = F.silu(pre).transpose(1, 2)
+    kd = Hk * Dk
+    q = c[..., :kd].reshape(B, T, Hk, Dk)
+    k = c[..., kd:2 * kd].reshape(B, T, Hk, Dk)
+    v = c[..., 2 * kd:].reshape(B, T, Hv, Dv)
+    q = q * (Dk ** -0.5) / torch.sqrt((q * q).sum(-1, keepdim=True) + eps)
+    k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + eps)
+    t = a + P["dt_bias"]
+    sp = torch.where(t > 20, t, torch.log1p(torch.exp(torch.clamp(t, max=20.0))))
+    decay = torch.exp(-torch.exp(P["A_log"]) * sp)
+    beta = torch.sigmoid(b)
+    y, _ = recurrence(q, k, v, decay, beta, x.new_zeros((B, Hv, Dv, Dk)))
+    zh = z.reshape(B, T, Hv, Dv)
+    n = y / torch.sqrt((y * y).mean(-1, keepdim=True) + eps)
+    o = (n * P["norm_w"] * F.silu(zh)).reshape(B, T, Hv * Dv)
+    return F.linear(o, W("out"))

@@ -288,3 +288,39 @@ def test_make_inputs_distributions():
     np.testing.assert_allclose(np.linalg.norm(d["q"], axis=-1), 128 ** -0.5, atol=1e-5)
     assert (d["g_log"] < 0).all() and (d["g_log"] > -16 * 25).all()
     assert abs(float(d["state"].std()) - 0.02) < 1e-3
+
+
+# ---------------------------------------------------------------- whole block (forward + VJP with LoRA)
+
+def test_block_vjp_matches_torch_autograd():
+    """The composed block VJP against torch float64 autograd of tests/naive_torch.py::gdn_block, with LoRA
+    adapters on all five projections (B random so that every adapter gradient is non-zero)."""
+    from oracle import gdn_block_oracle as BO
+    Bsz, T, h, Hk, Hv, Dk, Dv = 2, 37, 12, 2, 4, 8, 6
+    P = BO.make_block_params(h, Hk, Hv, Dk, Dv, K=4, rank=3, b_std=0.05, seed=1, w_std=0.3)
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((Bsz, T, h))
+    dout = rng.standard_normal((Bsz, T, h))
+    out, g = BO.block_vjp(x, P, dout, Hk, Hv, Dk, Dv, chunk=16)
+    tP = {k: (torch.tensor(np.asarray(v, np.float64), requires_grad=True) if isinstance(v, np.ndarray) else v)
+          for k, v in P.items()}
+    tx = torch.tensor(x, requires_grad=True)
+    tout = naive_torch.gdn_block(tx, tP, Hk, Hv, Dk, Dv)
+    np.testing.assert_allclose(out, tout.detach().numpy(), rtol=1e-9, atol=1e-12)
+    names = ["x", "conv_w", "A_log", "dt_bias", "norm_w"] + [f"{p}_{n}" for n in BO.PROJ for p in ("A", "B")]
+    leaves = [tx] + [tP[n] for n in names[1:]]
+    tg = torch.autograd.grad(tout, leaves, torch.tensor(dout))
+    for n, want in zip(names, tg):
+        np.testing.assert_allclose(g[n], want.numpy(), rtol=1e-8, atol=1e-10, err_msg=n)
+
+
+def test_block_lora_b_zero_gives_zero_a_gradient():
+    """With B = 0 (the LoRA initialisation) grad(A) = s B^T dW is exactly zero and grad(B) is not."""
+    from oracle import gdn_block_oracle as BO
+    P = BO.make_block_params(12, 2, 4, 8, 6, rank=3, b_std=0.0, seed=3, w_std=0.3)
+    rng = np.random.default_rng(4)
+    x, dout = rng.standard_normal((1, 20, 12)), rng.standard_normal((1, 20, 12))
+    _, g = BO.block_vjp(x, P, dout, 2, 4, 8, 6, chunk=8)
+    for n in BO.PROJ:
+        assert not np.any(g["A_" + n])
+        assert np.abs(g["B_" + n]).max() > 0
