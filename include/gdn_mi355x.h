@@ -167,6 +167,25 @@ int gdn_conv_silu_bwd(const void *x, const float *w, const float *state_in, cons
                       void *workspace, size_t workspace_bytes, int B, int T, int C, int K, int dtype, int dout_dtype,
                       void *stream);
 
+/* Conv + SiLU fused with the split into q, k, v and the per-head L2 norm of q and k: steps 2-4 of one block
+ * (engine/src/gdn_layer.c:29-39, gdn_conv_step then gdn_l2norm per head) in one pass over the sequence.
+ *   x [B][T][C], C = 2*Hk*Dk + Hv*Dv, channels [0, Hk*Dk) are q, [Hk*Dk, 2*Hk*Dk) k, the rest v;
+ *   q, k [B][T][Hk][Dk] and v [B][T][Hv][Dv] (dtype) receive silu(conv(x)), q scaled by
+ *   q_scale / sqrt(sum q_h^2 + eps) and k by 1 / sqrt(sum k_h^2 + eps) per head;
+ *   w, state_in, state_out as gdn_conv_silu_fwd.
+ * Needs K = 4, 16-byte aligned buffers, C % 4 == 0 and Dk / 8 (16-bit data; Dk / 4 for fp32) a power of two in
+ * [4, 64]; other shapes return GDN_ERR_UNSUPPORTED (compose gdn_conv_silu_fwd and gdn_l2norm_fwd instead). */
+int gdn_conv_qkv_fwd(const void *x, const float *w, const float *state_in, void *q, void *k, void *v,
+                     float *state_out, int B, int T, int Hk, int Dk, int Hv, int Dv, int K, float q_scale, float eps,
+                     int dtype, void *stream);
+
+/* Backward of gdn_conv_qkv_fwd from the cotangents dq, dk, dv of its outputs (g_dtype): dx [B][T][C] (dtype) and
+ * dw [C][K] fp32; workspace of gdn_conv_silu_bwd_workspace_bytes(B, T, C, K) bytes. */
+int gdn_conv_qkv_bwd(const void *x, const float *w, const float *state_in, const void *dq, const void *dk,
+                     const void *dv, void *dx, float *dw, void *workspace, size_t workspace_bytes, int B, int T,
+                     int Hk, int Dk, int Hv, int Dv, int K, float q_scale, float eps, int dtype, int g_dtype,
+                     void *stream);
+
 /* Gated RMSNorm, replacing op_rmsnorm + op_silu_mul per value head (engine/include/ops.h:7-11,
  * engine/src/gdn_layer.c:47-55):
  *   out = y / sqrt(mean(y^2) + eps) * w * silu(z)   over rows of D;  y, out [rows][D] (dtype), z (z_dtype),

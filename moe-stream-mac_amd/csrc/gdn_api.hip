@@ -464,10 +464,13 @@ int gdn_conv_silu_fwd(const void *x, const float *w, const float *state_in, void
     if (!w || (T > 0 && (!x || !out))) return fail(GDN_ERR_INVALID, "null pointer");
     if (state_out && state_out == state_in) return fail(GDN_ERR_INVALID, "state_out must not alias state_in");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    ConvCall c{};
+    c.x = x; c.w = w; c.state_in = state_in; c.v = out; c.state_out = state_out;
+    c.B = B; c.T = T; c.C = C; c.K = K; c.qk = 0; c.Dk = 0; c.dt = dtype; c.g_dt = dtype;
+    c.vec = all_aligned16({x, out});
     {
         Timed tm("conv_fwd", st);
-        launch_conv_fwd(x, w, state_in, out, state_out, B, T, C, K, dtype, C % 4 == 0 && all_aligned16({x, out}),
-                        st);
+        launch_conv_fwd(c, st);
     }
     return check_launch(st, "gdn_conv_silu_fwd");
 }
@@ -491,12 +494,78 @@ int gdn_conv_silu_bwd(const void *x, const float *w, const float *state_in, cons
         return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
                     workspace_bytes, need);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    ConvCall c{};
+    c.x = x; c.w = w; c.state_in = state_in; c.v = const_cast<void *>(dout); c.dx = dx; c.dw = dw;
+    c.work = static_cast<float *>(workspace);
+    c.B = B; c.T = T; c.C = C; c.K = K; c.qk = 0; c.Dk = 0; c.dt = dtype; c.g_dt = dout_dtype;
+    c.vec = all_aligned16({x, dout, dx});
     {
         Timed tm("conv_bwd", st);
-        launch_conv_bwd(x, w, state_in, dout, dx, dw, static_cast<float *>(workspace), B, T, C, K, dtype, dout_dtype,
-                        C % 4 == 0 && all_aligned16({x, dout, dx}), st);
+        launch_conv_bwd(c, st);
     }
     return check_launch(st, "gdn_conv_silu_bwd");
+}
+
+static int check_conv_qkv(int B, int T, int Hk, int Dk, int Hv, int Dv, int K, int dtype, int g_dtype, bool vec) {
+    if (Hk <= 0 || Dk <= 0 || Hv <= 0 || Dv <= 0) return fail(GDN_ERR_INVALID, "head counts and dims must be > 0");
+    const int64_t C = 2LL * Hk * Dk + (int64_t)Hv * Dv;
+    if (C > (1 << 30)) return fail(GDN_ERR_INVALID, "too many channels");
+    int rc = check_conv(B, T, (int)C, K, dtype);
+    if (rc) return rc;
+    if (!dtype_ok(g_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    if (!conv_qkv_supported(Dk, K, dtype, g_dtype, vec, (int)C))
+        return fail(GDN_ERR_UNSUPPORTED,
+                    "the fused conv + L2 norm needs K = 4, 16-byte aligned buffers, channels a multiple of 4 and "
+                    "Dk / (channels per lane) a power of two in [4, 64]; use gdn_conv_silu_* and gdn_l2norm_*");
+    return GDN_OK;
+}
+
+int gdn_conv_qkv_fwd(const void *x, const float *w, const float *state_in, void *q, void *k, void *v,
+                     float *state_out, int B, int T, int Hk, int Dk, int Hv, int Dv, int K, float q_scale, float eps,
+                     int dtype, void *stream) {
+    g_err[0] = 0;
+    int rc = check_conv_qkv(B, T, Hk, Dk, Hv, Dv, K, dtype, dtype, all_aligned16({x, q, k, v}));
+    if (rc) return rc;
+    if (B == 0) return GDN_OK;
+    if (!w || (T > 0 && (!x || !q || !k || !v))) return fail(GDN_ERR_INVALID, "null pointer");
+    if (state_out && state_out == state_in) return fail(GDN_ERR_INVALID, "state_out must not alias state_in");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    ConvCall c{};
+    c.x = x; c.w = w; c.state_in = state_in; c.q = q; c.k = k; c.v = v; c.state_out = state_out;
+    c.B = B; c.T = T; c.C = 2 * Hk * Dk + Hv * Dv; c.K = K; c.qk = Hk * Dk; c.Dk = Dk; c.dt = dtype; c.g_dt = dtype;
+    c.scale_q = q_scale; c.eps = eps; c.vec = true;
+    {
+        Timed tm("conv_qkv_fwd", st);
+        launch_conv_fwd(c, st);
+    }
+    return check_launch(st, "gdn_conv_qkv_fwd");
+}
+
+int gdn_conv_qkv_bwd(const void *x, const float *w, const float *state_in, const void *dq, const void *dk,
+                     const void *dv, void *dx, float *dw, void *workspace, size_t workspace_bytes, int B, int T,
+                     int Hk, int Dk, int Hv, int Dv, int K, float q_scale, float eps, int dtype, int g_dtype,
+                     void *stream) {
+    g_err[0] = 0;
+    int rc = check_conv_qkv(B, T, Hk, Dk, Hv, Dv, K, dtype, g_dtype, all_aligned16({x, dq, dk, dv, dx}));
+    if (rc) return rc;
+    const int C = 2 * Hk * Dk + Hv * Dv;
+    if (!w || !dw || (B > 0 && T > 0 && (!x || !dq || !dk || !dv || !dx))) return fail(GDN_ERR_INVALID, "null pointer");
+    const size_t need = gdn_conv_silu_bwd_workspace_bytes(B, T, C, K);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
+                    workspace_bytes, need);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    ConvCall c{};
+    c.x = x; c.w = w; c.state_in = state_in;
+    c.q = const_cast<void *>(dq); c.k = const_cast<void *>(dk); c.v = const_cast<void *>(dv);
+    c.dx = dx; c.dw = dw; c.work = static_cast<float *>(workspace);
+    c.B = B; c.T = T; c.C = C; c.K = K; c.qk = Hk * Dk; c.Dk = Dk; c.dt = dtype; c.g_dt = g_dtype;
+    c.scale_q = q_scale; c.eps = eps; c.vec = true;
+    {
+        Timed tm("conv_qkv_bwd", st);
+        launch_conv_bwd(c, st);
+    }
+    return check_launch(st, "gdn_conv_qkv_bwd");
 }
 
 static int check_grms(int64_t rows, int D, int dtype, int z_dtype, bool bwd) {

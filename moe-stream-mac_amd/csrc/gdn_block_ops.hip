@@ -161,7 +161,7 @@ __global__ __launch_bounds__(NT) void gates_fwd_kernel(const void *a, const void
 
 // da, db elementwise and per-workgroup partials of dA_log / ddt_bias.  A workgroup owns GATE_TOK tokens x
 // all Hv heads (Hv <= NT); thread tid handles head tid % Hv for tokens slot, slot + nslot, ...
-constexpr int GATE_TOK = 256;
+constexpr int GATE_TOK = 32;
 __global__ __launch_bounds__(NT) void gates_bwd_kernel(const void *a, const void *b, const float *A_log,
                                                        const float *dt_bias, const float *g, const float *dg,
                                                        const float *dbeta, void *da, void *db, float *part,
@@ -286,12 +286,30 @@ __global__ __launch_bounds__(NT) void l2norm_bwd_any(const void *x, const void *
 
 // ------------------------------------------------------------------------------------------------ conv1d + SiLU
 
+// Causal depthwise conv over time + SiLU (engine/include/gdn.h:7-15 over a whole sequence), optionally fused
+// with the q/k/v split and the per-head L2 norm of q and k (engine/src/gdn_layer.c:29-39):
+//   c[t, ch] = silu(sum_j w[ch*K + j] x[t - (K-1) + j, ch])      ch < C = 2*qk + nv
+//   channels [0, qk) are q, [qk, 2qk) k, [2qk, C) v; with L > 0 each head of Dk = L*V q/k channels is scaled by
+//   (scale_q for q, 1 for k) / sqrt(sum c^2 + eps) and q, k, v are written to separate contiguous tensors
+//   ([.., qk], [.., qk], [.., nv] per token).  With qk = 0 this is the plain conv: v is the [B,T,C] output.
 // A workgroup is 4 wavefronts stacked in time: wavefront s covers tokens [t0 + s*CONV_TT, +CONV_TT) and every
-// lane V consecutive channels.  Each thread walks its tokens in order keeping the last K-1 inputs in
-// registers, so an input is read once (plus a K-1 token halo per CONV_TT tokens).
+// lane V consecutive channels (16-byte loads: V = 8 for 16-bit data, 4 for fp32).  Each thread walks its
+// tokens in order keeping the last K-1 inputs in registers, so an input is read once (plus a K-1 token halo per
+// CONV_TT tokens); U tokens are loaded ahead per step to keep several loads in flight per lane.  The L lanes of
+// one q/k head reduce with xor shuffles (heads align with lane groups because 64V is a multiple of Dk).
 constexpr int CONV_TT = 64;
 constexpr int CONV_SLICES = NT / 64;
-constexpr int CONV_U = 4;  // tokens loaded ahead per step
+
+struct ConvArgs {
+    const void *x;          // [B][T][C]
+    const float *w;         // [C][K]
+    const float *state_in;  // [B][K-1][C] fp32 or null (zeros)
+    void *q, *k, *v;        // forward outputs / backward cotangents: [B][T][qk], [B][T][qk], [B][T][C - 2qk]
+    void *dx;               // backward output [B][T][C]
+    float *part;            // backward dw partials [B * ntiles][C][K]
+    int T, C, qk, dt, g_dt; // g_dt: dtype of q/k/v (the cotangents' dtype in the backward)
+    float scale_q, eps;
+};
 
 // x at token t (t < 0: the carried conv state, zero when absent; t >= T: zero)
 template <int K, int V>
@@ -308,30 +326,44 @@ __device__ __forceinline__ void conv_x(const void *x, const float *state_in, int
     }
 }
 
-// out[t, c] = silu(sum_j w[c*K + j] x[t - (K-1) + j, c])   (engine/include/gdn.h:7-15 over a whole sequence)
-template <int K, int V>
-__global__ __launch_bounds__(NT) void conv_fwd_kernel(const void *x, const float *w, const float *state_in,
-                                                      void *out, int T, int C, int dt) {
+// Where channel c0 of a token lives in the split q/k/v tensors: base pointer, row length, column; region 0/1/2.
+struct SplitPos {
+    void *base;
+    int row, col, region;
+};
+__device__ __forceinline__ SplitPos split_pos(const ConvArgs &a, int c0) {
+    if (c0 < a.qk) return {a.q, a.qk, c0, 0};
+    if (c0 < 2 * a.qk) return {a.k, a.qk, c0 - a.qk, 1};
+    return {a.v, a.C - 2 * a.qk, c0 - 2 * a.qk, 2};
+}
+
+template <int K, int V, int U, int L>
+__global__ __launch_bounds__(NT) void conv_fwd_kernel(ConvArgs a) {
     const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
     const int c0 = (blockIdx.x * 64 + lane) * V;
     const int t0 = (blockIdx.y * CONV_SLICES + slice) * CONV_TT, b = blockIdx.z;
-    if (c0 >= C || t0 >= T) return;
+    const int T = a.T, C = a.C;
+    if (t0 >= T) return;  // uniform over the wavefront
+    const bool active = c0 < C;  // lanes past C only take part in the head shuffles (v region, unused)
+    const int cc = active ? c0 : 0;
+    const SplitPos sp = split_pos(a, cc);
+    const float nscale = sp.region == 0 ? a.scale_q : 1.f;
     float wk[K][V], hist[K - 1][V];
 #pragma unroll
     for (int v = 0; v < V; ++v)
 #pragma unroll
-        for (int j = 0; j < K; ++j) wk[j][v] = w[(size_t)(c0 + v) * K + j];
+        for (int j = 0; j < K; ++j) wk[j][v] = a.w[(size_t)(cc + v) * K + j];
 #pragma unroll
-    for (int j = 0; j < K - 1; ++j) conv_x<K, V>(x, state_in, b, t0 - (K - 1) + j, T, C, c0, dt, hist[j]);
+    for (int j = 0; j < K - 1; ++j) conv_x<K, V>(a.x, a.state_in, b, t0 - (K - 1) + j, T, C, cc, a.dt, hist[j]);
     const int t1 = min(T, t0 + CONV_TT);
-    for (int t = t0; t < t1; t += CONV_U) {
-        float xs[CONV_U][V];
+    for (int t = t0; t < t1; t += U) {
+        float xs[U][V];
 #pragma unroll
-        for (int u = 0; u < CONV_U; ++u) conv_x<K, V>(x, nullptr, b, t + u < t1 ? t + u : T, T, C, c0, dt, xs[u]);
+        for (int u = 0; u < U; ++u) conv_x<K, V>(a.x, nullptr, b, t + u < t1 ? t + u : T, T, C, cc, a.dt, xs[u]);
 #pragma unroll
-        for (int u = 0; u < CONV_U; ++u) {
+        for (int u = 0; u < U; ++u) {
             if (t + u >= t1) break;
-            float o[V];
+            float o[V], ss = 0.f;
 #pragma unroll
             for (int v = 0; v < V; ++v) {
                 float pre = wk[K - 1][v] * xs[u][v];
@@ -341,8 +373,17 @@ __global__ __launch_bounds__(NT) void conv_fwd_kernel(const void *x, const float
                 for (int j = 0; j + 1 < K - 1; ++j) hist[j][v] = hist[j + 1][v];
                 hist[K - 2][v] = xs[u][v];
                 o[v] = pre * sigmoidf_(pre);
+                ss = fmaf(o[v], o[v], ss);
             }
-            storev<V>(out, ((size_t)b * T + t + u) * C + c0, dt, o);
+            if constexpr (L > 0) {
+                ss = group_sum<L>(ss);
+                if (sp.region < 2) {
+                    const float inv = nscale * rsqrtf(ss + a.eps);
+#pragma unroll
+                    for (int v = 0; v < V; ++v) o[v] *= inv;
+                }
+            }
+            if (active) storev<V>(sp.base, ((size_t)b * T + t + u) * sp.row + sp.col, a.dt, o);
         }
     }
 }
@@ -363,86 +404,109 @@ __global__ void conv_state_kernel(const void *x, const float *state_in, float *s
     state_out[i] = val;
 }
 
-// silu'(p) dout with p the pre-activation from the window xs[0..K-1] = x[t-(K-1) .. t]
-template <int K, int V>
-__device__ __forceinline__ void conv_dpre(const float (&wk)[K][V], const float (*xs)[V], const float (&go)[V],
-                                          float (&dp)[V]) {
-#pragma unroll
-    for (int v = 0; v < V; ++v) {
-        float pre = 0.f;
-#pragma unroll
-        for (int j = 0; j < K; ++j) pre = fmaf(wk[j][v], xs[j][v], pre);
-        const float s = sigmoidf_(pre);
-        dp[v] = go[v] * s * (1.f + pre * (1.f - s));
-    }
-}
-
-// Backward: dpre = dout silu'(pre);  dx[t] = sum_j w[j] dpre[t + K-1-j];  dw[j] = sum_t dpre[t] x[t-(K-1)+j].
-// Same grid as the forward.  dw partials of the workgroup (its 4 time slices summed in order) go to
+// Backward, in scatter form.  For each token t (in order) the thread rebuilds pre[t] from its window of K inputs,
+// turns the cotangent of the (normalised) output into dpre[t] = dc silu'(pre), adds dpre[t] x[t-(K-1)+j] to
+// dw[j] and w[j] dpre[t] to the running dx of token t-(K-1)+j; dx of token t-(K-1) is then complete and stored.
+// The thread runs K-1 tokens past its tile so its last dx values receive their full sums (those halo tokens add
+// nothing to dw).  L2 norm backward per q/k head: dc = s/n (g - c (c.g)/n^2), n^2 = sum c^2 + eps.
+// dw partials of the workgroup (its 4 time slices summed in order) go to
 // part[(b * gridDim.y + blockIdx.y) * C*K + c*K + j].
-template <int K, int V>
-__global__ __launch_bounds__(NT) void conv_bwd_kernel(const void *x, const float *w, const float *state_in,
-                                                      const void *dout, void *dx, float *part, int T, int C, int dt,
-                                                      int dout_dt) {
+template <int K, int V, int U, int L>
+__global__ __launch_bounds__(NT) void conv_bwd_kernel(ConvArgs a) {
     __shared__ float red[CONV_SLICES][64 * V * K];
     const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
     const int c0 = (blockIdx.x * 64 + lane) * V;
     const int t0 = (blockIdx.y * CONV_SLICES + slice) * CONV_TT, b = blockIdx.z;
-    const bool active = c0 < C && t0 < T;
+    const int T = a.T, C = a.C;
+    const bool active = c0 < C;
     float dwp[K][V];
 #pragma unroll
     for (int j = 0; j < K; ++j)
 #pragma unroll
         for (int v = 0; v < V; ++v) dwp[j][v] = 0.f;
-    if (active) {
-        float wk[K][V];
+    if (t0 < T) {  // uniform over the wavefront
+        const int cc = active ? c0 : 0;
+        const SplitPos sp = split_pos(a, cc);
+        const float nscale = sp.region == 0 ? a.scale_q : 1.f;
+        float wk[K][V], xw[K][V], acc[K][V];
 #pragma unroll
         for (int v = 0; v < V; ++v)
 #pragma unroll
-            for (int j = 0; j < K; ++j) wk[j][v] = w[(size_t)(c0 + v) * K + j];
-        float xw[2 * K - 1][V];  // x[t-(K-1) .. t+K-1]
-        float dp[K][V];          // dpre[t .. t+K-1]
+            for (int j = 0; j < K; ++j) {
+                wk[j][v] = a.w[(size_t)(cc + v) * K + j];
+                acc[j][v] = 0.f;
+            }
 #pragma unroll
-        for (int j = 0; j < 2 * K - 1; ++j) conv_x<K, V>(x, state_in, b, t0 - (K - 1) + j, T, C, c0, dt, xw[j]);
+        for (int j = 0; j < K - 1; ++j) conv_x<K, V>(a.x, a.state_in, b, t0 - (K - 1) + j, T, C, cc, a.dt, xw[j]);
+        const int t1 = min(T, t0 + CONV_TT), tend = min(T, t1 + K - 1);
+        for (int t = t0; t < tend; t += U) {
+            float xn[U][V], gn[U][V];
 #pragma unroll
-        for (int m = 0; m < K; ++m) {
-            float go[V];
-            conv_x<K, V>(dout, nullptr, b, t0 + m, T, C, c0, dout_dt, go);
-            conv_dpre<K, V>(wk, xw + m, go, dp[m]);
+            for (int u = 0; u < U; ++u) {
+                const int tn = t + u < tend ? t + u : T;
+                conv_x<K, V>(a.x, nullptr, b, tn, T, C, cc, a.dt, xn[u]);
+                if (tn < T)
+                    loadv<V>(sp.base, ((size_t)b * T + tn) * sp.row + sp.col, a.g_dt, gn[u]);
+                else
+#pragma unroll
+                    for (int v = 0; v < V; ++v) gn[u][v] = 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (t + u >= tend) break;
+                float pre[V], s[V], c[V], ss = 0.f, cg = 0.f;
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+                    xw[K - 1][v] = xn[u][v];
+                    float p = 0.f;
+#pragma unroll
+                    for (int j = 0; j < K; ++j) p = fmaf(wk[j][v], xw[j][v], p);
+                    pre[v] = p;
+                    s[v] = sigmoidf_(p);
+                    c[v] = p * s[v];
+                    ss = fmaf(c[v], c[v], ss);
+                    cg = fmaf(c[v], gn[u][v], cg);
+                }
+                float dc[V];
+#pragma unroll
+                for (int v = 0; v < V; ++v) dc[v] = gn[u][v];
+                if constexpr (L > 0) {
+                    ss = group_sum<L>(ss);
+                    cg = group_sum<L>(cg);
+                    if (sp.region < 2) {
+                        const float n2 = ss + a.eps, c1 = nscale * rsqrtf(n2), c2 = c1 * cg / n2;
+#pragma unroll
+                        for (int v = 0; v < V; ++v) dc[v] = c1 * dc[v] - c2 * c[v];
+                    }
+                }
+                const bool in_tile = t + u < t1;
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+                    const float dp = dc[v] * s[v] * (1.f + pre[v] * (1.f - s[v]));
+#pragma unroll
+                    for (int j = 0; j < K; ++j) {
+                        if (in_tile) dwp[j][v] = fmaf(dp, xw[j][v], dwp[j][v]);
+                        acc[j][v] = fmaf(wk[j][v], dp, acc[j][v]);
+                    }
+                }
+                const int ts = t + u - (K - 1);  // its dx is now complete
+                if (active && ts >= t0 && ts < t1) storev<V>(a.dx, ((size_t)b * T + ts) * C + cc, a.dt, acc[0]);
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+#pragma unroll
+                    for (int j = 0; j + 1 < K; ++j) {
+                        acc[j][v] = acc[j + 1][v];
+                        xw[j][v] = xw[j + 1][v];
+                    }
+                    acc[K - 1][v] = 0.f;
+                }
+            }
         }
-        const int t1 = min(T, t0 + CONV_TT);
-        for (int t = t0; t < t1; t += CONV_U) {
-            float xn[CONV_U][V], gn[CONV_U][V];  // x and dout at t + K + u
+        // the sequence ended before the halo did: the last K-1 tokens' sums are complete (dpre past T is zero)
 #pragma unroll
-            for (int u = 0; u < CONV_U; ++u) {
-                const int tn = t + K + u < T ? t + K + u : T;
-                conv_x<K, V>(x, nullptr, b, tn, T, C, c0, dt, xn[u]);
-                conv_x<K, V>(dout, nullptr, b, tn, T, C, c0, dout_dt, gn[u]);
-            }
-#pragma unroll
-            for (int u = 0; u < CONV_U; ++u) {
-                if (t + u >= t1) break;
-                float o[V];
-#pragma unroll
-                for (int v = 0; v < V; ++v) {
-                    float s = 0.f;
-#pragma unroll
-                    for (int j = 0; j < K; ++j) s = fmaf(wk[j][v], dp[K - 1 - j][v], s);
-                    o[v] = s;
-#pragma unroll
-                    for (int j = 0; j < K; ++j) dwp[j][v] = fmaf(dp[0][v], xw[j][v], dwp[j][v]);
-                }
-                storev<V>(dx, ((size_t)b * T + t + u) * C + c0, dt, o);
-#pragma unroll
-                for (int v = 0; v < V; ++v) {
-#pragma unroll
-                    for (int j = 0; j + 1 < 2 * K - 1; ++j) xw[j][v] = xw[j + 1][v];
-                    xw[2 * K - 2][v] = xn[u][v];
-#pragma unroll
-                    for (int m = 0; m + 1 < K; ++m) dp[m][v] = dp[m + 1][v];
-                }
-                conv_dpre<K, V>(wk, xw + (K - 1), gn[u], dp[K - 1]);
-            }
+        for (int m = 0; m < K - 1; ++m) {
+            const int ts = tend - (K - 1) + m;
+            if (active && ts >= t0 && ts < t1) storev<V>(a.dx, ((size_t)b * T + ts) * C + cc, a.dt, acc[m]);
         }
     }
 #pragma unroll
@@ -457,7 +521,7 @@ __global__ __launch_bounds__(NT) void conv_bwd_kernel(const void *x, const float
         float s = 0.f;
 #pragma unroll
         for (int sl = 0; sl < CONV_SLICES; ++sl) s += red[sl][e];
-        part[prow + (size_t)cbase * K + e] = s;
+        a.part[prow + (size_t)cbase * K + e] = s;
     }
 }
 
@@ -691,68 +755,108 @@ static dim3 conv_grid(int B, int T, int C, int V) {
     return dim3(nblocks(C, 64 * V), nblocks(T, ops::CONV_SLICES * ops::CONV_TT), B);
 }
 
-template <int K>
-static void conv_fwd_k(const void *x, const float *w, const float *state_in, void *out, int B, int T, int C, int dt,
-                       bool vec, hipStream_t st) {
-    if (vec)
-        hipLaunchKernelGGL((ops::conv_fwd_kernel<K, 4>), conv_grid(B, T, C, 4), dim3(ops::NT), 0, st, x, w, state_in,
-                           out, T, C, dt);
-    else
-        hipLaunchKernelGGL((ops::conv_fwd_kernel<K, 1>), conv_grid(B, T, C, 1), dim3(ops::NT), 0, st, x, w, state_in,
-                           out, T, C, dt);
+// Channels per lane: 8 when x and q/k/v are 16-bit (16-byte loads), 4 when either is fp32 (or C % 8 != 0),
+// 1 without aligned buffers; the backward holds a K-token window per channel, so it takes at most 4.
+static int conv_lanes(int C, int dt, int g_dt, bool vec, bool bwd) {
+    if (!vec || C % 4) return 1;
+    const bool half = dt != DT_F32 && g_dt != DT_F32;
+    return (half && C % 8 == 0 && !bwd) ? 8 : 4;
 }
 
-void launch_conv_fwd(const void *x, const float *w, const float *state_in, void *out, float *state_out, int B, int T,
-                     int C, int K, int dt, bool vec, hipStream_t st) {
-    if (B && T && C) {
-        switch (K) {
-        case 2: conv_fwd_k<2>(x, w, state_in, out, B, T, C, dt, vec, st); break;
-        case 3: conv_fwd_k<3>(x, w, state_in, out, B, T, C, dt, vec, st); break;
-        case 4: conv_fwd_k<4>(x, w, state_in, out, B, T, C, dt, vec, st); break;
-        case 5: conv_fwd_k<5>(x, w, state_in, out, B, T, C, dt, vec, st); break;
-        case 6: conv_fwd_k<6>(x, w, state_in, out, B, T, C, dt, vec, st); break;
-        case 7: conv_fwd_k<7>(x, w, state_in, out, B, T, C, dt, vec, st); break;
-        case 8: conv_fwd_k<8>(x, w, state_in, out, B, T, C, dt, vec, st); break;
+template <int K, int V, int L>
+static void conv_launch(const ops::ConvArgs &a, int B, bool bwd, hipStream_t st) {
+    const dim3 grid = conv_grid(B, a.T, a.C, V);
+    if (!bwd)
+        hipLaunchKernelGGL((ops::conv_fwd_kernel<K, V, 4, L>), grid, dim3(ops::NT), 0, st, a);
+    else if constexpr (V <= 4)  // conv_lanes never gives the backward 8 channels per lane
+        hipLaunchKernelGGL((ops::conv_bwd_kernel<K, V, 2, L>), grid, dim3(ops::NT), 0, st, a);
+}
+
+template <int K>
+static void conv_plain(const ops::ConvArgs &a, int B, int V, bool bwd, hipStream_t st) {
+    if (V == 8)
+        conv_launch<K, 8, 0>(a, B, bwd, st);
+    else if (V == 4)
+        conv_launch<K, 4, 0>(a, B, bwd, st);
+    else
+        conv_launch<K, 1, 0>(a, B, bwd, st);
+}
+
+// Lanes per q/k head of the fused kernels (a power of two in [4, 64]) for V channels per lane, or 0.
+static int conv_head_lanes(int Dk, int V) {
+    if (Dk % V) return 0;
+    const int L = Dk / V;
+    return (L >= 4 && L <= 64 && (L & (L - 1)) == 0) ? L : 0;
+}
+
+bool conv_qkv_supported(int Dk, int K, int dt, int g_dt, bool vec, int C) {
+    if (K != 4) return false;
+    const int Vf = conv_lanes(C, dt, g_dt, vec, false), Vb = conv_lanes(C, dt, g_dt, vec, true);
+    return Vf > 1 && Vb > 1 && conv_head_lanes(Dk, Vf) && conv_head_lanes(Dk, Vb);
+}
+
+// Dispatch: a.qk == 0 is the plain conv (any K in [2, 8]); a.qk > 0 the fused split + L2 norm (K = 4, checked by
+// the caller with conv_qkv_supported).
+static void conv_dispatch(const ops::ConvArgs &a, int B, int K, int Dk, bool vec, bool bwd, hipStream_t st) {
+    const int V = conv_lanes(a.C, a.dt, a.g_dt, vec, bwd);
+    if (a.qk > 0) {
+        switch (conv_head_lanes(Dk, V) * 16 + V) {
+        case 4 * 16 + 4: conv_launch<4, 4, 4>(a, B, bwd, st); break;
+        case 8 * 16 + 4: conv_launch<4, 4, 8>(a, B, bwd, st); break;
+        case 16 * 16 + 4: conv_launch<4, 4, 16>(a, B, bwd, st); break;
+        case 32 * 16 + 4: conv_launch<4, 4, 32>(a, B, bwd, st); break;
+        case 64 * 16 + 4: conv_launch<4, 4, 64>(a, B, bwd, st); break;
+        case 4 * 16 + 8: conv_launch<4, 8, 4>(a, B, bwd, st); break;
+        case 8 * 16 + 8: conv_launch<4, 8, 8>(a, B, bwd, st); break;
+        case 16 * 16 + 8: conv_launch<4, 8, 16>(a, B, bwd, st); break;
+        case 32 * 16 + 8: conv_launch<4, 8, 32>(a, B, bwd, st); break;
+        case 64 * 16 + 8: conv_launch<4, 8, 64>(a, B, bwd, st); break;
         default: break;
         }
+        return;
     }
-    if (state_out && B && C)
-        hipLaunchKernelGGL(ops::conv_state_kernel, dim3(nblocks((size_t)B * (K - 1) * C, ops::NT)), dim3(ops::NT), 0,
-                           st, x, state_in, state_out, B, T, C, K, dt);
+    switch (K) {
+    case 2: conv_plain<2>(a, B, V, bwd, st); break;
+    case 3: conv_plain<3>(a, B, V, bwd, st); break;
+    case 4: conv_plain<4>(a, B, V, bwd, st); break;
+    case 5: conv_plain<5>(a, B, V, bwd, st); break;
+    case 6: conv_plain<6>(a, B, V, bwd, st); break;
+    case 7: conv_plain<7>(a, B, V, bwd, st); break;
+    case 8: conv_plain<8>(a, B, V, bwd, st); break;
+    default: break;
+    }
+}
+
+void launch_conv_fwd(const ConvCall &c, hipStream_t st) {
+    if (c.B && c.T && c.C) {
+        ops::ConvArgs a{};
+        a.x = c.x; a.w = c.w; a.state_in = c.state_in;
+        a.q = c.q; a.k = c.k; a.v = c.v;
+        a.T = c.T; a.C = c.C; a.qk = c.qk; a.dt = c.dt; a.g_dt = c.dt;
+        a.scale_q = c.scale_q; a.eps = c.eps;
+        conv_dispatch(a, c.B, c.K, c.Dk, c.vec, false, st);
+    }
+    if (c.state_out && c.B && c.C)
+        hipLaunchKernelGGL(ops::conv_state_kernel, dim3(nblocks((size_t)c.B * (c.K - 1) * c.C, ops::NT)),
+                           dim3(ops::NT), 0, st, c.x, c.state_in, c.state_out, c.B, c.T, c.C, c.K, c.dt);
 }
 
 size_t conv_bwd_work_floats(int B, int T, int C, int K) {
     return (size_t)B * nblocks(T, ops::CONV_SLICES * ops::CONV_TT) * C * K;
 }
 
-template <int K>
-static void conv_bwd_k(const void *x, const float *w, const float *state_in, const void *dout, void *dx, float *work,
-                       int B, int T, int C, int dt, int dout_dt, bool vec, hipStream_t st) {
-    if (vec)
-        hipLaunchKernelGGL((ops::conv_bwd_kernel<K, 4>), conv_grid(B, T, C, 4), dim3(ops::NT), 0, st, x, w, state_in,
-                           dout, dx, work, T, C, dt, dout_dt);
-    else
-        hipLaunchKernelGGL((ops::conv_bwd_kernel<K, 1>), conv_grid(B, T, C, 1), dim3(ops::NT), 0, st, x, w, state_in,
-                           dout, dx, work, T, C, dt, dout_dt);
-}
-
-void launch_conv_bwd(const void *x, const float *w, const float *state_in, const void *dout, void *dx, float *dw,
-                     float *work, int B, int T, int C, int K, int dt, int dout_dt, bool vec, hipStream_t st) {
-    if (!C) return;
-    const int nparts = (B && T) ? (int)(B * nblocks(T, ops::CONV_SLICES * ops::CONV_TT)) : 0;
+void launch_conv_bwd(const ConvCall &c, hipStream_t st) {
+    if (!c.C) return;
+    const int nparts = (c.B && c.T) ? (int)(c.B * nblocks(c.T, ops::CONV_SLICES * ops::CONV_TT)) : 0;
     if (nparts) {
-        switch (K) {
-        case 2: conv_bwd_k<2>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
-        case 3: conv_bwd_k<3>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
-        case 4: conv_bwd_k<4>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
-        case 5: conv_bwd_k<5>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
-        case 6: conv_bwd_k<6>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
-        case 7: conv_bwd_k<7>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
-        case 8: conv_bwd_k<8>(x, w, state_in, dout, dx, work, B, T, C, dt, dout_dt, vec, st); break;
-        default: return;
-        }
+        ops::ConvArgs a{};
+        a.x = c.x; a.w = c.w; a.state_in = c.state_in;
+        a.q = c.q; a.k = c.k; a.v = c.v; a.dx = c.dx; a.part = c.work;
+        a.T = c.T; a.C = c.C; a.qk = c.qk; a.dt = c.dt; a.g_dt = c.g_dt;
+        a.scale_q = c.scale_q; a.eps = c.eps;
+        conv_dispatch(a, c.B, c.K, c.Dk, c.vec, true, st);
     }
-    launch_colsum(work, nparts, C * K, dw, dw, C * K, st);  // with no tokens: dw = 0
+    launch_colsum(c.work, nparts, c.C * c.K, c.dw, c.dw, c.C * c.K, st);  // with no tokens: dw = 0
 }
 
 int grms_dmax() { return ops::GRMS_DMAX; }

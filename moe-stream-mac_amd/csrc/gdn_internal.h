@@ -82,10 +82,23 @@ void launch_l2norm_fwd(const void *x, void *y, size_t rows, int D, float eps, fl
                        hipStream_t st);
 void launch_l2norm_bwd(const void *x, const void *dy, void *dx, size_t rows, int D, float eps, float scale, int dt,
                        int dy_dt, bool vec, hipStream_t st);
-void launch_conv_fwd(const void *x, const float *w, const float *state_in, void *out, float *state_out, int B, int T,
-                     int C, int K, int dt, bool vec, hipStream_t st);
-void launch_conv_bwd(const void *x, const float *w, const float *state_in, const void *dout, void *dx, float *dw,
-                     float *work, int B, int T, int C, int K, int dt, int dout_dt, bool vec, hipStream_t st);
+// Conv + SiLU over [B][T][C]; with qk > 0 fused with the q/k/v split ([0,qk) q, [qk,2qk) k, rest v) and the
+// per-head L2 norm of q (times scale_q) and k.  Forward: q/k/v are outputs (qk = 0: v is the [B][T][C] output).
+// Backward: q/k/v are the cotangents (dtype g_dt), dx/dw the results, work the dw partials.
+struct ConvCall {
+    const void *x;
+    const float *w, *state_in;
+    void *q, *k, *v;
+    float *state_out;
+    void *dx;
+    float *dw, *work;
+    int B, T, C, K, qk, Dk, dt, g_dt;
+    float scale_q, eps;
+    bool vec;
+};
+bool conv_qkv_supported(int Dk, int K, int dt, int g_dt, bool vec, int C);
+void launch_conv_fwd(const ConvCall &c, hipStream_t st);
+void launch_conv_bwd(const ConvCall &c, hipStream_t st);
 void launch_grms_fwd(const void *y, const void *z, const float *w, void *out, size_t rows, int D, float eps, int dt,
                      int z_dt, bool vec, hipStream_t st);
 void launch_grms_bwd(const void *y, const void *z, const float *w, const void *dout, void *dy, void *dz, float *dw,

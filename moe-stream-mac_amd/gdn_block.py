@@ -194,6 +194,80 @@ def conv_silu(x: Array, w: Array, state: Optional[Array] = None, *, return_state
     return (out, s) if return_state else out
 
 
+def _aligned16(t: Array) -> Array:
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+class _ConvQKV(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, state_in, heads, q_scale, eps, want_state):
+        Hk, Dk, Hv, Dv = heads
+        dev = _require_cuda(x, w, state_in)
+        if x.dim() != 3 or x.shape[-1] != 2 * Hk * Dk + Hv * Dv:
+            raise ValueError(f"conv input must be [B, T, 2*Hk*Dk + Hv*Dv]; got {tuple(x.shape)}")
+        B, T, C = x.shape
+        w32, K = _conv_weight(w, C)
+        x = _aligned16(x)
+        s_in = None if state_in is None else state_in.float().contiguous()
+        if s_in is not None and s_in.shape != (B, K - 1, C):
+            raise ValueError(f"conv state must be [B, K-1, C] = {(B, K - 1, C)}; got {tuple(s_in.shape)}")
+        q = torch.empty((B, T, Hk, Dk), dtype=x.dtype, device=dev)
+        k = torch.empty((B, T, Hk, Dk), dtype=x.dtype, device=dev)
+        v = torch.empty((B, T, Hv, Dv), dtype=x.dtype, device=dev)
+        s_out = torch.empty((B, K - 1, C), dtype=torch.float32, device=dev) if want_state else None
+        L.check(L.load().gdn_conv_qkv_fwd(L.ptr(x), L.ptr(w32), L.ptr(s_in), L.ptr(q), L.ptr(k), L.ptr(v),
+                                          L.ptr(s_out), B, T, Hk, Dk, Hv, Dv, K, float(q_scale), float(eps),
+                                          _code(x), L.stream_handle(dev)))
+        ctx.save_for_backward(x, w32, s_in)
+        ctx.meta = (heads, float(q_scale), float(eps), w.shape, w.dtype)
+        if s_out is not None:
+            ctx.mark_non_differentiable(s_out)
+        return q, k, v, s_out
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv, _ds):
+        x, w32, s_in = ctx.saved_tensors
+        (Hk, Dk, Hv, Dv), q_scale, eps, w_shape, w_dtype = ctx.meta
+        B, T, C = x.shape
+        K = w32.shape[1]
+        dev = x.device
+        gd = next((g.dtype for g in (dq, dk, dv) if g is not None), x.dtype)
+        fill = lambda g, shape: (torch.zeros(shape, dtype=gd, device=dev) if g is None else _aligned16(g.to(gd)))
+        dq, dk = fill(dq, (B, T, Hk, Dk)), fill(dk, (B, T, Hk, Dk))
+        dv = fill(dv, (B, T, Hv, Dv))
+        dx = torch.empty_like(x)
+        dw = torch.empty((C, K), dtype=torch.float32, device=dev)
+        lib = L.load()
+        nws = lib.gdn_conv_silu_bwd_workspace_bytes(B, T, C, K)
+        ws = _workspace(nws, dev)
+        L.check(lib.gdn_conv_qkv_bwd(L.ptr(x), L.ptr(w32), L.ptr(s_in), L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(dx),
+                                     L.ptr(dw), L.ptr(ws), nws, B, T, Hk, Dk, Hv, Dv, K, q_scale, eps, _code(x),
+                                     _code(dq), L.stream_handle(dev)))
+        return dx, dw.reshape(w_shape).to(w_dtype), None, None, None, None, None
+
+
+def conv_qkv(x: Array, w: Array, Hk: int, Dk: int, Hv: int, Dv: int, q_scale: float, eps: float = 1e-6,
+             state: Optional[Array] = None, *, return_state: bool = False):
+    """Steps 2-4 of one block (engine/src/gdn_layer.c:29-39) on x [B, T, 2*Hk*Dk + Hv*Dv]: causal depthwise conv
+    + SiLU, split into q, k [B, T, Hk, Dk] and v [B, T, Hv, Dv], q and k L2-normalised per head (q scaled by
+    q_scale).  One fused kernel pair where the shape allows (K = 4, 16-byte vector lanes per head), else the
+    separate conv and L2-norm kernels.  ``state``/``return_state`` as in ``conv_silu``."""
+    try:
+        q, k, v, s = _ConvQKV.apply(x, w, state, (Hk, Dk, Hv, Dv), q_scale, eps, return_state)
+    except L.GDNError as e:
+        if e.status != L.GDN_ERR_UNSUPPORTED:
+            raise
+        out, s = _ConvSiLU.apply(x, w, state, return_state)
+        B, T, _ = x.shape
+        kd = Hk * Dk
+        q = out[..., :kd].reshape(B, T, Hk, Dk)
+        k = out[..., kd:2 * kd].reshape(B, T, Hk, Dk)
+        v = out[..., 2 * kd:].reshape(B, T, Hv, Dv)
+        q, k = normalize_qk(q, k, q_scale, eps)
+    return (q, k, v, s) if return_state else (q, k, v)
+
+
 # ------------------------------------------------------------------------------------------------ gated RMSNorm
 
 

@@ -39,6 +39,8 @@ _SIGS = {
     "gdn_conv_silu_fwd": ([_vp] * 5 + [_i] * 5 + [_vp], _i),
     "gdn_conv_silu_bwd_workspace_bytes": ([_i] * 4, _sz),
     "gdn_conv_silu_bwd": ([_vp] * 7 + [_sz] + [_i] * 6 + [_vp], _i),
+    "gdn_conv_qkv_fwd": ([_vp] * 7 + [_i] * 7 + [_f, _f, _i, _vp], _i),
+    "gdn_conv_qkv_bwd": ([_vp] * 9 + [_sz] + [_i] * 7 + [_f, _f, _i, _i, _vp], _i),
     "gdn_gated_rmsnorm_fwd": ([_vp] * 4 + [_i64, _i, _f, _i, _i, _vp], _i),
     "gdn_gated_rmsnorm_bwd_workspace_bytes": ([_i64, _i], _sz),
     "gdn_gated_rmsnorm_bwd": ([_vp] * 8 + [_sz, _i64, _i, _f, _i, _i, _i, _vp], _i),

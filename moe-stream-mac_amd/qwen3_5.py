@@ -91,12 +91,9 @@ class GatedDeltaNet(nn.Module):
         a = self.in_proj_a(x)
         if mask is not None:
             qkv = qkv * mask[..., None].to(qkv.dtype)
-        conv = gdn_block.conv_silu(qkv, self.conv1d.weight)
-        q, k, v = torch.split(conv, [self.key_dim, self.key_dim, self.value_dim], dim=-1)
-        q = q.reshape(B, T, self.Hk, self.Dk)
-        k = k.reshape(B, T, self.Hk, self.Dk)
-        v = v.reshape(B, T, self.Hv, self.Dv)
-        q, k = normalize_qk(q, k, self.Dk ** -0.5, 1e-6)
+        # conv + SiLU, split, per-head q/k L2 norm (q scaled by Dk^-1/2): one fused kernel pair
+        q, k, v = gdn_block.conv_qkv(qkv, self.conv1d.weight, self.Hk, self.Dk, self.Hv, self.Dv,
+                                     self.Dk ** -0.5, 1e-6)
         update = globals()["gated_delta_update"]
         out, _ = update(q, k, v, a, b, self.A_log, self.dt_bias, state, mask, use_kernel=not self.training)
         out = self.norm(out.to(z.dtype), z)
@@ -203,8 +200,11 @@ class LoRALinear(nn.Module):
         return self.base.weight
 
     def forward(self, x: Array) -> Array:
-        return self.base(x) + self.scale * F.linear(F.linear(x, self.lora_a.to(x.dtype)),
-                                                    self.lora_b.to(x.dtype))
+        # base GEMM, then the adapter GEMM accumulating into it with alpha = scale: no separate scale or add pass
+        # over the [tokens, out] output, forward or backward
+        u = F.linear(x, self.lora_a.to(x.dtype)).flatten(0, -2)
+        y = torch.addmm(self.base(x).flatten(0, -2), u, self.lora_b.to(x.dtype).t(), alpha=self.scale)
+        return y.view(*x.shape[:-1], y.shape[-1])
 
 
 def freeze(module: nn.Module) -> None:

@@ -302,3 +302,92 @@ def test_block_op_errors(dev):
                         torch.zeros(257, device=dev), torch.zeros(257, device=dev))
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         gdn_block.l2norm(torch.zeros(4, 8))
+
+
+# ------------------------------------------------------------------------------------------------ fused conv + split + L2 norm
+
+
+def _conv_qkv_oracle(x, w, Hk, Dk, Hv, Dv, scale, dq, dk, dv, state=None):
+    """Composition of the oracle's conv, split and L2 norm (forward) and their backwards."""
+    B, T, C = x.shape
+    K = w.shape[1]
+    xx = x if state is None else np.concatenate([state, x], 1)
+    c, _ = O.conv_silu(xx, w)
+    c = c[:, -T:]
+    kd = Hk * Dk
+    q, k, v = c[..., :kd].reshape(B, T, Hk, Dk), c[..., kd:2 * kd].reshape(B, T, Hk, Dk), c[..., 2 * kd:]
+    outs = (O.l2norm(q, 1e-6, scale), O.l2norm(k, 1e-6, 1.0), v.reshape(B, T, Hv, Dv))
+    dc = np.concatenate([O.l2norm_bwd(q, dq, 1e-6, scale).reshape(B, T, -1),
+                         O.l2norm_bwd(k, dk, 1e-6, 1.0).reshape(B, T, -1), dv.reshape(B, T, -1)], -1)
+    if state is not None:
+        dc = np.concatenate([np.zeros((B, K - 1, C)), dc], 1)
+    dxx, dw = O.conv_silu_bwd(xx, w, dc)
+    return outs, dxx[:, -T:], dw
+
+
+@pytest.mark.parametrize("Hk,Dk,Hv,Dv,T", [(2, 128, 4, 128, 150), (16, 128, 32, 128, 70), (3, 64, 6, 32, 65),
+                                           (2, 256, 4, 64, 40), (2, 32, 2, 48, 33)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_conv_qkv_fused(dev, Hk, Dk, Hv, Dv, T, dtype):
+    import gdn_block
+    B, K = 2, 4
+    C = 2 * Hk * Dk + Hv * Dv
+    r = rng(Hk * Dk + T)
+    x = r.standard_normal((B, T, C))
+    if dtype == torch.bfloat16:
+        x = torch.tensor(x).bfloat16().double().numpy()
+    w = r.standard_normal((C, K)) * 0.5
+    dq, dk = r.standard_normal((B, T, Hk, Dk)), r.standard_normal((B, T, Hk, Dk))
+    dv = r.standard_normal((B, T, Hv, Dv))
+    scale = Dk ** -0.5
+    print(f"conv_qkv Hk={Hk} Dk={Dk} Hv={Hv} Dv={Dv} T={T} {dtype}", flush=True)
+    tx, tw = T_(x, dev, dtype, True), T_(w, dev, grad=True)
+    q, k, v = gdn_block.conv_qkv(tx, tw, Hk, Dk, Hv, Dv, scale)
+    gq, gk, gv = (T_(a, dev, dtype) for a in (dq, dk, dv))
+    dx, dw = torch.autograd.grad([q, k, v], [tx, tw], [gq, gk, gv])
+    torch.cuda.synchronize()
+    rq = lambda t: np_(t).astype(np.float64)
+    outs, want_dx, want_dw = _conv_qkv_oracle(x, w, Hk, Dk, Hv, Dv, scale, rq(gq), rq(gk), rq(gv))
+    tol_f, tol_b = (1e-5, 1e-4) if dtype == torch.float32 else (1e-2, 1e-2)
+    for name, got, want in zip("qkv", (q, k, v), outs):
+        assert got.is_contiguous()
+        assert nerr(np_(got), want) <= tol_f, (name, nerr(np_(got), want))
+    assert nerr(np_(dx), want_dx) <= tol_b, nerr(np_(dx), want_dx)
+    assert nerr(np_(dw), want_dw) <= tol_b, nerr(np_(dw), want_dw)
+
+
+def test_conv_qkv_state_and_fallback(dev):
+    """Carried conv state through the fused kernels, and the composed path (K = 3, unaligned input) giving the
+    same results as the oracle."""
+    import gdn_block
+    B, T, Hk, Dk, Hv, Dv, K = 1, 90, 2, 128, 4, 128, 4
+    C = 2 * Hk * Dk + Hv * Dv
+    r = rng(77)
+    x, w = r.standard_normal((B, T, C)), r.standard_normal((C, K)) * 0.5
+    st = r.standard_normal((B, K - 1, C))
+    dq, dk = r.standard_normal((B, T, Hk, Dk)), r.standard_normal((B, T, Hk, Dk))
+    dv = r.standard_normal((B, T, Hv, Dv))
+    tx, tw = T_(x, dev, grad=True), T_(w, dev, grad=True)
+    q, k, v, s_out = gdn_block.conv_qkv(tx, tw, Hk, Dk, Hv, Dv, 0.1, state=T_(st, dev), return_state=True)
+    dx, dw = torch.autograd.grad([q, k, v], [tx, tw], [T_(a, dev) for a in (dq, dk, dv)])
+    outs, want_dx, want_dw = _conv_qkv_oracle(x, w, Hk, Dk, Hv, Dv, 0.1, dq, dk, dv, state=st)
+    for got, want in zip((q, k, v), outs):
+        assert nerr(np_(got), want) <= 1e-5
+    assert nerr(np_(dx), want_dx) <= 1e-4 and nerr(np_(dw), want_dw) <= 1e-4
+    assert np.array_equal(np_(s_out), x[:, T - K + 1:].astype(np.float32))
+    # K = 3 is not fused: the composed kernels run instead
+    w3 = r.standard_normal((C, 3)) * 0.5
+    tw3 = T_(w3, dev, grad=True)
+    q, k, v = gdn_block.conv_qkv(tx, tw3, Hk, Dk, Hv, Dv, 0.1)
+    dx, dw = torch.autograd.grad([q, k, v], [tx, tw3], [T_(a, dev) for a in (dq, dk, dv)])
+    outs, want_dx, want_dw = _conv_qkv_oracle(x, w3, Hk, Dk, Hv, Dv, 0.1, dq, dk, dv)
+    for got, want in zip((q, k, v), outs):
+        assert nerr(np_(got), want) <= 1e-5
+    assert nerr(np_(dx), want_dx) <= 1e-4 and nerr(np_(dw), want_dw) <= 1e-4
+    # an input at a 4-byte offset is copied to an aligned buffer and still takes the fused path
+    base = T_(np.concatenate([[0.0], x.ravel()]), dev)
+    xo = base[1:].view(B, T, C)
+    q2, k2, v2 = gdn_block.conv_qkv(xo, tw, Hk, Dk, Hv, Dv, 0.1)
+    outs, _, _ = _conv_qkv_oracle(x, w, Hk, Dk, Hv, Dv, 0.1, dq, dk, dv)
+    for got, want in zip((q2, k2, v2), outs):
+        assert nerr(np_(got), want) <= 1e-5
