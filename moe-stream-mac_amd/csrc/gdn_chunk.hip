@@ -254,15 +254,16 @@ __device__ __forceinline__ const void *elem_ptr(const void *p, size_t idx, int d
     return static_cast<const char *>(p) + idx * (dt == DT_F32 ? 4 : 2);
 }
 
-// Write the [D][D] state slab [i0, i0+VS) x [0, D) from its LDS copy sH ([j][ii], stride LV) to global in the
-// reference layout S[i][j], one contiguous row of S per pass (coalesced along j).
+// Write the value slab [i0, i0+VS) of a [D][D] chunk state from its LDS copy sH ([j][ii], stride LV) to global
+// as h = S^T, element (j, i) at dst[j * D + i]: the layout the backward reads as MFMA operands (rows j, the
+// reduction index i contiguous).  Stores are coalesced along i.
 template <int VS, int LV, int NTH>
 __device__ __forceinline__ void store_state_slice(float *dst, const float *sH, int i0) {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int p = 0; p < VS * D / NTH; ++p) {
-        const int v = tid + p * NTH, ii = v / D, j = v - ii * D;
-        dst[(size_t)(i0 + ii) * D + j] = sH[j * LV + ii];
+        const int v = tid + p * NTH, j = v / VS, ii = v - j * VS;
+        dst[(size_t)j * D + i0 + ii] = sH[j * LV + ii];
     }
 }
 
@@ -275,14 +276,14 @@ __device__ __forceinline__ float gate_log(float g, int gate) {
 }
 
 struct Bufs {
-    float *H;    // [B][Hv][NC][D][D] chunk-entry states, reference layout S[i][j]
+    float *H;    // [B][Hv][NC][D][D] chunk-entry states h = S^T, element (j, i) at [j][i]
     double *G;   // [B][Hv][NC][C]
     float *T;    // [B][Hv][NC][C][C]
     float *P;    // [B][Hv][NC][C][C]
     float *W;    // [B][Hv][NC][C][D]
     float *U;    // [B][Hv][NC][C][D]
     float *Dl;   // [B][Hv][NC][C][D]  Delta
-    float *dH;   // [B][Hv][NC][D][D]  adjoint of each chunk's exit state
+    float *dH;   // [B][Hv][NC][D][D]  adjoint of each chunk's exit state, [j][i] like H
     float *dDl;  // [B][Hv][NC][C][D]  dDelta
     float *part; // [B][T][Hv][2][D]   dq | dk per value head
 };
@@ -707,7 +708,7 @@ constexpr int NTB = 512;  // ck_bwd_local: 8 waves; waves w and w+4 share the 16
 
 template <int MT>
 __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
-    __shared__ __align__(16) float R1[D * LD];       // h / dh' ([i][j]); then K at R1, Q / dW at R1 + C*LD
+    __shared__ __align__(16) float R1[D * LD];       // h / dh' ([j][i]); then K at R1, Q / dW at R1 + C*LD
     __shared__ __align__(16) float R2[C * LD];       // dY, then dDelta, then the pair matrix E
     __shared__ __align__(16) float RX[2 * C * LDC];  // V ([C][LD] fits), then R3 = RX (Y1), R4 = RX + C*LDC
     __shared__ __align__(16) float R5[C * LDC];      // T
@@ -776,8 +777,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
         f4 dw[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) dQ[t] = dw[t] = zero4();
-        mma_strip<MT, D, 4>(dQ, R2 + r0 * LD, LD, 1, R1 + 64 * ch, LD, 1, 16);
-        mma_strip<MT, D, 4>(dw, dDc + r0 * D, D, 1, R1 + 64 * ch, LD, 1, 16);
+        mma_strip<MT, D, 4>(dQ, R2 + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<MT, D, 4>(dw, dDc + r0 * D, D, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -793,7 +794,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < 4; ++t) dK[t] = zero4();
-    mma_strip<MT, D, 4, true, true>(dK, Dc + r0 * D, D, 1, R1 + 64 * ch, LD, 1, 16);
+    mma_strip<MT, D, 4, true, true>(dK, Dc + r0 * D, D, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -981,6 +982,540 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
         }
 }
 
+// ---------------------------------------------------------------------------------------------- bf16 tiles
+//
+// Operand tiles of v_mfma_f32_16x16x32_bf16 kept in LDS as bf16 with the reduction index k contiguous:
+// element (m, k) at t[m * ld + k], ld = K + 8.  A lane's fragment (8 consecutive k of row m0 + l%16, starting
+// at k0 + 8*(l/16)) is one 16-byte LDS read; the 16-byte row pad puts the 16 rows of a read in distinct bank
+// groups.  A computed fp32 operand whose rounding reaches the outputs is kept as two tiles hi = bf16(x) and
+// lo = bf16(x - hi) (the split of mma16 above), converted once when the tile is staged instead of at every use.
+typedef unsigned short bfr;  // raw bf16 bits
+constexpr int LA = D + 8;    // row stride of [*][128] tiles
+constexpr int LB = C + 8;    // row stride of [*][64] tiles
+
+__device__ __forceinline__ uint32_t bfbits(float x) { return __builtin_bit_cast(unsigned short, (__bf16)x); }
+__device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ uint32_t pk(float a, float b) { return bfbits(a) | (bfbits(b) << 16); }
+// hi / lo halves of a pair
+__device__ __forceinline__ void pk2(float a, float b, uint32_t &h, uint32_t &lo) {
+    const uint32_t ha = bfbits(a), hb = bfbits(b);
+    h = ha | (hb << 16);
+    lo = bfbits(a - bf2f(ha)) | (bfbits(b - bf2f(hb)) << 16);
+}
+
+__device__ __forceinline__ bf8 frag(const bfr *t, int ld, int m0, int k0) {
+    const int l = threadIdx.x & 63;
+    return *reinterpret_cast<const bf8 *>(t + (m0 + (l & 15)) * ld + k0 + 8 * (l >> 4));
+}
+
+// acc[t] += A(16 x K, rows m0.. of tile a) * B_t, B_t(k, n) = b[(n0 + 16 t + n) * ldb + k].  SA / SB add the lo
+// parts of a split operand.
+template <int K, int NTL, bool SA = false, bool SB = false>
+__device__ __forceinline__ void mmab(f4 (&acc)[NTL], const bfr *ah, const bfr *al, int lda, int m0, const bfr *bh,
+                                     const bfr *bl, int ldb, int n0) {
+#pragma unroll 2
+    for (int k0 = 0; k0 < K; k0 += 32) {
+        const bf8 x = frag(ah, lda, m0, k0);
+        bf8 x2;
+        if constexpr (SA) x2 = frag(al, lda, m0, k0);
+#pragma unroll
+        for (int t = 0; t < NTL; ++t) {
+            const bf8 y = frag(bh, ldb, n0 + 16 * t, k0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, acc[t], 0, 0, 0);
+            if constexpr (SA) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x2, y, acc[t], 0, 0, 0);
+            if constexpr (SB) {
+                const bf8 y2 = frag(bl, ldb, n0 + 16 * t, k0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y2, acc[t], 0, 0, 0);
+            }
+        }
+    }
+}
+
+// Global [ROWS][COLS] (row stride `stride` elements, rows >= n read as zero; fp32 when F32 else bf16) ->
+// LDS tile dst[r][c] (row stride ldd).  All of a thread's loads are issued before its LDS stores.
+template <int ROWS, int COLS, int NTH, bool F32, bool SPLIT>
+__device__ __forceinline__ void stage_N(bfr *hi, bfr *lo, int ldd, const void *src, size_t stride, int n) {
+    constexpr int CPR = COLS / 8, NCH = ROWS * CPR, PER = (NCH + NTH - 1) / NTH;
+    const int tid = threadIdx.x;
+    uint4 raw[F32 ? 2 * PER : PER];
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int ch = tid + p * NTH, r = ch / CPR, c = (ch - r * CPR) * 8;
+        const bool ok = ch < NCH && r < n;
+        if constexpr (F32) {
+            const float *s = static_cast<const float *>(src) + r * stride + c;
+            raw[2 * p] = ok ? *reinterpret_cast<const uint4 *>(s) : make_uint4(0, 0, 0, 0);
+            raw[2 * p + 1] = ok ? *reinterpret_cast<const uint4 *>(s + 4) : make_uint4(0, 0, 0, 0);
+        } else {
+            raw[p] = ok ? *reinterpret_cast<const uint4 *>(static_cast<const bfr *>(src) + r * stride + c)
+                        : make_uint4(0, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int ch = tid + p * NTH, r = ch / CPR, c = (ch - r * CPR) * 8;
+        if (ch >= NCH) break;
+        if constexpr (F32) {
+            const uint4 a = raw[2 * p], b = raw[2 * p + 1];
+            uint4 h, l;
+            pk2(__uint_as_float(a.x), __uint_as_float(a.y), h.x, l.x);
+            pk2(__uint_as_float(a.z), __uint_as_float(a.w), h.y, l.y);
+            pk2(__uint_as_float(b.x), __uint_as_float(b.y), h.z, l.z);
+            pk2(__uint_as_float(b.z), __uint_as_float(b.w), h.w, l.w);
+            *reinterpret_cast<uint4 *>(hi + r * ldd + c) = h;
+            if constexpr (SPLIT) *reinterpret_cast<uint4 *>(lo + r * ldd + c) = l;
+        } else {
+            *reinterpret_cast<uint4 *>(hi + r * ldd + c) = raw[p];
+        }
+    }
+}
+
+// Global [ROWS][COLS] -> transposed LDS tile dst[c][r] (row stride ldd).  A thread moves an 8-row x 4-column
+// block: 8 row loads, then 4 stores of 8 consecutive r.
+template <int ROWS, int COLS, int NTH, bool F32, bool SPLIT>
+__device__ __forceinline__ void stage_T(bfr *hi, bfr *lo, int ldd, const void *src, size_t stride, int n) {
+    constexpr int CB = COLS / 4, NB = (ROWS / 8) * CB, PER = (NB + NTH - 1) / NTH;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int blk = tid + p * NTH;
+        if (blk >= NB) break;
+        const int rb = blk / CB, c0 = (blk - rb * CB) * 4;
+        float v[8][4];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+            const int r = rb * 8 + rr;
+            if constexpr (F32) {
+                const float4 x = r < n ? *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + r * stride + c0)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+                v[rr][0] = x.x; v[rr][1] = x.y; v[rr][2] = x.z; v[rr][3] = x.w;
+            } else {
+                const uint2 x = r < n ? *reinterpret_cast<const uint2 *>(static_cast<const bfr *>(src) + r * stride + c0)
+                                      : make_uint2(0, 0);
+                v[rr][0] = bf2f(x.x & 0xffffu); v[rr][1] = bf2f(x.x >> 16);
+                v[rr][2] = bf2f(x.y & 0xffffu); v[rr][3] = bf2f(x.y >> 16);
+            }
+        }
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            uint4 h, l;
+            pk2(v[0][cc], v[1][cc], h.x, l.x);
+            pk2(v[2][cc], v[3][cc], h.y, l.y);
+            pk2(v[4][cc], v[5][cc], h.z, l.z);
+            pk2(v[6][cc], v[7][cc], h.w, l.w);
+            *reinterpret_cast<uint4 *>(hi + (c0 + cc) * ldd + rb * 8) = h;
+            if constexpr (SPLIT) *reinterpret_cast<uint4 *>(lo + (c0 + cc) * ldd + rb * 8) = l;
+        }
+    }
+}
+
+// Global [ROWS][COLS] -> natural tile N[r][c] (ldn, hi only) and transposed tile Tt[c][r] (ldt) from one load
+// of each element (8-row x 4-column blocks per thread).
+template <int ROWS, int COLS, int NTH, bool F32, bool SPLIT_T>
+__device__ __forceinline__ void stage_NT(bfr *nh, int ldn, bfr *th, bfr *tl, int ldt, const void *src, size_t stride,
+                                         int n) {
+    constexpr int CB = COLS / 4, NB = (ROWS / 8) * CB, PER = (NB + NTH - 1) / NTH;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int blk = tid + p * NTH;
+        if (blk >= NB) break;
+        const int rb = blk / CB, c0 = (blk - rb * CB) * 4;
+        float v[8][4];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+            const int r = rb * 8 + rr;
+            if constexpr (F32) {
+                const float4 x = r < n ? *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + r * stride + c0)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+                v[rr][0] = x.x; v[rr][1] = x.y; v[rr][2] = x.z; v[rr][3] = x.w;
+            } else {
+                const uint2 x = r < n ? *reinterpret_cast<const uint2 *>(static_cast<const bfr *>(src) + r * stride + c0)
+                                      : make_uint2(0, 0);
+                v[rr][0] = bf2f(x.x & 0xffffu); v[rr][1] = bf2f(x.x >> 16);
+                v[rr][2] = bf2f(x.y & 0xffffu); v[rr][3] = bf2f(x.y >> 16);
+            }
+        }
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr)
+            *reinterpret_cast<uint2 *>(nh + (rb * 8 + rr) * ldn + c0) = make_uint2(pk(v[rr][0], v[rr][1]), pk(v[rr][2], v[rr][3]));
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            uint4 h, l;
+            pk2(v[0][cc], v[1][cc], h.x, l.x);
+            pk2(v[2][cc], v[3][cc], h.y, l.y);
+            pk2(v[4][cc], v[5][cc], h.z, l.z);
+            pk2(v[6][cc], v[7][cc], h.w, l.w);
+            *reinterpret_cast<uint4 *>(th + (c0 + cc) * ldt + rb * 8) = h;
+            if constexpr (SPLIT_T) *reinterpret_cast<uint4 *>(tl + (c0 + cc) * ldt + rb * 8) = l;
+        }
+    }
+}
+
+// The two [D][D] fp32 chunk states h and dh' ([j][i]) -> tiles h (hi) and dh' (hi / lo), returning this thread's
+// part of the fp32 inner product <dh', h>.
+template <int NTH>
+__device__ __forceinline__ float stage_states(bfr *hh, bfr *dhh, bfr *dhl, const float *H, const float *dH) {
+    constexpr int CPR = D / 8, NCH = D * CPR, PER = NCH / NTH;
+    static_assert(PER * NTH == NCH, "even split");
+    const int tid = threadIdx.x;
+    float dot = 0.f;
+#pragma unroll
+    for (int p0 = 0; p0 < PER; p0 += 2) {
+        float4 hv[2][2], dv[2][2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int ch = tid + (p0 + p) * NTH;
+            hv[p][0] = reinterpret_cast<const float4 *>(H)[2 * ch];
+            hv[p][1] = reinterpret_cast<const float4 *>(H)[2 * ch + 1];
+            dv[p][0] = reinterpret_cast<const float4 *>(dH)[2 * ch];
+            dv[p][1] = reinterpret_cast<const float4 *>(dH)[2 * ch + 1];
+        }
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int ch = tid + (p0 + p) * NTH, r = ch / CPR, c = (ch - r * CPR) * 8;
+            uint4 h, dh, dl;
+            h = make_uint4(pk(hv[p][0].x, hv[p][0].y), pk(hv[p][0].z, hv[p][0].w), pk(hv[p][1].x, hv[p][1].y),
+                           pk(hv[p][1].z, hv[p][1].w));
+            pk2(dv[p][0].x, dv[p][0].y, dh.x, dl.x);
+            pk2(dv[p][0].z, dv[p][0].w, dh.y, dl.y);
+            pk2(dv[p][1].x, dv[p][1].y, dh.z, dl.z);
+            pk2(dv[p][1].z, dv[p][1].w, dh.w, dl.w);
+            *reinterpret_cast<uint4 *>(hh + r * LA + c) = h;
+            *reinterpret_cast<uint4 *>(dhh + r * LA + c) = dh;
+            *reinterpret_cast<uint4 *>(dhl + r * LA + c) = dl;
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                dot += hv[p][q].x * dv[p][q].x + hv[p][q].y * dv[p][q].y + hv[p][q].z * dv[p][q].z +
+                       hv[p][q].w * dv[p][q].w;
+        }
+    }
+    return dot;
+}
+
+// MFMA accumulator tile X (rows m0 + 4(l/16) + e, column n0 + l%16) -> LDS, transposed (dst[n][m]: four
+// consecutive bf16 per lane) or natural (dst[m][n]).
+template <bool SPLIT>
+__device__ __forceinline__ void acc_T(const f4 &x, bfr *hi, bfr *lo, int ld, int m0, int n0) {
+    const int l = threadIdx.x & 63;
+    const int o = (n0 + (l & 15)) * ld + m0 + 4 * (l >> 4);
+    uint2 h, lw;
+    pk2(x[0], x[1], h.x, lw.x);
+    pk2(x[2], x[3], h.y, lw.y);
+    *reinterpret_cast<uint2 *>(hi + o) = h;
+    if constexpr (SPLIT) *reinterpret_cast<uint2 *>(lo + o) = lw;
+}
+template <bool SPLIT>
+__device__ __forceinline__ void acc_N(const f4 &x, bfr *hi, bfr *lo, int ld, int m0, int n0) {
+    const int l = threadIdx.x & 63;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int o = (m0 + 4 * (l >> 4) + e) * ld + n0 + (l & 15);
+        const uint32_t h = bfbits(x[e]);
+        hi[o] = (bfr)h;
+        if constexpr (SPLIT) lo[o] = (bfr)bfbits(x[e] - bf2f(h));
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- ck_bwd_local (bf16)
+//
+// The same products as ck_bwd_local_kernel<1>, on bf16 operand tiles.  One workgroup of 8 waves per chunk-head;
+// wave w owns the 16-row strip r0 = 16 (w % 4) and column half w / 4 of every [64][*] product.  Phases and their
+// tiles (byte offsets into one LDS arena; lifetimes checked against the barriers between phases):
+//   S1  P3 dK = rc Delta dh'^T (split x split), P4 dp = dY Delta^T (Delta split)     dh' hi/lo, Delta hi/lo, dY
+//   S2  P1 dQ = gamma dY h^T, P2 dW = -dDelta h^T                                    h, dDelta, dY
+//   S3  P5 dQ += dPG K, P6 dK += dPG^T Q (dPG split)                                 dPG, dPG^T, K^T, Q^T
+//   S4a P7 tdw = T^T dW, P8 tdd = T^T dDelta (split x split); dv                      T^T, dW^T, dDelta^T, V
+//   S4b P9 t1 = dDelta V^T, P10 t2 = dW K^T                                           dDelta, V, dW, K
+//   S5  P11 y1 = dT T^T, P12 da = T^T Y1, P13 K K^T                                   dT, T, Y1^T, T^T, K
+//   S6  P14 dK += (M + M^T) K                                                          M + M^T, K^T
+// then the straddle sums for dg and the outputs, as in ck_bwd_local_kernel.
+constexpr int SZ_A = C * LA * 2;       // [64][136]  17408 B
+constexpr int SZ_B = D * LA * 2;       // [128][136] 34816 B
+constexpr int SZ_C = D * LB * 2;       // [128][72]  18432 B
+constexpr int SZ_D = C * LB * 2;       // [64][72]    9216 B
+// S1: dh' hi/lo, h, Delta hi/lo, dY
+constexpr int O_DHH = 0, O_DHL = O_DHH + SZ_B, O_H = O_DHL + SZ_B, O_DLH = O_H + SZ_B, O_DLL = O_DLH + SZ_A;
+constexpr int O_DY = O_DLL + SZ_A;
+constexpr int ARENA = O_DY + SZ_A;
+// S2: dDelta (h stays)
+constexpr int O_DD = 0;
+// S3: dPG, dPG^T (hi / lo), Q^T, K^T, K (dDelta stays)
+constexpr int O_PNH = O_DD + SZ_A, O_PNL = O_PNH + SZ_D, O_PTH = O_PNL + SZ_D, O_PTL = O_PTH + SZ_D;
+constexpr int O_QT = O_PTL + SZ_D, O_KT = O_QT + SZ_C, O_K = O_KT + SZ_C;
+// S4a: dDelta^T hi / lo, T^T hi / lo (in the dead dPG / Q^T space); dW^T, T, V after K
+constexpr int O_DDTH = O_DD + SZ_A, O_DDTL = O_DDTH + SZ_C, O_TTH = O_DDTL + SZ_C, O_TTL = O_TTH + SZ_D;
+constexpr int O_DWT = O_K + SZ_A, O_TN = O_DWT + SZ_C, O_V = O_TN + SZ_D;
+// S4b: dW; S5: dT, Y1^T; S6: M + M^T and the fp32 scratch of M (later the pair matrix E)
+constexpr int O_DW = O_DD + SZ_A, O_DT = O_DW + SZ_A, O_Y1T = O_DT + SZ_D;
+constexpr int O_MM = 0, O_SM = O_V;
+static_assert(O_TTL + SZ_D <= O_KT, "S4a tiles stay clear of K^T");
+static_assert(O_V + SZ_A <= ARENA && O_SM + C * LDC * 4 <= ARENA, "arena");
+static_assert(O_Y1T + SZ_D <= O_TTH, "S5 tiles stay clear of T^T");
+static_assert(ARENA <= 157 * 1024, "arena size");
+
+__global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
+    __shared__ __align__(16) unsigned char arena[ARENA];
+    __shared__ double sG[C];
+    __shared__ float sGam[C], sRc[C], sB[C], sEb[C], sT2[C], sDg[C];
+    __shared__ float sRow[3][2][C];
+    __shared__ float sLast[8];
+    auto T16 = [&](int off) { return reinterpret_cast<bfr *>(arena + off); };
+
+    const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
+    const int r0 = 16 * (w & 3), ch = w >> 2;
+    const int T = a.T, hk = hv / (a.Hv / a.Hk), t0 = c * C, n = min(C, T - t0);
+    const size_t ci = chunk_index(a, b, hv, c);
+    const float *Hc = a.w.H + ci * D * D;    // h = S^T, [j][i]
+    const float *dHc = a.w.dH + ci * D * D;  // dh', [j][i]
+    const float *Dc = a.w.Dl + ci * C * D;
+    const float *dDc = a.w.dDl + ci * C * D;
+    const float *Tc = a.w.T + ci * C * C;
+    const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
+    const size_t v0 = (((size_t)b * T + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
+    const bfr *qsrc = static_cast<const bfr *>(a.q) + qk0, *ksrc = static_cast<const bfr *>(a.k) + qk0;
+    const bfr *vsrc = static_cast<const bfr *>(a.v) + v0;
+
+    // ---- S1: gates; h, dh', Delta, dY; P1 dQ = diag(gamma) dY h^T, P3 dK = diag(rc) Delta dh'^T, P4 dp = dY Delta^T
+    if (tid < C) {
+        sG[tid] = a.w.G[ci * C + tid];
+        sB[tid] = tid < n ? a.beta[((size_t)b * T + t0 + tid) * a.Hv + hv] : 0.f;
+    }
+    float lastp = stage_states<NTB>(T16(O_H), T16(O_DHH), T16(O_DHL), Hc, dHc);  // <dh', h>, the pair (C-1, start)
+    stage_N<C, D, NTB, true, true>(T16(O_DLH), T16(O_DLL), LA, Dc, D, C);
+    if (a.dy_dt == DT_F32)
+        stage_N<C, D, NTB, true, false>(T16(O_DY), nullptr, LA, static_cast<const float *>(a.dy) + v0, v_row, n);
+    else
+        stage_N<C, D, NTB, false, false>(T16(O_DY), nullptr, LA, static_cast<const bfr *>(a.dy) + v0, v_row, n);
+    __syncthreads();
+    if (tid < C) {
+        sGam[tid] = expf((float)sG[tid]);
+        sRc[tid] = expf((float)(sG[C - 1] - sG[tid]));
+    }
+    float pP[2][4];  // P at this lane's dp positions
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pP[t][e] = a.w.P[ci * C * C + (r0 + 4 * lg + e) * C + 32 * ch + 16 * t + li];
+    float bnd[4] = {0.f, 0.f, 0.f, 0.f}, rowB[4] = {0.f, 0.f, 0.f, 0.f}, tl[4] = {0.f, 0.f, 0.f, 0.f};
+    f4 dQ[4], dK[4], dWr[4], dPG[2], Ep[2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) dQ[t] = dK[t] = dWr[t] = zero4();
+    {
+        f4 dp[2] = {zero4(), zero4()};
+        mmab<D, 4>(dQ, T16(O_DY), nullptr, LA, r0, T16(O_H), nullptr, LA, 64 * ch);
+        mmab<D, 4, true, true>(dK, T16(O_DLH), T16(O_DLL), LA, r0, T16(O_DHH), T16(O_DHL), LA, 64 * ch);
+        mmab<D, 2, false, true>(dp, T16(O_DY), nullptr, LA, r0, T16(O_DLH), T16(O_DLL), LA, 32 * ch);
+        __syncthreads();  // sGam / sRc ready; dh', Delta, dY read (h stays for P2)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                dQ[t][e] *= sGam[r0 + 4 * lg + e];
+                dK[t][e] *= sRc[r0 + 4 * lg + e];
+            }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
+                const float pv = s2 <= r ? dp[t][e] : 0.f;
+                Ep[t][e] = s2 < r ? pv * pP[t][e] : 0.f;
+                dPG[t][e] = s2 <= r ? pv * expf((float)(sG[r] - sG[s2])) : 0.f;
+            }
+    }
+    // ---- S2: P2 dW = -dDelta h^T
+    stage_N<C, D, NTB, true, false>(T16(O_DD), nullptr, LA, dDc, D, C);
+    __syncthreads();
+    mmab<D, 4>(dWr, T16(O_DD), nullptr, LA, r0, T16(O_H), nullptr, LA, 64 * ch);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) dWr[t] = -dWr[t];
+    __syncthreads();  // h read
+    // ---- S3: P5 dQ += dPG K, P6 dK += dPG^T Q
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        acc_N<true>(dPG[t], T16(O_PNH), T16(O_PNL), LB, r0, 32 * ch + 16 * t);
+        acc_T<true>(dPG[t], T16(O_PTH), T16(O_PTL), LB, r0, 32 * ch + 16 * t);
+    }
+    stage_T<C, D, NTB, false, false>(T16(O_QT), nullptr, LB, qsrc, qk_row, n);
+    stage_NT<C, D, NTB, false, false>(T16(O_K), LA, T16(O_KT), nullptr, LB, ksrc, qk_row, n);
+    __syncthreads();
+    {
+        const bfr *Qt = T16(O_QT), *Kt = T16(O_KT);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+                bnd[e] += bf2f(Qt[j * LB + r]) * dQ[t][e];
+                tl[e] += bf2f(Kt[j * LB + r]) * dK[t][e];
+            }
+    }
+    mmab<C, 4, true>(dQ, T16(O_PNH), T16(O_PNL), LB, r0, T16(O_KT), nullptr, LB, 64 * ch);
+    mmab<C, 4, true>(dK, T16(O_PTH), T16(O_PTL), LB, r0, T16(O_QT), nullptr, LB, 64 * ch);
+    __syncthreads();  // dPG and Q^T read (K^T, K, dDelta stay)
+    // ---- S4a: P7 tdw = T^T dW, P8 tdd = T^T dDelta; dv
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc_T<false>(dWr[t], T16(O_DWT), nullptr, LB, r0, 64 * ch + 16 * t);
+    stage_NT<C, C, NTB, true, true>(T16(O_TN), LB, T16(O_TTH), T16(O_TTL), LB, Tc, C, C);
+    stage_T<C, D, NTB, true, true>(T16(O_DDTH), T16(O_DDTL), LB, dDc, D, C);
+    stage_N<C, D, NTB, false, false>(T16(O_V), nullptr, LA, vsrc, v_row, n);
+    __syncthreads();
+    {
+        f4 tdw[4], tdd[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) tdw[t] = tdd[t] = zero4();
+        mmab<C, 4>(tdw, T16(O_TTH), nullptr, LB, r0, T16(O_DWT), nullptr, LB, 64 * ch);
+        mmab<C, 4, true, true>(tdd, T16(O_TTH), T16(O_TTL), LB, r0, T16(O_DDTH), T16(O_DDTL), LB, 64 * ch);
+        const bfr *Kt = T16(O_KT), *Vn = T16(O_V);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+                const float bg = sB[r] * sGam[r];
+                dK[t][e] += bg * tdw[t][e];
+                const float s4 = tdw[t][e] * bf2f(Kt[j * LB + r]);
+                rowB[e] += sGam[r] * s4;
+                bnd[e] += bg * s4;
+                rowB[e] += bf2f(Vn[r * LA + j]) * tdd[t][e];
+                if (r < n) store_from_f32(a.dv, v0 + (size_t)r * v_row + j, sB[r] * tdd[t][e], a.grad_dt);
+            }
+    }
+    __syncthreads();  // dDelta^T, dW^T read (T^T hi, T, V, K, K^T, dDelta stay)
+    // ---- S4b: P9 t1 = dDelta V^T, P10 t2 = dW K^T; dT = (t1 + t2 diag(gamma)) diag(beta)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc_N<false>(dWr[t], T16(O_DW), nullptr, LA, r0, 64 * ch + 16 * t);
+    __syncthreads();
+    f4 dT[2];
+    {
+        f4 t1[2] = {zero4(), zero4()}, t2[2] = {zero4(), zero4()};
+        mmab<D, 2>(t1, T16(O_DD), nullptr, LA, r0, T16(O_V), nullptr, LA, 32 * ch);
+        mmab<D, 2>(t2, T16(O_DW), nullptr, LA, r0, T16(O_K), nullptr, LA, 32 * ch);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int s2 = 32 * ch + 16 * t + li;
+                dT[t][e] = sB[s2] * (t1[t][e] + sGam[s2] * t2[t][e]);
+            }
+    }
+    // ---- S5: P11 y1 = dT T^T, P12 da = T^T Y1 (dA = -da), P13 K K^T; M = diag(beta) dA * Gam
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc_N<false>(dT[t], T16(O_DT), nullptr, LB, r0, 32 * ch + 16 * t);
+    __syncthreads();
+    {
+        f4 y1[2] = {zero4(), zero4()};
+        mmab<C, 2>(y1, T16(O_DT), nullptr, LB, r0, T16(O_TN), nullptr, LB, 32 * ch);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc_T<false>(y1[t], T16(O_Y1T), nullptr, LB, r0, 32 * ch + 16 * t);
+    }
+    __syncthreads();
+    f4 Mt[2];
+    {
+        f4 da[2] = {zero4(), zero4()}, kk[2] = {zero4(), zero4()};
+        mmab<C, 2>(da, T16(O_TTH), nullptr, LB, r0, T16(O_Y1T), nullptr, LB, 32 * ch);
+        mmab<D, 2>(kk, T16(O_K), nullptr, LA, r0, T16(O_K), nullptr, LA, 32 * ch);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
+                const float gam = s2 < r ? expf((float)(sG[r] - sG[s2])) : 0.f;
+                const float dav = s2 < r ? -da[t][e] : 0.f;
+                const float kg = kk[t][e] * gam;
+                rowB[e] += dav * kg;
+                Ep[t][e] += dav * sB[r] * kg;
+                Mt[t][e] = sB[r] * dav * gam;
+            }
+    }
+    // ---- S6: P14 dK += (M + M^T) K
+    float *const sM = reinterpret_cast<float *>(arena + O_SM);  // [64][LDC] fp32 (V is dead)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sM[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = Mt[t][e];
+    __syncthreads();
+    {
+        bfr *mm = T16(O_MM);
+        for (int i = tid; i < C * C / 2; i += NTB) {
+            const int r = i / (C / 2), s2 = (i - r * (C / 2)) * 2;
+            const float x0 = sM[r * LDC + s2] + sM[s2 * LDC + r];
+            const float x1 = sM[r * LDC + s2 + 1] + sM[(s2 + 1) * LDC + r];
+            *reinterpret_cast<uint32_t *>(mm + r * LB + s2) = pk(x0, x1);
+        }
+    }
+    __syncthreads();
+    mmab<C, 4>(dK, T16(O_MM), nullptr, LB, r0, T16(O_KT), nullptr, LB, 64 * ch);
+    __syncthreads();  // sM read: the pair matrix E reuses it
+    // ---- straddle sums for dg, dbeta, outputs
+    float *const sE = sM;
+    lastp = wave_sum(lastp);
+    if (l == 0) sLast[w] = lastp;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sE[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = Ep[t][e];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float bsum = row16_allreduce(bnd[e]);
+        const float t2 = row16_allreduce(tl[e]);
+        const float rbv = row16_allreduce(rowB[e]);
+        const int r = r0 + 4 * lg + e;
+        if (li == 0) {
+            sRow[0][ch][r] = bsum;
+            sRow[1][ch][r] = t2;
+            sRow[2][ch][r] = rbv;
+        }
+    }
+    __syncthreads();
+    if (tid < C) {
+        const int r = tid;
+        float eb = sRow[0][0][r] + sRow[0][1][r];
+        if (r == C - 1)
+            for (int i = 0; i < 8; ++i) eb += sLast[i] * sGam[C - 1];
+        sEb[r] = eb;
+        sT2[r] = r < C - 1 ? sRow[1][0][r] + sRow[1][1][r] : 0.f;
+        if (r < n) a.dbeta[((size_t)b * T + t0 + r) * a.Hv + hv] = sRow[2][0][r] + sRow[2][1][r];
+        float acc = 0.f;
+        for (int s2 = 0; s2 < C; ++s2) {
+            const float x = sE[r * LDC + s2];
+            sE[r * LDC + s2] = acc;
+            acc += s2 < r ? x : 0.f;
+        }
+    }
+    __syncthreads();
+    if (tid < C) {
+        const int u = tid;
+        float acc = 0.f;
+        for (int r = u; r < C; ++r) acc += sE[r * LDC + u] + sEb[r];
+        for (int s2 = 0; s2 < u; ++s2) acc += sT2[s2];
+        sDg[u] = acc;
+    }
+    __syncthreads();
+    if (tid < n) {
+        const size_t gi = ((size_t)b * T + t0 + tid) * a.Hv + hv;
+        float dgv = sDg[tid];
+        if (a.gate == GATE_DECAY) {
+            const float dec = a.g[gi];
+            dgv = dec > 1e-30f ? dgv / dec : 0.f;
+        }
+        a.dg[gi] = dgv;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+            if (r < n) {
+                const size_t tok = ((size_t)b * T + t0 + r) * a.Hv + hv;
+                a.w.part[tok * 2 * D + j] = dQ[t][e];
+                a.w.part[tok * 2 * D + D + j] = dK[t][e];
+            }
+        }
+}
+
 }  // namespace ck
 
 // ---------------------------------------------------------------------------------------------- host side
@@ -1068,6 +1603,8 @@ template <int MT>
 static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) {
     if (stage[0] == 's')
         seq_dispatch<MT>(a, st, false);
+    else if (MT == 1 && (a.dy_dt == DT_BF16 || a.dy_dt == DT_F32))
+        hipLaunchKernelGGL(ck::ck_bwd_local_bf16_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
     else
         hipLaunchKernelGGL((ck::ck_bwd_local_kernel<MT>), dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
 }

@@ -120,7 +120,7 @@ def test_saved_intermediates_match_chunk_model(dev):
             assert nerr(P[0, hv, c], Pm) < 1e-5, "P " + msg
             assert nerr(W[0, hv, c], Wm) < 1e-5, "W " + msg
             assert nerr(U[0, hv, c], Um) < 1e-5, "U " + msg
-            assert nerr(H[0, hv, c], h.T) < 1e-5, "H " + msg
+            assert nerr(H[0, hv, c], h) < 1e-5, "H " + msg   # saved as h = S^T ([Dk][Dv])
             Delta, _, h = chunk_model.fwd_chunk(h, qh[sl], kh[sl], Gm, Wm, Um, Pm)
             assert nerr(Dl[0, hv, c], Delta) < 1e-5, "Delta " + msg
         assert nerr(ST[0, hv].cpu().numpy(), h.T) < 1e-5
