@@ -286,6 +286,10 @@ struct Bufs {
     float *dH;   // [B][Hv][NC][D][D]  adjoint of each chunk's exit state, [j][i] like H
     float *dDl;  // [B][Hv][NC][C][D]  dDelta
     float *part; // [B][T][Hv][2][D]   dq | dk per value head
+    // bf16 operand tiles written by ck_prep for the bf16 sequential kernels (raw bf16 bits, k contiguous)
+    unsigned short *Wb;   // [B][Hv][NC][C][D]     W
+    unsigned short *KTb;  // [B][Hv][NC][D][C]     (K diag(gamma_C / gamma))^T
+    unsigned short *Pb;   // [B][Hv][NC][2][C][C]  P hi, P lo
 };
 
 struct Args {
@@ -359,7 +363,7 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
     __shared__ __align__(16) float sT[C * LDC];
     __shared__ float scratch[3 * 256];
     __shared__ double sG[C];
-    __shared__ float sB[C], sGam[C];
+    __shared__ float sB[C], sGam[C], sRc[C];
 
     const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
@@ -389,8 +393,31 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
         sB[tid] = bt;
         sG[tid] = x;
         sGam[tid] = expf((float)x);
+        sRc[tid] = expf((float)(__shfl(x, 63, 64) - x));  // gamma_C / gamma_r
     }
     __syncthreads();
+    if constexpr (MT == 1) {
+        // (K diag(gamma_C / gamma))^T as a bf16 operand tile [j][r] for the bf16 forward
+        // 8-token x 4-channel blocks: 8 row reads from LDS, 4 stores of 8 consecutive tokens
+        unsigned short *kt = a.w.KTb + ci * D * C;
+        if (tid < (C / 8) * (D / 4)) {
+            const int rb = tid / (D / 4), j0 = (tid - rb * (D / 4)) * 4;
+            float v[8][4];
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) {
+                const int r = rb * 8 + rr;
+                const float4 x = *reinterpret_cast<const float4 *>(sK + r * LD + j0);
+                const float sc = sRc[r];
+                v[rr][0] = x.x * sc; v[rr][1] = x.y * sc; v[rr][2] = x.z * sc; v[rr][3] = x.w * sc;
+            }
+            auto p2 = [](float x0, float x1) { return (uint32_t)f32_to_bf16(x0) | ((uint32_t)f32_to_bf16(x1) << 16); };
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+                *reinterpret_cast<uint4 *>(kt + (j0 + cc) * C + rb * 8) =
+                    make_uint4(p2(v[0][cc], v[1][cc]), p2(v[2][cc], v[3][cc]), p2(v[4][cc], v[5][cc]),
+                               p2(v[6][cc], v[7][cc]));
+        }
+    }
     // K K^T (waves 0-3) and Q K^T (waves 4-7): each wave a 16-row strip of 4 tiles
     {
         const int r0 = 16 * (w & 3);
@@ -405,8 +432,17 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
             for (int e = 0; e < 4; ++e) {
                 const int r = r0 + 4 * lg + e, s2 = 16 * t + li;
                 const float gam = s2 <= r ? expf((float)(sG[r] - sG[s2])) : 0.f;
-                if (isq) a.w.P[ci * C * C + r * C + s2] = acc[t][e] * gam;
-                else sA[r * LDC + s2] = s2 < r ? sB[r] * acc[t][e] * gam : 0.f;
+                if (isq) {
+                    const float pv = acc[t][e] * gam;
+                    a.w.P[ci * C * C + r * C + s2] = pv;
+                    if constexpr (MT == 1) {
+                        const uint16_t hi = f32_to_bf16(pv);
+                        a.w.Pb[ci * 2 * C * C + r * C + s2] = hi;
+                        a.w.Pb[ci * 2 * C * C + C * C + r * C + s2] = f32_to_bf16(pv - bf16_to_f32(hi));
+                    }
+                } else {
+                    sA[r * LDC + s2] = s2 < r ? sB[r] * acc[t][e] * gam : 0.f;
+                }
             }
     }
     __syncthreads();
@@ -433,7 +469,10 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
 #pragma unroll
         for (int t = 0; t < 8; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) out[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = acc[t][e];
+            for (int e = 0; e < 4; ++e) {
+                out[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = acc[t][e];
+                if (MT == 1 && !isu) a.w.Wb[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = f32_to_bf16(acc[t][e]);
+            }
     }
     for (int i = tid; i < C * C; i += NTP) a.w.T[ci * C * C + i] = sT[(i / C) * LDC + (i % C)];
     if (tid < C) a.w.G[ci * C + tid] = sG[tid];
@@ -1516,6 +1555,168 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         }
 }
 
+// ---------------------------------------------------------------------------------------------- ck_fwd (bf16)
+//
+// Sequential over chunks like ck_fwd_kernel, for bf16 inputs.  The A operands of every product (W, Q, P hi / lo,
+// (K diag(gamma_C/gamma))^T) are read as MFMA fragments straight from global memory into registers, one chunk
+// ahead (ck_prep wrote them as bf16 tiles); LDS only carries what the waves exchange each chunk: h as the
+// operand [i][j] (hi / lo) and Delta as [i][r] (hi / lo).  Two barriers per chunk.
+__device__ __forceinline__ bf8 ld_frag(const bfr *p) { return *reinterpret_cast<const bf8 *>(p); }
+__device__ __forceinline__ bf8 zero_frag() { return __builtin_bit_cast(bf8, make_uint4(0u, 0u, 0u, 0u)); }
+
+// acc[t] += A * B_t with the A fragments of the K/32 k-steps in registers (ah[k], al[k] for the lo part).
+template <int K, int NTL, bool SA = false, bool SB = false>
+__device__ __forceinline__ void mmar(f4 (&acc)[NTL], const bf8 *ah, const bf8 *al, const bfr *bh, const bfr *bl,
+                                     int ldb, int n0) {
+#pragma unroll
+    for (int k = 0; k < K / 32; ++k) {
+#pragma unroll
+        for (int t = 0; t < NTL; ++t) {
+            const bf8 y = frag(bh, ldb, n0 + 16 * t, 32 * k);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[k], y, acc[t], 0, 0, 0);
+            if constexpr (SA) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[k], y, acc[t], 0, 0, 0);
+            if constexpr (SB) {
+                const bf8 y2 = frag(bl, ldb, n0 + 16 * t, 32 * k);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[k], y2, acc[t], 0, 0, 0);
+            }
+        }
+    }
+}
+
+template <int DN>
+struct FwdFrags {
+    bf8 W[4], Q[4], P[4], K[2];  // P[0..1] hi, P[2..3] lo
+    float U[DN][4];
+    double g;
+};
+
+template <int VS>
+__global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
+    constexpr int NTN = VS / 16, DN = NTN >= 2 ? NTN / 2 : 1;
+    constexpr int LH = D + 8, LDd = C + 8;
+    __shared__ __align__(16) bfr sHh[VS * LH];
+    __shared__ __align__(16) bfr sHl[VS * LH];
+    __shared__ __align__(16) bfr sDh[VS * LDd];
+    __shared__ __align__(16) bfr sDl[VS * LDd];
+    __shared__ float sGam[C];
+
+    const int i0 = blockIdx.x * VS, hv = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
+    const int T = a.T, hk = hv / (a.Hv / a.Hk);
+    const size_t head = (size_t)b * a.Hv + hv;
+    const size_t qk_row = (size_t)a.Hk * D;
+    const int mrow = 16 * (w & 3);
+    const bool cwave = NTN >= 2 || w < 4;
+    const int nt0 = NTN >= 2 ? (w >> 2) * DN : 0;
+
+    f4 h[NTN];  // rows j = 16w + 4lg + e, columns i = i0 + 16t + li
+#pragma unroll
+    for (int t = 0; t < NTN; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
+            h[t][e] = a.state0 ? a.state0[(head * D + i) * D + j] : 0.f;
+        }
+    auto fetch = [&](FwdFrags<DN> &f, int c) {
+        const size_t ci = head * a.NC + c;
+        const int t0 = c * C, n = min(C, T - t0), r = mrow + li;
+        const bfr *wb = a.w.Wb + ci * C * D + r * D + 8 * lg;
+        const bfr *pb = a.w.Pb + ci * 2 * C * C + r * C + 8 * lg;
+        const bfr *kt = a.w.KTb + ci * D * C + (16 * w + li) * C + 8 * lg;
+        const bfr *qb = static_cast<const bfr *>(a.q) + (((size_t)b * T + t0 + r) * a.Hk + hk) * D + 8 * lg;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            f.W[k] = ld_frag(wb + 32 * k);
+            f.Q[k] = r < n ? ld_frag(qb + 32 * k) : zero_frag();
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            f.P[k] = ld_frag(pb + 32 * k);
+            f.P[2 + k] = ld_frag(pb + C * C + 32 * k);
+            f.K[k] = ld_frag(kt + 32 * k);
+        }
+        if (cwave) {
+#pragma unroll
+            for (int t = 0; t < DN; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    f.U[t][e] = a.w.U[ci * C * D + (size_t)(mrow + 4 * lg + e) * D + i0 + 16 * (nt0 + t) + li];
+        }
+        f.g = tid < C ? a.w.G[ci * C + tid] : 0.0;
+    };
+    FwdFrags<DN> cur, nxt;
+    fetch(cur, 0);
+    for (int c = 0; c < a.NC; ++c) {
+        const int t0 = c * C, n = min(C, T - t0);
+        const size_t ci = head * a.NC + c;
+        // h -> LDS as the operand [i][j]; the chunk-entry state -> saved H ([j][i], fp32)
+#pragma unroll
+        for (int t = 0; t < NTN; ++t) {
+            acc_T<true>(h[t], sHh, sHl, LH, 16 * w, 16 * t);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                a.w.H[ci * D * D + (size_t)(16 * w + 4 * lg + e) * D + i0 + 16 * t + li] = h[t][e];
+        }
+        if (tid < C) sGam[tid] = expf((float)cur.g);
+        __syncthreads();
+        if (c + 1 < a.NC) fetch(nxt, c + 1);
+        // Delta = U - W h ; Yi = Q h
+        f4 yi[DN];
+#pragma unroll
+        for (int t = 0; t < DN; ++t) yi[t] = zero4();
+        if (cwave) {
+            f4 wh[DN];
+#pragma unroll
+            for (int t = 0; t < DN; ++t) wh[t] = zero4();
+            mmar<D, DN>(wh, cur.W, nullptr, sHh, nullptr, LH, 16 * nt0);
+            mmar<D, DN, false, true>(yi, cur.Q, nullptr, sHh, sHl, LH, 16 * nt0);
+#pragma unroll
+            for (int t = 0; t < DN; ++t) {
+                f4 dl;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dl[e] = cur.U[t][e] - wh[t][e];
+                acc_T<true>(dl, sDh, sDl, LDd, mrow, 16 * (nt0 + t));
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    a.w.Dl[ci * C * D + (size_t)(mrow + 4 * lg + e) * D + i0 + 16 * (nt0 + t) + li] = dl[e];
+            }
+        }
+        __syncthreads();
+        if (cwave) {
+            // Y = diag(gamma) Q h + P Delta
+#pragma unroll
+            for (int t = 0; t < DN; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) yi[t][e] *= sGam[mrow + 4 * lg + e];
+            mmar<C, DN, true, true>(yi, cur.P, cur.P + 2, sDh, sDl, LDd, 16 * nt0);
+#pragma unroll
+            for (int t = 0; t < DN; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = mrow + 4 * lg + e;
+                    if (r < n)
+                        store_from_f32(a.y, (((size_t)b * T + t0 + r) * a.Hv + hv) * D + i0 + 16 * (nt0 + t) + li,
+                                       yi[t][e], a.out_dt);
+                }
+        }
+        // h = gamma_C h + (K diag(gamma_C / gamma))^T Delta
+        const float gC = sGam[C - 1];
+#pragma unroll
+        for (int t = 0; t < NTN; ++t) h[t] *= gC;
+        mmar<C, NTN>(h, cur.K, nullptr, sDh, nullptr, LDd, 0);
+        cur = nxt;
+    }
+    if (a.state_T) {
+#pragma unroll
+        for (int t = 0; t < NTN; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
+                a.state_T[(head * D + i) * D + j] = h[t][e];
+            }
+    }
+}
+
 }  // namespace ck
 
 // ---------------------------------------------------------------------------------------------- host side
@@ -1537,6 +1738,9 @@ ChunkSizes chunk_sizes(int B, int T, int Hv) {
     s.W = off; off += al256(heads * NC * CK_C * CK_D * 4);
     s.U = off; off += al256(heads * NC * CK_C * CK_D * 4);
     s.Dl = off; off += al256(heads * NC * CK_C * CK_D * 4);
+    s.Wb = off; off += al256(heads * NC * CK_C * CK_D * 2);
+    s.KTb = off; off += al256(heads * NC * CK_D * CK_C * 2);
+    s.Pb = off; off += al256(heads * NC * 2 * CK_C * CK_C * 2);
     s.saved = off;
     off = 0;
     s.dH = off; off += al256(heads * NC * CK_D * CK_D * 4);
@@ -1560,6 +1764,9 @@ static ck::Args make_args(const ChunkCall &cc) {
     a.w.W = reinterpret_cast<float *>(sv + s.W);
     a.w.U = reinterpret_cast<float *>(sv + s.U);
     a.w.Dl = reinterpret_cast<float *>(sv + s.Dl);
+    a.w.Wb = reinterpret_cast<unsigned short *>(sv + s.Wb);
+    a.w.KTb = reinterpret_cast<unsigned short *>(sv + s.KTb);
+    a.w.Pb = reinterpret_cast<unsigned short *>(sv + s.Pb);
     if (cc.work) {
         char *wk = static_cast<char *>(cc.work);
         a.w.dH = reinterpret_cast<float *>(wk + s.dH);
@@ -1578,7 +1785,8 @@ static int slice_width(int heads) { return heads >= 128 ? 64 : heads >= 64 ? 32 
 template <int MT, int VS>
 static void seq_launch(const ck::Args &a, hipStream_t st, bool fwd) {
     const dim3 grid(CK_D / VS, a.Hv, a.B);
-    if (fwd) hipLaunchKernelGGL((ck::ck_fwd_kernel<MT, VS>), grid, dim3(ck::NTS), 0, st, a);
+    if (fwd && MT == 1) hipLaunchKernelGGL((ck::ck_fwd_bf16_kernel<VS>), grid, dim3(ck::NTS), 0, st, a);
+    else if (fwd) hipLaunchKernelGGL((ck::ck_fwd_kernel<MT, VS>), grid, dim3(ck::NTS), 0, st, a);
     else hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<MT, VS>), grid, dim3(ck::NTS), 0, st, a);
 }
 
