@@ -19,6 +19,8 @@
 #include "gdn_common.h"
 #include "gdn_internal.h"
 
+#include <type_traits>
+
 namespace gdn {
 namespace ck {
 
@@ -290,6 +292,10 @@ struct Bufs {
     unsigned short *Wb;   // [B][Hv][NC][C][D]     W
     unsigned short *KTb;  // [B][Hv][NC][D][C]     (K diag(gamma_C / gamma))^T
     unsigned short *Pb;   // [B][Hv][NC][2][C][C]  P hi, P lo
+    // ... and for the bf16 backward sequential kernel
+    unsigned short *PTb;  // [B][Hv][NC][2][C][C]  P^T hi, P^T lo
+    unsigned short *QTb;  // [B][Hv][NC][D][C]     Q^T
+    unsigned short *nWTb; // [B][Hv][NC][D][C]     -W^T
 };
 
 struct Args {
@@ -397,17 +403,21 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
     }
     __syncthreads();
     if constexpr (MT == 1) {
-        // (K diag(gamma_C / gamma))^T as a bf16 operand tile [j][r] for the bf16 forward
-        // 8-token x 4-channel blocks: 8 row reads from LDS, 4 stores of 8 consecutive tokens
-        unsigned short *kt = a.w.KTb + ci * D * C;
-        if (tid < (C / 8) * (D / 4)) {
-            const int rb = tid / (D / 4), j0 = (tid - rb * (D / 4)) * 4;
+        // (K diag(gamma_C / gamma))^T (threads 0-255, for the bf16 forward) and Q^T (threads 256-511, for the
+        // bf16 backward) as bf16 operand tiles [j][r]: 8-token x 4-channel blocks, 8 row reads from LDS, 4
+        // stores of 8 consecutive tokens
+        static_assert(NTP == 2 * (C / 8) * (D / 4), "one block per thread");
+        const bool isq = tid >= (C / 8) * (D / 4);
+        unsigned short *kt = (isq ? a.w.QTb : a.w.KTb) + ci * D * C;
+        {
+            const int blk = isq ? tid - (C / 8) * (D / 4) : tid;
+            const int rb = blk / (D / 4), j0 = (blk - rb * (D / 4)) * 4;
             float v[8][4];
 #pragma unroll
             for (int rr = 0; rr < 8; ++rr) {
                 const int r = rb * 8 + rr;
-                const float4 x = *reinterpret_cast<const float4 *>(sK + r * LD + j0);
-                const float sc = sRc[r];
+                const float4 x = *reinterpret_cast<const float4 *>((isq ? sX : sK) + r * LD + j0);
+                const float sc = isq ? 1.f : sRc[r];
                 v[rr][0] = x.x * sc; v[rr][1] = x.y * sc; v[rr][2] = x.z * sc; v[rr][3] = x.w * sc;
             }
             auto p2 = [](float x0, float x1) { return (uint32_t)f32_to_bf16(x0) | ((uint32_t)f32_to_bf16(x1) << 16); };
@@ -427,7 +437,8 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
         for (int t = 0; t < 4; ++t) acc[t] = zero4();
         mma_strip<MT, D, 4>(acc, (isq ? sX : sK) + r0 * LD, LD, 1, sK, 1, LD, 16 * LD);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t) {
+            uint16_t ph[4], pl[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int r = r0 + 4 * lg + e, s2 = 16 * t + li;
@@ -436,14 +447,23 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
                     const float pv = acc[t][e] * gam;
                     a.w.P[ci * C * C + r * C + s2] = pv;
                     if constexpr (MT == 1) {
-                        const uint16_t hi = f32_to_bf16(pv);
-                        a.w.Pb[ci * 2 * C * C + r * C + s2] = hi;
-                        a.w.Pb[ci * 2 * C * C + C * C + r * C + s2] = f32_to_bf16(pv - bf16_to_f32(hi));
+                        ph[e] = f32_to_bf16(pv);
+                        pl[e] = f32_to_bf16(pv - bf16_to_f32(ph[e]));
+                        a.w.Pb[ci * 2 * C * C + r * C + s2] = ph[e];
+                        a.w.Pb[ci * 2 * C * C + C * C + r * C + s2] = pl[e];
                     }
                 } else {
                     sA[r * LDC + s2] = s2 < r ? sB[r] * acc[t][e] * gam : 0.f;
                 }
             }
+            if (MT == 1 && isq) {
+                // P^T [s][r]: this lane's four consecutive r of column s = 16t + li
+                unsigned short *pt = a.w.PTb + ci * 2 * C * C + (16 * t + li) * C + r0 + 4 * lg;
+                *reinterpret_cast<uint2 *>(pt) = make_uint2(ph[0] | ((uint32_t)ph[1] << 16), ph[2] | ((uint32_t)ph[3] << 16));
+                *reinterpret_cast<uint2 *>(pt + C * C) =
+                    make_uint2(pl[0] | ((uint32_t)pl[1] << 16), pl[2] | ((uint32_t)pl[3] << 16));
+            }
+        }
     }
     __syncthreads();
     unit_lower_inverse<NTP>(sA, sT, scratch);
@@ -465,14 +485,28 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
         for (int t = 0; t < 8; ++t) acc[t] = zero4();
         if (isu) mma_strip<MT, C, 8, true, true>(acc, sT + r0 * LDC, LDC, 1, sX, LD, 1, 16);
         else mma_strip<MT, C, 8>(acc, sT + r0 * LDC, LDC, 1, sK, LD, 1, 16);
-        float *out = isu ? a.w.U : a.w.W;
+        if (MT == 1 && !isu) {
+            // the bf16 path keeps W only as bf16 operand tiles: W [r][j] and -W^T [j][r]
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
+            for (int t = 0; t < 8; ++t) {
+                uint16_t wb[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                out[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = acc[t][e];
-                if (MT == 1 && !isu) a.w.Wb[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = f32_to_bf16(acc[t][e]);
+                for (int e = 0; e < 4; ++e) {
+                    wb[e] = f32_to_bf16(acc[t][e]);
+                    a.w.Wb[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = wb[e];
+                }
+                // bf16 negation flips the sign bit
+                unsigned short *wt = a.w.nWTb + ci * D * C + (16 * t + li) * C + r0 + 4 * lg;
+                *reinterpret_cast<uint2 *>(wt) = make_uint2((wb[0] | ((uint32_t)wb[1] << 16)) ^ 0x80008000u,
+                                                            (wb[2] | ((uint32_t)wb[3] << 16)) ^ 0x80008000u);
             }
+        } else {
+            float *out = isu ? a.w.U : a.w.W;
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) out[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = acc[t][e];
+        }
     }
     for (int i = tid; i < C * C; i += NTP) a.w.T[ci * C * C + i] = sT[(i / C) * LDC + (i % C)];
     if (tid < C) a.w.G[ci * C + tid] = sG[tid];
@@ -1604,7 +1638,6 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
     const size_t head = (size_t)b * a.Hv + hv;
-    const size_t qk_row = (size_t)a.Hk * D;
     const int mrow = 16 * (w & 3);
     const bool cwave = NTN >= 2 || w < 4;
     const int nt0 = NTN >= 2 ? (w >> 2) * DN : 0;
@@ -1717,6 +1750,177 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------- ck_bwd_seq (bf16)
+//
+// Reverse over chunks like ck_bwd_seq_kernel, for bf16 inputs.  Per chunk, with dh' the adjoint of the chunk's
+// exit state (this workgroup's value slice, in MFMA accumulators):
+//   dDelta = diag(rc) K dh' + P^T dY,   dh = gamma_C dh' + Q^T diag(gamma) dY - W^T dDelta.
+// The A operands (K straight from the input, P^T hi / lo, Q^T and -W^T written by ck_prep) are read as MFMA
+// fragments from global memory into registers one chunk ahead, with the chunk's dY slice; LDS carries only what
+// the waves exchange: dh' as the operand [i][j] (hi / lo), dY^T, (diag(gamma) dY)^T (hi / lo) and dDelta^T.
+// Two barriers per chunk.
+struct BwdFrags {
+    bf8 K[4], PT[4], QT[2], WT[2];  // PT[0..1] hi, PT[2..3] lo; WT = -W^T
+    double g;
+};
+
+template <int VS, bool DYF32>
+__global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
+    constexpr int NTN = VS / 16, DN = NTN >= 2 ? NTN / 2 : 1;
+    constexpr int LH = D + 8, LDd = C + 8;
+    constexpr int NYB = (C / 8) * (VS / 2);  // 8-token x 2-column blocks of the dY slice
+    static_assert(NYB <= NTS, "one dY block per thread");
+    __shared__ __align__(16) bfr sHh[VS * LH];    // dh' [i][j], hi
+    __shared__ __align__(16) bfr sHl[VS * LH];    // dh' lo
+    __shared__ __align__(16) bfr sY[VS * LDd];    // dY^T [i][s]
+    __shared__ __align__(16) bfr sYgh[VS * LDd];  // (diag(gamma) dY)^T hi
+    __shared__ __align__(16) bfr sYgl[VS * LDd];  // (diag(gamma) dY)^T lo
+    __shared__ __align__(16) bfr sDd[VS * LDd];   // dDelta^T [i][r]
+    __shared__ float sGam[C], sRc[C];
+
+    const int i0 = blockIdx.x * VS, hv = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
+    const int T = a.T, hk = hv / (a.Hv / a.Hk);
+    const size_t head = (size_t)b * a.Hv + hv;
+    const int mrow = 16 * (w & 3);
+    const bool cwave = NTN >= 2 || w < 4;
+    const int nt0 = NTN >= 2 ? (w >> 2) * DN : 0;
+    // this thread's block of the dY slice: tokens 8 yb .. 8 yb + 7, slice columns yc, yc + 1
+    const bool ythr = tid < NYB;
+    const int yb = tid / (VS / 2), yc = 2 * (tid - yb * (VS / 2));
+
+    f4 dh[NTN];  // rows j = 16w + 4lg + e, columns i = i0 + 16t + li
+#pragma unroll
+    for (int t = 0; t < NTN; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
+            dh[t][e] = a.dstate_T ? a.dstate_T[(head * D + i) * D + j] : 0.f;
+        }
+    using YRaw = typename std::conditional<DYF32, float2, uint32_t>::type;
+    auto fetch = [&](BwdFrags &f, YRaw (&y)[8], int c) {
+        const size_t ci = head * a.NC + c;
+        const int t0 = c * C, n = min(C, T - t0), r = mrow + li;
+        const bfr *kb = static_cast<const bfr *>(a.k) + (((size_t)b * T + t0 + r) * a.Hk + hk) * D + 8 * lg;
+        const bfr *pt = a.w.PTb + ci * 2 * C * C + r * C + 8 * lg;
+        const bfr *qt = a.w.QTb + ci * D * C + (16 * w + li) * C + 8 * lg;
+        const bfr *wt = a.w.nWTb + ci * D * C + (16 * w + li) * C + 8 * lg;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) f.K[k] = r < n ? ld_frag(kb + 32 * k) : zero_frag();
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            f.PT[k] = ld_frag(pt + 32 * k);
+            f.PT[2 + k] = ld_frag(pt + C * C + 32 * k);
+            f.QT[k] = ld_frag(qt + 32 * k);
+            f.WT[k] = ld_frag(wt + 32 * k);
+        }
+        f.g = tid < C ? a.w.G[ci * C + tid] : 0.0;
+        if (ythr) {
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) {
+                const int s2 = 8 * yb + rr;
+                const size_t off = (((size_t)b * T + t0 + s2) * a.Hv + hv) * D + i0 + yc;
+                if constexpr (DYF32)
+                    y[rr] = s2 < n ? *reinterpret_cast<const float2 *>(static_cast<const float *>(a.dy) + off)
+                                   : make_float2(0.f, 0.f);
+                else
+                    y[rr] = s2 < n ? *reinterpret_cast<const uint32_t *>(static_cast<const bfr *>(a.dy) + off) : 0u;
+            }
+        }
+    };
+    BwdFrags cur, nxt;
+    YRaw yr[8];
+    fetch(cur, yr, a.NC - 1);
+    for (int c = a.NC - 1; c >= 0; --c) {
+        const size_t ci = head * a.NC + c;
+        // dh' -> LDS as the operand [i][j] (hi / lo) and -> the saved dH ([j][i], fp32)
+#pragma unroll
+        for (int t = 0; t < NTN; ++t) {
+            acc_T<true>(dh[t], sHh, sHl, LH, 16 * w, 16 * t);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                a.w.dH[ci * D * D + (size_t)(16 * w + 4 * lg + e) * D + i0 + 16 * t + li] = dh[t][e];
+        }
+        // dY^T (exact for bf16 dY) and the gates
+        float yv[8][2];
+        if (ythr) {
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) {
+                if constexpr (DYF32) {
+                    yv[rr][0] = yr[rr].x;
+                    yv[rr][1] = yr[rr].y;
+                } else {
+                    yv[rr][0] = bf2f(yr[rr] & 0xffffu);
+                    yv[rr][1] = bf2f(yr[rr] >> 16);
+                }
+            }
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc)
+                *reinterpret_cast<uint4 *>(sY + (yc + cc) * LDd + 8 * yb) =
+                    make_uint4(pk(yv[0][cc], yv[1][cc]), pk(yv[2][cc], yv[3][cc]), pk(yv[4][cc], yv[5][cc]),
+                               pk(yv[6][cc], yv[7][cc]));
+        }
+        if (tid < C) {  // wave 0 holds the chunk's cumulative log decays
+            const double gl = __shfl(cur.g, C - 1, 64);
+            sGam[tid] = expf((float)cur.g);
+            sRc[tid] = expf((float)(gl - cur.g));
+        }
+        __syncthreads();
+        const float gC = sGam[C - 1];
+        if (ythr) {
+            float gm[8];
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) gm[rr] = sGam[8 * yb + rr];
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                uint4 hi, lo;
+                pk2(gm[0] * yv[0][cc], gm[1] * yv[1][cc], hi.x, lo.x);
+                pk2(gm[2] * yv[2][cc], gm[3] * yv[3][cc], hi.y, lo.y);
+                pk2(gm[4] * yv[4][cc], gm[5] * yv[5][cc], hi.z, lo.z);
+                pk2(gm[6] * yv[6][cc], gm[7] * yv[7][cc], hi.w, lo.w);
+                *reinterpret_cast<uint4 *>(sYgh + (yc + cc) * LDd + 8 * yb) = hi;
+                *reinterpret_cast<uint4 *>(sYgl + (yc + cc) * LDd + 8 * yb) = lo;
+            }
+        }
+        if (c > 0) fetch(nxt, yr, c - 1);
+        // dDelta = diag(rc) K dh' + P^T dY
+        if (cwave) {
+            f4 kd[DN], pd[DN];
+#pragma unroll
+            for (int t = 0; t < DN; ++t) kd[t] = pd[t] = zero4();
+            mmar<D, DN, false, true>(kd, cur.K, nullptr, sHh, sHl, LH, 16 * nt0);
+            mmar<C, DN, true, false>(pd, cur.PT, cur.PT + 2, sY, nullptr, LDd, 16 * nt0);
+#pragma unroll
+            for (int t = 0; t < DN; ++t) {
+                f4 dd;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = mrow + 4 * lg + e;
+                    dd[e] = kd[t][e] * sRc[r] + pd[t][e];
+                    a.w.dDl[ci * C * D + (size_t)r * D + i0 + 16 * (nt0 + t) + li] = dd[e];
+                }
+                acc_T<false>(dd, sDd, nullptr, LDd, mrow, 16 * (nt0 + t));
+            }
+        }
+        __syncthreads();
+        // dh = gamma_C dh' + Q^T diag(gamma) dY + (-W^T) dDelta
+#pragma unroll
+        for (int t = 0; t < NTN; ++t) dh[t] *= gC;
+        mmar<C, NTN, false, true>(dh, cur.QT, nullptr, sYgh, sYgl, LDd, 0);
+        mmar<C, NTN>(dh, cur.WT, nullptr, sDd, nullptr, LDd, 0);
+        cur = nxt;
+    }
+    if (a.dstate0) {
+#pragma unroll
+        for (int t = 0; t < NTN; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
+                a.dstate0[(head * D + i) * D + j] = dh[t][e];
+            }
+    }
+}
+
 }  // namespace ck
 
 // ---------------------------------------------------------------------------------------------- host side
@@ -1741,6 +1945,9 @@ ChunkSizes chunk_sizes(int B, int T, int Hv) {
     s.Wb = off; off += al256(heads * NC * CK_C * CK_D * 2);
     s.KTb = off; off += al256(heads * NC * CK_D * CK_C * 2);
     s.Pb = off; off += al256(heads * NC * 2 * CK_C * CK_C * 2);
+    s.PTb = off; off += al256(heads * NC * 2 * CK_C * CK_C * 2);
+    s.QTb = off; off += al256(heads * NC * CK_D * CK_C * 2);
+    s.nWTb = off; off += al256(heads * NC * CK_D * CK_C * 2);
     s.saved = off;
     off = 0;
     s.dH = off; off += al256(heads * NC * CK_D * CK_D * 4);
@@ -1767,6 +1974,9 @@ static ck::Args make_args(const ChunkCall &cc) {
     a.w.Wb = reinterpret_cast<unsigned short *>(sv + s.Wb);
     a.w.KTb = reinterpret_cast<unsigned short *>(sv + s.KTb);
     a.w.Pb = reinterpret_cast<unsigned short *>(sv + s.Pb);
+    a.w.PTb = reinterpret_cast<unsigned short *>(sv + s.PTb);
+    a.w.QTb = reinterpret_cast<unsigned short *>(sv + s.QTb);
+    a.w.nWTb = reinterpret_cast<unsigned short *>(sv + s.nWTb);
     if (cc.work) {
         char *wk = static_cast<char *>(cc.work);
         a.w.dH = reinterpret_cast<float *>(wk + s.dH);
@@ -1785,9 +1995,14 @@ static int slice_width(int heads) { return heads >= 128 ? 64 : heads >= 64 ? 32 
 template <int MT, int VS>
 static void seq_launch(const ck::Args &a, hipStream_t st, bool fwd) {
     const dim3 grid(CK_D / VS, a.Hv, a.B);
-    if (fwd && MT == 1) hipLaunchKernelGGL((ck::ck_fwd_bf16_kernel<VS>), grid, dim3(ck::NTS), 0, st, a);
-    else if (fwd) hipLaunchKernelGGL((ck::ck_fwd_kernel<MT, VS>), grid, dim3(ck::NTS), 0, st, a);
-    else hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<MT, VS>), grid, dim3(ck::NTS), 0, st, a);
+    if constexpr (MT == 1) {
+        if (fwd) hipLaunchKernelGGL((ck::ck_fwd_bf16_kernel<VS>), grid, dim3(ck::NTS), 0, st, a);
+        else if (a.dy_dt == DT_F32) hipLaunchKernelGGL((ck::ck_bwd_seq_bf16_kernel<VS, true>), grid, dim3(ck::NTS), 0, st, a);
+        else hipLaunchKernelGGL((ck::ck_bwd_seq_bf16_kernel<VS, false>), grid, dim3(ck::NTS), 0, st, a);
+    } else {
+        if (fwd) hipLaunchKernelGGL((ck::ck_fwd_kernel<MT, VS>), grid, dim3(ck::NTS), 0, st, a);
+        else hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<MT, VS>), grid, dim3(ck::NTS), 0, st, a);
+    }
 }
 
 template <int MT>
@@ -1811,7 +2026,7 @@ template <int MT>
 static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) {
     if (stage[0] == 's')
         seq_dispatch<MT>(a, st, false);
-    else if (MT == 1 && (a.dy_dt == DT_BF16 || a.dy_dt == DT_F32))
+    else if constexpr (MT == 1)
         hipLaunchKernelGGL(ck::ck_bwd_local_bf16_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
     else
         hipLaunchKernelGGL((ck::ck_bwd_local_kernel<MT>), dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);

@@ -35,7 +35,8 @@ struct RecBwdArgs {
 // Chunked (WY/UT) form, C = 64, Dk = Dv = 128 (gdn_chunk.hip).
 struct ChunkSizes {
     size_t H, G, T, P, W, U, Dl;         // offsets into the buffer kept from forward to backward
-    size_t Wb, KTb, Pb, saved;           // bf16 operand tiles of the bf16 path; size of that buffer
+    size_t Wb, KTb, Pb, PTb, QTb, nWTb;  // bf16 operand tiles of the bf16 path
+    size_t saved;                        // size of that buffer
     size_t dH, dDl, part, work;          // offsets into / size of the backward workspace
 };
 ChunkSizes chunk_sizes(int B, int T, int Hv);

@@ -151,6 +151,21 @@ def test_chunk_bf16_matches_oracle(dev, T):
             assert nerr(a, w) <= 1e-2, (hk, n, nerr(a, w))
 
 
+def test_chunk_bf16_measured_layout_against_oracle(dev):
+    """B=4, Hk=16, Hv=32 (value slices of 64 in the sequential kernels), T=600 (ten chunks, the last one ragged),
+    bf16 q/k/v/dO, fp32 state and gates: two key-head groups against the fp64 oracle."""
+    d = _inputs(4, 600, 16, 32, seed=21, s0_std=0.02)
+    bf = lambda x: torch.tensor(x).bfloat16().float().numpy()
+    d = dict(d, q=bf(d["q"]), k=bf(d["k"]), v=bf(d["v"]), dy=bf(d["dy"]))
+    got = _gpu(d, dev, "chunk", dtype=torch.bfloat16)
+    for b, hk in ((0, 0), (3, 13)):
+        want = _oracle_group(d, hk, 2, b)
+        errs = {n: nerr(a, w) for n, a, w in zip(NAMES, _slice(got, hk, 2, b), want)}
+        print(f"bf16 B=4 T=600 b={b} hk={hk}", {n: f"{e:.1e}" for n, e in errs.items()}, flush=True)
+        for n, e in errs.items():
+            assert e <= 1e-2, (b, hk, n, e)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_chunk_matches_recurrent_full_heads(dev, dtype):
     """B=1, T=1000, Hk=16, Hv=32: the two forms agree (recurrent form itself checked against the oracle)."""
