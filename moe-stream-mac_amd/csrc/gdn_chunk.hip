@@ -313,6 +313,20 @@ __device__ __forceinline__ size_t chunk_index(const Args &a, int b, int hv, int 
     return ((size_t)b * a.Hv + hv) * a.NC + c;
 }
 
+// Workgroups are dispatched to the 8 XCDs round-robin by linear id, and each XCD has its own L2.  The D / VS
+// workgroups of one head in the sequential kernels read the same chunk tiles, so their linear id L is remapped to
+// L' = (L mod 8) (N / 8) + L / 8 (N workgroups), which puts consecutive L' (the slices of one head) on one XCD,
+// next to each other in its dispatch order.  The identity when N / 8 is not a multiple of the slices per head.
+struct SeqBlock {
+    int slice, hv, b;
+};
+__device__ __forceinline__ SeqBlock seq_block() {
+    const int S = gridDim.x, Hv = gridDim.y, N = S * Hv * gridDim.z;
+    int L = blockIdx.x + S * (blockIdx.y + Hv * blockIdx.z);
+    if (N % 8 == 0 && (N / 8) % S == 0) L = (L % 8) * (N / 8) + L / 8;
+    return {L % S, (L / S) % Hv, L / (S * Hv)};
+}
+
 // (I + A)^-1 of a unit lower-triangular 64x64 matrix, A strictly lower in sA.  Diagonal 16x16 blocks by
 // column-parallel forward substitution, then off-diagonal blocks by distance:
 // T_ij = -T_ii sum_{u=j}^{i-1} A_iu T_uj.
@@ -538,7 +552,8 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
     __shared__ __align__(16) float sD[C * LV];  // Delta slice
     __shared__ double sG[C];
 
-    const int i0 = blockIdx.x * VS, hv = blockIdx.y, b = blockIdx.z;
+    const SeqBlock sb = seq_block();
+    const int i0 = sb.slice * VS, hv = sb.hv, b = sb.b;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
     const size_t head = (size_t)b * a.Hv + hv;
@@ -663,7 +678,8 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
     __shared__ __align__(16) float sD[C * LV];   // dDelta slice
     __shared__ double sG[C];
 
-    const int i0 = blockIdx.x * VS, hv = blockIdx.y, b = blockIdx.z;
+    const SeqBlock sb = seq_block();
+    const int i0 = sb.slice * VS, hv = sb.hv, b = sb.b;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
     const size_t head = (size_t)b * a.Hv + hv;
@@ -1634,7 +1650,8 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
     __shared__ __align__(16) bfr sDl[VS * LDd];
     __shared__ float sGam[C];
 
-    const int i0 = blockIdx.x * VS, hv = blockIdx.y, b = blockIdx.z;
+    const SeqBlock sb = seq_block();
+    const int i0 = sb.slice * VS, hv = sb.hv, b = sb.b;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
     const size_t head = (size_t)b * a.Hv + hv;
@@ -1778,7 +1795,8 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
     __shared__ __align__(16) bfr sDd[VS * LDd];   // dDelta^T [i][r]
     __shared__ float sGam[C], sRc[C];
 
-    const int i0 = blockIdx.x * VS, hv = blockIdx.y, b = blockIdx.z;
+    const SeqBlock sb = seq_block();
+    const int i0 = sb.slice * VS, hv = sb.hv, b = sb.b;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
     const size_t head = (size_t)b * a.Hv + hv;
