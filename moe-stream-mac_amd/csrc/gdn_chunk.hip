@@ -278,7 +278,7 @@ __device__ __forceinline__ float gate_log(float g, int gate) {
 }
 
 struct Bufs {
-    float *H;    // [B][Hv][NC][D][D] chunk-entry states h = S^T, element (j, i) at [j][i]
+    float *H;    // [B][Hv][NC][D][D] chunk-entry states h = S^T, element (j, i) at [j][i] (bf16 bits in the bf16 path)
     double *G;   // [B][Hv][NC][C]
     float *T;    // [B][Hv][NC][C][C]
     float *P;    // [B][Hv][NC][C][C]
@@ -287,7 +287,7 @@ struct Bufs {
     float *Dl;   // [B][Hv][NC][C][D]  Delta
     float *dH;   // [B][Hv][NC][D][D]  adjoint of each chunk's exit state, [j][i] like H
     float *dDl;  // [B][Hv][NC][C][D]  dDelta
-    float *part; // [B][T][Hv][2][D]   dq | dk per value head
+    float *part; // [B][T][Hv][2][D]   dq | dk per value head (bf16 bits when the gradients are bf16)
     // bf16 operand tiles written by ck_prep for the bf16 sequential kernels (raw bf16 bits, k contiguous)
     unsigned short *Wb;   // [B][Hv][NC][C][D]     W
     unsigned short *KTb;  // [B][Hv][NC][D][C]     (K diag(gamma_C / gamma))^T
@@ -303,7 +303,7 @@ struct Args {
     const float *g, *beta, *state0;
     const void *dy;
     const float *dstate_T;
-    void *y, *dv;
+    void *y, *dq, *dk, *dv;
     float *state_T, *dg, *dbeta, *dstate0;
     Bufs w;
     int B, T, Hk, Hv, NC, in_dt, out_dt, dy_dt, grad_dt, gate;
@@ -459,7 +459,7 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
                 const float gam = s2 <= r ? expf((float)(sG[r] - sG[s2])) : 0.f;
                 if (isq) {
                     const float pv = acc[t][e] * gam;
-                    a.w.P[ci * C * C + r * C + s2] = pv;
+                    if constexpr (MT == 0) a.w.P[ci * C * C + r * C + s2] = pv;
                     if constexpr (MT == 1) {
                         ph[e] = f32_to_bf16(pv);
                         pl[e] = f32_to_bf16(pv - bf16_to_f32(ph[e]));
@@ -1241,42 +1241,42 @@ __device__ __forceinline__ void stage_NT(bfr *nh, int ldn, bfr *th, bfr *tl, int
     }
 }
 
-// The two [D][D] fp32 chunk states h and dh' ([j][i]) -> tiles h (hi) and dh' (hi / lo), returning this thread's
-// part of the fp32 inner product <dh', h>.
+// The chunk states h (bf16) and dh' (fp32), both [D][D] as [j][i] -> tiles h and dh' (hi / lo), returning this
+// thread's part of the inner product <dh', h>.
 template <int NTH>
-__device__ __forceinline__ float stage_states(bfr *hh, bfr *dhh, bfr *dhl, const float *H, const float *dH) {
+__device__ __forceinline__ float stage_states(bfr *hh, bfr *dhh, bfr *dhl, const bfr *H, const float *dH) {
     constexpr int CPR = D / 8, NCH = D * CPR, PER = NCH / NTH;
     static_assert(PER * NTH == NCH, "even split");
     const int tid = threadIdx.x;
     float dot = 0.f;
 #pragma unroll
     for (int p0 = 0; p0 < PER; p0 += 2) {
-        float4 hv[2][2], dv[2][2];
+        uint4 hv[2];
+        float4 dv[2][2];
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const int ch = tid + (p0 + p) * NTH;
-            hv[p][0] = reinterpret_cast<const float4 *>(H)[2 * ch];
-            hv[p][1] = reinterpret_cast<const float4 *>(H)[2 * ch + 1];
+            hv[p] = reinterpret_cast<const uint4 *>(H)[ch];
             dv[p][0] = reinterpret_cast<const float4 *>(dH)[2 * ch];
             dv[p][1] = reinterpret_cast<const float4 *>(dH)[2 * ch + 1];
         }
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const int ch = tid + (p0 + p) * NTH, r = ch / CPR, c = (ch - r * CPR) * 8;
-            uint4 h, dh, dl;
-            h = make_uint4(pk(hv[p][0].x, hv[p][0].y), pk(hv[p][0].z, hv[p][0].w), pk(hv[p][1].x, hv[p][1].y),
-                           pk(hv[p][1].z, hv[p][1].w));
+            uint4 dh, dl;
             pk2(dv[p][0].x, dv[p][0].y, dh.x, dl.x);
             pk2(dv[p][0].z, dv[p][0].w, dh.y, dl.y);
             pk2(dv[p][1].x, dv[p][1].y, dh.z, dl.z);
             pk2(dv[p][1].z, dv[p][1].w, dh.w, dl.w);
-            *reinterpret_cast<uint4 *>(hh + r * LA + c) = h;
+            *reinterpret_cast<uint4 *>(hh + r * LA + c) = hv[p];
             *reinterpret_cast<uint4 *>(dhh + r * LA + c) = dh;
             *reinterpret_cast<uint4 *>(dhl + r * LA + c) = dl;
+            const uint32_t hw[4] = {hv[p].x, hv[p].y, hv[p].z, hv[p].w};
 #pragma unroll
-            for (int q = 0; q < 2; ++q)
-                dot += hv[p][q].x * dv[p][q].x + hv[p][q].y * dv[p][q].y + hv[p][q].z * dv[p][q].z +
-                       hv[p][q].w * dv[p][q].w;
+            for (int q = 0; q < 2; ++q) {
+                dot += bf2f(hw[2 * q] & 0xffffu) * dv[p][q].x + bf2f(hw[2 * q] >> 16) * dv[p][q].y +
+                       bf2f(hw[2 * q + 1] & 0xffffu) * dv[p][q].z + bf2f(hw[2 * q + 1] >> 16) * dv[p][q].w;
+            }
         }
     }
     return dot;
@@ -1356,8 +1356,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     const int r0 = 16 * (w & 3), ch = w >> 2;
     const int T = a.T, hk = hv / (a.Hv / a.Hk), t0 = c * C, n = min(C, T - t0);
     const size_t ci = chunk_index(a, b, hv, c);
-    const float *Hc = a.w.H + ci * D * D;    // h = S^T, [j][i]
-    const float *dHc = a.w.dH + ci * D * D;  // dh', [j][i]
+    const bfr *Hc = reinterpret_cast<const bfr *>(a.w.H) + ci * D * D;  // h = S^T, [j][i], bf16
+    const float *dHc = a.w.dH + ci * D * D;                                // dh', [j][i]
     const float *Dc = a.w.Dl + ci * C * D;
     const float *dDc = a.w.dDl + ci * C * D;
     const float *Tc = a.w.T + ci * C * C;
@@ -1386,7 +1386,10 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) pP[t][e] = a.w.P[ci * C * C + (r0 + 4 * lg + e) * C + 32 * ch + 16 * t + li];
+        for (int e = 0; e < 4; ++e) {
+            const size_t pi = ci * 2 * C * C + (r0 + 4 * lg + e) * C + 32 * ch + 16 * t + li;
+            pP[t][e] = bf16_to_f32(a.w.Pb[pi]) + bf16_to_f32(a.w.Pb[pi + C * C]);
+        }
     float bnd[4] = {0.f, 0.f, 0.f, 0.f}, rowB[4] = {0.f, 0.f, 0.f, 0.f}, tl[4] = {0.f, 0.f, 0.f, 0.f};
     f4 dQ[4], dK[4], dWr[4], dPG[2], Ep[2];
 #pragma unroll
@@ -1592,17 +1595,68 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         }
         a.dg[gi] = dgv;
     }
+    if (a.grad_dt == DT_BF16) {
+        // bf16 part: rows [64][2][D] (dq | dk) staged in the free arena, then 16-byte stores
+        bfr *sp = T16(0);
+        constexpr int LP = 2 * D + 8;
+        static_assert(C * LP * 2 <= O_SM, "part staging below the pair matrix");
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
-            if (r < n) {
-                const size_t tok = ((size_t)b * T + t0 + r) * a.Hv + hv;
-                a.w.part[tok * 2 * D + j] = dQ[t][e];
-                a.w.part[tok * 2 * D + D + j] = dK[t][e];
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+                sp[r * LP + j] = (bfr)bfbits(dQ[t][e]);
+                sp[r * LP + D + j] = (bfr)bfbits(dK[t][e]);
             }
+        __syncthreads();
+        bfr *pb = reinterpret_cast<bfr *>(a.w.part);
+        for (int i = tid; i < C * 2 * D / 8; i += NTB) {
+            const int r = i / (2 * D / 8), c8 = (i - r * (2 * D / 8)) * 8;
+            if (r < n)
+                *reinterpret_cast<uint4 *>(pb + (((size_t)b * T + t0 + r) * a.Hv + hv) * 2 * D + c8) =
+                    *reinterpret_cast<const uint4 *>(sp + r * LP + c8);
         }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+                if (r < n) {
+                    const size_t tok = ((size_t)b * T + t0 + r) * a.Hv + hv;
+                    a.w.part[tok * 2 * D + j] = dQ[t][e];
+                    a.w.part[tok * 2 * D + D + j] = dK[t][e];
+                }
+            }
+    }
+}
+
+// dq, dk of the bf16 path: sum of the bf16 per-value-head parts over the Hv / Hk value heads of each key head.
+// One thread per 8 channels of one (token, key head, q | k) row.
+__global__ __launch_bounds__(256) void ck_reduce_qk_kernel(Args a) {
+    const int rep = a.Hv / a.Hk;
+    const size_t rows = (size_t)a.B * a.T * a.Hk * 2;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * (D / 8)) return;
+    const int c8 = (int)(i % (D / 8)) * 8;
+    const size_t row = i / (D / 8);
+    const int which = (int)(row & 1);
+    const size_t bth = row >> 1, bt = bth / a.Hk;
+    const int hk = (int)(bth - bt * a.Hk);
+    const bfr *pb = reinterpret_cast<const bfr *>(a.w.part);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < rep; ++r) {
+        const uint4 x = *reinterpret_cast<const uint4 *>(pb + ((bt * a.Hv + hk * rep + r) * 2 + which) * D + c8);
+        const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc[2 * q] += bf2f(xw[q] & 0xffffu);
+            acc[2 * q + 1] += bf2f(xw[q] >> 16);
+        }
+    }
+    bfr *dst = static_cast<bfr *>(which ? a.dk : a.dq) + bth * D + c8;
+    *reinterpret_cast<uint4 *>(dst) =
+        make_uint4(pk(acc[0], acc[1]), pk(acc[2], acc[3]), pk(acc[4], acc[5]), pk(acc[6], acc[7]));
 }
 
 // ---------------------------------------------------------------------------------------------- ck_fwd (bf16)
@@ -1705,7 +1759,8 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
             acc_T<true>(h[t], sHh, sHl, LH, 16 * w, 16 * t);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                a.w.H[ci * D * D + (size_t)(16 * w + 4 * lg + e) * D + i0 + 16 * t + li] = h[t][e];
+                reinterpret_cast<bfr *>(a.w.H)[ci * D * D + (size_t)(16 * w + 4 * lg + e) * D + i0 + 16 * t + li] =
+                    (bfr)bfbits(h[t][e]);
         }
         if (tid < C) sGam[tid] = expf((float)cur.g);
         __syncthreads();
@@ -1978,7 +2033,8 @@ ChunkSizes chunk_sizes(int B, int T, int Hv) {
 static ck::Args make_args(const ChunkCall &cc) {
     ck::Args a{};
     a.q = cc.q; a.k = cc.k; a.v = cc.v; a.g = cc.g; a.beta = cc.beta; a.state0 = cc.state0;
-    a.dy = cc.dy; a.dstate_T = cc.dstate_T; a.y = cc.y; a.dv = cc.dv; a.state_T = cc.state_T;
+    a.dy = cc.dy; a.dstate_T = cc.dstate_T; a.y = cc.y; a.dq = cc.dq; a.dk = cc.dk; a.dv = cc.dv;
+    a.state_T = cc.state_T;
     a.dg = cc.dg; a.dbeta = cc.dbeta; a.dstate0 = cc.dstate0;
     const ChunkSizes s = chunk_sizes(cc.B, cc.T, cc.Hv);
     char *sv = static_cast<char *>(cc.saved);
@@ -2042,15 +2098,21 @@ static void ck_fwd_launch(const ck::Args &a, hipStream_t st, const char *stage) 
 
 template <int MT>
 static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) {
-    if (stage[0] == 's')
+    if (stage[0] == 's') {
         seq_dispatch<MT>(a, st, false);
-    else if constexpr (MT == 1)
+    } else if (stage[0] == 'r') {
+        const size_t n = (size_t)a.B * a.T * a.Hk * 2 * (CK_D / 8);
+        if (n) hipLaunchKernelGGL(ck::ck_reduce_qk_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
+    } else if constexpr (MT == 1) {
         hipLaunchKernelGGL(ck::ck_bwd_local_bf16_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
+    }
     else
         hipLaunchKernelGGL((ck::ck_bwd_local_kernel<MT>), dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
 }
 
 static int mma_kind(int in_dt) { return in_dt == DT_BF16 ? 1 : 0; }
+
+bool chunk_reduce_qk_bf16(int in_dt, int grad_dt) { return mma_kind(in_dt) == 1 && grad_dt == DT_BF16; }
 
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st) {
     const ck::Args a = make_args(cc);

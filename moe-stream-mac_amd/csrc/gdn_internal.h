@@ -46,13 +46,15 @@ struct ChunkCall {
     const float *g, *beta, *state0;
     const void *dy;
     const float *dstate_T;
-    void *y, *dv;
+    void *y, *dq, *dk, *dv;
     float *state_T, *dg, *dbeta, *dstate0;
     void *saved, *work;
     int B, T, Hk, Hv, in_dt, out_dt, dy_dt, grad_dt, gate;
 };
-// stage: "prep" | "fwd" (forward) or "seq" | "local" (backward)
+// stage: "prep" | "fwd" (forward) or "seq" | "local" | "reduce" (backward; "reduce" only when
+// chunk_reduce_qk_bf16, otherwise launch_reduce_qk collapses the fp32 per-value-head dq | dk)
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st);
+bool chunk_reduce_qk_bf16(int in_dt, int grad_dt);
 
 int pick_lane_width(int Dk);
 int rec_num_row_blocks(int Dv);
