@@ -1822,6 +1822,231 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------- ck_prep (bf16)
+//
+// ck_prep_kernel for bf16 inputs, on bf16 operand tiles read as 16-byte MFMA fragments.  The scalings are folded
+// into T so that the second operand of W and U is the exact bf16 input:
+//   W = (T diag(beta gamma)) K,   U = (T diag(beta)) V   (the T-side operand rounded to bf16, hi / lo for U).
+// LDS regions are time-shared so that two workgroups fit on a CU:
+//   R_K  K [64][LK]                          -> W staging (bf16 [64][LK])
+//   R_Q  Q [64][LK]  -> V^T [128][LT]        -> U staging (fp32, spans R_Q and R_A)
+//   R_A  A fp32 [64][LDC] -> K^T [128][LT]
+//   R_T  T fp32 [64][LDC]
+constexpr int LK = D + 8, LT = C + 8;
+constexpr int PR_K = 0;
+constexpr int PR_Q = PR_K + C * LK * 2;
+constexpr int PR_A = PR_Q + D * LT * 2;
+constexpr int PR_T = PR_A + D * LT * 2;
+constexpr int PR_END = PR_T + C * LDC * 4;
+constexpr int LU = D + 4;
+static_assert(C * LDC * 4 <= D * LT * 2, "A fits its region");
+static_assert(C * LU * 4 + C * LK * 2 <= PR_T, "U and W staging below T");
+
+__global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
+    __shared__ __align__(16) unsigned char pa[PR_END];
+    __shared__ float scratch[3 * 256];
+    __shared__ double sG[C];
+    __shared__ float sB[C], sBG[C], sRc[C];
+    bfr *const sK = reinterpret_cast<bfr *>(pa + PR_K);
+    bfr *const sQ = reinterpret_cast<bfr *>(pa + PR_Q);
+    bfr *const sVT = sQ;
+    float *const sA = reinterpret_cast<float *>(pa + PR_A);
+    bfr *const sKT = reinterpret_cast<bfr *>(pa + PR_A);
+    float *const sT = reinterpret_cast<float *>(pa + PR_T);
+
+    const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
+    const int T = a.T, hk = hv / (a.Hv / a.Hk), t0 = c * C, n = min(C, T - t0);
+    const size_t ci = chunk_index(a, b, hv, c);
+    const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
+    const size_t v0 = (((size_t)b * T + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
+
+    // V as 8-token x 2-channel blocks (one per thread) for the transposed tile, kept in registers until Q is dead
+    static_assert((C / 8) * (D / 2) == NTP, "one V block per thread");
+    const int vb = tid / (D / 2), vc = 2 * (tid - vb * (D / 2));
+    uint32_t vr[8];
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+        const int s2 = 8 * vb + rr;
+        vr[rr] = s2 < n ? *reinterpret_cast<const uint32_t *>(static_cast<const bfr *>(a.v) + v0 + s2 * v_row + vc)
+                        : 0u;
+    }
+    stage_N<C, D, NTP, false, false>(sK, nullptr, LK, static_cast<const bfr *>(a.k) + qk0, qk_row, n);
+    stage_N<C, D, NTP, false, false>(sQ, nullptr, LK, static_cast<const bfr *>(a.q) + qk0, qk_row, n);
+    if (tid < C) {
+        // inclusive prefix sum of the log decays in fp64 across wave 0
+        float bt = 0.f, gl = 0.f;
+        if (tid < n) {
+            const size_t gi = ((size_t)b * T + t0 + tid) * a.Hv + hv;
+            bt = a.beta[gi];
+            gl = gate_log(a.g[gi], a.gate);
+        }
+        double x = gl;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const double y = __shfl_up(x, d, 64);
+            if (tid >= d) x += y;
+        }
+        sB[tid] = bt;
+        sG[tid] = x;
+        sBG[tid] = bt * expf((float)x);
+        sRc[tid] = expf((float)(__shfl(x, 63, 64) - x));  // gamma_C / gamma_r
+    }
+    __syncthreads();
+    // (K diag(gamma_C / gamma))^T (threads 0-255, for the forward) and Q^T (threads 256-511, for the backward) as
+    // global bf16 tiles [j][r]: 8-token x 4-channel blocks, 4 stores of 8 consecutive tokens
+    {
+        const bool isq = tid >= (C / 8) * (D / 4);
+        const int blk = isq ? tid - (C / 8) * (D / 4) : tid;
+        const int rb = blk / (D / 4), j0 = (blk - rb * (D / 4)) * 4;
+        const bfr *src = isq ? sQ : sK;
+        float v[8][4];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+            const int r = rb * 8 + rr;
+            const uint2 x = *reinterpret_cast<const uint2 *>(src + r * LK + j0);
+            const float sc = isq ? 1.f : sRc[r];
+            v[rr][0] = bf2f(x.x & 0xffffu) * sc; v[rr][1] = bf2f(x.x >> 16) * sc;
+            v[rr][2] = bf2f(x.y & 0xffffu) * sc; v[rr][3] = bf2f(x.y >> 16) * sc;
+        }
+        bfr *dst = (isq ? a.w.QTb : a.w.KTb) + ci * D * C;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+            *reinterpret_cast<uint4 *>(dst + (j0 + cc) * C + rb * 8) =
+                make_uint4(pk(v[0][cc], v[1][cc]), pk(v[2][cc], v[3][cc]), pk(v[4][cc], v[5][cc]), pk(v[6][cc], v[7][cc]));
+    }
+    // K K^T (waves 0-3) -> A = strict_lower(diag(beta) K K^T * Gam); Q K^T (waves 4-7) -> P = lower(Q K^T * Gam)
+    {
+        const int r0 = 16 * (w & 3);
+        const bool isq = w >= 4;
+        f4 acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = zero4();
+        mmab<D, 4>(acc, isq ? sQ : sK, nullptr, LK, r0, sK, nullptr, LK, 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint16_t ph[4], pl[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, s2 = 16 * t + li;
+                const float gam = s2 <= r ? expf((float)(sG[r] - sG[s2])) : 0.f;
+                if (isq) {
+                    const float pv = acc[t][e] * gam;
+                    ph[e] = f32_to_bf16(pv);
+                    pl[e] = f32_to_bf16(pv - bf16_to_f32(ph[e]));
+                    a.w.Pb[ci * 2 * C * C + r * C + s2] = ph[e];
+                    a.w.Pb[ci * 2 * C * C + C * C + r * C + s2] = pl[e];
+                } else {
+                    sA[r * LDC + s2] = s2 < r ? sB[r] * acc[t][e] * gam : 0.f;
+                }
+            }
+            if (isq) {
+                // P^T [s][r]: this lane's four consecutive r of column s = 16t + li
+                bfr *pt = a.w.PTb + ci * 2 * C * C + (16 * t + li) * C + r0 + 4 * lg;
+                *reinterpret_cast<uint2 *>(pt) = make_uint2(ph[0] | ((uint32_t)ph[1] << 16), ph[2] | ((uint32_t)ph[3] << 16));
+                *reinterpret_cast<uint2 *>(pt + C * C) =
+                    make_uint2(pl[0] | ((uint32_t)pl[1] << 16), pl[2] | ((uint32_t)pl[3] << 16));
+            }
+        }
+    }
+    __syncthreads();  // Q read: its region takes V^T
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+        uint32_t x[8];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) x[rr] = cc ? vr[rr] >> 16 : vr[rr] & 0xffffu;
+        *reinterpret_cast<uint4 *>(sVT + (vc + cc) * LT + 8 * vb) =
+            make_uint4(x[0] | (x[1] << 16), x[2] | (x[3] << 16), x[4] | (x[5] << 16), x[6] | (x[7] << 16));
+    }
+    unit_lower_inverse<NTP>(sA, sT, scratch);  // ends with a barrier: A is dead
+    // K^T [j][s] (exact) in the A region
+    if (tid < (C / 8) * (D / 4)) {
+        const int rb = tid / (D / 4), j0 = (tid - rb * (D / 4)) * 4;
+        uint32_t x[8][2];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+            const uint2 y = *reinterpret_cast<const uint2 *>(sK + (rb * 8 + rr) * LK + j0);
+            x[rr][0] = y.x;
+            x[rr][1] = y.y;
+        }
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const int hw = cc >> 1, sh = (cc & 1) * 16;
+            uint32_t e8[8];
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) e8[rr] = (x[rr][hw] >> sh) & 0xffffu;
+            *reinterpret_cast<uint4 *>(sKT + (j0 + cc) * LT + rb * 8) =
+                make_uint4(e8[0] | (e8[1] << 16), e8[2] | (e8[3] << 16), e8[4] | (e8[5] << 16), e8[6] | (e8[7] << 16));
+        }
+    }
+    __syncthreads();
+    // W = (T diag(beta gamma)) K (waves 0-3), U = (T diag(beta)) V (waves 4-7): 16-row strips of 8 tiles, the
+    // T-side fragments built from fp32 T in registers
+    const int r0 = 16 * (w & 3);
+    const bool isu = w >= 4;
+    f4 acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = zero4();
+#pragma unroll
+    for (int k = 0; k < C / 32; ++k) {
+        const float *tr = sT + (r0 + li) * LDC + 32 * k + 8 * lg;
+        const float4 x0 = *reinterpret_cast<const float4 *>(tr), x1 = *reinterpret_cast<const float4 *>(tr + 4);
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const float *scl = (isu ? sB : sBG) + 32 * k + 8 * lg;
+        bf8 ah, al;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float y = xv[i] * scl[i];
+            ah[i] = (__bf16)y;
+            al[i] = (__bf16)(y - (float)ah[i]);
+        }
+        const bfr *bt = isu ? sVT : sKT;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const bf8 y = frag(bt, LT, 16 * t, 32 * k);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, y, acc[t], 0, 0, 0);
+            if (isu) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, y, acc[t], 0, 0, 0);
+        }
+    }
+    __syncthreads();  // K, V^T, K^T read: their regions stage U (fp32) and W (bf16)
+    float *const sU = reinterpret_cast<float *>(pa);
+    bfr *const sW = reinterpret_cast<bfr *>(pa + C * LU * 4);
+    if (isu) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sU[(r0 + 4 * lg + e) * LU + 16 * t + li] = acc[t][e];
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint16_t wb[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                wb[e] = f32_to_bf16(acc[t][e]);
+                sW[(r0 + 4 * lg + e) * LK + 16 * t + li] = wb[e];
+            }
+            // -W^T [j][r]; bf16 negation flips the sign bit
+            bfr *wt = a.w.nWTb + ci * D * C + (16 * t + li) * C + r0 + 4 * lg;
+            *reinterpret_cast<uint2 *>(wt) = make_uint2((wb[0] | ((uint32_t)wb[1] << 16)) ^ 0x80008000u,
+                                                        (wb[2] | ((uint32_t)wb[3] << 16)) ^ 0x80008000u);
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < C * D / 4; i += NTP) {  // U fp32
+        const int r = i / (D / 4), c4 = (i - r * (D / 4)) * 4;
+        *reinterpret_cast<float4 *>(a.w.U + ci * C * D + r * D + c4) = *reinterpret_cast<const float4 *>(sU + r * LU + c4);
+    }
+    for (int i = tid; i < C * D / 8; i += NTP) {  // W bf16
+        const int r = i / (D / 8), c8 = (i - r * (D / 8)) * 8;
+        *reinterpret_cast<uint4 *>(a.w.Wb + ci * C * D + r * D + c8) = *reinterpret_cast<const uint4 *>(sW + r * LK + c8);
+    }
+    for (int i = tid; i < C * C / 4; i += NTP) {  // T fp32
+        const int r = i / (C / 4), c4 = (i - r * (C / 4)) * 4;
+        *reinterpret_cast<float4 *>(a.w.T + ci * C * C + r * C + c4) = *reinterpret_cast<const float4 *>(sT + r * LDC + c4);
+    }
+    if (tid < C) a.w.G[ci * C + tid] = sG[tid];
+}
+
 // ---------------------------------------------------------------------------------------------- ck_bwd_seq (bf16)
 //
 // Reverse over chunks like ck_bwd_seq_kernel, for bf16 inputs.  Per chunk, with dh' the adjoint of the chunk's
@@ -2090,7 +2315,9 @@ static void seq_dispatch(const ck::Args &a, hipStream_t st, bool fwd) {
 
 template <int MT>
 static void ck_fwd_launch(const ck::Args &a, hipStream_t st, const char *stage) {
-    if (stage[0] == 'p')
+    if (stage[0] == 'p' && MT == 1)
+        hipLaunchKernelGGL(ck::ck_prep_bf16_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTP), 0, st, a);
+    else if (stage[0] == 'p')
         hipLaunchKernelGGL((ck::ck_prep_kernel<MT>), dim3(a.NC, a.Hv, a.B), dim3(ck::NTP), 0, st, a);
     else
         seq_dispatch<MT>(a, st, true);
