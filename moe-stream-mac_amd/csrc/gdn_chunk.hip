@@ -9,13 +9,13 @@
 // arithmetic.  The reverse pass is the adjoint of these matrix expressions (chunk-parallel except for the
 // state adjoint, which runs backward over chunks like the forward state does).
 //
-// Kernels:
-//   ck_prep      grid (NC, Hv, B): G, T (blocked 16x16 unit-lower inverse), W, U, P of one chunk.
-//   ck_fwd       grid (D/VS, Hv, B): sequential over chunks; one value slice of h lives in MFMA accumulators.
-//   ck_bwd_seq   grid (D/VS, Hv, B): reverse over chunks; the state adjoint dh and dDelta.
-//   ck_bwd_local grid (NC, Hv, B): dq, dk (per value head), dv, dbeta, dg of one chunk.
-// Matrix products run on MFMA: v_mfma_f32_16x16x4_f32 for fp32 inputs, v_mfma_f32_16x16x32_bf16 for bf16
-// inputs (fp32 accumulation; the state stays fp32 in the accumulators).
+// Kernels (one set for fp32 inputs on v_mfma_f32_16x16x4_f32, one for bf16 inputs on v_mfma_f32_16x16x32_bf16;
+// fp32 accumulation, the state stays fp32 in the accumulators):
+//   ck_prep[_bf16]       grid (NC, Hv, B): G, T (blocked 16x16 unit-lower inverse), W, U, P of one chunk.
+//   ck_fwd[_bf16]        grid (D/VS, Hv, B): sequential over chunks; one value slice of h lives in accumulators.
+//   ck_bwd_seq[_bf16]    grid (D/VS, Hv, B): reverse over chunks; the state adjoint dh and dDelta.
+//   ck_bwd_local[_bf16]  grid (NC, Hv, B): dq, dk (per value head), dv, dbeta, dg of one chunk.
+//   ck_reduce_qk         bf16 path: dq, dk summed over the value heads of each key head.
 #include "gdn_common.h"
 #include "gdn_internal.h"
 
@@ -33,82 +33,20 @@ constexpr int NT = 256;
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 
-// acc(16x16) += A(16 x K) * B(K x 16).  Element (r, c) of A is A[r*asr + c*asc]; element (k, n) of B is
-// B[k*bsr + n*bsc]; both pointers are at the tile origin.  Accumulator element e of lane l is
-// (row 4*(l/16) + e, column l%16).
-// With bf16 MFMA (MT == 1) an operand flagged SA / SB is a computed fp32 value, not an exact bf16 input: it
-// is split into hi = bf16(x) and lo = bf16(x - hi) and the product gets the extra hi*lo terms (about 16
-// mantissa bits instead of 8).
-template <int MT, int K, bool SA = false, bool SB = false>
-__device__ __forceinline__ void mma16(f4 &acc, const float *A, int asr, int asc, const float *B, int bsr,
-                                      int bsc) {
-    const int l = threadIdx.x & 63, li = l & 15, lg = l >> 4;
-    if constexpr (MT == 0) {
-#pragma unroll 8
-        for (int k0 = 0; k0 < K; k0 += 4) {
-            const float av = A[li * asr + (k0 + lg) * asc];
-            const float bv = B[(k0 + lg) * bsr + li * bsc];
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
-        }
-    } else {
-#pragma unroll 2
-        for (int k0 = 0; k0 < K; k0 += 32) {
-            bf8 ah, bh, al, bl;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float x = A[li * asr + (k0 + 8 * lg + i) * asc];
-                const float y = B[(k0 + 8 * lg + i) * bsr + li * bsc];
-                ah[i] = (__bf16)x;
-                bh[i] = (__bf16)y;
-                if constexpr (SA) al[i] = (__bf16)(x - (float)ah[i]);
-                if constexpr (SB) bl[i] = (__bf16)(y - (float)bh[i]);
-            }
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
-            if constexpr (SA) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
-            if constexpr (SB) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
-        }
-    }
-}
-
-// A 16-row strip of NTILES output tiles sharing one A operand: acc[t] += A(16 x K) * B_t(K x 16), where B_t
-// starts at B + t * btile.  Each A fragment is loaded (and converted / split) once per k-step for all tiles.
-template <int MT, int K, int NTILES, bool SA = false, bool SB = false>
+// A 16-row strip of NTILES output tiles sharing one A operand, fp32 MFMA (v_mfma_f32_16x16x4_f32):
+// acc[t] += A(16 x K) * B_t(K x 16), where B_t starts at B + t * btile.  Element (r, c) of A is A[r*asr + c*asc];
+// element (k, n) of B_t is B_t[k*bsr + n*bsc].  Accumulator element e of lane l is (row 4*(l/16) + e, column l%16).
+template <int K, int NTILES>
 __device__ __forceinline__ void mma_strip(f4 (&acc)[NTILES], const float *A, int asr, int asc, const float *B,
                                           int bsr, int bsc, int btile) {
     const int l = threadIdx.x & 63, li = l & 15, lg = l >> 4;
-    if constexpr (MT == 0) {
 #pragma unroll 4
-        for (int k0 = 0; k0 < K; k0 += 4) {
-            const float av = A[li * asr + (k0 + lg) * asc];
+    for (int k0 = 0; k0 < K; k0 += 4) {
+        const float av = A[li * asr + (k0 + lg) * asc];
 #pragma unroll
-            for (int t = 0; t < NTILES; ++t) {
-                const float bv = B[t * btile + (k0 + lg) * bsr + li * bsc];
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[t], 0, 0, 0);
-            }
-        }
-    } else {
-#pragma unroll 1
-        for (int k0 = 0; k0 < K; k0 += 32) {
-            bf8 ah, al;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float x = A[li * asr + (k0 + 8 * lg + i) * asc];
-                ah[i] = (__bf16)x;
-                if constexpr (SA) al[i] = (__bf16)(x - (float)ah[i]);
-            }
-#pragma unroll
-            for (int t = 0; t < NTILES; ++t) {
-                bf8 bh, bl;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float y = B[t * btile + (k0 + 8 * lg + i) * bsr + li * bsc];
-                    bh[i] = (__bf16)y;
-                    if constexpr (SB) bl[i] = (__bf16)(y - (float)bh[i]);
-                }
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc[t], 0, 0, 0);
-                if constexpr (SA) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc[t], 0, 0, 0);
-                if constexpr (SB) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc[t], 0, 0, 0);
-            }
+        for (int t = 0; t < NTILES; ++t) {
+            const float bv = B[t * btile + (k0 + lg) * bsr + li * bsc];
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[t], 0, 0, 0);
         }
     }
 }
@@ -375,7 +313,6 @@ __device__ void unit_lower_inverse(const float *sA, float *sT, float *scratch) {
 
 constexpr int NTP = 512;  // ck_prep: 8 waves
 
-template <int MT>
 __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
     __shared__ __align__(16) float sK[C * LD];
     __shared__ __align__(16) float sX[C * LD];
@@ -416,32 +353,6 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
         sRc[tid] = expf((float)(__shfl(x, 63, 64) - x));  // gamma_C / gamma_r
     }
     __syncthreads();
-    if constexpr (MT == 1) {
-        // (K diag(gamma_C / gamma))^T (threads 0-255, for the bf16 forward) and Q^T (threads 256-511, for the
-        // bf16 backward) as bf16 operand tiles [j][r]: 8-token x 4-channel blocks, 8 row reads from LDS, 4
-        // stores of 8 consecutive tokens
-        static_assert(NTP == 2 * (C / 8) * (D / 4), "one block per thread");
-        const bool isq = tid >= (C / 8) * (D / 4);
-        unsigned short *kt = (isq ? a.w.QTb : a.w.KTb) + ci * D * C;
-        {
-            const int blk = isq ? tid - (C / 8) * (D / 4) : tid;
-            const int rb = blk / (D / 4), j0 = (blk - rb * (D / 4)) * 4;
-            float v[8][4];
-#pragma unroll
-            for (int rr = 0; rr < 8; ++rr) {
-                const int r = rb * 8 + rr;
-                const float4 x = *reinterpret_cast<const float4 *>((isq ? sX : sK) + r * LD + j0);
-                const float sc = isq ? 1.f : sRc[r];
-                v[rr][0] = x.x * sc; v[rr][1] = x.y * sc; v[rr][2] = x.z * sc; v[rr][3] = x.w * sc;
-            }
-            auto p2 = [](float x0, float x1) { return (uint32_t)f32_to_bf16(x0) | ((uint32_t)f32_to_bf16(x1) << 16); };
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc)
-                *reinterpret_cast<uint4 *>(kt + (j0 + cc) * C + rb * 8) =
-                    make_uint4(p2(v[0][cc], v[1][cc]), p2(v[2][cc], v[3][cc]), p2(v[4][cc], v[5][cc]),
-                               p2(v[6][cc], v[7][cc]));
-        }
-    }
     // K K^T (waves 0-3) and Q K^T (waves 4-7): each wave a 16-row strip of 4 tiles
     {
         const int r0 = 16 * (w & 3);
@@ -449,35 +360,16 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
         f4 acc[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[t] = zero4();
-        mma_strip<MT, D, 4>(acc, (isq ? sX : sK) + r0 * LD, LD, 1, sK, 1, LD, 16 * LD);
+        mma_strip<D, 4>(acc, (isq ? sX : sK) + r0 * LD, LD, 1, sK, 1, LD, 16 * LD);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            uint16_t ph[4], pl[4];
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int r = r0 + 4 * lg + e, s2 = 16 * t + li;
                 const float gam = s2 <= r ? expf((float)(sG[r] - sG[s2])) : 0.f;
-                if (isq) {
-                    const float pv = acc[t][e] * gam;
-                    if constexpr (MT == 0) a.w.P[ci * C * C + r * C + s2] = pv;
-                    if constexpr (MT == 1) {
-                        ph[e] = f32_to_bf16(pv);
-                        pl[e] = f32_to_bf16(pv - bf16_to_f32(ph[e]));
-                        a.w.Pb[ci * 2 * C * C + r * C + s2] = ph[e];
-                        a.w.Pb[ci * 2 * C * C + C * C + r * C + s2] = pl[e];
-                    }
-                } else {
-                    sA[r * LDC + s2] = s2 < r ? sB[r] * acc[t][e] * gam : 0.f;
-                }
+                if (isq) a.w.P[ci * C * C + r * C + s2] = acc[t][e] * gam;
+                else sA[r * LDC + s2] = s2 < r ? sB[r] * acc[t][e] * gam : 0.f;
             }
-            if (MT == 1 && isq) {
-                // P^T [s][r]: this lane's four consecutive r of column s = 16t + li
-                unsigned short *pt = a.w.PTb + ci * 2 * C * C + (16 * t + li) * C + r0 + 4 * lg;
-                *reinterpret_cast<uint2 *>(pt) = make_uint2(ph[0] | ((uint32_t)ph[1] << 16), ph[2] | ((uint32_t)ph[3] << 16));
-                *reinterpret_cast<uint2 *>(pt + C * C) =
-                    make_uint2(pl[0] | ((uint32_t)pl[1] << 16), pl[2] | ((uint32_t)pl[3] << 16));
-            }
-        }
     }
     __syncthreads();
     unit_lower_inverse<NTP>(sA, sT, scratch);
@@ -497,30 +389,13 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
         f4 acc[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) acc[t] = zero4();
-        if (isu) mma_strip<MT, C, 8, true, true>(acc, sT + r0 * LDC, LDC, 1, sX, LD, 1, 16);
-        else mma_strip<MT, C, 8>(acc, sT + r0 * LDC, LDC, 1, sK, LD, 1, 16);
-        if (MT == 1 && !isu) {
-            // the bf16 path keeps W only as bf16 operand tiles: W [r][j] and -W^T [j][r]
+        if (isu) mma_strip<C, 8>(acc, sT + r0 * LDC, LDC, 1, sX, LD, 1, 16);
+        else mma_strip<C, 8>(acc, sT + r0 * LDC, LDC, 1, sK, LD, 1, 16);
+        float *out = isu ? a.w.U : a.w.W;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                uint16_t wb[4];
+        for (int t = 0; t < 8; ++t)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    wb[e] = f32_to_bf16(acc[t][e]);
-                    a.w.Wb[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = wb[e];
-                }
-                // bf16 negation flips the sign bit
-                unsigned short *wt = a.w.nWTb + ci * D * C + (16 * t + li) * C + r0 + 4 * lg;
-                *reinterpret_cast<uint2 *>(wt) = make_uint2((wb[0] | ((uint32_t)wb[1] << 16)) ^ 0x80008000u,
-                                                            (wb[2] | ((uint32_t)wb[3] << 16)) ^ 0x80008000u);
-            }
-        } else {
-            float *out = isu ? a.w.U : a.w.W;
-#pragma unroll
-            for (int t = 0; t < 8; ++t)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) out[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = acc[t][e];
-        }
+            for (int e = 0; e < 4; ++e) out[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = acc[t][e];
     }
     for (int i = tid; i < C * C; i += NTP) a.w.T[ci * C * C + i] = sT[(i / C) * LDC + (i % C)];
     if (tid < C) a.w.G[ci * C + tid] = sG[tid];
@@ -540,7 +415,7 @@ struct RcScale {
     __device__ float operator()(int r) const { return expf((float)(G[C - 1] - G[r])); }
 };
 
-template <int MT, int VS>
+template <int VS>
 __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
     constexpr int LV = VS + 4;
     constexpr int NTN = VS / 16;                 // value tiles of the slice
@@ -612,8 +487,8 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
 #pragma unroll
         for (int t = 0; t < DN; ++t) wh[t] = yi[t] = zero4();
         if (cwave) {
-            mma_strip<MT, D, DN>(wh, sW + mrow * LD, LD, 1, sH + 16 * nt0, LV, 1, 16);
-            mma_strip<MT, D, DN, false, true>(yi, sQ + mrow * LD, LD, 1, sH + 16 * nt0, LV, 1, 16);
+            mma_strip<D, DN>(wh, sW + mrow * LD, LD, 1, sH + 16 * nt0, LV, 1, 16);
+            mma_strip<D, DN>(yi, sQ + mrow * LD, LD, 1, sH + 16 * nt0, LV, 1, 16);
 #pragma unroll
             for (int t = 0; t < DN; ++t)
 #pragma unroll
@@ -635,7 +510,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
             for (int t = 0; t < DN; ++t)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) yi[t][e] *= expf((float)sG[mrow + 4 * lg + e]);
-            mma_strip<MT, C, DN, true, true>(yi, sW + mrow * LDC, LDC, 1, sD + 16 * nt0, LV, 1, 16);
+            mma_strip<C, DN>(yi, sW + mrow * LDC, LDC, 1, sD + 16 * nt0, LV, 1, 16);
 #pragma unroll
             for (int t = 0; t < DN; ++t)
 #pragma unroll
@@ -650,7 +525,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
         const float gC = expf((float)sG[C - 1]);
 #pragma unroll
         for (int t = 0; t < NTN; ++t) h[t] *= gC;
-        mma_strip<MT, C, NTN>(h, sQ + 16 * w, 1, LD, sD, LV, 1, 16);
+        mma_strip<C, NTN>(h, sQ + 16 * w, 1, LD, sD, LV, 1, 16);
     }
     if (a.state_T) {
 #pragma unroll
@@ -665,7 +540,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
 
 // ---------------------------------------------------------------------------------------------- ck_bwd_seq
 
-template <int MT, int VS>
+template <int VS>
 __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
     constexpr int LV = VS + 4;
     constexpr int NTN = VS / 16;
@@ -739,8 +614,8 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
             f4 kd[DN], pd[DN];
 #pragma unroll
             for (int t = 0; t < DN; ++t) kd[t] = pd[t] = zero4();
-            mma_strip<MT, D, DN, false, true>(kd, sQ + mrow * LD, LD, 1, sH + 16 * nt0, LV, 1, 16);
-            mma_strip<MT, C, DN, true, false>(pd, sW + mrow, 1, LDC, sY + 16 * nt0, LV, 1, 16);
+            mma_strip<D, DN>(kd, sQ + mrow * LD, LD, 1, sH + 16 * nt0, LV, 1, 16);
+            mma_strip<C, DN>(pd, sW + mrow, 1, LDC, sY + 16 * nt0, LV, 1, 16);
 #pragma unroll
             for (int t = 0; t < DN; ++t)
 #pragma unroll
@@ -764,8 +639,8 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
             dh[t] *= gC;
             wd[t] = zero4();
         }
-        mma_strip<MT, C, NTN, false, true>(dh, sQ + 16 * w, 1, LD, sYg, LV, 1, 16);
-        mma_strip<MT, C, NTN>(wd, sW + 16 * w, 1, LD, sD, LV, 1, 16);
+        mma_strip<C, NTN>(dh, sQ + 16 * w, 1, LD, sYg, LV, 1, 16);
+        mma_strip<C, NTN>(wd, sW + 16 * w, 1, LD, sD, LV, 1, 16);
 #pragma unroll
         for (int t = 0; t < NTN; ++t) dh[t] -= wd[t];
     }
@@ -795,7 +670,6 @@ __device__ __forceinline__ float wave_sum(float x) {
 // exp(g_u)) keeps dg accurate for tiny decays, where a reverse cumulative sum of dG would cancel.
 constexpr int NTB = 512;  // ck_bwd_local: 8 waves; waves w and w+4 share the 16-row strip w%4 (column halves)
 
-template <int MT>
 __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     __shared__ __align__(16) float R1[D * LD];       // h / dh' ([j][i]); then K at R1, Q / dW at R1 + C*LD
     __shared__ __align__(16) float R2[C * LD];       // dY, then dDelta, then the pair matrix E
@@ -866,8 +740,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
         f4 dw[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) dQ[t] = dw[t] = zero4();
-        mma_strip<MT, D, 4>(dQ, R2 + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
-        mma_strip<MT, D, 4>(dw, dDc + r0 * D, D, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<D, 4>(dQ, R2 + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<D, 4>(dw, dDc + r0 * D, D, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -883,7 +757,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < 4; ++t) dK[t] = zero4();
-    mma_strip<MT, D, 4, true, true>(dK, Dc + r0 * D, D, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
+    mma_strip<D, 4>(dK, Dc + r0 * D, D, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -891,7 +765,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     f4 dPG[2], Ep[2];
     {
         f4 dp[2] = {zero4(), zero4()};
-        mma_strip<MT, D, 2, false, true>(dp, R2 + r0 * LD, LD, 1, Dc + 32 * ch * D, 1, D, 16 * D);
+        mma_strip<D, 2>(dp, R2 + r0 * LD, LD, 1, Dc + 32 * ch * D, 1, D, 16 * D);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -919,8 +793,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
             bnd[e] += sQm[r * LD + j] * dQ[t][e];
             tl[e] += sKm[r * LD + j] * dK[t][e];
         }
-    mma_strip<MT, C, 4, true, false>(dQ, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16);
-    mma_strip<MT, C, 4, true, false>(dK, R4 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16);
+    mma_strip<C, 4>(dQ, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16);
+    mma_strip<C, 4>(dK, R4 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16);
     __syncthreads();
     // ---- phase 4: through T.  R1b <- dW, R2 <- dDelta, RX <- V, R5 <- T
     load_tile<C, D, NTB>(sQm, LD, dWpark, park_row, n, DT_F32);
@@ -932,8 +806,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
         f4 tdw[4], tdd[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) tdw[t] = tdd[t] = zero4();
-        mma_strip<MT, C, 4>(tdw, R5 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16);
-        mma_strip<MT, C, 4, true, true>(tdd, R5 + r0, 1, LDC, R2 + 64 * ch, LD, 1, 16);
+        mma_strip<C, 4>(tdw, R5 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16);
+        mma_strip<C, 4>(tdd, R5 + r0, 1, LDC, R2 + 64 * ch, LD, 1, 16);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -951,8 +825,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     f4 dT[2];
     {
         f4 t1[2] = {zero4(), zero4()}, t2[2] = {zero4(), zero4()};
-        mma_strip<MT, D, 2>(t1, R2 + r0 * LD, LD, 1, RX + 32 * ch * LD, 1, LD, 16 * LD);
-        mma_strip<MT, D, 2>(t2, sQm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<D, 2>(t1, R2 + r0 * LD, LD, 1, RX + 32 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<D, 2>(t2, sQm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -970,7 +844,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     // ---- phase 5: dA = -T^T dT T^T ; K K^T ; M = diag(beta) dA * Gam
     {
         f4 y1[2] = {zero4(), zero4()};
-        mma_strip<MT, C, 2>(y1, R4 + r0 * LDC, LDC, 1, R5 + 32 * ch * LDC, 1, LDC, 16 * LDC);
+        mma_strip<C, 2>(y1, R4 + r0 * LDC, LDC, 1, R5 + 32 * ch * LDC, 1, LDC, 16 * LDC);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -980,8 +854,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     f4 Mt[2];
     {
         f4 da[2] = {zero4(), zero4()}, kk[2] = {zero4(), zero4()};
-        mma_strip<MT, C, 2>(da, R5 + r0, 1, LDC, R3 + 32 * ch, LDC, 1, 16);
-        mma_strip<MT, D, 2>(kk, sKm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<C, 2>(da, R5 + r0, 1, LDC, R3 + 32 * ch, LDC, 1, 16);
+        mma_strip<D, 2>(kk, sKm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -1001,8 +875,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) R4[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = Mt[t][e];
     __syncthreads();
-    mma_strip<MT, C, 4>(dK, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16);
-    mma_strip<MT, C, 4>(dK, R4 + r0, 1, LDC, sKm + 64 * ch, LD, 1, 16);
+    mma_strip<C, 4>(dK, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16);
+    mma_strip<C, 4>(dK, R4 + r0, 1, LDC, sKm + 64 * ch, LD, 1, 16);
     // ---- phase 6: straddle sums for dg, dbeta, outputs.  R2 (dDelta) is free: E goes there.
     float *const sE = R2;
     lastp = wave_sum(lastp);
@@ -1077,7 +951,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
 // element (m, k) at t[m * ld + k], ld = K + 8.  A lane's fragment (8 consecutive k of row m0 + l%16, starting
 // at k0 + 8*(l/16)) is one 16-byte LDS read; the 16-byte row pad puts the 16 rows of a read in distinct bank
 // groups.  A computed fp32 operand whose rounding reaches the outputs is kept as two tiles hi = bf16(x) and
-// lo = bf16(x - hi) (the split of mma16 above), converted once when the tile is staged instead of at every use.
+// lo = bf16(x - hi), converted once when the tile is staged instead of at every use.
 typedef unsigned short bfr;  // raw bf16 bits
 constexpr int LA = D + 8;    // row stride of [*][128] tiles
 constexpr int LB = C + 8;    // row stride of [*][64] tiles
@@ -2299,8 +2173,8 @@ static void seq_launch(const ck::Args &a, hipStream_t st, bool fwd) {
         else if (a.dy_dt == DT_F32) hipLaunchKernelGGL((ck::ck_bwd_seq_bf16_kernel<VS, true>), grid, dim3(ck::NTS), 0, st, a);
         else hipLaunchKernelGGL((ck::ck_bwd_seq_bf16_kernel<VS, false>), grid, dim3(ck::NTS), 0, st, a);
     } else {
-        if (fwd) hipLaunchKernelGGL((ck::ck_fwd_kernel<MT, VS>), grid, dim3(ck::NTS), 0, st, a);
-        else hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<MT, VS>), grid, dim3(ck::NTS), 0, st, a);
+        if (fwd) hipLaunchKernelGGL((ck::ck_fwd_kernel<VS>), grid, dim3(ck::NTS), 0, st, a);
+        else hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<VS>), grid, dim3(ck::NTS), 0, st, a);
     }
 }
 
@@ -2318,7 +2192,7 @@ static void ck_fwd_launch(const ck::Args &a, hipStream_t st, const char *stage) 
     if (stage[0] == 'p' && MT == 1)
         hipLaunchKernelGGL(ck::ck_prep_bf16_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTP), 0, st, a);
     else if (stage[0] == 'p')
-        hipLaunchKernelGGL((ck::ck_prep_kernel<MT>), dim3(a.NC, a.Hv, a.B), dim3(ck::NTP), 0, st, a);
+        hipLaunchKernelGGL(ck::ck_prep_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTP), 0, st, a);
     else
         seq_dispatch<MT>(a, st, true);
 }
@@ -2334,7 +2208,7 @@ static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) 
         hipLaunchKernelGGL(ck::ck_bwd_local_bf16_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
     }
     else
-        hipLaunchKernelGGL((ck::ck_bwd_local_kernel<MT>), dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
+        hipLaunchKernelGGL(ck::ck_bwd_local_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
 }
 
 static int mma_kind(int in_dt) { return in_dt == DT_BF16 ? 1 : 0; }
