@@ -663,6 +663,87 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+// dbeta and dg of one chunk from the pair terms, after the barrier that completes sE / sRow / sLast:
+//   sE [C][LDC]      E[r][s'] (pair terms, s' < r); overwritten with row prefix sums
+//   sRow[0..2][h][r] the two column halves' row sums of the boundary terms, the pairs (C-1, r) and dbeta
+//   sLast[8]         the waves' parts of <dh', h> (times last_scale: the pair (C-1, chunk start))
+//   sScan[2][C]      scratch
+// dg_u = sum_{r >= u} (sum_{s' < u} E[r][s'] + Eb[r]) + sum_{s < u} T2[s]: row prefix sums in 8-lane segments,
+// column sums in 8-lane groups, and the Eb suffix / T2 prefix as wave-0 shuffle scans.  Every thread takes part.
+template <int NTH>
+__device__ __forceinline__ void chunk_dg_dbeta(float *sE, const float (*sRow)[2][C], const float *sLast, float last_scale,
+                                               float (*sScan)[C], const Args &a, int b, int hv, int t0, int n) {
+    static_assert(NTH == C * 8, "eight threads per row / column");
+    const int tid = threadIdx.x;
+    const size_t g0 = ((size_t)b * a.T + t0) * a.Hv + hv;
+    if (tid < C) {
+        const int r = tid;
+        float eb = sRow[0][0][r] + sRow[0][1][r];
+        if (r == C - 1)
+            for (int i = 0; i < 8; ++i) eb += sLast[i] * last_scale;
+        const float t2 = r < C - 1 ? sRow[1][0][r] + sRow[1][1][r] : 0.f;  // pair (C-1, r)
+        if (r < n) a.dbeta[g0 + (size_t)r * a.Hv] = sRow[2][0][r] + sRow[2][1][r];
+        float su = eb, pr = t2;
+#pragma unroll
+        for (int d = 1; d < C; d <<= 1) {
+            const float y = __shfl_down(su, d, 64);
+            const float z = __shfl_up(pr, d, 64);
+            if (r + d < C) su += y;
+            if (r >= d) pr += z;
+        }
+        // exclusive prefix by a one-lane shift, not by subtracting t2: every partial sum holds only terms whose span
+        // straddles the token (no cancellation of larger terms)
+        const float prx = __shfl_up(pr, 1, 64);
+        sScan[0][r] = su;                // sum_{r' >= r} Eb[r']
+        sScan[1][r] = r > 0 ? prx : 0.f;  // sum_{s < r} T2[s]
+    }
+    {
+        // sE[r][s2] <- sum_{s' < s2, s' < r} E[r][s']
+        const int r = tid >> 3, part = tid & 7, s0 = 8 * part;
+        float *row = sE + r * LDC + s0;
+        const float4 x0 = *reinterpret_cast<const float4 *>(row), x1 = *reinterpret_cast<const float4 *>(row + 4);
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        float ex[8], run = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            ex[i] = run;
+            run += s0 + i < r ? xv[i] : 0.f;
+        }
+        float sc = run;
+#pragma unroll
+        for (int d = 1; d < 8; d <<= 1) {
+            const float y = __shfl_up(sc, d, 8);
+            if (part >= d) sc += y;
+        }
+        const float scx = __shfl_up(sc, 1, 8);
+        const float off = part > 0 ? scx : 0.f;  // the earlier parts of the row (one-lane shift, no subtraction)
+        *reinterpret_cast<float4 *>(row) = make_float4(ex[0] + off, ex[1] + off, ex[2] + off, ex[3] + off);
+        *reinterpret_cast<float4 *>(row + 4) = make_float4(ex[4] + off, ex[5] + off, ex[6] + off, ex[7] + off);
+    }
+    __syncthreads();
+    {
+        const int u = tid >> 3, k = tid & 7;
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 8 * k + i;
+            acc += r >= u ? sE[r * LDC + u] : 0.f;
+        }
+        acc += __shfl_xor(acc, 1, 8);
+        acc += __shfl_xor(acc, 2, 8);
+        acc += __shfl_xor(acc, 4, 8);
+        if (k == 0 && u < n) {
+            const size_t gi = g0 + (size_t)u * a.Hv;
+            float dgv = acc + sScan[0][u] + sScan[1][u];
+            if (a.gate == GATE_DECAY) {
+                const float dec = a.g[gi];
+                dgv = dec > 1e-30f ? dgv / dec : 0.f;
+            }
+            a.dg[gi] = dgv;
+        }
+    }
+}
+
 // dG bookkeeping.  Every term of the log-decay gradient depends on a difference G_r - G_s' of cumulative log
 // decays (s' = -1 stands for the chunk start), so it is a "pair" term E[r][s'] that adds +E to dG_r and -E to
 // dG_s'.  The gradient of the per-token log decay g_u is then the sum of the pair terms whose span straddles
@@ -676,7 +757,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     __shared__ __align__(16) float RX[2 * C * LDC];  // V ([C][LD] fits), then R3 = RX (Y1), R4 = RX + C*LDC
     __shared__ __align__(16) float R5[C * LDC];      // T
     __shared__ double sG[C];
-    __shared__ float sGam[C], sRc[C], sB[C], sEb[C], sT2[C], sDg[C];
+    __shared__ float sGam[C], sRc[C], sB[C], sScan[2][C];
     __shared__ float sRow[3][2][C];                  // per column half: chunk-start pair terms, t2 terms, dbeta
     __shared__ float sLast[8];
 
@@ -898,40 +979,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
         }
     }
     __syncthreads();
-    if (tid < C) {
-        const int r = tid;
-        float eb = sRow[0][0][r] + sRow[0][1][r];
-        if (r == C - 1)
-            for (int i = 0; i < 8; ++i) eb += sLast[i];
-        sEb[r] = eb;
-        sT2[r] = r < C - 1 ? sRow[1][0][r] + sRow[1][1][r] : 0.f;  // pair (C-1, r)
-        if (r < n) a.dbeta[((size_t)b * T + t0 + r) * a.Hv + hv] = sRow[2][0][r] + sRow[2][1][r];
-        // row prefix sums of E over s' = 0 .. r-1, in place: sE[r][s2] <- sum_{s' < s2} E[r][s']
-        float acc = 0.f;
-        for (int s2 = 0; s2 < C; ++s2) {
-            const float x = sE[r * LDC + s2];
-            sE[r * LDC + s2] = acc;
-            acc += s2 < r ? x : 0.f;
-        }
-    }
-    __syncthreads();
-    if (tid < C) {
-        const int u = tid;
-        float acc = 0.f;
-        for (int r = u; r < C; ++r) acc += sE[r * LDC + u] + sEb[r];
-        for (int s2 = 0; s2 < u; ++s2) acc += sT2[s2];
-        sDg[u] = acc;
-    }
-    __syncthreads();
-    if (tid < n) {
-        const size_t gi = ((size_t)b * T + t0 + tid) * a.Hv + hv;
-        float dgv = sDg[tid];
-        if (a.gate == GATE_DECAY) {
-            const float dec = a.g[gi];
-            dgv = dec > 1e-30f ? dgv / dec : 0.f;
-        }
-        a.dg[gi] = dgv;
-    }
+    chunk_dg_dbeta<NTB>(sE, sRow, sLast, 1.f, sScan, a, b, hv, t0, n);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -1220,7 +1268,7 @@ static_assert(ARENA <= 157 * 1024, "arena size");
 __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     __shared__ __align__(16) unsigned char arena[ARENA];
     __shared__ double sG[C];
-    __shared__ float sGam[C], sRc[C], sB[C], sEb[C], sT2[C], sDg[C];
+    __shared__ float sGam[C], sRc[C], sB[C], sScan[2][C];
     __shared__ float sRow[3][2][C];
     __shared__ float sLast[8];
     auto T16 = [&](int off) { return reinterpret_cast<bfr *>(arena + off); };
@@ -1245,6 +1293,14 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         sG[tid] = a.w.G[ci * C + tid];
         sB[tid] = tid < n ? a.beta[((size_t)b * T + t0 + tid) * a.Hv + hv] : 0.f;
     }
+    float pP[2][4];  // P at this lane's dp positions (loads issued first: used after S1)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const size_t pi = ci * 2 * C * C + (r0 + 4 * lg + e) * C + 32 * ch + 16 * t + li;
+            pP[t][e] = bf16_to_f32(a.w.Pb[pi]) + bf16_to_f32(a.w.Pb[pi + C * C]);
+        }
     float lastp = stage_states<NTB>(T16(O_H), T16(O_DHH), T16(O_DHL), Hc, dHc);  // <dh', h>, the pair (C-1, start)
     stage_N<C, D, NTB, true, true>(T16(O_DLH), T16(O_DLL), LA, Dc, D, C);
     if (a.dy_dt == DT_F32)
@@ -1256,14 +1312,6 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         sGam[tid] = expf((float)sG[tid]);
         sRc[tid] = expf((float)(sG[C - 1] - sG[tid]));
     }
-    float pP[2][4];  // P at this lane's dp positions
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const size_t pi = ci * 2 * C * C + (r0 + 4 * lg + e) * C + 32 * ch + 16 * t + li;
-            pP[t][e] = bf16_to_f32(a.w.Pb[pi]) + bf16_to_f32(a.w.Pb[pi + C * C]);
-        }
     float bnd[4] = {0.f, 0.f, 0.f, 0.f}, rowB[4] = {0.f, 0.f, 0.f, 0.f}, tl[4] = {0.f, 0.f, 0.f, 0.f};
     f4 dQ[4], dK[4], dWr[4], dPG[2], Ep[2];
 #pragma unroll
@@ -1436,39 +1484,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         }
     }
     __syncthreads();
-    if (tid < C) {
-        const int r = tid;
-        float eb = sRow[0][0][r] + sRow[0][1][r];
-        if (r == C - 1)
-            for (int i = 0; i < 8; ++i) eb += sLast[i] * sGam[C - 1];
-        sEb[r] = eb;
-        sT2[r] = r < C - 1 ? sRow[1][0][r] + sRow[1][1][r] : 0.f;
-        if (r < n) a.dbeta[((size_t)b * T + t0 + r) * a.Hv + hv] = sRow[2][0][r] + sRow[2][1][r];
-        float acc = 0.f;
-        for (int s2 = 0; s2 < C; ++s2) {
-            const float x = sE[r * LDC + s2];
-            sE[r * LDC + s2] = acc;
-            acc += s2 < r ? x : 0.f;
-        }
-    }
-    __syncthreads();
-    if (tid < C) {
-        const int u = tid;
-        float acc = 0.f;
-        for (int r = u; r < C; ++r) acc += sE[r * LDC + u] + sEb[r];
-        for (int s2 = 0; s2 < u; ++s2) acc += sT2[s2];
-        sDg[u] = acc;
-    }
-    __syncthreads();
-    if (tid < n) {
-        const size_t gi = ((size_t)b * T + t0 + tid) * a.Hv + hv;
-        float dgv = sDg[tid];
-        if (a.gate == GATE_DECAY) {
-            const float dec = a.g[gi];
-            dgv = dec > 1e-30f ? dgv / dec : 0.f;
-        }
-        a.dg[gi] = dgv;
-    }
+    chunk_dg_dbeta<NTB>(sE, sRow, sLast, sGam[C - 1], sScan, a, b, hv, t0, n);
     if (a.grad_dt == DT_BF16) {
         // bf16 part: rows [64][2][D] (dq | dk) staged in the free arena, then 16-byte stores
         bfr *sp = T16(0);
