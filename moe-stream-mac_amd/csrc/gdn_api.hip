@@ -316,8 +316,8 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
     if (f == GDN_FORM_CHUNK) {
         if (misaligned16(q) || misaligned16(k) || misaligned16(v) || misaligned16(dy))
             return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned q, k, v and dy");
-        if (chunk_reduce_qk_bf16(in_dtype, grad_dtype) && (misaligned16(dq) || misaligned16(dk)))
-            return fail(GDN_ERR_INVALID, "the chunked form with bf16 gradients needs 16-byte aligned dq and dk");
+        if (misaligned16(dq) || misaligned16(dk))
+            return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned dq and dk");
         ChunkCall cc{};
         cc.q = q; cc.k = k; cc.v = v; cc.g = g; cc.beta = beta; cc.state0 = state0;
         cc.dy = dy; cc.dstate_T = dstate_T; cc.dq = dq; cc.dk = dk; cc.dv = dv; cc.dg = dg; cc.dbeta = dbeta;
@@ -337,16 +337,9 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
         }
         rc = check_launch(st, "gdn_bwd(ck_bwd_local)");
         if (rc) return rc;
-        if (chunk_reduce_qk_bf16(in_dtype, grad_dtype)) {
-            Timed tm("reduce_qk", st);
-            launch_chunk_stage(cc, "reduce", st);
-            return check_launch(st, "gdn_bwd(reduce_qk)");
-        }
-        a.part_qk = reinterpret_cast<float *>(static_cast<char *>(workspace) + chunk_sizes(B, T, Hv).part);
-        a.nrb = 1;
         {
             Timed tm("reduce_qk", st);
-            launch_reduce_qk(a, st);
+            launch_chunk_stage(cc, "reduce", st);
         }
         return check_launch(st, "gdn_bwd(reduce_qk)");
     }

@@ -15,7 +15,7 @@
 //   ck_fwd[_bf16]        grid (D/VS, Hv, B): sequential over chunks; one value slice of h lives in accumulators.
 //   ck_bwd_seq[_bf16]    grid (D/VS, Hv, B): reverse over chunks; the state adjoint dh and dDelta.
 //   ck_bwd_local[_bf16]  grid (NC, Hv, B): dq, dk (per value head), dv, dbeta, dg of one chunk.
-//   ck_reduce_qk         bf16 path: dq, dk summed over the value heads of each key head.
+//   ck_reduce_qk         dq, dk summed over the value heads of each key head.
 #include "gdn_common.h"
 #include "gdn_internal.h"
 
@@ -223,9 +223,9 @@ struct Bufs {
     float *W;    // [B][Hv][NC][C][D]
     float *U;    // [B][Hv][NC][C][D]
     float *Dl;   // [B][Hv][NC][C][D]  Delta
-    float *dH;   // [B][Hv][NC][D][D]  adjoint of each chunk's exit state, [j][i] like H
+    float *dH;   // [B][Hv][NC][D][D]  adjoint of each chunk's exit state, [j][i] like H (bf16 in the bf16 path)
     float *dDl;  // [B][Hv][NC][C][D]  dDelta
-    float *part; // [B][T][Hv][2][D]   dq | dk per value head (bf16 bits when the gradients are bf16)
+    float *part; // [B][T][Hv][2][D]   dq | dk per value head
     // bf16 operand tiles written by ck_prep for the bf16 sequential kernels (raw bf16 bits, k contiguous)
     unsigned short *Wb;   // [B][Hv][NC][C][D]     W
     unsigned short *KTb;  // [B][Hv][NC][D][C]     (K diag(gamma_C / gamma))^T
@@ -1163,43 +1163,30 @@ __device__ __forceinline__ void stage_NT(bfr *nh, int ldn, bfr *th, bfr *tl, int
     }
 }
 
-// The chunk states h (bf16) and dh' (fp32), both [D][D] as [j][i] -> tiles h and dh' (hi / lo), returning this
-// thread's part of the inner product <dh', h>.
+// The bf16 chunk states h and dh' ([D][D] as [j][i]) -> LDS tiles, returning this thread's part of the inner
+// product <dh', h> (fp32 sums of the bf16 products).
 template <int NTH>
-__device__ __forceinline__ float stage_states(bfr *hh, bfr *dhh, bfr *dhl, const bfr *H, const float *dH) {
+__device__ __forceinline__ float stage_states(bfr *hh, bfr *dhh, const bfr *H, const bfr *dH) {
     constexpr int CPR = D / 8, NCH = D * CPR, PER = NCH / NTH;
     static_assert(PER * NTH == NCH, "even split");
     const int tid = threadIdx.x;
+    uint4 hv[PER], dv[PER];
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int ch = tid + p * NTH;
+        hv[p] = reinterpret_cast<const uint4 *>(H)[ch];
+        dv[p] = reinterpret_cast<const uint4 *>(dH)[ch];
+    }
     float dot = 0.f;
 #pragma unroll
-    for (int p0 = 0; p0 < PER; p0 += 2) {
-        uint4 hv[2];
-        float4 dv[2][2];
+    for (int p = 0; p < PER; ++p) {
+        const int ch = tid + p * NTH, r = ch / CPR, c = (ch - r * CPR) * 8;
+        *reinterpret_cast<uint4 *>(hh + r * LA + c) = hv[p];
+        *reinterpret_cast<uint4 *>(dhh + r * LA + c) = dv[p];
+        const uint32_t hw[4] = {hv[p].x, hv[p].y, hv[p].z, hv[p].w}, dw[4] = {dv[p].x, dv[p].y, dv[p].z, dv[p].w};
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int ch = tid + (p0 + p) * NTH;
-            hv[p] = reinterpret_cast<const uint4 *>(H)[ch];
-            dv[p][0] = reinterpret_cast<const float4 *>(dH)[2 * ch];
-            dv[p][1] = reinterpret_cast<const float4 *>(dH)[2 * ch + 1];
-        }
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int ch = tid + (p0 + p) * NTH, r = ch / CPR, c = (ch - r * CPR) * 8;
-            uint4 dh, dl;
-            pk2(dv[p][0].x, dv[p][0].y, dh.x, dl.x);
-            pk2(dv[p][0].z, dv[p][0].w, dh.y, dl.y);
-            pk2(dv[p][1].x, dv[p][1].y, dh.z, dl.z);
-            pk2(dv[p][1].z, dv[p][1].w, dh.w, dl.w);
-            *reinterpret_cast<uint4 *>(hh + r * LA + c) = hv[p];
-            *reinterpret_cast<uint4 *>(dhh + r * LA + c) = dh;
-            *reinterpret_cast<uint4 *>(dhl + r * LA + c) = dl;
-            const uint32_t hw[4] = {hv[p].x, hv[p].y, hv[p].z, hv[p].w};
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                dot += bf2f(hw[2 * q] & 0xffffu) * dv[p][q].x + bf2f(hw[2 * q] >> 16) * dv[p][q].y +
-                       bf2f(hw[2 * q + 1] & 0xffffu) * dv[p][q].z + bf2f(hw[2 * q + 1] >> 16) * dv[p][q].w;
-            }
-        }
+        for (int q = 0; q < 4; ++q)
+            dot += bf2f(hw[q] & 0xffffu) * bf2f(dw[q] & 0xffffu) + bf2f(hw[q] >> 16) * bf2f(dw[q] >> 16);
     }
     return dot;
 }
@@ -1233,8 +1220,8 @@ __device__ __forceinline__ void acc_N(const f4 &x, bfr *hi, bfr *lo, int ld, int
 // The same products as ck_bwd_local_kernel<1>, on bf16 operand tiles.  One workgroup of 8 waves per chunk-head;
 // wave w owns the 16-row strip r0 = 16 (w % 4) and column half w / 4 of every [64][*] product.  Phases and their
 // tiles (byte offsets into one LDS arena; lifetimes checked against the barriers between phases):
-//   S1  P3 dK = rc Delta dh'^T (split x split), P4 dp = dY Delta^T (Delta split)     dh' hi/lo, Delta hi/lo, dY
-//   S2  P1 dQ = gamma dY h^T, P2 dW = -dDelta h^T                                    h, dDelta, dY
+//   S1  P1 dQ = gamma dY h^T, P2 dW = -dDelta h^T, P3 dK = rc Delta dh'^T (Delta split),   h, dh', dDelta,
+//       P4 dp = dY Delta^T (Delta split)                                                 Delta hi/lo, dY
 //   S3  P5 dQ += dPG K, P6 dK += dPG^T Q (dPG split)                                 dPG, dPG^T, K^T, Q^T
 //   S4a P7 tdw = T^T dW, P8 tdd = T^T dDelta (split x split); dv                      T^T, dW^T, dDelta^T, V
 //   S4b P9 t1 = dDelta V^T, P10 t2 = dW K^T                                           dDelta, V, dW, K
@@ -1245,12 +1232,10 @@ constexpr int SZ_A = C * LA * 2;       // [64][136]  17408 B
 constexpr int SZ_B = D * LA * 2;       // [128][136] 34816 B
 constexpr int SZ_C = D * LB * 2;       // [128][72]  18432 B
 constexpr int SZ_D = C * LB * 2;       // [64][72]    9216 B
-// S1: dh' hi/lo, h, Delta hi/lo, dY
-constexpr int O_DHH = 0, O_DHL = O_DHH + SZ_B, O_H = O_DHL + SZ_B, O_DLH = O_H + SZ_B, O_DLL = O_DLH + SZ_A;
-constexpr int O_DY = O_DLL + SZ_A;
-constexpr int ARENA = O_DY + SZ_A;
-// S2: dDelta (h stays)
+// S1: dDelta (stays until S4b), dh', h, Delta hi/lo, dY
 constexpr int O_DD = 0;
+constexpr int O_DHH = O_DD + SZ_A, O_H = O_DHH + SZ_B, O_DLH = O_H + SZ_B, O_DLL = O_DLH + SZ_A;
+constexpr int O_DY = O_DLL + SZ_A;
 // S3: dPG, dPG^T (hi / lo), Q^T, K^T, K (dDelta stays)
 constexpr int O_PNH = O_DD + SZ_A, O_PNL = O_PNH + SZ_D, O_PTH = O_PNL + SZ_D, O_PTL = O_PTH + SZ_D;
 constexpr int O_QT = O_PTL + SZ_D, O_KT = O_QT + SZ_C, O_K = O_KT + SZ_C;
@@ -1260,8 +1245,10 @@ constexpr int O_DWT = O_K + SZ_A, O_TN = O_DWT + SZ_C, O_V = O_TN + SZ_D;
 // S4b: dW; S5: dT, Y1^T; S6: M + M^T and the fp32 scratch of M (later the pair matrix E)
 constexpr int O_DW = O_DD + SZ_A, O_DT = O_DW + SZ_A, O_Y1T = O_DT + SZ_D;
 constexpr int O_MM = 0, O_SM = O_V;
+constexpr int ARENA = O_SM + C * LDC * 4;
+static_assert(O_DY + SZ_A <= ARENA, "S1 tiles fit");
 static_assert(O_TTL + SZ_D <= O_KT, "S4a tiles stay clear of K^T");
-static_assert(O_V + SZ_A <= ARENA && O_SM + C * LDC * 4 <= ARENA, "arena");
+static_assert(O_V + SZ_A <= ARENA, "arena");
 static_assert(O_Y1T + SZ_D <= O_TTH, "S5 tiles stay clear of T^T");
 static_assert(ARENA <= 157 * 1024, "arena size");
 
@@ -1279,7 +1266,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     const int T = a.T, hk = hv / (a.Hv / a.Hk), t0 = c * C, n = min(C, T - t0);
     const size_t ci = chunk_index(a, b, hv, c);
     const bfr *Hc = reinterpret_cast<const bfr *>(a.w.H) + ci * D * D;  // h = S^T, [j][i], bf16
-    const float *dHc = a.w.dH + ci * D * D;                                // dh', [j][i]
+    const bfr *dHc = reinterpret_cast<const bfr *>(a.w.dH) + ci * D * D;  // dh', [j][i], bf16
     const float *Dc = a.w.Dl + ci * C * D;
     const float *dDc = a.w.dDl + ci * C * D;
     const float *Tc = a.w.T + ci * C * C;
@@ -1301,8 +1288,9 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
             const size_t pi = ci * 2 * C * C + (r0 + 4 * lg + e) * C + 32 * ch + 16 * t + li;
             pP[t][e] = bf16_to_f32(a.w.Pb[pi]) + bf16_to_f32(a.w.Pb[pi + C * C]);
         }
-    float lastp = stage_states<NTB>(T16(O_H), T16(O_DHH), T16(O_DHL), Hc, dHc);  // <dh', h>, the pair (C-1, start)
+    float lastp = stage_states<NTB>(T16(O_H), T16(O_DHH), Hc, dHc);  // <dh', h>, the pair (C-1, start)
     stage_N<C, D, NTB, true, true>(T16(O_DLH), T16(O_DLL), LA, Dc, D, C);
+    stage_N<C, D, NTB, true, false>(T16(O_DD), nullptr, LA, dDc, D, C);
     if (a.dy_dt == DT_F32)
         stage_N<C, D, NTB, true, false>(T16(O_DY), nullptr, LA, static_cast<const float *>(a.dy) + v0, v_row, n);
     else
@@ -1319,9 +1307,10 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     {
         f4 dp[2] = {zero4(), zero4()};
         mmab<D, 4>(dQ, T16(O_DY), nullptr, LA, r0, T16(O_H), nullptr, LA, 64 * ch);
-        mmab<D, 4, true, true>(dK, T16(O_DLH), T16(O_DLL), LA, r0, T16(O_DHH), T16(O_DHL), LA, 64 * ch);
+        mmab<D, 4, true>(dK, T16(O_DLH), T16(O_DLL), LA, r0, T16(O_DHH), nullptr, LA, 64 * ch);
         mmab<D, 2, false, true>(dp, T16(O_DY), nullptr, LA, r0, T16(O_DLH), T16(O_DLL), LA, 32 * ch);
-        __syncthreads();  // sGam / sRc ready; dh', Delta, dY read (h stays for P2)
+        mmab<D, 4>(dWr, T16(O_DD), nullptr, LA, r0, T16(O_H), nullptr, LA, 64 * ch);
+        __syncthreads();  // sGam / sRc ready; the S1 tiles read (dDelta stays)
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -1339,13 +1328,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
                 dPG[t][e] = s2 <= r ? pv * expf((float)(sG[r] - sG[s2])) : 0.f;
             }
     }
-    // ---- S2: P2 dW = -dDelta h^T
-    stage_N<C, D, NTB, true, false>(T16(O_DD), nullptr, LA, dDc, D, C);
-    __syncthreads();
-    mmab<D, 4>(dWr, T16(O_DD), nullptr, LA, r0, T16(O_H), nullptr, LA, 64 * ch);
 #pragma unroll
     for (int t = 0; t < 4; ++t) dWr[t] = -dWr[t];
-    __syncthreads();  // h read
     // ---- S3: P5 dQ += dPG K, P6 dK += dPG^T Q
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -1485,43 +1469,30 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     }
     __syncthreads();
     chunk_dg_dbeta<NTB>(sE, sRow, sLast, sGam[C - 1], sScan, a, b, hv, t0, n);
-    if (a.grad_dt == DT_BF16) {
-        // bf16 part: rows [64][2][D] (dq | dk) staged in the free arena, then 16-byte stores
-        bfr *sp = T16(0);
-        constexpr int LP = 2 * D + 8;
-        static_assert(C * LP * 2 <= O_SM, "part staging below the pair matrix");
+    {
+        // fp32 part rows [64][2][D] (dq | dk), staged in the free arena, then 16-byte stores
+        float *sp = reinterpret_cast<float *>(arena);
+        constexpr int LP = 2 * D + 4;
+        static_assert(C * LP * 4 <= O_SM, "part staging below the pair matrix");
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
-                sp[r * LP + j] = (bfr)bfbits(dQ[t][e]);
-                sp[r * LP + D + j] = (bfr)bfbits(dK[t][e]);
+                sp[r * LP + j] = dQ[t][e];
+                sp[r * LP + D + j] = dK[t][e];
             }
         __syncthreads();
-        bfr *pb = reinterpret_cast<bfr *>(a.w.part);
-        for (int i = tid; i < C * 2 * D / 8; i += NTB) {
-            const int r = i / (2 * D / 8), c8 = (i - r * (2 * D / 8)) * 8;
+        for (int i = tid; i < C * 2 * D / 4; i += NTB) {
+            const int r = i / (2 * D / 4), c4 = (i - r * (2 * D / 4)) * 4;
             if (r < n)
-                *reinterpret_cast<uint4 *>(pb + (((size_t)b * T + t0 + r) * a.Hv + hv) * 2 * D + c8) =
-                    *reinterpret_cast<const uint4 *>(sp + r * LP + c8);
+                *reinterpret_cast<float4 *>(a.w.part + (((size_t)b * T + t0 + r) * a.Hv + hv) * 2 * D + c4) =
+                    *reinterpret_cast<const float4 *>(sp + r * LP + c4);
         }
-    } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
-                if (r < n) {
-                    const size_t tok = ((size_t)b * T + t0 + r) * a.Hv + hv;
-                    a.w.part[tok * 2 * D + j] = dQ[t][e];
-                    a.w.part[tok * 2 * D + D + j] = dK[t][e];
-                }
-            }
     }
 }
 
-// dq, dk of the bf16 path: sum of the bf16 per-value-head parts over the Hv / Hk value heads of each key head.
+// dq, dk: the per-value-head fp32 parts summed over the Hv / Hk value heads of each key head, in order.
 // One thread per 8 channels of one (token, key head, q | k) row.
 __global__ __launch_bounds__(256) void ck_reduce_qk_kernel(Args a) {
     const int rep = a.Hv / a.Hk;
@@ -1533,20 +1504,24 @@ __global__ __launch_bounds__(256) void ck_reduce_qk_kernel(Args a) {
     const int which = (int)(row & 1);
     const size_t bth = row >> 1, bt = bth / a.Hk;
     const int hk = (int)(bth - bt * a.Hk);
-    const bfr *pb = reinterpret_cast<const bfr *>(a.w.part);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int r = 0; r < rep; ++r) {
-        const uint4 x = *reinterpret_cast<const uint4 *>(pb + ((bt * a.Hv + hk * rep + r) * 2 + which) * D + c8);
-        const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            acc[2 * q] += bf2f(xw[q] & 0xffffu);
-            acc[2 * q + 1] += bf2f(xw[q] >> 16);
-        }
+        const float *src = a.w.part + ((bt * a.Hv + hk * rep + r) * 2 + which) * D + c8;
+        const float4 x = *reinterpret_cast<const float4 *>(src), y = *reinterpret_cast<const float4 *>(src + 4);
+        acc[0] += x.x; acc[1] += x.y; acc[2] += x.z; acc[3] += x.w;
+        acc[4] += y.x; acc[5] += y.y; acc[6] += y.z; acc[7] += y.w;
     }
-    bfr *dst = static_cast<bfr *>(which ? a.dk : a.dq) + bth * D + c8;
-    *reinterpret_cast<uint4 *>(dst) =
-        make_uint4(pk(acc[0], acc[1]), pk(acc[2], acc[3]), pk(acc[4], acc[5]), pk(acc[6], acc[7]));
+    void *dst = which ? a.dk : a.dq;
+    const size_t o = bth * D + c8;
+    if (a.grad_dt == DT_BF16) {
+        *reinterpret_cast<uint4 *>(static_cast<bfr *>(dst) + o) =
+            make_uint4(pk(acc[0], acc[1]), pk(acc[2], acc[3]), pk(acc[4], acc[5]), pk(acc[6], acc[7]));
+    } else if (a.grad_dt == DT_F32) {
+        *reinterpret_cast<float4 *>(static_cast<float *>(dst) + o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        *reinterpret_cast<float4 *>(static_cast<float *>(dst) + o + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    } else {
+        for (int q = 0; q < 8; ++q) store_from_f32(dst, o + q, acc[q], a.grad_dt);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------- ck_fwd (bf16)
@@ -2027,7 +2002,8 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
             acc_T<true>(dh[t], sHh, sHl, LH, 16 * w, 16 * t);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                a.w.dH[ci * D * D + (size_t)(16 * w + 4 * lg + e) * D + i0 + 16 * t + li] = dh[t][e];
+                reinterpret_cast<bfr *>(a.w.dH)[ci * D * D + (size_t)(16 * w + 4 * lg + e) * D + i0 + 16 * t + li] =
+                    (bfr)bfbits(dh[t][e]);
         }
         // dY^T (exact for bf16 dY) and the gates
         float yv[8][2];
@@ -2229,7 +2205,6 @@ static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) 
 
 static int mma_kind(int in_dt) { return in_dt == DT_BF16 ? 1 : 0; }
 
-bool chunk_reduce_qk_bf16(int in_dt, int grad_dt) { return mma_kind(in_dt) == 1 && grad_dt == DT_BF16; }
 
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st) {
     const ck::Args a = make_args(cc);

@@ -51,10 +51,9 @@ struct ChunkCall {
     void *saved, *work;
     int B, T, Hk, Hv, in_dt, out_dt, dy_dt, grad_dt, gate;
 };
-// stage: "prep" | "fwd" (forward) or "seq" | "local" | "reduce" (backward; "reduce" only when
-// chunk_reduce_qk_bf16, otherwise launch_reduce_qk collapses the fp32 per-value-head dq | dk)
+// stage: "prep" | "fwd" (forward) or "seq" | "local" | "reduce" (backward; "reduce" sums the per-value-head
+// dq | dk parts that "local" leaves in the workspace)
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st);
-bool chunk_reduce_qk_bf16(int in_dt, int grad_dt);
 
 int pick_lane_width(int Dk);
 int rec_num_row_blocks(int Dv);
@@ -64,7 +63,6 @@ size_t rec_sub_floats(int B, int Hv, int Dk, int Dv, int T, int chunk);
 void launch_rec_fwd(const RecFwdArgs &a, hipStream_t st);
 void launch_rec_bwd(const RecBwdArgs &a, hipStream_t st);
 void launch_rec_bwd_reduce(const RecBwdArgs &a, hipStream_t st);
-void launch_reduce_qk(const RecBwdArgs &a, hipStream_t st);
 void launch_copy_or_zero(float *dst, const float *src, size_t n, hipStream_t st);
 
 // Block ops around the recurrence (gdn_block_ops.hip).  `vec` selects the vector-load kernels; the caller

@@ -514,11 +514,6 @@ void launch_rec_bwd(const RecBwdArgs &a, hipStream_t st) {
     }
 }
 
-void launch_reduce_qk(const RecBwdArgs &a, hipStream_t st) {
-    const size_t nqk = (size_t)a.B * a.T * a.Hk * a.Dk;
-    if (nqk) hipLaunchKernelGGL(rec_bwd_reduce_qk, dim3((unsigned)((nqk + 255) / 256)), dim3(256), 0, st, a);
-}
-
 void launch_rec_bwd_reduce(const RecBwdArgs &a, hipStream_t st) {
     const size_t nqk = (size_t)a.B * a.T * a.Hk * a.Dk;
     const size_t ng = (size_t)a.B * a.T * a.Hv * (a.gate == GATE_DECAY_VEC ? a.Dk : 1);
