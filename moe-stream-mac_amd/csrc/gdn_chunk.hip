@@ -1191,6 +1191,57 @@ __device__ __forceinline__ float stage_states(bfr *hh, bfr *dhh, const bfr *H, c
     return dot;
 }
 
+// An 8-row x 4-column block of a global [ROWS][COLS] tile (rows >= n read as zero), kept as the raw loads so that
+// a phase can issue all of its loads before the first LDS store.  fp32 (F32) or bf16 source.
+template <bool F32>
+struct Blk84 {
+    typename std::conditional<F32, float4, uint2>::type raw[8];
+    int rb, c0;
+    __device__ __forceinline__ void load(const void *src, size_t stride, int blk, int cols, int n) {
+        rb = blk / (cols / 4);
+        c0 = (blk - rb * (cols / 4)) * 4;
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+            const int r = rb * 8 + rr;
+            if constexpr (F32)
+                raw[rr] = r < n ? *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + r * stride + c0)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+            else
+                raw[rr] = r < n ? *reinterpret_cast<const uint2 *>(static_cast<const bfr *>(src) + r * stride + c0)
+                                : make_uint2(0u, 0u);
+        }
+    }
+    __device__ __forceinline__ float val(int rr, int cc) const {
+        if constexpr (F32) {
+            return cc == 0 ? raw[rr].x : cc == 1 ? raw[rr].y : cc == 2 ? raw[rr].z : raw[rr].w;
+        } else {
+            const uint32_t w = cc < 2 ? raw[rr].x : raw[rr].y;
+            return bf2f(cc & 1 ? w >> 16 : w & 0xffffu);
+        }
+    }
+    // dst[c][r]: four stores of 8 consecutive rows (hi, and lo when SPLIT)
+    template <bool SPLIT>
+    __device__ __forceinline__ void store_T(bfr *hi, bfr *lo, int ldt) const {
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            uint4 h, l;
+            pk2(val(0, cc), val(1, cc), h.x, l.x);
+            pk2(val(2, cc), val(3, cc), h.y, l.y);
+            pk2(val(4, cc), val(5, cc), h.z, l.z);
+            pk2(val(6, cc), val(7, cc), h.w, l.w);
+            *reinterpret_cast<uint4 *>(hi + (c0 + cc) * ldt + rb * 8) = h;
+            if constexpr (SPLIT) *reinterpret_cast<uint4 *>(lo + (c0 + cc) * ldt + rb * 8) = l;
+        }
+    }
+    // dst[r][c] (hi): eight stores of 4 consecutive columns
+    __device__ __forceinline__ void store_N(bfr *nh, int ldn) const {
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr)
+            *reinterpret_cast<uint2 *>(nh + (rb * 8 + rr) * ldn + c0) =
+                make_uint2(pk(val(rr, 0), val(rr, 1)), pk(val(rr, 2), val(rr, 3)));
+    }
+};
+
 // MFMA accumulator tile X (rows m0 + 4(l/16) + e, column n0 + l%16) -> LDS, transposed (dst[n][m]: four
 // consecutive bf16 per lane) or natural (dst[m][n]).
 template <bool SPLIT>
@@ -1288,13 +1339,68 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
             const size_t pi = ci * 2 * C * C + (r0 + 4 * lg + e) * C + 32 * ch + 16 * t + li;
             pP[t][e] = bf16_to_f32(a.w.Pb[pi]) + bf16_to_f32(a.w.Pb[pi + C * C]);
         }
-    float lastp = stage_states<NTB>(T16(O_H), T16(O_DHH), Hc, dHc);  // <dh', h>, the pair (C-1, start)
-    stage_N<C, D, NTB, true, true>(T16(O_DLH), T16(O_DLL), LA, Dc, D, C);
-    stage_N<C, D, NTB, true, false>(T16(O_DD), nullptr, LA, dDc, D, C);
-    if (a.dy_dt == DT_F32)
-        stage_N<C, D, NTB, true, false>(T16(O_DY), nullptr, LA, static_cast<const float *>(a.dy) + v0, v_row, n);
-    else
-        stage_N<C, D, NTB, false, false>(T16(O_DY), nullptr, LA, static_cast<const bfr *>(a.dy) + v0, v_row, n);
+    // S1 staging: every global load of the phase is issued before the first LDS store
+    float lastp = 0.f;  // <dh', h>, the pair (C-1, chunk start)
+    {
+        constexpr int SPER = D * (D / 8) / NTB, NPER = C * (D / 8) / NTB;  // 8-element chunks per thread
+        static_assert(SPER * NTB == D * (D / 8) && NPER * NTB == C * (D / 8), "even split");
+        const bool yf32 = a.dy_dt == DT_F32;
+        uint4 hr[SPER], dhr[SPER], dl[2 * NPER], ddl[2 * NPER], yr[2 * NPER];
+#pragma unroll
+        for (int p = 0; p < SPER; ++p) {
+            hr[p] = reinterpret_cast<const uint4 *>(Hc)[tid + p * NTB];
+            dhr[p] = reinterpret_cast<const uint4 *>(dHc)[tid + p * NTB];
+        }
+#pragma unroll
+        for (int p = 0; p < NPER; ++p) {
+            const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
+            dl[2 * p] = *reinterpret_cast<const uint4 *>(Dc + r * D + c);
+            dl[2 * p + 1] = *reinterpret_cast<const uint4 *>(Dc + r * D + c + 4);
+            ddl[2 * p] = *reinterpret_cast<const uint4 *>(dDc + r * D + c);
+            ddl[2 * p + 1] = *reinterpret_cast<const uint4 *>(dDc + r * D + c + 4);
+            if (yf32) {
+                const float *ys = static_cast<const float *>(a.dy) + v0 + (size_t)r * v_row + c;
+                yr[2 * p] = r < n ? *reinterpret_cast<const uint4 *>(ys) : make_uint4(0u, 0u, 0u, 0u);
+                yr[2 * p + 1] = r < n ? *reinterpret_cast<const uint4 *>(ys + 4) : make_uint4(0u, 0u, 0u, 0u);
+            } else {
+                yr[p] = r < n ? *reinterpret_cast<const uint4 *>(static_cast<const bfr *>(a.dy) + v0 + (size_t)r * v_row + c)
+                              : make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+        bfr *const th = T16(O_H), *const tdh = T16(O_DHH);
+#pragma unroll
+        for (int p = 0; p < SPER; ++p) {
+            const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
+            *reinterpret_cast<uint4 *>(th + r * LA + c) = hr[p];
+            *reinterpret_cast<uint4 *>(tdh + r * LA + c) = dhr[p];
+            const uint32_t hw[4] = {hr[p].x, hr[p].y, hr[p].z, hr[p].w}, dw[4] = {dhr[p].x, dhr[p].y, dhr[p].z, dhr[p].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                lastp += bf2f(hw[q] & 0xffffu) * bf2f(dw[q] & 0xffffu) + bf2f(hw[q] >> 16) * bf2f(dw[q] >> 16);
+        }
+        auto f = [](uint32_t x) { return __uint_as_float(x); };
+#pragma unroll
+        for (int p = 0; p < NPER; ++p) {
+            const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
+            uint4 h, l;
+            const uint4 a0 = dl[2 * p], a1 = dl[2 * p + 1];
+            pk2(f(a0.x), f(a0.y), h.x, l.x);
+            pk2(f(a0.z), f(a0.w), h.y, l.y);
+            pk2(f(a1.x), f(a1.y), h.z, l.z);
+            pk2(f(a1.z), f(a1.w), h.w, l.w);
+            *reinterpret_cast<uint4 *>(T16(O_DLH) + r * LA + c) = h;
+            *reinterpret_cast<uint4 *>(T16(O_DLL) + r * LA + c) = l;
+            const uint4 b0 = ddl[2 * p], b1 = ddl[2 * p + 1];
+            *reinterpret_cast<uint4 *>(T16(O_DD) + r * LA + c) =
+                make_uint4(pk(f(b0.x), f(b0.y)), pk(f(b0.z), f(b0.w)), pk(f(b1.x), f(b1.y)), pk(f(b1.z), f(b1.w)));
+            uint4 yv = yr[p];
+            if (yf32) {
+                const uint4 y0 = yr[2 * p], y1 = yr[2 * p + 1];
+                yv = make_uint4(pk(f(y0.x), f(y0.y)), pk(f(y0.z), f(y0.w)), pk(f(y1.x), f(y1.y)), pk(f(y1.z), f(y1.w)));
+            }
+            *reinterpret_cast<uint4 *>(T16(O_DY) + r * LA + c) = yv;
+        }
+    }
     __syncthreads();
     if (tid < C) {
         sGam[tid] = expf((float)sG[tid]);
@@ -1336,8 +1442,20 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         acc_N<true>(dPG[t], T16(O_PNH), T16(O_PNL), LB, r0, 32 * ch + 16 * t);
         acc_T<true>(dPG[t], T16(O_PTH), T16(O_PTL), LB, r0, 32 * ch + 16 * t);
     }
-    stage_T<C, D, NTB, false, false>(T16(O_QT), nullptr, LB, qsrc, qk_row, n);
-    stage_NT<C, D, NTB, false, false>(T16(O_K), LA, T16(O_KT), nullptr, LB, ksrc, qk_row, n);
+    {
+        // Q^T (threads 0-255) and K, K^T (threads 256-511): one 8 x 4 block per thread, one memory round trip
+        constexpr int NBQ = (C / 8) * (D / 4);
+        static_assert(2 * NBQ == NTB, "one block per thread");
+        const bool isk = tid >= NBQ;
+        Blk84<false> bk;
+        bk.load(isk ? ksrc : qsrc, qk_row, isk ? tid - NBQ : tid, D, n);
+        if (isk) {
+            bk.store_N(T16(O_K), LA);
+            bk.store_T<false>(T16(O_KT), nullptr, LB);
+        } else {
+            bk.store_T<false>(T16(O_QT), nullptr, LB);
+        }
+    }
     __syncthreads();
     {
         const bfr *Qt = T16(O_QT), *Kt = T16(O_KT);
@@ -1356,9 +1474,31 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     // ---- S4a: P7 tdw = T^T dW, P8 tdd = T^T dDelta; dv
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc_T<false>(dWr[t], T16(O_DWT), nullptr, LB, r0, 64 * ch + 16 * t);
-    stage_NT<C, C, NTB, true, true>(T16(O_TN), LB, T16(O_TTH), T16(O_TTL), LB, Tc, C, C);
-    stage_T<C, D, NTB, true, true>(T16(O_DDTH), T16(O_DDTL), LB, dDc, D, C);
-    stage_N<C, D, NTB, false, false>(T16(O_V), nullptr, LA, vsrc, v_row, n);
+    {
+        // dDelta^T hi / lo (threads 0-255), T and T^T hi / lo (threads 256-383), V (all): one memory round trip
+        constexpr int NBD = (C / 8) * (D / 4), NBT = (C / 8) * (C / 4);
+        static_assert(NBD + NBT <= NTB && C * (D / 8) == 2 * NTB, "block split");
+        Blk84<true> bd;
+        const bool isd = tid < NBD, ist = tid >= NBD && tid < NBD + NBT;
+        if (isd) bd.load(dDc, D, tid, D, C);
+        if (ist) bd.load(Tc, C, tid - NBD, C, C);
+        uint4 vr[2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
+            vr[p] = r < n ? *reinterpret_cast<const uint4 *>(vsrc + (size_t)r * v_row + c) : make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (isd) bd.store_T<true>(T16(O_DDTH), T16(O_DDTL), LB);
+        if (ist) {
+            bd.store_N(T16(O_TN), LB);
+            bd.store_T<true>(T16(O_TTH), T16(O_TTL), LB);
+        }
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
+            *reinterpret_cast<uint4 *>(T16(O_V) + r * LA + c) = vr[p];
+        }
+    }
     __syncthreads();
     {
         f4 tdw[4], tdd[4];
