@@ -1470,6 +1470,15 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     }
     mmab<C, 4, true>(dQ, T16(O_PNH), T16(O_PNL), LB, r0, T16(O_KT), nullptr, LB, 64 * ch);
     mmab<C, 4, true>(dK, T16(O_PTH), T16(O_PTL), LB, r0, T16(O_QT), nullptr, LB, 64 * ch);
+    // dQ is complete: its fp32 part row goes out now (16 lanes write 64 contiguous bytes) instead of staying live
+    float *const part_row = a.w.part + (((size_t)b * T + t0) * a.Hv + hv) * 2 * D;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = r0 + 4 * lg + e;
+            if (r < n) part_row[(size_t)r * a.Hv * 2 * D + 64 * ch + 16 * t + li] = dQ[t][e];
+        }
     __syncthreads();  // dPG and Q^T read (K^T, K, dDelta stay)
     // ---- S4a: P7 tdw = T^T dW, P8 tdd = T^T dDelta; dv
 #pragma unroll
@@ -1610,23 +1619,19 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     __syncthreads();
     chunk_dg_dbeta<NTB>(sE, sRow, sLast, sGam[C - 1], sScan, a, b, hv, t0, n);
     {
-        // fp32 part rows [64][2][D] (dq | dk), staged in the free arena, then 16-byte stores
+        // the dk half of the fp32 part rows, staged in the free arena, then 16-byte stores
         float *sp = reinterpret_cast<float *>(arena);
-        constexpr int LP = 2 * D + 4;
+        constexpr int LP = D + 4;
         static_assert(C * LP * 4 <= O_SM, "part staging below the pair matrix");
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
-                sp[r * LP + j] = dQ[t][e];
-                sp[r * LP + D + j] = dK[t][e];
-            }
+            for (int e = 0; e < 4; ++e) sp[(r0 + 4 * lg + e) * LP + 64 * ch + 16 * t + li] = dK[t][e];
         __syncthreads();
-        for (int i = tid; i < C * 2 * D / 4; i += NTB) {
-            const int r = i / (2 * D / 4), c4 = (i - r * (2 * D / 4)) * 4;
+        for (int i = tid; i < C * D / 4; i += NTB) {
+            const int r = i / (D / 4), c4 = (i - r * (D / 4)) * 4;
             if (r < n)
-                *reinterpret_cast<float4 *>(a.w.part + (((size_t)b * T + t0 + r) * a.Hv + hv) * 2 * D + c4) =
+                *reinterpret_cast<float4 *>(part_row + (size_t)r * a.Hv * 2 * D + D + c4) =
                     *reinterpret_cast<const float4 *>(sp + r * LP + c4);
         }
     }
