@@ -1412,10 +1412,30 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     for (int t = 0; t < 4; ++t) dQ[t] = dK[t] = dWr[t] = zero4();
     {
         f4 dp[2] = {zero4(), zero4()};
-        mmab<D, 4>(dQ, T16(O_DY), nullptr, LA, r0, T16(O_H), nullptr, LA, 64 * ch);
-        mmab<D, 4, true>(dK, T16(O_DLH), T16(O_DLL), LA, r0, T16(O_DHH), nullptr, LA, 64 * ch);
-        mmab<D, 2, false, true>(dp, T16(O_DY), nullptr, LA, r0, T16(O_DLH), T16(O_DLL), LA, 32 * ch);
-        mmab<D, 4>(dWr, T16(O_DD), nullptr, LA, r0, T16(O_H), nullptr, LA, 64 * ch);
+        // P1, P2, P3, P4 in one pass over k: each fragment read from LDS once per k-step (P1 and P2 share the h
+        // fragments, P1 and P4 the dY fragment)
+        const bfr *const tY = T16(O_DY), *const tD = T16(O_DD), *const tH = T16(O_H), *const tDH = T16(O_DHH);
+        const bfr *const tLh = T16(O_DLH), *const tLl = T16(O_DLL);
+#pragma unroll 2
+        for (int k0 = 0; k0 < D; k0 += 32) {
+            const bf8 ay = frag(tY, LA, r0, k0), ad = frag(tD, LA, r0, k0);
+            const bf8 ah = frag(tLh, LA, r0, k0), al = frag(tLl, LA, r0, k0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bf8 hb = frag(tH, LA, 64 * ch + 16 * t, k0);
+                dQ[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ay, hb, dQ[t], 0, 0, 0);
+                dWr[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ad, hb, dWr[t], 0, 0, 0);
+                const bf8 db = frag(tDH, LA, 64 * ch + 16 * t, k0);
+                dK[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, db, dK[t], 0, 0, 0);
+                dK[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, db, dK[t], 0, 0, 0);
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const bf8 xh = frag(tLh, LA, 32 * ch + 16 * t, k0), xl = frag(tLl, LA, 32 * ch + 16 * t, k0);
+                dp[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ay, xh, dp[t], 0, 0, 0);
+                dp[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ay, xl, dp[t], 0, 0, 0);
+            }
+        }
         __syncthreads();  // sGam / sRc ready; the S1 tiles read (dDelta stays)
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -1527,8 +1547,26 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
                 rowB[e] += sGam[r] * s4;
                 bnd[e] += bg * s4;
                 rowB[e] += bf2f(Vn[r * LA + j]) * tdd[t][e];
-                if (r < n) store_from_f32(a.dv, v0 + (size_t)r * v_row + j, sB[r] * tdd[t][e], a.grad_dt);
+                tdd[t][e] *= sB[r];  // dv
             }
+        if (a.grad_dt == DT_BF16) {
+            bfr *dvp = static_cast<bfr *>(a.dv) + v0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = r0 + 4 * lg + e;
+                    if (r < n) dvp[(size_t)r * v_row + 64 * ch + 16 * t + li] = (bfr)bfbits(tdd[t][e]);
+                }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = r0 + 4 * lg + e;
+                    if (r < n) store_from_f32(a.dv, v0 + (size_t)r * v_row + 64 * ch + 16 * t + li, tdd[t][e], a.grad_dt);
+                }
+        }
     }
     __syncthreads();  // dDelta^T, dW^T read (T^T hi, T, V, K, K^T, dDelta stay)
     // ---- S4b: P9 t1 = dDelta V^T, P10 t2 = dW K^T; dT = (t1 + t2 diag(gamma)) diag(beta)
