@@ -48,28 +48,41 @@ def kernel_model(name, B, T, Hk, Hv, D, in_b):
     tokh = B * T * Hv           # head-tokens
     C = CK_C
     cd, cc, dd = C * D, C * C, D * D
+    bf = in_b == 2  # the bf16 path keeps bf16 operand tiles (hi / lo where split) and bf16 states
     if name == "ck_prep":
-        return ch * 4 * 2 * cd * C, ch * (3 * cd * in_b + 2 * C * 4 + 2 * cd * 4 + 2 * cc * 4 + C * 8)
-    if name == "ck_fwd":
-        return ch * (3 * 2 * cd * D + 2 * cc * D), ch * (2 * cd * 4 + cc * 4 + 2 * cd * in_b + C * 8
-                                                         + dd * 4 + cd * 4 + cd * in_b)
-    if name == "ck_bwd_seq":
-        return ch * (3 * 2 * cd * D + 2 * cc * D), ch * (cc * 4 + cd * 4 + 3 * cd * in_b + C * 8
-                                                         + dd * 4 + cd * 4)
+        f = ch * 4 * 2 * cc * D
+        if bf:  # reads q, k, v, g, beta; writes G, T (fp32), P and P^T (hi / lo), W, -W^T, K~^T, Q^T, U (fp32)
+            return f, ch * (3 * cd * 2 + 2 * C * 4 + C * 8 + cc * 4 + 4 * cc * 2 + 4 * cd * 2 + cd * 4)
+        return f, ch * (3 * cd * in_b + 2 * C * 4 + 2 * cd * 4 + 2 * cc * 4 + C * 8)
+    if name in ("ck_fwd", "ck_bwd_seq"):
+        f = ch * (3 * 2 * cd * D + 2 * cc * D)
+        if name == "ck_fwd":
+            if bf:  # reads W, Q, K~^T, P (hi / lo), U, G; writes h (bf16), Delta (fp32), y
+                return f, ch * (3 * cd * 2 + 2 * cc * 2 + cd * 4 + C * 8 + dd * 2 + cd * 4 + cd * 2)
+            return f, ch * (2 * cd * 4 + cc * 4 + 2 * cd * in_b + C * 8 + dd * 4 + cd * 4 + cd * in_b)
+        if bf:  # reads K, P^T (hi / lo), Q^T, -W^T, dY, G; writes dh' (bf16), dDelta (fp32)
+            return f, ch * (cd * 2 + 2 * cc * 2 + 2 * cd * 2 + cd * 2 + C * 8 + dd * 2 + cd * 4)
+        return f, ch * (cc * 4 + cd * 4 + 3 * cd * in_b + C * 8 + dd * 4 + cd * 4)
     if name == "ck_bwd_local":
         f = ch * (3 * 2 * cd * D + 10 * 2 * cc * D + 2 * 2 * cc * C)
+        if bf:  # reads h, dh' (bf16), Delta, dDelta, T (fp32), P (hi / lo), G, q, k, v, dy, beta;
+            #     writes the fp32 dq | dk part, dv, dg, dbeta
+            return f, ch * (2 * dd * 2 + 2 * cd * 4 + cc * 4 + 2 * cc * 2 + C * 8 + 4 * cd * 2 + C * 4
+                            + 2 * cd * 4 + cd * 2 + 2 * C * 4)
         by = ch * (2 * dd * 4 + 2 * cd * 4 + 2 * cc * 4 + C * 8 + 4 * cd * in_b + C * 4
                    + 2 * cd * 4 + cd * in_b + 2 * C * 4)
         return f, by
+    if name == "reduce_qk":  # the fp32 per-value-head parts in, dq and dk out
+        return 0, B * T * (Hv * 2 * D * 4 + Hk * 2 * D * in_b)
     if name == "rec_fwd":
         return 7 * tokh * D * D, B * T * (2 * Hk * D * in_b + Hv * D * in_b * 2 + 2 * Hv * 4)
     if name == "rec_bwd":
         return 20 * tokh * D * D, B * T * (2 * Hk * D * in_b + 3 * Hv * D * in_b + 2 * Hv * 4)
     # block ops (per launch): conv over C = 2*Hk*D + Hv*D channels; the L2 norm runs once for q and once for k
     C = 2 * Hk * D + Hv * D
-    if name == "conv_fwd":
+    if name in ("conv_fwd", "conv_qkv_fwd"):
         return 0, B * T * C * 2 * in_b
-    if name == "conv_bwd":
+    if name in ("conv_bwd", "conv_qkv_bwd"):
         return 0, B * T * C * 3 * in_b
     if name == "l2norm_fwd":
         return 0, B * T * Hk * D * 2 * in_b
