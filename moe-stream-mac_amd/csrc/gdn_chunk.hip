@@ -1750,7 +1750,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
     __shared__ __align__(16) bfr sHl[VS * LH];
     __shared__ __align__(16) bfr sDh[VS * LDd];
     __shared__ __align__(16) bfr sDl[VS * LDd];
-    __shared__ float sGam[C];
+    __shared__ float sGamBuf[2][C];  // by chunk parity: read after the second barrier, rewritten two chunks later
 
     const SeqBlock sb = seq_block();
     const int i0 = sb.slice * VS, hv = sb.hv, b = sb.b;
@@ -1796,12 +1796,12 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
         }
         f.g = tid < C ? a.w.G[ci * C + tid] : 0.0;
     };
-    FwdFrags<DN> cur, nxt;
-    fetch(cur, 0);
-    for (int c = 0; c < a.NC; ++c) {
+    // The chunk loop is unrolled by two over ping-pong fragment buffers: no register copy of the prefetched
+    // fragments, so the wait for them sits at their first use, one chunk step after the loads were issued.
+    auto step = [&](const int c, FwdFrags<DN> &cur, FwdFrags<DN> &nxt) {
         const int t0 = c * C, n = min(C, T - t0);
         const size_t ci = head * a.NC + c;
-        // h -> LDS as the operand [i][j]; the chunk-entry state -> saved H ([j][i], fp32)
+        // h -> LDS as the operand [i][j]; the chunk-entry state -> saved H ([j][i], bf16)
 #pragma unroll
         for (int t = 0; t < NTN; ++t) {
             acc_T<true>(h[t], sHh, sHl, LH, 16 * w, 16 * t);
@@ -1810,6 +1810,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
                 reinterpret_cast<bfr *>(a.w.H)[ci * D * D + (size_t)(16 * w + 4 * lg + e) * D + i0 + 16 * t + li] =
                     (bfr)bfbits(h[t][e]);
         }
+        float *const sGam = sGamBuf[c & 1];
         if (tid < C) sGam[tid] = expf((float)cur.g);
         __syncthreads();
         if (c + 1 < a.NC) fetch(nxt, c + 1);
@@ -1857,7 +1858,12 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
 #pragma unroll
         for (int t = 0; t < NTN; ++t) h[t] *= gC;
         mmar<C, NTN>(h, cur.K, nullptr, sDh, nullptr, LDd, 0);
-        cur = nxt;
+    };
+    FwdFrags<DN> fa, fb;
+    fetch(fa, 0);
+    for (int c = 0; c < a.NC; c += 2) {
+        step(c, fa, fb);
+        if (c + 1 < a.NC) step(c + 1, fb, fa);
     }
     if (a.state_T) {
 #pragma unroll
@@ -2174,10 +2180,10 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
             }
         }
     };
-    BwdFrags cur, nxt;
+    // unrolled by two over ping-pong fragment buffers, as in ck_fwd_bf16_kernel; both steps of a pair are
+    // unconditional (a prefetch used only under a branch is sunk to its use by the compiler)
     YRaw yr[8];
-    fetch(cur, yr, a.NC - 1);
-    for (int c = a.NC - 1; c >= 0; --c) {
+    auto step = [&](const int c, BwdFrags &cur, BwdFrags &nxt) {
         const size_t ci = head * a.NC + c;
         // dh' -> LDS as the operand [i][j] (hi / lo) and -> the saved dH ([j][i], fp32)
 #pragma unroll
@@ -2255,8 +2261,15 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
         for (int t = 0; t < NTN; ++t) dh[t] *= gC;
         mmar<C, NTN, false, true>(dh, cur.QT, nullptr, sYgh, sYgl, LDd, 0);
         mmar<C, NTN>(dh, cur.WT, nullptr, sDd, nullptr, LDd, 0);
-        cur = nxt;
+    };
+    BwdFrags fa, fb;
+    fetch(fa, yr, a.NC - 1);
+    int c = a.NC - 1;
+    for (; c > 0; c -= 2) {
+        step(c, fa, fb);
+        step(c - 1, fb, fa);
     }
+    if (c == 0) step(0, fa, fb);
     if (a.dstate0) {
 #pragma unroll
         for (int t = 0; t < NTN; ++t)
