@@ -265,12 +265,23 @@ __device__ __forceinline__ SeqBlock seq_block() {
     return {L % S, (L / S) % Hv, L / (S * Hv)};
 }
 
-// (I + A)^-1 of a unit lower-triangular 64x64 matrix, A strictly lower in sA.  Diagonal 16x16 blocks by
-// column-parallel forward substitution, then off-diagonal blocks by distance:
-// T_ij = -T_ii sum_{u=j}^{i-1} A_iu T_uj.
+// acc += X(16x16) * Y(16x16) on v_mfma_f32_16x16x4_f32; X, Y in LDS with row strides ldx, ldy.  Accumulator element
+// e of lane l is (row 4*(l/16) + e, column l%16).
+__device__ __forceinline__ void blk16_mma(f4 &acc, const float *X, int ldx, const float *Y, int ldy) {
+    const int l = threadIdx.x & 63, li = l & 15, lg = l >> 4;
+#pragma unroll
+    for (int k0 = 0; k0 < 16; k0 += 4)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(X[li * ldx + k0 + lg], Y[(k0 + lg) * ldy + li], acc, 0, 0, 0);
+}
+
+// (I + A)^-1 of a unit lower-triangular 64x64 matrix, A strictly lower in sA, in fp32.  Diagonal 16x16 blocks by
+// column-parallel forward substitution; then the off-diagonal blocks by distance d = i - j on fp32 MFMA, one wave
+// per block: T_ij = -T_ii sum_{u=j}^{i-1} A_iu T_uj (the inner sum goes through a wave-private 16x16 scratch to
+// become an operand).  scratch holds 3 * 256 floats.  Ends with a barrier.
 template <int NTH>
 __device__ void unit_lower_inverse(const float *sA, float *sT, float *scratch) {
-    const int tid = threadIdx.x;
+    static_assert(NTH >= 3 * 64, "one wave per off-diagonal block of a round");
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     for (int i = tid; i < C * C; i += NTH) {
         const int r = i / C, s = i - r * C;
         if ((s >> 4) > (r >> 4)) sT[r * LDC + s] = 0.f;
@@ -290,20 +301,18 @@ __device__ void unit_lower_inverse(const float *sA, float *sT, float *scratch) {
     }
     __syncthreads();
     for (int d = 1; d < 4; ++d) {
-        const int nb = 4 - d;
-        for (int e = tid; e < nb * 256; e += NTH) {
-            const int blk = e >> 8, bi = blk + d, bj = blk, r = (e >> 4) & 15, cc = e & 15;
-            float x = 0.f;
-            for (int u = 16 * bj; u < 16 * bi; ++u) x = fmaf(sA[(16 * bi + r) * LDC + u], sT[u * LDC + 16 * bj + cc], x);
-            scratch[e] = x;
-        }
-        __syncthreads();
-        for (int e = tid; e < nb * 256; e += NTH) {
-            const int blk = e >> 8, bi = blk + d, bj = blk, r = (e >> 4) & 15, cc = e & 15;
-            float t = 0.f;
+        if (w < 4 - d) {
+            const int bj = w, bi = w + d;
+            f4 x = zero4();
+            for (int u = bj; u < bi; ++u) blk16_mma(x, sA + 16 * bi * LDC + 16 * u, LDC, sT + 16 * u * LDC + 16 * bj, LDC);
+            float *sc = scratch + 256 * w;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) t = fmaf(sT[(16 * bi + r) * LDC + 16 * bi + v], scratch[(blk << 8) + v * 16 + cc], t);
-            sT[(16 * bi + r) * LDC + 16 * bj + cc] = -t;
+            for (int e = 0; e < 4; ++e) sc[(4 * lg + e) * 16 + li] = x[e];
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the wave's scratch writes before its reads
+            f4 y = zero4();
+            blk16_mma(y, sT + 16 * bi * LDC + 16 * bi, LDC, sc, 16);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sT[(16 * bi + 4 * lg + e) * LDC + 16 * bj + li] = -y[e];
         }
         __syncthreads();
     }
