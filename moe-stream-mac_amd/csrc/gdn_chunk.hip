@@ -1908,7 +1908,7 @@ static_assert(C * LU * 4 + C * LK * 2 <= PR_T, "U and W staging below T");
 __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
     __shared__ __align__(16) unsigned char pa[PR_END];
     __shared__ float scratch[3 * 256];
-    __shared__ double sG[C];
+    __shared__ double sG[C], sG2[C];  // G and G log2(e)
     __shared__ float sB[C], sBG[C], sRc[C];
     bfr *const sK = reinterpret_cast<bfr *>(pa + PR_K);
     bfr *const sQ = reinterpret_cast<bfr *>(pa + PR_Q);
@@ -1952,6 +1952,7 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
         }
         sB[tid] = bt;
         sG[tid] = x;
+        sG2[tid] = x * 1.4426950408889634;  // log2(e): Gam_rs = 2^(G2_r - G2_s) on v_exp_f32
         sBG[tid] = bt * expf((float)x);
         sRc[tid] = expf((float)(__shfl(x, 63, 64) - x));  // gamma_C / gamma_r
     }
@@ -1979,8 +1980,12 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
                 make_uint4(pk(v[0][cc], v[1][cc]), pk(v[2][cc], v[3][cc]), pk(v[4][cc], v[5][cc]), pk(v[6][cc], v[7][cc]));
     }
     // K K^T (waves 0-3) -> A = strict_lower(diag(beta) K K^T * Gam); Q K^T (waves 4-7) -> P = lower(Q K^T * Gam)
+    // P hi / lo are staged in the T region (T is written only by the inverse, after the next barrier) and go out
+    // in 16-byte stores; tiles above the diagonal (16t > r) are zero without an exponential.
+    bfr *const sPb = reinterpret_cast<bfr *>(sT);  // [2][C][C]
+    static_assert(2 * C * C * 2 <= C * LDC * 4, "P hi / lo fit the T region");
     {
-        const int r0 = 16 * (w & 3);
+        const int rb = w & 3, r0 = 16 * rb;
         const bool isq = w >= 4;
         f4 acc[4];
 #pragma unroll
@@ -1992,13 +1997,13 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int r = r0 + 4 * lg + e, s2 = 16 * t + li;
-                const float gam = s2 <= r ? expf((float)(sG[r] - sG[s2])) : 0.f;
+                const float gam = t <= rb && s2 <= r ? __builtin_amdgcn_exp2f((float)(sG2[r] - sG2[s2])) : 0.f;
                 if (isq) {
                     const float pv = acc[t][e] * gam;
                     ph[e] = f32_to_bf16(pv);
                     pl[e] = f32_to_bf16(pv - bf16_to_f32(ph[e]));
-                    a.w.Pb[ci * 2 * C * C + r * C + s2] = ph[e];
-                    a.w.Pb[ci * 2 * C * C + C * C + r * C + s2] = pl[e];
+                    sPb[r * C + s2] = ph[e];
+                    sPb[C * C + r * C + s2] = pl[e];
                 } else {
                     sA[r * LDC + s2] = s2 < r ? sB[r] * acc[t][e] * gam : 0.f;
                 }
@@ -2012,7 +2017,7 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
             }
         }
     }
-    __syncthreads();  // Q read: its region takes V^T
+    __syncthreads();  // Q read: its region takes V^T; P staged
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
         uint32_t x[8];
@@ -2021,6 +2026,9 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
         *reinterpret_cast<uint4 *>(sVT + (vc + cc) * LT + 8 * vb) =
             make_uint4(x[0] | (x[1] << 16), x[2] | (x[3] << 16), x[4] | (x[5] << 16), x[6] | (x[7] << 16));
     }
+    for (int i = tid; i < 2 * C * C / 8; i += NTP)  // P hi / lo out
+        *reinterpret_cast<uint4 *>(a.w.Pb + ci * 2 * C * C + 8 * i) = *reinterpret_cast<const uint4 *>(sPb + 8 * i);
+    __syncthreads();  // P read out of the T region
     unit_lower_inverse<NTP>(sA, sT, scratch);  // ends with a barrier: A is dead
     // K^T [j][s] (exact) in the A region
     if (tid < (C / 8) * (D / 4)) {
