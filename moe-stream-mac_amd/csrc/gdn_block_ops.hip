@@ -16,7 +16,10 @@ namespace ops {
 
 constexpr int NT = 256;
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+// 1 / (1 + 2^(-x log2(e))) on v_exp_f32 and v_rcp_f32 (about 2 ulp); 0 and 1 at the ends, NaN stays NaN
+__device__ __forceinline__ float sigmoidf_(float x) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
 
 // softplus(t) = t > 20 ? t : log1p(exp(t))   (engine/include/gdn.h:23-24)
 __device__ __forceinline__ float softplus_(float t) { return t > 20.f ? t : log1pf(expf(t)); }
