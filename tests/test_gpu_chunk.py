@@ -166,6 +166,23 @@ def test_chunk_bf16_measured_layout_against_oracle(dev):
             assert e <= 1e-2, (b, hk, n, e)
 
 
+@pytest.mark.parametrize("Hk,Hv", [(3, 3), (1, 4)])
+def test_chunk_bf16_value_head_groups(dev, Hk, Hv):
+    """dq, dk summed over groups of one and of four value heads per key head (the bf16 backward runs once per
+    value head of a group and keeps a running sum) against the fp64 oracle."""
+    rep = Hv // Hk
+    d = _inputs(2, 150, Hk, Hv, seed=40 + Hv, s0_std=0.05)
+    bf = lambda x: torch.tensor(x).bfloat16().float().numpy()
+    d = dict(d, q=bf(d["q"]), k=bf(d["k"]), v=bf(d["v"]), dy=bf(d["dy"]))
+    print(f"chunk bf16 value-head groups Hk={Hk} Hv={Hv}", flush=True)
+    got = _gpu(d, dev, "chunk", dtype=torch.bfloat16)
+    for b in (0, 1):
+        for hk in range(Hk):
+            want = _oracle_group(d, hk, rep, b)
+            for n, a, w in zip(NAMES, _slice(got, hk, rep, b), want):
+                assert nerr(a, w) <= 1e-2, (b, hk, n, nerr(a, w))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_chunk_matches_recurrent_full_heads(dev, dtype):
     """B=1, T=1000, Hk=16, Hv=32: the two forms agree (recurrent form itself checked against the oracle)."""
