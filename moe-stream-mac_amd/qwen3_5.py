@@ -85,10 +85,12 @@ class GatedDeltaNet(nn.Module):
 
     def forward(self, x: Array, mask: Optional[Array] = None, state: Optional[Array] = None) -> Array:
         B, T, _ = x.shape
-        qkv = self.in_proj_qkv(x)
-        z = self.in_proj_z(x).reshape(B, T, self.Hv, self.Dv)
-        b = self.in_proj_b(x)
-        a = self.in_proj_a(x)
+        projs = (self.in_proj_qkv, self.in_proj_z, self.in_proj_b, self.in_proj_a)
+        if all(isinstance(m, LoRALinear) and m.base.bias is None for m in projs):
+            qkv, z, b, a = lora_group(x, projs)  # the four adapters share one pass over x
+        else:
+            qkv, z, b, a = (m(x) for m in projs)
+        z = z.reshape(B, T, self.Hv, self.Dv)
         if mask is not None:
             qkv = qkv * mask[..., None].to(qkv.dtype)
         # conv + SiLU, split, per-head q/k L2 norm (q scaled by Dk^-1/2): one fused kernel pair
@@ -184,6 +186,86 @@ class Model(nn.Module):
 Qwen3_5TextModel = TextModel
 
 
+def _mm(a: Array, b: Array, alpha: float = 1.0) -> Array:
+    """alpha * a @ b with alpha applied inside the GEMM (one rounding)."""
+    if alpha == 1.0:
+        return a @ b
+    return torch.addmm(a.new_empty(a.shape[0], b.shape[1]), a, b, beta=0, alpha=alpha)
+
+
+class _LoRAGroupFn(torch.autograd.Function):
+    """y_i = x W_i^T + s_i (x A_i^T) B_i^T for LoRA projections i that share the input x, with no pass of its own
+    over any [tokens, features] tensor: the adapters' A products come from one GEMM over x, each adapter GEMM
+    accumulates into its base output in place, and the backward accumulates dx in one buffer (beta = 1 GEMMs)
+    and takes every dA from one GEMM over x.  Arguments: x, the scales, then W_i, A_i, B_i per projection."""
+
+    @staticmethod
+    def forward(ctx, x: Array, scales: tuple, *wab: Array):
+        n = len(scales)
+        Ws, As, Bs = wab[0::3], wab[1::3], wab[2::3]
+        x2 = x.reshape(-1, x.shape[-1])
+        ranks = tuple(a.shape[0] for a in As)
+        a_cat = torch.cat(As) if n > 1 else As[0]
+        u = x2 @ a_cat.t()  # [tokens, sum of ranks]
+        outs, o = [], 0
+        for W, B, s, r in zip(Ws, Bs, scales, ranks):
+            y = x2 @ W.t()
+            y.addmm_(u[:, o:o + r], B.t(), alpha=s)
+            outs.append(y.view(*x.shape[:-1], W.shape[0]))
+            o += r
+        ctx.scales, ctx.ranks, ctx.xshape = scales, ranks, x.shape
+        ctx.save_for_backward(x2, u, a_cat, *Ws, *Bs)
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *dys: Array):
+        x2, u, a_cat, *rest = ctx.saved_tensors
+        n = len(ctx.scales)
+        Ws, Bs = rest[:n], rest[n:]
+        need = ctx.needs_input_grad  # x, scales, then W_i, A_i, B_i
+        grads: list = [None] * (3 * n)
+        dx, du_parts, o = None, [], 0
+        for i, (dy, W, B, s, r) in enumerate(zip(dys, Ws, Bs, ctx.scales, ctx.ranks)):
+            if dy is None:
+                du_parts.append(u.new_zeros(u.shape[0], r))
+                o += r
+                continue
+            dy2 = dy.reshape(-1, dy.shape[-1])
+            if need[0]:
+                if dx is None:
+                    dx = dy2 @ W
+                else:
+                    dx.addmm_(dy2, W)
+            if need[2 + 3 * i]:
+                grads[3 * i] = dy2.t() @ x2
+            if need[4 + 3 * i]:
+                grads[3 * i + 2] = _mm(dy2.t(), u[:, o:o + r], s)
+            du_parts.append(_mm(dy2, B, s))
+            o += r
+        du = torch.cat(du_parts, 1) if n > 1 else du_parts[0]  # s_i (dy_i B_i), [tokens, sum of ranks]
+        if need[0]:
+            if dx is None:
+                dx = du @ a_cat
+            else:
+                dx.addmm_(du, a_cat)
+        if any(need[3 + 3 * i] for i in range(n)):
+            da = du.t() @ x2
+            o = 0
+            for i, r in enumerate(ctx.ranks):
+                if need[3 + 3 * i]:
+                    grads[3 * i + 1] = da[o:o + r]
+                o += r
+        return (dx.view(ctx.xshape) if dx is not None else None, None, *grads)
+
+
+def lora_group(x: Array, mods) -> tuple:
+    """The outputs of LoRALinear modules without bias that share the input x (see _LoRAGroupFn)."""
+    wab = []
+    for m in mods:
+        wab += [m.base.weight.to(x.dtype), m.lora_a.to(x.dtype), m.lora_b.to(x.dtype)]
+    return _LoRAGroupFn.apply(x, tuple(float(m.scale) for m in mods), *wab)
+
+
 class LoRALinear(nn.Module):
     """y = W x + scale * B(A x) with A ~ N(0, std), B = 0; W frozen."""
 
@@ -200,8 +282,8 @@ class LoRALinear(nn.Module):
         return self.base.weight
 
     def forward(self, x: Array) -> Array:
-        # base GEMM, then the adapter GEMM accumulating into it with alpha = scale: no separate scale or add pass
-        # over the [tokens, out] output, forward or backward
+        if self.base.bias is None:
+            return lora_group(x, (self,))[0]
         u = F.linear(x, self.lora_a.to(x.dtype)).flatten(0, -2)
         y = torch.addmm(self.base(x).flatten(0, -2), u, self.lora_b.to(x.dtype).t(), alpha=self.scale)
         return y.view(*x.shape[:-1], y.shape[-1])
