@@ -218,13 +218,13 @@ __device__ __forceinline__ float gate_log(float g, int gate) {
 struct Bufs {
     float *H;    // [B][Hv][NC][D][D] chunk-entry states h = S^T, element (j, i) at [j][i] (bf16 bits in the bf16 path)
     double *G;   // [B][Hv][NC][C]
-    float *T;    // [B][Hv][NC][C][C]
+    float *T;    // [B][Hv][NC][C][C] (bf16 path: bf16 hi and lo planes [2][C][C] in the same space)
     float *P;    // [B][Hv][NC][C][C]
     float *W;    // [B][Hv][NC][C][D]
     float *U;    // [B][Hv][NC][C][D]
     float *Dl;   // [B][Hv][NC][C][D]  Delta
     float *dH;   // [B][Hv][NC][D][D]  adjoint of each chunk's exit state, [j][i] like H (bf16 in the bf16 path)
-    float *dDl;  // [B][Hv][NC][C][D]  dDelta
+    float *dDl;  // [B][Hv][NC][C][D]  dDelta (bf16 path: dDelta^T as bf16 hi and lo planes [2][D][C], same space)
     float *part; // [B][T][Hv][2][D]   dq | dk per value head
     // bf16 operand tiles written by ck_prep for the bf16 sequential kernels (raw bf16 bits, k contiguous)
     unsigned short *Wb;   // [B][Hv][NC][C][D]     W
@@ -1251,6 +1251,43 @@ struct Blk84 {
     }
 };
 
+// The same block of a tile stored as bf16 hi and lo planes (the lo plane `plane` elements after the hi one).
+struct Blk84Split {
+    uint2 hi[8], lo[8];
+    int rb, c0;
+    __device__ __forceinline__ void load(const bfr *src, size_t stride, size_t plane, int blk, int cols, int n) {
+        rb = blk / (cols / 4);
+        c0 = (blk - rb * (cols / 4)) * 4;
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+            const int r = rb * 8 + rr;
+            hi[rr] = r < n ? *reinterpret_cast<const uint2 *>(src + r * stride + c0) : make_uint2(0u, 0u);
+            lo[rr] = r < n ? *reinterpret_cast<const uint2 *>(src + plane + r * stride + c0) : make_uint2(0u, 0u);
+        }
+    }
+    static __device__ __forceinline__ uint32_t e16(const uint2 &v, int cc) {
+        const uint32_t w = cc < 2 ? v.x : v.y;
+        return cc & 1 ? w >> 16 : w & 0xffffu;
+    }
+    // dst[c][r] hi and lo: four stores of 8 consecutive rows each
+    __device__ __forceinline__ void store_T(bfr *dh, bfr *dl, int ldt) const {
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const uint4 h = make_uint4(e16(hi[0], cc) | (e16(hi[1], cc) << 16), e16(hi[2], cc) | (e16(hi[3], cc) << 16),
+                                       e16(hi[4], cc) | (e16(hi[5], cc) << 16), e16(hi[6], cc) | (e16(hi[7], cc) << 16));
+            const uint4 l = make_uint4(e16(lo[0], cc) | (e16(lo[1], cc) << 16), e16(lo[2], cc) | (e16(lo[3], cc) << 16),
+                                       e16(lo[4], cc) | (e16(lo[5], cc) << 16), e16(lo[6], cc) | (e16(lo[7], cc) << 16));
+            *reinterpret_cast<uint4 *>(dh + (c0 + cc) * ldt + rb * 8) = h;
+            *reinterpret_cast<uint4 *>(dl + (c0 + cc) * ldt + rb * 8) = l;
+        }
+    }
+    // dst[r][c] (hi): eight stores of 4 consecutive columns
+    __device__ __forceinline__ void store_N(bfr *nh, int ldn) const {
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) *reinterpret_cast<uint2 *>(nh + (rb * 8 + rr) * ldn + c0) = hi[rr];
+    }
+};
+
 // MFMA accumulator tile X (rows m0 + 4(l/16) + e, column n0 + l%16) -> LDS, transposed (dst[n][m]: four
 // consecutive bf16 per lane) or natural (dst[m][n]).
 template <bool SPLIT>
@@ -1328,8 +1365,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     const bfr *Hc = reinterpret_cast<const bfr *>(a.w.H) + ci * D * D;  // h = S^T, [j][i], bf16
     const bfr *dHc = reinterpret_cast<const bfr *>(a.w.dH) + ci * D * D;  // dh', [j][i], bf16
     const float *Dc = a.w.Dl + ci * C * D;
-    const float *dDc = a.w.dDl + ci * C * D;
-    const float *Tc = a.w.T + ci * C * C;
+    const bfr *dDc = reinterpret_cast<const bfr *>(a.w.dDl) + ci * 2 * D * C;  // dDelta^T hi, lo planes [i][r]
+    const bfr *Tc = reinterpret_cast<const bfr *>(a.w.T) + ci * 2 * C * C;      // T hi, lo planes [r][s]
     const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
     const size_t v0 = (((size_t)b * T + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
     const bfr *qsrc = static_cast<const bfr *>(a.q) + qk0, *ksrc = static_cast<const bfr *>(a.k) + qk0;
@@ -1354,7 +1391,12 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         constexpr int SPER = D * (D / 8) / NTB, NPER = C * (D / 8) / NTB;  // 8-element chunks per thread
         static_assert(SPER * NTB == D * (D / 8) && NPER * NTB == C * (D / 8), "even split");
         const bool yf32 = a.dy_dt == DT_F32;
-        uint4 hr[SPER], dhr[SPER], dl[2 * NPER], ddl[2 * NPER], yr[2 * NPER];
+        uint4 hr[SPER], dhr[SPER], dl[2 * NPER], yr[2 * NPER];
+        // dDelta (hi) into [r][i]: threads 0-255 each transpose one 8 (i) x 4 (r) block of the [i][r] plane
+        constexpr int NBDD = (D / 8) * (C / 4);
+        static_assert(NBDD <= NTB, "one dDelta block per thread");
+        Blk84<false> bdd;
+        if (tid < NBDD) bdd.load(dDc, C, tid, C, D);
 #pragma unroll
         for (int p = 0; p < SPER; ++p) {
             hr[p] = reinterpret_cast<const uint4 *>(Hc)[tid + p * NTB];
@@ -1365,8 +1407,6 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
             const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
             dl[2 * p] = *reinterpret_cast<const uint4 *>(Dc + r * D + c);
             dl[2 * p + 1] = *reinterpret_cast<const uint4 *>(Dc + r * D + c + 4);
-            ddl[2 * p] = *reinterpret_cast<const uint4 *>(dDc + r * D + c);
-            ddl[2 * p + 1] = *reinterpret_cast<const uint4 *>(dDc + r * D + c + 4);
             if (yf32) {
                 const float *ys = static_cast<const float *>(a.dy) + v0 + (size_t)r * v_row + c;
                 yr[2 * p] = r < n ? *reinterpret_cast<const uint4 *>(ys) : make_uint4(0u, 0u, 0u, 0u);
@@ -1376,6 +1416,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
                               : make_uint4(0u, 0u, 0u, 0u);
             }
         }
+        if (tid < NBDD) bdd.store_T<false>(T16(O_DD), nullptr, LA);
         bfr *const th = T16(O_H), *const tdh = T16(O_DHH);
 #pragma unroll
         for (int p = 0; p < SPER; ++p) {
@@ -1399,9 +1440,6 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
             pk2(f(a1.z), f(a1.w), h.w, l.w);
             *reinterpret_cast<uint4 *>(T16(O_DLH) + r * LA + c) = h;
             *reinterpret_cast<uint4 *>(T16(O_DLL) + r * LA + c) = l;
-            const uint4 b0 = ddl[2 * p], b1 = ddl[2 * p + 1];
-            *reinterpret_cast<uint4 *>(T16(O_DD) + r * LA + c) =
-                make_uint4(pk(f(b0.x), f(b0.y)), pk(f(b0.z), f(b0.w)), pk(f(b1.x), f(b1.y)), pk(f(b1.z), f(b1.w)));
             uint4 yv = yr[p];
             if (yf32) {
                 const uint4 y0 = yr[2 * p], y1 = yr[2 * p + 1];
@@ -1513,23 +1551,34 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc_T<false>(dWr[t], T16(O_DWT), nullptr, LB, r0, 64 * ch + 16 * t);
     {
-        // dDelta^T hi / lo (threads 0-255), T and T^T hi / lo (threads 256-383), V (all): one memory round trip
-        constexpr int NBD = (C / 8) * (D / 4), NBT = (C / 8) * (C / 4);
-        static_assert(NBD + NBT <= NTB && C * (D / 8) == 2 * NTB, "block split");
-        Blk84<true> bd;
-        const bool isd = tid < NBD, ist = tid >= NBD && tid < NBD + NBT;
-        if (isd) bd.load(dDc, D, tid, D, C);
-        if (ist) bd.load(Tc, C, tid - NBD, C, C);
+        // dDelta^T hi / lo (all threads, straight copies of the [i][r] planes), T and T^T hi / lo (threads
+        // 0-127), V (all): one memory round trip
+        constexpr int NBT = (C / 8) * (C / 4), NDP = D * C / 8 / NTB;  // 16-byte pieces per plane and thread
+        static_assert(NBT <= NTB && NDP * NTB * 8 == D * C && C * (D / 8) == 2 * NTB, "block split");
+        Blk84Split bd;
+        const bool ist = tid < NBT;
+        if (ist) bd.load(Tc, C, (size_t)C * C, tid, C, C);
+        uint4 ddh[NDP], ddlo[NDP];
+#pragma unroll
+        for (int p = 0; p < NDP; ++p) {
+            ddh[p] = reinterpret_cast<const uint4 *>(dDc)[tid + p * NTB];
+            ddlo[p] = reinterpret_cast<const uint4 *>(dDc + D * C)[tid + p * NTB];
+        }
         uint4 vr[2];
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
             vr[p] = r < n ? *reinterpret_cast<const uint4 *>(vsrc + (size_t)r * v_row + c) : make_uint4(0u, 0u, 0u, 0u);
         }
-        if (isd) bd.store_T<true>(T16(O_DDTH), T16(O_DDTL), LB);
+#pragma unroll
+        for (int p = 0; p < NDP; ++p) {
+            const int pc = tid + p * NTB, i = pc / (C / 8), r8 = (pc - i * (C / 8)) * 8;
+            *reinterpret_cast<uint4 *>(T16(O_DDTH) + i * LB + r8) = ddh[p];
+            *reinterpret_cast<uint4 *>(T16(O_DDTL) + i * LB + r8) = ddlo[p];
+        }
         if (ist) {
             bd.store_N(T16(O_TN), LB);
-            bd.store_T<true>(T16(O_TTH), T16(O_TTL), LB);
+            bd.store_T(T16(O_TTH), T16(O_TTL), LB);
         }
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
@@ -2111,9 +2160,15 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
         const int r = i / (D / 8), c8 = (i - r * (D / 8)) * 8;
         *reinterpret_cast<uint4 *>(a.w.Wb + ci * C * D + r * D + c8) = *reinterpret_cast<const uint4 *>(sW + r * LK + c8);
     }
-    for (int i = tid; i < C * C / 4; i += NTP) {  // T fp32
+    for (int i = tid; i < C * C / 4; i += NTP) {  // T as bf16 hi and lo planes
         const int r = i / (C / 4), c4 = (i - r * (C / 4)) * 4;
-        *reinterpret_cast<float4 *>(a.w.T + ci * C * C + r * C + c4) = *reinterpret_cast<const float4 *>(sT + r * LDC + c4);
+        const float4 x = *reinterpret_cast<const float4 *>(sT + r * LDC + c4);
+        uint2 h, l;
+        pk2(x.x, x.y, h.x, l.x);
+        pk2(x.z, x.w, h.y, l.y);
+        bfr *const tb = reinterpret_cast<bfr *>(a.w.T) + ci * 2 * C * C + r * C + c4;
+        *reinterpret_cast<uint2 *>(tb) = h;
+        *reinterpret_cast<uint2 *>(tb + C * C) = l;
     }
     if (tid < C) a.w.G[ci * C + tid] = sG[tid];
 }
@@ -2264,10 +2319,16 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
             for (int t = 0; t < DN; ++t) {
                 f4 dd;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = mrow + 4 * lg + e;
-                    dd[e] = kd[t][e] * sRc[r] + pd[t][e];
-                    a.w.dDl[ci * C * D + (size_t)r * D + i0 + 16 * (nt0 + t) + li] = dd[e];
+                for (int e = 0; e < 4; ++e) dd[e] = kd[t][e] * sRc[mrow + 4 * lg + e] + pd[t][e];
+                {
+                    // saved dDelta^T: bf16 hi and lo planes [i][r], this lane's four rows in one 8-byte store each
+                    uint2 hb, lb;
+                    pk2(dd[0], dd[1], hb.x, lb.x);
+                    pk2(dd[2], dd[3], hb.y, lb.y);
+                    bfr *const db = reinterpret_cast<bfr *>(a.w.dDl) + ci * 2 * D * C +
+                                    (size_t)(i0 + 16 * (nt0 + t) + li) * C + mrow + 4 * lg;
+                    *reinterpret_cast<uint2 *>(db) = hb;
+                    *reinterpret_cast<uint2 *>(db + D * C) = lb;
                 }
                 acc_T<false>(dd, sDd, nullptr, LDd, mrow, 16 * (nt0 + t));
             }
