@@ -2198,7 +2198,8 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
     __shared__ __align__(16) bfr sY[VS * LDd];    // dY^T [i][s]
     __shared__ __align__(16) bfr sYgh[VS * LDd];  // (diag(gamma) dY)^T hi
     __shared__ __align__(16) bfr sYgl[VS * LDd];  // (diag(gamma) dY)^T lo
-    __shared__ __align__(16) bfr sDd[VS * LDd];   // dDelta^T [i][r]
+    __shared__ __align__(16) bfr sDd[VS * LDd];   // dDelta^T [i][r], hi
+    __shared__ __align__(16) bfr sDdl[VS * LDd];  // dDelta^T lo
     __shared__ float sGam[C], sRc[C];
 
     const SeqBlock sb = seq_block();
@@ -2320,20 +2321,19 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
                 f4 dd;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) dd[e] = kd[t][e] * sRc[mrow + 4 * lg + e] + pd[t][e];
-                {
-                    // saved dDelta^T: bf16 hi and lo planes [i][r], this lane's four rows in one 8-byte store each
-                    uint2 hb, lb;
-                    pk2(dd[0], dd[1], hb.x, lb.x);
-                    pk2(dd[2], dd[3], hb.y, lb.y);
-                    bfr *const db = reinterpret_cast<bfr *>(a.w.dDl) + ci * 2 * D * C +
-                                    (size_t)(i0 + 16 * (nt0 + t) + li) * C + mrow + 4 * lg;
-                    *reinterpret_cast<uint2 *>(db) = hb;
-                    *reinterpret_cast<uint2 *>(db + D * C) = lb;
-                }
-                acc_T<false>(dd, sDd, nullptr, LDd, mrow, 16 * (nt0 + t));
+                acc_T<true>(dd, sDd, sDdl, LDd, mrow, 16 * (nt0 + t));
             }
         }
         __syncthreads();
+        {
+            // saved dDelta^T: the slice's rows of the bf16 hi and lo planes [i][r], in 16-byte pieces
+            bfr *const db = reinterpret_cast<bfr *>(a.w.dDl) + ci * 2 * D * C + (size_t)i0 * C;
+            for (int p = tid; p < VS * C / 8; p += NTS) {
+                const int i = p / (C / 8), r8 = (p - i * (C / 8)) * 8;
+                *reinterpret_cast<uint4 *>(db + i * C + r8) = *reinterpret_cast<const uint4 *>(sDd + i * LDd + r8);
+                *reinterpret_cast<uint4 *>(db + D * C + i * C + r8) = *reinterpret_cast<const uint4 *>(sDdl + i * LDd + r8);
+            }
+        }
         // dh = gamma_C dh' + Q^T diag(gamma) dY + (-W^T) dDelta
 #pragma unroll
         for (int t = 0; t < NTN; ++t) dh[t] *= gC;
