@@ -60,12 +60,12 @@ def kernel_model(name, B, T, Hk, Hv, D, in_b):
             if bf:  # reads W, Q, K~^T, P (hi / lo), U, G; writes h (bf16), Delta (fp32), y
                 return f, ch * (3 * cd * 2 + 2 * cc * 2 + cd * 4 + C * 8 + dd * 2 + cd * 4 + cd * 2)
             return f, ch * (2 * cd * 4 + cc * 4 + 2 * cd * in_b + C * 8 + dd * 4 + cd * 4 + cd * in_b)
-        if bf:  # reads K, P^T (hi / lo), Q^T, -W^T, dY, G; writes dh' (bf16), dDelta (fp32)
+        if bf:  # reads K, P^T (hi / lo), Q^T, -W^T, dY, G; writes dh' (bf16), dDelta (bf16 hi / lo planes)
             return f, ch * (cd * 2 + 2 * cc * 2 + 2 * cd * 2 + cd * 2 + C * 8 + dd * 2 + cd * 4)
         return f, ch * (cc * 4 + cd * 4 + 3 * cd * in_b + C * 8 + dd * 4 + cd * 4)
     if name == "ck_bwd_local":
         f = ch * (3 * 2 * cd * D + 10 * 2 * cc * D + 2 * 2 * cc * C)
-        if bf:  # reads h, dh' (bf16), Delta, dDelta, T (fp32), P (hi / lo), G, q, k, v, dy, beta;
+        if bf:  # reads h, dh' (bf16), Delta (fp32), dDelta, T (bf16 hi / lo), P (hi / lo), G, q, k, v, dy, beta;
             #     writes the fp32 dq | dk part, dv, dg, dbeta
             return f, ch * (2 * dd * 2 + 2 * cd * 4 + cc * 4 + 2 * cc * 2 + C * 8 + 4 * cd * 2 + C * 4
                             + 2 * cd * 4 + cd * 2 + 2 * C * 4)
