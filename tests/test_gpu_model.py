@@ -157,3 +157,26 @@ def test_memory_probe_reports_backward_peak_per_token(dev, capsys):
     m = re.search(r"T=1024 impl=chunked: backward_peak=(\d+) MiB MiB_per_token=([0-9.]+)", out)
     assert m, out
     assert 0.0 < float(m.group(2)) < 2.0, out
+
+
+@pytest.mark.parametrize("env", [("1", "0", "0"), ("0", "1", "1")])
+def test_lora_step_driver(dev, monkeypatch, capsys, env):
+    """The counterpart of tools/ft_lora_lowmem.py installs what GDN_CHECKPOINT / GDN_VJP / FROZEN_GDN_KERNEL ask
+    for and runs AdamW LoRA steps through the chunked form (head dim 128) with finite losses, printing the
+    reference's timing line and the peak memory."""
+    import math
+    import re
+    import lora_step
+    _patchable(monkeypatch)
+    names = ("GDN_CHECKPOINT", "GDN_VJP", "FROZEN_GDN_KERNEL")
+    for name, value in zip(names, env):
+        monkeypatch.setenv(name, value)
+    print(f"lora_step env {dict(zip(names, env))}", flush=True)
+    assert lora_step.main(["--steps", "2", "--tokens", "256", "--hidden", "128", "--layers", "4",
+                           "--lora-layers", "2", "--bf16"]) == 0
+    out = capsys.readouterr().out
+    want = [m for m, v in zip(("gdn_checkpoint", "gdn_vjp", "frozen_gdn"), env) if v == "1"]
+    assert f"installed: {', '.join(want)};" in out, out
+    losses = [float(x) for x in re.findall(r"step \d+: loss ([0-9.]+)", out)]
+    assert len(losses) == 2 and all(math.isfinite(v) for v in losses), out
+    assert "training_steps=2" in out and "peak_memory_gib=" in out, out
