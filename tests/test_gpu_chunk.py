@@ -194,6 +194,20 @@ def test_chunk_matches_recurrent_full_heads(dev, dtype):
         assert nerr(x, y) <= tol, (n, nerr(x, y))
 
 
+def test_headline_config_chunk_matches_recurrent(dev):
+    """The measured workload itself, B=4, T=4096, Hk=16, Hv=32, bf16 q/k/v/dO, fp32 state: every output of the
+    chunked form against the recurrent form (each form checked against the fp64 oracle at smaller sizes),
+    normalised error <= 1e-2."""
+    d = _inputs(4, 4096, 16, 32, seed=5, s0_std=0.02)
+    print("headline config B=4 T=4096 chunk vs recurrent (bf16)", flush=True)
+    a = _gpu(d, dev, "chunk", dtype=torch.bfloat16)
+    b = _gpu(d, dev, "recurrent", dtype=torch.bfloat16)
+    errs = {n: nerr(x, y) for n, x, y in zip(NAMES, a, b)}
+    print({n: f"{e:.1e}" for n, e in errs.items()}, flush=True)
+    for n, e in errs.items():
+        assert e <= 1e-2, (n, e)
+
+
 @pytest.mark.parametrize("B", [2, 4])
 def test_chunk_matches_recurrent_wide_slices(dev, B):
     """B*Hv = 64 / 128 heads select value slices of 32 / 64 in the sequential kernels."""
