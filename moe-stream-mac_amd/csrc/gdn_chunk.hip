@@ -1200,54 +1200,36 @@ __device__ __forceinline__ float stage_states(bfr *hh, bfr *dhh, const bfr *H, c
     return dot;
 }
 
-// An 8-row x 4-column block of a global [ROWS][COLS] tile (rows >= n read as zero), kept as the raw loads so that
-// a phase can issue all of its loads before the first LDS store.  fp32 (F32) or bf16 source.
-template <bool F32>
+// An 8-row x 4-column block of a global bf16 [ROWS][COLS] tile (rows >= n read as zero), kept as the raw loads
+// so that a phase can issue all of its loads before the first LDS store.
 struct Blk84 {
-    typename std::conditional<F32, float4, uint2>::type raw[8];
+    uint2 raw[8];
     int rb, c0;
-    __device__ __forceinline__ void load(const void *src, size_t stride, int blk, int cols, int n) {
+    __device__ __forceinline__ void load(const bfr *src, size_t stride, int blk, int cols, int n) {
         rb = blk / (cols / 4);
         c0 = (blk - rb * (cols / 4)) * 4;
 #pragma unroll
         for (int rr = 0; rr < 8; ++rr) {
             const int r = rb * 8 + rr;
-            if constexpr (F32)
-                raw[rr] = r < n ? *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + r * stride + c0)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
-            else
-                raw[rr] = r < n ? *reinterpret_cast<const uint2 *>(static_cast<const bfr *>(src) + r * stride + c0)
-                                : make_uint2(0u, 0u);
+            raw[rr] = r < n ? *reinterpret_cast<const uint2 *>(src + r * stride + c0) : make_uint2(0u, 0u);
         }
     }
-    __device__ __forceinline__ float val(int rr, int cc) const {
-        if constexpr (F32) {
-            return cc == 0 ? raw[rr].x : cc == 1 ? raw[rr].y : cc == 2 ? raw[rr].z : raw[rr].w;
-        } else {
-            const uint32_t w = cc < 2 ? raw[rr].x : raw[rr].y;
-            return bf2f(cc & 1 ? w >> 16 : w & 0xffffu);
-        }
+    __device__ __forceinline__ uint32_t e16(int rr, int cc) const {
+        const uint32_t w = cc < 2 ? raw[rr].x : raw[rr].y;
+        return cc & 1 ? w >> 16 : w & 0xffffu;
     }
-    // dst[c][r]: four stores of 8 consecutive rows (hi, and lo when SPLIT)
-    template <bool SPLIT>
-    __device__ __forceinline__ void store_T(bfr *hi, bfr *lo, int ldt) const {
+    // dst[c][r]: four stores of 8 consecutive rows
+    __device__ __forceinline__ void store_T(bfr *dst, int ldt) const {
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-            uint4 h, l;
-            pk2(val(0, cc), val(1, cc), h.x, l.x);
-            pk2(val(2, cc), val(3, cc), h.y, l.y);
-            pk2(val(4, cc), val(5, cc), h.z, l.z);
-            pk2(val(6, cc), val(7, cc), h.w, l.w);
-            *reinterpret_cast<uint4 *>(hi + (c0 + cc) * ldt + rb * 8) = h;
-            if constexpr (SPLIT) *reinterpret_cast<uint4 *>(lo + (c0 + cc) * ldt + rb * 8) = l;
-        }
+        for (int cc = 0; cc < 4; ++cc)
+            *reinterpret_cast<uint4 *>(dst + (c0 + cc) * ldt + rb * 8) =
+                make_uint4(e16(0, cc) | (e16(1, cc) << 16), e16(2, cc) | (e16(3, cc) << 16),
+                           e16(4, cc) | (e16(5, cc) << 16), e16(6, cc) | (e16(7, cc) << 16));
     }
-    // dst[r][c] (hi): eight stores of 4 consecutive columns
+    // dst[r][c]: eight stores of 4 consecutive columns
     __device__ __forceinline__ void store_N(bfr *nh, int ldn) const {
 #pragma unroll
-        for (int rr = 0; rr < 8; ++rr)
-            *reinterpret_cast<uint2 *>(nh + (rb * 8 + rr) * ldn + c0) =
-                make_uint2(pk(val(rr, 0), val(rr, 1)), pk(val(rr, 2), val(rr, 3)));
+        for (int rr = 0; rr < 8; ++rr) *reinterpret_cast<uint2 *>(nh + (rb * 8 + rr) * ldn + c0) = raw[rr];
     }
 };
 
@@ -1395,7 +1377,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         // dDelta (hi) into [r][i]: threads 0-255 each transpose one 8 (i) x 4 (r) block of the [i][r] plane
         constexpr int NBDD = (D / 8) * (C / 4);
         static_assert(NBDD <= NTB, "one dDelta block per thread");
-        Blk84<false> bdd;
+        Blk84 bdd;
         if (tid < NBDD) bdd.load(dDc, C, tid, C, D);
 #pragma unroll
         for (int p = 0; p < SPER; ++p) {
@@ -1416,7 +1398,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
                               : make_uint4(0u, 0u, 0u, 0u);
             }
         }
-        if (tid < NBDD) bdd.store_T<false>(T16(O_DD), nullptr, LA);
+        if (tid < NBDD) bdd.store_T(T16(O_DD), LA);
         bfr *const th = T16(O_H), *const tdh = T16(O_DHH);
 #pragma unroll
         for (int p = 0; p < SPER; ++p) {
@@ -1514,13 +1496,13 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         constexpr int NBQ = (C / 8) * (D / 4);
         static_assert(2 * NBQ == NTB, "one block per thread");
         const bool isk = tid >= NBQ;
-        Blk84<false> bk;
+        Blk84 bk;
         bk.load(isk ? ksrc : qsrc, qk_row, isk ? tid - NBQ : tid, D, n);
         if (isk) {
             bk.store_N(T16(O_K), LA);
-            bk.store_T<false>(T16(O_KT), nullptr, LB);
+            bk.store_T(T16(O_KT), LB);
         } else {
-            bk.store_T<false>(T16(O_QT), nullptr, LB);
+            bk.store_T(T16(O_QT), LB);
         }
     }
     __syncthreads();
