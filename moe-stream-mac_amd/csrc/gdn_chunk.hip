@@ -1480,7 +1480,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
                 const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
                 const float pv = s2 <= r ? dp[t][e] : 0.f;
                 Ep[t][e] = s2 < r ? pv * pP[t][e] : 0.f;
-                dPG[t][e] = s2 <= r ? pv * expf((float)(sG[r] - sG[s2])) : 0.f;
+                dPG[t][e] = s2 <= r ? pv * __builtin_amdgcn_exp2f((float)(sG[r] - sG[s2]) * 1.4426950408889634f) : 0.f;
             }
     }
 #pragma unroll
@@ -1647,7 +1647,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
-                const float gam = s2 < r ? expf((float)(sG[r] - sG[s2])) : 0.f;
+                const float gam = s2 < r ? __builtin_amdgcn_exp2f((float)(sG[r] - sG[s2]) * 1.4426950408889634f) : 0.f;
                 const float dav = s2 < r ? -da[t][e] : 0.f;
                 const float kg = kk[t][e] * gam;
                 rowB[e] += dav * kg;
