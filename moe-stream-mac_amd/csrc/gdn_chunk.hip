@@ -763,7 +763,7 @@ constexpr int NTB = 512;  // ck_bwd_local: 8 waves; waves w and w+4 share the 16
 __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     __shared__ __align__(16) float R1[D * LD];       // h / dh' ([j][i]); then K at R1, Q / dW at R1 + C*LD
     __shared__ __align__(16) float R2[C * LD];       // dY, then dDelta, then the pair matrix E
-    __shared__ __align__(16) float RX[2 * C * LDC];  // V ([C][LD] fits), then R3 = RX (Y1), R4 = RX + C*LDC
+    __shared__ __align__(16) float RX[2 * C * LDC];  // dDelta, Delta; V ([C][LD] fits); R3 = RX (Y1), R4 = RX + C*LDC
     __shared__ __align__(16) float R5[C * LDC];      // T
     __shared__ double sG[C];
     __shared__ float sGam[C], sRc[C], sB[C], sScan[2][C];
@@ -779,6 +779,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     float *const sQm = R1 + C * LD;
     float *const R3 = RX;
     float *const R4 = RX + C * LDC;
+    static_assert(C * LD <= 2 * C * LDC, "a [C][D] tile fits RX");
     const float *Hc = a.w.H + ci * D * D;
     const float *dHc = a.w.dH + ci * D * D;
     const float *Dc = a.w.Dl + ci * C * D;
@@ -799,6 +800,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     }
     load_tile<D, D, NTB>(R1, LD, Hc, D, D, DT_F32);
     load_tile<C, D, NTB>(R2, LD, elem_ptr(a.dy, v0, a.dy_dt), v_row, n, a.dy_dt);
+    load_tile<C, D, NTB>(RX, LD, dDc, D, C, DT_F32);  // dDelta, an MFMA operand of phase 1 (RX is free until V)
     __syncthreads();
     if (tid < C) {
         sGam[tid] = expf((float)sG[tid]);
@@ -831,7 +833,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) dQ[t] = dw[t] = zero4();
         mma_strip<D, 4>(dQ, R2 + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
-        mma_strip<D, 4>(dw, dDc + r0 * D, D, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<D, 4>(dw, RX + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -844,10 +846,11 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     __syncthreads();
     // ---- phase 2: dK = diag(gamma_C/gamma) Delta dh'^T ; dP = lower(dY Delta^T)
     load_tile<D, D, NTB>(R1, LD, dHc, D, D, DT_F32);
+    load_tile<C, D, NTB>(RX, LD, Dc, D, C, DT_F32);  // Delta in place of dDelta (phase 1 is done)
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < 4; ++t) dK[t] = zero4();
-    mma_strip<D, 4>(dK, Dc + r0 * D, D, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
+    mma_strip<D, 4>(dK, RX + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -855,7 +858,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     f4 dPG[2], Ep[2];
     {
         f4 dp[2] = {zero4(), zero4()};
-        mma_strip<D, 2>(dp, R2 + r0 * LD, LD, 1, Dc + 32 * ch * D, 1, D, 16 * D);
+        mma_strip<D, 2>(dp, R2 + r0 * LD, LD, 1, RX + 32 * ch * LD, 1, LD, 16 * LD);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
