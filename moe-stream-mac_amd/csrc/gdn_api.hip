@@ -336,7 +336,7 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
             launch_chunk_stage(cc, "local", st);
         }
         rc = check_launch(st, "gdn_bwd(ck_bwd_local)");
-        if (rc) return rc;
+        if (rc || !chunk_has_reduce(in_dtype)) return rc;
         {
             Timed tm("reduce_qk", st);
             launch_chunk_stage(cc, "reduce", st);

@@ -681,9 +681,9 @@ __device__ __forceinline__ float wave_sum(float x) {
 // column sums in 8-lane groups, and the Eb suffix / T2 prefix as wave-0 shuffle scans.  Every thread takes part.
 template <int NTH>
 __device__ __forceinline__ void chunk_dg_dbeta(float *sE, const float (*sRow)[2][C], const float *sLast, float last_scale,
-                                               float (*sScan)[C], const Args &a, int b, int hv, int t0, int n) {
+                                               float (*sScan)[C], const Args &a, int b, int hv, int t0, int n,
+                                               int tid) {
     static_assert(NTH == C * 8, "eight threads per row / column");
-    const int tid = threadIdx.x;
     const size_t g0 = ((size_t)b * a.T + t0) * a.Hv + hv;
     if (tid < C) {
         const int r = tid;
@@ -991,7 +991,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
         }
     }
     __syncthreads();
-    chunk_dg_dbeta<NTB>(sE, sRow, sLast, 1.f, sScan, a, b, hv, t0, n);
+    chunk_dg_dbeta<NTB>(sE, sRow, sLast, 1.f, sScan, a, b, hv, t0, n, tid);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -1026,8 +1026,7 @@ __device__ __forceinline__ void pk2(float a, float b, uint32_t &h, uint32_t &lo)
     lo = bfbits(a - bf2f(ha)) | (bfbits(b - bf2f(hb)) << 16);
 }
 
-__device__ __forceinline__ bf8 frag(const bfr *t, int ld, int m0, int k0) {
-    const int l = threadIdx.x & 63;
+__device__ __forceinline__ bf8 frag(const bfr *t, int ld, int m0, int k0, int l = threadIdx.x & 63) {
     return *reinterpret_cast<const bf8 *>(t + (m0 + (l & 15)) * ld + k0 + 8 * (l >> 4));
 }
 
@@ -1035,19 +1034,19 @@ __device__ __forceinline__ bf8 frag(const bfr *t, int ld, int m0, int k0) {
 // parts of a split operand.
 template <int K, int NTL, bool SA = false, bool SB = false>
 __device__ __forceinline__ void mmab(f4 (&acc)[NTL], const bfr *ah, const bfr *al, int lda, int m0, const bfr *bh,
-                                     const bfr *bl, int ldb, int n0) {
+                                     const bfr *bl, int ldb, int n0, int l = threadIdx.x & 63) {
 #pragma unroll 2
     for (int k0 = 0; k0 < K; k0 += 32) {
-        const bf8 x = frag(ah, lda, m0, k0);
+        const bf8 x = frag(ah, lda, m0, k0, l);
         bf8 x2;
-        if constexpr (SA) x2 = frag(al, lda, m0, k0);
+        if constexpr (SA) x2 = frag(al, lda, m0, k0, l);
 #pragma unroll
         for (int t = 0; t < NTL; ++t) {
-            const bf8 y = frag(bh, ldb, n0 + 16 * t, k0);
+            const bf8 y = frag(bh, ldb, n0 + 16 * t, k0, l);
             acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, acc[t], 0, 0, 0);
             if constexpr (SA) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x2, y, acc[t], 0, 0, 0);
             if constexpr (SB) {
-                const bf8 y2 = frag(bl, ldb, n0 + 16 * t, k0);
+                const bf8 y2 = frag(bl, ldb, n0 + 16 * t, k0, l);
                 acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y2, acc[t], 0, 0, 0);
             }
         }
@@ -1276,8 +1275,7 @@ struct Blk84Split {
 // MFMA accumulator tile X (rows m0 + 4(l/16) + e, column n0 + l%16) -> LDS, transposed (dst[n][m]: four
 // consecutive bf16 per lane) or natural (dst[m][n]).
 template <bool SPLIT>
-__device__ __forceinline__ void acc_T(const f4 &x, bfr *hi, bfr *lo, int ld, int m0, int n0) {
-    const int l = threadIdx.x & 63;
+__device__ __forceinline__ void acc_T(const f4 &x, bfr *hi, bfr *lo, int ld, int m0, int n0, int l = threadIdx.x & 63) {
     const int o = (n0 + (l & 15)) * ld + m0 + 4 * (l >> 4);
     uint2 h, lw;
     pk2(x[0], x[1], h.x, lw.x);
@@ -1286,8 +1284,7 @@ __device__ __forceinline__ void acc_T(const f4 &x, bfr *hi, bfr *lo, int ld, int
     if constexpr (SPLIT) *reinterpret_cast<uint2 *>(lo + o) = lw;
 }
 template <bool SPLIT>
-__device__ __forceinline__ void acc_N(const f4 &x, bfr *hi, bfr *lo, int ld, int m0, int n0) {
-    const int l = threadIdx.x & 63;
+__device__ __forceinline__ void acc_N(const f4 &x, bfr *hi, bfr *lo, int ld, int m0, int n0, int l = threadIdx.x & 63) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int o = (m0 + 4 * (l >> 4) + e) * ld + n0 + (l & 15);
@@ -1334,7 +1331,10 @@ static_assert(O_V + SZ_A <= ARENA, "arena");
 static_assert(O_Y1T + SZ_D <= O_TTH, "S5 tiles stay clear of T^T");
 static_assert(ARENA <= 157 * 1024, "arena size");
 
-__global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
+// One value head hv = hk * rep + rr of key head hk.  dq | dk of the key head: the value heads' fp32 parts are summed
+// in order (rr = 0, 1, ...) in the part rows of the key head, each thread reading back only the elements it wrote
+// itself, and the last value head writes dq and dk in the gradient dtype.
+__device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk, int b, int rr, int rep) {
     __shared__ __align__(16) unsigned char arena[ARENA];
     __shared__ double sG[C];
     __shared__ float sGam[C], sRc[C], sB[C], sScan[2][C];
@@ -1342,10 +1342,18 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     __shared__ float sLast[8];
     auto T16 = [&](int off) { return reinterpret_cast<bfr *>(arena + off); };
 
-    const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
+    const bool first = rr == 0, last = rr == rep - 1;
+    const int hv = hk * rep + rr;
+    const int T = a.T, t0 = c * C, n = min(C, T - t0);
+    float *const part_row = a.w.part + (((size_t)b * T + t0) * a.Hk + hk) * 2 * D;
+    const size_t part_rs = (size_t)a.Hk * 2 * D;
+    const size_t qk_out = (((size_t)b * T + t0) * a.Hk + hk) * D;
+    // an opaque lane index per value head: the lane-dependent addresses are formed inside the head instead of
+    // being hoisted out of the caller's loop and held in registers across the whole head
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int r0 = 16 * (w & 3), ch = w >> 2;
-    const int T = a.T, hk = hv / (a.Hv / a.Hk), t0 = c * C, n = min(C, T - t0);
     const size_t ci = chunk_index(a, b, hv, c);
     const bfr *Hc = reinterpret_cast<const bfr *>(a.w.H) + ci * D * D;  // h = S^T, [j][i], bf16
     const bfr *dHc = reinterpret_cast<const bfr *>(a.w.dH) + ci * D * D;  // dh', [j][i], bf16
@@ -1362,14 +1370,6 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         sG[tid] = a.w.G[ci * C + tid];
         sB[tid] = tid < n ? a.beta[((size_t)b * T + t0 + tid) * a.Hv + hv] : 0.f;
     }
-    float pP[2][4];  // P at this lane's dp positions (loads issued first: used after S1)
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const size_t pi = ci * 2 * C * C + (r0 + 4 * lg + e) * C + 32 * ch + 16 * t + li;
-            pP[t][e] = bf16_to_f32(a.w.Pb[pi]) + bf16_to_f32(a.w.Pb[pi + C * C]);
-        }
     // S1 staging: every global load of the phase is issued before the first LDS store
     float lastp = 0.f;  // <dh', h>, the pair (C-1, chunk start)
     {
@@ -1450,20 +1450,20 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         const bfr *const tLh = T16(O_DLH), *const tLl = T16(O_DLL);
 #pragma unroll 2
         for (int k0 = 0; k0 < D; k0 += 32) {
-            const bf8 ay = frag(tY, LA, r0, k0), ad = frag(tD, LA, r0, k0);
-            const bf8 ah = frag(tLh, LA, r0, k0), al = frag(tLl, LA, r0, k0);
+            const bf8 ay = frag(tY, LA, r0, k0, l), ad = frag(tD, LA, r0, k0, l);
+            const bf8 ah = frag(tLh, LA, r0, k0, l), al = frag(tLl, LA, r0, k0, l);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const bf8 hb = frag(tH, LA, 64 * ch + 16 * t, k0);
+                const bf8 hb = frag(tH, LA, 64 * ch + 16 * t, k0, l);
                 dQ[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ay, hb, dQ[t], 0, 0, 0);
                 dWr[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ad, hb, dWr[t], 0, 0, 0);
-                const bf8 db = frag(tDH, LA, 64 * ch + 16 * t, k0);
+                const bf8 db = frag(tDH, LA, 64 * ch + 16 * t, k0, l);
                 dK[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, db, dK[t], 0, 0, 0);
                 dK[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, db, dK[t], 0, 0, 0);
             }
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                const bf8 xh = frag(tLh, LA, 32 * ch + 16 * t, k0), xl = frag(tLl, LA, 32 * ch + 16 * t, k0);
+                const bf8 xh = frag(tLh, LA, 32 * ch + 16 * t, k0, l), xl = frag(tLl, LA, 32 * ch + 16 * t, k0, l);
                 dp[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ay, xh, dp[t], 0, 0, 0);
                 dp[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ay, xl, dp[t], 0, 0, 0);
             }
@@ -1482,7 +1482,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
             for (int e = 0; e < 4; ++e) {
                 const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
                 const float pv = s2 <= r ? dp[t][e] : 0.f;
-                Ep[t][e] = s2 < r ? pv * pP[t][e] : 0.f;
+                Ep[t][e] = s2 < r ? pv : 0.f;  // times P in S5
                 dPG[t][e] = s2 <= r ? pv * __builtin_amdgcn_exp2f((float)(sG[r] - sG[s2]) * 1.4426950408889634f) : 0.f;
             }
     }
@@ -1491,8 +1491,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     // ---- S3: P5 dQ += dPG K, P6 dK += dPG^T Q
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-        acc_N<true>(dPG[t], T16(O_PNH), T16(O_PNL), LB, r0, 32 * ch + 16 * t);
-        acc_T<true>(dPG[t], T16(O_PTH), T16(O_PTL), LB, r0, 32 * ch + 16 * t);
+        acc_N<true>(dPG[t], T16(O_PNH), T16(O_PNL), LB, r0, 32 * ch + 16 * t, l);
+        acc_T<true>(dPG[t], T16(O_PTH), T16(O_PTL), LB, r0, 32 * ch + 16 * t, l);
     }
     {
         // Q^T (threads 0-255) and K, K^T (threads 256-511): one 8 x 4 block per thread, one memory round trip
@@ -1508,6 +1508,17 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
             bk.store_T(T16(O_QT), LB);
         }
     }
+    // the running dq sum of the previous value heads at this lane's positions, in flight during P5 / P6
+    float prevq[4][4];
+    if (!first) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e;
+                prevq[t][e] = r < n ? part_row[(size_t)r * part_rs + 64 * ch + 16 * t + li] : 0.f;
+            }
+    }
     __syncthreads();
     {
         const bfr *Qt = T16(O_QT), *Kt = T16(O_KT);
@@ -1520,21 +1531,30 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
                 tl[e] += bf2f(Kt[j * LB + r]) * dK[t][e];
             }
     }
-    mmab<C, 4, true>(dQ, T16(O_PNH), T16(O_PNL), LB, r0, T16(O_KT), nullptr, LB, 64 * ch);
-    mmab<C, 4, true>(dK, T16(O_PTH), T16(O_PTL), LB, r0, T16(O_QT), nullptr, LB, 64 * ch);
-    // dQ is complete: its fp32 part row goes out now (16 lanes write 64 contiguous bytes) instead of staying live
-    float *const part_row = a.w.part + (((size_t)b * T + t0) * a.Hv + hv) * 2 * D;
+    mmab<C, 4, true>(dQ, T16(O_PNH), T16(O_PNL), LB, r0, T16(O_KT), nullptr, LB, 64 * ch, l);
+    mmab<C, 4, true>(dK, T16(O_PTH), T16(O_PTL), LB, r0, T16(O_QT), nullptr, LB, 64 * ch, l);
+    // dQ is complete: it goes out now (to the running sum, or as dq from the last value head) instead of staying
+    // live; 16 lanes cover 16 consecutive columns of a row
+    if (!first) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dQ[t][e] = prevq[t][e] + dQ[t][e];
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int r = r0 + 4 * lg + e;
-            if (r < n) part_row[(size_t)r * a.Hv * 2 * D + 64 * ch + 16 * t + li] = dQ[t][e];
+            const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+            if (r >= n) continue;
+            if (!last) part_row[(size_t)r * part_rs + j] = dQ[t][e];
+            else if (a.grad_dt == DT_BF16) static_cast<bfr *>(a.dq)[qk_out + (size_t)r * a.Hk * D + j] = (bfr)bfbits(dQ[t][e]);
+            else store_from_f32(a.dq, qk_out + (size_t)r * a.Hk * D + j, dQ[t][e], a.grad_dt);
         }
     __syncthreads();  // dPG and Q^T read (K^T, K, dDelta stay)
     // ---- S4a: P7 tdw = T^T dW, P8 tdd = T^T dDelta; dv
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc_T<false>(dWr[t], T16(O_DWT), nullptr, LB, r0, 64 * ch + 16 * t);
+    for (int t = 0; t < 4; ++t) acc_T<false>(dWr[t], T16(O_DWT), nullptr, LB, r0, 64 * ch + 16 * t, l);
     {
         // dDelta^T hi / lo (all threads, straight copies of the [i][r] planes), T and T^T hi / lo (threads
         // 0-127), V (all): one memory round trip
@@ -1576,8 +1596,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         f4 tdw[4], tdd[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) tdw[t] = tdd[t] = zero4();
-        mmab<C, 4>(tdw, T16(O_TTH), nullptr, LB, r0, T16(O_DWT), nullptr, LB, 64 * ch);
-        mmab<C, 4, true, true>(tdd, T16(O_TTH), T16(O_TTL), LB, r0, T16(O_DDTH), T16(O_DDTL), LB, 64 * ch);
+        mmab<C, 4>(tdw, T16(O_TTH), nullptr, LB, r0, T16(O_DWT), nullptr, LB, 64 * ch, l);
+        mmab<C, 4, true, true>(tdd, T16(O_TTH), T16(O_TTL), LB, r0, T16(O_DDTH), T16(O_DDTL), LB, 64 * ch, l);
         const bfr *Kt = T16(O_KT), *Vn = T16(O_V);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -1612,15 +1632,25 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         }
     }
     __syncthreads();  // dDelta^T, dW^T read (T^T hi, T, V, K, K^T, dDelta stay)
+    // P at this lane's pair positions (hi + lo planes), in flight during S4b and S5
+    uint32_t pP[2][4][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const size_t pi = ci * 2 * C * C + (r0 + 4 * lg + e) * C + 32 * ch + 16 * t + li;
+            pP[t][e][0] = a.w.Pb[pi];
+            pP[t][e][1] = a.w.Pb[pi + C * C];
+        }
     // ---- S4b: P9 t1 = dDelta V^T, P10 t2 = dW K^T; dT = (t1 + t2 diag(gamma)) diag(beta)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc_N<false>(dWr[t], T16(O_DW), nullptr, LA, r0, 64 * ch + 16 * t);
+    for (int t = 0; t < 4; ++t) acc_N<false>(dWr[t], T16(O_DW), nullptr, LA, r0, 64 * ch + 16 * t, l);
     __syncthreads();
     f4 dT[2];
     {
         f4 t1[2] = {zero4(), zero4()}, t2[2] = {zero4(), zero4()};
-        mmab<D, 2>(t1, T16(O_DD), nullptr, LA, r0, T16(O_V), nullptr, LA, 32 * ch);
-        mmab<D, 2>(t2, T16(O_DW), nullptr, LA, r0, T16(O_K), nullptr, LA, 32 * ch);
+        mmab<D, 2>(t1, T16(O_DD), nullptr, LA, r0, T16(O_V), nullptr, LA, 32 * ch, l);
+        mmab<D, 2>(t2, T16(O_DW), nullptr, LA, r0, T16(O_K), nullptr, LA, 32 * ch, l);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -1631,20 +1661,20 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     }
     // ---- S5: P11 y1 = dT T^T, P12 da = T^T Y1 (dA = -da), P13 K K^T; M = diag(beta) dA * Gam
 #pragma unroll
-    for (int t = 0; t < 2; ++t) acc_N<false>(dT[t], T16(O_DT), nullptr, LB, r0, 32 * ch + 16 * t);
+    for (int t = 0; t < 2; ++t) acc_N<false>(dT[t], T16(O_DT), nullptr, LB, r0, 32 * ch + 16 * t, l);
     __syncthreads();
     {
         f4 y1[2] = {zero4(), zero4()};
-        mmab<C, 2>(y1, T16(O_DT), nullptr, LB, r0, T16(O_TN), nullptr, LB, 32 * ch);
+        mmab<C, 2>(y1, T16(O_DT), nullptr, LB, r0, T16(O_TN), nullptr, LB, 32 * ch, l);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) acc_T<false>(y1[t], T16(O_Y1T), nullptr, LB, r0, 32 * ch + 16 * t);
+        for (int t = 0; t < 2; ++t) acc_T<false>(y1[t], T16(O_Y1T), nullptr, LB, r0, 32 * ch + 16 * t, l);
     }
     __syncthreads();
     f4 Mt[2];
     {
         f4 da[2] = {zero4(), zero4()}, kk[2] = {zero4(), zero4()};
-        mmab<C, 2>(da, T16(O_TTH), nullptr, LB, r0, T16(O_Y1T), nullptr, LB, 32 * ch);
-        mmab<D, 2>(kk, T16(O_K), nullptr, LA, r0, T16(O_K), nullptr, LA, 32 * ch);
+        mmab<C, 2>(da, T16(O_TTH), nullptr, LB, r0, T16(O_Y1T), nullptr, LB, 32 * ch, l);
+        mmab<D, 2>(kk, T16(O_K), nullptr, LA, r0, T16(O_K), nullptr, LA, 32 * ch, l);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -1654,7 +1684,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
                 const float dav = s2 < r ? -da[t][e] : 0.f;
                 const float kg = kk[t][e] * gam;
                 rowB[e] += dav * kg;
-                Ep[t][e] += dav * sB[r] * kg;
+                Ep[t][e] = Ep[t][e] * (bf2f(pP[t][e][0]) + bf2f(pP[t][e][1])) + dav * sB[r] * kg;
                 Mt[t][e] = sB[r] * dav * gam;
             }
     }
@@ -1675,8 +1705,27 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         }
     }
     __syncthreads();
-    mmab<C, 4>(dK, T16(O_MM), nullptr, LB, r0, T16(O_KT), nullptr, LB, 64 * ch);
-    __syncthreads();  // sM read: the pair matrix E reuses it
+    mmab<C, 4>(dK, T16(O_MM), nullptr, LB, r0, T16(O_KT), nullptr, LB, 64 * ch, l);
+    __syncthreads();  // sM, M + M^T and K^T read: the pair matrix E reuses sM, the dk staging the space below
+    // dK staged as fp32 rows in the free arena for 16-byte stores, and the running dk sum of the previous value
+    // heads at this thread's row pieces, in flight during the straddle sums
+    float *const sp = reinterpret_cast<float *>(arena);
+    constexpr int LP = D + 4, PER = C * D / 4 / NTB;
+    static_assert(C * LP * 4 <= O_SM, "part staging below the pair matrix");
+    static_assert(PER * NTB * 4 == C * D, "even split");
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sp[(r0 + 4 * lg + e) * LP + 64 * ch + 16 * t + li] = dK[t][e];
+    float4 prevk[PER];
+    if (!first) {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const int i = tid + p * NTB, r = i / (D / 4), c4 = (i - r * (D / 4)) * 4;
+            prevk[p] = r < n ? *reinterpret_cast<const float4 *>(part_row + (size_t)r * part_rs + D + c4)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
     // ---- straddle sums for dg, dbeta, outputs
     float *const sE = sM;
     lastp = wave_sum(lastp);
@@ -1698,23 +1747,39 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         }
     }
     __syncthreads();
-    chunk_dg_dbeta<NTB>(sE, sRow, sLast, sGam[C - 1], sScan, a, b, hv, t0, n);
-    {
-        // the dk half of the fp32 part rows, staged in the free arena, then 16-byte stores
-        float *sp = reinterpret_cast<float *>(arena);
-        constexpr int LP = D + 4;
-        static_assert(C * LP * 4 <= O_SM, "part staging below the pair matrix");
+    chunk_dg_dbeta<NTB>(sE, sRow, sLast, sGam[C - 1], sScan, a, b, hv, t0, n, tid);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sp[(r0 + 4 * lg + e) * LP + 64 * ch + 16 * t + li] = dK[t][e];
-        __syncthreads();
-        for (int i = tid; i < C * D / 4; i += NTB) {
-            const int r = i / (D / 4), c4 = (i - r * (D / 4)) * 4;
-            if (r < n)
-                *reinterpret_cast<float4 *>(part_row + (size_t)r * a.Hv * 2 * D + D + c4) =
-                    *reinterpret_cast<const float4 *>(sp + r * LP + c4);
+    for (int p = 0; p < PER; ++p) {
+        const int i = tid + p * NTB, r = i / (D / 4), c4 = (i - r * (D / 4)) * 4;
+        if (r >= n) continue;
+        float4 v = *reinterpret_cast<const float4 *>(sp + r * LP + c4);
+        if (!first) v = make_float4(prevk[p].x + v.x, prevk[p].y + v.y, prevk[p].z + v.z, prevk[p].w + v.w);
+        const size_t o = qk_out + (size_t)r * a.Hk * D + c4;
+        if (!last) {
+            *reinterpret_cast<float4 *>(part_row + (size_t)r * part_rs + D + c4) = v;
+        } else if (a.grad_dt == DT_BF16) {
+            *reinterpret_cast<uint2 *>(static_cast<bfr *>(a.dk) + o) = make_uint2(pk(v.x, v.y), pk(v.z, v.w));
+        } else if (a.grad_dt == DT_F32) {
+            *reinterpret_cast<float4 *>(static_cast<float *>(a.dk) + o) = v;
+        } else {
+            store_from_f32(a.dk, o, v.x, a.grad_dt);
+            store_from_f32(a.dk, o + 1, v.y, a.grad_dt);
+            store_from_f32(a.dk, o + 2, v.z, a.grad_dt);
+            store_from_f32(a.dk, o + 3, v.w, a.grad_dt);
         }
+    }
+    __syncthreads();  // the staging tile read: the next value head's tiles reuse the arena
+}
+
+// One workgroup of 8 waves per (chunk, key head), walking the key head's value heads in order.
+__global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
+    typedef const __attribute__((address_space(4))) Args *KArgs;  // the kernel arguments (constant memory)
+    const int rep = a.Hv / a.Hk;
+    for (int rr = 0; rr < rep; ++rr) {
+        // the arguments are read anew for each value head instead of being held in scalar registers across it
+        KArgs ap = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
+        asm volatile("" : "+s"(ap));
+        bwd_local_bf16_head(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep);
     }
 }
 
@@ -2454,15 +2519,18 @@ static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) 
         seq_dispatch<MT>(a, st, false);
     } else if (stage[0] == 'r') {
         const size_t n = (size_t)a.B * a.T * a.Hk * 2 * (CK_D / 8);
-        if (n) hipLaunchKernelGGL(ck::ck_reduce_qk_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
+        if (MT == 0 && n)
+            hipLaunchKernelGGL(ck::ck_reduce_qk_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
     } else if constexpr (MT == 1) {
-        hipLaunchKernelGGL(ck::ck_bwd_local_bf16_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
+        hipLaunchKernelGGL(ck::ck_bwd_local_bf16_kernel, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
     }
     else
         hipLaunchKernelGGL(ck::ck_bwd_local_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
 }
 
 static int mma_kind(int in_dt) { return in_dt == DT_BF16 ? 1 : 0; }
+
+bool chunk_has_reduce(int in_dt) { return mma_kind(in_dt) == 0; }
 
 
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st) {

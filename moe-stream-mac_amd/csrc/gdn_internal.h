@@ -54,6 +54,9 @@ struct ChunkCall {
 // stage: "prep" | "fwd" (forward) or "seq" | "local" | "reduce" (backward; "reduce" sums the per-value-head
 // dq | dk parts that "local" leaves in the workspace)
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st);
+// Whether the backward has a "reduce" stage: the bf16 "local" stage sums the value heads of each key head itself
+// and writes dq and dk.
+bool chunk_has_reduce(int in_dt);
 
 int pick_lane_width(int Dk);
 int rec_num_row_blocks(int Dv);
