@@ -1433,6 +1433,9 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
             *reinterpret_cast<uint4 *>(T16(O_DY) + r * LA + c) = yv;
         }
     }
+    // the waves' parts of <dh', h> go to LDS now (the raw h / dh' loads are not kept live until the straddle sums)
+    lastp = wave_sum(lastp);
+    if (l == 0) sLast[w] = lastp;
     __syncthreads();
     if (tid < C) {
         sGam[tid] = expf((float)sG[tid]);
@@ -1728,8 +1731,6 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     }
     // ---- straddle sums for dg, dbeta, outputs
     float *const sE = sM;
-    lastp = wave_sum(lastp);
-    if (l == 0) sLast[w] = lastp;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
