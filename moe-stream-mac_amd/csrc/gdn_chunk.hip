@@ -1441,6 +1441,13 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
         sGam[tid] = expf((float)sG[tid]);
         sRc[tid] = expf((float)(sG[C - 1] - sG[tid]));
     }
+    // S3's Q^T (threads 0-255) and K, K^T (threads 256-511) blocks, in flight during the S1 products: one 8 x 4
+    // block per thread
+    constexpr int NBQ = (C / 8) * (D / 4);
+    static_assert(2 * NBQ == NTB, "one block per thread");
+    const bool isk = tid >= NBQ;
+    Blk84 bk;
+    bk.load(isk ? ksrc : qsrc, qk_row, isk ? tid - NBQ : tid, D, n);
     float bnd[4] = {0.f, 0.f, 0.f, 0.f}, rowB[4] = {0.f, 0.f, 0.f, 0.f}, tl[4] = {0.f, 0.f, 0.f, 0.f};
     f4 dQ[4], dK[4], dWr[4], dPG[2], Ep[2];
 #pragma unroll
@@ -1497,19 +1504,11 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
         acc_N<true>(dPG[t], T16(O_PNH), T16(O_PNL), LB, r0, 32 * ch + 16 * t, l);
         acc_T<true>(dPG[t], T16(O_PTH), T16(O_PTL), LB, r0, 32 * ch + 16 * t, l);
     }
-    {
-        // Q^T (threads 0-255) and K, K^T (threads 256-511): one 8 x 4 block per thread, one memory round trip
-        constexpr int NBQ = (C / 8) * (D / 4);
-        static_assert(2 * NBQ == NTB, "one block per thread");
-        const bool isk = tid >= NBQ;
-        Blk84 bk;
-        bk.load(isk ? ksrc : qsrc, qk_row, isk ? tid - NBQ : tid, D, n);
-        if (isk) {
-            bk.store_N(T16(O_K), LA);
-            bk.store_T(T16(O_KT), LB);
-        } else {
-            bk.store_T(T16(O_QT), LB);
-        }
+    if (isk) {
+        bk.store_N(T16(O_K), LA);
+        bk.store_T(T16(O_KT), LB);
+    } else {
+        bk.store_T(T16(O_QT), LB);
     }
     // the running dq sum of the previous value heads at this lane's positions, in flight during P5 / P6
     float prevq[4][4];
@@ -1523,6 +1522,18 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
             }
     }
     __syncthreads();
+    // S4a's T hi / lo (threads 0-127, 8 x 4 blocks) and V (all), in flight during the S3 products
+    constexpr int NBT = (C / 8) * (C / 4), NDP = D * C / 8 / NTB;  // 16-byte pieces per plane and thread
+    static_assert(NBT <= NTB && NDP * NTB * 8 == D * C && C * (D / 8) == 2 * NTB, "block split");
+    Blk84Split bd;
+    const bool ist = tid < NBT;
+    if (ist) bd.load(Tc, C, (size_t)C * C, tid, C, C);
+    uint4 vr[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int pc = tid + p * NTB, r = pc / (D / 8), c8 = (pc - r * (D / 8)) * 8;
+        vr[p] = r < n ? *reinterpret_cast<const uint4 *>(vsrc + (size_t)r * v_row + c8) : make_uint4(0u, 0u, 0u, 0u);
+    }
     {
         const bfr *Qt = T16(O_QT), *Kt = T16(O_KT);
 #pragma unroll
@@ -1559,24 +1570,12 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc_T<false>(dWr[t], T16(O_DWT), nullptr, LB, r0, 64 * ch + 16 * t, l);
     {
-        // dDelta^T hi / lo (all threads, straight copies of the [i][r] planes), T and T^T hi / lo (threads
-        // 0-127), V (all): one memory round trip
-        constexpr int NBT = (C / 8) * (C / 4), NDP = D * C / 8 / NTB;  // 16-byte pieces per plane and thread
-        static_assert(NBT <= NTB && NDP * NTB * 8 == D * C && C * (D / 8) == 2 * NTB, "block split");
-        Blk84Split bd;
-        const bool ist = tid < NBT;
-        if (ist) bd.load(Tc, C, (size_t)C * C, tid, C, C);
+        // dDelta^T hi / lo: straight copies of the [i][r] planes
         uint4 ddh[NDP], ddlo[NDP];
 #pragma unroll
         for (int p = 0; p < NDP; ++p) {
             ddh[p] = reinterpret_cast<const uint4 *>(dDc)[tid + p * NTB];
             ddlo[p] = reinterpret_cast<const uint4 *>(dDc + D * C)[tid + p * NTB];
-        }
-        uint4 vr[2];
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
-            vr[p] = r < n ? *reinterpret_cast<const uint4 *>(vsrc + (size_t)r * v_row + c) : make_uint4(0u, 0u, 0u, 0u);
         }
 #pragma unroll
         for (int p = 0; p < NDP; ++p) {
