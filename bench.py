@@ -65,14 +65,16 @@ def kernel_model(name, B, T, Hk, Hv, D, in_b):
         return f, ch * (cc * 4 + cd * 4 + 3 * cd * in_b + C * 8 + dd * 4 + cd * 4)
     if name == "ck_bwd_local":
         f = ch * (3 * 2 * cd * D + 10 * 2 * cc * D + 2 * 2 * cc * C)
-        if bf:  # reads h, dh' (bf16), Delta (fp32), dDelta, T (bf16 hi / lo), P (hi / lo), G, q, k, v, dy, beta;
-            #     writes the fp32 dq | dk part, dv, dg, dbeta
-            return f, ch * (2 * dd * 2 + 2 * cd * 4 + cc * 4 + 2 * cc * 2 + C * 8 + 4 * cd * 2 + C * 4
-                            + 2 * cd * 4 + cd * 2 + 2 * C * 4)
+        if bf:  # reads h, dh' (bf16), Delta (fp32), dDelta, T (bf16 hi / lo), P (hi / lo), G, v, dy, beta and the
+            #     key head's q, k; writes dv, dg, dbeta and the key head's dq, dk (one workgroup per key head sums
+            #     its value heads; the fp32 running sum between them is not counted)
+            kv = Hk / Hv  # key-head rows per value head
+            return f, ch * (2 * dd * 2 + 2 * cd * 4 + cc * 4 + 2 * cc * 2 + C * 8 + 2 * cd * 2 + 2 * cd * 2 * kv
+                            + C * 4 + 2 * cd * 2 * kv + cd * 2 + 2 * C * 4)
         by = ch * (2 * dd * 4 + 2 * cd * 4 + 2 * cc * 4 + C * 8 + 4 * cd * in_b + C * 4
                    + 2 * cd * 4 + cd * in_b + 2 * C * 4)
         return f, by
-    if name == "reduce_qk":  # the fp32 per-value-head parts in, dq and dk out
+    if name == "reduce_qk":  # fp32 set: the fp32 per-value-head parts in, dq and dk out
         return 0, B * T * (Hv * 2 * D * 4 + Hk * 2 * D * in_b)
     if name == "rec_fwd":
         return 7 * tokh * D * D, B * T * (2 * Hk * D * in_b + Hv * D * in_b * 2 + 2 * Hv * 4)

@@ -824,7 +824,9 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
             lastp += dv4[p].x * hh[0] + dv4[p].y * hh[1] + dv4[p].z * hh[2] + dv4[p].w * hh[3];
         }
     }
-    lastp *= gC;
+    // the waves' parts go to LDS now (the raw dh' loads and h reads are not kept live until the straddle sums)
+    lastp = wave_sum(lastp * gC);
+    if (l == 0) sLast[w] = lastp;
 
     // ---- phase 1: dQ = diag(gamma) dY h^T ; dW = -dDelta h^T (parked)
     f4 dQ[4], dK[4];
@@ -972,8 +974,6 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     mma_strip<C, 4>(dK, R4 + r0, 1, LDC, sKm + 64 * ch, LD, 1, 16);
     // ---- phase 6: straddle sums for dg, dbeta, outputs.  R2 (dDelta) is free: E goes there.
     float *const sE = R2;
-    lastp = wave_sum(lastp);
-    if (l == 0) sLast[w] = lastp;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
