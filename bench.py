@@ -74,8 +74,6 @@ def kernel_model(name, B, T, Hk, Hv, D, in_b):
         by = ch * (2 * dd * 4 + 2 * cd * 4 + 2 * cc * 4 + C * 8 + 4 * cd * in_b + C * 4
                    + 2 * cd * 4 + cd * in_b + 2 * C * 4)
         return f, by
-    if name == "reduce_qk":  # fp32 set: the fp32 per-value-head parts in, dq and dk out
-        return 0, B * T * (Hv * 2 * D * 4 + Hk * 2 * D * in_b)
     if name == "rec_fwd":
         return 7 * tokh * D * D, B * T * (2 * Hk * D * in_b + Hv * D * in_b * 2 + 2 * Hv * 4)
     if name == "rec_bwd":

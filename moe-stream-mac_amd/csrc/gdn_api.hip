@@ -335,13 +335,7 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
             Timed tm("ck_bwd_local", st);
             launch_chunk_stage(cc, "local", st);
         }
-        rc = check_launch(st, "gdn_bwd(ck_bwd_local)");
-        if (rc || !chunk_has_reduce(in_dtype)) return rc;
-        {
-            Timed tm("reduce_qk", st);
-            launch_chunk_stage(cc, "reduce", st);
-        }
-        return check_launch(st, "gdn_bwd(reduce_qk)");
+        return check_launch(st, "gdn_bwd(ck_bwd_local)");
     }
     const BwdLayout L = bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind);
     char *ws = static_cast<char *>(workspace);

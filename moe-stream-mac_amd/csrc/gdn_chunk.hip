@@ -14,8 +14,8 @@
 //   ck_prep[_bf16]       grid (NC, Hv, B): G, T (blocked 16x16 unit-lower inverse), W, U, P of one chunk.
 //   ck_fwd[_bf16]        grid (D/VS, Hv, B): sequential over chunks; one value slice of h lives in accumulators.
 //   ck_bwd_seq[_bf16]    grid (D/VS, Hv, B): reverse over chunks; the state adjoint dh and dDelta.
-//   ck_bwd_local[_bf16]  grid (NC, Hv, B): dq, dk (per value head), dv, dbeta, dg of one chunk.
-//   ck_reduce_qk         dq, dk summed over the value heads of each key head.
+//   ck_bwd_local[_bf16]  grid (NC, Hk, B): dv, dbeta, dg of one chunk for each value head of a key head in turn,
+//                        and the key head's dq, dk (the value heads' parts summed in order).
 #include "gdn_common.h"
 #include "gdn_internal.h"
 
@@ -38,8 +38,8 @@ typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 // element (k, n) of B_t is B_t[k*bsr + n*bsc].  Accumulator element e of lane l is (row 4*(l/16) + e, column l%16).
 template <int K, int NTILES>
 __device__ __forceinline__ void mma_strip(f4 (&acc)[NTILES], const float *A, int asr, int asc, const float *B,
-                                          int bsr, int bsc, int btile) {
-    const int l = threadIdx.x & 63, li = l & 15, lg = l >> 4;
+                                          int bsr, int bsc, int btile, int l = threadIdx.x & 63) {
+    const int li = l & 15, lg = l >> 4;
 #pragma unroll 4
     for (int k0 = 0; k0 < K; k0 += 4) {
         const float av = A[li * asr + (k0 + lg) * asc];
@@ -56,8 +56,7 @@ __device__ __forceinline__ void mma_strip(f4 (&acc)[NTILES], const float *A, int
 // and all of a thread's loads are issued before the first LDS store, so the tile costs one memory latency.
 template <int ROWS, int COLS, int NTH = NT>
 __device__ __forceinline__ void load_tile(float *dst, int lds_stride, const void *src, size_t src_stride, int n,
-                                          int dt, const float *scale = nullptr) {
-    const int tid = threadIdx.x;
+                                          int dt, const float *scale = nullptr, int tid = threadIdx.x) {
     constexpr int BATCH = 8;  // 16-byte loads in flight per thread
     if (dt == DT_F32) {
         constexpr int VPR = COLS / 4;
@@ -225,7 +224,9 @@ struct Bufs {
     float *Dl;   // [B][Hv][NC][C][D]  Delta
     float *dH;   // [B][Hv][NC][D][D]  adjoint of each chunk's exit state, [j][i] like H (bf16 in the bf16 path)
     float *dDl;  // [B][Hv][NC][C][D]  dDelta (bf16 path: dDelta^T as bf16 hi and lo planes [2][D][C], same space)
-    float *part; // [B][T][Hv][2][D]   dq | dk per value head
+    float *part; // [B][T][Hv][2][D]   ck_bwd_local scratch: the running dq | dk sum of a key head (bf16 set: in the
+                 // rows [B][T][Hk][2][D]; fp32 set: in the slot of the key head's first value head, the other slots
+                 // parking each value head's dW)
     // bf16 operand tiles written by ck_prep for the bf16 sequential kernels (raw bf16 bits, k contiguous)
     unsigned short *Wb;   // [B][Hv][NC][C][D]     W
     unsigned short *KTb;  // [B][Hv][NC][D][C]     (K diag(gamma_C / gamma))^T
@@ -760,7 +761,10 @@ __device__ __forceinline__ void chunk_dg_dbeta(float *sE, const float (*sRow)[2]
 // exp(g_u)) keeps dg accurate for tiny decays, where a reverse cumulative sum of dG would cancel.
 constexpr int NTB = 512;  // ck_bwd_local: 8 waves; waves w and w+4 share the 16-row strip w%4 (column halves)
 
-__global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
+// One value head hv = hk * rep + rr of key head hk.  dq | dk of the key head are summed in order (rr = 0, 1, ...)
+// in the part rows of its first value head hk * rep, each thread reading back only the elements it wrote itself,
+// and the last value head writes dq and dk in the gradient dtype.
+__device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk, int b, int rr, int rep) {
     __shared__ __align__(16) float R1[D * LD];       // h / dh' ([j][i]); then K at R1, Q / dW at R1 + C*LD
     __shared__ __align__(16) float R2[C * LD];       // dY, then dDelta, then the pair matrix E
     __shared__ __align__(16) float RX[2 * C * LDC];  // dDelta, Delta; V ([C][LD] fits); R3 = RX (Y1), R4 = RX + C*LDC
@@ -770,10 +774,15 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     __shared__ float sRow[3][2][C];                  // per column half: chunk-start pair terms, t2 terms, dbeta
     __shared__ float sLast[8];
 
-    const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
+    const bool first = rr == 0, last = rr == rep - 1;
+    const int hv = hk * rep + rr;
+    // an opaque thread index per value head: the lane-dependent addresses are formed inside the head instead of
+    // being hoisted out of the caller's loop and held in registers across the whole head
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int r0 = 16 * (w & 3), ch = w >> 2;  // this wave's rows r0..r0+15 and column half
-    const int T = a.T, hk = hv / (a.Hv / a.Hk), t0 = c * C, n = min(C, T - t0);
+    const int T = a.T, t0 = c * C, n = min(C, T - t0);
     const size_t ci = chunk_index(a, b, hv, c);
     float *const sKm = R1;
     float *const sQm = R1 + C * LD;
@@ -798,9 +807,9 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
         if (tid < n) bt = a.beta[((size_t)b * T + t0 + tid) * a.Hv + hv];
         sB[tid] = bt;
     }
-    load_tile<D, D, NTB>(R1, LD, Hc, D, D, DT_F32);
-    load_tile<C, D, NTB>(R2, LD, elem_ptr(a.dy, v0, a.dy_dt), v_row, n, a.dy_dt);
-    load_tile<C, D, NTB>(RX, LD, dDc, D, C, DT_F32);  // dDelta, an MFMA operand of phase 1 (RX is free until V)
+    load_tile<D, D, NTB>(R1, LD, Hc, D, D, DT_F32, nullptr, tid);
+    load_tile<C, D, NTB>(R2, LD, elem_ptr(a.dy, v0, a.dy_dt), v_row, n, a.dy_dt, nullptr, tid);
+    load_tile<C, D, NTB>(RX, LD, dDc, D, C, DT_F32, nullptr, tid);  // dDelta, an MFMA operand of phase 1 (RX is free until V)
     __syncthreads();
     if (tid < C) {
         sGam[tid] = expf((float)sG[tid]);
@@ -834,8 +843,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
         f4 dw[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) dQ[t] = dw[t] = zero4();
-        mma_strip<D, 4>(dQ, R2 + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
-        mma_strip<D, 4>(dw, RX + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<D, 4>(dQ, R2 + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD, l);
+        mma_strip<D, 4>(dw, RX + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD, l);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -847,12 +856,12 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     }
     __syncthreads();
     // ---- phase 2: dK = diag(gamma_C/gamma) Delta dh'^T ; dP = lower(dY Delta^T)
-    load_tile<D, D, NTB>(R1, LD, dHc, D, D, DT_F32);
-    load_tile<C, D, NTB>(RX, LD, Dc, D, C, DT_F32);  // Delta in place of dDelta (phase 1 is done)
+    load_tile<D, D, NTB>(R1, LD, dHc, D, D, DT_F32, nullptr, tid);
+    load_tile<C, D, NTB>(RX, LD, Dc, D, C, DT_F32, nullptr, tid);  // Delta in place of dDelta (phase 1 is done)
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < 4; ++t) dK[t] = zero4();
-    mma_strip<D, 4>(dK, RX + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD);
+    mma_strip<D, 4>(dK, RX + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD, l);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -860,7 +869,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     f4 dPG[2], Ep[2];
     {
         f4 dp[2] = {zero4(), zero4()};
-        mma_strip<D, 2>(dp, R2 + r0 * LD, LD, 1, RX + 32 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<D, 2>(dp, R2 + r0 * LD, LD, 1, RX + 32 * ch * LD, 1, LD, 16 * LD, l);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -873,8 +882,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     }
     __syncthreads();
     // ---- phase 3: dQ += dPG K ; dK += dPG^T Q
-    load_tile<C, D, NTB>(sKm, LD, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
-    load_tile<C, D, NTB>(sQm, LD, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
+    load_tile<C, D, NTB>(sKm, LD, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt, nullptr, tid);
+    load_tile<C, D, NTB>(sQm, LD, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt, nullptr, tid);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -888,21 +897,21 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
             bnd[e] += sQm[r * LD + j] * dQ[t][e];
             tl[e] += sKm[r * LD + j] * dK[t][e];
         }
-    mma_strip<C, 4>(dQ, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16);
-    mma_strip<C, 4>(dK, R4 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16);
+    mma_strip<C, 4>(dQ, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16, l);
+    mma_strip<C, 4>(dK, R4 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16, l);
     __syncthreads();
     // ---- phase 4: through T.  R1b <- dW, R2 <- dDelta, RX <- V, R5 <- T
-    load_tile<C, D, NTB>(sQm, LD, dWpark, park_row, n, DT_F32);
-    load_tile<C, D, NTB>(R2, LD, dDc, D, C, DT_F32);
-    load_tile<C, D, NTB>(RX, LD, elem_ptr(a.v, v0, a.in_dt), v_row, n, a.in_dt);
-    load_tile<C, C, NTB>(R5, LDC, a.w.T + ci * C * C, C, C, DT_F32);
+    load_tile<C, D, NTB>(sQm, LD, dWpark, park_row, n, DT_F32, nullptr, tid);
+    load_tile<C, D, NTB>(R2, LD, dDc, D, C, DT_F32, nullptr, tid);
+    load_tile<C, D, NTB>(RX, LD, elem_ptr(a.v, v0, a.in_dt), v_row, n, a.in_dt, nullptr, tid);
+    load_tile<C, C, NTB>(R5, LDC, a.w.T + ci * C * C, C, C, DT_F32, nullptr, tid);
     __syncthreads();
     {
         f4 tdw[4], tdd[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) tdw[t] = tdd[t] = zero4();
-        mma_strip<C, 4>(tdw, R5 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16);
-        mma_strip<C, 4>(tdd, R5 + r0, 1, LDC, R2 + 64 * ch, LD, 1, 16);
+        mma_strip<C, 4>(tdw, R5 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16, l);
+        mma_strip<C, 4>(tdd, R5 + r0, 1, LDC, R2 + 64 * ch, LD, 1, 16, l);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -920,8 +929,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     f4 dT[2];
     {
         f4 t1[2] = {zero4(), zero4()}, t2[2] = {zero4(), zero4()};
-        mma_strip<D, 2>(t1, R2 + r0 * LD, LD, 1, RX + 32 * ch * LD, 1, LD, 16 * LD);
-        mma_strip<D, 2>(t2, sQm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<D, 2>(t1, R2 + r0 * LD, LD, 1, RX + 32 * ch * LD, 1, LD, 16 * LD, l);
+        mma_strip<D, 2>(t2, sQm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD, l);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -939,7 +948,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     // ---- phase 5: dA = -T^T dT T^T ; K K^T ; M = diag(beta) dA * Gam
     {
         f4 y1[2] = {zero4(), zero4()};
-        mma_strip<C, 2>(y1, R4 + r0 * LDC, LDC, 1, R5 + 32 * ch * LDC, 1, LDC, 16 * LDC);
+        mma_strip<C, 2>(y1, R4 + r0 * LDC, LDC, 1, R5 + 32 * ch * LDC, 1, LDC, 16 * LDC, l);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -949,8 +958,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     f4 Mt[2];
     {
         f4 da[2] = {zero4(), zero4()}, kk[2] = {zero4(), zero4()};
-        mma_strip<C, 2>(da, R5 + r0, 1, LDC, R3 + 32 * ch, LDC, 1, 16);
-        mma_strip<D, 2>(kk, sKm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD);
+        mma_strip<C, 2>(da, R5 + r0, 1, LDC, R3 + 32 * ch, LDC, 1, 16, l);
+        mma_strip<D, 2>(kk, sKm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD, l);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -970,8 +979,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) R4[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = Mt[t][e];
     __syncthreads();
-    mma_strip<C, 4>(dK, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16);
-    mma_strip<C, 4>(dK, R4 + r0, 1, LDC, sKm + 64 * ch, LD, 1, 16);
+    mma_strip<C, 4>(dK, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16, l);
+    mma_strip<C, 4>(dK, R4 + r0, 1, LDC, sKm + 64 * ch, LD, 1, 16, l);
     // ---- phase 6: straddle sums for dg, dbeta, outputs.  R2 (dDelta) is free: E goes there.
     float *const sE = R2;
 #pragma unroll
@@ -991,18 +1000,54 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
         }
     }
     __syncthreads();
+    // the running dq | dk sum of the previous value heads at this lane's positions, in flight during the sums
+    float *const sum_row = a.w.part + ((size_t)b * T + t0) * a.Hv * 2 * D + (size_t)hk * rep * 2 * D;
+    float pq[4][4], pk[4][4];
+    if (!first) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+                pq[t][e] = r < n ? sum_row[(size_t)r * park_row + j] : 0.f;
+                pk[t][e] = r < n ? sum_row[(size_t)r * park_row + D + j] : 0.f;
+            }
+    }
     chunk_dg_dbeta<NTB>(sE, sRow, sLast, 1.f, sScan, a, b, hv, t0, n, tid);
+    const size_t qk_out = (((size_t)b * T + t0) * a.Hk + hk) * D;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
-            if (r < n) {
-                const size_t tok = ((size_t)b * T + t0 + r) * a.Hv + hv;
-                a.w.part[tok * 2 * D + j] = dQ[t][e];
-                a.w.part[tok * 2 * D + D + j] = dK[t][e];
+            if (r >= n) continue;
+            float q = dQ[t][e], k = dK[t][e];
+            if (!first) {
+                q = pq[t][e] + q;
+                k = pk[t][e] + k;
+            }
+            if (!last) {
+                sum_row[(size_t)r * park_row + j] = q;
+                sum_row[(size_t)r * park_row + D + j] = k;
+            } else {
+                const size_t o = qk_out + (size_t)r * a.Hk * D + j;
+                store_from_f32(a.dq, o, q, a.grad_dt);
+                store_from_f32(a.dk, o, k, a.grad_dt);
             }
         }
+    __syncthreads();  // the pair matrix read: the next value head's tiles reuse its space
+}
+
+// One workgroup of 8 waves per (chunk, key head), walking the key head's value heads in order.
+__global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
+    typedef const __attribute__((address_space(4))) Args *KArgs;  // the kernel arguments (constant memory)
+    const int rep = a.Hv / a.Hk;
+    for (int rr = 0; rr < rep; ++rr) {
+        // the arguments are read anew for each value head instead of being held in scalar registers across it
+        KArgs ap = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
+        asm volatile("" : "+s"(ap));
+        bwd_local_f32_head(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------- bf16 tiles
@@ -1783,38 +1828,6 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     }
 }
 
-// dq, dk: the per-value-head fp32 parts summed over the Hv / Hk value heads of each key head, in order.
-// One thread per 8 channels of one (token, key head, q | k) row.
-__global__ __launch_bounds__(256) void ck_reduce_qk_kernel(Args a) {
-    const int rep = a.Hv / a.Hk;
-    const size_t rows = (size_t)a.B * a.T * a.Hk * 2;
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= rows * (D / 8)) return;
-    const int c8 = (int)(i % (D / 8)) * 8;
-    const size_t row = i / (D / 8);
-    const int which = (int)(row & 1);
-    const size_t bth = row >> 1, bt = bth / a.Hk;
-    const int hk = (int)(bth - bt * a.Hk);
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int r = 0; r < rep; ++r) {
-        const float *src = a.w.part + ((bt * a.Hv + hk * rep + r) * 2 + which) * D + c8;
-        const float4 x = *reinterpret_cast<const float4 *>(src), y = *reinterpret_cast<const float4 *>(src + 4);
-        acc[0] += x.x; acc[1] += x.y; acc[2] += x.z; acc[3] += x.w;
-        acc[4] += y.x; acc[5] += y.y; acc[6] += y.z; acc[7] += y.w;
-    }
-    void *dst = which ? a.dk : a.dq;
-    const size_t o = bth * D + c8;
-    if (a.grad_dt == DT_BF16) {
-        *reinterpret_cast<uint4 *>(static_cast<bfr *>(dst) + o) =
-            make_uint4(pk(acc[0], acc[1]), pk(acc[2], acc[3]), pk(acc[4], acc[5]), pk(acc[6], acc[7]));
-    } else if (a.grad_dt == DT_F32) {
-        *reinterpret_cast<float4 *>(static_cast<float *>(dst) + o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-        *reinterpret_cast<float4 *>(static_cast<float *>(dst) + o + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
-    } else {
-        for (int q = 0; q < 8; ++q) store_from_f32(dst, o + q, acc[q], a.grad_dt);
-    }
-}
-
 // ---------------------------------------------------------------------------------------------- ck_fwd (bf16)
 //
 // Sequential over chunks like ck_fwd_kernel, for bf16 inputs.  The A operands of every product (W, Q, P hi / lo,
@@ -2517,20 +2530,14 @@ template <int MT>
 static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) {
     if (stage[0] == 's') {
         seq_dispatch<MT>(a, st, false);
-    } else if (stage[0] == 'r') {
-        const size_t n = (size_t)a.B * a.T * a.Hk * 2 * (CK_D / 8);
-        if (MT == 0 && n)
-            hipLaunchKernelGGL(ck::ck_reduce_qk_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
     } else if constexpr (MT == 1) {
         hipLaunchKernelGGL(ck::ck_bwd_local_bf16_kernel, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
     }
     else
-        hipLaunchKernelGGL(ck::ck_bwd_local_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTB), 0, st, a);
+        hipLaunchKernelGGL(ck::ck_bwd_local_kernel, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
 }
 
 static int mma_kind(int in_dt) { return in_dt == DT_BF16 ? 1 : 0; }
-
-bool chunk_has_reduce(int in_dt) { return mma_kind(in_dt) == 0; }
 
 
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st) {

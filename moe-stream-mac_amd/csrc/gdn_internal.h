@@ -51,12 +51,9 @@ struct ChunkCall {
     void *saved, *work;
     int B, T, Hk, Hv, in_dt, out_dt, dy_dt, grad_dt, gate;
 };
-// stage: "prep" | "fwd" (forward) or "seq" | "local" | "reduce" (backward; "reduce" sums the per-value-head
-// dq | dk parts that "local" leaves in the workspace)
+// stage: "prep" | "fwd" (forward) or "seq" | "local" (backward; "local" walks the value heads of each key head
+// and writes dq and dk)
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st);
-// Whether the backward has a "reduce" stage: the bf16 "local" stage sums the value heads of each key head itself
-// and writes dq and dk.
-bool chunk_has_reduce(int in_dt);
 
 int pick_lane_width(int Dk);
 int rec_num_row_blocks(int Dv);
