@@ -679,32 +679,27 @@ __device__ __forceinline__ float wave_sum(float x) {
 //   sLast[8]         the waves' parts of <dh', h> (times last_scale: the pair (C-1, chunk start))
 //   sScan[2][C]      scratch
 // dg_u = sum_{r >= u} (sum_{s' < u} E[r][s'] + Eb[r]) + sum_{s < u} T2[s]: row prefix sums in 8-lane segments,
-// column sums in 8-lane groups, and the Eb suffix / T2 prefix as wave-0 shuffle scans.  Every thread takes part.
+// column sums in 8-lane groups, and the Eb suffix / T2 prefix as wave-0 DPP scans (the suffix as a prefix over
+// lanes holding Eb in reverse row order).  Every thread takes part.
 template <int NTH>
 __device__ __forceinline__ void chunk_dg_dbeta(float *sE, const float (*sRow)[2][C], const float *sLast, float last_scale,
                                                float (*sScan)[C], const Args &a, int b, int hv, int t0, int n,
                                                int tid) {
     static_assert(NTH == C * 8, "eight threads per row / column");
     const size_t g0 = ((size_t)b * a.T + t0) * a.Hv + hv;
+    static_assert(C == 64, "one wave scans the chunk");
     if (tid < C) {
-        const int r = tid;
-        float eb = sRow[0][0][r] + sRow[0][1][r];
-        if (r == C - 1)
+        const int r = tid, rs = C - 1 - tid;  // rs: this lane's row of the suffix scan
+        float eb = sRow[0][0][rs] + sRow[0][1][rs];
+        if (rs == C - 1)
             for (int i = 0; i < 8; ++i) eb += sLast[i] * last_scale;
         const float t2 = r < C - 1 ? sRow[1][0][r] + sRow[1][1][r] : 0.f;  // pair (C-1, r)
         if (r < n) a.dbeta[g0 + (size_t)r * a.Hv] = sRow[2][0][r] + sRow[2][1][r];
-        float su = eb, pr = t2;
-#pragma unroll
-        for (int d = 1; d < C; d <<= 1) {
-            const float y = __shfl_down(su, d, 64);
-            const float z = __shfl_up(pr, d, 64);
-            if (r + d < C) su += y;
-            if (r >= d) pr += z;
-        }
+        const float su = wave_prefix_sum(eb), pr = wave_prefix_sum(t2);
         // exclusive prefix by a one-lane shift, not by subtracting t2: every partial sum holds only terms whose span
         // straddles the token (no cancellation of larger terms)
-        const float prx = __shfl_up(pr, 1, 64);
-        sScan[0][r] = su;                // sum_{r' >= r} Eb[r']
+        const float prx = wave_shr1(pr);
+        sScan[0][rs] = su;                // sum_{r' >= rs} Eb[r']
         sScan[1][r] = r > 0 ? prx : 0.f;  // sum_{s < r} T2[s]
     }
     {
@@ -719,13 +714,15 @@ __device__ __forceinline__ void chunk_dg_dbeta(float *sE, const float (*sRow)[2]
             ex[i] = run;
             run += s0 + i < r ? xv[i] : 0.f;
         }
+        // inclusive scan over the row's 8 parts (DPP row shifts; a shifted value from another segment is unused)
         float sc = run;
-#pragma unroll
-        for (int d = 1; d < 8; d <<= 1) {
-            const float y = __shfl_up(sc, d, 8);
-            if (part >= d) sc += y;
-        }
-        const float scx = __shfl_up(sc, 1, 8);
+        float y = dpp_mov<0x111>(sc);  // row_shr:1
+        if (part >= 1) sc += y;
+        y = dpp_mov<0x112>(sc);        // row_shr:2
+        if (part >= 2) sc += y;
+        y = dpp_mov<0x114>(sc);        // row_shr:4
+        if (part >= 4) sc += y;
+        const float scx = dpp_mov<0x111>(sc);
         const float off = part > 0 ? scx : 0.f;  // the earlier parts of the row (one-lane shift, no subtraction)
         *reinterpret_cast<float4 *>(row) = make_float4(ex[0] + off, ex[1] + off, ex[2] + off, ex[3] + off);
         *reinterpret_cast<float4 *>(row + 4) = make_float4(ex[4] + off, ex[5] + off, ex[6] + off, ex[7] + off);
@@ -739,9 +736,9 @@ __device__ __forceinline__ void chunk_dg_dbeta(float *sE, const float (*sRow)[2]
             const int r = 8 * k + i;
             acc += r >= u ? sE[r * LDC + u] : 0.f;
         }
-        acc += __shfl_xor(acc, 1, 8);
-        acc += __shfl_xor(acc, 2, 8);
-        acc += __shfl_xor(acc, 4, 8);
+        acc += dpp_mov<DPP_QUAD_1032>(acc);
+        acc += dpp_mov<DPP_QUAD_2301>(acc);
+        acc += dpp_mov<DPP_ROW_HALF_MIRROR>(acc);  // the other quad of the 8-lane group
         if (k == 0 && u < n) {
             const size_t gi = g0 + (size_t)u * a.Hv;
             float dgv = acc + sScan[0][u] + sScan[1][u];

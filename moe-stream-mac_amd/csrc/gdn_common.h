@@ -56,6 +56,25 @@ __device__ __forceinline__ float row16_allreduce(float x) {
     return x;
 }
 
+// Inclusive prefix sum over the 64 lanes (all active): Hillis-Steele inside each row of 16 lanes (row_shr 1, 2, 4, 8,
+// out-of-row sources read 0), then the row totals carried by row_bcast:15 (rows 1 and 3) and row_bcast:31 (rows 2
+// and 3).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_masked(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_prefix_sum(float x) {
+    x += dpp_mov<0x111>(x);  // row_shr:1
+    x += dpp_mov<0x112>(x);  // row_shr:2
+    x += dpp_mov<0x114>(x);  // row_shr:4
+    x += dpp_mov<0x118>(x);  // row_shr:8
+    x += dpp_masked<0x142, 0xA>(x);  // row_bcast:15
+    x += dpp_masked<0x143, 0xC>(x);  // row_bcast:31
+    return x;
+}
+// Lane i receives lane i - 1 of the wave (lane 0 receives 0): wave_shr:1.
+__device__ __forceinline__ float wave_shr1(float x) { return dpp_mov<0x138>(x); }
+
 __device__ __forceinline__ float shfl_xor(float x, int mask) { return __shfl_xor(x, mask, 64); }
 
 }  // namespace gdn
