@@ -351,16 +351,11 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
             bt = a.beta[gi];
             gl = gate_log(a.g[gi], a.gate);
         }
-        double x = gl;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const double y = __shfl_up(x, d, 64);
-            if (tid >= d) x += y;
-        }
+        const double x = wave_prefix_sum((double)gl);
         sB[tid] = bt;
         sG[tid] = x;
         sGam[tid] = expf((float)x);
-        sRc[tid] = expf((float)(__shfl(x, 63, 64) - x));  // gamma_C / gamma_r
+        sRc[tid] = expf((float)(readlane_f64(x, 63) - x));  // gamma_C / gamma_r
     }
     __syncthreads();
     // K K^T (waves 0-3) and Q K^T (waves 4-7): each wave a 16-row strip of 4 tiles
@@ -667,10 +662,11 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
 
 // ---------------------------------------------------------------------------------------------- ck_bwd_local
 
+// Sum over the wave, the same in every lane: DPP row sums, then the four row totals read as scalars.
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) x += __shfl_xor(x, m, 64);
-    return x;
+    x = row16_allreduce(x);
+    const auto lane = [](float v, int i) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i)); };
+    return (lane(x, 0) + lane(x, 16)) + (lane(x, 32) + lane(x, 48));
 }
 
 // dbeta and dg of one chunk from the pair terms, after the barrier that completes sE / sRow / sLast:
@@ -2053,17 +2049,12 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
             bt = a.beta[gi];
             gl = gate_log(a.g[gi], a.gate);
         }
-        double x = gl;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const double y = __shfl_up(x, d, 64);
-            if (tid >= d) x += y;
-        }
+        const double x = wave_prefix_sum((double)gl);
         sB[tid] = bt;
         sG[tid] = x;
         sG2[tid] = x * 1.4426950408889634;  // log2(e): Gam_rs = 2^(G2_r - G2_s) on v_exp_f32
         sBG[tid] = bt * expf((float)x);
-        sRc[tid] = expf((float)(__shfl(x, 63, 64) - x));  // gamma_C / gamma_r
+        sRc[tid] = expf((float)(readlane_f64(x, 63) - x));  // gamma_C / gamma_r
     }
     __syncthreads();
     // (K diag(gamma_C / gamma))^T (threads 0-255, for the forward) and Q^T (threads 256-511, for the backward) as
@@ -2347,7 +2338,7 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
                                pk(yv[6][cc], yv[7][cc]));
         }
         if (tid < C) {  // wave 0 holds the chunk's cumulative log decays
-            const double gl = __shfl(cur.g, C - 1, 64);
+            const double gl = readlane_f64(cur.g, C - 1);
             sGam[tid] = expf((float)cur.g);
             sRc[tid] = expf((float)(gl - cur.g));
         }

@@ -72,6 +72,30 @@ __device__ __forceinline__ float wave_prefix_sum(float x) {
     x += dpp_masked<0x143, 0xC>(x);  // row_bcast:31
     return x;
 }
+// The same scan in fp64 (each DPP move carries the two halves of a lane's double).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_mov_f64(double x) {
+    const long long v = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(v & 0xffffffffll), CTRL, ROW_MASK, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(v >> 32), CTRL, ROW_MASK, 0xF, false);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+__device__ __forceinline__ double wave_prefix_sum(double x) {
+    x += dpp_mov_f64<0x111>(x);
+    x += dpp_mov_f64<0x112>(x);
+    x += dpp_mov_f64<0x114>(x);
+    x += dpp_mov_f64<0x118>(x);
+    x += dpp_mov_f64<0x142, 0xA>(x);
+    x += dpp_mov_f64<0x143, 0xC>(x);
+    return x;
+}
+// Lane `lane`'s double, read into every lane (a scalar read, no LDS round trip).
+__device__ __forceinline__ double readlane_f64(double x, int lane) {
+    const long long v = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_readlane((int)(v & 0xffffffffll), lane);
+    const int hi = __builtin_amdgcn_readlane((int)(v >> 32), lane);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
 // Lane i receives lane i - 1 of the wave (lane 0 receives 0): wave_shr:1.
 __device__ __forceinline__ float wave_shr1(float x) { return dpp_mov<0x138>(x); }
 
