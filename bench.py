@@ -51,8 +51,11 @@ def kernel_model(name, B, T, Hk, Hv, D, in_b):
     bf = in_b == 2  # the bf16 path keeps bf16 operand tiles (hi / lo where split) and bf16 states
     if name == "ck_prep":
         f = ch * 4 * 2 * cc * D
-        if bf:  # reads q, k, v, g, beta; writes G, T (fp32), P and P^T (hi / lo), W, -W^T, K~^T, Q^T, U (fp32)
-            return f, ch * (3 * cd * 2 + 2 * C * 4 + C * 8 + cc * 4 + 4 * cc * 2 + 4 * cd * 2 + cd * 4)
+        if bf:  # reads q, k (per key head), v, g, beta; writes G, T (fp32), P and P^T (hi / lo), W, -W^T, K~^T, U
+            #     (fp32) and Q^T (per key head)
+            kv = Hk / Hv
+            return f, ch * (2 * cd * 2 * kv + cd * 2 + 2 * C * 4 + C * 8 + cc * 4 + 4 * cc * 2 + 3 * cd * 2
+                            + cd * 2 * kv + cd * 4)
         return f, ch * (3 * cd * in_b + 2 * C * 4 + 2 * cd * 4 + 2 * cc * 4 + C * 8)
     if name in ("ck_fwd", "ck_bwd_seq"):
         f = ch * (3 * 2 * cd * D + 2 * cc * D)

@@ -233,7 +233,7 @@ struct Bufs {
     unsigned short *Pb;   // [B][Hv][NC][2][C][C]  P hi, P lo
     // ... and for the bf16 backward sequential kernel
     unsigned short *PTb;  // [B][Hv][NC][2][C][C]  P^T hi, P^T lo
-    unsigned short *QTb;  // [B][Hv][NC][D][C]     Q^T
+    unsigned short *QTb;  // [B][Hk][NC][D][C]     Q^T (per key head)
     unsigned short *nWTb; // [B][Hv][NC][D][C]     -W^T
 };
 
@@ -2073,11 +2073,15 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
             v[rr][0] = bf2f(x.x & 0xffffu) * sc; v[rr][1] = bf2f(x.x >> 16) * sc;
             v[rr][2] = bf2f(x.y & 0xffffu) * sc; v[rr][3] = bf2f(x.y >> 16) * sc;
         }
-        bfr *dst = (isq ? a.w.QTb : a.w.KTb) + ci * D * C;
+        // Q^T depends on the key head only: the first value head of each key head writes it
+        const int rep = a.Hv / a.Hk;
+        bfr *dst = isq ? a.w.QTb + (((size_t)b * a.Hk + hk) * a.NC + c) * D * C : a.w.KTb + ci * D * C;
+        if (!isq || hv % rep == 0) {
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc)
-            *reinterpret_cast<uint4 *>(dst + (j0 + cc) * C + rb * 8) =
-                make_uint4(pk(v[0][cc], v[1][cc]), pk(v[2][cc], v[3][cc]), pk(v[4][cc], v[5][cc]), pk(v[6][cc], v[7][cc]));
+            for (int cc = 0; cc < 4; ++cc)
+                *reinterpret_cast<uint4 *>(dst + (j0 + cc) * C + rb * 8) =
+                    make_uint4(pk(v[0][cc], v[1][cc]), pk(v[2][cc], v[3][cc]), pk(v[4][cc], v[5][cc]), pk(v[6][cc], v[7][cc]));
+        }
     }
     // K K^T (waves 0-3) -> A = strict_lower(diag(beta) K K^T * Gam); Q K^T (waves 4-7) -> P = lower(Q K^T * Gam)
     // P hi / lo are staged in the T region (T is written only by the inverse, after the next barrier) and go out
@@ -2279,7 +2283,7 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
         const int t0 = c * C, n = min(C, T - t0), r = mrow + li;
         const bfr *kb = static_cast<const bfr *>(a.k) + (((size_t)b * T + t0 + r) * a.Hk + hk) * D + 8 * lg;
         const bfr *pt = a.w.PTb + ci * 2 * C * C + r * C + 8 * lg;
-        const bfr *qt = a.w.QTb + ci * D * C + (16 * w + li) * C + 8 * lg;
+        const bfr *qt = a.w.QTb + (((size_t)b * a.Hk + hk) * a.NC + c) * D * C + (16 * w + li) * C + 8 * lg;
         const bfr *wt = a.w.nWTb + ci * D * C + (16 * w + li) * C + 8 * lg;
 #pragma unroll
         for (int k = 0; k < 4; ++k) f.K[k] = r < n ? ld_frag(kb + 32 * k) : zero_frag();
