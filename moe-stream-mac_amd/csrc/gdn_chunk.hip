@@ -1548,16 +1548,21 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     } else {
         bk.store_T(T16(O_QT), LB);
     }
-    // the running dq sum of the previous value heads at this lane's positions, in flight during P5 / P6
-    float prevq[4][4];
+    // dQ leaves through a wave-private staging block (the wave's 16 x 64 fp32 part of dQ, row stride LQ) in the
+    // space of the S4a tiles, which is free until the barrier after the S3 products: each lane then moves four
+    // 16-byte row pieces (piece p: row (l + 64p) / 16, columns 4 ((l + 64p) % 16) .. +3) instead of 16 scattered
+    // 4-byte elements.  The running dq sum of the previous value heads at those pieces is in flight during P5 / P6.
+    constexpr int LQ = 64 + 4;
+    static_assert(O_DWT + 8 * 16 * LQ * 4 <= ARENA, "dq staging fits the S4a space");
+    float *const stq = reinterpret_cast<float *>(arena + O_DWT) + w * 16 * LQ;
+    float4 prevq[4];
     if (!first) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = r0 + 4 * lg + e;
-                prevq[t][e] = r < n ? part_row[(size_t)r * part_rs + 64 * ch + 16 * t + li] : 0.f;
-            }
+        for (int p = 0; p < 4; ++p) {
+            const int i = l + 64 * p, r = r0 + (i >> 4), c4 = 64 * ch + 4 * (i & 15);
+            prevq[p] = r < n ? *reinterpret_cast<const float4 *>(part_row + (size_t)r * part_rs + c4)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     }
     __syncthreads();
     // S4a's T hi / lo (threads 0-127, 8 x 4 blocks) and V (all), in flight during the S3 products
@@ -1586,24 +1591,32 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     mmab<C, 4, true>(dQ, T16(O_PNH), T16(O_PNL), LB, r0, T16(O_KT), nullptr, LB, 64 * ch, l);
     mmab<C, 4, true>(dK, T16(O_PTH), T16(O_PTL), LB, r0, T16(O_QT), nullptr, LB, 64 * ch, l);
     // dQ is complete: it goes out now (to the running sum, or as dq from the last value head) instead of staying
-    // live; 16 lanes cover 16 consecutive columns of a row
-    if (!first) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dQ[t][e] = prevq[t][e] + dQ[t][e];
-    }
+    // live
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
-            if (r >= n) continue;
-            if (!last) part_row[(size_t)r * part_rs + j] = dQ[t][e];
-            else if (a.grad_dt == DT_BF16) static_cast<bfr *>(a.dq)[qk_out + (size_t)r * a.Hk * D + j] = (bfr)bfbits(dQ[t][e]);
-            else store_from_f32(a.dq, qk_out + (size_t)r * a.Hk * D + j, dQ[t][e], a.grad_dt);
+        for (int e = 0; e < 4; ++e) stq[(4 * lg + e) * LQ + 16 * t + li] = dQ[t][e];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int i = l + 64 * p, rr = i >> 4, r = r0 + rr, c4 = 64 * ch + 4 * (i & 15);
+        float4 v = *reinterpret_cast<const float4 *>(stq + rr * LQ + 4 * (i & 15));
+        if (r >= n) continue;
+        if (!first) v = make_float4(prevq[p].x + v.x, prevq[p].y + v.y, prevq[p].z + v.z, prevq[p].w + v.w);
+        const size_t o = qk_out + (size_t)r * a.Hk * D + c4;
+        if (!last) {
+            *reinterpret_cast<float4 *>(part_row + (size_t)r * part_rs + c4) = v;
+        } else if (a.grad_dt == DT_BF16) {
+            *reinterpret_cast<uint2 *>(static_cast<bfr *>(a.dq) + o) = make_uint2(pk(v.x, v.y), pk(v.z, v.w));
+        } else if (a.grad_dt == DT_F32) {
+            *reinterpret_cast<float4 *>(static_cast<float *>(a.dq) + o) = v;
+        } else {
+            store_from_f32(a.dq, o, v.x, a.grad_dt);
+            store_from_f32(a.dq, o + 1, v.y, a.grad_dt);
+            store_from_f32(a.dq, o + 2, v.z, a.grad_dt);
+            store_from_f32(a.dq, o + 3, v.w, a.grad_dt);
         }
-    __syncthreads();  // dPG and Q^T read (K^T, K, dDelta stay)
+    }
+    __syncthreads();  // dPG and Q^T read (K^T, K, dDelta stay); the dq staging read
     // ---- S4a: P7 tdw = T^T dW, P8 tdd = T^T dDelta; dv
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc_T<false>(dWr[t], T16(O_DWT), nullptr, LB, r0, 64 * ch + 16 * t, l);
