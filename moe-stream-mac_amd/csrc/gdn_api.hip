@@ -316,8 +316,8 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
     if (f == GDN_FORM_CHUNK) {
         if (misaligned16(q) || misaligned16(k) || misaligned16(v) || misaligned16(dy))
             return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned q, k, v and dy");
-        if (misaligned16(dq) || misaligned16(dk))
-            return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned dq and dk");
+        if (misaligned16(dq) || misaligned16(dk) || misaligned16(dv))
+            return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned dq, dk and dv");
         ChunkCall cc{};
         cc.q = q; cc.k = k; cc.v = v; cc.g = g; cc.beta = beta; cc.state0 = state0;
         cc.dy = dy; cc.dstate_T = dstate_T; cc.dq = dq; cc.dk = dk; cc.dv = dv; cc.dg = dg; cc.dbeta = dbeta;

@@ -1645,6 +1645,7 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
         }
     }
     __syncthreads();
+    uint32_t dvb[4][4];  // dv as bf16 bits at this lane's accumulator positions
     {
         f4 tdw[4], tdd[4];
 #pragma unroll
@@ -1663,28 +1664,39 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
                 rowB[e] += sGam[r] * s4;
                 bnd[e] += bg * s4;
                 rowB[e] += bf2f(Vn[r * LA + j]) * tdd[t][e];
-                tdd[t][e] *= sB[r];  // dv
+                dvb[t][e] = bfbits(tdd[t][e] * sB[r]);  // dv
             }
-        if (a.grad_dt == DT_BF16) {
-            bfr *dvp = static_cast<bfr *>(a.dv) + v0;
+        if (a.grad_dt != DT_BF16) {
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int r = r0 + 4 * lg + e;
-                    if (r < n) dvp[(size_t)r * v_row + 64 * ch + 16 * t + li] = (bfr)bfbits(tdd[t][e]);
-                }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = r0 + 4 * lg + e;
-                    if (r < n) store_from_f32(a.dv, v0 + (size_t)r * v_row + 64 * ch + 16 * t + li, tdd[t][e], a.grad_dt);
+                    if (r < n)
+                        store_from_f32(a.dv, v0 + (size_t)r * v_row + 64 * ch + 16 * t + li, tdd[t][e] * sB[r], a.grad_dt);
                 }
         }
     }
     __syncthreads();  // dDelta^T, dW^T read (T^T hi, T, V, K, K^T, dDelta stay)
+    if (a.grad_dt == DT_BF16) {
+        // bf16 dv leaves through a wave-private staging block (16 x 64, row stride LV) in the dead dDelta^T lo space
+        // (rewritten only after the next barrier): two 16-byte row pieces per lane (piece p: row (l + 64p) / 8,
+        // columns 8 ((l + 64p) % 8) .. +7)
+        constexpr int LV = 64 + 8;
+        static_assert(8 * 16 * LV * 2 <= SZ_C && O_DDTL + SZ_C <= O_TTH, "dv staging fits the dDelta^T lo space");
+        bfr *const stv = T16(O_DDTL) + w * 16 * LV;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) stv[(4 * lg + e) * LV + 16 * t + li] = (bfr)dvb[t][e];
+        bfr *const dvp = static_cast<bfr *>(a.dv) + v0;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int i = l + 64 * p, rr = i >> 3, c8 = 8 * (i & 7), r = r0 + rr;
+            const uint4 x = *reinterpret_cast<const uint4 *>(stv + rr * LV + c8);
+            if (r < n) *reinterpret_cast<uint4 *>(dvp + (size_t)r * v_row + 64 * ch + c8) = x;
+        }
+    }
     // P at this lane's pair positions (hi + lo planes), in flight during S4b and S5
     uint32_t pP[2][4][2];
 #pragma unroll
