@@ -993,41 +993,52 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
         }
     }
     __syncthreads();
-    // the running dq | dk sum of the previous value heads at this lane's positions, in flight during the sums
+    // dq and dk leave through a wave-private staging block in R1 (free after the barrier above: the wave's 16 x 64
+    // fp32 part, row stride LQ), one matrix after the other: each lane moves four 16-byte row pieces per matrix
+    // (piece p: row (l + 64p) / 16, columns 4 ((l + 64p) % 16) .. +3) instead of 16 scattered 4-byte elements.
+    // The running dq | dk sum of the previous value heads at those pieces is in flight during the sums.
+    constexpr int LQ = 64 + 4;
+    static_assert(8 * 16 * LQ <= D * LD, "staging fits R1");
+    float *const stg = R1 + w * 16 * LQ;
     float *const sum_row = a.w.part + ((size_t)b * T + t0) * a.Hv * 2 * D + (size_t)hk * rep * 2 * D;
-    float pq[4][4], pk[4][4];
+    float4 prq[4], prk[4];
     if (!first) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
-                pq[t][e] = r < n ? sum_row[(size_t)r * park_row + j] : 0.f;
-                pk[t][e] = r < n ? sum_row[(size_t)r * park_row + D + j] : 0.f;
-            }
+        for (int p = 0; p < 4; ++p) {
+            const int i = l + 64 * p, r = r0 + (i >> 4), c4 = 64 * ch + 4 * (i & 15);
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            prq[p] = r < n ? *reinterpret_cast<const float4 *>(sum_row + (size_t)r * park_row + c4) : z;
+            prk[p] = r < n ? *reinterpret_cast<const float4 *>(sum_row + (size_t)r * park_row + D + c4) : z;
+        }
     }
     chunk_dg_dbeta<NTB>(sE, sRow, sLast, 1.f, sScan, a, b, hv, t0, n, tid);
     const size_t qk_out = (((size_t)b * T + t0) * a.Hk + hk) * D;
+    auto out = [&](const f4 (&X)[4], const float4 (&prev)[4], int half, void *dst) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+            for (int e = 0; e < 4; ++e) stg[(4 * lg + e) * LQ + 16 * t + li] = X[t][e];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int i = l + 64 * p, rr = i >> 4, r = r0 + rr, c4 = 64 * ch + 4 * (i & 15);
+            float4 v = *reinterpret_cast<const float4 *>(stg + rr * LQ + 4 * (i & 15));
             if (r >= n) continue;
-            float q = dQ[t][e], k = dK[t][e];
-            if (!first) {
-                q = pq[t][e] + q;
-                k = pk[t][e] + k;
-            }
+            if (!first) v = make_float4(prev[p].x + v.x, prev[p].y + v.y, prev[p].z + v.z, prev[p].w + v.w);
+            const size_t o = qk_out + (size_t)r * a.Hk * D + c4;
             if (!last) {
-                sum_row[(size_t)r * park_row + j] = q;
-                sum_row[(size_t)r * park_row + D + j] = k;
+                *reinterpret_cast<float4 *>(sum_row + (size_t)r * park_row + half * D + c4) = v;
+            } else if (a.grad_dt == DT_F32) {
+                *reinterpret_cast<float4 *>(static_cast<float *>(dst) + o) = v;
             } else {
-                const size_t o = qk_out + (size_t)r * a.Hk * D + j;
-                store_from_f32(a.dq, o, q, a.grad_dt);
-                store_from_f32(a.dk, o, k, a.grad_dt);
+                store_from_f32(dst, o, v.x, a.grad_dt);
+                store_from_f32(dst, o + 1, v.y, a.grad_dt);
+                store_from_f32(dst, o + 2, v.z, a.grad_dt);
+                store_from_f32(dst, o + 3, v.w, a.grad_dt);
             }
         }
+    };
+    out(dQ, prq, 0, a.dq);
+    out(dK, prk, 1, a.dk);
     __syncthreads();  // the pair matrix read: the next value head's tiles reuse its space
 }
 
