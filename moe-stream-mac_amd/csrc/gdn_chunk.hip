@@ -899,6 +899,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
     load_tile<C, D, NTB>(RX, LD, elem_ptr(a.v, v0, a.in_dt), v_row, n, a.in_dt, nullptr, tid);
     load_tile<C, C, NTB>(R5, LDC, a.w.T + ci * C * C, C, C, DT_F32, nullptr, tid);
     __syncthreads();
+    f4 dvv[4];  // dv at this lane's accumulator positions
     {
         f4 tdw[4], tdd[4];
 #pragma unroll
@@ -916,7 +917,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
                 rowB[e] += sGam[r] * s4;
                 bnd[e] += bg * s4;
                 rowB[e] += RX[r * LD + j] * tdd[t][e];
-                if (r < n) store_from_f32(a.dv, v0 + (size_t)r * v_row + j, sB[r] * tdd[t][e], a.grad_dt);
+                dvv[t][e] = sB[r] * tdd[t][e];
             }
     }
     f4 dT[2];
@@ -933,6 +934,31 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             }
     }
     __syncthreads();
+    {
+        // dv leaves through a wave-private staging block in R2 (dDelta is read; R2 next holds the pair matrix after
+        // two more barriers): the wave's 16 x 64 fp32 part at row stride 64, four 16-byte row pieces per lane
+        static_assert(8 * 16 * 64 <= C * LD, "dv staging fits R2");
+        float *const stv = R2 + w * 16 * 64;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) stv[(4 * lg + e) * 64 + 16 * t + li] = dvv[t][e];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int i = l + 64 * p, rr = i >> 4, r = r0 + rr, c4 = 4 * (i & 15);
+            const float4 v = *reinterpret_cast<const float4 *>(stv + rr * 64 + c4);
+            if (r >= n) continue;
+            const size_t o = v0 + (size_t)r * v_row + 64 * ch + c4;
+            if (a.grad_dt == DT_F32) {
+                *reinterpret_cast<float4 *>(static_cast<float *>(a.dv) + o) = v;
+            } else {
+                store_from_f32(a.dv, o, v.x, a.grad_dt);
+                store_from_f32(a.dv, o + 1, v.y, a.grad_dt);
+                store_from_f32(a.dv, o + 2, v.z, a.grad_dt);
+                store_from_f32(a.dv, o + 3, v.w, a.grad_dt);
+            }
+        }
+    }
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
