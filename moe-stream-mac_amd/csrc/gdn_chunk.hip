@@ -227,7 +227,8 @@ struct Bufs {
     float *part; // [B][T][Hv][2][D]   ck_bwd_local scratch: the running dq | dk sum of a key head (bf16 set: in the
                  // rows [B][T][Hk][2][D]; fp32 set: in the slot of the key head's first value head, the other slots
                  // parking each value head's dW)
-    // bf16 operand tiles written by ck_prep for the bf16 sequential kernels (raw bf16 bits, k contiguous)
+    // bf16 operand tiles written by ck_prep for the bf16 sequential kernels (raw bf16 bits), each [M][K] tile in
+    // fragment order (frag_off<K>); the bf16 set keeps U in accumulator order (acc_off)
     unsigned short *Wb;   // [B][Hv][NC][C][D]     W
     unsigned short *KTb;  // [B][Hv][NC][D][C]     (K diag(gamma_C / gamma))^T
     unsigned short *Pb;   // [B][Hv][NC][2][C][C]  P hi, P lo
@@ -1101,6 +1102,22 @@ __device__ __forceinline__ void pk2(float a, float b, uint32_t &h, uint32_t &lo)
     lo = bfbits(a - bf2f(ha)) | (bfbits(b - bf2f(hb)) << 16);
 }
 
+// Fragment order of the bf16 A-operand tiles that ck_prep writes for the sequential kernels (and the P tile
+// ck_bwd_local reads): element (m, k) of an [M][K] tile sits at frag_off<K>(m, k), so that the 16-byte fragment lane
+// l of a wave loads for rows m0..m0+15 and k0..k0+31 (m0 % 16 = k0 % 32 = 0) is at frag_off<K>(m0, k0) + 8 l and one
+// load instruction of the wave reads 1 KiB contiguous (a row-major tile gives 16 rows x 64 bytes per instruction).
+template <int K>
+__device__ __forceinline__ int frag_off(int m, int k) {
+    return (((m >> 4) * (K / 32) + (k >> 5)) * 64 + (m & 15) + 16 * ((k & 31) >> 3)) * 8 + (k & 7);
+}
+constexpr int FRAG_BLOCK = 64 * 8;  // elements of one wave's 16 x 32 fragment block
+// Accumulator order of the fp32 U tile [C][D] (bf16 set): the four rows m0 + 4 (l / 16) .. +3 of column n0 + l % 16
+// that lane l of a 16 x 16 MFMA accumulator tile holds are 16 contiguous bytes at acc_off(m0 + 4 (l / 16), n0 + l % 16)
+// (m0, n0 multiples of 16), one wave's tile 1 KiB.
+__device__ __forceinline__ int acc_off(int m, int n) {
+    return (((m >> 4) * (D / 16) + (n >> 4)) * 64 + (n & 15) + 16 * ((m & 15) >> 2)) * 4 + (m & 3);
+}
+
 __device__ __forceinline__ bf8 frag(const bfr *t, int ld, int m0, int k0, int l = threadIdx.x & 63) {
     return *reinterpret_cast<const bf8 *>(t + (m0 + (l & 15)) * ld + k0 + 8 * (l >> 4));
 }
@@ -1740,7 +1757,7 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const size_t pi = ci * 2 * C * C + (r0 + 4 * lg + e) * C + 32 * ch + 16 * t + li;
+            const size_t pi = ci * 2 * C * C + frag_off<C>(r0 + 4 * lg + e, 32 * ch + 16 * t + li);
             pP[t][e][0] = a.w.Pb[pi];
             pP[t][e][1] = a.w.Pb[pi + C * C];
         }
@@ -1948,27 +1965,27 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
     auto fetch = [&](FwdFrags<DN> &f, int c) {
         const size_t ci = head * a.NC + c;
         const int t0 = c * C, n = min(C, T - t0), r = mrow + li;
-        const bfr *wb = a.w.Wb + ci * C * D + r * D + 8 * lg;
-        const bfr *pb = a.w.Pb + ci * 2 * C * C + r * C + 8 * lg;
-        const bfr *kt = a.w.KTb + ci * D * C + (16 * w + li) * C + 8 * lg;
+        const bfr *wb = a.w.Wb + ci * C * D + frag_off<D>(mrow, 0) + 8 * l;
+        const bfr *pb = a.w.Pb + ci * 2 * C * C + frag_off<C>(mrow, 0) + 8 * l;
+        const bfr *kt = a.w.KTb + ci * D * C + frag_off<C>(16 * w, 0) + 8 * l;
         const bfr *qb = static_cast<const bfr *>(a.q) + (((size_t)b * T + t0 + r) * a.Hk + hk) * D + 8 * lg;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            f.W[k] = ld_frag(wb + 32 * k);
+            f.W[k] = ld_frag(wb + FRAG_BLOCK * k);
             f.Q[k] = r < n ? ld_frag(qb + 32 * k) : zero_frag();
         }
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            f.P[k] = ld_frag(pb + 32 * k);
-            f.P[2 + k] = ld_frag(pb + C * C + 32 * k);
-            f.K[k] = ld_frag(kt + 32 * k);
+            f.P[k] = ld_frag(pb + FRAG_BLOCK * k);
+            f.P[2 + k] = ld_frag(pb + C * C + FRAG_BLOCK * k);
+            f.K[k] = ld_frag(kt + FRAG_BLOCK * k);
         }
         if (cwave) {
 #pragma unroll
-            for (int t = 0; t < DN; ++t)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    f.U[t][e] = a.w.U[ci * C * D + (size_t)(mrow + 4 * lg + e) * D + i0 + 16 * (nt0 + t) + li];
+            for (int t = 0; t < DN; ++t) {
+                const float4 x = *reinterpret_cast<const float4 *>(a.w.U + ci * C * D + acc_off(mrow + 4 * lg, i0 + 16 * (nt0 + t) + li));
+                f.U[t][0] = x.x; f.U[t][1] = x.y; f.U[t][2] = x.z; f.U[t][3] = x.w;
+            }
         }
         f.g = tid < C ? a.w.G[ci * C + tid] : 0.0;
     };
@@ -2141,7 +2158,7 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
         if (!isq || hv % rep == 0) {
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc)
-                *reinterpret_cast<uint4 *>(dst + (j0 + cc) * C + rb * 8) =
+                *reinterpret_cast<uint4 *>(dst + frag_off<C>(j0 + cc, rb * 8)) =
                     make_uint4(pk(v[0][cc], v[1][cc]), pk(v[2][cc], v[3][cc]), pk(v[4][cc], v[5][cc]), pk(v[6][cc], v[7][cc]));
         }
     }
@@ -2176,7 +2193,7 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
             }
             if (isq) {
                 // P^T [s][r]: this lane's four consecutive r of column s = 16t + li
-                bfr *pt = a.w.PTb + ci * 2 * C * C + (16 * t + li) * C + r0 + 4 * lg;
+                bfr *pt = a.w.PTb + ci * 2 * C * C + frag_off<C>(16 * t + li, r0 + 4 * lg);
                 *reinterpret_cast<uint2 *>(pt) = make_uint2(ph[0] | ((uint32_t)ph[1] << 16), ph[2] | ((uint32_t)ph[3] << 16));
                 *reinterpret_cast<uint2 *>(pt + C * C) =
                     make_uint2(pl[0] | ((uint32_t)pl[1] << 16), pl[2] | ((uint32_t)pl[3] << 16));
@@ -2192,8 +2209,11 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
         *reinterpret_cast<uint4 *>(sVT + (vc + cc) * LT + 8 * vb) =
             make_uint4(x[0] | (x[1] << 16), x[2] | (x[3] << 16), x[4] | (x[5] << 16), x[6] | (x[7] << 16));
     }
-    for (int i = tid; i < 2 * C * C / 8; i += NTP)  // P hi / lo out
-        *reinterpret_cast<uint4 *>(a.w.Pb + ci * 2 * C * C + 8 * i) = *reinterpret_cast<const uint4 *>(sPb + 8 * i);
+    for (int i = tid; i < 2 * C * C / 8; i += NTP) {  // P hi / lo out, in fragment order
+        const int pl = i / (C * C / 8), e0 = 8 * i - pl * C * C, m = e0 / C;
+        *reinterpret_cast<uint4 *>(a.w.Pb + ci * 2 * C * C + pl * C * C + frag_off<C>(m, e0 - m * C)) =
+            *reinterpret_cast<const uint4 *>(sPb + 8 * i);
+    }
     __syncthreads();  // P read out of the T region
     unit_lower_inverse<NTP>(sA, sT, scratch);  // ends with a barrier: A is dead
     // K^T [j][s] (exact) in the A region
@@ -2263,19 +2283,20 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
                 sW[(r0 + 4 * lg + e) * LK + 16 * t + li] = wb[e];
             }
             // -W^T [j][r]; bf16 negation flips the sign bit
-            bfr *wt = a.w.nWTb + ci * D * C + (16 * t + li) * C + r0 + 4 * lg;
+            bfr *wt = a.w.nWTb + ci * D * C + frag_off<C>(16 * t + li, r0 + 4 * lg);
             *reinterpret_cast<uint2 *>(wt) = make_uint2((wb[0] | ((uint32_t)wb[1] << 16)) ^ 0x80008000u,
                                                         (wb[2] | ((uint32_t)wb[3] << 16)) ^ 0x80008000u);
         }
     }
     __syncthreads();
-    for (int i = tid; i < C * D / 4; i += NTP) {  // U fp32
-        const int r = i / (D / 4), c4 = (i - r * (D / 4)) * 4;
-        *reinterpret_cast<float4 *>(a.w.U + ci * C * D + r * D + c4) = *reinterpret_cast<const float4 *>(sU + r * LU + c4);
+    for (int i = tid; i < C * D / 4; i += NTP) {  // U fp32 in accumulator order: 16-byte piece i holds 4 rows
+        const int blk = i >> 6, ln = i & 63, rw = 16 * (blk / (D / 16)) + 4 * (ln >> 4), cl = 16 * (blk % (D / 16)) + (ln & 15);
+        *reinterpret_cast<float4 *>(a.w.U + ci * C * D + 4 * i) =
+            make_float4(sU[rw * LU + cl], sU[(rw + 1) * LU + cl], sU[(rw + 2) * LU + cl], sU[(rw + 3) * LU + cl]);
     }
-    for (int i = tid; i < C * D / 8; i += NTP) {  // W bf16
+    for (int i = tid; i < C * D / 8; i += NTP) {  // W bf16 in fragment order
         const int r = i / (D / 8), c8 = (i - r * (D / 8)) * 8;
-        *reinterpret_cast<uint4 *>(a.w.Wb + ci * C * D + r * D + c8) = *reinterpret_cast<const uint4 *>(sW + r * LK + c8);
+        *reinterpret_cast<uint4 *>(a.w.Wb + ci * C * D + frag_off<D>(r, c8)) = *reinterpret_cast<const uint4 *>(sW + r * LK + c8);
     }
     for (int i = tid; i < C * C / 4; i += NTP) {  // T as bf16 hi and lo planes
         const int r = i / (C / 4), c4 = (i - r * (C / 4)) * 4;
@@ -2344,17 +2365,17 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
         const size_t ci = head * a.NC + c;
         const int t0 = c * C, n = min(C, T - t0), r = mrow + li;
         const bfr *kb = static_cast<const bfr *>(a.k) + (((size_t)b * T + t0 + r) * a.Hk + hk) * D + 8 * lg;
-        const bfr *pt = a.w.PTb + ci * 2 * C * C + r * C + 8 * lg;
-        const bfr *qt = a.w.QTb + (((size_t)b * a.Hk + hk) * a.NC + c) * D * C + (16 * w + li) * C + 8 * lg;
-        const bfr *wt = a.w.nWTb + ci * D * C + (16 * w + li) * C + 8 * lg;
+        const bfr *pt = a.w.PTb + ci * 2 * C * C + frag_off<C>(mrow, 0) + 8 * l;
+        const bfr *qt = a.w.QTb + (((size_t)b * a.Hk + hk) * a.NC + c) * D * C + frag_off<C>(16 * w, 0) + 8 * l;
+        const bfr *wt = a.w.nWTb + ci * D * C + frag_off<C>(16 * w, 0) + 8 * l;
 #pragma unroll
         for (int k = 0; k < 4; ++k) f.K[k] = r < n ? ld_frag(kb + 32 * k) : zero_frag();
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            f.PT[k] = ld_frag(pt + 32 * k);
-            f.PT[2 + k] = ld_frag(pt + C * C + 32 * k);
-            f.QT[k] = ld_frag(qt + 32 * k);
-            f.WT[k] = ld_frag(wt + 32 * k);
+            f.PT[k] = ld_frag(pt + FRAG_BLOCK * k);
+            f.PT[2 + k] = ld_frag(pt + C * C + FRAG_BLOCK * k);
+            f.QT[k] = ld_frag(qt + FRAG_BLOCK * k);
+            f.WT[k] = ld_frag(wt + FRAG_BLOCK * k);
         }
         f.g = tid < C ? a.w.G[ci * C + tid] : 0.0;
         if (ythr) {
