@@ -1751,16 +1751,15 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
             if (r < n) *reinterpret_cast<uint4 *>(dvp + (size_t)r * v_row + 64 * ch + c8) = x;
         }
     }
-    // P at this lane's pair positions (hi + lo planes), in flight during S4b and S5
-    uint32_t pP[2][4][2];
+    // P at this lane's pair positions (r = r0 + 4 lg + e, s = 32 ch + 16 t + li), read from the P^T tile (fragment
+    // order), where the four rows of one column are 8 contiguous bytes per plane; in flight during S4b and S5
+    uint2 pP[2][2];  // [t][hi, lo]
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const size_t pi = ci * 2 * C * C + frag_off<C>(r0 + 4 * lg + e, 32 * ch + 16 * t + li);
-            pP[t][e][0] = a.w.Pb[pi];
-            pP[t][e][1] = a.w.Pb[pi + C * C];
-        }
+    for (int t = 0; t < 2; ++t) {
+        const size_t pi = ci * 2 * C * C + frag_off<C>(32 * ch + 16 * t + li, r0 + 4 * lg);
+        pP[t][0] = *reinterpret_cast<const uint2 *>(a.w.PTb + pi);
+        pP[t][1] = *reinterpret_cast<const uint2 *>(a.w.PTb + pi + C * C);
+    }
     // ---- S4b: P9 t1 = dDelta V^T, P10 t2 = dW K^T; dT = (t1 + t2 diag(gamma)) diag(beta)
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc_N<false>(dWr[t], T16(O_DW), nullptr, LA, r0, 64 * ch + 16 * t, l);
@@ -1803,7 +1802,8 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
                 const float dav = s2 < r ? -da[t][e] : 0.f;
                 const float kg = kk[t][e] * gam;
                 rowB[e] += dav * kg;
-                Ep[t][e] = Ep[t][e] * (bf2f(pP[t][e][0]) + bf2f(pP[t][e][1])) + dav * sB[r] * kg;
+                const auto half = [e](uint2 v) { const uint32_t x = e < 2 ? v.x : v.y; return bf2f(e & 1 ? x >> 16 : x & 0xffffu); };
+                Ep[t][e] = Ep[t][e] * (half(pP[t][0]) + half(pP[t][1])) + dav * sB[r] * kg;
                 Mt[t][e] = sB[r] * dav * gam;
             }
     }
