@@ -2118,16 +2118,32 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
         vr[rr] = s2 < n ? *reinterpret_cast<const uint32_t *>(static_cast<const bfr *>(a.v) + v0 + s2 * v_row + vc)
                         : 0u;
     }
-    stage_N<C, D, NTP, false, false>(sK, nullptr, LK, static_cast<const bfr *>(a.k) + qk0, qk_row, n);
-    stage_N<C, D, NTP, false, false>(sQ, nullptr, LK, static_cast<const bfr *>(a.q) + qk0, qk_row, n);
+    // K and Q rows (16-byte pieces) and the gates: every load of the phase is issued before the first LDS store
+    constexpr int KPER = C * (D / 8) / NTP;
+    static_assert(KPER * NTP == C * (D / 8), "even split");
+    uint4 kr[KPER], qr[KPER];
+#pragma unroll
+    for (int p = 0; p < KPER; ++p) {
+        const int pc = tid + p * NTP, r = pc / (D / 8), c8 = (pc - r * (D / 8)) * 8;
+        const size_t o = qk0 + (size_t)r * qk_row + c8;
+        kr[p] = r < n ? *reinterpret_cast<const uint4 *>(static_cast<const bfr *>(a.k) + o) : make_uint4(0u, 0u, 0u, 0u);
+        qr[p] = r < n ? *reinterpret_cast<const uint4 *>(static_cast<const bfr *>(a.q) + o) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    float bt = 0.f, graw = 1.f;
+    if (tid < n) {
+        const size_t gi = ((size_t)b * T + t0 + tid) * a.Hv + hv;
+        bt = a.beta[gi];
+        graw = a.g[gi];
+    }
+#pragma unroll
+    for (int p = 0; p < KPER; ++p) {
+        const int pc = tid + p * NTP, r = pc / (D / 8), c8 = (pc - r * (D / 8)) * 8;
+        *reinterpret_cast<uint4 *>(sK + r * LK + c8) = kr[p];
+        *reinterpret_cast<uint4 *>(sQ + r * LK + c8) = qr[p];
+    }
     if (tid < C) {
         // inclusive prefix sum of the log decays in fp64 across wave 0
-        float bt = 0.f, gl = 0.f;
-        if (tid < n) {
-            const size_t gi = ((size_t)b * T + t0 + tid) * a.Hv + hv;
-            bt = a.beta[gi];
-            gl = gate_log(a.g[gi], a.gate);
-        }
+        const float gl = tid < n ? gate_log(graw, a.gate) : 0.f;
         const double x = wave_prefix_sum((double)gl);
         sB[tid] = bt;
         sG[tid] = x;
