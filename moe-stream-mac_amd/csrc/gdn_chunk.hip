@@ -2192,17 +2192,20 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
         mmab<D, 4>(acc, isq ? sQ : sK, nullptr, LK, r0, sK, nullptr, LK, 0);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            uint16_t ph[4], pl[4];
+            uint32_t ph[4], pl[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
+                // branch-free: the exponential is formed in every lane and selected (above the diagonal it may
+                // overflow; it is not used there)
                 const int r = r0 + 4 * lg + e, s2 = 16 * t + li;
-                const float gam = t <= rb && s2 <= r ? __builtin_amdgcn_exp2f((float)(sG2[r] - sG2[s2])) : 0.f;
+                const float ex = __builtin_amdgcn_exp2f((float)(sG2[r] - sG2[s2]));
+                const float gam = t <= rb && s2 <= r ? ex : 0.f;
                 if (isq) {
                     const float pv = acc[t][e] * gam;
-                    ph[e] = f32_to_bf16(pv);
-                    pl[e] = f32_to_bf16(pv - bf16_to_f32(ph[e]));
-                    sPb[r * C + s2] = ph[e];
-                    sPb[C * C + r * C + s2] = pl[e];
+                    ph[e] = bfbits(pv);
+                    pl[e] = bfbits(pv - bf2f(ph[e]));
+                    sPb[r * C + s2] = (bfr)ph[e];
+                    sPb[C * C + r * C + s2] = (bfr)pl[e];
                 } else {
                     sA[r * LDC + s2] = s2 < r ? sB[r] * acc[t][e] * gam : 0.f;
                 }
@@ -2210,9 +2213,8 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
             if (isq) {
                 // P^T [s][r]: this lane's four consecutive r of column s = 16t + li
                 bfr *pt = a.w.PTb + ci * 2 * C * C + frag_off<C>(16 * t + li, r0 + 4 * lg);
-                *reinterpret_cast<uint2 *>(pt) = make_uint2(ph[0] | ((uint32_t)ph[1] << 16), ph[2] | ((uint32_t)ph[3] << 16));
-                *reinterpret_cast<uint2 *>(pt + C * C) =
-                    make_uint2(pl[0] | ((uint32_t)pl[1] << 16), pl[2] | ((uint32_t)pl[3] << 16));
+                *reinterpret_cast<uint2 *>(pt) = make_uint2(ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16));
+                *reinterpret_cast<uint2 *>(pt + C * C) = make_uint2(pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16));
             }
         }
     }
@@ -2292,16 +2294,15 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
     } else {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            uint16_t wb[4];
+            uint32_t wb[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                wb[e] = f32_to_bf16(acc[t][e]);
-                sW[(r0 + 4 * lg + e) * LK + 16 * t + li] = wb[e];
+                wb[e] = bfbits(acc[t][e]);
+                sW[(r0 + 4 * lg + e) * LK + 16 * t + li] = (bfr)wb[e];
             }
             // -W^T [j][r]; bf16 negation flips the sign bit
             bfr *wt = a.w.nWTb + ci * D * C + frag_off<C>(16 * t + li, r0 + 4 * lg);
-            *reinterpret_cast<uint2 *>(wt) = make_uint2((wb[0] | ((uint32_t)wb[1] << 16)) ^ 0x80008000u,
-                                                        (wb[2] | ((uint32_t)wb[3] << 16)) ^ 0x80008000u);
+            *reinterpret_cast<uint2 *>(wt) = make_uint2((wb[0] | (wb[1] << 16)) ^ 0x80008000u, (wb[2] | (wb[3] << 16)) ^ 0x80008000u);
         }
     }
     __syncthreads();
