@@ -12,13 +12,15 @@ enum : int { GATE_DECAY = 0, GATE_DECAY_VEC = 1, GATE_LOG = 2 };
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
-// Round-to-nearest-even float -> bfloat16 (NaN stays a quiet NaN).
+// Round-to-nearest-even float -> bfloat16 (NaN stays a quiet NaN), in integer arithmetic.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     uint32_t u = __float_as_uint(f);
     if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
     u += 0x7fffu + ((u >> 16) & 1u);
     return (uint16_t)(u >> 16);
 }
+// The same rounding by gfx950's v_cvt_pk_bf16_f32 (no branch): faster for scattered single-element stores.
+__device__ __forceinline__ uint16_t f32_to_bf16_cvt(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // Load element i of a buffer of dtype dt as float.  dt is uniform across the wave.
 __device__ __forceinline__ float load_as_f32(const void *p, size_t i, int dt) {
@@ -31,7 +33,7 @@ __device__ __forceinline__ void store_from_f32(void *p, size_t i, float x, int d
     if (dt == DT_F32) {
         static_cast<float *>(p)[i] = x;
     } else if (dt == DT_BF16) {
-        static_cast<uint16_t *>(p)[i] = f32_to_bf16(x);
+        static_cast<uint16_t *>(p)[i] = f32_to_bf16_cvt(x);
     } else {
         static_cast<__half *>(p)[i] = __float2half(x);
     }
