@@ -281,7 +281,7 @@ __device__ __forceinline__ void blk16_mma(f4 &acc, const float *X, int ldx, cons
 // per block: T_ij = -T_ii sum_{u=j}^{i-1} A_iu T_uj (the inner sum goes through a wave-private 16x16 scratch to
 // become an operand).  scratch holds 3 * 256 floats.  Ends with a barrier.
 template <int NTH>
-__device__ void unit_lower_inverse(const float *sA, float *sT, float *scratch) {
+__device__ __forceinline__ void unit_lower_inverse(const float *sA, float *sT, float *scratch) {
     static_assert(NTH >= 3 * 64, "one wave per off-diagonal block of a round");
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     for (int i = tid; i < C * C; i += NTH) {
@@ -290,14 +290,15 @@ __device__ void unit_lower_inverse(const float *sA, float *sT, float *scratch) {
     }
     if (tid < 64) {
         const int base = (tid >> 4) * 16, cc = tid & 15;
+        // right-looking substitution: once x_u is final it updates every later row, so the dependency chain is
+        // 16 multiply-adds long instead of 120 (each x_r still receives its terms in the order u = 0, 1, ...)
         float col[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            float s = (r == cc) ? 1.f : 0.f;
+        for (int r = 0; r < 16; ++r) col[r] = (r == cc) ? 1.f : 0.f;
 #pragma unroll
-            for (int u = 0; u < r; ++u) s = fmaf(-sA[(base + r) * LDC + base + u], col[u], s);
-            col[r] = s;
-        }
+        for (int u = 0; u < 16; ++u)
+#pragma unroll
+            for (int r = u + 1; r < 16; ++r) col[r] = fmaf(-sA[(base + r) * LDC + base + u], col[u], col[r]);
 #pragma unroll
         for (int r = 0; r < 16; ++r) sT[(base + r) * LDC + base + cc] = col[r];
     }
