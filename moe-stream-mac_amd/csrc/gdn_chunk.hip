@@ -1389,8 +1389,9 @@ __device__ __forceinline__ void acc_N(const f4 &x, bfr *hi, bfr *lo, int ld, int
 
 // ---------------------------------------------------------------------------------------------- ck_bwd_local (bf16)
 //
-// The same products as ck_bwd_local_kernel<1>, on bf16 operand tiles.  One workgroup of 8 waves per chunk-head;
-// wave w owns the 16-row strip r0 = 16 (w % 4) and column half w / 4 of every [64][*] product.  Phases and their
+// The same products as ck_bwd_local_kernel, on bf16 operand tiles.  One workgroup of 8 waves per (chunk, key head)
+// takes the key head's value heads in turn; for each, wave w owns the 16-row strip r0 = 16 (w % 4) and column half
+// w / 4 of every [64][*] product.  Phases and their
 // tiles (byte offsets into one LDS arena; lifetimes checked against the barriers between phases):
 //   S1  P1 dQ = gamma dY h^T, P2 dW = -dDelta h^T, P3 dK = rc Delta dh'^T (Delta split),   h, dh', dDelta,
 //       P4 dp = dY Delta^T (Delta split)                                                 Delta hi/lo, dY
