@@ -1328,43 +1328,6 @@ struct Blk84 {
     }
 };
 
-// The same block of a tile stored as bf16 hi and lo planes (the lo plane `plane` elements after the hi one).
-struct Blk84Split {
-    uint2 hi[8], lo[8];
-    int rb, c0;
-    __device__ __forceinline__ void load(const bfr *src, size_t stride, size_t plane, int blk, int cols, int n) {
-        rb = blk / (cols / 4);
-        c0 = (blk - rb * (cols / 4)) * 4;
-#pragma unroll
-        for (int rr = 0; rr < 8; ++rr) {
-            const int r = rb * 8 + rr;
-            hi[rr] = r < n ? *reinterpret_cast<const uint2 *>(src + r * stride + c0) : make_uint2(0u, 0u);
-            lo[rr] = r < n ? *reinterpret_cast<const uint2 *>(src + plane + r * stride + c0) : make_uint2(0u, 0u);
-        }
-    }
-    static __device__ __forceinline__ uint32_t e16(const uint2 &v, int cc) {
-        const uint32_t w = cc < 2 ? v.x : v.y;
-        return cc & 1 ? w >> 16 : w & 0xffffu;
-    }
-    // dst[c][r] hi and lo: four stores of 8 consecutive rows each
-    __device__ __forceinline__ void store_T(bfr *dh, bfr *dl, int ldt) const {
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-            const uint4 h = make_uint4(e16(hi[0], cc) | (e16(hi[1], cc) << 16), e16(hi[2], cc) | (e16(hi[3], cc) << 16),
-                                       e16(hi[4], cc) | (e16(hi[5], cc) << 16), e16(hi[6], cc) | (e16(hi[7], cc) << 16));
-            const uint4 l = make_uint4(e16(lo[0], cc) | (e16(lo[1], cc) << 16), e16(lo[2], cc) | (e16(lo[3], cc) << 16),
-                                       e16(lo[4], cc) | (e16(lo[5], cc) << 16), e16(lo[6], cc) | (e16(lo[7], cc) << 16));
-            *reinterpret_cast<uint4 *>(dh + (c0 + cc) * ldt + rb * 8) = h;
-            *reinterpret_cast<uint4 *>(dl + (c0 + cc) * ldt + rb * 8) = l;
-        }
-    }
-    // dst[r][c] (hi): eight stores of 4 consecutive columns
-    __device__ __forceinline__ void store_N(bfr *nh, int ldn) const {
-#pragma unroll
-        for (int rr = 0; rr < 8; ++rr) *reinterpret_cast<uint2 *>(nh + (rb * 8 + rr) * ldn + c0) = hi[rr];
-    }
-};
-
 // MFMA accumulator tile X (rows m0 + 4(l/16) + e, column n0 + l%16) -> LDS, transposed (dst[n][m]: four
 // consecutive bf16 per lane) or natural (dst[m][n]).
 template <bool SPLIT>
@@ -1621,12 +1584,15 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
         }
     }
     __syncthreads();
-    // S4a's T hi / lo (threads 0-127, 8 x 4 blocks) and V (all), in flight during the S3 products
-    constexpr int NBT = (C / 8) * (C / 4), NDP = D * C / 8 / NTB;  // 16-byte pieces per plane and thread
-    static_assert(NBT <= NTB && NDP * NTB * 8 == D * C && C * (D / 8) == 2 * NTB, "block split");
-    Blk84Split bd;
-    const bool ist = tid < NBT;
-    if (ist) bd.load(Tc, C, (size_t)C * C, tid, C, C);
+    // S4a's T and V, in flight during the S3 products.  T: thread tid takes plane tid / 256 (hi, lo) and the 8-row x
+    // 2-column block tid % 256 of it (four-byte row pieces), so every wave stages an equal share
+    constexpr int NDP = D * C / 8 / NTB;  // 16-byte dDelta^T pieces per plane and thread
+    static_assert((C / 8) * (C / 2) * 2 == NTB && NDP * NTB * 8 == D * C && C * (D / 8) == 2 * NTB, "block split");
+    const int tpl = tid >> 8, tblk = tid & 255, trb = tblk / (C / 2), tc2 = 2 * (tblk - trb * (C / 2));
+    uint32_t tr[8];
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr)
+        tr[rr] = *reinterpret_cast<const uint32_t *>(Tc + (size_t)tpl * C * C + (trb * 8 + rr) * C + tc2);
     uint4 vr[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -1690,9 +1656,19 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
             *reinterpret_cast<uint4 *>(T16(O_DDTH) + i * LB + r8) = ddh[p];
             *reinterpret_cast<uint4 *>(T16(O_DDTL) + i * LB + r8) = ddlo[p];
         }
-        if (ist) {
-            bd.store_N(T16(O_TN), LB);
-            bd.store_T(T16(O_TTH), T16(O_TTL), LB);
+        // T^T (this thread's plane): two columns of eight consecutive rows; T [r][s] (hi plane only): eight row pieces
+        bfr *const tdst = T16(tpl ? O_TTL : O_TTH);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            uint32_t x[8];
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) x[rr] = cc ? tr[rr] >> 16 : tr[rr] & 0xffffu;
+            *reinterpret_cast<uint4 *>(tdst + (tc2 + cc) * LB + trb * 8) =
+                make_uint4(x[0] | (x[1] << 16), x[2] | (x[3] << 16), x[4] | (x[5] << 16), x[6] | (x[7] << 16));
+        }
+        if (tpl == 0) {
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) *reinterpret_cast<uint32_t *>(T16(O_TN) + (trb * 8 + rr) * LB + tc2) = tr[rr];
         }
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
