@@ -1434,11 +1434,12 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
         static_assert(SPER * NTB == D * (D / 8) && NPER * NTB == C * (D / 8), "even split");
         const bool yf32 = a.dy_dt == DT_F32;
         uint4 hr[SPER], dhr[SPER], dl[2 * NPER], yr[2 * NPER];
-        // dDelta (hi) into [r][i]: threads 0-255 each transpose one 8 (i) x 4 (r) block of the [i][r] plane
-        constexpr int NBDD = (D / 8) * (C / 4);
-        static_assert(NBDD <= NTB, "one dDelta block per thread");
-        Blk84 bdd;
-        if (tid < NBDD) bdd.load(dDc, C, tid, C, D);
+        // dDelta (hi) into [r][i]: every thread transposes one 8 (i) x 2 (r) block of the [i][r] plane
+        static_assert((D / 8) * (C / 2) == NTB, "one dDelta block per thread");
+        const int drb = tid / (C / 2), dc2 = 2 * (tid - drb * (C / 2));
+        uint32_t ddr[8];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) ddr[rr] = *reinterpret_cast<const uint32_t *>(dDc + (drb * 8 + rr) * C + dc2);
 #pragma unroll
         for (int p = 0; p < SPER; ++p) {
             hr[p] = reinterpret_cast<const uint4 *>(Hc)[tid + p * NTB];
@@ -1458,7 +1459,14 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
                               : make_uint4(0u, 0u, 0u, 0u);
             }
         }
-        if (tid < NBDD) bdd.store_T(T16(O_DD), LA);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            uint32_t x[8];
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) x[rr] = cc ? ddr[rr] >> 16 : ddr[rr] & 0xffffu;
+            *reinterpret_cast<uint4 *>(T16(O_DD) + (dc2 + cc) * LA + drb * 8) =
+                make_uint4(x[0] | (x[1] << 16), x[2] | (x[3] << 16), x[4] | (x[5] << 16), x[6] | (x[7] << 16));
+        }
         bfr *const th = T16(O_H), *const tdh = T16(O_DHH);
 #pragma unroll
         for (int p = 0; p < SPER; ++p) {
