@@ -107,7 +107,7 @@ size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int
  *   dbeta  [B][T][Hv] fp32
  *   dstate0 [B][Hv][Dv][Dk] fp32 (may be NULL)
  * dy has dy_dtype; dstate_T may be NULL (zero cotangent).  Results are deterministic (no atomics).
- * The chunked form needs 16-byte aligned q, k, v, dy, dq and dk. */
+ * The chunked form needs 16-byte aligned q, k, v, dy, dq, dk and dv. */
 int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
             const float *state0, const uint8_t *mask, const void *saved, size_t saved_bytes,
             const void *dy, const float *dstate_T,
