@@ -1429,15 +1429,16 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     }
     // S1 staging: every global load of the phase is issued before the first LDS store
     float lastp = 0.f;  // <dh', h>, the pair (C-1, chunk start)
+    static_assert((D / 8) * (C / 2) == NTB, "one dDelta block per thread");
+    const int drb = tid / (C / 2), dc2 = 2 * (tid - drb * (C / 2));
+    uint32_t ddr[8];  // rows i = 8 drb .. +7, columns r = dc2, dc2 + 1 of the dDelta^T hi plane
     {
         constexpr int SPER = D * (D / 8) / NTB, NPER = C * (D / 8) / NTB;  // 8-element chunks per thread
         static_assert(SPER * NTB == D * (D / 8) && NPER * NTB == C * (D / 8), "even split");
         const bool yf32 = a.dy_dt == DT_F32;
         uint4 hr[SPER], dhr[SPER], dl[2 * NPER], yr[2 * NPER];
-        // dDelta (hi) into [r][i]: every thread transposes one 8 (i) x 2 (r) block of the [i][r] plane
-        static_assert((D / 8) * (C / 2) == NTB, "one dDelta block per thread");
-        const int drb = tid / (C / 2), dc2 = 2 * (tid - drb * (C / 2));
-        uint32_t ddr[8];
+        // dDelta (hi) into [r][i]: every thread transposes one 8 (i) x 2 (r) block of the [i][r] plane (kept in
+        // registers for the dDelta^T hi tile of S4a)
 #pragma unroll
         for (int rr = 0; rr < 8; ++rr) ddr[rr] = *reinterpret_cast<const uint32_t *>(dDc + (drb * 8 + rr) * C + dc2);
 #pragma unroll
@@ -1651,17 +1652,15 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc_T<false>(dWr[t], T16(O_DWT), nullptr, LB, r0, 64 * ch + 16 * t, l);
     {
-        // dDelta^T hi / lo: straight copies of the [i][r] planes
-        uint4 ddh[NDP], ddlo[NDP];
+        // dDelta^T lo: a straight copy of the [i][r] plane; hi: this thread's S1 block, still in registers
+        uint4 ddlo[NDP];
 #pragma unroll
-        for (int p = 0; p < NDP; ++p) {
-            ddh[p] = reinterpret_cast<const uint4 *>(dDc)[tid + p * NTB];
-            ddlo[p] = reinterpret_cast<const uint4 *>(dDc + D * C)[tid + p * NTB];
-        }
+        for (int p = 0; p < NDP; ++p) ddlo[p] = reinterpret_cast<const uint4 *>(dDc + D * C)[tid + p * NTB];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) *reinterpret_cast<uint32_t *>(T16(O_DDTH) + (drb * 8 + rr) * LB + dc2) = ddr[rr];
 #pragma unroll
         for (int p = 0; p < NDP; ++p) {
             const int pc = tid + p * NTB, i = pc / (C / 8), r8 = (pc - i * (C / 8)) * 8;
-            *reinterpret_cast<uint4 *>(T16(O_DDTH) + i * LB + r8) = ddh[p];
             *reinterpret_cast<uint4 *>(T16(O_DDTL) + i * LB + r8) = ddlo[p];
         }
         // T^T (this thread's plane): two columns of eight consecutive rows; T [r][s] (hi plane only): eight row pieces
