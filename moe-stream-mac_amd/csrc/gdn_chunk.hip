@@ -1989,7 +1989,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
                     (bfr)bfbits(h[t][e]);
         }
         float *const sGam = sGamBuf[c & 1];
-        if (tid < C) sGam[tid] = expf((float)cur.g);
+        if (tid < C) sGam[tid] = __builtin_amdgcn_exp2f((float)(cur.g * 1.4426950408889634));  // v_exp_f32 on log2 units
         __syncthreads();
         if (c + 1 < a.NC) fetch(nxt, c + 1);
         // Delta = U - W h ; Yi = Q h
@@ -2428,8 +2428,8 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
         }
         if (tid < C) {  // wave 0 holds the chunk's cumulative log decays
             const double gl = readlane_f64(cur.g, C - 1);
-            sGam[tid] = expf((float)cur.g);
-            sRc[tid] = expf((float)(gl - cur.g));
+            sGam[tid] = __builtin_amdgcn_exp2f((float)(cur.g * 1.4426950408889634));  // v_exp_f32 on log2 units
+            sRc[tid] = __builtin_amdgcn_exp2f((float)((gl - cur.g) * 1.4426950408889634));
         }
         __syncthreads();
         const float gC = sGam[C - 1];
