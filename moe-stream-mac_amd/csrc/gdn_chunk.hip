@@ -1389,9 +1389,11 @@ static_assert(O_Y1T + SZ_D <= O_TTH, "S5 tiles stay clear of T^T");
 static_assert(ARENA <= 157 * 1024, "arena size");
 
 // One value head hv = hk * rep + rr of key head hk.  dq | dk of the key head: the value heads' fp32 parts are summed
-// in order (rr = 0, 1, ...) in the part rows of the key head, each thread reading back only the elements it wrote
-// itself, and the last value head writes dq and dk in the gradient dtype.
-__device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk, int b, int rr, int rep) {
+// in order (rr = 0, 1, ...), dq in the part rows of the key head (each thread reading back only the elements it
+// wrote itself), dk in registers (ck: the four 16-byte row pieces this thread writes out), and the last value head
+// writes dq and dk in the gradient dtype.
+__device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk, int b, int rr, int rep,
+                                                    float4 (&ck)[4]) {
     __shared__ __align__(16) unsigned char arena[ARENA];
     __shared__ double sG[C];
     __shared__ float sGam[C], sRc[C], sB[C], sScan[2][C];
@@ -1811,8 +1813,7 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     __syncthreads();
     mmab<C, 4>(dK, T16(O_MM), nullptr, LB, r0, T16(O_KT), nullptr, LB, 64 * ch, l);
     __syncthreads();  // sM, M + M^T and K^T read: the pair matrix E reuses sM, the dk staging the space below
-    // dK staged as fp32 rows in the free arena for 16-byte stores, and the running dk sum of the previous value
-    // heads at this thread's row pieces, in flight during the straddle sums
+    // dK staged as fp32 rows in the free arena for 16-byte stores
     float *const sp = reinterpret_cast<float *>(arena);
     constexpr int LP = D + 4, PER = C * D / 4 / NTB;
     static_assert(C * LP * 4 <= O_SM, "part staging below the pair matrix");
@@ -1821,15 +1822,6 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) sp[(r0 + 4 * lg + e) * LP + 64 * ch + 16 * t + li] = dK[t][e];
-    float4 prevk[PER];
-    if (!first) {
-#pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            const int i = tid + p * NTB, r = i / (D / 4), c4 = (i - r * (D / 4)) * 4;
-            prevk[p] = r < n ? *reinterpret_cast<const float4 *>(part_row + (size_t)r * part_rs + D + c4)
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    }
     // ---- straddle sums for dg, dbeta, outputs
     float *const sE = sM;
 #pragma unroll
@@ -1855,10 +1847,10 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
         const int i = tid + p * NTB, r = i / (D / 4), c4 = (i - r * (D / 4)) * 4;
         if (r >= n) continue;
         float4 v = *reinterpret_cast<const float4 *>(sp + r * LP + c4);
-        if (!first) v = make_float4(prevk[p].x + v.x, prevk[p].y + v.y, prevk[p].z + v.z, prevk[p].w + v.w);
+        if (!first) v = make_float4(ck[p].x + v.x, ck[p].y + v.y, ck[p].z + v.z, ck[p].w + v.w);
         const size_t o = qk_out + (size_t)r * a.Hk * D + c4;
         if (!last) {
-            *reinterpret_cast<float4 *>(part_row + (size_t)r * part_rs + D + c4) = v;
+            ck[p] = v;
         } else if (a.grad_dt == DT_BF16) {
             *reinterpret_cast<uint2 *>(static_cast<bfr *>(a.dk) + o) = make_uint2(pk(v.x, v.y), pk(v.z, v.w));
         } else if (a.grad_dt == DT_F32) {
@@ -1877,11 +1869,13 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
 __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     typedef const __attribute__((address_space(4))) Args *KArgs;  // the kernel arguments (constant memory)
     const int rep = a.Hv / a.Hk;
+    float4 ck[4];  // the running dk sum of the value heads done so far
+    static_assert(C * D / 4 / NTB == 4, "four dk row pieces per thread");
     for (int rr = 0; rr < rep; ++rr) {
         // the arguments are read anew for each value head instead of being held in scalar registers across it
         KArgs ap = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
         asm volatile("" : "+s"(ap));
-        bwd_local_bf16_head(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep);
+        bwd_local_bf16_head(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep, ck);
     }
 }
 
