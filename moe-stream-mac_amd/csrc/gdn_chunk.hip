@@ -1388,12 +1388,14 @@ static_assert(O_V + SZ_A <= ARENA, "arena");
 static_assert(O_Y1T + SZ_D <= O_TTH, "S5 tiles stay clear of T^T");
 static_assert(ARENA <= 157 * 1024, "arena size");
 
+constexpr int NQR = 2;  // dq row pieces per thread whose running sum stays in registers (of four)
+
 // One value head hv = hk * rep + rr of key head hk.  dq | dk of the key head: the value heads' fp32 parts are summed
-// in order (rr = 0, 1, ...), dq in the part rows of the key head (each thread reading back only the elements it
-// wrote itself), dk in registers (ck: the four 16-byte row pieces this thread writes out), and the last value head
-// writes dq and dk in the gradient dtype.
+// in order (rr = 0, 1, ...) at the 16-byte row pieces each thread writes out: dk (ck) and the first NQR dq pieces
+// (cq) in registers, the other dq pieces in the part rows of the key head (each thread reading back only the
+// elements it wrote itself); the last value head writes dq and dk in the gradient dtype.
 __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk, int b, int rr, int rep,
-                                                    float4 (&ck)[4]) {
+                                                    float4 (&ck)[4], float4 (&cq)[NQR]) {
     __shared__ __align__(16) unsigned char arena[ARENA];
     __shared__ double sG[C];
     __shared__ float sGam[C], sRc[C], sB[C], sScan[2][C];
@@ -1588,7 +1590,7 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     float4 prevq[4];
     if (!first) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
+        for (int p = NQR; p < 4; ++p) {
             const int i = l + 64 * p, r = r0 + (i >> 4), c4 = 64 * ch + 4 * (i & 15);
             prevq[p] = r < n ? *reinterpret_cast<const float4 *>(part_row + (size_t)r * part_rs + c4)
                              : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1634,10 +1636,14 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
         const int i = l + 64 * p, rr = i >> 4, r = r0 + rr, c4 = 64 * ch + 4 * (i & 15);
         float4 v = *reinterpret_cast<const float4 *>(stq + rr * LQ + 4 * (i & 15));
         if (r >= n) continue;
-        if (!first) v = make_float4(prevq[p].x + v.x, prevq[p].y + v.y, prevq[p].z + v.z, prevq[p].w + v.w);
+        if (!first) {
+            const float4 s = p < NQR ? cq[p < NQR ? p : 0] : prevq[p];
+            v = make_float4(s.x + v.x, s.y + v.y, s.z + v.z, s.w + v.w);
+        }
         const size_t o = qk_out + (size_t)r * a.Hk * D + c4;
         if (!last) {
-            *reinterpret_cast<float4 *>(part_row + (size_t)r * part_rs + c4) = v;
+            if (p < NQR) cq[p < NQR ? p : 0] = v;
+            else *reinterpret_cast<float4 *>(part_row + (size_t)r * part_rs + c4) = v;
         } else if (a.grad_dt == DT_BF16) {
             *reinterpret_cast<uint2 *>(static_cast<bfr *>(a.dq) + o) = make_uint2(pk(v.x, v.y), pk(v.z, v.w));
         } else if (a.grad_dt == DT_F32) {
@@ -1869,13 +1875,13 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
 __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     typedef const __attribute__((address_space(4))) Args *KArgs;  // the kernel arguments (constant memory)
     const int rep = a.Hv / a.Hk;
-    float4 ck[4];  // the running dk sum of the value heads done so far
+    float4 ck[4], cq[NQR];  // the running dk sum and part of the running dq sum of the value heads done so far
     static_assert(C * D / 4 / NTB == 4, "four dk row pieces per thread");
     for (int rr = 0; rr < rep; ++rr) {
         // the arguments are read anew for each value head instead of being held in scalar registers across it
         KArgs ap = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
         asm volatile("" : "+s"(ap));
-        bwd_local_bf16_head(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep, ck);
+        bwd_local_bf16_head(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep, ck, cq);
     }
 }
 
