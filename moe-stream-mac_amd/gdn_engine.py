@@ -45,6 +45,9 @@ def _saved_bytes(lib, B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form) -> int:
 class _GDNRecurrence(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, g, beta, state, mask, chunk, log_gate, out_dtype, need_saved, form):
+        # an output that the loss does not use reaches backward as None instead of a zero tensor filled for it
+        # (the library takes a NULL exit-state cotangent as zero)
+        ctx.set_materialize_grads(False)
         dev = _require_device(q, k, v, g, beta, state)
         B, T, Hk, Dk = q.shape
         Hv, Dv = v.shape[2], v.shape[3]
@@ -190,5 +193,8 @@ class _NoCtx:
     """Stand-in ctx for calling the forward without building an autograd node."""
 
     def save_for_backward(self, *args):
+        pass
+
+    def set_materialize_grads(self, value):
         pass
 
