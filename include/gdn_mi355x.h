@@ -4,7 +4,7 @@
  *   A = S * decay;  r = v - A k;  delta = beta r;  S~ = A + delta (x) k;  y = S~ q;
  *   S_next = mask ? S~ : S            (y always reads the candidate S~)
  * with S the [Dv][Dk] state of one head.  This is the arithmetic of the reference's
- * tools/gdn_vjp.py:3-25 (_step_parts :238-256) and engine/include/gdn.h:217-226.
+ * tools/gdn_vjp.py:3-25 (_step_parts :238-256) and engine/include/gdn.h:27-38 (engine/src/gdn.c:63-108).
  *
  * Layouts (all row-major, contiguous):
  *   q, k    [B][T][Hk][Dk]          dtype in_dtype (GDN_F32 / GDN_BF16 / GDN_F16)
@@ -50,7 +50,7 @@ enum gdn_gate {
 enum gdn_form {
     GDN_FORM_AUTO = 0,       /* the chunked form when eligible, else the recurrent form */
     GDN_FORM_RECURRENT = 1,  /* token-sequential recurrence, state rows resident in VGPRs; any shape */
-    GDN_FORM_CHUNK = 2       /* chunked WY/UT form on MFMA (chunk 64); Dk = Dv = 128, no mask, scalar gate */
+    GDN_FORM_CHUNK = 2       /* chunked WY/UT form on MFMA (64-token tiles); Dk = Dv = 128, no mask, scalar gate */
 };
 
 /* Library version, (major << 16) | minor. */
@@ -76,26 +76,44 @@ int64_t gdn_num_snapshots(int T, int chunk);
  * requested form cannot run them.  gdn_fwd and gdn_bwd resolve the form the same way. */
 int gdn_select_form(int Dk, int Dv, int has_mask, int gate_kind, int form);
 
-/* Size of the buffer gdn_fwd fills for gdn_bwd (the "saved" activations).  Recurrent form: the chunk
- * snapshots.  Chunked form: per 64-token chunk, the entry state, the cumulative log decays, T = (I+A)^-1, the
- * intra-chunk output matrix, W, U and Delta (all recomputable from the inputs; kept because HBM is ample). */
+/* What `chunk` means.
+ *   Recurrent form: the forward keeps the state every `chunk` tokens (gdn_num_snapshots) and the backward replays
+ *   each chunk from its snapshot.
+ *   Chunked form (WY/UT, 64-token MFMA tiles whatever `chunk` is):
+ *     chunk <= 64  the forward keeps every 64-token tile the backward reads (fastest; the saved buffer grows with
+ *                  T at about 3.2 KiB (bf16) / 4.2 KiB (fp32) per head-token);
+ *     chunk > 64   checkpointing (tools/gdn_checkpoint.py:39-50): windows of W = chunk rounded up to a multiple of
+ *                  64 tokens; the forward keeps only the ceil(T / W) - 1 fp32 states at the window boundaries, and
+ *                  the backward rebuilds the tiles of one group of windows at a time from them.
+ *   A forward-only call (saved = NULL) of the chunked form keeps nothing and runs group by group in the workspace.
+ * Group-wise calls use the largest group of windows (or of 64-token chunks, forward-only) that fits the workspace
+ * given, up to the size the *_workspace_bytes queries return; fewer groups is faster, one window (chunk) is the
+ * minimum. */
+
+/* Size of the buffer gdn_fwd fills for gdn_bwd (the "saved" activations) for inputs of in_dtype. */
 size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind, int has_mask,
-                       int form);
+                       int form, int in_dtype);
+
+/* Device workspace gdn_fwd uses during the call (released afterwards), with or without a saved buffer; 0 when the
+ * call needs none (the recurrent form; the chunked form with chunk <= 64 and a saved buffer). */
+size_t gdn_fwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind, int has_mask,
+                               int form, int in_dtype, int with_saved);
 
 /* Forward.  Replaces the forward of gated_delta_chunked (tools/gdn_vjp.py:503-528 via _forward :205-235)
  * and of gated_delta_ops_checkpointed (tools/gdn_checkpoint.py:53-95).
  * Writes y (out_dtype), state_T (fp32; may be NULL) and, when saved is not NULL, the gdn_saved_bytes()
- * buffer gdn_bwd reads.  In the recurrent form saved may be NULL: the forward-only path of frozen layers
- * (tools/frozen_gdn.py:19-25, mlx-lm gated_delta_kernel); the chunked form always needs it. */
+ * buffer gdn_bwd reads.  saved = NULL is the forward-only path of frozen layers (tools/frozen_gdn.py:19-25,
+ * mlx-lm gated_delta_kernel): nothing is kept.  workspace: gdn_fwd_workspace_bytes() bytes (256-byte aligned),
+ * or NULL when that is 0. */
 int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
             const float *state0, const uint8_t *mask,
-            void *y, float *state_T, void *saved, size_t saved_bytes,
+            void *y, float *state_T, void *saved, size_t saved_bytes, void *workspace, size_t workspace_bytes,
             int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk,
             int in_dtype, int out_dtype, int gate_kind, int form, void *stream);
 
 /* Device workspace gdn_bwd needs, in bytes (256-byte aligned base expected). */
 size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind,
-                               int has_mask, int form);
+                               int has_mask, int form, int in_dtype);
 
 /* Backward (VJP).  Replaces _backward / _chunk_vjp / the Metal kernel gdn_chunk_backward
  * (tools/gdn_vjp.py:273-320, :341-423, :426-474) and the mx.checkpoint recompute of
@@ -107,7 +125,7 @@ size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int
  *   dbeta  [B][T][Hv] fp32
  *   dstate0 [B][Hv][Dv][Dk] fp32 (may be NULL)
  * dy has dy_dtype; dstate_T may be NULL (zero cotangent).  Results are deterministic (no atomics).
- * The chunked form needs 16-byte aligned q, k, v, dy, dq, dk and dv. */
+ * The chunked form needs 16-byte aligned q, k, v, dy, dq, dk and dv, and with bf16 inputs a bf16 or fp32 dy. */
 int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
             const float *state0, const uint8_t *mask, const void *saved, size_t saved_bytes,
             const void *dy, const float *dstate_T,

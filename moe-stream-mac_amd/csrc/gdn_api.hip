@@ -6,7 +6,9 @@
 
 #include <map>
 #include <mutex>
+#include <algorithm>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "gdn_common.h"
@@ -145,13 +147,83 @@ static size_t rec_saved_bytes(int B, int T, int Hv, int Dk, int Dv, int chunk) {
     return (size_t)(ns > 0 ? ns : 0) * B * Hv * Dv * Dk * sizeof(float);
 }
 
+// ---- chunked form: how a call is split
+//
+// chunk <= 64 keeps the whole tile set from forward to backward ("saved").  chunk > 64 checkpoints: the forward keeps
+// only the states at every window of W = chunk rounded up to 64 tokens (ceil(T / W) - 1 fp32 snapshots, like the
+// recurrent form's boundaries), and the backward rebuilds one group of windows at a time (prep, then the forward of
+// every window of the group side by side from its snapshot) before running the backward stages over that group.
+// A forward-only call (no saved buffer) runs group by group as well.  Groups live in the caller's workspace: the
+// largest whole number of units (windows, or 64-token chunks when forward-only) that fits, capped at about
+// kGroupChunkHeads chunk-heads.
+
+constexpr int kGroupChunkHeads = 2048;
+
+static int ck_window(int chunk) { return chunk <= kChunkC ? 0 : (chunk + kChunkC - 1) / kChunkC * kChunkC; }
+
+static size_t ck_state_bytes(int B, int Hv) { return (size_t)B * Hv * kChunkD * kChunkD * sizeof(float); }
+
+static size_t ck_snap_bytes(int B, int T, int Hv, int W) {
+    const int nwin = (T + W - 1) / W;
+    return nwin > 1 ? (size_t)(nwin - 1) * ck_state_bytes(B, Hv) : 0;
+}
+
+struct CkShape {
+    int B, T, Hk, Hv;
+    bool bf16;
+};
+
+// Forward group workspace: the forward tile set of Tg tokens, plus two carried states between groups when no
+// snapshots carry them.
+static size_t ck_fwd_group_bytes(const CkShape &s, int Tg, bool ckpt) {
+    return chunk_sizes(s.B, Tg, s.Hk, s.Hv, s.bf16, false).saved + (ckpt ? 0 : 2 * align256(ck_state_bytes(s.B, s.Hv)));
+}
+
+// Backward group workspace: two carried state adjoints, the whole tile set and the backward buffers of Tg tokens.
+static size_t ck_bwd_group_bytes(const CkShape &s, int Tg) {
+    const ChunkSizes cs = chunk_sizes(s.B, Tg, s.Hk, s.Hv, s.bf16, true);
+    return 2 * align256(ck_state_bytes(s.B, s.Hv)) + align256(cs.saved) + cs.work;
+}
+
+// Units of u tokens per group: the target count, or fewer when the workspace is smaller; 0 when one unit does not fit.
+template <class Bytes>
+static int ck_group_units(const CkShape &s, int u, size_t avail, Bytes bytes) {
+    const int total = (s.T + u - 1) / u;
+    const size_t per_unit = (size_t)s.B * s.Hv * (u / kChunkC);
+    int g = (int)std::max<size_t>(1, kGroupChunkHeads / per_unit);
+    g = std::min(g, total);
+    for (; g >= 1; --g)
+        if (bytes(std::min(g * u, s.T)) <= avail) return g;
+    return 0;
+}
+
+static size_t ck_fwd_target_bytes(const CkShape &s, int W, bool ckpt) {
+    const int u = ckpt ? W : kChunkC;
+    const int g = ck_group_units(s, u, SIZE_MAX, [](int) { return (size_t)0; });
+    return ck_fwd_group_bytes(s, std::min(g * u, s.T), ckpt);
+}
+
+static size_t ck_bwd_target_bytes(const CkShape &s, int W) {
+    const int g = ck_group_units(s, W, SIZE_MAX, [](int) { return (size_t)0; });
+    return ck_bwd_group_bytes(s, std::min(g * W, s.T));
+}
+
+static size_t dt_size(int dt) { return dt == DT_F32 ? 4 : 2; }
+
+template <class P>
+static P *tok_offset(P *p, size_t elems, int dt) {
+    if (!p) return p;
+    using C = typename std::conditional<std::is_const<P>::value, const char, char>::type;
+    return reinterpret_cast<P *>(reinterpret_cast<C *>(p) + elems * dt_size(dt));
+}
+
 }  // namespace gdn
 
 using namespace gdn;
 
 extern "C" {
 
-int gdn_version(void) { return (1 << 16) | 0; }
+int gdn_version(void) { return (2 << 16) | 0; }
 
 int gdn_profile_enable(int on) {
     std::lock_guard<std::mutex> lk(g_prof_mu);
@@ -204,18 +276,220 @@ int gdn_select_form(int Dk, int Dv, int has_mask, int gate_kind, int form) {
 }
 
 size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind, int has_mask,
-                       int form) {
+                       int form, int in_dtype) {
     if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
     const int f = resolve_form(Dk, Dv, has_mask, gate_kind, form);
     if (f < 0 || B == 0 || T == 0) return 0;
-    if (f == GDN_FORM_CHUNK) return chunk_sizes(B, T, Hv).saved;
+    if (f == GDN_FORM_CHUNK) {
+        const int W = ck_window(chunk);
+        if (W) return ck_snap_bytes(B, T, Hv, W);
+        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true).saved;
+    }
     return rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
 }
 
+size_t gdn_fwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind, int has_mask,
+                               int form, int in_dtype, int with_saved) {
+    if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
+    const int f = resolve_form(Dk, Dv, has_mask, gate_kind, form);
+    if (f != GDN_FORM_CHUNK || B == 0 || T == 0) return 0;
+    const int W = ck_window(chunk);
+    if (with_saved && !W) return 0;
+    return ck_fwd_target_bytes({B, T, Hk, Hv, in_dtype == DT_BF16}, W, with_saved != 0);
+}
+
+}  // extern "C"
+
+namespace gdn {
+
+// Chunked forward (resolved form GDN_FORM_CHUNK, arguments checked).
+static int ck_forward(const ChunkCall &base, int chunk, void *saved, size_t saved_bytes, void *ws, size_t ws_bytes,
+                      hipStream_t st) {
+    const int B = base.B, T = base.T, Hk = base.Hk, Hv = base.Hv;
+    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16};
+    const int W = ck_window(chunk);
+    int rc;
+    if (saved && !W) {  // the whole tile set, kept for the backward
+        const size_t need = chunk_sizes(B, T, Hk, Hv, shp.bf16, true).saved;
+        if (saved_bytes < need)
+            return fail(GDN_ERR_WORKSPACE, "saved buffer of %zu bytes is smaller than the %zu bytes required",
+                        saved_bytes, need);
+        ChunkCall cc = base;
+        cc.tiles = saved;
+        cc.Ts = T;
+        {
+            Timed tm("ck_prep", st);
+            launch_chunk_stage(cc, "prep", st);
+        }
+        if ((rc = check_launch(st, "gdn_fwd(ck_prep)"))) return rc;
+        {
+            Timed tm("ck_fwd", st);
+            launch_chunk_stage(cc, "fwd", st);
+        }
+        return check_launch(st, "gdn_fwd(ck_fwd)");
+    }
+    const bool ckpt = saved != nullptr;
+    float *snap = static_cast<float *>(saved);
+    if (ckpt && saved_bytes < ck_snap_bytes(B, T, Hv, W))
+        return fail(GDN_ERR_WORKSPACE, "saved buffer of %zu bytes is smaller than the %zu bytes of snapshots",
+                    saved_bytes, ck_snap_bytes(B, T, Hv, W));
+    const int u = ckpt ? W : kChunkC;
+    const int units = ck_group_units(shp, u, ws ? ws_bytes : 0,
+                                     [&](int Tg) { return ck_fwd_group_bytes(shp, Tg, ckpt); });
+    if (units == 0)
+        return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes of one %d-token group",
+                    ws ? ws_bytes : 0, ck_fwd_group_bytes(shp, std::min(u, T), ckpt), u);
+    const int Gt = units * u;
+    const size_t sb = align256(ck_state_bytes(B, Hv)), S = (size_t)B * Hv * kChunkD * kChunkD;
+    char *w8 = static_cast<char *>(ws);
+    float *carry[2] = {nullptr, nullptr};
+    if (!ckpt) {
+        carry[0] = reinterpret_cast<float *>(w8);
+        carry[1] = reinterpret_cast<float *>(w8 + sb);
+        w8 += 2 * sb;
+    }
+    for (int g = 0, ts = 0; ts < T; ++g, ts += Gt) {
+        const int Tg = std::min(Gt, T - ts);
+        const bool last = ts + Tg >= T;
+        ChunkCall cc = base;
+        cc.q = tok_offset(base.q, (size_t)ts * Hk * kChunkD, base.in_dt);
+        cc.k = tok_offset(base.k, (size_t)ts * Hk * kChunkD, base.in_dt);
+        cc.v = tok_offset(base.v, (size_t)ts * Hv * kChunkD, base.in_dt);
+        cc.g = base.g + (size_t)ts * Hv;
+        cc.beta = base.beta + (size_t)ts * Hv;
+        cc.y = tok_offset(base.y, (size_t)ts * Hv * kChunkD, base.out_dt);
+        cc.T = Tg;
+        cc.Ts = T;
+        cc.tiles = w8;
+        cc.fwd_only = 1;
+        if (ckpt) {
+            const int win0 = ts / W;
+            cc.snap = snap;
+            cc.wc = W / kChunkC;
+            cc.win0 = win0;
+            cc.state0 = g == 0 ? base.state0 : snap + (size_t)(win0 - 1) * S;
+            cc.state_T = last ? base.state_T : snap + (size_t)(win0 + Gt / W - 1) * S;
+        } else {
+            cc.state0 = g == 0 ? base.state0 : carry[g & 1];
+            cc.state_T = last ? base.state_T : carry[(g + 1) & 1];
+        }
+        {
+            Timed tm("ck_prep", st);
+            launch_chunk_stage(cc, "prep", st);
+        }
+        if ((rc = check_launch(st, "gdn_fwd(ck_prep)"))) return rc;
+        {
+            Timed tm("ck_fwd", st);
+            launch_chunk_stage(cc, "fwd", st);
+        }
+        if ((rc = check_launch(st, "gdn_fwd(ck_fwd)"))) return rc;
+    }
+    return GDN_OK;
+}
+
+// Chunked backward (resolved form GDN_FORM_CHUNK, arguments checked).
+static int ck_backward(const ChunkCall &base, int chunk, const void *saved, size_t saved_bytes, void *ws,
+                       size_t ws_bytes, hipStream_t st) {
+    const int B = base.B, T = base.T, Hk = base.Hk, Hv = base.Hv;
+    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16};
+    const int W = ck_window(chunk);
+    int rc;
+    if (!W) {
+        const ChunkSizes cs = chunk_sizes(B, T, Hk, Hv, shp.bf16, true);
+        if (!saved || saved_bytes < cs.saved)
+            return fail(GDN_ERR_INVALID, "the saved buffer written by gdn_fwd (%zu bytes) is required", cs.saved);
+        if (!ws || ws_bytes < cs.work)
+            return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", ws_bytes,
+                        cs.work);
+        ChunkCall cc = base;
+        cc.tiles = const_cast<void *>(saved);
+        cc.work = ws;
+        cc.Ts = T;
+        {
+            Timed tm("ck_bwd_seq", st);
+            launch_chunk_stage(cc, "seq", st);
+        }
+        if ((rc = check_launch(st, "gdn_bwd(ck_bwd_seq)"))) return rc;
+        {
+            Timed tm("ck_bwd_local", st);
+            launch_chunk_stage(cc, "local", st);
+        }
+        return check_launch(st, "gdn_bwd(ck_bwd_local)");
+    }
+    const size_t need_snap = ck_snap_bytes(B, T, Hv, W);
+    if (need_snap && (!saved || saved_bytes < need_snap))
+        return fail(GDN_ERR_INVALID, "the snapshots written by gdn_fwd (%zu bytes) are required", need_snap);
+    const int units = ck_group_units(shp, W, ws ? ws_bytes : 0, [&](int Tg) { return ck_bwd_group_bytes(shp, Tg); });
+    if (units == 0)
+        return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes of one %d-token group",
+                    ws ? ws_bytes : 0, ck_bwd_group_bytes(shp, std::min(W, T)), W);
+    const int Gt = units * W, ng = (T + Gt - 1) / Gt;
+    const size_t sb = align256(ck_state_bytes(B, Hv));
+    char *w8 = static_cast<char *>(ws);
+    float *carry[2] = {reinterpret_cast<float *>(w8), reinterpret_cast<float *>(w8 + sb)};
+    const ChunkSizes full = chunk_sizes(B, std::min(Gt, T), Hk, Hv, shp.bf16, true);
+    char *tiles = w8 + 2 * sb, *work = tiles + align256(full.saved);
+    for (int g = ng - 1; g >= 0; --g) {
+        const int ts = g * Gt, Tg = std::min(Gt, T - ts);
+        const size_t qk = (size_t)ts * Hk * kChunkD, vv = (size_t)ts * Hv * kChunkD;
+        ChunkCall cc = base;
+        cc.q = tok_offset(base.q, qk, base.in_dt);
+        cc.k = tok_offset(base.k, qk, base.in_dt);
+        cc.v = tok_offset(base.v, vv, base.in_dt);
+        cc.g = base.g + (size_t)ts * Hv;
+        cc.beta = base.beta + (size_t)ts * Hv;
+        cc.dy = tok_offset(base.dy, vv, base.dy_dt);
+        cc.dq = tok_offset(base.dq, qk, base.grad_dt);
+        cc.dk = tok_offset(base.dk, qk, base.grad_dt);
+        cc.dv = tok_offset(base.dv, vv, base.grad_dt);
+        cc.dg = base.dg + (size_t)ts * Hv;
+        cc.dbeta = base.dbeta + (size_t)ts * Hv;
+        cc.T = Tg;
+        cc.Ts = T;
+        cc.tiles = tiles;
+        cc.work = work;
+        {
+            Timed tm("ck_prep", st);
+            launch_chunk_stage(cc, "prep", st);
+        }
+        if ((rc = check_launch(st, "gdn_bwd(ck_prep)"))) return rc;
+        {
+            ChunkCall rf = cc;  // every window of the group from its entry state: H and Delta only
+            rf.recompute = 1;
+            rf.snap = static_cast<float *>(const_cast<void *>(saved));
+            rf.wc = W / kChunkC;
+            rf.win0 = ts / W;
+            rf.state0 = base.state0;
+            rf.y = nullptr;
+            rf.state_T = nullptr;
+            Timed tm("ck_fwd_recompute", st);
+            launch_chunk_stage(rf, "fwd", st);
+        }
+        if ((rc = check_launch(st, "gdn_bwd(ck_fwd recompute)"))) return rc;
+        cc.dstate_T = g == ng - 1 ? base.dstate_T : carry[(g + 1) & 1];
+        cc.dstate0 = g == 0 ? base.dstate0 : carry[g & 1];
+        {
+            Timed tm("ck_bwd_seq", st);
+            launch_chunk_stage(cc, "seq", st);
+        }
+        if ((rc = check_launch(st, "gdn_bwd(ck_bwd_seq)"))) return rc;
+        {
+            Timed tm("ck_bwd_local", st);
+            launch_chunk_stage(cc, "local", st);
+        }
+        if ((rc = check_launch(st, "gdn_bwd(ck_bwd_local)"))) return rc;
+    }
+    return GDN_OK;
+}
+
+}  // namespace gdn
+
+extern "C" {
+
 int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
             const float *state0, const uint8_t *mask, void *y, float *state_T, void *saved, size_t saved_bytes,
-            int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int in_dtype, int out_dtype, int gate_kind,
-            int form, void *stream) {
+            void *workspace, size_t workspace_bytes, int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk,
+            int in_dtype, int out_dtype, int gate_kind, int form, void *stream) {
     g_err[0] = 0;
     int rc = check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form);
     if (rc) return rc;
@@ -232,26 +506,12 @@ int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const f
     if (f == GDN_FORM_CHUNK) {
         if (misaligned16(q) || misaligned16(k) || misaligned16(v))
             return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned q, k and v");
-        // the chunked form always needs its per-chunk buffers, also for a forward-only call
-        const size_t need = chunk_sizes(B, T, Hv).saved;
-        if (!saved || saved_bytes < need)
-            return fail(GDN_ERR_WORKSPACE, "saved buffer of %zu bytes is smaller than the %zu bytes required",
-                        saved_bytes, need);
         ChunkCall cc{};
         cc.q = q; cc.k = k; cc.v = v; cc.g = g; cc.beta = beta; cc.state0 = state0;
-        cc.y = y; cc.state_T = state_T; cc.saved = saved;
-        cc.B = B; cc.T = T; cc.Hk = Hk; cc.Hv = Hv; cc.in_dt = in_dtype; cc.out_dt = out_dtype; cc.gate = gate_kind;
-        {
-            Timed tm("ck_prep", st);
-            launch_chunk_stage(cc, "prep", st);
-        }
-        rc = check_launch(st, "gdn_fwd(ck_prep)");
-        if (rc) return rc;
-        {
-            Timed tm("ck_fwd", st);
-            launch_chunk_stage(cc, "fwd", st);
-        }
-        return check_launch(st, "gdn_fwd(ck_fwd)");
+        cc.y = y; cc.state_T = state_T;
+        cc.B = B; cc.T = T; cc.Ts = T; cc.Hk = Hk; cc.Hv = Hv; cc.in_dt = in_dtype; cc.out_dt = out_dtype;
+        cc.gate = gate_kind;
+        return ck_forward(cc, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
     }
     const size_t need = rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
     float *snaps = nullptr;
@@ -271,11 +531,16 @@ int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const f
 }
 
 size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind,
-                               int has_mask, int form) {
+                               int has_mask, int form, int in_dtype) {
     if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
     const int f = resolve_form(Dk, Dv, has_mask, gate_kind, form);
     if (f < 0) return 0;
-    if (f == GDN_FORM_CHUNK) return chunk_sizes(B, T, Hv).work;
+    if (f == GDN_FORM_CHUNK) {
+        if (B == 0 || T == 0) return 0;
+        const int W = ck_window(chunk);
+        if (W) return ck_bwd_target_bytes({B, T, Hk, Hv, in_dtype == DT_BF16}, W);
+        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true).work;
+    }
     return bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind).total;
 }
 
@@ -299,11 +564,25 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
     }
     if (!q || !k || !v || !g || !beta || !dy || !dq || !dk || !dv || !dg || !dbeta)
         return fail(GDN_ERR_INVALID, "null input or output pointer");
-    const size_t need_saved = f == GDN_FORM_CHUNK ? chunk_sizes(B, T, Hv).saved : rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
+    if (f == GDN_FORM_CHUNK) {
+        if (in_dtype == DT_BF16 && dy_dtype == DT_F16)
+            return fail(GDN_ERR_UNSUPPORTED, "the chunked form with bf16 inputs takes a bf16 or fp32 dy, not fp16");
+        if (misaligned16(q) || misaligned16(k) || misaligned16(v) || misaligned16(dy))
+            return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned q, k, v and dy");
+        if (misaligned16(dq) || misaligned16(dk) || misaligned16(dv))
+            return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned dq, dk and dv");
+        ChunkCall cc{};
+        cc.q = q; cc.k = k; cc.v = v; cc.g = g; cc.beta = beta; cc.state0 = state0;
+        cc.dy = dy; cc.dstate_T = dstate_T; cc.dq = dq; cc.dk = dk; cc.dv = dv; cc.dg = dg; cc.dbeta = dbeta;
+        cc.dstate0 = dstate0;
+        cc.B = B; cc.T = T; cc.Ts = T; cc.Hk = Hk; cc.Hv = Hv; cc.in_dt = in_dtype; cc.dy_dt = dy_dtype;
+        cc.grad_dt = grad_dtype; cc.gate = gate_kind;
+        return ck_backward(cc, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
+    }
+    const size_t need_saved = rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
     if (need_saved && (!saved || saved_bytes < need_saved))
         return fail(GDN_ERR_INVALID, "the saved buffer written by gdn_fwd (%zu bytes) is required", need_saved);
-    const size_t need_ws = f == GDN_FORM_CHUNK ? chunk_sizes(B, T, Hv).work
-                                               : bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind).total;
+    const size_t need_ws = bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind).total;
     if (workspace_bytes < need_ws || (need_ws && !workspace))
         return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required",
                     workspace_bytes, need_ws);
@@ -313,30 +592,6 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
     a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dstate0 = dstate0;
     a.B = B; a.T = T; a.Hk = Hk; a.Hv = Hv; a.Dk = Dk; a.Dv = Dv; a.chunk = chunk;
     a.in_dt = in_dtype; a.dy_dt = dy_dtype; a.grad_dt = grad_dtype; a.gate = gate_kind;
-    if (f == GDN_FORM_CHUNK) {
-        if (misaligned16(q) || misaligned16(k) || misaligned16(v) || misaligned16(dy))
-            return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned q, k, v and dy");
-        if (misaligned16(dq) || misaligned16(dk) || misaligned16(dv))
-            return fail(GDN_ERR_INVALID, "the chunked form needs 16-byte aligned dq, dk and dv");
-        ChunkCall cc{};
-        cc.q = q; cc.k = k; cc.v = v; cc.g = g; cc.beta = beta; cc.state0 = state0;
-        cc.dy = dy; cc.dstate_T = dstate_T; cc.dq = dq; cc.dk = dk; cc.dv = dv; cc.dg = dg; cc.dbeta = dbeta;
-        cc.dstate0 = dstate0;
-        cc.saved = const_cast<void *>(saved); cc.work = workspace;
-        cc.B = B; cc.T = T; cc.Hk = Hk; cc.Hv = Hv; cc.in_dt = in_dtype; cc.dy_dt = dy_dtype;
-        cc.grad_dt = grad_dtype; cc.gate = gate_kind;
-        {
-            Timed tm("ck_bwd_seq", st);
-            launch_chunk_stage(cc, "seq", st);
-        }
-        rc = check_launch(st, "gdn_bwd(ck_bwd_seq)");
-        if (rc) return rc;
-        {
-            Timed tm("ck_bwd_local", st);
-            launch_chunk_stage(cc, "local", st);
-        }
-        return check_launch(st, "gdn_bwd(ck_bwd_local)");
-    }
     const BwdLayout L = bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind);
     char *ws = static_cast<char *>(workspace);
     a.ws_sub = reinterpret_cast<float *>(ws + L.sub);

@@ -5,7 +5,7 @@
 //   A = strict_lower(diag(beta) (K K^T) * Gam),  T = (I + A)^-1,  W = T diag(beta gamma) K,  U = T diag(beta) V
 //   Delta = U - W h,  P = lower(Q K^T * Gam),  Y = diag(gamma) Q h + P Delta,
 //   h' = gamma_C h + K^T diag(gamma_C / gamma) Delta
-// which equals the token recurrence of engine/include/gdn.h:217-226 / tools/gdn_vjp.py:3-6 exactly in exact
+// which equals the token recurrence of engine/include/gdn.h:27-38 / tools/gdn_vjp.py:3-6 exactly in exact
 // arithmetic.  The reverse pass is the adjoint of these matrix expressions (chunk-parallel except for the
 // state adjoint, which runs backward over chunks like the forward state does).
 //
@@ -246,11 +246,57 @@ struct Args {
     void *y, *dq, *dk, *dv;
     float *state_T, *dg, *dbeta, *dstate0;
     Bufs w;
-    int B, T, Hk, Hv, NC, in_dt, out_dt, dy_dt, grad_dt, gate;
+    // A launch covers T tokens (NC chunks) of every sequence, starting at the token the input / output pointers
+    // are offset to; Ts is the token stride of a sequence in those tensors (the full sequence length).  The
+    // chunk buffers above are indexed by the launch's own chunks.
+    int B, T, Ts, Hk, Hv, NC, in_dt, out_dt, dy_dt, grad_dt, gate;
+    // Windows of wc chunks (0: none).  snap holds fp32 states [B][Hv][D][D] at the window boundaries, snapshot k
+    // being the state entering window k + 1 of the sequence; win0 is the sequence window the launch starts at.
+    //   forward (recompute = 0): the sequential forward writes snapshot win0 + c / wc - 1 on entering local
+    //     chunk c > 0 with c % wc == 0;
+    //   recompute = 1: the sequential forward runs grid.z = B * (windows in the launch), every window from its
+    //     entry state (state0 for sequence window 0, else its snapshot), writing only H and Delta.
+    float *snap;
+    int wc, win0, recompute;
+    int fwd_only;  // forward-only: ck_prep writes only the tiles the sequential forward reads
 };
 
 __device__ __forceinline__ size_t chunk_index(const Args &a, int b, int hv, int c) {
     return ((size_t)b * a.Hv + hv) * a.NC + c;
+}
+
+// Chunks [cb, ce) and entry state of a sequential forward workgroup whose grid.z index is z (Args::recompute).
+struct SeqRange {
+    int b, cb, ce;
+    const float *s0;
+};
+__device__ __forceinline__ SeqRange seq_range(const Args &a, int z) {
+    SeqRange r{z, 0, a.NC, a.state0};
+    if (a.recompute) {
+        const int w = z / a.B, gw = a.win0 + w;
+        r.b = z - w * a.B;
+        r.cb = w * a.wc;
+        r.ce = min(a.NC, r.cb + a.wc);
+        r.s0 = gw == 0 ? a.state0 : a.snap + (size_t)(gw - 1) * a.B * a.Hv * D * D;
+    }
+    return r;
+}
+
+// The state slice a sequential workgroup holds in accumulators (rows j = 16 w + 4 lg + e, value columns
+// i = i0 + 16 t + li) stored as S [head][i][j] fp32.
+template <int NTN>
+__device__ __forceinline__ void store_state_acc(float *dst, const f4 (&h)[NTN], size_t head, int i0, int w, int lg,
+                                                int li) {
+#pragma unroll
+    for (int t = 0; t < NTN; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[(head * D + i0 + 16 * t + li) * D + 16 * w + 4 * lg + e] = h[t][e];
+}
+
+// Forward mode with windows: the snapshot taken on entering local chunk c, or NULL.
+__device__ __forceinline__ float *snap_at(const Args &a, int c) {
+    if (!a.snap || a.recompute || a.wc <= 0 || c == 0 || c % a.wc) return nullptr;
+    return a.snap + (size_t)(a.win0 + c / a.wc - 1) * a.B * a.Hv * D * D;
 }
 
 // Workgroups are dispatched to the 8 XCDs round-robin by linear id, and each XCD has its own L2.  The D / VS
@@ -338,8 +384,8 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk), t0 = c * C, n = min(C, T - t0);
     const size_t ci = chunk_index(a, b, hv, c);
-    const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
-    const size_t v0 = (((size_t)b * T + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
+    const size_t qk0 = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
+    const size_t v0 = (((size_t)b * a.Ts + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
 
     TileRegs<C, D, NTP> rV;  // V is needed only after the inverse: fetch it now, store it later
     tile_fetch(rV, elem_ptr(a.v, v0, a.in_dt), v_row, n, a.in_dt);
@@ -349,7 +395,7 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
         // inclusive prefix sum of the log decays in fp64 across wave 0
         float bt = 0.f, gl = 0.f;
         if (tid < n) {
-            const size_t gi = ((size_t)b * T + t0 + tid) * a.Hv + hv;
+            const size_t gi = ((size_t)b * a.Ts + t0 + tid) * a.Hv + hv;
             bt = a.beta[gi];
             gl = gate_log(a.g[gi], a.gate);
         }
@@ -404,7 +450,8 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) out[ci * C * D + (r0 + 4 * lg + e) * D + 16 * t + li] = acc[t][e];
     }
-    for (int i = tid; i < C * C; i += NTP) a.w.T[ci * C * C + i] = sT[(i / C) * LDC + (i % C)];
+    if (!a.fwd_only)
+        for (int i = tid; i < C * C; i += NTP) a.w.T[ci * C * C + i] = sT[(i / C) * LDC + (i % C)];
     if (tid < C) a.w.G[ci * C + tid] = sG[tid];
 }
 
@@ -435,7 +482,8 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
     __shared__ double sG[C];
 
     const SeqBlock sb = seq_block();
-    const int i0 = sb.slice * VS, hv = sb.hv, b = sb.b;
+    const SeqRange sr = seq_range(a, sb.b);
+    const int i0 = sb.slice * VS, hv = sb.hv, b = sr.b, cb = sr.cb, ce = sr.ce;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
     const size_t head = (size_t)b * a.Hv + hv;
@@ -450,7 +498,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
-            h[t][e] = a.state0 ? a.state0[(head * D + i) * D + j] : 0.f;
+            h[t][e] = sr.s0 ? sr.s0[(head * D + i) * D + j] : 0.f;
         }
     TileRegs<C, D, NTS> rW, rQ, rK;
     TileRegs<C, VS, NTS> rU;
@@ -458,7 +506,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
     double rG = 0.0;
     auto fetchA = [&](int c) {
         const size_t ci = head * a.NC + c;
-        const size_t qk0 = (((size_t)b * T + c * C) * a.Hk + hk) * D;
+        const size_t qk0 = (((size_t)b * a.Ts + c * C) * a.Hk + hk) * D;
         const int n = min(C, T - c * C);
         tile_fetch(rW, a.w.W + ci * C * D, D, C, DT_F32);
         tile_fetch(rU, a.w.U + ci * C * D + i0, D, C, DT_F32);
@@ -467,16 +515,17 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
     };
     auto fetchB = [&](int c) {
         const size_t ci = head * a.NC + c;
-        const size_t qk0 = (((size_t)b * T + c * C) * a.Hk + hk) * D;
+        const size_t qk0 = (((size_t)b * a.Ts + c * C) * a.Hk + hk) * D;
         const int n = min(C, T - c * C);
         tile_fetch(rP, a.w.P + ci * C * C, C, C, DT_F32);
         tile_fetch(rK, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
     };
-    fetchA(0);
-    fetchB(0);
-    for (int c = 0; c < a.NC; ++c) {
+    fetchA(cb);
+    fetchB(cb);
+    for (int c = cb; c < ce; ++c) {
         const int t0 = c * C, n = min(C, T - t0);
         const size_t ci = head * a.NC + c;
+        if (float *sp = snap_at(a, c)) store_state_acc<NTN>(sp, h, head, i0, w, lg, li);
         __syncthreads();
 #pragma unroll
         for (int t = 0; t < NTN; ++t)
@@ -487,8 +536,8 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
         tile_store(sQ, LD, rQ, a.in_dt, NoScale{});
         if (tid < C) sG[tid] = rG;
         __syncthreads();
-        if (c + 1 < a.NC) fetchA(c + 1);
-        store_state_slice<VS, LV, NTS>(a.w.H + ci * D * D, sH, i0);
+        if (c + 1 < ce) fetchA(c + 1);
+        if (a.w.H) store_state_slice<VS, LV, NTS>(a.w.H + ci * D * D, sH, i0);
         // Delta = U - W h ; Yi = Q h
         f4 wh[DN], yi[DN];
 #pragma unroll
@@ -503,15 +552,15 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
                     const int r = mrow + 4 * lg + e, ii = 16 * (nt0 + t) + li;
                     const float dl = sU[r * LV + ii] - wh[t][e];
                     sD[r * LV + ii] = dl;
-                    a.w.Dl[ci * C * D + r * D + i0 + ii] = dl;
+                    if (a.w.Dl) a.w.Dl[ci * C * D + r * D + i0 + ii] = dl;
                 }
         }
         __syncthreads();
         tile_store(sW, LDC, rP, DT_F32, NoScale{});
         tile_store(sQ, LD, rK, a.in_dt, RcScale{sG});
         __syncthreads();
-        if (c + 1 < a.NC) fetchB(c + 1);
-        if (cwave) {
+        if (c + 1 < ce) fetchB(c + 1);
+        if (cwave && a.y) {
             // Y = diag(gamma) Q h + P Delta
 #pragma unroll
             for (int t = 0; t < DN; ++t)
@@ -524,7 +573,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
                 for (int e = 0; e < 4; ++e) {
                     const int r = mrow + 4 * lg + e, ii = 16 * (nt0 + t) + li;
                     if (r < n)
-                        store_from_f32(a.y, (((size_t)b * T + t0 + r) * a.Hv + hv) * D + i0 + ii, yi[t][e],
+                        store_from_f32(a.y, (((size_t)b * a.Ts + t0 + r) * a.Hv + hv) * D + i0 + ii, yi[t][e],
                                        a.out_dt);
                 }
         }
@@ -534,15 +583,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
         for (int t = 0; t < NTN; ++t) h[t] *= gC;
         mma_strip<C, NTN>(h, sQ + 16 * w, 1, LD, sD, LV, 1, 16);
     }
-    if (a.state_T) {
-#pragma unroll
-        for (int t = 0; t < NTN; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
-                a.state_T[(head * D + i) * D + j] = h[t][e];
-            }
-    }
+    if (a.state_T && !a.recompute) store_state_acc<NTN>(a.state_T, h, head, i0, w, lg, li);
 }
 
 // ---------------------------------------------------------------------------------------------- ck_bwd_seq
@@ -584,8 +625,8 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
     double rG = 0.0;
     auto fetchA = [&](int c) {
         const size_t ci = head * a.NC + c;
-        const size_t qk0 = (((size_t)b * T + c * C) * a.Hk + hk) * D;
-        const size_t v0 = (((size_t)b * T + c * C) * a.Hv + hv) * D;
+        const size_t qk0 = (((size_t)b * a.Ts + c * C) * a.Hk + hk) * D;
+        const size_t v0 = (((size_t)b * a.Ts + c * C) * a.Hv + hv) * D;
         const int n = min(C, T - c * C);
         tile_fetch(rP, a.w.P + ci * C * C, C, C, DT_F32);
         tile_fetch(rK, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
@@ -594,7 +635,7 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
     };
     auto fetchB = [&](int c) {
         const size_t ci = head * a.NC + c;
-        const size_t qk0 = (((size_t)b * T + c * C) * a.Hk + hk) * D;
+        const size_t qk0 = (((size_t)b * a.Ts + c * C) * a.Hk + hk) * D;
         const int n = min(C, T - c * C);
         tile_fetch(rW, a.w.W + ci * C * D, D, C, DT_F32);
         tile_fetch(rQ, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
@@ -684,7 +725,7 @@ __device__ __forceinline__ void chunk_dg_dbeta(float *sE, const float (*sRow)[2]
                                                float (*sScan)[C], const Args &a, int b, int hv, int t0, int n,
                                                int tid) {
     static_assert(NTH == C * 8, "eight threads per row / column");
-    const size_t g0 = ((size_t)b * a.T + t0) * a.Hv + hv;
+    const size_t g0 = ((size_t)b * a.Ts + t0) * a.Hv + hv;
     static_assert(C == 64, "one wave scans the chunk");
     if (tid < C) {
         const int r = tid, rs = C - 1 - tid;  // rs: this lane's row of the suffix scan
@@ -788,8 +829,8 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
     const float *dHc = a.w.dH + ci * D * D;
     const float *Dc = a.w.Dl + ci * C * D;
     const float *dDc = a.w.dDl + ci * C * D;
-    const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
-    const size_t v0 = (((size_t)b * T + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
+    const size_t qk0 = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
+    const size_t v0 = (((size_t)b * a.Ts + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
     // dW of this chunk is parked in its rows of the dq|dk output buffer until it is needed (rows >= n of dW
     // are zero: padded tokens have k = 0, so their dDelta vanishes)
     float *const dWpark = a.w.part + ((size_t)b * T + t0) * a.Hv * 2 * D + (size_t)hv * 2 * D;
@@ -799,7 +840,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
     if (tid < C) {
         sG[tid] = a.w.G[ci * C + tid];
         float bt = 0.f;
-        if (tid < n) bt = a.beta[((size_t)b * T + t0 + tid) * a.Hv + hv];
+        if (tid < n) bt = a.beta[((size_t)b * a.Ts + t0 + tid) * a.Hv + hv];
         sB[tid] = bt;
     }
     load_tile<D, D, NTB>(R1, LD, Hc, D, D, DT_F32, nullptr, tid);
@@ -1040,7 +1081,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
         }
     }
     chunk_dg_dbeta<NTB>(sE, sRow, sLast, 1.f, sScan, a, b, hv, t0, n, tid);
-    const size_t qk_out = (((size_t)b * T + t0) * a.Hk + hk) * D;
+    const size_t qk_out = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D;
     auto out = [&](const f4 (&X)[4], const float4 (&prev)[4], int half, void *dst) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -1408,7 +1449,7 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     const int T = a.T, t0 = c * C, n = min(C, T - t0);
     float *const part_row = a.w.part + (((size_t)b * T + t0) * a.Hk + hk) * 2 * D;
     const size_t part_rs = (size_t)a.Hk * 2 * D;
-    const size_t qk_out = (((size_t)b * T + t0) * a.Hk + hk) * D;
+    const size_t qk_out = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D;
     // an opaque lane index per value head: the lane-dependent addresses are formed inside the head instead of
     // being hoisted out of the caller's loop and held in registers across the whole head
     int tid = threadIdx.x;
@@ -1421,15 +1462,15 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     const float *Dc = a.w.Dl + ci * C * D;
     const bfr *dDc = reinterpret_cast<const bfr *>(a.w.dDl) + ci * 2 * D * C;  // dDelta^T hi, lo planes [i][r]
     const bfr *Tc = reinterpret_cast<const bfr *>(a.w.T) + ci * 2 * C * C;      // T hi, lo planes [r][s]
-    const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
-    const size_t v0 = (((size_t)b * T + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
+    const size_t qk0 = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
+    const size_t v0 = (((size_t)b * a.Ts + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
     const bfr *qsrc = static_cast<const bfr *>(a.q) + qk0, *ksrc = static_cast<const bfr *>(a.k) + qk0;
     const bfr *vsrc = static_cast<const bfr *>(a.v) + v0;
 
     // ---- S1: gates; h, dh', Delta, dY; P1 dQ = diag(gamma) dY h^T, P3 dK = diag(rc) Delta dh'^T, P4 dp = dY Delta^T
     if (tid < C) {
         sG[tid] = a.w.G[ci * C + tid];
-        sB[tid] = tid < n ? a.beta[((size_t)b * T + t0 + tid) * a.Hv + hv] : 0.f;
+        sB[tid] = tid < n ? a.beta[((size_t)b * a.Ts + t0 + tid) * a.Hv + hv] : 0.f;
     }
     // S1 staging: every global load of the phase is issued before the first LDS store
     float lastp = 0.f;  // <dh', h>, the pair (C-1, chunk start)
@@ -1931,7 +1972,8 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
     __shared__ float sGamBuf[2][C];  // by chunk parity: read after the second barrier, rewritten two chunks later
 
     const SeqBlock sb = seq_block();
-    const int i0 = sb.slice * VS, hv = sb.hv, b = sb.b;
+    const SeqRange sr = seq_range(a, sb.b);
+    const int i0 = sb.slice * VS, hv = sb.hv, b = sr.b, cb = sr.cb, ce = sr.ce;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
     const size_t head = (size_t)b * a.Hv + hv;
@@ -1945,7 +1987,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
-            h[t][e] = a.state0 ? a.state0[(head * D + i) * D + j] : 0.f;
+            h[t][e] = sr.s0 ? sr.s0[(head * D + i) * D + j] : 0.f;
         }
     auto fetch = [&](FwdFrags<DN> &f, int c) {
         const size_t ci = head * a.NC + c;
@@ -1953,7 +1995,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
         const bfr *wb = a.w.Wb + ci * C * D + frag_off<D>(mrow, 0) + 8 * l;
         const bfr *pb = a.w.Pb + ci * 2 * C * C + frag_off<C>(mrow, 0) + 8 * l;
         const bfr *kt = a.w.KTb + ci * D * C + frag_off<C>(16 * w, 0) + 8 * l;
-        const bfr *qb = static_cast<const bfr *>(a.q) + (((size_t)b * T + t0 + r) * a.Hk + hk) * D + 8 * lg;
+        const bfr *qb = static_cast<const bfr *>(a.q) + (((size_t)b * a.Ts + t0 + r) * a.Hk + hk) * D + 8 * lg;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             f.W[k] = ld_frag(wb + FRAG_BLOCK * k);
@@ -1979,19 +2021,22 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
     auto step = [&](const int c, FwdFrags<DN> &cur, FwdFrags<DN> &nxt) {
         const int t0 = c * C, n = min(C, T - t0);
         const size_t ci = head * a.NC + c;
+        if (float *sp = snap_at(a, c)) store_state_acc<NTN>(sp, h, head, i0, w, lg, li);
         // h -> LDS as the operand [i][j]; the chunk-entry state -> saved H ([j][i], bf16)
 #pragma unroll
         for (int t = 0; t < NTN; ++t) {
             acc_T<true>(h[t], sHh, sHl, LH, 16 * w, 16 * t);
+            if (a.w.H) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                reinterpret_cast<bfr *>(a.w.H)[ci * D * D + (size_t)(16 * w + 4 * lg + e) * D + i0 + 16 * t + li] =
-                    (bfr)bfbits(h[t][e]);
+                for (int e = 0; e < 4; ++e)
+                    reinterpret_cast<bfr *>(a.w.H)[ci * D * D + (size_t)(16 * w + 4 * lg + e) * D + i0 + 16 * t + li] =
+                        (bfr)bfbits(h[t][e]);
+            }
         }
         float *const sGam = sGamBuf[c & 1];
         if (tid < C) sGam[tid] = __builtin_amdgcn_exp2f((float)(cur.g * 1.4426950408889634));  // v_exp_f32 on log2 units
         __syncthreads();
-        if (c + 1 < a.NC) fetch(nxt, c + 1);
+        if (c + 1 < ce) fetch(nxt, c + 1);
         // Delta = U - W h ; Yi = Q h
         f4 yi[DN];
 #pragma unroll
@@ -2008,13 +2053,15 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) dl[e] = cur.U[t][e] - wh[t][e];
                 acc_T<true>(dl, sDh, sDl, LDd, mrow, 16 * (nt0 + t));
+                if (a.w.Dl) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    a.w.Dl[ci * C * D + (size_t)(mrow + 4 * lg + e) * D + i0 + 16 * (nt0 + t) + li] = dl[e];
+                    for (int e = 0; e < 4; ++e)
+                        a.w.Dl[ci * C * D + (size_t)(mrow + 4 * lg + e) * D + i0 + 16 * (nt0 + t) + li] = dl[e];
+                }
             }
         }
         __syncthreads();
-        if (cwave) {
+        if (cwave && a.y) {
             // Y = diag(gamma) Q h + P Delta
 #pragma unroll
             for (int t = 0; t < DN; ++t)
@@ -2027,7 +2074,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
                 for (int e = 0; e < 4; ++e) {
                     const int r = mrow + 4 * lg + e;
                     if (r < n)
-                        store_from_f32(a.y, (((size_t)b * T + t0 + r) * a.Hv + hv) * D + i0 + 16 * (nt0 + t) + li,
+                        store_from_f32(a.y, (((size_t)b * a.Ts + t0 + r) * a.Hv + hv) * D + i0 + 16 * (nt0 + t) + li,
                                        yi[t][e], a.out_dt);
                 }
         }
@@ -2038,20 +2085,12 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
         mmar<C, NTN>(h, cur.K, nullptr, sDh, nullptr, LDd, 0);
     };
     FwdFrags<DN> fa, fb;
-    fetch(fa, 0);
-    for (int c = 0; c < a.NC; c += 2) {
+    fetch(fa, cb);
+    for (int c = cb; c < ce; c += 2) {
         step(c, fa, fb);
-        if (c + 1 < a.NC) step(c + 1, fb, fa);
+        if (c + 1 < ce) step(c + 1, fb, fa);
     }
-    if (a.state_T) {
-#pragma unroll
-        for (int t = 0; t < NTN; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
-                a.state_T[(head * D + i) * D + j] = h[t][e];
-            }
-    }
+    if (a.state_T && !a.recompute) store_state_acc<NTN>(a.state_T, h, head, i0, w, lg, li);
 }
 
 // ---------------------------------------------------------------------------------------------- ck_prep (bf16)
@@ -2090,8 +2129,8 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk), t0 = c * C, n = min(C, T - t0);
     const size_t ci = chunk_index(a, b, hv, c);
-    const size_t qk0 = (((size_t)b * T + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
-    const size_t v0 = (((size_t)b * T + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
+    const size_t qk0 = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
+    const size_t v0 = (((size_t)b * a.Ts + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
 
     // V as 8-token x 2-channel blocks (one per thread) for the transposed tile, kept in registers until Q is dead
     static_assert((C / 8) * (D / 2) == NTP, "one V block per thread");
@@ -2116,7 +2155,7 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
     }
     float bt = 0.f, graw = 1.f;
     if (tid < n) {
-        const size_t gi = ((size_t)b * T + t0 + tid) * a.Hv + hv;
+        const size_t gi = ((size_t)b * a.Ts + t0 + tid) * a.Hv + hv;
         bt = a.beta[gi];
         graw = a.g[gi];
     }
@@ -2156,7 +2195,7 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
         // Q^T depends on the key head only: the first value head of each key head writes it
         const int rep = a.Hv / a.Hk;
         bfr *dst = isq ? a.w.QTb + (((size_t)b * a.Hk + hk) * a.NC + c) * D * C : a.w.KTb + ci * D * C;
-        if (!isq || hv % rep == 0) {
+        if (!isq || (hv % rep == 0 && !a.fwd_only)) {
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc)
                 *reinterpret_cast<uint4 *>(dst + frag_off<C>(j0 + cc, rb * 8)) =
@@ -2195,7 +2234,7 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
                     sA[r * LDC + s2] = s2 < r ? sB[r] * acc[t][e] * gam : 0.f;
                 }
             }
-            if (isq) {
+            if (isq && !a.fwd_only) {
                 // P^T [s][r]: this lane's four consecutive r of column s = 16t + li
                 bfr *pt = a.w.PTb + ci * 2 * C * C + frag_off<C>(16 * t + li, r0 + 4 * lg);
                 *reinterpret_cast<uint2 *>(pt) = make_uint2(ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16));
@@ -2286,8 +2325,11 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
                 sW[(r0 + 4 * lg + e) * LK + 16 * t + li] = (bfr)wb[e];
             }
             // -W^T [j][r]; bf16 negation flips the sign bit
-            bfr *wt = a.w.nWTb + ci * D * C + frag_off<C>(16 * t + li, r0 + 4 * lg);
-            *reinterpret_cast<uint2 *>(wt) = make_uint2((wb[0] | (wb[1] << 16)) ^ 0x80008000u, (wb[2] | (wb[3] << 16)) ^ 0x80008000u);
+            if (!a.fwd_only) {
+                bfr *wt = a.w.nWTb + ci * D * C + frag_off<C>(16 * t + li, r0 + 4 * lg);
+                *reinterpret_cast<uint2 *>(wt) = make_uint2((wb[0] | (wb[1] << 16)) ^ 0x80008000u,
+                                                            (wb[2] | (wb[3] << 16)) ^ 0x80008000u);
+            }
         }
     }
     __syncthreads();
@@ -2300,15 +2342,17 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
         const int r = i / (D / 8), c8 = (i - r * (D / 8)) * 8;
         *reinterpret_cast<uint4 *>(a.w.Wb + ci * C * D + frag_off<D>(r, c8)) = *reinterpret_cast<const uint4 *>(sW + r * LK + c8);
     }
-    for (int i = tid; i < C * C / 4; i += NTP) {  // T as bf16 hi and lo planes
-        const int r = i / (C / 4), c4 = (i - r * (C / 4)) * 4;
-        const float4 x = *reinterpret_cast<const float4 *>(sT + r * LDC + c4);
-        uint2 h, l;
-        pk2(x.x, x.y, h.x, l.x);
-        pk2(x.z, x.w, h.y, l.y);
-        bfr *const tb = reinterpret_cast<bfr *>(a.w.T) + ci * 2 * C * C + r * C + c4;
-        *reinterpret_cast<uint2 *>(tb) = h;
-        *reinterpret_cast<uint2 *>(tb + C * C) = l;
+    if (!a.fwd_only) {
+        for (int i = tid; i < C * C / 4; i += NTP) {  // T as bf16 hi and lo planes
+            const int r = i / (C / 4), c4 = (i - r * (C / 4)) * 4;
+            const float4 x = *reinterpret_cast<const float4 *>(sT + r * LDC + c4);
+            uint2 h, l;
+            pk2(x.x, x.y, h.x, l.x);
+            pk2(x.z, x.w, h.y, l.y);
+            bfr *const tb = reinterpret_cast<bfr *>(a.w.T) + ci * 2 * C * C + r * C + c4;
+            *reinterpret_cast<uint2 *>(tb) = h;
+            *reinterpret_cast<uint2 *>(tb + C * C) = l;
+        }
     }
     if (tid < C) a.w.G[ci * C + tid] = sG[tid];
 }
@@ -2366,7 +2410,7 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
     auto fetch = [&](BwdFrags &f, YRaw (&y)[8], int c) {
         const size_t ci = head * a.NC + c;
         const int t0 = c * C, n = min(C, T - t0), r = mrow + li;
-        const bfr *kb = static_cast<const bfr *>(a.k) + (((size_t)b * T + t0 + r) * a.Hk + hk) * D + 8 * lg;
+        const bfr *kb = static_cast<const bfr *>(a.k) + (((size_t)b * a.Ts + t0 + r) * a.Hk + hk) * D + 8 * lg;
         const bfr *pt = a.w.PTb + ci * 2 * C * C + frag_off<C>(mrow, 0) + 8 * l;
         const bfr *qt = a.w.QTb + (((size_t)b * a.Hk + hk) * a.NC + c) * D * C + frag_off<C>(16 * w, 0) + 8 * l;
         const bfr *wt = a.w.nWTb + ci * D * C + frag_off<C>(16 * w, 0) + 8 * l;
@@ -2384,7 +2428,7 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
 #pragma unroll
             for (int rr = 0; rr < 8; ++rr) {
                 const int s2 = 8 * yb + rr;
-                const size_t off = (((size_t)b * T + t0 + s2) * a.Hv + hv) * D + i0 + yc;
+                const size_t off = (((size_t)b * a.Ts + t0 + s2) * a.Hv + hv) * D + i0 + yc;
                 if constexpr (DYF32)
                     y[rr] = s2 < n ? *reinterpret_cast<const float2 *>(static_cast<const float *>(a.dy) + off)
                                    : make_float2(0.f, 0.f);
@@ -2508,29 +2552,36 @@ constexpr int CK_D = ck::D;
 
 static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-ChunkSizes chunk_sizes(int B, int T, int Hv) {
+ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd) {
+    static_assert(CK_C == kChunkC && CK_D == kChunkD, "chunk geometry");
     ChunkSizes s{};
     const size_t NC = (size_t)(T + CK_C - 1) / CK_C;
-    const size_t heads = (size_t)B * Hv;
+    const size_t n = (size_t)B * Hv * NC, nk = (size_t)B * Hk * NC;  // chunk-heads, chunk-key-heads
+    const size_t cd = (size_t)CK_C * CK_D, cc = (size_t)CK_C * CK_C, dd = (size_t)CK_D * CK_D;
     size_t off = 0;
-    s.H = off; off += al256(heads * NC * CK_D * CK_D * 4);
-    s.G = off; off += al256(heads * NC * CK_C * 8);
-    s.T = off; off += al256(heads * NC * CK_C * CK_C * 4);
-    s.P = off; off += al256(heads * NC * CK_C * CK_C * 4);
-    s.W = off; off += al256(heads * NC * CK_C * CK_D * 4);
-    s.U = off; off += al256(heads * NC * CK_C * CK_D * 4);
-    s.Dl = off; off += al256(heads * NC * CK_C * CK_D * 4);
-    s.Wb = off; off += al256(heads * NC * CK_C * CK_D * 2);
-    s.KTb = off; off += al256(heads * NC * CK_D * CK_C * 2);
-    s.Pb = off; off += al256(heads * NC * 2 * CK_C * CK_C * 2);
-    s.PTb = off; off += al256(heads * NC * 2 * CK_C * CK_C * 2);
-    s.QTb = off; off += al256(heads * NC * CK_D * CK_C * 2);
-    s.nWTb = off; off += al256(heads * NC * CK_D * CK_C * 2);
+    auto put = [&](ChunkSizes::Buf &bf, size_t bytes) {
+        bf.off = off;
+        bf.size = bytes;
+        off += al256(bytes);
+    };
+    put(s.G, n * CK_C * 8);
+    put(s.U, n * cd * 4);
+    put(s.H, bwd ? n * dd * (bf16 ? 2 : 4) : 0);
+    put(s.Dl, bwd ? n * cd * 4 : 0);
+    put(s.T, bwd ? n * cc * 4 : 0);            // fp32, or bf16 hi / lo planes
+    put(s.P, bf16 ? 0 : n * cc * 4);
+    put(s.W, bf16 ? 0 : n * cd * 4);
+    put(s.Wb, bf16 ? n * cd * 2 : 0);
+    put(s.KTb, bf16 ? n * cd * 2 : 0);
+    put(s.Pb, bf16 ? n * 2 * cc * 2 : 0);
+    put(s.PTb, bf16 && bwd ? n * 2 * cc * 2 : 0);
+    put(s.QTb, bf16 && bwd ? nk * cd * 2 : 0);
+    put(s.nWTb, bf16 && bwd ? n * cd * 2 : 0);
     s.saved = off;
     off = 0;
-    s.dH = off; off += al256(heads * NC * CK_D * CK_D * 4);
-    s.dDl = off; off += al256(heads * NC * CK_C * CK_D * 4);
-    s.part = off; off += al256((size_t)B * T * Hv * 2 * CK_D * 4);
+    put(s.dH, n * dd * (bf16 ? 2 : 4));
+    put(s.dDl, n * cd * 4);                    // fp32, or dDelta^T as bf16 hi / lo planes
+    put(s.part, (size_t)B * T * (bf16 ? Hk : Hv) * 2 * CK_D * 4);
     s.work = off;
     return s;
 }
@@ -2541,29 +2592,32 @@ static ck::Args make_args(const ChunkCall &cc) {
     a.dy = cc.dy; a.dstate_T = cc.dstate_T; a.y = cc.y; a.dq = cc.dq; a.dk = cc.dk; a.dv = cc.dv;
     a.state_T = cc.state_T;
     a.dg = cc.dg; a.dbeta = cc.dbeta; a.dstate0 = cc.dstate0;
-    const ChunkSizes s = chunk_sizes(cc.B, cc.T, cc.Hv);
-    char *sv = static_cast<char *>(cc.saved);
-    a.w.H = reinterpret_cast<float *>(sv + s.H);
-    a.w.G = reinterpret_cast<double *>(sv + s.G);
-    a.w.T = reinterpret_cast<float *>(sv + s.T);
-    a.w.P = reinterpret_cast<float *>(sv + s.P);
-    a.w.W = reinterpret_cast<float *>(sv + s.W);
-    a.w.U = reinterpret_cast<float *>(sv + s.U);
-    a.w.Dl = reinterpret_cast<float *>(sv + s.Dl);
-    a.w.Wb = reinterpret_cast<unsigned short *>(sv + s.Wb);
-    a.w.KTb = reinterpret_cast<unsigned short *>(sv + s.KTb);
-    a.w.Pb = reinterpret_cast<unsigned short *>(sv + s.Pb);
-    a.w.PTb = reinterpret_cast<unsigned short *>(sv + s.PTb);
-    a.w.QTb = reinterpret_cast<unsigned short *>(sv + s.QTb);
-    a.w.nWTb = reinterpret_cast<unsigned short *>(sv + s.nWTb);
+    const bool bf16 = cc.in_dt == DT_BF16;
+    const ChunkSizes s = chunk_sizes(cc.B, cc.T, cc.Hk, cc.Hv, bf16, !cc.fwd_only);
+    char *sv = static_cast<char *>(cc.tiles);
+    auto at = [&](const ChunkSizes::Buf &bf) -> void * { return bf.size ? sv + bf.off : nullptr; };
+    a.w.H = static_cast<float *>(at(s.H));
+    a.w.G = static_cast<double *>(at(s.G));
+    a.w.T = static_cast<float *>(at(s.T));
+    a.w.P = static_cast<float *>(at(s.P));
+    a.w.W = static_cast<float *>(at(s.W));
+    a.w.U = static_cast<float *>(at(s.U));
+    a.w.Dl = static_cast<float *>(at(s.Dl));
+    a.w.Wb = static_cast<unsigned short *>(at(s.Wb));
+    a.w.KTb = static_cast<unsigned short *>(at(s.KTb));
+    a.w.Pb = static_cast<unsigned short *>(at(s.Pb));
+    a.w.PTb = static_cast<unsigned short *>(at(s.PTb));
+    a.w.QTb = static_cast<unsigned short *>(at(s.QTb));
+    a.w.nWTb = static_cast<unsigned short *>(at(s.nWTb));
     if (cc.work) {
         char *wk = static_cast<char *>(cc.work);
-        a.w.dH = reinterpret_cast<float *>(wk + s.dH);
-        a.w.dDl = reinterpret_cast<float *>(wk + s.dDl);
-        a.w.part = reinterpret_cast<float *>(wk + s.part);
+        a.w.dH = reinterpret_cast<float *>(wk + s.dH.off);
+        a.w.dDl = reinterpret_cast<float *>(wk + s.dDl.off);
+        a.w.part = reinterpret_cast<float *>(wk + s.part.off);
     }
-    a.B = cc.B; a.T = cc.T; a.Hk = cc.Hk; a.Hv = cc.Hv; a.NC = (cc.T + CK_C - 1) / CK_C;
+    a.B = cc.B; a.T = cc.T; a.Ts = cc.Ts; a.Hk = cc.Hk; a.Hv = cc.Hv; a.NC = (cc.T + CK_C - 1) / CK_C;
     a.in_dt = cc.in_dt; a.out_dt = cc.out_dt; a.dy_dt = cc.dy_dt; a.grad_dt = cc.grad_dt; a.gate = cc.gate;
+    a.snap = cc.snap; a.wc = cc.wc; a.win0 = cc.win0; a.recompute = cc.recompute; a.fwd_only = cc.fwd_only;
     return a;
 }
 
@@ -2571,9 +2625,12 @@ static ck::Args make_args(const ChunkCall &cc) {
 // (256 CUs), so fewer workgroups re-read the chunk's shared W / Q / K / P tiles.
 static int slice_width(int heads) { return heads >= 128 ? 64 : heads >= 64 ? 32 : 16; }
 
+// Workgroups along grid.z of the sequential kernels: the sequences, times the windows when they run side by side.
+static int seq_z(const ck::Args &a) { return a.recompute ? a.B * ((a.NC + a.wc - 1) / a.wc) : a.B; }
+
 template <int MT, int VS>
 static void seq_launch(const ck::Args &a, hipStream_t st, bool fwd) {
-    const dim3 grid(CK_D / VS, a.Hv, a.B);
+    const dim3 grid(CK_D / VS, a.Hv, seq_z(a));
     if constexpr (MT == 1) {
         if (fwd) hipLaunchKernelGGL((ck::ck_fwd_bf16_kernel<VS>), grid, dim3(ck::NTS), 0, st, a);
         else if (a.dy_dt == DT_F32) hipLaunchKernelGGL((ck::ck_bwd_seq_bf16_kernel<VS, true>), grid, dim3(ck::NTS), 0, st, a);
@@ -2586,7 +2643,7 @@ static void seq_launch(const ck::Args &a, hipStream_t st, bool fwd) {
 
 template <int MT>
 static void seq_dispatch(const ck::Args &a, hipStream_t st, bool fwd) {
-    switch (slice_width(a.B * a.Hv)) {
+    switch (slice_width(seq_z(a) * a.Hv)) {
         case 64: seq_launch<MT, 64>(a, st, fwd); break;
         case 32: seq_launch<MT, 32>(a, st, fwd); break;
         default: seq_launch<MT, 16>(a, st, fwd); break;

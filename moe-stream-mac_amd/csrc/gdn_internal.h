@@ -33,14 +33,28 @@ struct RecBwdArgs {
 };
 
 // Chunked (WY/UT) form, C = 64, Dk = Dv = 128 (gdn_chunk.hip).
-struct ChunkSizes {
-    size_t H, G, T, P, W, U, Dl;         // offsets into the buffer kept from forward to backward
-    size_t Wb, KTb, Pb, PTb, QTb, nWTb;  // bf16 operand tiles of the bf16 path
-    size_t saved;                        // size of that buffer
-    size_t dH, dDl, part, work;          // offsets into / size of the backward workspace
-};
-ChunkSizes chunk_sizes(int B, int T, int Hv);
+constexpr int kChunkC = 64;
+constexpr int kChunkD = 128;
 
+// Offsets of the per-chunk buffers of one launch covering T tokens of B sequences: the tile set ck_prep and the
+// sequential forward write ("saved"; bwd = false leaves out what only the backward reads), and the backward
+// workspace.  A zero-sized buffer has no storage.  The fp32 set (bf16 = false) and the bf16 set keep different
+// tiles.
+struct ChunkSizes {
+    struct Buf {
+        size_t off, size;
+    };
+    Buf H, G, T, P, W, U, Dl;         // tile set
+    Buf Wb, KTb, Pb, PTb, QTb, nWTb;  // bf16 operand tiles of the bf16 set
+    size_t saved;                     // size of the tile set
+    Buf dH, dDl, part;                // backward workspace
+    size_t work;                      // its size
+};
+ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd);
+
+// One launch of a chunked stage.  q, k, v, g, beta, y, dy, dq, dk, dv, dg and dbeta point at the launch's first
+// token; T is the launch's token count and Ts the token stride of a sequence (the full length).  tiles / work are
+// the chunk_sizes(B, T, ...) buffers of this launch.
 struct ChunkCall {
     const void *q, *k, *v;
     const float *g, *beta, *state0;
@@ -48,11 +62,13 @@ struct ChunkCall {
     const float *dstate_T;
     void *y, *dq, *dk, *dv;
     float *state_T, *dg, *dbeta, *dstate0;
-    void *saved, *work;
-    int B, T, Hk, Hv, in_dt, out_dt, dy_dt, grad_dt, gate;
+    void *tiles, *work;
+    float *snap;        // window snapshots (see ck::Args)
+    int wc, win0, recompute, fwd_only;
+    int B, T, Ts, Hk, Hv, in_dt, out_dt, dy_dt, grad_dt, gate;
 };
 // stage: "prep" | "fwd" (forward) or "seq" | "local" (backward; "local" walks the value heads of each key head
-// and writes dq and dk)
+// and writes dq and dk).  With recompute, "fwd" runs every window of the launch at once.
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st);
 
 int pick_lane_width(int Dk);

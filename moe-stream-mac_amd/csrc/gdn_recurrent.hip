@@ -1,6 +1,6 @@
 // Token-sequential ("recurrent") form of the Gated DeltaNet forward and VJP for gfx950.
 //
-// Work split.  The rows of the [Dv][Dk] state are independent in the forward (engine/include/gdn.h:226), so a
+// Work split.  The rows of the [Dv][Dk] state are independent in the forward (engine/include/gdn.h:36), so a
 // workgroup owns one (batch, value head, block of 16 value rows).  Each row lives in the VGPRs of one DPP row
 // of 16 lanes, E = Dk/16 key channels per lane; row dot products (S k, S q, dS~ k) are 4-step DPP all-reduces
 // with no LDS traffic and no barriers.  Per-token inputs are staged through LDS in tiles.

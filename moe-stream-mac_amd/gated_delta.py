@@ -4,7 +4,7 @@
 
 ``gated_delta_update`` is the un-patched update bound into ``qwen3_5``: ``use_kernel=True`` is the
 forward-only inference path (no snapshots, no autograd graph), ``use_kernel=False`` the differentiable
-recurrence.  The arithmetic is the per-step rule of ``engine/include/gdn.h:217-226``.
+recurrence.  The arithmetic is the per-step rule of ``engine/include/gdn.h:27-38`` (``engine/src/gdn.c:63-108``).
 """
 
 from __future__ import annotations

@@ -38,8 +38,8 @@ def gate_kind_for(g: torch.Tensor, log_gate: bool) -> int:
     raise ValueError(f"Unsupported gating shape {tuple(g.shape)}")
 
 
-def _saved_bytes(lib, B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form) -> int:
-    return int(lib.gdn_saved_bytes(B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form))
+def _saved_bytes(lib, B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form, in_code) -> int:
+    return int(lib.gdn_saved_bytes(B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form, in_code))
 
 
 class _GDNRecurrence(torch.autograd.Function):
@@ -60,13 +60,19 @@ class _GDNRecurrence(torch.autograd.Function):
             L.check(resolved)
         y = torch.empty((B, T, Hv, Dv), device=dev, dtype=out_dtype)
         state_T = torch.empty((B, Hv, Dv, Dk), device=dev, dtype=torch.float32)
-        keep = need_saved or resolved == L.FORM_CHUNK
-        n_saved = _saved_bytes(lib, B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form) if keep else 0
-        saved = torch.empty((n_saved,), device=dev, dtype=torch.uint8)
+        in_code = L.DTYPE_CODE[in_dtype]
+        n_saved = _saved_bytes(lib, B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form, in_code) if need_saved else 0
+        # a forward-only call keeps nothing (saved = NULL); the saved buffer of a training call may still be empty
+        # (T <= chunk), which is passed as a real pointer so that the library sees a training call
+        saved = torch.empty((max(n_saved, 1) if need_saved else 0,), device=dev, dtype=torch.uint8)
+        n_ws = int(lib.gdn_fwd_workspace_bytes(B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form, in_code,
+                                               int(need_saved)))
+        ws = torch.empty((n_ws,), device=dev, dtype=torch.uint8) if n_ws else None
         L.check(lib.gdn_fwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), L.ptr(state),
-                            L.ptr(mask), L.ptr(y), L.ptr(state_T), L.ptr(saved) if n_saved else None, n_saved,
-                            B, T, Hk, Hv, Dk, Dv, chunk, L.DTYPE_CODE[in_dtype], L.DTYPE_CODE[out_dtype],
+                            L.ptr(mask), L.ptr(y), L.ptr(state_T), L.ptr(saved) if need_saved else None, n_saved,
+                            L.ptr(ws), n_ws, B, T, Hk, Hv, Dk, Dv, chunk, in_code, L.DTYPE_CODE[out_dtype],
                             gate, form, L.stream_handle(dev)))
+        del ws
         ctx.save_for_backward(q, k, v, g, beta, state, mask, saved)
         ctx.meta = (chunk, gate, form)
         return y, state_T
@@ -83,7 +89,8 @@ class _GDNRecurrence(torch.autograd.Function):
         if dy is None:
             dy = torch.zeros((B, T, Hv, Dv), device=dev, dtype=torch.float32)
         dy = dy.contiguous()
-        if dy.dtype not in L.DTYPE_CODE:
+        if dy.dtype not in L.DTYPE_CODE or (q.dtype == torch.bfloat16 and dy.dtype == torch.float16):
+            # the chunked form with bf16 inputs reads a bf16 or fp32 cotangent
             dy = dy.float()
         dy = _aligned(dy)
         dstate_T = None if dstate_T is None else dstate_T.contiguous().float()
@@ -94,10 +101,11 @@ class _GDNRecurrence(torch.autograd.Function):
         dg = torch.empty(g.shape, device=dev, dtype=torch.float32)
         dbeta = torch.empty((B, T, Hv), device=dev, dtype=torch.float32)
         dS0 = torch.empty((B, Hv, Dv, Dk), device=dev, dtype=torch.float32)
-        ws_bytes = int(lib.gdn_bwd_workspace_bytes(B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form))
+        ws_bytes = int(lib.gdn_bwd_workspace_bytes(B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form,
+                                                   L.DTYPE_CODE[q.dtype]))
         ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
         L.check(lib.gdn_bwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), L.ptr(state), L.ptr(mask),
-                            L.ptr(saved) if saved.numel() else None, saved.numel(), L.ptr(dy),
+                            L.ptr(saved), saved.numel(), L.ptr(dy),
                             L.ptr(dstate_T), L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(dg), L.ptr(dbeta),
                             L.ptr(dS0), L.ptr(ws), ws_bytes, B, T, Hk, Hv, Dk, Dv, chunk,
                             L.DTYPE_CODE[q.dtype], L.DTYPE_CODE[dy.dtype], L.DTYPE_CODE[grad_dtype], gate,

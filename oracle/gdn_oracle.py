@@ -17,10 +17,10 @@ This is a NumPy restatement of the reference's arithmetic, one function per refe
 * ``gated_delta_chunked`` / ``gated_delta_chunked_vjp``
                         <- ``tools/gdn_vjp.py:503-528`` (public entry; state defaults to fp32 zeros)
 * ``gated_delta_ops_checkpointed`` <- ``tools/gdn_checkpoint.py:53-95`` (same forward, chunked by ``chunk``)
-* ``compute_g`` / ``gates``  <- ``engine/include/gdn.h:20-25``, ``engine/src/gdn.c:281-291``
+* ``compute_g`` / ``gates``  <- ``engine/include/gdn.h:20-25``, ``engine/src/gdn.c:51-61``
                                 (mlx-lm ``compute_g`` returns the multiplicative decay)
-* ``l2norm``            <- ``engine/include/gdn.h:17-18``, ``engine/src/gdn.c:270-279``
-* ``conv_silu``         <- ``engine/include/gdn.h:7-15``, ``engine/src/gdn.c:245-268`` (whole sequence)
+* ``l2norm``            <- ``engine/include/gdn.h:17-18``, ``engine/src/gdn.c:40-49``
+* ``conv_silu``         <- ``engine/include/gdn.h:7-15``, ``engine/src/gdn.c:15-38`` (whole sequence)
 * ``rmsnorm`` / ``silu_mul`` <- ``engine/include/ops.h:7-11``, ``engine/src/ops.c``
 * ``gated_rmsnorm``     <- ``engine/src/gdn_layer.c:47-55`` (rmsnorm(y)*silu(z) per value head)
 
@@ -261,7 +261,7 @@ def compute_g(A_log, a, dt_bias):
 
 
 def gates(a, b, A_log, dt_bias):
-    """(decay, beta) as gdn_gates (engine/src/gdn.c:281-291)."""
+    """(decay, beta) as gdn_gates (engine/src/gdn.c:51-61)."""
     return compute_g(A_log, a, dt_bias), 1.0 / (1.0 + np.exp(-b))
 
 
@@ -288,7 +288,7 @@ def gates_bwd(a, b, A_log, dt_bias, d_decay, d_beta, allow_neg_eigval=False):
 
 
 def l2norm(x, eps=1e-6, scale=1.0):
-    """scale * x / sqrt(sum x^2 + eps) over the last axis, sum in float64 (engine/src/gdn.c:270-279)."""
+    """scale * x / sqrt(sum x^2 + eps) over the last axis, sum in float64 (engine/src/gdn.c:40-49)."""
     x = np.asarray(x)
     ss = (x.astype(np.float64) ** 2).sum(axis=-1, keepdims=True)
     return (x * (scale / np.sqrt(ss + eps)).astype(x.dtype)).astype(x.dtype)

@@ -43,7 +43,7 @@ def _p(a: np.ndarray):
 
 
 def recurrence(q, k, v, g, beta, state0=None):
-    """Whole-sequence forward by repeated ``gdn_recurrent_step`` (engine/src/gdn.c:293-338).
+    """Whole-sequence forward by repeated ``gdn_recurrent_step`` (engine/include/gdn.h:27-38, engine/src/gdn.c:63-108).
 
     q, k [T,Hk,Dk]; v [T,Hv,Dv]; g, beta [T,Hv] (multiplicative decay); state [Hv,Dv,Dk].
     Returns (y [T,Hv,Dv], final state).  No mask, scalar gates (the C spec's scope).

@@ -1,6 +1,6 @@
 """Independent float64 torch statement of the delta-rule recurrence, for pinning the oracle's hand-derived
 backward with torch autograd (a library routine).  Written from the recurrence's definition
-(engine/include/gdn.h:217-226 plus the mask rule of tools/gdn_vjp.py:3-6), not from the oracle's code."""
+(engine/include/gdn.h:27-38 plus the mask rule of tools/gdn_vjp.py:3-6), not from the oracle's code."""
 
 import torch
 

@@ -16,7 +16,7 @@ def test_library_exports_every_declared_symbol():
             "gdn_profile_collect"} <= set(declared)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.gdn_version() >> 16 == 1
+    assert lib.gdn_version() >> 16 == 2
 
 
 def test_snapshot_count_matches_reference_boundaries():
@@ -31,7 +31,7 @@ def test_snapshot_count_matches_reference_boundaries():
 def test_abi_rejects_bad_arguments_without_launching():
     lib = gdn_lib.load()
     null = None
-    fwd = lambda *ints: lib.gdn_fwd(*([null] * 10), 0, *ints, null)
+    fwd = lambda *ints: lib.gdn_fwd(*([null] * 10), 0, null, 0, *ints, null)
     rc = fwd(1, 4, 2, 3, 8, 8, 0, 0, 0, 0, 0)
     assert rc == gdn_lib.GDN_ERR_INVALID
     assert b"chunk must be a positive integer" in lib.gdn_last_error()
@@ -48,14 +48,20 @@ def test_abi_rejects_bad_arguments_without_launching():
     # the chunked form cannot run a vector gate, and says so
     rc = fwd(1, 4, 1, 1, 128, 128, 64, 0, 0, gdn_lib.GATE_DECAY_VEC, gdn_lib.FORM_CHUNK)
     assert rc == gdn_lib.GDN_ERR_UNSUPPORTED and b"chunked form" in lib.gdn_last_error()
-    # the chunked form needs its saved buffer even for a forward-only call
+    # a forward-only call of the chunked form needs its group workspace; a training call its saved buffer
     fake = ctypes.c_void_p(256)   # never dereferenced: the size checks fail first
-    rc = lib.gdn_fwd(*([fake] * 6), null, fake, fake, null, 0, 1, 4, 1, 1, 128, 128, 64, 0, 0, 2, 0, null)
-    assert rc == gdn_lib.GDN_ERR_WORKSPACE
-    need = lib.gdn_bwd_workspace_bytes(1, 4, 1, 1, 8, 8, 64, 0, 0, 0)
-    assert need > 0 and lib.gdn_bwd_workspace_bytes(1, 4, 1, 1, 8, 8, 0, 0, 0, 0) == 0
+    rc = lib.gdn_fwd(*([fake] * 6), null, fake, fake, null, 0, null, 0, 1, 4, 1, 1, 128, 128, 64, 0, 0, 2, 0, null)
+    assert rc == gdn_lib.GDN_ERR_WORKSPACE and b"workspace of 0 bytes" in lib.gdn_last_error()
+    rc = lib.gdn_fwd(*([fake] * 6), null, fake, fake, fake, 16, null, 0, 1, 4, 1, 1, 128, 128, 64, 0, 0, 2, 0, null)
+    assert rc == gdn_lib.GDN_ERR_WORKSPACE and b"saved buffer of 16 bytes" in lib.gdn_last_error()
+    need = lib.gdn_bwd_workspace_bytes(1, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0)
+    assert need > 0 and lib.gdn_bwd_workspace_bytes(1, 4, 1, 1, 8, 8, 0, 0, 0, 0, 0) == 0
     rc = lib.gdn_bwd(*([fake] * 8), 0, *([fake] * 9), need - 1, 1, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0, 0, null)
     assert rc == gdn_lib.GDN_ERR_WORKSPACE
+    # bf16 inputs with an fp16 cotangent cannot run on the chunked form (its kernels read bf16 or fp32 dy)
+    rc = lib.gdn_bwd(*([fake] * 6), null, fake, 1 << 40, *([fake] * 9), 1 << 40, 1, 4, 1, 1, 128, 128, 64, 1, 2,
+                     1, 2, gdn_lib.FORM_CHUNK, null)
+    assert rc == gdn_lib.GDN_ERR_UNSUPPORTED and b"fp16" in lib.gdn_last_error()
     # B == 0 is a no-op
     assert fwd(0, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0) == 0
 
@@ -113,19 +119,70 @@ def test_block_wrappers_error_on_cpu_tensors():
 def test_saved_sizes_by_form():
     lib = gdn_lib.load()
     L = gdn_lib
-    rec = lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_RECURRENT)
+    rec = lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_RECURRENT, L.F32)
     assert rec == 63 * 32 * 128 * 128 * 4
-    ck = lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_AUTO)
-    assert ck == lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_CHUNK) > rec
+    ck = lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_AUTO, L.F32)
+    assert ck == lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_CHUNK, L.F32) > rec
     assert lib.gdn_select_form(128, 128, 0, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK
     assert lib.gdn_select_form(128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_RECURRENT
     assert lib.gdn_select_form(8, 8, 0, L.GATE_DECAY, L.FORM_AUTO) == L.FORM_RECURRENT
 
 
+def _ck_tile_bytes_per_chunk_head(bf16: bool) -> int:
+    """Bytes the chunked form keeps per (head, 64-token chunk) at chunk <= 64, stated independently of the
+    library: G (fp64), U, Delta (fp32 [64][128]), the entry state h, and T, plus per set
+      fp32: h fp32, T, P fp32 [64][64], W fp32 [64][128];
+      bf16: h bf16, T as hi / lo bf16 planes, W, (K diag(gamma_C/gamma))^T, -W^T (bf16 [64][128]), P and P^T as
+            hi / lo bf16 planes, and Q^T (bf16 [128][64]) once per key head (half a tile per value head at Hv/Hk=2)."""
+    C, D = 64, 128
+    common = C * 8 + 2 * C * D * 4 + C * C * 4
+    if bf16:
+        return common + D * D * 2 + 3 * C * D * 2 + 2 * (2 * C * C * 2) + C * D * 2 // 2
+    return common + D * D * 4 + C * C * 4 + C * D * 4
+
+
+@pytest.mark.parametrize("dt, bf16", [(gdn_lib.F32, False), (gdn_lib.BF16, True)])
+def test_chunked_saved_bytes_keep_tiles_or_snapshots(dt, bf16):
+    lib = gdn_lib.load()
+    L = gdn_lib
+    B, T, Hk, Hv = 4, 4096, 16, 32
+    full = lib.gdn_saved_bytes(B, T, Hk, Hv, 128, 128, 64, L.GATE_LOG, 0, L.FORM_CHUNK, dt)
+    per = _ck_tile_bytes_per_chunk_head(bf16)
+    assert full == pytest.approx(B * Hv * (T // 64) * per, rel=1e-3)
+    # chunk > 64 checkpoints: ceil(T / W) - 1 fp32 states, W = chunk rounded up to a multiple of 64
+    state = B * Hv * 128 * 128 * 4
+    for chunk, W in [(256, 256), (100, 128), (65, 128), (4096, 4096), (5000, 5056)]:
+        snaps = lib.gdn_saved_bytes(B, T, Hk, Hv, 128, 128, chunk, L.GATE_LOG, 0, L.FORM_CHUNK, dt)
+        assert snaps == max(-(-T // W) - 1, 0) * state
+    # chunk <= 64 always keeps the tiles
+    assert lib.gdn_saved_bytes(B, T, Hk, Hv, 128, 128, 16, L.GATE_LOG, 0, L.FORM_CHUNK, dt) == full
+
+
+def test_chunked_workspaces_are_bounded_by_groups():
+    lib = gdn_lib.load()
+    L = gdn_lib
+    args = lambda T, chunk: (1, T, 16, 32, 128, 128, chunk, L.GATE_LOG, 0, L.FORM_CHUNK, L.F32)
+    # full save: no forward workspace, a backward workspace that grows with T
+    assert lib.gdn_fwd_workspace_bytes(*args(4096, 64), 1) == 0
+    a, b = lib.gdn_bwd_workspace_bytes(*args(4096, 64)), lib.gdn_bwd_workspace_bytes(*args(8192, 64))
+    assert 1.9 < b / a < 2.1
+    # checkpointing and forward-only calls work group by group: the workspaces stop growing with T once a
+    # group (about 2048 chunk-heads) is reached
+    for fn in (lambda T: lib.gdn_bwd_workspace_bytes(*args(T, 256)),
+               lambda T: lib.gdn_fwd_workspace_bytes(*args(T, 256), 1),
+               lambda T: lib.gdn_fwd_workspace_bytes(*args(T, 64), 0)):
+        small, big, huge = fn(1024), fn(16384), fn(65536)
+        assert 0 < small < big == huge
+    # the checkpointed backward workspace is well below the full-save saved buffer plus workspace at T=16384
+    full = lib.gdn_saved_bytes(*args(16384, 64)) + lib.gdn_bwd_workspace_bytes(*args(16384, 64))
+    ckpt = lib.gdn_saved_bytes(*args(16384, 256)) + lib.gdn_bwd_workspace_bytes(*args(16384, 256))
+    assert ckpt < full / 3
+
+
 def test_workspace_scales_with_row_blocks_and_tokens():
     lib = gdn_lib.load()
-    a = lib.gdn_bwd_workspace_bytes(1, 4096, 16, 32, 128, 128, 64, 0, 0, 1)
-    b = lib.gdn_bwd_workspace_bytes(1, 8192, 16, 32, 128, 128, 64, 0, 0, 1)
+    a = lib.gdn_bwd_workspace_bytes(1, 4096, 16, 32, 128, 128, 64, 0, 0, 1, 0)
+    b = lib.gdn_bwd_workspace_bytes(1, 8192, 16, 32, 128, 128, 64, 0, 0, 1, 0)
     assert 1.9 < b / a < 2.1
 
 

@@ -80,23 +80,26 @@ def test_saved_intermediates_match_chunk_model(dev):
     q, k, v, g, beta, S0 = (t(d[n]) for n in ("q", "k", "v", "g_log", "beta", "state"))
     y = torch.empty((B, T, Hv, D), device=dev)
     ST = torch.empty((B, Hv, D, D), device=dev)
-    nbytes = lib.gdn_saved_bytes(B, T, Hk, Hv, D, D, 64, L.GATE_LOG, 0, L.FORM_CHUNK)
+    nbytes = lib.gdn_saved_bytes(B, T, Hk, Hv, D, D, 64, L.GATE_LOG, 0, L.FORM_CHUNK, L.F32)
     saved = torch.zeros(nbytes, device=dev, dtype=torch.uint8)
+    assert lib.gdn_fwd_workspace_bytes(B, T, Hk, Hv, D, D, 64, L.GATE_LOG, 0, L.FORM_CHUNK, L.F32, 1) == 0
     L.check(lib.gdn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), S0.data_ptr(),
-                        None, y.data_ptr(), ST.data_ptr(), saved.data_ptr(), nbytes, B, T, Hk, Hv, D, D, 64,
+                        None, y.data_ptr(), ST.data_ptr(), saved.data_ptr(), nbytes, None, 0, B, T, Hk, Hv, D, D, 64,
                         L.F32, L.F32, L.GATE_LOG, L.FORM_CHUNK, None))
     torch.cuda.synchronize()
     raw = saved.cpu().numpy()
     NC = -(-T // C)
     al = lambda x: (x + 255) // 256 * 256
-    sizes = [("H", B * Hv * NC * D * D * 4, np.float32), ("G", B * Hv * NC * C * 8, np.float64),
+    # the fp32 set's buffers in their order (the bf16 operand tiles have no storage in this set)
+    sizes = [("G", B * Hv * NC * C * 8, np.float64), ("U", B * Hv * NC * C * D * 4, np.float32),
+             ("H", B * Hv * NC * D * D * 4, np.float32), ("Dl", B * Hv * NC * C * D * 4, np.float32),
              ("T", B * Hv * NC * C * C * 4, np.float32), ("P", B * Hv * NC * C * C * 4, np.float32),
-             ("W", B * Hv * NC * C * D * 4, np.float32), ("U", B * Hv * NC * C * D * 4, np.float32),
-             ("Dl", B * Hv * NC * C * D * 4, np.float32)]
+             ("W", B * Hv * NC * C * D * 4, np.float32)]
     buf, off = {}, 0
     for name, n, dt in sizes:
         buf[name] = raw[off:off + n].view(dt)
         off += al(n)
+    assert off == nbytes
     H = buf["H"].reshape(B, Hv, NC, D, D)
     G = buf["G"].reshape(B, Hv, NC, C)
     Tm = buf["T"].reshape(B, Hv, NC, C, C)
