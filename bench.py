@@ -39,10 +39,42 @@ PEAK_BF16_TFLOPS = 2500.0
 CK_C = 64
 
 
+def algo_model(w):
+    """Algorithmic work per token of one fwd+VJP, as the roofline accounting of the measured path states it:
+
+    bf16 chunked form (bf16 q/k/v/dO/y/dq/dk/dv, fp32 gates and their gradients):
+      bytes 2 * (4 Hk D + 4 Hv D) + 4 * 4 Hv  (= 49,664 B at Hk=16, Hv=32, D=128);
+      flops per head-token: intra-chunk contractions 10 C D forward, x3 with the backward; state contractions
+      6 D^2 forward, x3 with the backward.  This build runs both on bf16 MFMA (the state operands are cast to
+      bf16 hi / lo pairs), so both are priced at the bf16 dense peak.
+    fp32 (recurrent arithmetic): bytes 4 * (4 Hk D + 4 Hv D + 4 Hv) (= 98,816 B); flops 27 D^2 per head-token
+      (7 D^2 forward + 20 D^2 backward), priced at the fp32 peak.
+    The per-sequence state traffic (S0, S_T, dS_T, dS0) and snapshot traffic are not algorithmic."""
+    Hk, Hv, D, C = w["Hk"], w["Hv"], w["D"], CK_C
+    if w["dtype"] == "bf16":
+        nbytes = 2 * (4 * Hk * D + 4 * Hv * D) + 4 * 4 * Hv
+        flops = {"bf16_intra_chunk": 3 * 10 * C * D * Hv, "bf16_state": 3 * 6 * D * D * Hv}
+        return nbytes, flops, PEAK_BF16_TFLOPS
+    nbytes = 4 * (4 * Hk * D + 4 * Hv * D + 4 * Hv)
+    return nbytes, {"fp32": 27 * D * D * Hv}, PEAK_FP32_TFLOPS
+
+
+def roof(nbytes, flops, peak_tflops, seconds):
+    """HBM and MFMA fractions of `nbytes` / `flops` done in `seconds`; the binding roof is the larger fraction."""
+    hbm = nbytes / seconds / 1e9
+    fl = flops / seconds / 1e12
+    f_hbm, f_fl = hbm / PEAK_HBM_GBS, fl / peak_tflops
+    if f_hbm >= f_fl:
+        return {"bound": "hbm", "achieved": round(hbm, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(f_hbm, 4), "other_roof_frac": round(f_fl, 4)}
+    return {"bound": "mfma", "achieved": round(fl, 3), "peak": peak_tflops, "unit": "TFLOP/s",
+            "frac": round(f_fl, 4), "other_roof_frac": round(f_hbm, 4)}
+
+
 def kernel_model(name, B, T, Hk, Hv, D, in_b):
-    """Algorithmic (flops, HBM bytes) of one launch of a kernel, from what the kernel must read and write
-    and the products it must form (recompute and padding excluded).  Chunk kernels: per (head, 64-token
-    chunk); recurrent kernels: per head-token state element."""
+    """Implementation model of one launch of a kernel: (flops, HBM bytes) from what this implementation's kernel
+    reads and writes, saved tiles included (recompute and padding excluded).  Chunk kernels: per (head, 64-token
+    chunk); recurrent kernels: per head-token state element.  Reported beside the roofline, never as it."""
     nc = -(-T // CK_C)
     ch = B * Hv * nc            # chunk-heads
     tokh = B * T * Hv           # head-tokens
@@ -178,9 +210,25 @@ def cpu_info():
     return info
 
 
-def cpu_baseline(T_sample=256):
-    """The NumPy oracle (restating tools/gdn_vjp.py _forward + _backward, impl="staged") on a bounded
-    sample: B=1, T_sample tokens, Hk=16, Hv=32, D=128, fp32, chunk 64; median of 3 after one warm-up."""
+def _oracle_group_run(args):
+    """One key-head group of the CPU baseline: the oracle's fwd+VJP on its value heads (worker process)."""
+    T, hk, rep = args
+    from oracle import gdn_oracle as O
+    d = O.make_inputs(1, T, 16, 32, 128, seed=0)
+    sl = slice(hk * rep, (hk + 1) * rep)
+    O.gated_delta_chunked_vjp(d["q"][:, :, hk:hk + 1], d["k"][:, :, hk:hk + 1], d["v"][:, :, sl],
+                              d["decay"][:, :, sl], d["beta"][:, :, sl], d["state"][:, sl], None,
+                              d["dy"][:, :, sl], None, chunk=64)
+
+
+def cpu_baseline(T_sample=256, T_parallel=1024, workers=None):
+    """The NumPy oracle (restating tools/gdn_vjp.py _forward + _backward, impl="staged"), fp32, chunk 64,
+    B=1, Hk=16, Hv=32, D=128, on bounded samples:
+      single core: the whole head set over T_sample tokens, median of 3 after one warm-up;
+      all cores: the 16 key-head groups (2 value heads each) in worker processes over T_parallel tokens, the wall
+      time of the slowest, median of 3 after one warm-up.
+    Runs before the GPU is touched (the workers are forked)."""
+    import multiprocessing as mp
     import numpy as np
     from oracle import gdn_oracle as O
     d = O.make_inputs(1, T_sample, 16, 32, 128, seed=0)
@@ -192,11 +240,24 @@ def cpu_baseline(T_sample=256):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    med1 = float(np.median(times))
+    n = workers or min(16, len(os.sched_getaffinity(0)))
+    jobs = [(T_parallel, hk, 2) for hk in range(16)]
+    ptimes = []
+    with mp.get_context("fork").Pool(n) as pool:
+        pool.map(_oracle_group_run, [(64, hk, 2) for hk in range(16)])
+        for _ in range(3):
+            t0 = time.perf_counter()
+            pool.map(_oracle_group_run, jobs, chunksize=1)
+            ptimes.append(time.perf_counter() - t0)
+    medp = float(np.median(ptimes))
     info = cpu_info()
-    return {"value": T_sample / med, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle fwd+VJP, B=1 T={T_sample} Hk=16 Hv=32 D=128 fp32 chunk 64, "
-                      f"median of 3 ({med:.2f} s) after 1 warm-up; elementwise numpy is single-threaded",
+    return {"value": round(T_parallel / medp, 1), "unit": "tokens/s", "cores": n, "kind": "port",
+            "sample": f"numpy oracle fwd+VJP, B=1 T={T_parallel} Hk=16 Hv=32 D=128 fp32 chunk 64: the 16 key-head "
+                      f"groups over {n} worker processes, median of 3 ({medp:.2f} s) after 1 warm-up",
+            "single_core": {"value": round(T_sample / med1, 1), "unit": "tokens/s", "cores": 1,
+                            "sample": f"the whole head set in one process, B=1 T={T_sample}, median of 3 "
+                                      f"({med1:.2f} s) after 1 warm-up; elementwise numpy is single-threaded"},
             "host": info}
 
 
@@ -215,6 +276,13 @@ def main():
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the GDN path here is "
               "single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
+
+    cb = None
+    if not args.no_cpu_baseline:
+        log("bench: cpu baseline (before the GPU is initialised)")
+        cb = cpu_baseline(args.cpu_sample)
+        log(f"bench: cpu baseline {cb['value']} tokens/s on {cb['cores']} cores, "
+            f"{cb['single_core']['value']} on one")
 
     import torch
     import gdn_engine
@@ -273,28 +341,30 @@ def main():
     ms, cnt = kt[dom]
     avg_ms = ms / cnt
     in_b = 2 if w["dtype"] == "bf16" else 4
-    flops, nbytes = kernel_model(dom, B, T, Hk, Hv, D, in_b)
-    t_s = avg_ms * 1e-3
-    peak_flops = PEAK_BF16_TFLOPS if (w["dtype"] == "bf16" and dom.startswith("ck_")) else PEAK_FP32_TFLOPS
-    f_frac = flops / t_s / 1e12 / peak_flops
-    b_frac = nbytes / t_s / 1e9 / PEAK_HBM_GBS
-    if b_frac >= f_frac:
-        roofline = {"bound": "hbm", "achieved": round(nbytes / t_s / 1e9, 1), "peak": PEAK_HBM_GBS,
-                    "unit": "GB/s", "frac": round(b_frac, 4)}
-    else:
-        roofline = {"bound": "mfma", "achieved": round(flops / t_s / 1e12, 3), "peak": peak_flops,
-                    "unit": "TFLOP/s", "frac": round(f_frac, 4)}
+    step_s = elapsed / args.steps
+    a_bytes, a_flops, a_peak = algo_model(w)
+    # units one launch processes: tokens of the batch per launch (a launch covers a group of tokens when the
+    # call runs group-wise)
+    launch_tokens = tokens * args.steps / cnt
+    roofline = roof(a_bytes * launch_tokens, sum(a_flops.values()) * launch_tokens, a_peak, avg_ms * 1e-3)
     traffic = None
     tj = ROOT / "profiles" / "traffic.json"
     if tj.exists():
         rec = json.loads(tj.read_text()).get(args.workload, {}).get(dom)
         if rec:
             traffic = rec["read_bytes"] + rec["write_bytes"]
+    i_flops, i_bytes = kernel_model(dom, B, T, Hk, Hv, D, in_b)
     roofline.update({
         "traffic": traffic, "traffic_source": "profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE)"
         if traffic else None, "kernel": dom, "avg_launch_ms": round(avg_ms, 4),
-        "algo_flops_per_launch": flops, "algo_bytes_per_launch": nbytes,
-        "other_roof_frac": round(min(f_frac, b_frac), 4),
+        "algo_bytes_per_token": a_bytes, "algo_flops_per_token": a_flops, "tokens_per_launch": launch_tokens,
+        "algo_bytes_per_launch": a_bytes * launch_tokens,
+        "algo_flops_per_launch": sum(a_flops.values()) * launch_tokens,
+        # the whole step against the same roofline (a block step also runs the projections: no step roof there)
+        "step": None if "block" in w else dict(roof(a_bytes * tokens, sum(a_flops.values()) * tokens, a_peak,
+                                                     step_s), ms=round(step_s * 1e3, 4)),
+        "implementation_model": {"bytes_per_launch": i_bytes, "flops_per_launch": i_flops,
+                                 "hbm_frac": round(i_bytes / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
         "kernels_ms_per_step": {n: round(v[0] / args.steps, 4) for n, v in kt.items()}})
     if "block" in w:
         lib_ms = sum(v[0] for v in kt.values()) / args.steps
@@ -311,9 +381,7 @@ def main():
         "peak_hbm_gib": round(peak_gib, 3),
         "roofline": roofline,
     }
-    if not args.no_cpu_baseline:
-        log("bench: cpu baseline")
-        cb = cpu_baseline(args.cpu_sample)
+    if cb is not None:
         line["cpu_baseline"] = cb
         line["gpu_over_cpu"] = round(value / cb["value"], 1)
     print(json.dumps(line), flush=True)
