@@ -111,6 +111,17 @@ int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const f
             int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk,
             int in_dtype, int out_dtype, int gate_kind, int form, void *stream);
 
+/* One decode step: the recurrence over a single token of B sequences, replacing gdn_recurrent_step
+ * (engine/include/gdn.h:27-38, engine/src/gdn.c:63-108) batched over sequences.
+ *   q, k [B][Hk][Dk], v [B][Hv][Dv] (in_dtype); g, beta [B][Hv] (g as gate_kind: GDN_GATE_DECAY, GDN_GATE_LOG,
+ *   or [B][Hv][Dk] for GDN_GATE_DECAY_VEC) fp32; y [B][Hv][Dv] (out_dtype);
+ *   state_in, state_out [B][Hv][Dv][Dk] fp32: state_out may be state_in (updated in place, as gdn_recurrent_step
+ *   does); state_in NULL means zeros.
+ * Forward only; any Dk <= 256 and Dv. */
+int gdn_decode_step(const void *q, const void *k, const void *v, const float *g, const float *beta,
+                    const float *state_in, float *state_out, void *y, int B, int Hk, int Hv, int Dk, int Dv,
+                    int in_dtype, int out_dtype, int gate_kind, void *stream);
+
 /* Device workspace gdn_bwd needs, in bytes (256-byte aligned base expected). */
 size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind,
                                int has_mask, int form, int in_dtype);

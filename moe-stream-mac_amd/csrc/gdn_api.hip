@@ -530,6 +530,28 @@ int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const f
     return check_launch(st, "gdn_fwd");
 }
 
+int gdn_decode_step(const void *q, const void *k, const void *v, const float *g, const float *beta,
+                    const float *state_in, float *state_out, void *y, int B, int Hk, int Hv, int Dk, int Dv,
+                    int in_dtype, int out_dtype, int gate_kind, void *stream) {
+    g_err[0] = 0;
+    int rc = check_shape(B, 1, Hk, Hv, Dk, Dv, 1, gate_kind, GDN_FORM_RECURRENT);
+    if (rc) return rc;
+    if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    if (B == 0) return GDN_OK;
+    if (!q || !k || !v || !g || !beta || !y || !state_out)
+        return fail(GDN_ERR_INVALID, "null input or output pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // one token of the recurrent form: every thread reads its state elements before writing the same ones, so
+    // state_out may be state_in
+    RecFwdArgs a{q, k, v, g, beta, state_in, nullptr, y, state_out, nullptr,
+                 B, 1, Hk, Hv, Dk, Dv, 1, in_dtype, out_dtype, gate_kind};
+    {
+        Timed tm("rec_decode", st);
+        launch_rec_fwd(a, st);
+    }
+    return check_launch(st, "gdn_decode_step");
+}
+
 size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind,
                                int has_mask, int form, int in_dtype) {
     if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;

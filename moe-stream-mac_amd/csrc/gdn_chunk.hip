@@ -265,14 +265,20 @@ __device__ __forceinline__ size_t chunk_index(const Args &a, int b, int hv, int 
     return ((size_t)b * a.Hv + hv) * a.NC + c;
 }
 
-// Chunks [cb, ce) and entry state of a sequential forward workgroup whose grid.z index is z (Args::recompute).
+// What a sequential forward launch writes.  FWD_TRAIN: y, the final state and the tiles the backward reads (H,
+// Delta); FWD_ONLY: y, the final state and the window snapshots (when Args::snap is set); FWD_RECOMPUTE: the windows
+// of the launch side by side, H and Delta only (Args::recompute).
+enum FwdMode { FWD_TRAIN = 0, FWD_ONLY = 1, FWD_RECOMPUTE = 2 };
+
+// Chunks [cb, ce) and entry state of a sequential forward workgroup whose grid.z index is z.
 struct SeqRange {
     int b, cb, ce;
     const float *s0;
 };
+template <int MODE>
 __device__ __forceinline__ SeqRange seq_range(const Args &a, int z) {
     SeqRange r{z, 0, a.NC, a.state0};
-    if (a.recompute) {
+    if constexpr (MODE == FWD_RECOMPUTE) {
         const int w = z / a.B, gw = a.win0 + w;
         r.b = z - w * a.B;
         r.cb = w * a.wc;
@@ -293,9 +299,10 @@ __device__ __forceinline__ void store_state_acc(float *dst, const f4 (&h)[NTN], 
         for (int e = 0; e < 4; ++e) dst[(head * D + i0 + 16 * t + li) * D + 16 * w + 4 * lg + e] = h[t][e];
 }
 
-// Forward mode with windows: the snapshot taken on entering local chunk c, or NULL.
+// FWD_ONLY with windows: the snapshot taken on entering local chunk c, or NULL.
+template <int MODE>
 __device__ __forceinline__ float *snap_at(const Args &a, int c) {
-    if (!a.snap || a.recompute || a.wc <= 0 || c == 0 || c % a.wc) return nullptr;
+    if (MODE != FWD_ONLY || !a.snap || a.wc <= 0 || c == 0 || c % a.wc) return nullptr;
     return a.snap + (size_t)(a.win0 + c / a.wc - 1) * a.B * a.Hv * D * D;
 }
 
@@ -469,8 +476,9 @@ struct RcScale {
     __device__ float operator()(int r) const { return expf((float)(G[C - 1] - G[r])); }
 };
 
-template <int VS>
+template <int VS, int MODE>
 __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
+    constexpr bool kTiles = MODE != FWD_ONLY, kOut = MODE != FWD_RECOMPUTE;
     constexpr int LV = VS + 4;
     constexpr int NTN = VS / 16;                 // value tiles of the slice
     constexpr int DN = NTN >= 2 ? NTN / 2 : 1;   // value tiles per wave for [C][VS] products
@@ -482,7 +490,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
     __shared__ double sG[C];
 
     const SeqBlock sb = seq_block();
-    const SeqRange sr = seq_range(a, sb.b);
+    const SeqRange sr = seq_range<MODE>(a, sb.b);
     const int i0 = sb.slice * VS, hv = sb.hv, b = sr.b, cb = sr.cb, ce = sr.ce;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
@@ -525,7 +533,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
     for (int c = cb; c < ce; ++c) {
         const int t0 = c * C, n = min(C, T - t0);
         const size_t ci = head * a.NC + c;
-        if (float *sp = snap_at(a, c)) store_state_acc<NTN>(sp, h, head, i0, w, lg, li);
+        if (float *sp = snap_at<MODE>(a, c)) store_state_acc<NTN>(sp, h, head, i0, w, lg, li);
         __syncthreads();
 #pragma unroll
         for (int t = 0; t < NTN; ++t)
@@ -537,7 +545,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
         if (tid < C) sG[tid] = rG;
         __syncthreads();
         if (c + 1 < ce) fetchA(c + 1);
-        if (a.w.H) store_state_slice<VS, LV, NTS>(a.w.H + ci * D * D, sH, i0);
+        if (kTiles) store_state_slice<VS, LV, NTS>(a.w.H + ci * D * D, sH, i0);
         // Delta = U - W h ; Yi = Q h
         f4 wh[DN], yi[DN];
 #pragma unroll
@@ -552,7 +560,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
                     const int r = mrow + 4 * lg + e, ii = 16 * (nt0 + t) + li;
                     const float dl = sU[r * LV + ii] - wh[t][e];
                     sD[r * LV + ii] = dl;
-                    if (a.w.Dl) a.w.Dl[ci * C * D + r * D + i0 + ii] = dl;
+                    if (kTiles) a.w.Dl[ci * C * D + r * D + i0 + ii] = dl;
                 }
         }
         __syncthreads();
@@ -560,7 +568,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
         tile_store(sQ, LD, rK, a.in_dt, RcScale{sG});
         __syncthreads();
         if (c + 1 < ce) fetchB(c + 1);
-        if (cwave && a.y) {
+        if (cwave && kOut) {
             // Y = diag(gamma) Q h + P Delta
 #pragma unroll
             for (int t = 0; t < DN; ++t)
@@ -583,7 +591,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
         for (int t = 0; t < NTN; ++t) h[t] *= gC;
         mma_strip<C, NTN>(h, sQ + 16 * w, 1, LD, sD, LV, 1, 16);
     }
-    if (a.state_T && !a.recompute) store_state_acc<NTN>(a.state_T, h, head, i0, w, lg, li);
+    if (kOut && a.state_T) store_state_acc<NTN>(a.state_T, h, head, i0, w, lg, li);
 }
 
 // ---------------------------------------------------------------------------------------------- ck_bwd_seq
@@ -1961,8 +1969,9 @@ struct FwdFrags {
     double g;
 };
 
-template <int VS>
+template <int VS, int MODE>
 __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
+    constexpr bool kTiles = MODE != FWD_ONLY, kOut = MODE != FWD_RECOMPUTE;
     constexpr int NTN = VS / 16, DN = NTN >= 2 ? NTN / 2 : 1;
     constexpr int LH = D + 8, LDd = C + 8;
     __shared__ __align__(16) bfr sHh[VS * LH];
@@ -1972,7 +1981,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
     __shared__ float sGamBuf[2][C];  // by chunk parity: read after the second barrier, rewritten two chunks later
 
     const SeqBlock sb = seq_block();
-    const SeqRange sr = seq_range(a, sb.b);
+    const SeqRange sr = seq_range<MODE>(a, sb.b);
     const int i0 = sb.slice * VS, hv = sb.hv, b = sr.b, cb = sr.cb, ce = sr.ce;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
@@ -2021,12 +2030,12 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
     auto step = [&](const int c, FwdFrags<DN> &cur, FwdFrags<DN> &nxt) {
         const int t0 = c * C, n = min(C, T - t0);
         const size_t ci = head * a.NC + c;
-        if (float *sp = snap_at(a, c)) store_state_acc<NTN>(sp, h, head, i0, w, lg, li);
+        if (float *sp = snap_at<MODE>(a, c)) store_state_acc<NTN>(sp, h, head, i0, w, lg, li);
         // h -> LDS as the operand [i][j]; the chunk-entry state -> saved H ([j][i], bf16)
 #pragma unroll
         for (int t = 0; t < NTN; ++t) {
             acc_T<true>(h[t], sHh, sHl, LH, 16 * w, 16 * t);
-            if (a.w.H) {
+            if constexpr (kTiles) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     reinterpret_cast<bfr *>(a.w.H)[ci * D * D + (size_t)(16 * w + 4 * lg + e) * D + i0 + 16 * t + li] =
@@ -2053,7 +2062,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) dl[e] = cur.U[t][e] - wh[t][e];
                 acc_T<true>(dl, sDh, sDl, LDd, mrow, 16 * (nt0 + t));
-                if (a.w.Dl) {
+                if constexpr (kTiles) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         a.w.Dl[ci * C * D + (size_t)(mrow + 4 * lg + e) * D + i0 + 16 * (nt0 + t) + li] = dl[e];
@@ -2061,7 +2070,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
             }
         }
         __syncthreads();
-        if (cwave && a.y) {
+        if (cwave && kOut) {
             // Y = diag(gamma) Q h + P Delta
 #pragma unroll
             for (int t = 0; t < DN; ++t)
@@ -2090,7 +2099,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
         step(c, fa, fb);
         if (c + 1 < ce) step(c + 1, fb, fa);
     }
-    if (a.state_T && !a.recompute) store_state_acc<NTN>(a.state_T, h, head, i0, w, lg, li);
+    if (kOut && a.state_T) store_state_acc<NTN>(a.state_T, h, head, i0, w, lg, li);
 }
 
 // ---------------------------------------------------------------------------------------------- ck_prep (bf16)
@@ -2628,16 +2637,24 @@ static int slice_width(int heads) { return heads >= 128 ? 64 : heads >= 64 ? 32 
 // Workgroups along grid.z of the sequential kernels: the sequences, times the windows when they run side by side.
 static int seq_z(const ck::Args &a) { return a.recompute ? a.B * ((a.NC + a.wc - 1) / a.wc) : a.B; }
 
+template <int MT, int VS, int MODE>
+static void fwd_launch(const ck::Args &a, hipStream_t st, dim3 grid) {
+    if constexpr (MT == 1) hipLaunchKernelGGL((ck::ck_fwd_bf16_kernel<VS, MODE>), grid, dim3(ck::NTS), 0, st, a);
+    else hipLaunchKernelGGL((ck::ck_fwd_kernel<VS, MODE>), grid, dim3(ck::NTS), 0, st, a);
+}
+
 template <int MT, int VS>
 static void seq_launch(const ck::Args &a, hipStream_t st, bool fwd) {
     const dim3 grid(CK_D / VS, a.Hv, seq_z(a));
-    if constexpr (MT == 1) {
-        if (fwd) hipLaunchKernelGGL((ck::ck_fwd_bf16_kernel<VS>), grid, dim3(ck::NTS), 0, st, a);
-        else if (a.dy_dt == DT_F32) hipLaunchKernelGGL((ck::ck_bwd_seq_bf16_kernel<VS, true>), grid, dim3(ck::NTS), 0, st, a);
+    if (fwd) {
+        if (a.recompute) fwd_launch<MT, VS, ck::FWD_RECOMPUTE>(a, st, grid);
+        else if (a.fwd_only) fwd_launch<MT, VS, ck::FWD_ONLY>(a, st, grid);
+        else fwd_launch<MT, VS, ck::FWD_TRAIN>(a, st, grid);
+    } else if constexpr (MT == 1) {
+        if (a.dy_dt == DT_F32) hipLaunchKernelGGL((ck::ck_bwd_seq_bf16_kernel<VS, true>), grid, dim3(ck::NTS), 0, st, a);
         else hipLaunchKernelGGL((ck::ck_bwd_seq_bf16_kernel<VS, false>), grid, dim3(ck::NTS), 0, st, a);
     } else {
-        if (fwd) hipLaunchKernelGGL((ck::ck_fwd_kernel<VS>), grid, dim3(ck::NTS), 0, st, a);
-        else hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<VS>), grid, dim3(ck::NTS), 0, st, a);
+        hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<VS>), grid, dim3(ck::NTS), 0, st, a);
     }
 }
 

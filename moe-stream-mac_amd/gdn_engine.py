@@ -189,12 +189,47 @@ def recurrence(q, k, v, g, beta, state, mask=None, chunk: int = 64, log_gate: bo
         need_grad = grads_wanted
     form_code = default_form() if form is None else L.FORMS[form]
     pq, pk, pv, pg, pb, ps, pm = _prep(q, k, v, g, beta, state, mask)
+    if not (need_grad and grads_wanted) and q.shape[1] == 1 and pm is None:
+        # one token, no gradient: the decode step (gdn_recurrent_step's counterpart)
+        with torch.no_grad():
+            state_T = torch.empty_like(ps)
+            y = decode_step(pq[:, 0], pk[:, 0], pv[:, 0], pg[:, 0], pb[:, 0], ps, state_T, log_gate, out_dtype)
+        return y[:, None], state_T
     if not (need_grad and grads_wanted):
         with torch.no_grad():
             return _GDNRecurrence.forward(_NoCtx(), pq, pk, pv, pg, pb, ps, pm, chunk, log_gate, out_dtype,
                                           False, form_code)
     y, state_T = _GDNRecurrence.apply(pq, pk, pv, pg, pb, ps, pm, chunk, log_gate, out_dtype, True, form_code)
     return y, state_T
+
+
+def decode_step(q, k, v, g, beta, state_in, state_out, log_gate: bool = False,
+                out_dtype: Optional[torch.dtype] = None):
+    """One token of B sequences: q, k [B, Hk, Dk], v [B, Hv, Dv], g [B, Hv] (or [B, Hv, Dk]), beta [B, Hv];
+    reads state_in [B, Hv, Dv, Dk] fp32 (None = zeros) and writes state_out (which may be state_in: in place).
+    Returns y [B, Hv, Dv].  Forward only (engine/include/gdn.h:27-38)."""
+    dev = _require_device(q, k, v, g, beta, state_out)
+    B, Hk, Dk = q.shape
+    Hv, Dv = v.shape[1], v.shape[2]
+    if state_out.dtype != torch.float32 or not state_out.is_contiguous() or \
+            tuple(state_out.shape) != (B, Hv, Dv, Dk):
+        raise ValueError("state_out must be a contiguous float32 [B, Hv, Dv, Dk] tensor")
+    if state_in is not None:
+        state_in = state_in.to(torch.float32).contiguous()
+    gate = gate_kind_for(g[:, None], log_gate)
+    out_dtype = out_dtype or q.dtype
+    if out_dtype not in L.DTYPE_CODE:
+        out_dtype = torch.float32
+    y = torch.empty((B, Hv, Dv), device=dev, dtype=out_dtype)
+    lib = L.load()
+    # the contiguous copies stay referenced until the launch is enqueued (a copy freed earlier could hand its
+    # memory to the next one)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    g, beta = g.float().contiguous(), beta.float().contiguous()
+    L.check(lib.gdn_decode_step(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), L.ptr(state_in),
+                                L.ptr(state_out), L.ptr(y), B, Hk, Hv, Dk, Dv, L.DTYPE_CODE[q.dtype],
+                                L.DTYPE_CODE[out_dtype], gate, L.stream_handle(dev)))
+    return y
 
 
 class _NoCtx:

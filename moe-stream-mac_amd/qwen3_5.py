@@ -83,7 +83,10 @@ class GatedDeltaNet(nn.Module):
         self.norm = RMSNormGated(self.Dv, args.rms_norm_eps)
         self.out_proj = nn.Linear(self.value_dim, h, bias=False)
 
-    def forward(self, x: Array, mask: Optional[Array] = None, state: Optional[Array] = None) -> Array:
+    def forward(self, x: Array, mask: Optional[Array] = None, cache: Optional["GDNCache"] = None) -> Array:
+        """x [B, T, hidden] -> [B, T, hidden].  With a cache (mlx-lm's two-entry cache: the conv state, then the
+        recurrent state) the call continues the sequences the cache holds and leaves their states after x in it:
+        a prefill, then one call per decoded token."""
         B, T, _ = x.shape
         projs = (self.in_proj_qkv, self.in_proj_z, self.in_proj_b, self.in_proj_a)
         if all(isinstance(m, LoRALinear) and m.base.bias is None for m in projs):
@@ -94,12 +97,41 @@ class GatedDeltaNet(nn.Module):
         if mask is not None:
             qkv = qkv * mask[..., None].to(qkv.dtype)
         # conv + SiLU, split, per-head q/k L2 norm (q scaled by Dk^-1/2): one fused kernel pair
-        q, k, v = gdn_block.conv_qkv(qkv, self.conv1d.weight, self.Hk, self.Dk, self.Hv, self.Dv,
-                                     self.Dk ** -0.5, 1e-6)
+        conv_state = None if cache is None else cache[0]
+        q, k, v, *conv_next = gdn_block.conv_qkv(qkv, self.conv1d.weight, self.Hk, self.Dk, self.Hv, self.Dv,
+                                                 self.Dk ** -0.5, 1e-6, state=conv_state,
+                                                 return_state=cache is not None)
         update = globals()["gated_delta_update"]
-        out, _ = update(q, k, v, a, b, self.A_log, self.dt_bias, state, mask, use_kernel=not self.training)
+        state = None if cache is None else cache[1]
+        out, state_next = update(q, k, v, a, b, self.A_log, self.dt_bias, state, mask,
+                                 use_kernel=not self.training)
+        if cache is not None:
+            cache[0], cache[1] = conv_next[0], state_next
         out = self.norm(out.to(z.dtype), z)
         return self.out_proj(out.reshape(B, T, -1))
+
+
+class GDNCache:
+    """Decode state of one GatedDeltaNet layer, indexed like mlx-lm's ArraysCache(2): [0] the conv state
+    [B, K-1, conv_dim] fp32 (the last K-1 conv inputs, oldest first), [1] the recurrent state [B, Hv, Dv, Dk] fp32.
+    Both start as None (zeros)."""
+
+    def __init__(self):
+        self.entries: list[Optional[Array]] = [None, None]
+
+    def __getitem__(self, i: int) -> Optional[Array]:
+        return self.entries[i]
+
+    def __setitem__(self, i: int, value: Optional[Array]) -> None:
+        self.entries[i] = value
+
+
+class KVCache:
+    """Keys and values seen so far by one Attention layer, [B, T_past, heads, head_dim] each."""
+
+    def __init__(self):
+        self.k: Optional[Array] = None
+        self.v: Optional[Array] = None
 
 
 class Attention(nn.Module):
@@ -112,11 +144,17 @@ class Attention(nn.Module):
         self.qkv = nn.Linear(h, 3 * h, bias=False)
         self.o_proj = nn.Linear(h, h, bias=False)
 
-    def forward(self, x: Array, mask: Optional[Array] = None, state: Optional[Array] = None) -> Array:
+    def forward(self, x: Array, mask: Optional[Array] = None, cache: Optional[KVCache] = None) -> Array:
         B, T, H = x.shape
         q, k, v = self.qkv(x).float().reshape(B, T, 3, self.nh, H // self.nh).unbind(2)
+        past = 0
+        if cache is not None:
+            if cache.k is not None:
+                past = cache.k.shape[1]
+                k, v = torch.cat([cache.k, k], 1), torch.cat([cache.v, v], 1)
+            cache.k, cache.v = k, v
         att = torch.einsum("bqhd,bkhd->bhqk", q, k) / math.sqrt(H // self.nh)
-        causal = torch.ones(T, T, dtype=torch.bool, device=x.device).tril()
+        causal = torch.ones(T, past + T, dtype=torch.bool, device=x.device).tril(past)
         att = att.masked_fill(~causal, float("-inf")).softmax(-1)
         out = torch.einsum("bhqk,bkhd->bqhd", att, v).reshape(B, T, H).to(x.dtype)
         return self.o_proj(out)
@@ -147,9 +185,12 @@ class DecoderLayer(nn.Module):
         self.gate_up = nn.Linear(h, 2 * args.intermediate_size, bias=False)
         self.down = nn.Linear(args.intermediate_size, h, bias=False)
 
-    def forward(self, x: Array, mask: Optional[Array] = None) -> Array:
+    def make_cache(self):
+        return GDNCache() if self.is_linear else KVCache()
+
+    def forward(self, x: Array, mask: Optional[Array] = None, cache=None) -> Array:
         mixer = self.linear_attn if self.is_linear else self.self_attn
-        x = x + mixer(self.input_layernorm(x), mask)
+        x = x + mixer(self.input_layernorm(x), mask, cache)
         gate, up = self.gate_up(self.post_attention_layernorm(x)).chunk(2, dim=-1)
         return x + self.down(F.silu(gate) * up)
 
@@ -162,10 +203,14 @@ class TextModel(nn.Module):
         self.layers = nn.ModuleList(DecoderLayer(args, t) for t in args.layer_types)
         self.norm = RMSNorm(args.hidden_size, args.rms_norm_eps)
 
-    def forward(self, tokens: Array, mask: Optional[Array] = None) -> Array:
+    def make_cache(self) -> list:
+        """One cache per decoder layer (GDNCache for linear attention, KVCache for attention)."""
+        return [layer.make_cache() for layer in self.layers]
+
+    def forward(self, tokens: Array, mask: Optional[Array] = None, cache: Optional[list] = None) -> Array:
         x = self.embed_tokens(tokens)
-        for layer in self.layers:
-            x = layer(x, mask)
+        for i, layer in enumerate(self.layers):
+            x = layer(x, mask, None if cache is None else cache[i])
         return self.norm(x)
 
 
@@ -179,8 +224,11 @@ class Model(nn.Module):
     def layers(self):
         return self.model.layers
 
-    def forward(self, tokens: Array, mask: Optional[Array] = None) -> Array:
-        return self.lm_head(self.model(tokens, mask))
+    def make_cache(self) -> list:
+        return self.model.make_cache()
+
+    def forward(self, tokens: Array, mask: Optional[Array] = None, cache: Optional[list] = None) -> Array:
+        return self.lm_head(self.model(tokens, mask, cache))
 
 
 Qwen3_5TextModel = TextModel

@@ -19,6 +19,19 @@ def test_library_exports_every_declared_symbol():
     assert lib.gdn_version() >> 16 == 2
 
 
+def test_bindings_match_header_arities():
+    """Every declared function has a ctypes binding with as many arguments as its prototype."""
+    import re
+    text = gdn_lib.HEADER.read_text()
+    protos = re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(gdn_[a-z_0-9]+)\s*\(([^)]*)\)\s*;", text, re.M)
+    assert len(protos) >= 20
+    for name, params in protos:
+        params = params.strip()
+        n = 0 if params in ("", "void") else params.count(",") + 1
+        assert name in gdn_lib._SIGS, name
+        assert len(gdn_lib._SIGS[name][0]) == n, (name, len(gdn_lib._SIGS[name][0]), n)
+
+
 def test_snapshot_count_matches_reference_boundaries():
     lib = gdn_lib.load()
     # the reference keeps ceil(T/chunk)+1 boundaries including S0 and S_T (tools/gdn_vjp.py:205-235)
@@ -64,6 +77,14 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert rc == gdn_lib.GDN_ERR_UNSUPPORTED and b"fp16" in lib.gdn_last_error()
     # B == 0 is a no-op
     assert fwd(0, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0) == 0
+    # the decode step checks its arguments the same way
+    dec = lambda ptrs, *ints: lib.gdn_decode_step(*ptrs, *ints, null)
+    assert dec([fake] * 8, 0, 1, 1, 8, 8, 0, 0, 0) == 0
+    assert dec([fake] * 8, 1, 1, 1, 300, 8, 0, 0, 0) == gdn_lib.GDN_ERR_UNSUPPORTED
+    assert dec([fake] * 8, 1, 2, 3, 8, 8, 0, 0, 0) == gdn_lib.GDN_ERR_INVALID
+    assert dec([fake] * 7 + [null], 1, 1, 1, 8, 8, 0, 0, 0) == gdn_lib.GDN_ERR_INVALID
+    assert b"null" in lib.gdn_last_error()
+    assert dec([fake] * 8, 1, 1, 1, 8, 8, 0, 0, 9) == gdn_lib.GDN_ERR_INVALID
 
 
 def test_block_op_abi_rejects_bad_arguments_without_launching():
