@@ -111,6 +111,16 @@ int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const f
             int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk,
             int in_dtype, int out_dtype, int gate_kind, int form, void *stream);
 
+/* gdn_fwd without a saved buffer (the forward-only call) that allocates nothing and takes no workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  Its group buffers live in a fixed 64 MiB device array, one per
+ * GPU, held until the process ends; results equal gdn_fwd's.  The chunked form needs one 64-token group of all
+ * B * Hv heads to fit (B * Hv up to about 300); larger calls return GDN_ERR_UNSUPPORTED.  Calls that overlap on
+ * one GPU (other streams or threads) share the array and race; calls on one stream are ordered. */
+int gdn_fwd_noalloc(const void *q, const void *k, const void *v, const float *g, const float *beta,
+                    const float *state0, const uint8_t *mask, void *y, float *state_T, int B, int T, int Hk, int Hv,
+                    int Dk, int Dv, int in_dtype, int out_dtype, int gate_kind, int form, void *stream);
+
 /* One decode step: the recurrence over a single token of B sequences, replacing gdn_recurrent_step
  * (engine/include/gdn.h:27-38, engine/src/gdn.c:63-108) batched over sequences.
  *   q, k [B][Hk][Dk], v [B][Hv][Dv] (in_dtype); g, beta [B][Hv] (g as gate_kind: GDN_GATE_DECAY, GDN_GATE_LOG,

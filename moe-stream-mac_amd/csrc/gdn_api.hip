@@ -482,9 +482,70 @@ static int ck_backward(const ChunkCall &base, int chunk, const void *saved, size
     return GDN_OK;
 }
 
+// Fixed device scratch of gdn_fwd_noalloc: a file-scope device array, one copy per GPU, held until the process
+// ends.  Host code never passes the array's name to a kernel (that is a host-side stand-in); it uses the address
+// hipGetSymbolAddress returns for the current device.
+constexpr size_t kNoAllocScratchBytes = 64u << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices];  // device ordinal -> that device's copy of `scratch` (NULL: not looked up)
+
+// The current device's scratch address, looked up once per device with that device current; NULL (with the
+// error set) on failure.
+static void *device_scratch() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+        fail(GDN_ERR_LAUNCH, "gdn_fwd_noalloc: no current HIP device");
+        return nullptr;
+    }
+    if (dev >= kMaxDevices) {
+        fail(GDN_ERR_UNSUPPORTED, "gdn_fwd_noalloc: device ordinal %d >= %d", dev, kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev]) return g_scratch_ptr[dev];
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+        fail(GDN_ERR_LAUNCH, "gdn_fwd_noalloc: hipGetSymbolAddress of the scratch failed: %s", hipGetErrorString(e));
+        return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+    return ptr;
+}
+
 }  // namespace gdn
 
 extern "C" {
+
+int gdn_fwd_noalloc(const void *q, const void *k, const void *v, const float *g, const float *beta,
+                    const float *state0, const uint8_t *mask, void *y, float *state_T, int B, int T, int Hk, int Hv,
+                    int Dk, int Dv, int in_dtype, int out_dtype, int gate_kind, int form, void *stream) {
+    g_err[0] = 0;
+    int rc = check_shape(B, T, Hk, Hv, Dk, Dv, kChunkC, gate_kind, form);
+    if (rc) return rc;
+    if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    const int f = resolve_form(Dk, Dv, mask != nullptr, gate_kind, form);
+    if (f < 0) return f;
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+    if (f == GDN_FORM_CHUNK && B > 0 && T > 0) {
+        const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16};
+        const size_t one = ck_fwd_group_bytes(shp, std::min(kChunkC, T), false);
+        if (one > kNoAllocScratchBytes)
+            return fail(GDN_ERR_UNSUPPORTED,
+                        "gdn_fwd_noalloc: one 64-token group of %d x %d heads needs %zu bytes; the fixed scratch "
+                        "holds %zu (use gdn_fwd with a workspace)", B, Hv, one, kNoAllocScratchBytes);
+        ws = device_scratch();
+        if (!ws) return GDN_ERR_LAUNCH;
+        ws_bytes = kNoAllocScratchBytes;
+    }
+    // the forward-only call of gdn_fwd, with the fixed scratch as its workspace
+    return gdn_fwd(q, k, v, g, beta, state0, mask, y, state_T, nullptr, 0, ws, ws_bytes, B, T, Hk, Hv, Dk, Dv,
+                   kChunkC, in_dtype, out_dtype, gate_kind, form, stream);
+}
 
 int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const float *beta,
             const float *state0, const uint8_t *mask, void *y, float *state_T, void *saved, size_t saved_bytes,

@@ -53,6 +53,7 @@ _SIGS = {
     "gdn_fwd": ([_vp] * 10 + [_sz, _vp, _sz] + [_i] * 11 + [_vp], _i),
     "gdn_bwd_workspace_bytes": ([_i] * 11, ctypes.c_size_t),
     "gdn_decode_step": ([_vp] * 8 + [_i] * 8 + [_vp], _i),
+    "gdn_fwd_noalloc": ([_vp] * 9 + [_i] * 10 + [_vp], _i),
     "gdn_bwd": ([_vp] * 8 + [ctypes.c_size_t] + [_vp] * 9 + [ctypes.c_size_t] + [_i] * 12 + [_vp], _i),
     "gdn_profile_enable": ([_i], _i),
     "gdn_profile_collect": ([_i, ctypes.c_char_p, _i, ctypes.POINTER(ctypes.c_double),

@@ -1,0 +1,87 @@
+"""gdn_fwd_noalloc (the forward-only call with no allocation and no workspace) against the existing entry point,
+gdn_fwd with saved = NULL and a workspace, through the C ABI: two calls in a row, the second with a smaller input.
+
+Both run the same kernels, group by group from carried fp32 states, so the outputs are equal bit for bit whatever
+the group sizes (the fixed scratch holds fewer chunks per group than the workspace gdn_fwd_workspace_bytes sizes).
+The recurrent form (a mask) needs no scratch and is checked the same way.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import gdn_lib
+    gdn_lib.load()
+    return torch.device("cuda:0")
+
+
+def _inputs(B, T, Hk, Hv, D, dtype, dev, seed):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    n = lambda *s: torch.randn(*s, device=dev, generator=g)
+    q = torch.nn.functional.normalize(n(B, T, Hk, D), dim=-1) * D ** -0.5
+    k = torch.nn.functional.normalize(n(B, T, Hk, D), dim=-1)
+    return dict(q=q.to(dtype), k=k.to(dtype), v=n(B, T, Hv, D).to(dtype), g=-torch.rand(B, T, Hv, device=dev,
+                generator=g), beta=torch.rand(B, T, Hv, device=dev, generator=g),
+                S0=n(B, Hv, D, D) * 0.02)
+
+
+def _run(x, dev, noalloc, mask=None):
+    import gdn_lib as L
+    lib = L.load()
+    B, T, Hk, D = x["q"].shape
+    Hv = x["v"].shape[2]
+    code = L.DTYPE_CODE[x["q"].dtype]
+    y = torch.full((B, T, Hv, D), float("nan"), device=dev, dtype=x["q"].dtype)
+    S = torch.full((B, Hv, D, D), float("nan"), device=dev)
+    ptrs = [x[n].data_ptr() for n in ("q", "k", "v", "g", "beta", "S0")]
+    m = None if mask is None else mask.data_ptr()
+    if noalloc:
+        rc = lib.gdn_fwd_noalloc(*ptrs, m, y.data_ptr(), S.data_ptr(), B, T, Hk, Hv, D, D, code, code, L.GATE_LOG,
+                                 L.FORM_AUTO, None)
+    else:
+        n_ws = lib.gdn_fwd_workspace_bytes(B, T, Hk, Hv, D, D, 64, L.GATE_LOG, int(mask is not None), L.FORM_AUTO,
+                                           code, 0)
+        ws = torch.empty(max(n_ws, 1), device=dev, dtype=torch.uint8)
+        rc = lib.gdn_fwd(*ptrs, m, y.data_ptr(), S.data_ptr(), None, 0, ws.data_ptr(), n_ws, B, T, Hk, Hv, D, D, 64,
+                         code, code, L.GATE_LOG, L.FORM_AUTO, None)
+    L.check(rc)
+    torch.cuda.synchronize()
+    return y, S
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_noalloc_forward_matches_gdn_fwd_twice(dev, dtype):
+    # first call: 4 x 32 heads over 1000 tokens (several groups in the fixed scratch); second: a smaller input
+    for B, T, seed in ((4, 1000, 1), (2, 300, 2)):
+        print(f"gdn_fwd_noalloc {dtype} B={B} T={T} Hk=16 Hv=32 D=128", flush=True)
+        x = _inputs(B, T, 16, 32, 128, dtype, dev, seed)
+        y0, S0 = _run(x, dev, noalloc=False)
+        y1, S1 = _run(x, dev, noalloc=True)
+        assert torch.isfinite(y1.float()).all() and torch.isfinite(S1).all()
+        assert torch.equal(y0, y1) and torch.equal(S0, S1)
+
+
+def test_noalloc_recurrent_form_and_limits(dev):
+    """A masked call runs the recurrent form (no scratch); a call whose one-chunk group exceeds the fixed scratch is
+    refused with a clear error before anything runs."""
+    import gdn_lib as L
+    x = _inputs(2, 70, 2, 4, 128, torch.float32, dev, 3)
+    mask = torch.ones(2, 70, dtype=torch.uint8, device=dev)
+    mask[:, 50:] = 0
+    for _ in range(2):
+        y0, S0 = _run(x, dev, noalloc=False, mask=mask)
+        y1, S1 = _run(x, dev, noalloc=True, mask=mask)
+        assert torch.equal(y0, y1) and torch.equal(S0, S1)
+    lib = L.load()
+    fake = 256
+    rc = lib.gdn_fwd_noalloc(*([fake] * 6), None, fake, fake, 16, 64, 16, 64, 128, 128, L.BF16, L.BF16, L.GATE_LOG,
+                             L.FORM_CHUNK, None)
+    assert rc == L.GDN_ERR_UNSUPPORTED and b"fixed scratch" in lib.gdn_last_error()
