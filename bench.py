@@ -11,6 +11,12 @@ Workloads (one GPU; the default is the T=4096 configuration the metric is quoted
   fp32_b1_t4096   B=1, T=4096, same heads, fp32
   fp32_b1_t2048   B=1, T=2048, fp32, S0 ~ N(0, 0.02), full dS0
   ckpt_b1_t16384  B=1, T=16384, fp32, snapshots every 256 tokens, peak HBM reported
+  masked_bf16_b4_t4096
+                  bf16_b4_t4096 with a mask (each sequence's last 10% masked, padding); masks run the recurrent form
+  stream_ops_bf16_b2_t8192
+                  the streaming kernels around the recurrence on block-shaped bf16 inputs (B=2, T=8192, Hk=16,
+                  Hv=32, D=128): fused conv + SiLU + split + q/k L2 norm, plain conv + SiLU (8192 channels), q/k L2
+                  norm, gates, gated RMSNorm; a step is each forward and its backward once
   block_bf16_b2_t8192
                   one whole GDN block (projections with LoRA rank 16, conv1d K=4 + SiLU, q/k L2 norm, gates,
                   recurrence, gated RMSNorm * SiLU(z), out-projection), B=2, T=8192, hidden 2048, bf16 weights
@@ -39,7 +45,7 @@ PEAK_BF16_TFLOPS = 2500.0
 CK_C = 64
 
 
-def algo_model(w):
+def algo_model(w, form="chunk"):
     """Algorithmic work per token of one fwd+VJP, as the roofline accounting of the measured path states it:
 
     bf16 chunked form (bf16 q/k/v/dO/y/dq/dk/dv, fp32 gates and their gradients):
@@ -49,8 +55,13 @@ def algo_model(w):
       bf16 hi / lo pairs), so both are priced at the bf16 dense peak.
     fp32 (recurrent arithmetic): bytes 4 * (4 Hk D + 4 Hv D + 4 Hv) (= 98,816 B); flops 27 D^2 per head-token
       (7 D^2 forward + 20 D^2 backward), priced at the fp32 peak.
+    The recurrent form (masks, vector gates) computes the recurrence itself, 27 D^2 flops per head-token on fp32
+    VALU, whatever the input dtype; its bytes follow the dtype as above.
     The per-sequence state traffic (S0, S_T, dS_T, dS0) and snapshot traffic are not algorithmic."""
     Hk, Hv, D, C = w["Hk"], w["Hv"], w["D"], CK_C
+    if form == "recurrent":
+        b = 2 if w["dtype"] == "bf16" else 4
+        return b * (4 * Hk * D + 4 * Hv * D) + 4 * 4 * Hv, {"fp32": 27 * D * D * Hv}, PEAK_FP32_TFLOPS
     if w["dtype"] == "bf16":
         nbytes = 2 * (4 * Hk * D + 4 * Hv * D) + 4 * 4 * Hv
         flops = {"bf16_intra_chunk": 3 * 10 * C * D * Hv, "bf16_state": 3 * 6 * D * D * Hv}
@@ -138,6 +149,10 @@ WORKLOADS = {
     "fp32_b1_t4096": dict(B=1, T=4096, Hk=16, Hv=32, D=128, dtype="fp32", chunk=64, s0_std=0.0),
     "fp32_b1_t2048": dict(B=1, T=2048, Hk=16, Hv=32, D=128, dtype="fp32", chunk=64, s0_std=0.02),
     "ckpt_b1_t16384": dict(B=1, T=16384, Hk=16, Hv=32, D=128, dtype="fp32", chunk=256, s0_std=0.0),
+    "masked_bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
+                                 masked_tail=0.1),
+    "stream_ops_bf16_b2_t8192": dict(B=2, T=8192, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
+                                     ops=True),
     "block_bf16_b2_t8192": dict(B=2, T=8192, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
                                 block=dict(hidden=2048, K=4, rank=16, lora_scale=20.0)),
 }
@@ -193,6 +208,23 @@ def make_block(w, dev, seed=0):
     x = torch.randn(shape, device=dev, generator=gen).to(torch.bfloat16).requires_grad_(True)
     dout = torch.randn(shape, device=dev, generator=gen).to(torch.bfloat16)
     return blk, x, dout
+
+
+def make_stream_ops(w, dev, seed=0):
+    """Inputs, leaves and cotangents of the streaming block kernels at the workload's shape (bf16 activations,
+    fp32 parameters)."""
+    import torch
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    B, T, Hk, Hv, D = w["B"], w["T"], w["Hk"], w["Hv"], w["D"]
+    C = 2 * Hk * D + Hv * D
+    n = lambda *s: torch.randn(*s, device=dev, generator=gen)
+    bf = torch.bfloat16
+    x = dict(qkv=n(B, T, C).to(bf), conv_w=n(C, 4) * 0.3, qr=n(B, T, Hk, D).to(bf), kr=n(B, T, Hk, D).to(bf),
+             a=n(B, T, Hv).to(bf), b=n(B, T, Hv).to(bf), A_log=torch.rand(Hv, device=dev, generator=gen) * 2.7,
+             dt_bias=n(Hv) * 0.1, y=n(B, T, Hv, D).to(bf), z=n(B, T, Hv, D).to(bf), norm_w=1 + 0.1 * n(D))
+    leaves = [t.requires_grad_(True) for t in x.values()]
+    return x, leaves
 
 
 def cpu_info():
@@ -308,13 +340,35 @@ def main():
 
         def step():
             return torch.autograd.grad(blk(xb), leaves, dout)
+    elif "ops" in w:
+        import gdn_block as GB
+        so, leaves = make_stream_ops(w, dev)
+        cot = None
+
+        def outputs():
+            q, k, v = GB.conv_qkv(so["qkv"], so["conv_w"], Hk, D, Hv, D, D ** -0.5)
+            c = GB.conv_silu(so["qkv"], so["conv_w"])
+            qn, kn = GB.normalize_qk(so["qr"], so["kr"], D ** -0.5)
+            g, beta = GB.gates(so["a"], so["b"], so["A_log"], so["dt_bias"])
+            o = GB.gated_rmsnorm(so["y"], so["z"], so["norm_w"])
+            return [q, k, v, c, qn, kn, g, beta, o]
+
+        with torch.no_grad():
+            cot = [torch.randn_like(t) for t in outputs()]
+
+        def step():
+            return torch.autograd.grad(outputs(), leaves, cot)
     else:
         x = make_inputs(w, dev)
         out_dtype = x["q"].dtype
         leaves = [x[n].requires_grad_(True) for n in ("q", "k", "v", "g_log", "beta", "state")]
+        mask = None
+        if w.get("masked_tail"):
+            mask = torch.ones(B, T, dtype=torch.bool, device=dev)
+            mask[:, T - int(T * w["masked_tail"]):] = False
 
         def step():
-            y, S = gdn_engine.recurrence(x["q"], x["k"], x["v"], x["g_log"], x["beta"], x["state"], None,
+            y, S = gdn_engine.recurrence(x["q"], x["k"], x["v"], x["g_log"], x["beta"], x["state"], mask,
                                          chunk=w["chunk"], log_gate=True, output_dtype=out_dtype)
             return torch.autograd.grad([y], leaves, [x["dy"]])
 
@@ -342,10 +396,14 @@ def main():
     avg_ms = ms / cnt
     in_b = 2 if w["dtype"] == "bf16" else 4
     step_s = elapsed / args.steps
-    a_bytes, a_flops, a_peak = algo_model(w)
+    form = "chunk" if any(n.startswith("ck_") for n in kt) else "recurrent"
+    a_bytes, a_flops, a_peak = algo_model(w, form)
     # units one launch processes: tokens of the batch per launch (a launch covers a group of tokens when the
     # call runs group-wise)
     launch_tokens = tokens * args.steps / cnt
+    if "ops" in w:
+        # streaming kernels: the bytes the launch must read and write, against the HBM roof
+        a_bytes, a_flops = kernel_model(dom, B, T, Hk, Hv, D, in_b)[1] / tokens, {"none": 0}
     roofline = roof(a_bytes * launch_tokens, sum(a_flops.values()) * launch_tokens, a_peak, avg_ms * 1e-3)
     traffic = None
     tj = ROOT / "profiles" / "traffic.json"
@@ -361,20 +419,24 @@ def main():
         "algo_bytes_per_launch": a_bytes * launch_tokens,
         "algo_flops_per_launch": sum(a_flops.values()) * launch_tokens,
         # the whole step against the same roofline (a block step also runs the projections: no step roof there)
-        "step": None if "block" in w else dict(roof(a_bytes * tokens, sum(a_flops.values()) * tokens, a_peak,
+        "step": None if ("block" in w or "ops" in w) else dict(roof(a_bytes * tokens, sum(a_flops.values()) * tokens, a_peak,
                                                      step_s), ms=round(step_s * 1e3, 4)),
         "implementation_model": {"bytes_per_launch": i_bytes, "flops_per_launch": i_flops,
                                  "hbm_frac": round(i_bytes / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
-        "kernels_ms_per_step": {n: round(v[0] / args.steps, 4) for n, v in kt.items()}})
+        "kernels_ms_per_step": {n: round(v[0] / args.steps, 4) for n, v in kt.items()},
+        # every kernel's modelled bytes per launch over its own average launch time
+        "kernels_gbs": {n: round(kernel_model(n, B, T, Hk, Hv, D, in_b)[1] / (v[0] / v[1] * 1e-3) / 1e9, 1)
+                        for n, v in kt.items() if kernel_model(n, B, T, Hk, Hv, D, in_b)[1]}})
     if "block" in w:
         lib_ms = sum(v[0] for v in kt.values()) / args.steps
         roofline["outside_library_ms_per_step"] = round(elapsed / args.steps * 1e3 - lib_ms, 4)
-    form = "chunk" if any(n.startswith("ck_") for n in kt) else "recurrent"
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16" if (w["dtype"] == "bf16" and form == "chunk") else "fp32", "data": "synthetic",
+        "dtype": "bf16" if (w["dtype"] == "bf16" and (form == "chunk" or "ops" in w)) else "fp32",
+        "data": "synthetic",
+        # the masked workload's inputs are bf16 but the recurrent form computes in fp32
         "config": {"workload": args.workload, "B": B, "T": T, "Hk": Hk, "Hv": Hv, "Dk": D, "Dv": D,
                    "chunk": w["chunk"], "inputs": w["dtype"], "state": "fp32", "form": form,
                    "global_batch": B, "seq_len": T, "parallelism": "single-gpu", **w.get("block", {})},
