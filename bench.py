@@ -12,7 +12,8 @@ Workloads (one GPU; the default is the T=4096 configuration the metric is quoted
   fp32_b1_t2048   B=1, T=2048, fp32, S0 ~ N(0, 0.02), full dS0
   ckpt_b1_t16384  B=1, T=16384, fp32, snapshots every 256 tokens, peak HBM reported
   masked_bf16_b4_t4096
-                  bf16_b4_t4096 with a mask (each sequence's last 10% masked, padding); masks run the recurrent form
+                  bf16_b4_t4096 with a mask (each sequence's last 10% masked, padding): two chunked
+                  passes plus the masked tokens' fix-up
   stream_ops_bf16_b2_t8192
                   the streaming kernels around the recurrence on block-shaped bf16 inputs (B=2, T=8192, Hk=16,
                   Hv=32, D=128): fused conv + SiLU + split + q/k L2 norm, plain conv + SiLU (8192 channels), q/k L2
@@ -436,7 +437,7 @@ def main():
         "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16" if (w["dtype"] == "bf16" and (form == "chunk" or "ops" in w)) else "fp32",
         "data": "synthetic",
-        # the masked workload's inputs are bf16 but the recurrent form computes in fp32
+        # inputs in bf16 run in bf16 only on the chunked form: the recurrent form computes in fp32
         "config": {"workload": args.workload, "B": B, "T": T, "Hk": Hk, "Hv": Hv, "Dk": D, "Dv": D,
                    "chunk": w["chunk"], "inputs": w["dtype"], "state": "fp32", "form": form,
                    "global_batch": B, "seq_len": T, "parallelism": "single-gpu", **w.get("block", {})},

@@ -50,7 +50,8 @@ enum gdn_gate {
 enum gdn_form {
     GDN_FORM_AUTO = 0,       /* the chunked form when eligible, else the recurrent form */
     GDN_FORM_RECURRENT = 1,  /* token-sequential recurrence, state rows resident in VGPRs; any shape */
-    GDN_FORM_CHUNK = 2       /* chunked WY/UT form on MFMA (64-token tiles); Dk = Dv = 128, no mask, scalar gate */
+    GDN_FORM_CHUNK = 2       /* chunked WY/UT form on MFMA (64-token tiles); Dk = Dv = 128, scalar gate; a mask runs
+                                two chunked passes (see below) */
 };
 
 /* Library version, (major << 16) | minor. */
@@ -89,6 +90,12 @@ int gdn_select_form(int Dk, int Dv, int has_mask, int gate_kind, int form);
  * Group-wise calls use the largest group of windows (or of 64-token chunks, forward-only) that fits the workspace
  * given, up to the size the *_workspace_bytes queries return; fewer groups is faster, one window (chunk) is the
  * minimum. */
+
+/* Masks on the chunked form.  A masked step keeps the state but its output reads the candidate state.  The chunked
+ * form runs the recurrence with decay 1 and beta 0 at masked tokens (the same states), once with q and once with k as
+ * the query, and rewrites y at masked tokens as decay y' + beta (k . q) (v - decay z) from the two outputs; the
+ * backward runs both passes' backwards and the rewrite's VJP.  Needs Hv <= 256; the saved buffer holds both passes
+ * (checkpointing: pass 1's snapshots serve both) plus fp32 [B][T][Hv][Dv] copies of the two outputs. */
 
 /* Size of the buffer gdn_fwd fills for gdn_bwd (the "saved" activations) for inputs of in_dtype. */
 size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind, int has_mask,

@@ -103,8 +103,10 @@ static int check_shape(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, 
     return GDN_OK;
 }
 
+// Masked calls run the chunked form as two passes (gdn_mask.hip) and need no other condition.
 static bool chunk_eligible(int Dk, int Dv, int has_mask, int gate) {
-    return Dk == 128 && Dv == 128 && !has_mask && (gate == GATE_DECAY || gate == GATE_LOG);
+    (void)has_mask;
+    return Dk == 128 && Dv == 128 && (gate == GATE_DECAY || gate == GATE_LOG);
 }
 
 // The form a (shape, mask, gate, requested form) resolves to, or < 0 when a requested form cannot run.
@@ -113,7 +115,7 @@ static int resolve_form(int Dk, int Dv, int has_mask, int gate, int form) {
     const bool ok = chunk_eligible(Dk, Dv, has_mask, gate);
     if (form == GDN_FORM_CHUNK)
         return ok ? GDN_FORM_CHUNK
-                  : fail(GDN_ERR_UNSUPPORTED, "the chunked form needs Dk = Dv = 128, no mask and a scalar gate");
+                  : fail(GDN_ERR_UNSUPPORTED, "the chunked form needs Dk = Dv = 128 and a scalar gate");
     return ok ? GDN_FORM_CHUNK : GDN_FORM_RECURRENT;
 }
 
@@ -208,6 +210,58 @@ static size_t ck_bwd_target_bytes(const CkShape &s, int W) {
     return ck_bwd_group_bytes(s, std::min(g * W, s.T));
 }
 
+// ---- masked calls on the chunked form: two chunked passes over the effective gates (gdn_mask.hip)
+//
+// saved (training): pass 1's saved buffer (tiles or snapshots), pass 2's tiles (chunk <= 64 only: checkpointing
+// rebuilds pass 2 from pass 1's snapshots, the state sequences being the same), the effective gates g', beta', and
+// z and y' (fp32 [B][T][Hv][Dv], read at masked tokens).
+struct MaskSaved {
+    size_t p1, p2, g2, b2, Z, Yp, total;
+};
+static MaskSaved mask_saved(const CkShape &s, int chunk) {
+    const int W = ck_window(chunk);
+    const size_t tiles = chunk_sizes(s.B, s.T, s.Hk, s.Hv, s.bf16, true).saved;
+    const size_t ng = (size_t)s.B * s.T * s.Hv * 4, nv = ng * kChunkD;
+    MaskSaved m{};
+    size_t off = 0;
+    m.p1 = off; off += align256(W ? ck_snap_bytes(s.B, s.T, s.Hv, W) : tiles);
+    m.p2 = off; off += align256(W ? 0 : tiles);
+    m.g2 = off; off += align256(ng);
+    m.b2 = off; off += align256(ng);
+    m.Z = off; off += align256(nv);
+    m.Yp = off; off += align256(nv);
+    m.total = off;
+    return m;
+}
+
+// Backward workspace: one pass's workspace (used by both passes in turn), the passes' cotangents and their fp32
+// gradients.
+struct MaskWork {
+    size_t pass, pass_bytes, dy1, dz, g1[6], g2[6], total;  // g1 / g2: dq, dk, dv, dg, dbeta, dS0
+};
+static MaskWork mask_work(const CkShape &s, int chunk) {
+    const int W = ck_window(chunk);
+    MaskWork m{};
+    m.pass_bytes = W ? ck_bwd_target_bytes(s, W) : chunk_sizes(s.B, s.T, s.Hk, s.Hv, s.bf16, true).work;
+    const size_t nqk = (size_t)s.B * s.T * s.Hk * kChunkD * 4, ng = (size_t)s.B * s.T * s.Hv * 4, nv = ng * kChunkD;
+    const size_t nst = ck_state_bytes(s.B, s.Hv);
+    const size_t sizes[6] = {nqk, nqk, nv, ng, ng, nst};
+    size_t off = 0;
+    m.pass = off; off += align256(m.pass_bytes);
+    m.dy1 = off; off += align256(nv);
+    m.dz = off; off += align256(nv);
+    for (int i = 0; i < 6; ++i) { m.g1[i] = off; off += align256(sizes[i]); }
+    for (int i = 0; i < 6; ++i) { m.g2[i] = off; off += align256(sizes[i]); }
+    m.total = off;
+    return m;
+}
+
+// Forward-only workspace: g', beta', z, then the group workspace.
+static size_t mask_fwd_only_head(const CkShape &s) {
+    const size_t ng = (size_t)s.B * s.T * s.Hv * 4;
+    return 2 * align256(ng) + align256(ng * kChunkD);
+}
+
 static size_t dt_size(int dt) { return dt == DT_F32 ? 4 : 2; }
 
 template <class P>
@@ -282,6 +336,7 @@ size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, 
     if (f < 0 || B == 0 || T == 0) return 0;
     if (f == GDN_FORM_CHUNK) {
         const int W = ck_window(chunk);
+        if (has_mask) return mask_saved({B, T, Hk, Hv, in_dtype == DT_BF16}, chunk).total;
         if (W) return ck_snap_bytes(B, T, Hv, W);
         return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true).saved;
     }
@@ -294,8 +349,14 @@ size_t gdn_fwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int
     const int f = resolve_form(Dk, Dv, has_mask, gate_kind, form);
     if (f != GDN_FORM_CHUNK || B == 0 || T == 0) return 0;
     const int W = ck_window(chunk);
+    const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16};
+    if (has_mask) {
+        // pass 2 runs forward-only when checkpointing; a forward-only call also holds g', beta' and z
+        if (with_saved) return W ? std::max(ck_fwd_target_bytes(shp, W, true), ck_fwd_target_bytes(shp, W, false)) : 0;
+        return mask_fwd_only_head(shp) + ck_fwd_target_bytes(shp, W, false);
+    }
     if (with_saved && !W) return 0;
-    return ck_fwd_target_bytes({B, T, Hk, Hv, in_dtype == DT_BF16}, W, with_saved != 0);
+    return ck_fwd_target_bytes(shp, W, with_saved != 0);
 }
 
 }  // extern "C"
@@ -482,6 +543,145 @@ static int ck_backward(const ChunkCall &base, int chunk, const void *saved, size
     return GDN_OK;
 }
 
+static char *at_off(void *base, size_t off) { return static_cast<char *>(base) + off; }
+
+// Masked chunked forward (resolved form GDN_FORM_CHUNK, arguments checked).  base holds the caller's q, k, v, g,
+// beta, state0, y, state_T and shapes.
+static int ck_masked_forward(const ChunkCall &base, const uint8_t *mask, int chunk, void *saved, size_t saved_bytes,
+                             void *ws, size_t ws_bytes, hipStream_t st) {
+    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16};
+    const int W = ck_window(chunk);
+    const size_t tokens = (size_t)base.B * base.T;
+    float *g2, *b2, *Z, *Yp = nullptr;
+    void *p1 = nullptr, *p2 = nullptr;
+    size_t p1_bytes = 0, p2_bytes = 0;
+    void *gws = ws;
+    size_t gws_bytes = ws ? ws_bytes : 0;
+    if (saved) {
+        const MaskSaved m = mask_saved(shp, chunk);
+        if (saved_bytes < m.total)
+            return fail(GDN_ERR_WORKSPACE, "saved buffer of %zu bytes is smaller than the %zu bytes required",
+                        saved_bytes, m.total);
+        p1 = at_off(saved, m.p1);
+        p1_bytes = m.p2 - m.p1;
+        if (!W) {
+            p2 = at_off(saved, m.p2);
+            p2_bytes = m.g2 - m.p2;
+        }
+        g2 = reinterpret_cast<float *>(at_off(saved, m.g2));
+        b2 = reinterpret_cast<float *>(at_off(saved, m.b2));
+        Z = reinterpret_cast<float *>(at_off(saved, m.Z));
+        Yp = reinterpret_cast<float *>(at_off(saved, m.Yp));
+    } else {
+        const size_t head = mask_fwd_only_head(shp);
+        if (!ws || ws_bytes < head)
+            return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes a masked call needs",
+                        ws ? ws_bytes : 0, head);
+        const size_t ng = align256(tokens * base.Hv * 4);
+        g2 = reinterpret_cast<float *>(ws);
+        b2 = reinterpret_cast<float *>(at_off(ws, ng));
+        Z = reinterpret_cast<float *>(at_off(ws, 2 * ng));
+        gws = at_off(ws, head);
+        gws_bytes = ws_bytes - head;
+    }
+    launch_mask_gates(base.g, base.beta, mask, g2, b2, tokens, base.Hv, base.gate, st);
+    int rc = check_launch(st, "gdn_fwd(mask gates)");
+    if (rc) return rc;
+    // pass 2: k as the query, z = S' k (fp32); its tiles kept only without checkpointing
+    ChunkCall c2 = base;
+    c2.q = base.k;
+    c2.g = g2;
+    c2.beta = b2;
+    c2.y = Z;
+    c2.out_dt = DT_F32;
+    c2.state_T = nullptr;
+    if ((rc = ck_forward(c2, chunk, p2, p2_bytes, gws, gws_bytes, st))) return rc;
+    // pass 1: y' into y, or in fp32 into Yp when the backward needs it (the fix-up then writes every y)
+    ChunkCall c1 = base;
+    c1.g = g2;
+    c1.beta = b2;
+    if (Yp) {
+        c1.y = Yp;
+        c1.out_dt = DT_F32;
+    }
+    if ((rc = ck_forward(c1, chunk, p1, p1_bytes, gws, gws_bytes, st))) return rc;
+    MaskArgs ma{};
+    ma.q = base.q; ma.k = base.k; ma.v = base.v; ma.g = base.g; ma.beta = base.beta; ma.mask = mask;
+    ma.y = base.y; ma.Z = Z; ma.Yp = Yp;
+    ma.Hk = base.Hk; ma.Hv = base.Hv; ma.Dk = kChunkD; ma.Dv = kChunkD;
+    ma.in_dt = base.in_dt; ma.out_dt = base.out_dt; ma.gate = base.gate;
+    {
+        Timed tm("mask_fix_fwd", st);
+        launch_mask_fix_fwd(ma, tokens, st);
+    }
+    return check_launch(st, "gdn_fwd(mask fix-up)");
+}
+
+// Masked chunked backward (resolved form GDN_FORM_CHUNK, arguments checked).
+static int ck_masked_backward(const ChunkCall &base, const uint8_t *mask, int chunk, const void *saved,
+                              size_t saved_bytes, void *ws, size_t ws_bytes, hipStream_t st) {
+    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16};
+    const int W = ck_window(chunk);
+    const size_t tokens = (size_t)base.B * base.T;
+    const MaskSaved m = mask_saved(shp, chunk);
+    if (!saved || saved_bytes < m.total)
+        return fail(GDN_ERR_INVALID, "the saved buffer written by gdn_fwd (%zu bytes) is required", m.total);
+    const MaskWork k = mask_work(shp, chunk);
+    if (!ws || ws_bytes < k.total)
+        return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", ws_bytes,
+                    k.total);
+    void *sv = const_cast<void *>(saved);
+    const float *g2 = reinterpret_cast<const float *>(at_off(sv, m.g2));
+    const float *b2 = reinterpret_cast<const float *>(at_off(sv, m.b2));
+    float *wf[2][6];
+    for (int i = 0; i < 6; ++i) {
+        wf[0][i] = reinterpret_cast<float *>(at_off(ws, k.g1[i]));
+        wf[1][i] = reinterpret_cast<float *>(at_off(ws, k.g2[i]));
+    }
+    MaskArgs ma{};
+    ma.q = base.q; ma.k = base.k; ma.v = base.v; ma.dy = base.dy; ma.g = base.g; ma.beta = base.beta;
+    ma.mask = mask;
+    ma.Z = reinterpret_cast<const float *>(at_off(sv, m.Z));
+    ma.Yp = reinterpret_cast<float *>(at_off(sv, m.Yp));
+    ma.dy1 = reinterpret_cast<float *>(at_off(ws, k.dy1));
+    ma.dz = reinterpret_cast<float *>(at_off(ws, k.dz));
+    ma.Hk = base.Hk; ma.Hv = base.Hv; ma.Dk = kChunkD; ma.Dv = kChunkD;
+    ma.in_dt = base.in_dt; ma.dy_dt = base.dy_dt; ma.grad_dt = base.grad_dt; ma.gate = base.gate;
+    {
+        Timed tm("mask_bwd_cot", st);
+        launch_mask_bwd_cot(ma, tokens, st);
+    }
+    int rc = check_launch(st, "gdn_bwd(mask cotangents)");
+    if (rc) return rc;
+    const bool want_ds0 = base.dstate0 != nullptr;
+    for (int pass = 0; pass < 2; ++pass) {
+        ChunkCall c = base;
+        c.g = g2;
+        c.beta = b2;
+        c.dy = pass ? ma.dz : ma.dy1;
+        c.dy_dt = DT_F32;
+        c.grad_dt = DT_F32;
+        c.dq = wf[pass][0]; c.dk = wf[pass][1]; c.dv = wf[pass][2]; c.dg = wf[pass][3]; c.dbeta = wf[pass][4];
+        c.dstate0 = want_ds0 ? wf[pass][5] : nullptr;
+        if (pass) {
+            c.q = base.k;           // pass 2 ran with k as its query
+            c.dstate_T = nullptr;   // the final state is pass 1's
+        }
+        const void *ps = pass && !W ? at_off(sv, m.p2) : at_off(sv, m.p1);
+        const size_t ps_bytes = pass && !W ? m.g2 - m.p2 : m.p2 - m.p1;
+        if ((rc = ck_backward(c, chunk, ps, ps_bytes, at_off(ws, k.pass), k.pass_bytes, st))) return rc;
+    }
+    ma.dq1 = wf[0][0]; ma.dk1 = wf[0][1]; ma.dv1 = wf[0][2]; ma.dg1 = wf[0][3]; ma.dbeta1 = wf[0][4];
+    ma.dq2 = wf[1][0]; ma.dk2 = wf[1][1]; ma.dv2 = wf[1][2]; ma.dg2 = wf[1][3]; ma.dbeta2 = wf[1][4];
+    ma.dq = base.dq; ma.dk = base.dk; ma.dv = base.dv; ma.dg = base.dg; ma.dbeta = base.dbeta;
+    {
+        Timed tm("mask_bwd_combine", st);
+        launch_mask_bwd_combine(ma, tokens, st);
+        if (want_ds0) launch_add2(base.dstate0, wf[0][5], wf[1][5], ck_state_bytes(base.B, base.Hv) / 4, st);
+    }
+    return check_launch(st, "gdn_bwd(mask combine)");
+}
+
 // Fixed device scratch of gdn_fwd_noalloc: a file-scope device array, one copy per GPU, held until the process
 // ends.  Host code never passes the array's name to a kernel (that is a host-side stand-in); it uses the address
 // hipGetSymbolAddress returns for the current device.
@@ -527,6 +727,10 @@ int gdn_fwd_noalloc(const void *q, const void *k, const void *v, const float *g,
     int rc = check_shape(B, T, Hk, Hv, Dk, Dv, kChunkC, gate_kind, form);
     if (rc) return rc;
     if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
+    // masked calls keep the recurrent form here: the chunked form's masked passes need buffers that grow with T
+    if (mask && form == GDN_FORM_CHUNK)
+        return fail(GDN_ERR_UNSUPPORTED, "gdn_fwd_noalloc runs masked calls in the recurrent form only");
+    if (mask) form = GDN_FORM_RECURRENT;
     const int f = resolve_form(Dk, Dv, mask != nullptr, gate_kind, form);
     if (f < 0) return f;
     void *ws = nullptr;
@@ -572,6 +776,11 @@ int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const f
         cc.y = y; cc.state_T = state_T;
         cc.B = B; cc.T = T; cc.Ts = T; cc.Hk = Hk; cc.Hv = Hv; cc.in_dt = in_dtype; cc.out_dt = out_dtype;
         cc.gate = gate_kind;
+        if (mask) {
+            if (Hv > mask_max_heads())
+                return fail(GDN_ERR_UNSUPPORTED, "masked calls of the chunked form take Hv <= %d", mask_max_heads());
+            return ck_masked_forward(cc, mask, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
+        }
         return ck_forward(cc, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
     }
     const size_t need = rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
@@ -621,6 +830,7 @@ size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int
     if (f == GDN_FORM_CHUNK) {
         if (B == 0 || T == 0) return 0;
         const int W = ck_window(chunk);
+        if (has_mask) return mask_work({B, T, Hk, Hv, in_dtype == DT_BF16}, chunk).total;
         if (W) return ck_bwd_target_bytes({B, T, Hk, Hv, in_dtype == DT_BF16}, W);
         return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true).work;
     }
@@ -660,6 +870,11 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
         cc.dstate0 = dstate0;
         cc.B = B; cc.T = T; cc.Ts = T; cc.Hk = Hk; cc.Hv = Hv; cc.in_dt = in_dtype; cc.dy_dt = dy_dtype;
         cc.grad_dt = grad_dtype; cc.gate = gate_kind;
+        if (mask) {
+            if (Hv > mask_max_heads())
+                return fail(GDN_ERR_UNSUPPORTED, "masked calls of the chunked form take Hv <= %d", mask_max_heads());
+            return ck_masked_backward(cc, mask, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
+        }
         return ck_backward(cc, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
     }
     const size_t need_saved = rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);

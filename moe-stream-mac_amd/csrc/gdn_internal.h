@@ -71,6 +71,29 @@ struct ChunkCall {
 // and writes dq and dk).  With recompute, "fwd" runs every window of the launch at once.
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st);
 
+// Masked steps on the chunked form (gdn_mask.hip): tensors of B*T tokens, contiguous; q, k [tok][Hk][Dk], v, y, dy
+// [tok][Hv][Dv], g, beta [tok][Hv] (the raw gates), mask [tok]; Z, Yp, dy1, dz and the passes' parts fp32.
+struct MaskArgs {
+    const void *q, *k, *v, *dy;
+    const float *g, *beta;
+    const uint8_t *mask;
+    void *y;          // forward: holds y' on entry, y on exit
+    const float *Z;   // second pass output S' k
+    float *Yp;        // the first pass's fp32 output y' (read at masked tokens by the backward), or NULL
+    float *dy1, *dz;  // cotangents of the two passes
+    const float *dq1, *dk1, *dv1, *dg1, *dbeta1, *dq2, *dk2, *dv2, *dg2, *dbeta2;
+    void *dq, *dk, *dv;
+    float *dg, *dbeta;
+    int Hk, Hv, Dk, Dv, in_dt, out_dt, dy_dt, grad_dt, gate;
+};
+int mask_max_heads();
+void launch_mask_gates(const float *g, const float *beta, const uint8_t *mask, float *g2, float *beta2,
+                       size_t tokens, int Hv, int gate, hipStream_t st);
+void launch_mask_fix_fwd(const MaskArgs &a, size_t tokens, hipStream_t st);
+void launch_mask_bwd_cot(const MaskArgs &a, size_t tokens, hipStream_t st);
+void launch_mask_bwd_combine(const MaskArgs &a, size_t tokens, hipStream_t st);
+void launch_add2(float *dst, const float *x, const float *y, size_t n, hipStream_t st);
+
 int pick_lane_width(int Dk);
 int rec_num_row_blocks(int Dv);
 int rec_max_sub(int T, int chunk);

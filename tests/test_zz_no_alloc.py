@@ -33,7 +33,7 @@ def _inputs(B, T, Hk, Hv, D, dtype, dev, seed):
                 S0=n(B, Hv, D, D) * 0.02)
 
 
-def _run(x, dev, noalloc, mask=None):
+def _run(x, dev, noalloc, mask=None, form=None):
     import gdn_lib as L
     lib = L.load()
     B, T, Hk, D = x["q"].shape
@@ -43,15 +43,16 @@ def _run(x, dev, noalloc, mask=None):
     S = torch.full((B, Hv, D, D), float("nan"), device=dev)
     ptrs = [x[n].data_ptr() for n in ("q", "k", "v", "g", "beta", "S0")]
     m = None if mask is None else mask.data_ptr()
+    form = L.FORM_AUTO if form is None else form
     if noalloc:
         rc = lib.gdn_fwd_noalloc(*ptrs, m, y.data_ptr(), S.data_ptr(), B, T, Hk, Hv, D, D, code, code, L.GATE_LOG,
-                                 L.FORM_AUTO, None)
+                                 form, None)
     else:
-        n_ws = lib.gdn_fwd_workspace_bytes(B, T, Hk, Hv, D, D, 64, L.GATE_LOG, int(mask is not None), L.FORM_AUTO,
+        n_ws = lib.gdn_fwd_workspace_bytes(B, T, Hk, Hv, D, D, 64, L.GATE_LOG, int(mask is not None), form,
                                            code, 0)
         ws = torch.empty(max(n_ws, 1), device=dev, dtype=torch.uint8)
         rc = lib.gdn_fwd(*ptrs, m, y.data_ptr(), S.data_ptr(), None, 0, ws.data_ptr(), n_ws, B, T, Hk, Hv, D, D, 64,
-                         code, code, L.GATE_LOG, L.FORM_AUTO, None)
+                         code, code, L.GATE_LOG, form, None)
     L.check(rc)
     torch.cuda.synchronize()
     return y, S
@@ -70,18 +71,22 @@ def test_noalloc_forward_matches_gdn_fwd_twice(dev, dtype):
 
 
 def test_noalloc_recurrent_form_and_limits(dev):
-    """A masked call runs the recurrent form (no scratch); a call whose one-chunk group exceeds the fixed scratch is
-    refused with a clear error before anything runs."""
+    """A masked call runs the recurrent form (no scratch), equal to gdn_fwd's recurrent form; a masked call that asks
+    for the chunked form, or whose one-chunk group exceeds the fixed scratch, is refused with a clear error before
+    anything runs."""
     import gdn_lib as L
     x = _inputs(2, 70, 2, 4, 128, torch.float32, dev, 3)
     mask = torch.ones(2, 70, dtype=torch.uint8, device=dev)
     mask[:, 50:] = 0
     for _ in range(2):
-        y0, S0 = _run(x, dev, noalloc=False, mask=mask)
+        y0, S0 = _run(x, dev, noalloc=False, mask=mask, form=L.FORM_RECURRENT)
         y1, S1 = _run(x, dev, noalloc=True, mask=mask)
         assert torch.equal(y0, y1) and torch.equal(S0, S1)
     lib = L.load()
     fake = 256
+    rc = lib.gdn_fwd_noalloc(*([fake] * 6), fake, fake, fake, 2, 70, 2, 4, 128, 128, L.F32, L.F32, L.GATE_LOG,
+                             L.FORM_CHUNK, None)
+    assert rc == L.GDN_ERR_UNSUPPORTED and b"recurrent form only" in lib.gdn_last_error()
     rc = lib.gdn_fwd_noalloc(*([fake] * 6), None, fake, fake, 16, 64, 16, 64, 128, 128, L.BF16, L.BF16, L.GATE_LOG,
                              L.FORM_CHUNK, None)
     assert rc == L.GDN_ERR_UNSUPPORTED and b"fixed scratch" in lib.gdn_last_error()
