@@ -217,13 +217,13 @@ __device__ __forceinline__ float gate_log(float g, int gate) {
 struct Bufs {
     float *H;    // [B][Hv][NC][D][D] chunk-entry states h = S^T, element (j, i) at [j][i] (bf16 bits in the bf16 path)
     double *G;   // [B][Hv][NC][C]
-    float *T;    // [B][Hv][NC][C][C] (bf16 path: bf16 hi and lo planes [2][C][C] in the same space)
+    float *T;    // [B][Hv][NC][C][C] (bf16 path: T^T as bf16 hi and lo planes [2][C][C] in fragment order, same space)
     float *P;    // [B][Hv][NC][C][C]
     float *W;    // [B][Hv][NC][C][D]
     float *U;    // [B][Hv][NC][C][D]
     float *Dl;   // [B][Hv][NC][C][D]  Delta
     float *dH;   // [B][Hv][NC][D][D]  adjoint of each chunk's exit state, [j][i] like H (bf16 in the bf16 path)
-    float *dDl;  // [B][Hv][NC][C][D]  dDelta (bf16 path: dDelta^T as bf16 hi and lo planes [2][D][C], same space)
+    float *dDl;  // [B][Hv][NC][C][D]  dDelta (bf16 path: TdD = T^T dDelta, fp32)
     float *part; // [B][T][Hv][2][D]   ck_bwd_local scratch: the running dq | dk sum of a key head (bf16 set: in the
                  // rows [B][T][Hk][2][D]; fp32 set: in the slot of the key head's first value head, the other slots
                  // parking each value head's dW)
@@ -1401,41 +1401,36 @@ __device__ __forceinline__ void acc_N(const f4 &x, bfr *hi, bfr *lo, int ld, int
 
 // ---------------------------------------------------------------------------------------------- ck_bwd_local (bf16)
 //
-// The same products as ck_bwd_local_kernel, on bf16 operand tiles.  One workgroup of 8 waves per (chunk, key head)
-// takes the key head's value heads in turn; for each, wave w owns the 16-row strip r0 = 16 (w % 4) and column half
-// w / 4 of every [64][*] product.  Phases and their
-// tiles (byte offsets into one LDS arena; lifetimes checked against the barriers between phases):
-//   S1  P1 dQ = gamma dY h^T, P2 dW = -dDelta h^T, P3 dK = rc Delta dh'^T (Delta split),   h, dh', dDelta,
-//       P4 dp = dY Delta^T (Delta split)                                                 Delta hi/lo, dY
-//   S3  P5 dQ += dPG K, P6 dK += dPG^T Q (dPG split)                                 dPG, dPG^T, K^T, Q^T
-//   S4a P7 tdw = T^T dW, P8 tdd = T^T dDelta (split x split); dv                      T^T, dW^T, dDelta^T, V
-//   S4b P9 t1 = dDelta V^T, P10 t2 = dW K^T                                           dDelta, V, dW, K
-//   S5  P11 y1 = dT T^T, P12 da = T^T Y1, P13 K K^T                                   dT, T, Y1^T, T^T, K
-//   S6  P14 dK += (M + M^T) K                                                          M + M^T, K^T
+// One workgroup of 8 waves per (chunk, key head) takes the key head's value heads in turn; for each, wave w owns
+// the 16-row strip r0 = 16 (w % 4) and column half w / 4 of every [64][*] product.  T and dDelta enter only through
+// TdD = T^T dDelta, which ck_bwd_seq_bf16 saves: with Delta = T Z, Z = diag(beta) V - diag(beta gamma) K h,
+//   dv = diag(beta) TdD,   dK -= diag(beta gamma) Y2 (Y2 = TdD h^T),   dA = -strict_lower(TdD Delta^T),
+//   dbeta += rowsum(V * TdD) - gamma s4,   dG -= beta gamma s4   (s4 = rowsum(K * Y2)).
+// Phases and their tiles (byte offsets into one LDS arena; lifetimes checked against the barriers between phases):
+//   S1  dQ = gamma dY h^T, Y2 = TdD h^T, dK = rc Delta dh'^T, dp = dY Delta^T, dA = TdD Delta^T in one pass over
+//       the value index (Delta split; TdD as bf16, dv and rowsum(V * TdD) from its fp32 loads)
+//                                                                  TdD, h, dh', Delta hi / lo, dY
+//   S3  dQ += dPG K, dK += dPG^T Q (dPG split), K K^T               dPG, dPG^T, Q^T, K^T, K
+//   S6  dK += (M + M^T) K, M = diag(beta) dA * Gam                  M + M^T, K^T
 // then the straddle sums for dg and the outputs, as in ck_bwd_local_kernel.
 constexpr int SZ_A = C * LA * 2;       // [64][136]  17408 B
 constexpr int SZ_B = D * LA * 2;       // [128][136] 34816 B
 constexpr int SZ_C = D * LB * 2;       // [128][72]  18432 B
 constexpr int SZ_D = C * LB * 2;       // [64][72]    9216 B
-// S1: dDelta (stays until S4b), dh', h, Delta hi/lo, dY
-constexpr int O_DD = 0;
-constexpr int O_DHH = O_DD + SZ_A, O_H = O_DHH + SZ_B, O_DLH = O_H + SZ_B, O_DLL = O_DLH + SZ_A;
+constexpr int LQ = 64 + 4;             // row stride of a wave's fp32 dq staging block
+// S1: TdD, dh', h, Delta hi / lo, dY
+constexpr int O_TD = 0;
+constexpr int O_DHH = O_TD + SZ_A, O_H = O_DHH + SZ_B, O_DLH = O_H + SZ_B, O_DLL = O_DLH + SZ_A;
 constexpr int O_DY = O_DLL + SZ_A;
-// S3: dPG, dPG^T (hi / lo), Q^T, K^T, K (dDelta stays)
-constexpr int O_PNH = O_DD + SZ_A, O_PNL = O_PNH + SZ_D, O_PTH = O_PNL + SZ_D, O_PTL = O_PTH + SZ_D;
-constexpr int O_QT = O_PTL + SZ_D, O_KT = O_QT + SZ_C, O_K = O_KT + SZ_C;
-// S4a: dDelta^T hi / lo, T^T hi / lo (in the dead dPG / Q^T space); dW^T, T, V after K
-constexpr int O_DDTH = O_DD + SZ_A, O_DDTL = O_DDTH + SZ_C, O_TTH = O_DDTL + SZ_C, O_TTL = O_TTH + SZ_D;
-constexpr int O_DWT = O_K + SZ_A, O_TN = O_DWT + SZ_C, O_V = O_TN + SZ_D;
-// S4b: dW; S5: dT, Y1^T; S6: M + M^T and the fp32 scratch of M (later the pair matrix E)
-constexpr int O_DW = O_DD + SZ_A, O_DT = O_DW + SZ_A, O_Y1T = O_DT + SZ_D;
-constexpr int O_MM = 0, O_SM = O_V;
-constexpr int ARENA = O_SM + C * LDC * 4;
-static_assert(O_DY + SZ_A <= ARENA, "S1 tiles fit");
-static_assert(O_TTL + SZ_D <= O_KT, "S4a tiles stay clear of K^T");
-static_assert(O_V + SZ_A <= ARENA, "arena");
-static_assert(O_Y1T + SZ_D <= O_TTH, "S5 tiles stay clear of T^T");
-static_assert(ARENA <= 157 * 1024, "arena size");
+// S3: dPG, dPG^T (hi / lo), Q^T, K^T, K, then the waves' dq staging blocks
+constexpr int O_PNH = 0, O_PNL = O_PNH + SZ_D, O_PTH = O_PNL + SZ_D, O_PTL = O_PTH + SZ_D;
+constexpr int O_QT = O_PTL + SZ_D, O_KT = O_QT + SZ_C, O_K = O_KT + SZ_C, O_STQ = O_K + SZ_A;
+// S6: M + M^T (bf16) over the dead dPG tiles; the fp32 M, later the pair matrix E, over the dq staging
+constexpr int O_MM = 0, O_SM = O_STQ;
+constexpr int ARENA = O_DY + SZ_A;
+static_assert(O_STQ + 8 * 16 * LQ * 4 <= ARENA, "dq staging fits");
+static_assert(O_SM + C * LDC * 4 <= ARENA && O_MM + SZ_D <= O_QT, "S6 tiles fit, clear of K^T");
+static_assert(C * (D + 4) * 4 <= O_KT, "dk staging below K^T and the pair matrix");
 
 constexpr int NQR = 2;  // dq row pieces per thread whose running sum stays in registers (of four)
 
@@ -1447,7 +1442,7 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
                                                     float4 (&ck)[4], float4 (&cq)[NQR]) {
     __shared__ __align__(16) unsigned char arena[ARENA];
     __shared__ double sG[C];
-    __shared__ float sGam[C], sRc[C], sB[C], sScan[2][C];
+    __shared__ float sGam[C], sRc[C], sB[C], sVT[C], sScan[2][C];
     __shared__ float sRow[3][2][C];
     __shared__ float sLast[8];
     auto T16 = [&](int off) { return reinterpret_cast<bfr *>(arena + off); };
@@ -1465,35 +1460,28 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     const int w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int r0 = 16 * (w & 3), ch = w >> 2;
     const size_t ci = chunk_index(a, b, hv, c);
-    const bfr *Hc = reinterpret_cast<const bfr *>(a.w.H) + ci * D * D;  // h = S^T, [j][i], bf16
+    const bfr *Hc = reinterpret_cast<const bfr *>(a.w.H) + ci * D * D;    // h = S^T, [j][i], bf16
     const bfr *dHc = reinterpret_cast<const bfr *>(a.w.dH) + ci * D * D;  // dh', [j][i], bf16
-    const float *Dc = a.w.Dl + ci * C * D;
-    const bfr *dDc = reinterpret_cast<const bfr *>(a.w.dDl) + ci * 2 * D * C;  // dDelta^T hi, lo planes [i][r]
-    const bfr *Tc = reinterpret_cast<const bfr *>(a.w.T) + ci * 2 * C * C;      // T hi, lo planes [r][s]
+    const float *Dc = a.w.Dl + ci * C * D;                                // Delta [r][i]
+    const float *TDc = a.w.dDl + ci * C * D;                              // TdD [r][i]
     const size_t qk0 = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
     const size_t v0 = (((size_t)b * a.Ts + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
     const bfr *qsrc = static_cast<const bfr *>(a.q) + qk0, *ksrc = static_cast<const bfr *>(a.k) + qk0;
     const bfr *vsrc = static_cast<const bfr *>(a.v) + v0;
 
-    // ---- S1: gates; h, dh', Delta, dY; P1 dQ = diag(gamma) dY h^T, P3 dK = diag(rc) Delta dh'^T, P4 dp = dY Delta^T
+    // ---- S1 staging: gates; h, dh', Delta, TdD, dY, V.  Every global load of the phase is issued before the
+    // first LDS store.  dv = diag(beta) TdD leaves from the fp32 TdD loads, and rowsum(V * TdD) goes to sVT.
     if (tid < C) {
         sG[tid] = a.w.G[ci * C + tid];
         sB[tid] = tid < n ? a.beta[((size_t)b * a.Ts + t0 + tid) * a.Hv + hv] : 0.f;
     }
-    // S1 staging: every global load of the phase is issued before the first LDS store
     float lastp = 0.f;  // <dh', h>, the pair (C-1, chunk start)
-    static_assert((D / 8) * (C / 2) == NTB, "one dDelta block per thread");
-    const int drb = tid / (C / 2), dc2 = 2 * (tid - drb * (C / 2));
-    uint32_t ddr[8];  // rows i = 8 drb .. +7, columns r = dc2, dc2 + 1 of the dDelta^T hi plane
     {
-        constexpr int SPER = D * (D / 8) / NTB, NPER = C * (D / 8) / NTB;  // 8-element chunks per thread
+        constexpr int SPER = D * (D / 8) / NTB, NPER = C * (D / 8) / NTB;  // 8-element pieces per thread
         static_assert(SPER * NTB == D * (D / 8) && NPER * NTB == C * (D / 8), "even split");
         const bool yf32 = a.dy_dt == DT_F32;
-        uint4 hr[SPER], dhr[SPER], dl[2 * NPER], yr[2 * NPER];
-        // dDelta (hi) into [r][i]: every thread transposes one 8 (i) x 2 (r) block of the [i][r] plane (kept in
-        // registers for the dDelta^T hi tile of S4a)
-#pragma unroll
-        for (int rr = 0; rr < 8; ++rr) ddr[rr] = *reinterpret_cast<const uint32_t *>(dDc + (drb * 8 + rr) * C + dc2);
+        uint4 hr[SPER], dhr[SPER], dl[2 * NPER], td[2 * NPER], yr[2 * NPER], vr[NPER];
+        float bt[NPER];
 #pragma unroll
         for (int p = 0; p < SPER; ++p) {
             hr[p] = reinterpret_cast<const uint4 *>(Hc)[tid + p * NTB];
@@ -1501,32 +1489,28 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
         }
 #pragma unroll
         for (int p = 0; p < NPER; ++p) {
-            const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
-            dl[2 * p] = *reinterpret_cast<const uint4 *>(Dc + r * D + c);
-            dl[2 * p + 1] = *reinterpret_cast<const uint4 *>(Dc + r * D + c + 4);
+            const int pc = tid + p * NTB, r = pc / (D / 8), c8 = (pc - r * (D / 8)) * 8;
+            dl[2 * p] = *reinterpret_cast<const uint4 *>(Dc + r * D + c8);
+            dl[2 * p + 1] = *reinterpret_cast<const uint4 *>(Dc + r * D + c8 + 4);
+            td[2 * p] = *reinterpret_cast<const uint4 *>(TDc + r * D + c8);
+            td[2 * p + 1] = *reinterpret_cast<const uint4 *>(TDc + r * D + c8 + 4);
+            vr[p] = r < n ? *reinterpret_cast<const uint4 *>(vsrc + (size_t)r * v_row + c8) : make_uint4(0u, 0u, 0u, 0u);
+            bt[p] = r < n ? a.beta[((size_t)b * a.Ts + t0 + r) * a.Hv + hv] : 0.f;
             if (yf32) {
-                const float *ys = static_cast<const float *>(a.dy) + v0 + (size_t)r * v_row + c;
+                const float *ys = static_cast<const float *>(a.dy) + v0 + (size_t)r * v_row + c8;
                 yr[2 * p] = r < n ? *reinterpret_cast<const uint4 *>(ys) : make_uint4(0u, 0u, 0u, 0u);
                 yr[2 * p + 1] = r < n ? *reinterpret_cast<const uint4 *>(ys + 4) : make_uint4(0u, 0u, 0u, 0u);
             } else {
-                yr[p] = r < n ? *reinterpret_cast<const uint4 *>(static_cast<const bfr *>(a.dy) + v0 + (size_t)r * v_row + c)
+                yr[p] = r < n ? *reinterpret_cast<const uint4 *>(static_cast<const bfr *>(a.dy) + v0 + (size_t)r * v_row + c8)
                               : make_uint4(0u, 0u, 0u, 0u);
             }
-        }
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            uint32_t x[8];
-#pragma unroll
-            for (int rr = 0; rr < 8; ++rr) x[rr] = cc ? ddr[rr] >> 16 : ddr[rr] & 0xffffu;
-            *reinterpret_cast<uint4 *>(T16(O_DD) + (dc2 + cc) * LA + drb * 8) =
-                make_uint4(x[0] | (x[1] << 16), x[2] | (x[3] << 16), x[4] | (x[5] << 16), x[6] | (x[7] << 16));
         }
         bfr *const th = T16(O_H), *const tdh = T16(O_DHH);
 #pragma unroll
         for (int p = 0; p < SPER; ++p) {
-            const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
-            *reinterpret_cast<uint4 *>(th + r * LA + c) = hr[p];
-            *reinterpret_cast<uint4 *>(tdh + r * LA + c) = dhr[p];
+            const int pc = tid + p * NTB, r = pc / (D / 8), c8 = (pc - r * (D / 8)) * 8;
+            *reinterpret_cast<uint4 *>(th + r * LA + c8) = hr[p];
+            *reinterpret_cast<uint4 *>(tdh + r * LA + c8) = dhr[p];
             const uint32_t hw[4] = {hr[p].x, hr[p].y, hr[p].z, hr[p].w}, dw[4] = {dhr[p].x, dhr[p].y, dhr[p].z, dhr[p].w};
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -1535,21 +1519,50 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
         auto f = [](uint32_t x) { return __uint_as_float(x); };
 #pragma unroll
         for (int p = 0; p < NPER; ++p) {
-            const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
-            uint4 h, l;
+            const int pc = tid + p * NTB, r = pc / (D / 8), c8 = (pc - r * (D / 8)) * 8;
+            uint4 h, lo;
             const uint4 a0 = dl[2 * p], a1 = dl[2 * p + 1];
-            pk2(f(a0.x), f(a0.y), h.x, l.x);
-            pk2(f(a0.z), f(a0.w), h.y, l.y);
-            pk2(f(a1.x), f(a1.y), h.z, l.z);
-            pk2(f(a1.z), f(a1.w), h.w, l.w);
-            *reinterpret_cast<uint4 *>(T16(O_DLH) + r * LA + c) = h;
-            *reinterpret_cast<uint4 *>(T16(O_DLL) + r * LA + c) = l;
+            pk2(f(a0.x), f(a0.y), h.x, lo.x);
+            pk2(f(a0.z), f(a0.w), h.y, lo.y);
+            pk2(f(a1.x), f(a1.y), h.z, lo.z);
+            pk2(f(a1.z), f(a1.w), h.w, lo.w);
+            *reinterpret_cast<uint4 *>(T16(O_DLH) + r * LA + c8) = h;
+            *reinterpret_cast<uint4 *>(T16(O_DLL) + r * LA + c8) = lo;
+            const uint4 t0v = td[2 * p], t1v = td[2 * p + 1];
+            const float tv[8] = {f(t0v.x), f(t0v.y), f(t0v.z), f(t0v.w), f(t1v.x), f(t1v.y), f(t1v.z), f(t1v.w)};
+            *reinterpret_cast<uint4 *>(T16(O_TD) + r * LA + c8) =
+                make_uint4(pk(tv[0], tv[1]), pk(tv[2], tv[3]), pk(tv[4], tv[5]), pk(tv[6], tv[7]));
             uint4 yv = yr[p];
             if (yf32) {
                 const uint4 y0 = yr[2 * p], y1 = yr[2 * p + 1];
                 yv = make_uint4(pk(f(y0.x), f(y0.y)), pk(f(y0.z), f(y0.w)), pk(f(y1.x), f(y1.y)), pk(f(y1.z), f(y1.w)));
             }
-            *reinterpret_cast<uint4 *>(T16(O_DY) + r * LA + c) = yv;
+            *reinterpret_cast<uint4 *>(T16(O_DY) + r * LA + c8) = yv;
+            // rowsum(V * TdD): the 16 lanes of a DPP row hold one token's row
+            const uint32_t vw[4] = {vr[p].x, vr[p].y, vr[p].z, vr[p].w};
+            float vt = 0.f, dvv[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                vt += bf2f(vw[q] & 0xffffu) * tv[2 * q] + bf2f(vw[q] >> 16) * tv[2 * q + 1];
+                dvv[2 * q] = bt[p] * tv[2 * q];
+                dvv[2 * q + 1] = bt[p] * tv[2 * q + 1];
+            }
+            vt = row16_allreduce(vt);
+            if ((tid & 15) == 0) sVT[r] = vt;
+            if (r < n) {
+                const size_t o = v0 + (size_t)r * v_row + c8;
+                if (a.grad_dt == DT_BF16) {
+                    *reinterpret_cast<uint4 *>(static_cast<bfr *>(a.dv) + o) =
+                        make_uint4(pk(dvv[0], dvv[1]), pk(dvv[2], dvv[3]), pk(dvv[4], dvv[5]), pk(dvv[6], dvv[7]));
+                } else if (a.grad_dt == DT_F32) {
+                    float *dvp = static_cast<float *>(a.dv) + o;
+                    *reinterpret_cast<float4 *>(dvp) = make_float4(dvv[0], dvv[1], dvv[2], dvv[3]);
+                    *reinterpret_cast<float4 *>(dvp + 4) = make_float4(dvv[4], dvv[5], dvv[6], dvv[7]);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) store_from_f32(a.dv, o + q, dvv[q], a.grad_dt);
+                }
+            }
         }
     }
     // the waves' parts of <dh', h> go to LDS now (the raw h / dh' loads are not kept live until the straddle sums)
@@ -1568,24 +1581,26 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     Blk84 bk;
     bk.load(isk ? ksrc : qsrc, qk_row, isk ? tid - NBQ : tid, D, n);
     float bnd[4] = {0.f, 0.f, 0.f, 0.f}, rowB[4] = {0.f, 0.f, 0.f, 0.f}, tl[4] = {0.f, 0.f, 0.f, 0.f};
-    f4 dQ[4], dK[4], dWr[4], dPG[2], Ep[2];
+    f4 dQ[4], dK[4], Y2[4], dPG[2], Ep[2], dA[2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) dQ[t] = dK[t] = dWr[t] = zero4();
+    for (int t = 0; t < 4; ++t) dQ[t] = dK[t] = Y2[t] = zero4();
     {
         f4 dp[2] = {zero4(), zero4()};
-        // P1, P2, P3, P4 in one pass over k: each fragment read from LDS once per k-step (P1 and P2 share the h
-        // fragments, P1 and P4 the dY fragment)
-        const bfr *const tY = T16(O_DY), *const tD = T16(O_DD), *const tH = T16(O_H), *const tDH = T16(O_DHH);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) dA[t] = zero4();
+        // one pass over the value index: each fragment read from LDS once per k-step (dQ and Y2 share the h
+        // fragments, dp and dA the Delta fragments)
+        const bfr *const tY = T16(O_DY), *const tT = T16(O_TD), *const tH = T16(O_H), *const tDH = T16(O_DHH);
         const bfr *const tLh = T16(O_DLH), *const tLl = T16(O_DLL);
 #pragma unroll 2
         for (int k0 = 0; k0 < D; k0 += 32) {
-            const bf8 ay = frag(tY, LA, r0, k0, l), ad = frag(tD, LA, r0, k0, l);
+            const bf8 ay = frag(tY, LA, r0, k0, l), at = frag(tT, LA, r0, k0, l);
             const bf8 ah = frag(tLh, LA, r0, k0, l), al = frag(tLl, LA, r0, k0, l);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const bf8 hb = frag(tH, LA, 64 * ch + 16 * t, k0, l);
                 dQ[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ay, hb, dQ[t], 0, 0, 0);
-                dWr[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ad, hb, dWr[t], 0, 0, 0);
+                Y2[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(at, hb, Y2[t], 0, 0, 0);
                 const bf8 db = frag(tDH, LA, 64 * ch + 16 * t, k0, l);
                 dK[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, db, dK[t], 0, 0, 0);
                 dK[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, db, dK[t], 0, 0, 0);
@@ -1595,9 +1610,11 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
                 const bf8 xh = frag(tLh, LA, 32 * ch + 16 * t, k0, l), xl = frag(tLl, LA, 32 * ch + 16 * t, k0, l);
                 dp[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ay, xh, dp[t], 0, 0, 0);
                 dp[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ay, xl, dp[t], 0, 0, 0);
+                dA[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(at, xh, dA[t], 0, 0, 0);
+                dA[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(at, xl, dA[t], 0, 0, 0);
             }
         }
-        __syncthreads();  // sGam / sRc ready; the S1 tiles read (dDelta stays)
+        __syncthreads();  // sGam / sRc ready; the S1 tiles read
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -1611,13 +1628,11 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
             for (int e = 0; e < 4; ++e) {
                 const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
                 const float pv = s2 <= r ? dp[t][e] : 0.f;
-                Ep[t][e] = s2 < r ? pv : 0.f;  // times P in S5
+                Ep[t][e] = s2 < r ? pv : 0.f;  // times P below
                 dPG[t][e] = s2 <= r ? pv * __builtin_amdgcn_exp2f((float)(sG[r] - sG[s2]) * 1.4426950408889634f) : 0.f;
             }
     }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) dWr[t] = -dWr[t];
-    // ---- S3: P5 dQ += dPG K, P6 dK += dPG^T Q
+    // ---- S3: dQ += dPG K, dK += dPG^T Q, K K^T
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         acc_N<true>(dPG[t], T16(O_PNH), T16(O_PNL), LB, r0, 32 * ch + 16 * t, l);
@@ -1629,13 +1644,11 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     } else {
         bk.store_T(T16(O_QT), LB);
     }
-    // dQ leaves through a wave-private staging block (the wave's 16 x 64 fp32 part of dQ, row stride LQ) in the
-    // space of the S4a tiles, which is free until the barrier after the S3 products: each lane then moves four
-    // 16-byte row pieces (piece p: row (l + 64p) / 16, columns 4 ((l + 64p) % 16) .. +3) instead of 16 scattered
-    // 4-byte elements.  The running dq sum of the previous value heads at those pieces is in flight during P5 / P6.
-    constexpr int LQ = 64 + 4;
-    static_assert(O_DWT + 8 * 16 * LQ * 4 <= ARENA, "dq staging fits the S4a space");
-    float *const stq = reinterpret_cast<float *>(arena + O_DWT) + w * 16 * LQ;
+    // dQ leaves through a wave-private staging block (the wave's 16 x 64 fp32 part of dQ, row stride LQ): each lane
+    // then moves four 16-byte row pieces (piece p: row (l + 64p) / 16, columns 4 ((l + 64p) % 16) .. +3) instead of
+    // 16 scattered 4-byte elements.  The running dq sum of the previous value heads at those pieces, and P at this
+    // lane's pair positions, are in flight during the S3 products.
+    float *const stq = reinterpret_cast<float *>(arena + O_STQ) + w * 16 * LQ;
     float4 prevq[4];
     if (!first) {
 #pragma unroll
@@ -1645,31 +1658,32 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
                              : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
-    __syncthreads();
-    // S4a's T and V, in flight during the S3 products.  T: thread tid takes plane tid / 256 (hi, lo) and the 8-row x
-    // 2-column block tid % 256 of it (four-byte row pieces), so every wave stages an equal share
-    constexpr int NDP = D * C / 8 / NTB;  // 16-byte dDelta^T pieces per plane and thread
-    static_assert((C / 8) * (C / 2) * 2 == NTB && NDP * NTB * 8 == D * C && C * (D / 8) == 2 * NTB, "block split");
-    const int tpl = tid >> 8, tblk = tid & 255, trb = tblk / (C / 2), tc2 = 2 * (tblk - trb * (C / 2));
-    uint32_t tr[8];
+    // P at (r = r0 + 4 lg + e, s = 32 ch + 16 t + li), read from the P^T tile (fragment order), where the four rows
+    // of one column are 8 contiguous bytes per plane
+    uint2 pP[2][2];  // [t][hi, lo]
 #pragma unroll
-    for (int rr = 0; rr < 8; ++rr)
-        tr[rr] = *reinterpret_cast<const uint32_t *>(Tc + (size_t)tpl * C * C + (trb * 8 + rr) * C + tc2);
-    uint4 vr[2];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int pc = tid + p * NTB, r = pc / (D / 8), c8 = (pc - r * (D / 8)) * 8;
-        vr[p] = r < n ? *reinterpret_cast<const uint4 *>(vsrc + (size_t)r * v_row + c8) : make_uint4(0u, 0u, 0u, 0u);
+    for (int t = 0; t < 2; ++t) {
+        const size_t pi = ci * 2 * C * C + frag_off<C>(32 * ch + 16 * t + li, r0 + 4 * lg);
+        pP[t][0] = *reinterpret_cast<const uint2 *>(a.w.PTb + pi);
+        pP[t][1] = *reinterpret_cast<const uint2 *>(a.w.PTb + pi + C * C);
     }
+    __syncthreads();
     {
+        // the boundary terms q . dQ and k . dK (before the S3 products), and Z's terms through Y2 = TdD h^T:
+        // s4 = k . Y2 (dbeta -= gamma s4, dG -= beta gamma s4), dK -= beta gamma Y2
         const bfr *Qt = T16(O_QT), *Kt = T16(O_KT);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+                const float kv = bf2f(Kt[j * LB + r]), bg = sB[r] * sGam[r];
                 bnd[e] += bf2f(Qt[j * LB + r]) * dQ[t][e];
-                tl[e] += bf2f(Kt[j * LB + r]) * dK[t][e];
+                tl[e] += kv * dK[t][e];
+                const float s4 = kv * Y2[t][e];
+                rowB[e] -= sGam[r] * s4;
+                bnd[e] -= bg * s4;
+                dK[t][e] -= bg * Y2[t][e];
             }
     }
     mmab<C, 4, true>(dQ, T16(O_PNH), T16(O_PNL), LB, r0, T16(O_KT), nullptr, LB, 64 * ch, l);
@@ -1682,8 +1696,8 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
         for (int e = 0; e < 4; ++e) stq[(4 * lg + e) * LQ + 16 * t + li] = dQ[t][e];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-        const int i = l + 64 * p, rr = i >> 4, r = r0 + rr, c4 = 64 * ch + 4 * (i & 15);
-        float4 v = *reinterpret_cast<const float4 *>(stq + rr * LQ + 4 * (i & 15));
+        const int i = l + 64 * p, rr2 = i >> 4, r = r0 + rr2, c4 = 64 * ch + 4 * (i & 15);
+        float4 v = *reinterpret_cast<const float4 *>(stq + rr2 * LQ + 4 * (i & 15));
         if (r >= n) continue;
         if (!first) {
             const float4 s = p < NQR ? cq[p < NQR ? p : 0] : prevq[p];
@@ -1704,153 +1718,27 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
             store_from_f32(a.dq, o + 3, v.w, a.grad_dt);
         }
     }
-    __syncthreads();  // dPG and Q^T read (K^T, K, dDelta stay); the dq staging read
-    // ---- S4a: P7 tdw = T^T dW, P8 tdd = T^T dDelta; dv
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc_T<false>(dWr[t], T16(O_DWT), nullptr, LB, r0, 64 * ch + 16 * t, l);
-    {
-        // dDelta^T lo: a straight copy of the [i][r] plane; hi: this thread's S1 block, still in registers
-        uint4 ddlo[NDP];
-#pragma unroll
-        for (int p = 0; p < NDP; ++p) ddlo[p] = reinterpret_cast<const uint4 *>(dDc + D * C)[tid + p * NTB];
-#pragma unroll
-        for (int rr = 0; rr < 8; ++rr) *reinterpret_cast<uint32_t *>(T16(O_DDTH) + (drb * 8 + rr) * LB + dc2) = ddr[rr];
-#pragma unroll
-        for (int p = 0; p < NDP; ++p) {
-            const int pc = tid + p * NTB, i = pc / (C / 8), r8 = (pc - i * (C / 8)) * 8;
-            *reinterpret_cast<uint4 *>(T16(O_DDTL) + i * LB + r8) = ddlo[p];
-        }
-        // T^T (this thread's plane): two columns of eight consecutive rows; T [r][s] (hi plane only): eight row pieces
-        bfr *const tdst = T16(tpl ? O_TTL : O_TTH);
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            uint32_t x[8];
-#pragma unroll
-            for (int rr = 0; rr < 8; ++rr) x[rr] = cc ? tr[rr] >> 16 : tr[rr] & 0xffffu;
-            *reinterpret_cast<uint4 *>(tdst + (tc2 + cc) * LB + trb * 8) =
-                make_uint4(x[0] | (x[1] << 16), x[2] | (x[3] << 16), x[4] | (x[5] << 16), x[6] | (x[7] << 16));
-        }
-        if (tpl == 0) {
-#pragma unroll
-            for (int rr = 0; rr < 8; ++rr) *reinterpret_cast<uint32_t *>(T16(O_TN) + (trb * 8 + rr) * LB + tc2) = tr[rr];
-        }
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int ch = tid + p * NTB, r = ch / (D / 8), c = (ch - r * (D / 8)) * 8;
-            *reinterpret_cast<uint4 *>(T16(O_V) + r * LA + c) = vr[p];
-        }
-    }
-    __syncthreads();
-    uint32_t dvb[4][4];  // dv as bf16 bits at this lane's accumulator positions
-    {
-        f4 tdw[4], tdd[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) tdw[t] = tdd[t] = zero4();
-        mmab<C, 4>(tdw, T16(O_TTH), nullptr, LB, r0, T16(O_DWT), nullptr, LB, 64 * ch, l);
-        mmab<C, 4, true, true>(tdd, T16(O_TTH), T16(O_TTL), LB, r0, T16(O_DDTH), T16(O_DDTL), LB, 64 * ch, l);
-        const bfr *Kt = T16(O_KT), *Vn = T16(O_V);
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
-                const float bg = sB[r] * sGam[r];
-                dK[t][e] += bg * tdw[t][e];
-                const float s4 = tdw[t][e] * bf2f(Kt[j * LB + r]);
-                rowB[e] += sGam[r] * s4;
-                bnd[e] += bg * s4;
-                rowB[e] += bf2f(Vn[r * LA + j]) * tdd[t][e];
-                dvb[t][e] = bfbits(tdd[t][e] * sB[r]);  // dv
-            }
-        if (a.grad_dt != DT_BF16) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = r0 + 4 * lg + e;
-                    if (r < n)
-                        store_from_f32(a.dv, v0 + (size_t)r * v_row + 64 * ch + 16 * t + li, tdd[t][e] * sB[r], a.grad_dt);
-                }
-        }
-    }
-    __syncthreads();  // dDelta^T, dW^T read (T^T hi, T, V, K, K^T, dDelta stay)
-    if (a.grad_dt == DT_BF16) {
-        // bf16 dv leaves through a wave-private staging block (16 x 64, row stride LV) in the dead dDelta^T lo space
-        // (rewritten only after the next barrier): two 16-byte row pieces per lane (piece p: row (l + 64p) / 8,
-        // columns 8 ((l + 64p) % 8) .. +7)
-        constexpr int LV = 64 + 8;
-        static_assert(8 * 16 * LV * 2 <= SZ_C && O_DDTL + SZ_C <= O_TTH, "dv staging fits the dDelta^T lo space");
-        bfr *const stv = T16(O_DDTL) + w * 16 * LV;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) stv[(4 * lg + e) * LV + 16 * t + li] = (bfr)dvb[t][e];
-        bfr *const dvp = static_cast<bfr *>(a.dv) + v0;
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int i = l + 64 * p, rr = i >> 3, c8 = 8 * (i & 7), r = r0 + rr;
-            const uint4 x = *reinterpret_cast<const uint4 *>(stv + rr * LV + c8);
-            if (r < n) *reinterpret_cast<uint4 *>(dvp + (size_t)r * v_row + 64 * ch + c8) = x;
-        }
-    }
-    // P at this lane's pair positions (r = r0 + 4 lg + e, s = 32 ch + 16 t + li), read from the P^T tile (fragment
-    // order), where the four rows of one column are 8 contiguous bytes per plane; in flight during S4b and S5
-    uint2 pP[2][2];  // [t][hi, lo]
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const size_t pi = ci * 2 * C * C + frag_off<C>(32 * ch + 16 * t + li, r0 + 4 * lg);
-        pP[t][0] = *reinterpret_cast<const uint2 *>(a.w.PTb + pi);
-        pP[t][1] = *reinterpret_cast<const uint2 *>(a.w.PTb + pi + C * C);
-    }
-    // ---- S4b: P9 t1 = dDelta V^T, P10 t2 = dW K^T; dT = (t1 + t2 diag(gamma)) diag(beta)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc_N<false>(dWr[t], T16(O_DW), nullptr, LA, r0, 64 * ch + 16 * t, l);
-    __syncthreads();
-    f4 dT[2];
-    {
-        f4 t1[2] = {zero4(), zero4()}, t2[2] = {zero4(), zero4()};
-        mmab<D, 2>(t1, T16(O_DD), nullptr, LA, r0, T16(O_V), nullptr, LA, 32 * ch, l);
-        mmab<D, 2>(t2, T16(O_DW), nullptr, LA, r0, T16(O_K), nullptr, LA, 32 * ch, l);
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int s2 = 32 * ch + 16 * t + li;
-                dT[t][e] = sB[s2] * (t1[t][e] + sGam[s2] * t2[t][e]);
-            }
-    }
-    // ---- S5: P11 y1 = dT T^T, P12 da = T^T Y1 (dA = -da), P13 K K^T; M = diag(beta) dA * Gam
-#pragma unroll
-    for (int t = 0; t < 2; ++t) acc_N<false>(dT[t], T16(O_DT), nullptr, LB, r0, 32 * ch + 16 * t, l);
-    __syncthreads();
-    {
-        f4 y1[2] = {zero4(), zero4()};
-        mmab<C, 2>(y1, T16(O_DT), nullptr, LB, r0, T16(O_TN), nullptr, LB, 32 * ch, l);
-#pragma unroll
-        for (int t = 0; t < 2; ++t) acc_T<false>(y1[t], T16(O_Y1T), nullptr, LB, r0, 32 * ch + 16 * t, l);
-    }
-    __syncthreads();
+    // A's terms: dA = -TdD Delta^T strictly below the diagonal; dbeta += dA . (K K^T * Gam), the pair terms
+    // E += P * dP + dA * A, M = diag(beta) dA * Gam (K K^T after dQ has left: fewer accumulators live)
+    f4 kk[2] = {zero4(), zero4()};
+    mmab<D, 2>(kk, T16(O_K), nullptr, LA, r0, T16(O_K), nullptr, LA, 32 * ch, l);
     f4 Mt[2];
-    {
-        f4 da[2] = {zero4(), zero4()}, kk[2] = {zero4(), zero4()};
-        mmab<C, 2>(da, T16(O_TTH), nullptr, LB, r0, T16(O_Y1T), nullptr, LB, 32 * ch, l);
-        mmab<D, 2>(kk, T16(O_K), nullptr, LA, r0, T16(O_K), nullptr, LA, 32 * ch, l);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
-                const float gam = s2 < r ? __builtin_amdgcn_exp2f((float)(sG[r] - sG[s2]) * 1.4426950408889634f) : 0.f;
-                const float dav = s2 < r ? -da[t][e] : 0.f;
-                const float kg = kk[t][e] * gam;
-                rowB[e] += dav * kg;
-                const auto half = [e](uint2 v) { const uint32_t x = e < 2 ? v.x : v.y; return bf2f(e & 1 ? x >> 16 : x & 0xffffu); };
-                Ep[t][e] = Ep[t][e] * (half(pP[t][0]) + half(pP[t][1])) + dav * sB[r] * kg;
-                Mt[t][e] = sB[r] * dav * gam;
-            }
-    }
-    // ---- S6: P14 dK += (M + M^T) K
-    float *const sM = reinterpret_cast<float *>(arena + O_SM);  // [64][LDC] fp32 (V is dead)
+        for (int e = 0; e < 4; ++e) {
+            const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
+            const float gam = s2 < r ? __builtin_amdgcn_exp2f((float)(sG[r] - sG[s2]) * 1.4426950408889634f) : 0.f;
+            const float dav = s2 < r ? -dA[t][e] : 0.f;
+            const float kg = kk[t][e] * gam;
+            rowB[e] += dav * kg;
+            const auto half = [e](uint2 v) { const uint32_t x = e < 2 ? v.x : v.y; return bf2f(e & 1 ? x >> 16 : x & 0xffffu); };
+            Ep[t][e] = Ep[t][e] * (half(pP[t][0]) + half(pP[t][1])) + dav * sB[r] * kg;
+            Mt[t][e] = sB[r] * dav * gam;
+        }
+    __syncthreads();  // dPG, Q^T and the dq staging read (K^T stays)
+    // ---- S6: dK += (M + M^T) K
+    float *const sM = reinterpret_cast<float *>(arena + O_SM);  // [64][LDC] fp32
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -1871,7 +1759,6 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     // dK staged as fp32 rows in the free arena for 16-byte stores
     float *const sp = reinterpret_cast<float *>(arena);
     constexpr int LP = D + 4, PER = C * D / 4 / NTB;
-    static_assert(C * LP * 4 <= O_SM, "part staging below the pair matrix");
     static_assert(PER * NTB * 4 == C * D, "even split");
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -1892,7 +1779,7 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
         if (li == 0) {
             sRow[0][ch][r] = bsum;
             sRow[1][ch][r] = t2;
-            sRow[2][ch][r] = rbv;
+            sRow[2][ch][r] = ch == 0 ? rbv + sVT[r] : rbv;
         }
     }
     __syncthreads();
@@ -2352,16 +2239,21 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
         *reinterpret_cast<uint4 *>(a.w.Wb + ci * C * D + frag_off<D>(r, c8)) = *reinterpret_cast<const uint4 *>(sW + r * LK + c8);
     }
     if (!a.fwd_only) {
-        for (int i = tid; i < C * C / 4; i += NTP) {  // T as bf16 hi and lo planes
-            const int r = i / (C / 4), c4 = (i - r * (C / 4)) * 4;
-            const float4 x = *reinterpret_cast<const float4 *>(sT + r * LDC + c4);
-            uint2 h, l;
-            pk2(x.x, x.y, h.x, l.x);
-            pk2(x.z, x.w, h.y, l.y);
-            bfr *const tb = reinterpret_cast<bfr *>(a.w.T) + ci * 2 * C * C + r * C + c4;
-            *reinterpret_cast<uint2 *>(tb) = h;
-            *reinterpret_cast<uint2 *>(tb + C * C) = l;
-        }
+        // T^T as bf16 hi and lo planes in fragment order, the A operand of TdD = T^T dDelta in ck_bwd_seq_bf16: the
+        // 16-byte unit (s, r8) holds T^T[s][r8 .. r8 + 7] = T[r8 .. r8 + 7][s]; consecutive threads take consecutive s
+        static_assert(C * C / 8 == NTP, "one unit per thread");
+        bfr *const tb = reinterpret_cast<bfr *>(a.w.T) + ci * 2 * C * C;
+        const int s = tid % C, r8 = (tid / C) * 8;
+        float x[8];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) x[rr] = sT[(r8 + rr) * LDC + s];
+        uint4 h, l;
+        pk2(x[0], x[1], h.x, l.x);
+        pk2(x[2], x[3], h.y, l.y);
+        pk2(x[4], x[5], h.z, l.z);
+        pk2(x[6], x[7], h.w, l.w);
+        *reinterpret_cast<uint4 *>(tb + frag_off<C>(s, r8)) = h;
+        *reinterpret_cast<uint4 *>(tb + C * C + frag_off<C>(s, r8)) = l;
     }
     if (tid < C) a.w.G[ci * C + tid] = sG[tid];
 }
@@ -2370,11 +2262,13 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
 //
 // Reverse over chunks like ck_bwd_seq_kernel, for bf16 inputs.  Per chunk, with dh' the adjoint of the chunk's
 // exit state (this workgroup's value slice, in MFMA accumulators):
-//   dDelta = diag(rc) K dh' + P^T dY,   dh = gamma_C dh' + Q^T diag(gamma) dY - W^T dDelta.
+//   dDelta = diag(rc) K dh' + P^T dY,   dh = gamma_C dh' + Q^T diag(gamma) dY - W^T dDelta,
+// and it saves TdD = T^T dDelta (fp32 [C][D]), the only form in which ck_bwd_local_bf16 needs T and dDelta.
 // The A operands (K straight from the input, P^T hi / lo, Q^T and -W^T written by ck_prep) are read as MFMA
-// fragments from global memory into registers one chunk ahead, with the chunk's dY slice; LDS carries only what
-// the waves exchange: dh' as the operand [i][j] (hi / lo), dY^T, (diag(gamma) dY)^T (hi / lo) and dDelta^T.
-// Two barriers per chunk.
+// fragments from global memory into registers one chunk ahead, with the chunk's dY slice; LDS carries what the
+// waves exchange: dh' as the operand [i][j] (hi / lo), dY^T, (diag(gamma) dY)^T (hi / lo) and dDelta^T (hi / lo),
+// and T^T (hi / lo, fragment order), whose 32 bytes per thread are loaded one chunk ahead and stored between the
+// two barriers of the chunk that uses them.  Two barriers per chunk.
 struct BwdFrags {
     bf8 K[4], PT[4], QT[2], WT[2];  // PT[0..1] hi, PT[2..3] lo; WT = -W^T
     double g;
@@ -2393,7 +2287,9 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
     __shared__ __align__(16) bfr sYgl[VS * LDd];  // (diag(gamma) dY)^T lo
     __shared__ __align__(16) bfr sDd[VS * LDd];   // dDelta^T [i][r], hi
     __shared__ __align__(16) bfr sDdl[VS * LDd];  // dDelta^T lo
+    __shared__ __align__(16) bfr sTT[2 * C * C];  // T^T hi, lo (fragment order)
     __shared__ float sGam[C], sRc[C];
+    static_assert(2 * C * C / 8 == 2 * NTS, "two 16-byte pieces of T^T per thread");
 
     const SeqBlock sb = seq_block();
     const int i0 = sb.slice * VS, hv = sb.hv, b = sb.b;
@@ -2415,6 +2311,14 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
             const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
             dh[t][e] = a.dstate_T ? a.dstate_T[(head * D + i) * D + j] : 0.f;
         }
+    // this thread's two 16-byte pieces of the fragment-order T^T (hi | lo) of the chunk processed next
+    uint4 ttr0, ttr1;  // two scalars, not an array: an array of them stays on the stack at VS = 16
+    auto fetch_tt = [&](int c) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const bfr *>(a.w.T) +
+                                                           (head * a.NC + c) * 2 * C * C);
+        ttr0 = src[tid];
+        ttr1 = src[tid + NTS];
+    };
     using YRaw = typename std::conditional<DYF32, float2, uint32_t>::type;
     auto fetch = [&](BwdFrags &f, YRaw (&y)[8], int c) {
         const size_t ci = head * a.NC + c;
@@ -2501,6 +2405,10 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
                 *reinterpret_cast<uint4 *>(sYgl + (yc + cc) * LDd + 8 * yb) = lo;
             }
         }
+        // T^T of this chunk -> LDS (read after the second barrier; the previous chunk's reads ended before the
+        // first barrier of this one); the next chunk's pieces are loaded after the second barrier
+        reinterpret_cast<uint4 *>(sTT)[tid] = ttr0;
+        reinterpret_cast<uint4 *>(sTT)[tid + NTS] = ttr1;
         if (c > 0) fetch(nxt, yr, c - 1);
         // dDelta = diag(rc) K dh' + P^T dY
         if (cwave) {
@@ -2518,14 +2426,29 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
             }
         }
         __syncthreads();
-        {
-            // saved dDelta^T: the slice's rows of the bf16 hi and lo planes [i][r], in 16-byte pieces
-            bfr *const db = reinterpret_cast<bfr *>(a.w.dDl) + ci * 2 * D * C + (size_t)i0 * C;
-            for (int p = tid; p < VS * C / 8; p += NTS) {
-                const int i = p / (C / 8), r8 = (p - i * (C / 8)) * 8;
-                *reinterpret_cast<uint4 *>(db + i * C + r8) = *reinterpret_cast<const uint4 *>(sDd + i * LDd + r8);
-                *reinterpret_cast<uint4 *>(db + D * C + i * C + r8) = *reinterpret_cast<const uint4 *>(sDdl + i * LDd + r8);
+        if (c > 0) fetch_tt(c - 1);
+        if (cwave) {
+            // saved TdD = T^T dDelta (T^T and dDelta split): rows s = mrow + 4 lg + e, this slice's columns
+            f4 tdd[DN];
+#pragma unroll
+            for (int t = 0; t < DN; ++t) tdd[t] = zero4();
+#pragma unroll
+            for (int k = 0; k < C / 32; ++k) {
+                const bf8 th = ld_frag(sTT + frag_off<C>(mrow, 32 * k) + 8 * l);
+                const bf8 tl = ld_frag(sTT + C * C + frag_off<C>(mrow, 32 * k) + 8 * l);
+#pragma unroll
+                for (int t = 0; t < DN; ++t) {
+                    const bf8 yh = frag(sDd, LDd, 16 * (nt0 + t), 32 * k), ylo = frag(sDdl, LDd, 16 * (nt0 + t), 32 * k);
+                    tdd[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yh, tdd[t], 0, 0, 0);
+                    tdd[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tl, yh, tdd[t], 0, 0, 0);
+                    tdd[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, ylo, tdd[t], 0, 0, 0);
+                }
             }
+            float *const td = a.w.dDl + ci * C * D;
+#pragma unroll
+            for (int t = 0; t < DN; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) td[(size_t)(mrow + 4 * lg + e) * D + i0 + 16 * (nt0 + t) + li] = tdd[t][e];
         }
         // dh = gamma_C dh' + Q^T diag(gamma) dY + (-W^T) dDelta
 #pragma unroll
@@ -2535,6 +2458,7 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
     };
     BwdFrags fa, fb;
     fetch(fa, yr, a.NC - 1);
+    fetch_tt(a.NC - 1);
     int c = a.NC - 1;
     for (; c > 0; c -= 2) {
         step(c, fa, fb);
@@ -2577,7 +2501,7 @@ ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd) {
     put(s.U, n * cd * 4);
     put(s.H, bwd ? n * dd * (bf16 ? 2 : 4) : 0);
     put(s.Dl, bwd ? n * cd * 4 : 0);
-    put(s.T, bwd ? n * cc * 4 : 0);            // fp32, or bf16 hi / lo planes
+    put(s.T, bwd ? n * cc * 4 : 0);            // fp32, or T^T as bf16 hi / lo planes
     put(s.P, bf16 ? 0 : n * cc * 4);
     put(s.W, bf16 ? 0 : n * cd * 4);
     put(s.Wb, bf16 ? n * cd * 2 : 0);
@@ -2589,7 +2513,7 @@ ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd) {
     s.saved = off;
     off = 0;
     put(s.dH, n * dd * (bf16 ? 2 : 4));
-    put(s.dDl, n * cd * 4);                    // fp32, or dDelta^T as bf16 hi / lo planes
+    put(s.dDl, n * cd * 4);                    // fp32 dDelta, or TdD = T^T dDelta (bf16 set)
     put(s.part, (size_t)B * T * (bf16 ? Hk : Hv) * 2 * CK_D * 4);
     s.work = off;
     return s;

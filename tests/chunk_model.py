@@ -95,11 +95,58 @@ def bwd_local_chunk(q, k, v, beta, G, T, P, h, dh_next, Delta, dDelta, dY):
     return dq, dk, dv, dbeta, dg_log
 
 
-def run(q, k, v, g_log, beta, S0, dY, dS_T, C=64):
+def bwd_local_chunk_z(q, k, v, beta, G, P, h, dh_next, Delta, TdD, dY):
+    """bwd_local_chunk through Z = diag(beta) V - diag(beta gamma) K h (Delta = T Z), from TdD = T^T dDelta.
+
+    Everything T contributes then follows from TdD alone: dV = diag(beta) TdD, dK -= diag(beta gamma) TdD h^T, the
+    beta and gate terms of Z, and dA = -strict_lower(T^T dT T^T) = -strict_lower(TdD Delta^T) (dT = dDelta Z^T).
+    T and dDelta themselves are not needed."""
+    C = q.shape[0]
+    gam = np.exp(G)
+    gC = gam[-1]
+    r_C = np.exp(G[-1] - G)
+    Gam = np.tril(np.exp(np.tril(G[:, None] - G[None, :])))
+    dG = np.zeros(C)
+    X1 = dY @ h.T
+    dq = gam[:, None] * X1
+    dG += (q * dq).sum(1)
+    X2 = Delta @ dh_next.T
+    dk = r_C[:, None] * X2
+    t2 = (k * dk).sum(1)
+    dG -= t2
+    dG[-1] += t2.sum() + gC * (dh_next * h).sum()
+    dP = np.tril(dY @ Delta.T)
+    dPG = dP * Gam
+    dq += dPG @ k
+    dk += dPG.T @ q
+    e = dP * P
+    dG += e.sum(1) - e.sum(0)
+    # through Z
+    Y2 = TdD @ h.T
+    s4 = (Y2 * k).sum(1)
+    dk -= (beta * gam)[:, None] * Y2
+    dv = beta[:, None] * TdD
+    dbeta = (v * TdD).sum(1) - gam * s4
+    dG -= beta * gam * s4
+    # through A
+    dA = -np.tril(TdD @ Delta.T, -1)
+    KK = k @ k.T
+    dbeta += (dA * KK * Gam).sum(1)
+    Amat = np.tril(beta[:, None] * KK * Gam, -1)
+    e = dA * Amat
+    dG += e.sum(1) - e.sum(0)
+    M = beta[:, None] * dA * Gam
+    dk += (M + M.T) @ k
+    dg_log = np.cumsum(dG[::-1])[::-1]
+    return dq, dk, dv, dbeta, dg_log
+
+
+def run(q, k, v, g_log, beta, S0, dY, dS_T, C=64, z_form=False):
     """Whole-sequence forward + VJP for one batch element and one value head.
 
     q, k [T,Dk]; v, dY [T,Dv]; g_log, beta [T]; S0, dS_T [Dv,Dk] in the reference's state layout.
-    Returns (y, S_T, dq, dk, dv, dg_log, dbeta, dS0) with the states in [Dv,Dk] layout.
+    Returns (y, S_T, dq, dk, dv, dg_log, dbeta, dS0) with the states in [Dv,Dk] layout.  z_form runs the local
+    backward through TdD = T^T dDelta (bwd_local_chunk_z), as the bf16 kernel set does.
     """
     T_len, Dk = q.shape
     Dv = v.shape[1]
@@ -127,7 +174,10 @@ def run(q, k, v, g_log, beta, S0, dY, dS_T, C=64):
         sl = slice(c * C, (c + 1) * C)
         G, T, W, U, P = preps[c]
         dDelta, dh_prev = bwd_state_chunk(dh, q[sl], k[sl], G, W, P, dY[sl])
-        out = bwd_local_chunk(q[sl], k[sl], v[sl], beta[sl], G, T, P, hs[c], dh, Ds[c], dDelta, dY[sl])
+        if z_form:
+            out = bwd_local_chunk_z(q[sl], k[sl], v[sl], beta[sl], G, P, hs[c], dh, Ds[c], T.T @ dDelta, dY[sl])
+        else:
+            out = bwd_local_chunk(q[sl], k[sl], v[sl], beta[sl], G, T, P, hs[c], dh, Ds[c], dDelta, dY[sl])
         dq[sl], dk[sl], dv[sl], db[sl], dg[sl] = out
         dh = dh_prev
     n = T_len
