@@ -35,6 +35,37 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+// Four consecutive elements (i % 4 == 0) of a tensor of dtype dt, as fp32 / from fp32.
+__device__ __forceinline__ float4 load4(const void *p, size_t i, int dt) {
+    if (dt == DT_F32) return *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
+    if (dt == DT_BF16) {
+        const uint2 w = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(p) + i);
+        return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
+                           __uint_as_float(w.y & 0xffff0000u));
+    }
+    return make_float4(load_as_f32(p, i, dt), load_as_f32(p, i + 1, dt), load_as_f32(p, i + 2, dt),
+                       load_as_f32(p, i + 3, dt));
+}
+__device__ __forceinline__ void store4(void *p, size_t i, float4 x, int dt) {
+    if (dt == DT_F32) {
+        *reinterpret_cast<float4 *>(static_cast<float *>(p) + i) = x;
+    } else if (dt == DT_BF16) {
+        const uint32_t a = f32_to_bf16_cvt(x.x) | ((uint32_t)f32_to_bf16_cvt(x.y) << 16);
+        const uint32_t b = f32_to_bf16_cvt(x.z) | ((uint32_t)f32_to_bf16_cvt(x.w) << 16);
+        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(p) + i) = make_uint2(a, b);
+    } else {
+        store_from_f32(p, i, x.x, dt);
+        store_from_f32(p, i + 1, x.y, dt);
+        store_from_f32(p, i + 2, x.z, dt);
+        store_from_f32(p, i + 3, x.w, dt);
+    }
+}
+__device__ __forceinline__ float4 ld4f(const float *p, size_t i) { return *reinterpret_cast<const float4 *>(p + i); }
+__device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+__device__ __forceinline__ float4 fma4(float s, float4 a, float4 b) {
+    return make_float4(fmaf(s, a.x, b.x), fmaf(s, a.y, b.y), fmaf(s, a.z, b.z), fmaf(s, a.w, b.w));
+}
+
 __device__ __forceinline__ float decay_of(const float *g, size_t gi, int gate) {
     return gate == GATE_LOG ? expf(g[gi]) : g[gi];
 }
@@ -62,40 +93,42 @@ __global__ __launch_bounds__(MK_THREADS) void mask_fix_fwd_kernel(MaskArgs a) {
     __shared__ float c[MK_MAX_HEADS];
     if (!keep) key_dots(a, tok, c);
     const int rep = a.Hv / a.Hk;
-    for (int e = threadIdx.x; e < a.Hv * a.Dv; e += MK_THREADS) {
+    // four consecutive elements per thread and step (Dv % 4 == 0)
+    for (int e = 4 * threadIdx.x; e < a.Hv * a.Dv; e += 4 * MK_THREADS) {
         const size_t vi = tok * a.Hv * a.Dv + e;
-        const float yp = a.Yp ? a.Yp[vi] : load_as_f32(a.y, vi, a.out_dt);
-        float y = yp;
+        float4 y = a.Yp ? ld4f(a.Yp, vi) : load4(a.y, vi, a.out_dt);
         if (!keep) {
             const int hv = e / a.Dv;
             const size_t gi = tok * a.Hv + hv;
-            const float d = decay_of(a.g, gi, a.gate), bt = a.beta[gi];
-            y = d * yp + bt * c[hv / rep] * (load_as_f32(a.v, vi, a.in_dt) - d * a.Z[vi]);
+            const float d = decay_of(a.g, gi, a.gate), bc = a.beta[gi] * c[hv / rep];
+            const float4 v = load4(a.v, vi, a.in_dt), z = ld4f(a.Z, vi);
+            y = make_float4(d * y.x + bc * (v.x - d * z.x), d * y.y + bc * (v.y - d * z.y), d * y.z + bc * (v.z - d * z.z),
+                            d * y.w + bc * (v.w - d * z.w));
         }
-        store_from_f32(a.y, vi, y, a.out_dt);
+        store4(a.y, vi, y, a.out_dt);
     }
 }
 
-// Cotangents of the two passes: dy1 = (masked ? d dy : dy), dz = (masked ? -beta c d dy : 0), both fp32.
+// Cotangents of the two passes: dy1 = (masked ? d dy : dy), dz = (masked ? -beta c d dy : 0), both fp32; four
+// consecutive elements per thread and step (Dv % 4 == 0).
 __global__ __launch_bounds__(MK_THREADS) void mask_bwd_cot_kernel(MaskArgs a) {
     const size_t tok = blockIdx.x;
     const bool keep = a.mask[tok] != 0;
     __shared__ float c[MK_MAX_HEADS];
     if (!keep) key_dots(a, tok, c);
     const int rep = a.Hv / a.Hk;
-    for (int e = threadIdx.x; e < a.Hv * a.Dv; e += MK_THREADS) {
+    for (int e = 4 * threadIdx.x; e < a.Hv * a.Dv; e += 4 * MK_THREADS) {
         const size_t vi = tok * a.Hv * a.Dv + e;
-        const float dy = load_as_f32(a.dy, vi, a.dy_dt);
-        if (keep) {
-            a.dy1[vi] = dy;
-            a.dz[vi] = 0.f;
-        } else {
+        const float4 dy = load4(a.dy, vi, a.dy_dt);
+        float s1 = 1.f, sz = 0.f;
+        if (!keep) {
             const int hv = e / a.Dv;
             const size_t gi = tok * a.Hv + hv;
-            const float d = decay_of(a.g, gi, a.gate);
-            a.dy1[vi] = d * dy;
-            a.dz[vi] = -a.beta[gi] * c[hv / rep] * d * dy;
+            s1 = decay_of(a.g, gi, a.gate);
+            sz = -a.beta[gi] * c[hv / rep] * s1;
         }
+        *reinterpret_cast<float4 *>(a.dy1 + vi) = make_float4(s1 * dy.x, s1 * dy.y, s1 * dy.z, s1 * dy.w);
+        *reinterpret_cast<float4 *>(a.dz + vi) = make_float4(sz * dy.x, sz * dy.y, sz * dy.z, sz * dy.w);
     }
 }
 
@@ -126,30 +159,31 @@ __global__ __launch_bounds__(MK_THREADS) void mask_bwd_combine_kernel(MaskArgs a
         }
         __syncthreads();
     }
-    for (int e = tid; e < a.Hk * a.Dk; e += MK_THREADS) {
+    // four consecutive elements per thread and step (Dk, Dv % 4 == 0)
+    for (int e = 4 * tid; e < a.Hk * a.Dk; e += 4 * MK_THREADS) {
         const int hk = e / a.Dk;
         const size_t i = tok * a.Hk * a.Dk + e;
-        float dq = a.dq1[i], dk = a.dk1[i] + a.dk2[i] + a.dq2[i];
+        float4 dq = ld4f(a.dq1, i), dk = add4(add4(ld4f(a.dk1, i), ld4f(a.dk2, i)), ld4f(a.dq2, i));
         if (!keep) {
             float f = 0.f;
             for (int r = 0; r < rep; ++r) {
                 const int hv = hk * rep + r;
                 f += a.beta[tok * a.Hv + hv] * su[hv];
             }
-            dq += f * load_as_f32(a.k, i, a.in_dt);
-            dk += f * load_as_f32(a.q, i, a.in_dt);
+            dq = fma4(f, load4(a.k, i, a.in_dt), dq);
+            dk = fma4(f, load4(a.q, i, a.in_dt), dk);
         }
-        store_from_f32(a.dq, i, dq, a.grad_dt);
-        store_from_f32(a.dk, i, dk, a.grad_dt);
+        store4(a.dq, i, dq, a.grad_dt);
+        store4(a.dk, i, dk, a.grad_dt);
     }
-    for (int e = tid; e < a.Hv * a.Dv; e += MK_THREADS) {
+    for (int e = 4 * tid; e < a.Hv * a.Dv; e += 4 * MK_THREADS) {
         const size_t i = tok * a.Hv * a.Dv + e;
-        float dv = a.dv1[i] + a.dv2[i];
+        float4 dv = add4(ld4f(a.dv1, i), ld4f(a.dv2, i));
         if (!keep) {
             const int hv = e / a.Dv;
-            dv += a.beta[tok * a.Hv + hv] * c[hv / rep] * load_as_f32(a.dy, i, a.dy_dt);
+            dv = fma4(a.beta[tok * a.Hv + hv] * c[hv / rep], load4(a.dy, i, a.dy_dt), dv);
         }
-        store_from_f32(a.dv, i, dv, a.grad_dt);
+        store4(a.dv, i, dv, a.grad_dt);
     }
     for (int hv = tid; hv < a.Hv; hv += MK_THREADS) {
         const size_t gi = tok * a.Hv + hv;
