@@ -605,9 +605,11 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
     __shared__ __align__(16) float sQ[C * LD];   // K, then Q
     __shared__ __align__(16) float sY[C * LV];   // dY slice
     __shared__ __align__(16) float sYg[C * LV];  // diag(gamma) dY slice
-    __shared__ __align__(16) float sH[D * LV];   // dh slice, [j][i]
+    // dh slice [j][i]; after the dDelta products (second barrier) T [r][s] (stride LDC) until the step ends
+    __shared__ __align__(16) float sH[(D * LV > C * LDC) ? D * LV : C * LDC];
     __shared__ __align__(16) float sD[C * LV];   // dDelta slice
     __shared__ double sG[C];
+    float *const sT = sH;
 
     const SeqBlock sb = seq_block();
     const int i0 = sb.slice * VS, hv = sb.hv, b = sb.b;
@@ -627,7 +629,7 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
             const int j = 16 * w + 4 * lg + e, i = i0 + 16 * t + li;
             dh[t][e] = a.dstate_T ? a.dstate_T[(head * D + i) * D + j] : 0.f;
         }
-    TileRegs<C, C, NTS> rP;
+    TileRegs<C, C, NTS> rP, rT;
     TileRegs<C, D, NTS> rK, rW, rQ;
     TileRegs<C, VS, NTS> rY;
     double rG = 0.0;
@@ -647,6 +649,7 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
         const int n = min(C, T - c * C);
         tile_fetch(rW, a.w.W + ci * C * D, D, C, DT_F32);
         tile_fetch(rQ, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
+        tile_fetch(rT, a.w.T + ci * C * C, C, C, DT_F32);
     };
     fetchA(a.NC - 1);
     fetchB(a.NC - 1);
@@ -677,16 +680,27 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int r = mrow + 4 * lg + e, ii = 16 * (nt0 + t) + li;
-                    const float dd = kd[t][e] * expf((float)(sG[C - 1] - sG[r])) + pd[t][e];
-                    sD[r * LV + ii] = dd;
-                    a.w.dDl[ci * C * D + r * D + i0 + ii] = dd;
+                    sD[r * LV + ii] = kd[t][e] * expf((float)(sG[C - 1] - sG[r])) + pd[t][e];
                 }
         }
         __syncthreads();
         tile_store(sW, LD, rW, DT_F32, NoScale{});
         tile_store(sQ, LD, rQ, a.in_dt, NoScale{});
+        tile_store(sT, LDC, rT, DT_F32, NoScale{});  // over dh', read before the barrier above
         __syncthreads();
         if (c > 0) fetchB(c - 1);
+        // saved TdD = T^T dDelta, the only form in which ck_bwd_local_kernel needs T and dDelta
+        if (cwave) {
+            f4 tdd[DN];
+#pragma unroll
+            for (int t = 0; t < DN; ++t) tdd[t] = zero4();
+            mma_strip<C, DN>(tdd, sT + mrow, 1, LDC, sD + 16 * nt0, LV, 1, 16);
+#pragma unroll
+            for (int t = 0; t < DN; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    a.w.dDl[ci * C * D + (size_t)(mrow + 4 * lg + e) * D + i0 + 16 * (nt0 + t) + li] = tdd[t][e];
+        }
         // dh = gamma_C dh' + Q^T diag(gamma) dY - W^T dDelta
         const float gC = expf((float)sG[C - 1]);
         f4 wd[NTN];
@@ -807,14 +821,15 @@ constexpr int NTB = 512;  // ck_bwd_local: 8 waves; waves w and w+4 share the 16
 
 // One value head hv = hk * rep + rr of key head hk.  dq | dk of the key head are summed in order (rr = 0, 1, ...)
 // in the part rows of its first value head hk * rep, each thread reading back only the elements it wrote itself,
-// and the last value head writes dq and dk in the gradient dtype.
+// and the last value head writes dq and dk in the gradient dtype.  T and dDelta enter only through TdD = T^T dDelta
+// (saved by ck_bwd_seq_kernel): dv = diag(beta) TdD, dK -= diag(beta gamma) Y2 (Y2 = TdD h^T), dA = -TdD Delta^T
+// below the diagonal, dbeta += rowsum(V * TdD) - gamma s4 and dG -= beta gamma s4 (s4 = rowsum(K * Y2)).
 __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk, int b, int rr, int rep) {
-    __shared__ __align__(16) float R1[D * LD];       // h / dh' ([j][i]); then K at R1, Q / dW at R1 + C*LD
-    __shared__ __align__(16) float R2[C * LD];       // dY, then dDelta, then the pair matrix E
-    __shared__ __align__(16) float RX[2 * C * LDC];  // dDelta, Delta; V ([C][LD] fits); R3 = RX (Y1), R4 = RX + C*LDC
-    __shared__ __align__(16) float R5[C * LDC];      // T
+    __shared__ __align__(16) float R1[D * LD];       // h, then dh' ([j][i]); then K at R1, Q at R1 + C*LD
+    __shared__ __align__(16) float R2[C * LD];       // dY, then the pair matrix E
+    __shared__ __align__(16) float RX[2 * C * LDC];  // TdD, then Delta ([C][LD] fits); R4 = RX + C*LDC: dPG, M
     __shared__ double sG[C];
-    __shared__ float sGam[C], sRc[C], sB[C], sScan[2][C];
+    __shared__ float sGam[C], sRc[C], sB[C], sVT[C], sScan[2][C];
     __shared__ float sRow[3][2][C];                  // per column half: chunk-start pair terms, t2 terms, dbeta
     __shared__ float sLast[8];
 
@@ -830,21 +845,17 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
     const size_t ci = chunk_index(a, b, hv, c);
     float *const sKm = R1;
     float *const sQm = R1 + C * LD;
-    float *const R3 = RX;
     float *const R4 = RX + C * LDC;
     static_assert(C * LD <= 2 * C * LDC, "a [C][D] tile fits RX");
     const float *Hc = a.w.H + ci * D * D;
     const float *dHc = a.w.dH + ci * D * D;
     const float *Dc = a.w.Dl + ci * C * D;
-    const float *dDc = a.w.dDl + ci * C * D;
+    const float *TDc = a.w.dDl + ci * C * D;
     const size_t qk0 = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
     const size_t v0 = (((size_t)b * a.Ts + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
-    // dW of this chunk is parked in its rows of the dq|dk output buffer until it is needed (rows >= n of dW
-    // are zero: padded tokens have k = 0, so their dDelta vanishes)
-    float *const dWpark = a.w.part + ((size_t)b * T + t0) * a.Hv * 2 * D + (size_t)hv * 2 * D;
     const size_t park_row = (size_t)a.Hv * 2 * D;
 
-    // ---- phase 0: gates, dY, h
+    // ---- phase 0: gates, dY, h; TdD with dv = diag(beta) TdD and rowsum(V * TdD) from its loads
     if (tid < C) {
         sG[tid] = a.w.G[ci * C + tid];
         float bt = 0.f;
@@ -853,18 +864,47 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
     }
     load_tile<D, D, NTB>(R1, LD, Hc, D, D, DT_F32, nullptr, tid);
     load_tile<C, D, NTB>(R2, LD, elem_ptr(a.dy, v0, a.dy_dt), v_row, n, a.dy_dt, nullptr, tid);
-    load_tile<C, D, NTB>(RX, LD, dDc, D, C, DT_F32, nullptr, tid);  // dDelta, an MFMA operand of phase 1 (RX is free until V)
+    {
+        constexpr int PER = C * D / 4 / NTB;  // float4 pieces per thread; 32 consecutive threads hold one row
+        static_assert(PER * NTB * 4 == C * D && (D / 4) == 32, "even split, half a wave per row");
+        float4 td[PER];
+        float vv[PER][4], bt[PER];
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const int v = tid + p * NTB, r = v / (D / 4), c4 = (v - r * (D / 4)) * 4;
+            td[p] = *reinterpret_cast<const float4 *>(TDc + r * D + c4);
+            bt[p] = r < n ? a.beta[((size_t)b * a.Ts + t0 + r) * a.Hv + hv] : 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) vv[p][q] = r < n ? load_as_f32(a.v, v0 + (size_t)r * v_row + c4 + q, a.in_dt) : 0.f;
+        }
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const int v = tid + p * NTB, r = v / (D / 4), c4 = (v - r * (D / 4)) * 4;
+            *reinterpret_cast<float4 *>(RX + r * LD + c4) = td[p];
+            float vt = vv[p][0] * td[p].x + vv[p][1] * td[p].y + vv[p][2] * td[p].z + vv[p][3] * td[p].w;
+            vt = row16_allreduce(vt);
+            vt += __shfl_xor(vt, 16, 64);
+            if ((tid & 31) == 0) sVT[r] = vt;
+            if (r < n) {
+                const float4 dv = make_float4(bt[p] * td[p].x, bt[p] * td[p].y, bt[p] * td[p].z, bt[p] * td[p].w);
+                const size_t o = v0 + (size_t)r * v_row + c4;
+                if (a.grad_dt == DT_F32) {
+                    *reinterpret_cast<float4 *>(static_cast<float *>(a.dv) + o) = dv;
+                } else {
+                    store_from_f32(a.dv, o, dv.x, a.grad_dt);
+                    store_from_f32(a.dv, o + 1, dv.y, a.grad_dt);
+                    store_from_f32(a.dv, o + 2, dv.z, a.grad_dt);
+                    store_from_f32(a.dv, o + 3, dv.w, a.grad_dt);
+                }
+            }
+        }
+    }
     __syncthreads();
     if (tid < C) {
         sGam[tid] = expf((float)sG[tid]);
         sRc[tid] = expf((float)(sG[C - 1] - sG[tid]));
     }
-    __syncthreads();
-    const float gC = sGam[C - 1];
-    float bnd[4] = {0.f, 0.f, 0.f, 0.f};   // pair terms (r, chunk start) of rows r0+4lg+e, this lane's columns
-    float rowB[4] = {0.f, 0.f, 0.f, 0.f};  // dbeta partials
-    float tl[4] = {0.f, 0.f, 0.f, 0.f};    // pair terms (C-1, r)
-    float lastp = 0.f;                     // pair (C-1, chunk start): gamma_C <dh', h>
+    float lastp = 0.f;  // pair (C-1, chunk start): gamma_C <dh', h>
     {
         constexpr int PER = D * D / 4 / NTB;
         float4 dv4[PER];
@@ -877,31 +917,42 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             lastp += dv4[p].x * hh[0] + dv4[p].y * hh[1] + dv4[p].z * hh[2] + dv4[p].w * hh[3];
         }
     }
-    // the waves' parts go to LDS now (the raw dh' loads and h reads are not kept live until the straddle sums)
-    lastp = wave_sum(lastp * gC);
-    if (l == 0) sLast[w] = lastp;
+    float bnd[4] = {0.f, 0.f, 0.f, 0.f};   // pair terms (r, chunk start) of rows r0+4lg+e, this lane's columns
+    float rowB[4] = {0.f, 0.f, 0.f, 0.f};  // dbeta partials
+    float tl[4] = {0.f, 0.f, 0.f, 0.f};    // pair terms (C-1, r)
 
-    // ---- phase 1: dQ = diag(gamma) dY h^T ; dW = -dDelta h^T (parked)
-    f4 dQ[4], dK[4];
+    // ---- phase 1: dQ = diag(gamma) dY h^T ; Y2 = TdD h^T.  This lane's A values of TdD (row r0 + li, columns
+    // 4 k + lg) stay in registers for dA = TdD Delta^T in phase 2.
+    f4 dQ[4], dK[4], Y2[4];
+    float tdA[D / 4];
     {
-        f4 dw[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) dQ[t] = dw[t] = zero4();
-        mma_strip<D, 4>(dQ, R2 + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD, l);
-        mma_strip<D, 4>(dw, RX + r0 * LD, LD, 1, R1 + 64 * ch * LD, 1, LD, 16 * LD, l);
+        for (int t = 0; t < 4; ++t) dQ[t] = Y2[t] = zero4();
+        const float *ay = R2 + (r0 + li) * LD + lg, *at = RX + (r0 + li) * LD + lg;
+        const float *bh = R1 + (64 * ch + li) * LD + lg;
+#pragma unroll 8
+        for (int k = 0; k < D / 4; ++k) {
+            const float yv = ay[4 * k], tv = at[4 * k];
+            tdA[k] = tv;
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
-                dQ[t][e] *= sGam[r];
-                if (r < n) dWpark[r * park_row + j] = -dw[t][e];
+            for (int t = 0; t < 4; ++t) {
+                const float bv = bh[16 * t * LD + 4 * k];
+                dQ[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(yv, bv, dQ[t], 0, 0, 0);
+                Y2[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(tv, bv, Y2[t], 0, 0, 0);
             }
+        }
     }
+    // the waves' parts of <dh', h> go to LDS now
+    lastp = wave_sum(lastp * sGam[C - 1]);
+    if (l == 0) sLast[w] = lastp;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dQ[t][e] *= sGam[r0 + 4 * lg + e];
     __syncthreads();
-    // ---- phase 2: dK = diag(gamma_C/gamma) Delta dh'^T ; dP = lower(dY Delta^T)
+    // ---- phase 2: dK = diag(gamma_C/gamma) Delta dh'^T ; dP = lower(dY Delta^T) ; dA = -TdD Delta^T
     load_tile<D, D, NTB>(R1, LD, dHc, D, D, DT_F32, nullptr, tid);
-    load_tile<C, D, NTB>(RX, LD, Dc, D, C, DT_F32, nullptr, tid);  // Delta in place of dDelta (phase 1 is done)
+    load_tile<C, D, NTB>(RX, LD, Dc, D, C, DT_F32, nullptr, tid);  // Delta in place of TdD (phase 1 is done)
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < 4; ++t) dK[t] = zero4();
@@ -910,10 +961,17 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) dK[t][e] *= sRc[r0 + 4 * lg + e];
-    f4 dPG[2], Ep[2];
+    f4 dPG[2], Ep[2], dA[2];
     {
         f4 dp[2] = {zero4(), zero4()};
+        dA[0] = dA[1] = zero4();
         mma_strip<D, 2>(dp, R2 + r0 * LD, LD, 1, RX + 32 * ch * LD, 1, LD, 16 * LD, l);
+        const float *bd = RX + (32 * ch + li) * LD + lg;
+#pragma unroll 8
+        for (int k = 0; k < D / 4; ++k)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                dA[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(tdA[k], bd[16 * t * LD + 4 * k], dA[t], 0, 0, 0);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -925,7 +983,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             }
     }
     __syncthreads();
-    // ---- phase 3: dQ += dPG K ; dK += dPG^T Q
+    // ---- phase 3: dQ += dPG K ; dK += dPG^T Q ; K K^T
     load_tile<C, D, NTB>(sKm, LD, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt, nullptr, tid);
     load_tile<C, D, NTB>(sQm, LD, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt, nullptr, tid);
 #pragma unroll
@@ -933,102 +991,26 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
 #pragma unroll
         for (int e = 0; e < 4; ++e) R4[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = dPG[t][e];
     __syncthreads();
+    // the boundary terms q . dQ and k . dK (before the products), and Z's terms through Y2: s4 = k . Y2
+    // (dbeta -= gamma s4, dG -= beta gamma s4), dK -= beta gamma Y2
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+            const float kv = sKm[r * LD + j], bg = sB[r] * sGam[r];
             bnd[e] += sQm[r * LD + j] * dQ[t][e];
-            tl[e] += sKm[r * LD + j] * dK[t][e];
+            tl[e] += kv * dK[t][e];
+            const float s4 = kv * Y2[t][e];
+            rowB[e] -= sGam[r] * s4;
+            bnd[e] -= bg * s4;
+            dK[t][e] -= bg * Y2[t][e];
         }
     mma_strip<C, 4>(dQ, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16, l);
     mma_strip<C, 4>(dK, R4 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16, l);
-    __syncthreads();
-    // ---- phase 4: through T.  R1b <- dW, R2 <- dDelta, RX <- V, R5 <- T
-    load_tile<C, D, NTB>(sQm, LD, dWpark, park_row, n, DT_F32, nullptr, tid);
-    load_tile<C, D, NTB>(R2, LD, dDc, D, C, DT_F32, nullptr, tid);
-    load_tile<C, D, NTB>(RX, LD, elem_ptr(a.v, v0, a.in_dt), v_row, n, a.in_dt, nullptr, tid);
-    load_tile<C, C, NTB>(R5, LDC, a.w.T + ci * C * C, C, C, DT_F32, nullptr, tid);
-    __syncthreads();
-    f4 dvv[4];  // dv at this lane's accumulator positions
-    {
-        f4 tdw[4], tdd[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) tdw[t] = tdd[t] = zero4();
-        mma_strip<C, 4>(tdw, R5 + r0, 1, LDC, sQm + 64 * ch, LD, 1, 16, l);
-        mma_strip<C, 4>(tdd, R5 + r0, 1, LDC, R2 + 64 * ch, LD, 1, 16, l);
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
-                const float bg = sB[r] * sGam[r];
-                dK[t][e] += bg * tdw[t][e];
-                const float s4 = tdw[t][e] * sKm[r * LD + j];
-                rowB[e] += sGam[r] * s4;
-                bnd[e] += bg * s4;
-                rowB[e] += RX[r * LD + j] * tdd[t][e];
-                dvv[t][e] = sB[r] * tdd[t][e];
-            }
-    }
-    f4 dT[2];
-    {
-        f4 t1[2] = {zero4(), zero4()}, t2[2] = {zero4(), zero4()};
-        mma_strip<D, 2>(t1, R2 + r0 * LD, LD, 1, RX + 32 * ch * LD, 1, LD, 16 * LD, l);
-        mma_strip<D, 2>(t2, sQm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD, l);
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int s2 = 32 * ch + 16 * t + li;
-                dT[t][e] = sB[s2] * (t1[t][e] + sGam[s2] * t2[t][e]);
-            }
-    }
-    __syncthreads();
-    {
-        // dv leaves through a wave-private staging block in R2 (dDelta is read; R2 next holds the pair matrix after
-        // two more barriers): the wave's 16 x 64 fp32 part at row stride 64, four 16-byte row pieces per lane
-        static_assert(8 * 16 * 64 <= C * LD, "dv staging fits R2");
-        float *const stv = R2 + w * 16 * 64;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) stv[(4 * lg + e) * 64 + 16 * t + li] = dvv[t][e];
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const int i = l + 64 * p, rr = i >> 4, r = r0 + rr, c4 = 4 * (i & 15);
-            const float4 v = *reinterpret_cast<const float4 *>(stv + rr * 64 + c4);
-            if (r >= n) continue;
-            const size_t o = v0 + (size_t)r * v_row + 64 * ch + c4;
-            if (a.grad_dt == DT_F32) {
-                *reinterpret_cast<float4 *>(static_cast<float *>(a.dv) + o) = v;
-            } else {
-                store_from_f32(a.dv, o, v.x, a.grad_dt);
-                store_from_f32(a.dv, o + 1, v.y, a.grad_dt);
-                store_from_f32(a.dv, o + 2, v.z, a.grad_dt);
-                store_from_f32(a.dv, o + 3, v.w, a.grad_dt);
-            }
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) R4[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = dT[t][e];
-    __syncthreads();
-    // ---- phase 5: dA = -T^T dT T^T ; K K^T ; M = diag(beta) dA * Gam
-    {
-        f4 y1[2] = {zero4(), zero4()};
-        mma_strip<C, 2>(y1, R4 + r0 * LDC, LDC, 1, R5 + 32 * ch * LDC, 1, LDC, 16 * LDC, l);
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) R3[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = y1[t][e];
-    }
-    __syncthreads();
     f4 Mt[2];
     {
-        f4 da[2] = {zero4(), zero4()}, kk[2] = {zero4(), zero4()};
-        mma_strip<C, 2>(da, R5 + r0, 1, LDC, R3 + 32 * ch, LDC, 1, 16, l);
+        f4 kk[2] = {zero4(), zero4()};
         mma_strip<D, 2>(kk, sKm + r0 * LD, LD, 1, sKm + 32 * ch * LD, 1, LD, 16 * LD, l);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -1036,7 +1018,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             for (int e = 0; e < 4; ++e) {
                 const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
                 const float gam = s2 < r ? expf((float)(sG[r] - sG[s2])) : 0.f;
-                const float dav = s2 < r ? -da[t][e] : 0.f;
+                const float dav = s2 < r ? -dA[t][e] : 0.f;
                 const float kg = kk[t][e] * gam;
                 rowB[e] += dav * kg;
                 Ep[t][e] += dav * sB[r] * kg;
@@ -1044,6 +1026,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             }
     }
     __syncthreads();
+    // ---- phase 4: dK += (M + M^T) K
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -1051,7 +1034,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
     __syncthreads();
     mma_strip<C, 4>(dK, R4 + r0 * LDC, LDC, 1, sKm + 64 * ch, LD, 1, 16, l);
     mma_strip<C, 4>(dK, R4 + r0, 1, LDC, sKm + 64 * ch, LD, 1, 16, l);
-    // ---- phase 6: straddle sums for dg, dbeta, outputs.  R2 (dDelta) is free: E goes there.
+    // ---- phase 6: straddle sums for dg, dbeta, outputs.  R2 (dY) is free: E goes there.
     float *const sE = R2;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -1066,7 +1049,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
         if (li == 0) {
             sRow[0][ch][r] = bsum;
             sRow[1][ch][r] = t2;
-            sRow[2][ch][r] = rbv;
+            sRow[2][ch][r] = ch == 0 ? rbv + sVT[r] : rbv;
         }
     }
     __syncthreads();
@@ -1097,8 +1080,8 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             for (int e = 0; e < 4; ++e) stg[(4 * lg + e) * LQ + 16 * t + li] = X[t][e];
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            const int i = l + 64 * p, rr = i >> 4, r = r0 + rr, c4 = 64 * ch + 4 * (i & 15);
-            float4 v = *reinterpret_cast<const float4 *>(stg + rr * LQ + 4 * (i & 15));
+            const int i = l + 64 * p, rr2 = i >> 4, r = r0 + rr2, c4 = 64 * ch + 4 * (i & 15);
+            float4 v = *reinterpret_cast<const float4 *>(stg + rr2 * LQ + 4 * (i & 15));
             if (r >= n) continue;
             if (!first) v = make_float4(prev[p].x + v.x, prev[p].y + v.y, prev[p].z + v.z, prev[p].w + v.w);
             const size_t o = qk_out + (size_t)r * a.Hk * D + c4;
