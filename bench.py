@@ -107,18 +107,20 @@ def kernel_model(name, B, T, Hk, Hv, D, in_b):
             if bf:  # reads W, Q, K~^T, P (hi / lo), U, G; writes h (bf16), Delta (fp32), y
                 return f, ch * (3 * cd * 2 + 2 * cc * 2 + cd * 4 + C * 8 + dd * 2 + cd * 4 + cd * 2)
             return f, ch * (2 * cd * 4 + cc * 4 + 2 * cd * in_b + C * 8 + dd * 4 + cd * 4 + cd * in_b)
-        if bf:  # reads K, P^T (hi / lo), Q^T, -W^T, dY, G; writes dh' (bf16), dDelta (bf16 hi / lo planes)
-            return f, ch * (cd * 2 + 2 * cc * 2 + 2 * cd * 2 + cd * 2 + C * 8 + dd * 2 + cd * 4)
-        return f, ch * (cc * 4 + cd * 4 + 3 * cd * in_b + C * 8 + dd * 4 + cd * 4)
+        f += ch * 2 * cc * D  # TdD = T^T dDelta
+        if bf:  # reads K, P^T (hi / lo), Q^T, -W^T, T^T (hi / lo), dY, G; writes dh' (bf16), TdD (fp32)
+            return f, ch * (cd * 2 + 2 * cc * 2 + 2 * cd * 2 + 2 * cc * 2 + cd * 2 + C * 8 + dd * 2 + cd * 4)
+        return f, ch * (2 * cc * 4 + cd * 4 + 3 * cd * in_b + C * 8 + dd * 4 + cd * 4)
     if name == "ck_bwd_local":
-        f = ch * (3 * 2 * cd * D + 10 * 2 * cc * D + 2 * 2 * cc * C)
-        if bf:  # reads h, dh' (bf16), Delta (fp32), dDelta, T (bf16 hi / lo), P (hi / lo), G, v, dy, beta and the
-            #     key head's q, k; writes dv, dg, dbeta and the key head's dq, dk (one workgroup per key head sums
-            #     its value heads; the fp32 running sum between them is not counted)
+        # dQ, TdD h^T, dK (Dv contractions), dp, dA = TdD Delta^T, dPG K, dPG^T Q, K K^T, (M + M^T) K
+        f = ch * (3 * 2 * cd * D + 6 * 2 * cc * D)
+        if bf:  # reads h, dh' (bf16), Delta, TdD (fp32), P (hi / lo), G, v, dy, beta and the key head's q, k;
+            #     writes dv, dg, dbeta and the key head's dq, dk (one workgroup per key head sums its value heads;
+            #     the fp32 running sum between them is not counted)
             kv = Hk / Hv  # key-head rows per value head
-            return f, ch * (2 * dd * 2 + 2 * cd * 4 + cc * 4 + 2 * cc * 2 + C * 8 + 2 * cd * 2 + 2 * cd * 2 * kv
+            return f, ch * (2 * dd * 2 + 2 * cd * 4 + 2 * cc * 2 + C * 8 + 2 * cd * 2 + 2 * cd * 2 * kv
                             + C * 4 + 2 * cd * 2 * kv + cd * 2 + 2 * C * 4)
-        by = ch * (2 * dd * 4 + 2 * cd * 4 + 2 * cc * 4 + C * 8 + 4 * cd * in_b + C * 4
+        by = ch * (2 * dd * 4 + 2 * cd * 4 + cc * 4 + C * 8 + 4 * cd * in_b + C * 4
                    + 2 * cd * 4 + cd * in_b + 2 * C * 4)
         return f, by
     if name == "rec_fwd":
