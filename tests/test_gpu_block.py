@@ -146,3 +146,42 @@ def test_block_lora_bf16(dev):
     for name, g in got.items():
         key = "x" if name == "x" else lora_key(name)
         assert nerr(g, want[key]) <= 3e-2, (name, nerr(g, want[key]))
+
+
+def test_block_config4_full_size(dev, monkeypatch):
+    """The block configuration itself: B=2, T=8192, hidden 2048, Hk=16, Hv=32, D=128, bf16 weights and activations,
+    LoRA rank 16 on the five projections (A ~ N(0, 0.02), B = 0), gradients to the adapters and the input.  At this
+    size: grad(A) is exactly zero and every gradient finite (B = 0); the chunked and the recurrent form of the
+    recurrence (each pinned against the oracle above and in the recurrence tests) agree on the output, dx and every
+    grad(B); and the output's first 256 tokens equal the block run on those tokens alone (causality), which the
+    float64 block oracle pins."""
+    h, Hk, Hv, D, rank, scale, B, T = 2048, 16, 32, 128, 16, 2.0, 2, 8192
+    P = BO.make_block_params(h, Hk, Hv, D, D, rank=rank, lora_scale=scale, b_std=0.0, seed=21, w_std=0.02)
+    P = {k: (torch.tensor(v).bfloat16().float().numpy() if isinstance(v, np.ndarray) else v) for k, v in P.items()}
+    r = np.random.default_rng(22)
+    bf = lambda a: torch.tensor(a).bfloat16().float().numpy()
+    x = bf(r.standard_normal((B, T, h)).astype(np.float32))
+    dout = bf(r.standard_normal((B, T, h)).astype(np.float32))
+    dims = (h, Hk, Hv, D, D)
+    print("block B=2 T=8192 hidden 2048 bf16 LoRA 16: chunked form", flush=True)
+    out_c, g_c = run_block(P, x, dout, dims, dev, torch.bfloat16, rank, scale)
+    for name, g in g_c.items():
+        assert np.all(np.isfinite(g)), name
+        if name.endswith("lora_a"):
+            assert not np.any(g), name
+    assert np.all(np.isfinite(out_c))
+    monkeypatch.setenv("GDN_FORM", "recurrent")
+    print("  recurrent form", flush=True)
+    out_r, g_r = run_block(P, x, dout, dims, dev, torch.bfloat16, rank, scale)
+    monkeypatch.delenv("GDN_FORM")
+    errs = {"out": nerr(out_c, out_r)}
+    errs.update({n: nerr(g_c[n], g_r[n]) for n in g_c if not n.endswith("lora_a")})
+    print("  chunked vs recurrent", {n: f"{e:.1e}" for n, e in errs.items()}, flush=True)
+    for n, e in errs.items():
+        assert e <= 3e-2, (n, e)
+    print("  the first 256 tokens alone, and the float64 block oracle", flush=True)
+    out_p, _ = run_block(P, x[:, :256], dout[:, :256], dims, dev, torch.bfloat16, rank, scale)
+    want, _ = BO.block_forward(x[:, :256], P, Hk, Hv, D, D)
+    e_pre, e_orc = nerr(out_c[:, :256], out_p), nerr(out_p, want)
+    print(f"  prefix {e_pre:.1e}, oracle {e_orc:.1e}", flush=True)
+    assert e_pre <= 1e-2 and e_orc <= 3e-2
