@@ -52,7 +52,7 @@ def algo_model(w, form="chunk"):
     bf16 chunked form (bf16 q/k/v/dO/y/dq/dk/dv, fp32 gates and their gradients):
       bytes 2 * (4 Hk D + 4 Hv D) + 4 * 4 Hv  (= 49,664 B at Hk=16, Hv=32, D=128);
       flops per head-token: intra-chunk contractions 10 C D forward, x3 with the backward; state contractions
-      6 D^2 forward, x3 with the backward.  This build runs both on bf16 MFMA (the state operands are cast to
+      6 D^2 forward, x3 with the backward.  The chunked kernels run both on bf16 MFMA (the state operands are cast to
       bf16 hi / lo pairs), so both are priced at the bf16 dense peak.
     fp32 (recurrent arithmetic): bytes 4 * (4 Hk D + 4 Hv D + 4 Hv) (= 98,816 B); flops 27 D^2 per head-token
       (7 D^2 forward + 20 D^2 backward), priced at the fp32 peak.
@@ -256,7 +256,7 @@ def _oracle_group_run(args):
                               d["dy"][:, :, sl], None, chunk=64)
 
 
-def cpu_baseline(T_sample=256, T_parallel=1024, workers=None):
+def cpu_baseline(T_sample=1024, T_parallel=4096, workers=None):
     """The NumPy oracle (restating tools/gdn_vjp.py _forward + _backward, impl="staged"), fp32, chunk 64,
     B=1, Hk=16, Hv=32, D=128, on bounded samples:
       single core: the whole head set over T_sample tokens, median of 3 after one warm-up;
@@ -303,13 +303,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="bf16_b4_t4096", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=256)
+    ap.add_argument("--cpu-sample", type=int, default=1024)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (scales rocprof FETCH/WRITE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the GDN path here is "
-              "single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "single-GPU; across GPUs it would shard by (batch, key-head group), which needs no exchange)",
+              file=sys.stderr)
         sys.exit(2)
 
     cb = None

@@ -34,7 +34,7 @@ extern "C" {
 enum gdn_status {
     GDN_OK = 0,
     GDN_ERR_INVALID = -1,      /* bad shape, chunk, pointer or enum (reference: ValueError) */
-    GDN_ERR_UNSUPPORTED = -2,  /* valid request this build does not implement (e.g. Dk > 256) */
+    GDN_ERR_UNSUPPORTED = -2,  /* valid request the library does not implement (e.g. Dk > 256) */
     GDN_ERR_WORKSPACE = -3,    /* workspace smaller than gdn_bwd_workspace_bytes() */
     GDN_ERR_LAUNCH = -4        /* a HIP launch or runtime call failed */
 };
