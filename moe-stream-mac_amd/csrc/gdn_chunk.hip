@@ -942,6 +942,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             }
         }
     }
+    __syncthreads();  // sGam / sRc ready; phase 1's tiles read
     // the waves' parts of <dh', h> go to LDS now
     lastp = wave_sum(lastp * sGam[C - 1]);
     if (l == 0) sLast[w] = lastp;
@@ -949,7 +950,6 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) dQ[t][e] *= sGam[r0 + 4 * lg + e];
-    __syncthreads();
     // ---- phase 2: dK = diag(gamma_C/gamma) Delta dh'^T ; dP = lower(dY Delta^T) ; dA = -TdD Delta^T
     load_tile<D, D, NTB>(R1, LD, dHc, D, D, DT_F32, nullptr, tid);
     load_tile<C, D, NTB>(RX, LD, Dc, D, C, DT_F32, nullptr, tid);  // Delta in place of TdD (phase 1 is done)
