@@ -7,6 +7,7 @@
 #include <map>
 #include <mutex>
 #include <algorithm>
+#include <atomic>
 #include <string>
 #include <type_traits>
 #include <vector>
@@ -54,14 +55,14 @@ struct ProfRec {
 };
 static std::mutex g_prof_mu;
 static std::vector<ProfRec> g_prof;
-static bool g_prof_on = false;
+static std::atomic<bool> g_prof_on{false};  // read by every launch without the lock
 
 struct Timed {
     const char *name;
     hipStream_t st;
     hipEvent_t start = nullptr, stop = nullptr;
     Timed(const char *n, hipStream_t s) : name(n), st(s) {
-        if (!g_prof_on) return;
+        if (!g_prof_on.load(std::memory_order_relaxed)) return;
         if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess) {
             start = stop = nullptr;
             return;
@@ -280,8 +281,7 @@ extern "C" {
 int gdn_version(void) { return (2 << 16) | 0; }
 
 int gdn_profile_enable(int on) {
-    std::lock_guard<std::mutex> lk(g_prof_mu);
-    g_prof_on = on != 0;
+    g_prof_on.store(on != 0, std::memory_order_relaxed);
     return GDN_OK;
 }
 
