@@ -8,6 +8,7 @@ dv, dg, dbeta, dS0), with every input already resident in HBM.  Prints ONE JSON 
 
 Workloads (one GPU; the default is the T=4096 configuration the metric is quoted on):
   bf16_b4_t4096   B=4, T=4096, Hk=16, Hv=32, D=128, bf16 q/k/v/dO, fp32 state and gates, chunk 64
+  bf16_b1_t4096   B=1, T=4096, same heads, bf16 q/k/v/dO
   fp32_b1_t4096   B=1, T=4096, same heads, fp32
   fp32_b1_t2048   B=1, T=2048, fp32, S0 ~ N(0, 0.02), full dS0
   ckpt_b1_t16384  B=1, T=16384, fp32, snapshots every 256 tokens, peak HBM reported
@@ -149,6 +150,7 @@ def kernel_model(name, B, T, Hk, Hv, D, in_b):
 
 WORKLOADS = {
     "bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0),
+    "bf16_b1_t4096": dict(B=1, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0),
     "fp32_b1_t4096": dict(B=1, T=4096, Hk=16, Hv=32, D=128, dtype="fp32", chunk=64, s0_std=0.0),
     "fp32_b1_t2048": dict(B=1, T=2048, Hk=16, Hv=32, D=128, dtype="fp32", chunk=64, s0_std=0.02),
     "ckpt_b1_t16384": dict(B=1, T=16384, Hk=16, Hv=32, D=128, dtype="fp32", chunk=256, s0_std=0.0),
