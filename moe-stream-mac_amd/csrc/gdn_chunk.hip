@@ -1875,17 +1875,22 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
         const bfr *pb = a.w.Pb + ci * 2 * C * C + frag_off<C>(mrow, 0) + 8 * l;
         const bfr *kt = a.w.KTb + ci * D * C + frag_off<C>(16 * w, 0) + 8 * l;
         const bfr *qb = static_cast<const bfr *>(a.q) + (((size_t)b * a.Ts + t0 + r) * a.Hk + hk) * D + 8 * lg;
+        // W, Q and P only in the waves that form Delta and y (all of them when NTN >= 2; with 16-wide slices the
+        // other four waves only update their rows of h)
+        if (cwave) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            f.W[k] = ld_frag(wb + FRAG_BLOCK * k);
-            f.Q[k] = r < n ? ld_frag(qb + 32 * k) : zero_frag();
+            for (int k = 0; k < 4; ++k) {
+                f.W[k] = ld_frag(wb + FRAG_BLOCK * k);
+                f.Q[k] = r < n ? ld_frag(qb + 32 * k) : zero_frag();
+            }
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                f.P[k] = ld_frag(pb + FRAG_BLOCK * k);
+                f.P[2 + k] = ld_frag(pb + C * C + FRAG_BLOCK * k);
+            }
         }
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            f.P[k] = ld_frag(pb + FRAG_BLOCK * k);
-            f.P[2 + k] = ld_frag(pb + C * C + FRAG_BLOCK * k);
-            f.K[k] = ld_frag(kt + FRAG_BLOCK * k);
-        }
+        for (int k = 0; k < 2; ++k) f.K[k] = ld_frag(kt + FRAG_BLOCK * k);
         if (cwave) {
 #pragma unroll
             for (int t = 0; t < DN; ++t) {
@@ -2310,12 +2315,18 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
         const bfr *pt = a.w.PTb + ci * 2 * C * C + frag_off<C>(mrow, 0) + 8 * l;
         const bfr *qt = a.w.QTb + (((size_t)b * a.Hk + hk) * a.NC + c) * D * C + frag_off<C>(16 * w, 0) + 8 * l;
         const bfr *wt = a.w.nWTb + ci * D * C + frag_off<C>(16 * w, 0) + 8 * l;
+        // K and P^T only in the waves that form dDelta (all of them when NTN >= 2)
+        if (cwave) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) f.K[k] = r < n ? ld_frag(kb + 32 * k) : zero_frag();
+            for (int k = 0; k < 4; ++k) f.K[k] = r < n ? ld_frag(kb + 32 * k) : zero_frag();
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                f.PT[k] = ld_frag(pt + FRAG_BLOCK * k);
+                f.PT[2 + k] = ld_frag(pt + C * C + FRAG_BLOCK * k);
+            }
+        }
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            f.PT[k] = ld_frag(pt + FRAG_BLOCK * k);
-            f.PT[2 + k] = ld_frag(pt + C * C + FRAG_BLOCK * k);
             f.QT[k] = ld_frag(qt + FRAG_BLOCK * k);
             f.WT[k] = ld_frag(wt + FRAG_BLOCK * k);
         }
