@@ -1162,18 +1162,20 @@ __device__ __forceinline__ void mmab(f4 (&acc)[NTL], const bfr *ah, const bfr *a
                                      const bfr *bl, int ldb, int n0, int l = threadIdx.x & 63) {
 #pragma unroll 2
     for (int k0 = 0; k0 < K; k0 += 32) {
+        // every fragment of the k-step is read before its first product, so the LDS reads overlap
         const bf8 x = frag(ah, lda, m0, k0, l);
-        bf8 x2;
+        bf8 x2, y[NTL], y2[SB ? NTL : 1];
         if constexpr (SA) x2 = frag(al, lda, m0, k0, l);
 #pragma unroll
         for (int t = 0; t < NTL; ++t) {
-            const bf8 y = frag(bh, ldb, n0 + 16 * t, k0, l);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, acc[t], 0, 0, 0);
-            if constexpr (SA) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x2, y, acc[t], 0, 0, 0);
-            if constexpr (SB) {
-                const bf8 y2 = frag(bl, ldb, n0 + 16 * t, k0, l);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y2, acc[t], 0, 0, 0);
-            }
+            y[t] = frag(bh, ldb, n0 + 16 * t, k0, l);
+            if constexpr (SB) y2[t] = frag(bl, ldb, n0 + 16 * t, k0, l);
+        }
+#pragma unroll
+        for (int t = 0; t < NTL; ++t) {
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y[t], acc[t], 0, 0, 0);
+            if constexpr (SA) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x2, y[t], acc[t], 0, 0, 0);
+            if constexpr (SB) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y2[t], acc[t], 0, 0, 0);
         }
     }
 }
@@ -1819,15 +1821,18 @@ __device__ __forceinline__ void mmar(f4 (&acc)[NTL], const bf8 *ah, const bf8 *a
                                      int ldb, int n0) {
 #pragma unroll
     for (int k = 0; k < K / 32; ++k) {
+        // the k-step's LDS fragments are all read before its first product: one LDS round trip per k-step
+        bf8 y[NTL], y2[SB ? NTL : 1];
 #pragma unroll
         for (int t = 0; t < NTL; ++t) {
-            const bf8 y = frag(bh, ldb, n0 + 16 * t, 32 * k);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[k], y, acc[t], 0, 0, 0);
-            if constexpr (SA) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[k], y, acc[t], 0, 0, 0);
-            if constexpr (SB) {
-                const bf8 y2 = frag(bl, ldb, n0 + 16 * t, 32 * k);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[k], y2, acc[t], 0, 0, 0);
-            }
+            y[t] = frag(bh, ldb, n0 + 16 * t, 32 * k);
+            if constexpr (SB) y2[t] = frag(bl, ldb, n0 + 16 * t, 32 * k);
+        }
+#pragma unroll
+        for (int t = 0; t < NTL; ++t) {
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[k], y[t], acc[t], 0, 0, 0);
+            if constexpr (SA) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[k], y[t], acc[t], 0, 0, 0);
+            if constexpr (SB) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[k], y2[t], acc[t], 0, 0, 0);
         }
     }
 }
