@@ -329,6 +329,18 @@ __device__ __forceinline__ void conv_x(const void *x, const float *state_in, int
     }
 }
 
+// x at token t of the token loop (0 <= t; t >= tend reads as zero) without a branch: the load goes to a clamped
+// token and a select zeroes it, so the loads of several tokens stay in flight together.
+template <int V>
+__device__ __forceinline__ void conv_x_in(const void *x, int b, int t, int tend, int T, int C, int c0, int dt,
+                                          float (&o)[V]) {
+    const bool ok = t < tend;
+    float r[V];
+    loadv<V>(x, ((size_t)b * T + (ok ? t : tend - 1)) * C + c0, dt, r);
+#pragma unroll
+    for (int v = 0; v < V; ++v) o[v] = ok ? r[v] : 0.f;
+}
+
 // Where channel c0 of a token lives in the split q/k/v tensors: base pointer, row length, column; region 0/1/2.
 struct SplitPos {
     void *base;
@@ -340,8 +352,12 @@ __device__ __forceinline__ SplitPos split_pos(const ConvArgs &a, int c0) {
     return {a.v, a.C - 2 * a.qk, c0 - 2 * a.qk, 2};
 }
 
-template <int K, int V, int U, int L>
+// DT >= 0: x and q/k/v are all of that dtype, known at compile time (the loads and stores of the token loop then
+// carry no dtype branches, which would make the compiler wait for every load where the branches join); DT < 0:
+// the dtypes are read from the arguments.
+template <int K, int V, int U, int L, int DT>
 __global__ __launch_bounds__(NT) void conv_fwd_kernel(ConvArgs a) {
+    const int dt = DT >= 0 ? DT : a.dt;
     const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
     const int c0 = (blockIdx.x * 64 + lane) * V;
     const int t0 = (blockIdx.y * CONV_SLICES + slice) * CONV_TT, b = blockIdx.z;
@@ -357,12 +373,12 @@ __global__ __launch_bounds__(NT) void conv_fwd_kernel(ConvArgs a) {
 #pragma unroll
         for (int j = 0; j < K; ++j) wk[j][v] = a.w[(size_t)(cc + v) * K + j];
 #pragma unroll
-    for (int j = 0; j < K - 1; ++j) conv_x<K, V>(a.x, a.state_in, b, t0 - (K - 1) + j, T, C, cc, a.dt, hist[j]);
+    for (int j = 0; j < K - 1; ++j) conv_x<K, V>(a.x, a.state_in, b, t0 - (K - 1) + j, T, C, cc, dt, hist[j]);
     const int t1 = min(T, t0 + CONV_TT);
     for (int t = t0; t < t1; t += U) {
         float xs[U][V];
 #pragma unroll
-        for (int u = 0; u < U; ++u) conv_x<K, V>(a.x, nullptr, b, t + u < t1 ? t + u : T, T, C, cc, a.dt, xs[u]);
+        for (int u = 0; u < U; ++u) conv_x_in<V>(a.x, b, t + u, t1, T, C, cc, dt, xs[u]);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (t + u >= t1) break;
@@ -386,7 +402,7 @@ __global__ __launch_bounds__(NT) void conv_fwd_kernel(ConvArgs a) {
                     for (int v = 0; v < V; ++v) o[v] *= inv;
                 }
             }
-            if (active) storev<V>(sp.base, ((size_t)b * T + t + u) * sp.row + sp.col, a.dt, o);
+            if (active) storev<V>(sp.base, ((size_t)b * T + t + u) * sp.row + sp.col, dt, o);
         }
     }
 }
@@ -414,9 +430,10 @@ __global__ void conv_state_kernel(const void *x, const float *state_in, float *s
 // nothing to dw).  L2 norm backward per q/k head: dc = s/n (g - c (c.g)/n^2), n^2 = sum c^2 + eps.
 // dw partials of the workgroup (its 4 time slices summed in order) go to
 // part[(b * gridDim.y + blockIdx.y) * C*K + c*K + j].
-template <int K, int V, int U, int L>
+template <int K, int V, int U, int L, int DT>
 __global__ __launch_bounds__(NT) void conv_bwd_kernel(ConvArgs a) {
     __shared__ float red[CONV_SLICES][64 * V * K];
+    const int dt = DT >= 0 ? DT : a.dt, gdt = DT >= 0 ? DT : a.g_dt;
     const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
     const int c0 = (blockIdx.x * 64 + lane) * V;
     const int t0 = (blockIdx.y * CONV_SLICES + slice) * CONV_TT, b = blockIdx.z;
@@ -440,19 +457,18 @@ __global__ __launch_bounds__(NT) void conv_bwd_kernel(ConvArgs a) {
                 acc[j][v] = 0.f;
             }
 #pragma unroll
-        for (int j = 0; j < K - 1; ++j) conv_x<K, V>(a.x, a.state_in, b, t0 - (K - 1) + j, T, C, cc, a.dt, xw[j]);
+        for (int j = 0; j < K - 1; ++j) conv_x<K, V>(a.x, a.state_in, b, t0 - (K - 1) + j, T, C, cc, dt, xw[j]);
         const int t1 = min(T, t0 + CONV_TT), tend = min(T, t1 + K - 1);
         for (int t = t0; t < tend; t += U) {
             float xn[U][V], gn[U][V];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int tn = t + u < tend ? t + u : T;
-                conv_x<K, V>(a.x, nullptr, b, tn, T, C, cc, a.dt, xn[u]);
-                if (tn < T)
-                    loadv<V>(sp.base, ((size_t)b * T + tn) * sp.row + sp.col, a.g_dt, gn[u]);
-                else
+                conv_x_in<V>(a.x, b, t + u, tend, T, C, cc, dt, xn[u]);
+                const bool ok = t + u < tend;
+                float r[V];
+                loadv<V>(sp.base, ((size_t)b * T + (ok ? t + u : tend - 1)) * sp.row + sp.col, gdt, r);
 #pragma unroll
-                    for (int v = 0; v < V; ++v) gn[u][v] = 0.f;
+                for (int v = 0; v < V; ++v) gn[u][v] = ok ? r[v] : 0.f;
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -493,7 +509,7 @@ __global__ __launch_bounds__(NT) void conv_bwd_kernel(ConvArgs a) {
                     }
                 }
                 const int ts = t + u - (K - 1);  // its dx is now complete
-                if (active && ts >= t0 && ts < t1) storev<V>(a.dx, ((size_t)b * T + ts) * C + cc, a.dt, acc[0]);
+                if (active && ts >= t0 && ts < t1) storev<V>(a.dx, ((size_t)b * T + ts) * C + cc, dt, acc[0]);
 #pragma unroll
                 for (int v = 0; v < V; ++v) {
 #pragma unroll
@@ -509,7 +525,7 @@ __global__ __launch_bounds__(NT) void conv_bwd_kernel(ConvArgs a) {
 #pragma unroll
         for (int m = 0; m < K - 1; ++m) {
             const int ts = tend - (K - 1) + m;
-            if (active && ts >= t0 && ts < t1) storev<V>(a.dx, ((size_t)b * T + ts) * C + cc, a.dt, acc[m]);
+            if (active && ts >= t0 && ts < t1) storev<V>(a.dx, ((size_t)b * T + ts) * C + cc, dt, acc[m]);
         }
     }
 #pragma unroll
@@ -766,13 +782,23 @@ static int conv_lanes(int C, int dt, int g_dt, bool vec, bool bwd) {
     return (half && C % 8 == 0 && !bwd) ? 8 : 4;
 }
 
-template <int K, int V, int L>
-static void conv_launch(const ops::ConvArgs &a, int B, bool bwd, hipStream_t st) {
+template <int K, int V, int L, int DT>
+static void conv_launch_dt(const ops::ConvArgs &a, int B, bool bwd, hipStream_t st) {
     const dim3 grid = conv_grid(B, a.T, a.C, V);
     if (!bwd)
-        hipLaunchKernelGGL((ops::conv_fwd_kernel<K, V, 4, L>), grid, dim3(ops::NT), 0, st, a);
+        hipLaunchKernelGGL((ops::conv_fwd_kernel<K, V, 4, L, DT>), grid, dim3(ops::NT), 0, st, a);
     else if constexpr (V <= 4)  // conv_lanes never gives the backward 8 channels per lane
-        hipLaunchKernelGGL((ops::conv_bwd_kernel<K, V, 2, L>), grid, dim3(ops::NT), 0, st, a);
+        hipLaunchKernelGGL((ops::conv_bwd_kernel<K, V, 4, L, DT>), grid, dim3(ops::NT), 0, st, a);
+}
+
+// The vector paths with one dtype throughout (bf16 or fp32) run kernels with that dtype fixed at compile time.
+template <int K, int V, int L>
+static void conv_launch(const ops::ConvArgs &a, int B, bool bwd, hipStream_t st) {
+    if constexpr (V >= 4) {
+        if (a.dt == a.g_dt && a.dt == DT_BF16) return conv_launch_dt<K, V, L, DT_BF16>(a, B, bwd, st);
+        if (a.dt == a.g_dt && a.dt == DT_F32) return conv_launch_dt<K, V, L, DT_F32>(a, B, bwd, st);
+    }
+    conv_launch_dt<K, V, L, -1>(a, B, bwd, st);
 }
 
 template <int K>
