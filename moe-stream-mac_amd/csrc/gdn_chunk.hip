@@ -1423,6 +1423,7 @@ constexpr int NQR = 2;  // dq row pieces per thread whose running sum stays in r
 // in order (rr = 0, 1, ...) at the 16-byte row pieces each thread writes out: dk (ck) and the first NQR dq pieces
 // (cq) in registers, the other dq pieces in the part rows of the key head (each thread reading back only the
 // elements it wrote itself); the last value head writes dq and dk in the gradient dtype.
+template <bool DYF32>
 __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk, int b, int rr, int rep,
                                                     float4 (&ck)[4], float4 (&cq)[NQR]) {
     __shared__ __align__(16) unsigned char arena[ARENA];
@@ -1455,17 +1456,21 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
     const bfr *vsrc = static_cast<const bfr *>(a.v) + v0;
 
     // ---- S1 staging: gates; h, dh', Delta, TdD, dY, V.  Every global load of the phase is issued before the
-    // first LDS store.  dv = diag(beta) TdD leaves from the fp32 TdD loads, and rowsum(V * TdD) goes to sVT.
+    // first LDS store, the gates' too, and the dtype of dY is a template parameter: a gate stored to LDS before
+    // the tile loads, or a branch on the dtype among them, made the compiler wait for the loads in flight and split
+    // the phase's loads into serial batches.  dv = diag(beta) TdD leaves from the fp32 TdD loads, and
+    // rowsum(V * TdD) goes to sVT.
+    double gch = 0.0;
+    float bch = 0.f;
     if (tid < C) {
-        sG[tid] = a.w.G[ci * C + tid];
-        sB[tid] = tid < n ? a.beta[((size_t)b * a.Ts + t0 + tid) * a.Hv + hv] : 0.f;
+        gch = a.w.G[ci * C + tid];
+        bch = tid < n ? a.beta[((size_t)b * a.Ts + t0 + tid) * a.Hv + hv] : 0.f;
     }
     float lastp = 0.f;  // <dh', h>, the pair (C-1, chunk start)
     {
         constexpr int SPER = D * (D / 8) / NTB, NPER = C * (D / 8) / NTB;  // 8-element pieces per thread
         static_assert(SPER * NTB == D * (D / 8) && NPER * NTB == C * (D / 8), "even split");
-        const bool yf32 = a.dy_dt == DT_F32;
-        uint4 hr[SPER], dhr[SPER], dl[2 * NPER], td[2 * NPER], yr[2 * NPER], vr[NPER];
+        uint4 hr[SPER], dhr[SPER], dl[2 * NPER], td[2 * NPER], yr[DYF32 ? 2 * NPER : NPER], vr[NPER];
         float bt[NPER];
 #pragma unroll
         for (int p = 0; p < SPER; ++p) {
@@ -1481,7 +1486,7 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
             td[2 * p + 1] = *reinterpret_cast<const uint4 *>(TDc + r * D + c8 + 4);
             vr[p] = r < n ? *reinterpret_cast<const uint4 *>(vsrc + (size_t)r * v_row + c8) : make_uint4(0u, 0u, 0u, 0u);
             bt[p] = r < n ? a.beta[((size_t)b * a.Ts + t0 + r) * a.Hv + hv] : 0.f;
-            if (yf32) {
+            if constexpr (DYF32) {
                 const float *ys = static_cast<const float *>(a.dy) + v0 + (size_t)r * v_row + c8;
                 yr[2 * p] = r < n ? *reinterpret_cast<const uint4 *>(ys) : make_uint4(0u, 0u, 0u, 0u);
                 yr[2 * p + 1] = r < n ? *reinterpret_cast<const uint4 *>(ys + 4) : make_uint4(0u, 0u, 0u, 0u);
@@ -1489,6 +1494,10 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
                 yr[p] = r < n ? *reinterpret_cast<const uint4 *>(static_cast<const bfr *>(a.dy) + v0 + (size_t)r * v_row + c8)
                               : make_uint4(0u, 0u, 0u, 0u);
             }
+        }
+        if (tid < C) {
+            sG[tid] = gch;
+            sB[tid] = bch;
         }
         bfr *const th = T16(O_H), *const tdh = T16(O_DHH);
 #pragma unroll
@@ -1517,10 +1526,12 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
             const float tv[8] = {f(t0v.x), f(t0v.y), f(t0v.z), f(t0v.w), f(t1v.x), f(t1v.y), f(t1v.z), f(t1v.w)};
             *reinterpret_cast<uint4 *>(T16(O_TD) + r * LA + c8) =
                 make_uint4(pk(tv[0], tv[1]), pk(tv[2], tv[3]), pk(tv[4], tv[5]), pk(tv[6], tv[7]));
-            uint4 yv = yr[p];
-            if (yf32) {
+            uint4 yv;
+            if constexpr (DYF32) {
                 const uint4 y0 = yr[2 * p], y1 = yr[2 * p + 1];
                 yv = make_uint4(pk(f(y0.x), f(y0.y)), pk(f(y0.z), f(y0.w)), pk(f(y1.x), f(y1.y)), pk(f(y1.z), f(y1.w)));
+            } else {
+                yv = yr[p];
             }
             *reinterpret_cast<uint4 *>(T16(O_DY) + r * LA + c8) = yv;
             // rowsum(V * TdD): the 16 lanes of a DPP row hold one token's row
@@ -1793,6 +1804,7 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
 }
 
 // One workgroup of 8 waves per (chunk, key head), walking the key head's value heads in order.
+template <bool DYF32>
 __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     typedef const __attribute__((address_space(4))) Args *KArgs;  // the kernel arguments (constant memory)
     const int rep = a.Hv / a.Hk;
@@ -1802,7 +1814,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
         // the arguments are read anew for each value head instead of being held in scalar registers across it
         KArgs ap = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
         asm volatile("" : "+s"(ap));
-        bwd_local_bf16_head(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep, ck, cq);
+        bwd_local_bf16_head<DYF32>(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep, ck, cq);
     }
 }
 
@@ -2605,7 +2617,10 @@ static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) 
     if (stage[0] == 's') {
         seq_dispatch<MT>(a, st, false);
     } else if constexpr (MT == 1) {
-        hipLaunchKernelGGL(ck::ck_bwd_local_bf16_kernel, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
+        if (a.dy_dt == DT_F32)
+            hipLaunchKernelGGL(ck::ck_bwd_local_bf16_kernel<true>, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
+        else
+            hipLaunchKernelGGL(ck::ck_bwd_local_bf16_kernel<false>, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
     }
     else
         hipLaunchKernelGGL(ck::ck_bwd_local_kernel, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
