@@ -24,10 +24,28 @@ __device__ __forceinline__ float sigmoidf_(float x) {
 // softplus(t) = t > 20 ? t : log1p(exp(t))   (engine/include/gdn.h:23-24)
 __device__ __forceinline__ float softplus_(float t) { return t > 20.f ? t : log1pf(expf(t)); }
 
+// The value of lane l ^ 16 / l ^ 32 on gfx950's VALU lane swaps (no LDS round trip): permlane16_swap exchanges
+// the odd rows of its first operand with the even rows of its second, permlane32_swap the upper half of the first
+// with the lower half of the second; with both operands x, a lane's partner is in the half it did not keep.
+__device__ __forceinline__ float lane_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+// Sum over aligned groups of L lanes (every lane of the wave active); all lanes of a group get the same bits.
 template <int L>
 __device__ __forceinline__ float group_sum(float x) {
-#pragma unroll
-    for (int m = L / 2; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+    static_assert(L == 1 || L == 2 || L == 4 || L == 8 || L == 16 || L == 32 || L == 64, "L is a power of two");
+    if constexpr (L >= 2) x += dpp_mov<DPP_QUAD_1032>(x);
+    if constexpr (L >= 4) x += dpp_mov<DPP_QUAD_2301>(x);
+    if constexpr (L >= 8) x += dpp_mov<DPP_ROW_HALF_MIRROR>(x);
+    if constexpr (L >= 16) x += dpp_mov<DPP_ROW_MIRROR>(x);
+    if constexpr (L >= 32) x += lane_xor16(x);
+    if constexpr (L >= 64) x += lane_xor32(x);
     return x;
 }
 
