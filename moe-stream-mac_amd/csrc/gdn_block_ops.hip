@@ -24,18 +24,6 @@ __device__ __forceinline__ float sigmoidf_(float x) {
 // softplus(t) = t > 20 ? t : log1p(exp(t))   (engine/include/gdn.h:23-24)
 __device__ __forceinline__ float softplus_(float t) { return t > 20.f ? t : log1pf(expf(t)); }
 
-// The value of lane l ^ 16 / l ^ 32 on gfx950's VALU lane swaps (no LDS round trip): permlane16_swap exchanges
-// the odd rows of its first operand with the even rows of its second, permlane32_swap the upper half of the first
-// with the lower half of the second; with both operands x, a lane's partner is in the half it did not keep.
-__device__ __forceinline__ float lane_xor16(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
-}
-__device__ __forceinline__ float lane_xor32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
-}
-
 // Sum over aligned groups of L lanes (every lane of the wave active); all lanes of a group get the same bits.
 template <int L>
 __device__ __forceinline__ float group_sum(float x) {

@@ -883,7 +883,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             *reinterpret_cast<float4 *>(RX + r * LD + c4) = td[p];
             float vt = vv[p][0] * td[p].x + vv[p][1] * td[p].y + vv[p][2] * td[p].z + vv[p][3] * td[p].w;
             vt = row16_allreduce(vt);
-            vt += __shfl_xor(vt, 16, 64);
+            vt += lane_xor16(vt);
             if ((tid & 31) == 0) sVT[r] = vt;
             if (r < n) {
                 const float4 dv = make_float4(bt[p] * td[p].x, bt[p] * td[p].y, bt[p] * td[p].z, bt[p] * td[p].w);

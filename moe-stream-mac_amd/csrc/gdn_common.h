@@ -101,6 +101,16 @@ __device__ __forceinline__ double readlane_f64(double x, int lane) {
 // Lane i receives lane i - 1 of the wave (lane 0 receives 0): wave_shr:1.
 __device__ __forceinline__ float wave_shr1(float x) { return dpp_mov<0x138>(x); }
 
-__device__ __forceinline__ float shfl_xor(float x, int mask) { return __shfl_xor(x, mask, 64); }
+// The value of lane l ^ 16 / l ^ 32 on gfx950's VALU lane swaps (no LDS round trip): permlane16_swap exchanges
+// the odd rows of its first operand with the even rows of its second, permlane32_swap the upper half of the first
+// with the lower half of the second; with both operands x, a lane's partner is in the half it did not keep.
+__device__ __forceinline__ float lane_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
 
 }  // namespace gdn

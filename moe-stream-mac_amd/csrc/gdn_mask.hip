@@ -29,10 +29,11 @@ __global__ __launch_bounds__(256) void mask_gates_kernel(const float *g, const f
     beta2[i] = keep ? beta[i] : 0.f;
 }
 
+// Sum over the wave, the same bits in every lane: DPP row sums, then the lane swaps across rows and halves.
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
-    return x;
+    x = row16_allreduce(x);
+    x += lane_xor16(x);
+    return x + lane_xor32(x);
 }
 
 // Four consecutive elements (i % 4 == 0) of a tensor of dtype dt, as fp32 / from fp32.

@@ -337,7 +337,7 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
                     for (int e = 0; e < E; ++e) {
                         const float mine = h ? pk[e] : pq[e];
                         const float other = h ? pq[e] : pk[e];
-                        W[e] = mine + shfl_xor(other, 16);
+                        W[e] = mine + lane_xor16(other);
                     }
                     if constexpr (E >= 2) {
                         constexpr int H = E / 2;
@@ -346,17 +346,17 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
                         for (int e = 0; e < H; ++e) {
                             const float mine = h2 ? W[H + e] : W[e];
                             const float other = h2 ? W[e] : W[H + e];
-                            s_red[s][wave][h * DKP + c * E + h2 * H + e] = mine + shfl_xor(other, 32);
+                            s_red[s][wave][h * DKP + c * E + h2 * H + e] = mine + lane_xor32(other);
                         }
                     } else {
-                        const float x = W[0] + shfl_xor(W[0], 32);
+                        const float x = W[0] + lane_xor32(W[0]);
                         if ((gw >> 1) == 0) s_red[s][wave][h * DKP + c] = x;
                     }
                     if constexpr (VEC) {
 #pragma unroll
                         for (int e = 0; e < E; ++e) {
-                            float x = pg[e] + shfl_xor(pg[e], 16);
-                            x += shfl_xor(x, 32);
+                            float x = pg[e] + lane_xor16(pg[e]);
+                            x += lane_xor32(x);
                             if (gw == 0) s_red[s][wave][2 * DKP + c * E + e] = x;
                         }
                     }
