@@ -1396,7 +1396,7 @@ __device__ __forceinline__ void acc_N(const f4 &x, bfr *hi, bfr *lo, int ld, int
 //       the value index (Delta split; TdD as bf16, dv and rowsum(V * TdD) from its fp32 loads)
 //                                                                  TdD, h, dh', Delta hi / lo, dY
 //   S3  dQ += dPG K, dK += dPG^T Q (dPG split), K K^T               dPG, dPG^T, Q^T, K^T, K
-//   S6  dK += (M + M^T) K, M = diag(beta) dA * Gam                  M + M^T, K^T
+//   S6  dK += M K + M^T K, M = diag(beta) dA * Gam                   M, M^T, K^T
 // then the straddle sums for dg and the outputs, as in ck_bwd_local_kernel.
 constexpr int SZ_A = C * LA * 2;       // [64][136]  17408 B
 constexpr int SZ_B = D * LA * 2;       // [128][136] 34816 B
@@ -1410,11 +1410,11 @@ constexpr int O_DY = O_DLL + SZ_A;
 // S3: dPG, dPG^T (hi / lo), Q^T, K^T, K, then the waves' dq staging blocks
 constexpr int O_PNH = 0, O_PNL = O_PNH + SZ_D, O_PTH = O_PNL + SZ_D, O_PTL = O_PTH + SZ_D;
 constexpr int O_QT = O_PTL + SZ_D, O_KT = O_QT + SZ_C, O_K = O_KT + SZ_C, O_STQ = O_K + SZ_A;
-// S6: M + M^T (bf16) over the dead dPG tiles; the fp32 M, later the pair matrix E, over the dq staging
-constexpr int O_MM = 0, O_SM = O_STQ;
+// S6: M and M^T (bf16) over the dead dPG tiles; then the pair matrix E over the dq staging
+constexpr int O_MM = 0, O_MT = O_MM + SZ_D, O_SM = O_STQ;
 constexpr int ARENA = O_DY + SZ_A;
 static_assert(O_STQ + 8 * 16 * LQ * 4 <= ARENA, "dq staging fits");
-static_assert(O_SM + C * LDC * 4 <= ARENA && O_MM + SZ_D <= O_QT, "S6 tiles fit, clear of K^T");
+static_assert(O_SM + C * LDC * 4 <= ARENA && O_MT + SZ_D <= O_QT, "S6 tiles fit, clear of K^T");
 static_assert(C * (D + 4) * 4 <= O_KT, "dk staging below K^T and the pair matrix");
 
 constexpr int NQR = 2;  // dq row pieces per thread whose running sum stays in registers (of four)
@@ -1733,25 +1733,17 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
             Mt[t][e] = sB[r] * dav * gam;
         }
     __syncthreads();  // dPG, Q^T and the dq staging read (K^T stays)
-    // ---- S6: dK += (M + M^T) K
-    float *const sM = reinterpret_cast<float *>(arena + O_SM);  // [64][LDC] fp32
+    // ---- S6: dK += (M + M^T) K.  M is strictly lower triangular, so M and M^T never overlap: the bf16 tiles of M
+    // and of M^T, written from the accumulators in both orientations, are exactly the rounded M + M^T, and the two
+    // products (the second A operand in mmab's lo slot) replace a pairing pass over an fp32 copy of M
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sM[(r0 + 4 * lg + e) * LDC + 32 * ch + 16 * t + li] = Mt[t][e];
-    __syncthreads();
-    {
-        bfr *mm = T16(O_MM);
-        for (int i = tid; i < C * C / 2; i += NTB) {
-            const int r = i / (C / 2), s2 = (i - r * (C / 2)) * 2;
-            const float x0 = sM[r * LDC + s2] + sM[s2 * LDC + r];
-            const float x1 = sM[r * LDC + s2 + 1] + sM[(s2 + 1) * LDC + r];
-            *reinterpret_cast<uint32_t *>(mm + r * LB + s2) = pk(x0, x1);
-        }
+    for (int t = 0; t < 2; ++t) {
+        acc_N<false>(Mt[t], T16(O_MM), nullptr, LB, r0, 32 * ch + 16 * t, l);
+        acc_T<false>(Mt[t], T16(O_MT), nullptr, LB, r0, 32 * ch + 16 * t, l);
     }
     __syncthreads();
-    mmab<C, 4>(dK, T16(O_MM), nullptr, LB, r0, T16(O_KT), nullptr, LB, 64 * ch, l);
-    __syncthreads();  // sM, M + M^T and K^T read: the pair matrix E reuses sM, the dk staging the space below
+    mmab<C, 4, true>(dK, T16(O_MM), T16(O_MT), LB, r0, T16(O_KT), nullptr, LB, 64 * ch, l);
+    __syncthreads();  // M, M^T and K^T read: the pair matrix E takes the dq staging space, the dk staging the space below
     // dK staged as fp32 rows in the free arena for 16-byte stores
     float *const sp = reinterpret_cast<float *>(arena);
     constexpr int LP = D + 4, PER = C * D / 4 / NTB;
@@ -1761,7 +1753,7 @@ __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk
 #pragma unroll
         for (int e = 0; e < 4; ++e) sp[(r0 + 4 * lg + e) * LP + 64 * ch + 16 * t + li] = dK[t][e];
     // ---- straddle sums for dg, dbeta, outputs
-    float *const sE = sM;
+    float *const sE = reinterpret_cast<float *>(arena + O_SM);  // [64][LDC] fp32
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
