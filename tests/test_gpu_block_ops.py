@@ -168,16 +168,18 @@ def test_conv_fixture(dev):
     assert nerr(np_(out)[0], want.reshape(T, C)) <= 1e-5
 
 
+# fp16 runs the kernels that read the element dtype from their arguments (bf16 and fp32 have it fixed at compile
+# time)
 @pytest.mark.parametrize("C,K,T", [(8192, 4, 300), (64, 4, 6), (100, 4, 70), (256, 2, 513), (96, 3, 129),
                                    (64, 8, 200)])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_conv_fwd_bwd(dev, C, K, T, dtype):
     import gdn_block
     B = 2
     r = rng(C + K + T)
     x = r.standard_normal((B, T, C))
-    if dtype == torch.bfloat16:
-        x = torch.tensor(x).bfloat16().double().numpy()
+    if dtype != torch.float32:
+        x = torch.tensor(x).to(dtype).double().numpy()
     w = r.standard_normal((C, K)) * 0.5
     dout = r.standard_normal((B, T, C))
     print(f"conv C={C} K={K} T={T} {dtype}", flush=True)
@@ -327,15 +329,15 @@ def _conv_qkv_oracle(x, w, Hk, Dk, Hv, Dv, scale, dq, dk, dv, state=None):
 
 @pytest.mark.parametrize("Hk,Dk,Hv,Dv,T", [(2, 128, 4, 128, 150), (16, 128, 32, 128, 70), (3, 64, 6, 32, 65),
                                            (2, 256, 4, 64, 40), (2, 32, 2, 48, 33)])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_conv_qkv_fused(dev, Hk, Dk, Hv, Dv, T, dtype):
     import gdn_block
     B, K = 2, 4
     C = 2 * Hk * Dk + Hv * Dv
     r = rng(Hk * Dk + T)
     x = r.standard_normal((B, T, C))
-    if dtype == torch.bfloat16:
-        x = torch.tensor(x).bfloat16().double().numpy()
+    if dtype != torch.float32:
+        x = torch.tensor(x).to(dtype).double().numpy()
     w = r.standard_normal((C, K)) * 0.5
     dq, dk = r.standard_normal((B, T, Hk, Dk)), r.standard_normal((B, T, Hk, Dk))
     dv = r.standard_normal((B, T, Hv, Dv))
