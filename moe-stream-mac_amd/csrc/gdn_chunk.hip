@@ -378,7 +378,17 @@ __device__ __forceinline__ void unit_lower_inverse(const float *sA, float *sT, f
 
 constexpr int NTP = 512;  // ck_prep: 8 waves
 
+// The element dtypes of a launch of the fp32 kernel set: constants when AF32 (inputs, cotangent, outputs and
+// gradients all fp32), so that no load or store of a tile sits under a dtype branch (where the branches join, the
+// compiler waits for every load in flight); read from the arguments otherwise (fp16 inputs).
+#define DTYPES_OF(args)                                                                     \
+    const int k_in_dt = AF32 ? (int)DT_F32 : (args).in_dt, k_dy_dt = AF32 ? (int)DT_F32 : (args).dy_dt, \
+              k_out_dt = AF32 ? (int)DT_F32 : (args).out_dt, k_grad_dt = AF32 ? (int)DT_F32 : (args).grad_dt; \
+    (void)k_in_dt; (void)k_dy_dt; (void)k_out_dt; (void)k_grad_dt
+
+template <bool AF32>
 __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
+    DTYPES_OF(a);
     __shared__ __align__(16) float sK[C * LD];
     __shared__ __align__(16) float sX[C * LD];
     __shared__ __align__(16) float sA[C * LDC];
@@ -395,9 +405,9 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
     const size_t v0 = (((size_t)b * a.Ts + t0) * a.Hv + hv) * D, v_row = (size_t)a.Hv * D;
 
     TileRegs<C, D, NTP> rV;  // V is needed only after the inverse: fetch it now, store it later
-    tile_fetch(rV, elem_ptr(a.v, v0, a.in_dt), v_row, n, a.in_dt);
-    load_tile<C, D, NTP>(sK, LD, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
-    load_tile<C, D, NTP>(sX, LD, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
+    tile_fetch(rV, elem_ptr(a.v, v0, k_in_dt), v_row, n, k_in_dt);
+    load_tile<C, D, NTP>(sK, LD, elem_ptr(a.k, qk0, k_in_dt), qk_row, n, k_in_dt);
+    load_tile<C, D, NTP>(sX, LD, elem_ptr(a.q, qk0, k_in_dt), qk_row, n, k_in_dt);
     if (tid < C) {
         // inclusive prefix sum of the log decays in fp64 across wave 0
         float bt = 0.f, gl = 0.f;
@@ -439,7 +449,7 @@ __global__ __launch_bounds__(NTP) void ck_prep_kernel(Args a) {
     }
     {
         const float *bp = sB;
-        tile_store(sX, LD, rV, a.in_dt, [bp](int r) { return bp[r]; });
+        tile_store(sX, LD, rV, k_in_dt, [bp](int r) { return bp[r]; });
     }
     __syncthreads();
     // W = T diag(beta gamma) K (waves 0-3) and U = T diag(beta) V (waves 4-7), 16-row strips of 8 tiles
@@ -476,8 +486,9 @@ struct RcScale {
     __device__ float operator()(int r) const { return expf((float)(G[C - 1] - G[r])); }
 };
 
-template <int VS, int MODE>
+template <int VS, int MODE, bool AF32>
 __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
+    DTYPES_OF(a);
     constexpr bool kTiles = MODE != FWD_ONLY, kOut = MODE != FWD_RECOMPUTE;
     constexpr int LV = VS + 4;
     constexpr int NTN = VS / 16;                 // value tiles of the slice
@@ -518,7 +529,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
         const int n = min(C, T - c * C);
         tile_fetch(rW, a.w.W + ci * C * D, D, C, DT_F32);
         tile_fetch(rU, a.w.U + ci * C * D + i0, D, C, DT_F32);
-        tile_fetch(rQ, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
+        tile_fetch(rQ, elem_ptr(a.q, qk0, k_in_dt), qk_row, n, k_in_dt);
         if (tid < C) rG = a.w.G[ci * C + tid];
     };
     auto fetchB = [&](int c) {
@@ -526,7 +537,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
         const size_t qk0 = (((size_t)b * a.Ts + c * C) * a.Hk + hk) * D;
         const int n = min(C, T - c * C);
         tile_fetch(rP, a.w.P + ci * C * C, C, C, DT_F32);
-        tile_fetch(rK, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
+        tile_fetch(rK, elem_ptr(a.k, qk0, k_in_dt), qk_row, n, k_in_dt);
     };
     fetchA(cb);
     fetchB(cb);
@@ -541,7 +552,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
             for (int e = 0; e < 4; ++e) sH[(16 * w + 4 * lg + e) * LV + 16 * t + li] = h[t][e];
         tile_store(sW, LD, rW, DT_F32, NoScale{});
         tile_store(sU, LV, rU, DT_F32, NoScale{});
-        tile_store(sQ, LD, rQ, a.in_dt, NoScale{});
+        tile_store(sQ, LD, rQ, k_in_dt, NoScale{});
         if (tid < C) sG[tid] = rG;
         __syncthreads();
         if (c + 1 < ce) fetchA(c + 1);
@@ -565,7 +576,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
         }
         __syncthreads();
         tile_store(sW, LDC, rP, DT_F32, NoScale{});
-        tile_store(sQ, LD, rK, a.in_dt, RcScale{sG});
+        tile_store(sQ, LD, rK, k_in_dt, RcScale{sG});
         __syncthreads();
         if (c + 1 < ce) fetchB(c + 1);
         if (cwave && kOut) {
@@ -582,7 +593,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
                     const int r = mrow + 4 * lg + e, ii = 16 * (nt0 + t) + li;
                     if (r < n)
                         store_from_f32(a.y, (((size_t)b * a.Ts + t0 + r) * a.Hv + hv) * D + i0 + ii, yi[t][e],
-                                       a.out_dt);
+                                       k_out_dt);
                 }
         }
         // h = gamma_C h + Ktilde^T Delta
@@ -596,8 +607,9 @@ __global__ __launch_bounds__(NTS) void ck_fwd_kernel(Args a) {
 
 // ---------------------------------------------------------------------------------------------- ck_bwd_seq
 
-template <int VS>
+template <int VS, bool AF32>
 __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
+    DTYPES_OF(a);
     constexpr int LV = VS + 4;
     constexpr int NTN = VS / 16;
     constexpr int DN = NTN >= 2 ? NTN / 2 : 1;
@@ -639,8 +651,8 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
         const size_t v0 = (((size_t)b * a.Ts + c * C) * a.Hv + hv) * D;
         const int n = min(C, T - c * C);
         tile_fetch(rP, a.w.P + ci * C * C, C, C, DT_F32);
-        tile_fetch(rK, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt);
-        tile_fetch(rY, elem_ptr(a.dy, v0 + i0, a.dy_dt), v_row, n, a.dy_dt);
+        tile_fetch(rK, elem_ptr(a.k, qk0, k_in_dt), qk_row, n, k_in_dt);
+        tile_fetch(rY, elem_ptr(a.dy, v0 + i0, k_dy_dt), v_row, n, k_dy_dt);
         if (tid < C) rG = a.w.G[ci * C + tid];
     };
     auto fetchB = [&](int c) {
@@ -648,7 +660,7 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
         const size_t qk0 = (((size_t)b * a.Ts + c * C) * a.Hk + hk) * D;
         const int n = min(C, T - c * C);
         tile_fetch(rW, a.w.W + ci * C * D, D, C, DT_F32);
-        tile_fetch(rQ, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt);
+        tile_fetch(rQ, elem_ptr(a.q, qk0, k_in_dt), qk_row, n, k_in_dt);
         tile_fetch(rT, a.w.T + ci * C * C, C, C, DT_F32);
     };
     fetchA(a.NC - 1);
@@ -661,11 +673,11 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) sH[(16 * w + 4 * lg + e) * LV + 16 * t + li] = dh[t][e];
         tile_store(sW, LDC, rP, DT_F32, NoScale{});
-        tile_store(sQ, LD, rK, a.in_dt, NoScale{});
-        tile_store(sY, LV, rY, a.dy_dt, NoScale{});
+        tile_store(sQ, LD, rK, k_in_dt, NoScale{});
+        tile_store(sY, LV, rY, k_dy_dt, NoScale{});
         if (tid < C) sG[tid] = rG;
         __syncthreads();
-        tile_store(sYg, LV, rY, a.dy_dt, GamScale{sG});   // before rY is refilled
+        tile_store(sYg, LV, rY, k_dy_dt, GamScale{sG});   // before rY is refilled
         if (c > 0) fetchA(c - 1);
         store_state_slice<VS, LV, NTS>(a.w.dH + ci * D * D, sH, i0);
         // dDelta = diag(gamma_C / gamma) K dh' + P^T dY
@@ -685,7 +697,7 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_kernel(Args a) {
         }
         __syncthreads();
         tile_store(sW, LD, rW, DT_F32, NoScale{});
-        tile_store(sQ, LD, rQ, a.in_dt, NoScale{});
+        tile_store(sQ, LD, rQ, k_in_dt, NoScale{});
         tile_store(sT, LDC, rT, DT_F32, NoScale{});  // over dh', read before the barrier above
         __syncthreads();
         if (c > 0) fetchB(c - 1);
@@ -824,7 +836,9 @@ constexpr int NTB = 512;  // ck_bwd_local: 8 waves; waves w and w+4 share the 16
 // and the last value head writes dq and dk in the gradient dtype.  T and dDelta enter only through TdD = T^T dDelta
 // (saved by ck_bwd_seq_kernel): dv = diag(beta) TdD, dK -= diag(beta gamma) Y2 (Y2 = TdD h^T), dA = -TdD Delta^T
 // below the diagonal, dbeta += rowsum(V * TdD) - gamma s4 and dG -= beta gamma s4 (s4 = rowsum(K * Y2)).
+template <bool AF32>
 __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk, int b, int rr, int rep) {
+    DTYPES_OF(a);
     __shared__ __align__(16) float R1[D * LD];       // h, then dh' ([j][i]); then K at R1, Q at R1 + C*LD
     __shared__ __align__(16) float R2[C * LD];       // dY, then the pair matrix E
     __shared__ __align__(16) float RX[2 * C * LDC];  // TdD, then Delta ([C][LD] fits); R4 = RX + C*LDC: dPG, M
@@ -863,7 +877,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
         sB[tid] = bt;
     }
     load_tile<D, D, NTB>(R1, LD, Hc, D, D, DT_F32, nullptr, tid);
-    load_tile<C, D, NTB>(R2, LD, elem_ptr(a.dy, v0, a.dy_dt), v_row, n, a.dy_dt, nullptr, tid);
+    load_tile<C, D, NTB>(R2, LD, elem_ptr(a.dy, v0, k_dy_dt), v_row, n, k_dy_dt, nullptr, tid);
     {
         constexpr int PER = C * D / 4 / NTB;  // float4 pieces per thread; 32 consecutive threads hold one row
         static_assert(PER * NTB * 4 == C * D && (D / 4) == 32, "even split, half a wave per row");
@@ -875,7 +889,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             td[p] = *reinterpret_cast<const float4 *>(TDc + r * D + c4);
             bt[p] = r < n ? a.beta[((size_t)b * a.Ts + t0 + r) * a.Hv + hv] : 0.f;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) vv[p][q] = r < n ? load_as_f32(a.v, v0 + (size_t)r * v_row + c4 + q, a.in_dt) : 0.f;
+            for (int q = 0; q < 4; ++q) vv[p][q] = r < n ? load_as_f32(a.v, v0 + (size_t)r * v_row + c4 + q, k_in_dt) : 0.f;
         }
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
@@ -888,13 +902,13 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             if (r < n) {
                 const float4 dv = make_float4(bt[p] * td[p].x, bt[p] * td[p].y, bt[p] * td[p].z, bt[p] * td[p].w);
                 const size_t o = v0 + (size_t)r * v_row + c4;
-                if (a.grad_dt == DT_F32) {
+                if (k_grad_dt == DT_F32) {
                     *reinterpret_cast<float4 *>(static_cast<float *>(a.dv) + o) = dv;
                 } else {
-                    store_from_f32(a.dv, o, dv.x, a.grad_dt);
-                    store_from_f32(a.dv, o + 1, dv.y, a.grad_dt);
-                    store_from_f32(a.dv, o + 2, dv.z, a.grad_dt);
-                    store_from_f32(a.dv, o + 3, dv.w, a.grad_dt);
+                    store_from_f32(a.dv, o, dv.x, k_grad_dt);
+                    store_from_f32(a.dv, o + 1, dv.y, k_grad_dt);
+                    store_from_f32(a.dv, o + 2, dv.z, k_grad_dt);
+                    store_from_f32(a.dv, o + 3, dv.w, k_grad_dt);
                 }
             }
         }
@@ -984,8 +998,8 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
     }
     __syncthreads();
     // ---- phase 3: dQ += dPG K ; dK += dPG^T Q ; K K^T
-    load_tile<C, D, NTB>(sKm, LD, elem_ptr(a.k, qk0, a.in_dt), qk_row, n, a.in_dt, nullptr, tid);
-    load_tile<C, D, NTB>(sQm, LD, elem_ptr(a.q, qk0, a.in_dt), qk_row, n, a.in_dt, nullptr, tid);
+    load_tile<C, D, NTB>(sKm, LD, elem_ptr(a.k, qk0, k_in_dt), qk_row, n, k_in_dt, nullptr, tid);
+    load_tile<C, D, NTB>(sQm, LD, elem_ptr(a.q, qk0, k_in_dt), qk_row, n, k_in_dt, nullptr, tid);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -1087,13 +1101,13 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             const size_t o = qk_out + (size_t)r * a.Hk * D + c4;
             if (!last) {
                 *reinterpret_cast<float4 *>(sum_row + (size_t)r * park_row + half * D + c4) = v;
-            } else if (a.grad_dt == DT_F32) {
+            } else if (k_grad_dt == DT_F32) {
                 *reinterpret_cast<float4 *>(static_cast<float *>(dst) + o) = v;
             } else {
-                store_from_f32(dst, o, v.x, a.grad_dt);
-                store_from_f32(dst, o + 1, v.y, a.grad_dt);
-                store_from_f32(dst, o + 2, v.z, a.grad_dt);
-                store_from_f32(dst, o + 3, v.w, a.grad_dt);
+                store_from_f32(dst, o, v.x, k_grad_dt);
+                store_from_f32(dst, o + 1, v.y, k_grad_dt);
+                store_from_f32(dst, o + 2, v.z, k_grad_dt);
+                store_from_f32(dst, o + 3, v.w, k_grad_dt);
             }
         }
     };
@@ -1103,6 +1117,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
 }
 
 // One workgroup of 8 waves per (chunk, key head), walking the key head's value heads in order.
+template <bool AF32>
 __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
     typedef const __attribute__((address_space(4))) Args *KArgs;  // the kernel arguments (constant memory)
     const int rep = a.Hv / a.Hk;
@@ -1110,7 +1125,7 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_kernel(Args a) {
         // the arguments are read anew for each value head instead of being held in scalar registers across it
         KArgs ap = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
         asm volatile("" : "+s"(ap));
-        bwd_local_f32_head(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep);
+        bwd_local_f32_head<AF32>(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep);
     }
 }
 
@@ -2564,10 +2579,16 @@ static int slice_width(int heads) { return heads >= 128 ? 64 : heads >= 64 ? 32 
 // Workgroups along grid.z of the sequential kernels: the sequences, times the windows when they run side by side.
 static int seq_z(const ck::Args &a) { return a.recompute ? a.B * ((a.NC + a.wc - 1) / a.wc) : a.B; }
 
+// fp32 throughout: the fp32 set's kernels with the dtypes fixed at compile time
+static bool all_f32(const ck::Args &a) {
+    return a.in_dt == DT_F32 && a.dy_dt == DT_F32 && a.out_dt == DT_F32 && a.grad_dt == DT_F32;
+}
+
 template <int MT, int VS, int MODE>
 static void fwd_launch(const ck::Args &a, hipStream_t st, dim3 grid) {
     if constexpr (MT == 1) hipLaunchKernelGGL((ck::ck_fwd_bf16_kernel<VS, MODE>), grid, dim3(ck::NTS), 0, st, a);
-    else hipLaunchKernelGGL((ck::ck_fwd_kernel<VS, MODE>), grid, dim3(ck::NTS), 0, st, a);
+    else if (all_f32(a)) hipLaunchKernelGGL((ck::ck_fwd_kernel<VS, MODE, true>), grid, dim3(ck::NTS), 0, st, a);
+    else hipLaunchKernelGGL((ck::ck_fwd_kernel<VS, MODE, false>), grid, dim3(ck::NTS), 0, st, a);
 }
 
 template <int MT, int VS>
@@ -2581,7 +2602,8 @@ static void seq_launch(const ck::Args &a, hipStream_t st, bool fwd) {
         if (a.dy_dt == DT_F32) hipLaunchKernelGGL((ck::ck_bwd_seq_bf16_kernel<VS, true>), grid, dim3(ck::NTS), 0, st, a);
         else hipLaunchKernelGGL((ck::ck_bwd_seq_bf16_kernel<VS, false>), grid, dim3(ck::NTS), 0, st, a);
     } else {
-        hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<VS>), grid, dim3(ck::NTS), 0, st, a);
+        if (all_f32(a)) hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<VS, true>), grid, dim3(ck::NTS), 0, st, a);
+        else hipLaunchKernelGGL((ck::ck_bwd_seq_kernel<VS, false>), grid, dim3(ck::NTS), 0, st, a);
     }
 }
 
@@ -2598,8 +2620,10 @@ template <int MT>
 static void ck_fwd_launch(const ck::Args &a, hipStream_t st, const char *stage) {
     if (stage[0] == 'p' && MT == 1)
         hipLaunchKernelGGL(ck::ck_prep_bf16_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTP), 0, st, a);
+    else if (stage[0] == 'p' && all_f32(a))
+        hipLaunchKernelGGL(ck::ck_prep_kernel<true>, dim3(a.NC, a.Hv, a.B), dim3(ck::NTP), 0, st, a);
     else if (stage[0] == 'p')
-        hipLaunchKernelGGL(ck::ck_prep_kernel, dim3(a.NC, a.Hv, a.B), dim3(ck::NTP), 0, st, a);
+        hipLaunchKernelGGL(ck::ck_prep_kernel<false>, dim3(a.NC, a.Hv, a.B), dim3(ck::NTP), 0, st, a);
     else
         seq_dispatch<MT>(a, st, true);
 }
@@ -2614,8 +2638,10 @@ static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) 
         else
             hipLaunchKernelGGL(ck::ck_bwd_local_bf16_kernel<false>, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
     }
+    else if (all_f32(a))
+        hipLaunchKernelGGL(ck::ck_bwd_local_kernel<true>, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
     else
-        hipLaunchKernelGGL(ck::ck_bwd_local_kernel, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
+        hipLaunchKernelGGL(ck::ck_bwd_local_kernel<false>, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
 }
 
 static int mma_kind(int in_dt) { return in_dt == DT_BF16 ? 1 : 0; }
