@@ -85,6 +85,85 @@ __device__ __forceinline__ void stage_tokens(StageBuf<E, VEC, TT> &sb, const voi
     }
 }
 
+// One thread's share of a stage of TT tokens, in registers: stage_fetch issues every load of the stage at once,
+// stage_store moves them to LDS.  The loads take clamped indices (a token past T reads token T - 1, a channel or
+// row past Dk / Dv the last one) and sit under no branch, and the dtypes are template parameters: loads under a
+// branch or a dtype switch made the compiler wait for each one where the branches joined, so a stage's loads came
+// in one after another.  stage_store zeroes what lies past the tokens, channels and rows (decay 1), as
+// stage_tokens does.
+template <int E, bool VEC, int TT, bool WITH_DY>
+struct TokRegs {
+    static constexpr int DKP = 16 * E;
+    static constexpr int NKQ = (TT * DKP + THREADS - 1) / THREADS;
+    static constexpr int NV = (TT * ROWS + THREADS - 1) / THREADS;
+    float k[NKQ], q[NKQ], g[VEC ? NKQ : 1], v[NV], dy[WITH_DY ? NV : 1];
+    float bt, gt, mt;
+};
+
+template <int E, bool VEC, int TT, bool WITH_DY, int DT, int DYT>
+__device__ __forceinline__ void stage_fetch(TokRegs<E, VEC, TT, WITH_DY> &r, const void *q, const void *k,
+                                            const void *v, const float *g, const float *beta, const uint8_t *mask,
+                                            const void *dy, int b, int hv, int hk, int rb, int t0, int T, int Hk,
+                                            int Hv, int Dk, int Dv) {
+    using R = TokRegs<E, VEC, TT, WITH_DY>;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int p = 0; p < R::NKQ; ++p) {
+        const int i = tid + p * THREADS, tt = i / R::DKP, j = i - tt * R::DKP;
+        const int t = min(t0 + tt, T - 1), jc = min(j, Dk - 1);
+        const size_t idx = (((size_t)b * T + t) * Hk + hk) * Dk + jc;
+        r.k[p] = load_as_f32(k, idx, DT);
+        r.q[p] = load_as_f32(q, idx, DT);
+        if constexpr (VEC) r.g[p] = g[(((size_t)b * T + t) * Hv + hv) * Dk + jc];
+    }
+#pragma unroll
+    for (int p = 0; p < R::NV; ++p) {
+        const int i = tid + p * THREADS, tt = i / ROWS, rr = rb * ROWS + (i - tt * ROWS);
+        const size_t idx = (((size_t)b * T + min(t0 + tt, T - 1)) * Hv + hv) * Dv + min(rr, Dv - 1);
+        r.v[p] = load_as_f32(v, idx, DT);
+        if constexpr (WITH_DY) r.dy[p] = load_as_f32(dy, idx, DYT);
+    }
+    const int t = min(t0 + tid % TT, T - 1);
+    const size_t gi = ((size_t)b * T + t) * Hv + hv;
+    r.bt = beta[gi];
+    if constexpr (!VEC) r.gt = g[gi];
+    // without a mask, a byte of beta is read in its place (and ignored): no branch around the load
+    const uint8_t *mp = mask ? mask + (size_t)b * T + t : reinterpret_cast<const uint8_t *>(beta + gi);
+    r.mt = *mp ? 1.f : 0.f;
+}
+
+template <int E, bool VEC, int TT, bool WITH_DY>
+__device__ __forceinline__ void stage_store(StageBuf<E, VEC, TT> &sb, const TokRegs<E, VEC, TT, WITH_DY> &r,
+                                            bool masked, int n, int Dk, int Dv, int rb, int gate) {
+    using R = TokRegs<E, VEC, TT, WITH_DY>;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int p = 0; p < R::NKQ; ++p) {
+        const int i = tid + p * THREADS, tt = i / R::DKP, j = i - tt * R::DKP;
+        if (i < TT * R::DKP) {
+            const bool ok = tt < n && j < Dk;
+            sb.k[tt][j] = ok ? r.k[p] : 0.f;
+            sb.q[tt][j] = ok ? r.q[p] : 0.f;
+            if constexpr (VEC) sb.g[tt][j] = ok ? r.g[p] : 1.f;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < R::NV; ++p) {
+        const int i = tid + p * THREADS, tt = i / ROWS, rl = i - tt * ROWS;
+        if (i < TT * ROWS) {
+            const bool ok = tt < n && rb * ROWS + rl < Dv;
+            sb.v[tt][rl] = ok ? r.v[p] : 0.f;
+            if constexpr (WITH_DY) sb.dy[tt][rl] = ok ? r.dy[p] : 0.f;
+        }
+    }
+    if (tid < TT) {
+        const bool ok = tid < n;
+        sb.beta[tid] = ok ? r.bt : 0.f;
+        if constexpr (!VEC) sb.g[tid][0] = ok ? (gate == GATE_LOG ? expf(r.gt) : r.gt) : 1.f;
+        sb.m[tid] = ok && masked ? r.mt : 1.f;
+    }
+}
+
 template <int E>
 __device__ __forceinline__ void lds_vec(float (&dst)[E], const float *src) {
     if constexpr (E % 4 == 0) {
@@ -130,7 +209,7 @@ __device__ __forceinline__ float row_step(const StageBuf<E, VEC, TT> &sb, int tt
 
 // ---------------------------------------------------------------------------------------------------- forward
 
-template <int E, bool VEC>
+template <int E, bool VEC, int DT>
 __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
     __shared__ __align__(16) StageBuf<E, VEC, FWD_TT> sb;
     __shared__ float s_y[FWD_TT][ROWS];
@@ -151,12 +230,17 @@ __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
         S[e] = (a.state0 && row_ok && j < Dk) ? a.state0[row_off + j] : 0.f;
     }
     int until_snap = a.chunk;  // tokens left before the next chunk boundary
+    // the next stage's tokens are loaded into registers while this one computes
+    TokRegs<E, VEC, FWD_TT, false> tr;
+    stage_fetch<E, VEC, FWD_TT, false, DT, DT>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb, 0, T,
+                                               a.Hk, a.Hv, Dk, Dv);
     for (int t0 = 0; t0 < T; t0 += FWD_TT) {
         const int n = min(FWD_TT, T - t0);
         __syncthreads();
-        stage_tokens<E, VEC, FWD_TT, false>(sb, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb,
-                                            t0, n, T, a.Hk, a.Hv, Dk, Dv, a.in_dt, 0, a.gate);
+        stage_store<E, VEC, FWD_TT, false>(sb, tr, a.mask != nullptr, n, Dk, Dv, rb, a.gate);
         __syncthreads();
+        stage_fetch<E, VEC, FWD_TT, false, DT, DT>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb,
+                                                   t0 + FWD_TT, T, a.Hk, a.Hv, Dk, Dv);
         for (int tt = 0; tt < n; ++tt) {
             float cand[E], kk[E], qq[E], delta;
             row_step<E, VEC, FWD_TT>(sb, tt, grp, c, S, cand, kk, delta);
@@ -476,13 +560,20 @@ size_t rec_sub_floats(int B, int Hv, int Dk, int Dv, int T, int chunk) {
     return (size_t)B * Hv * rec_num_row_blocks(Dv) * rec_max_sub(T, chunk) * ROWS * 16 * E;
 }
 
-template <int E>
-static void launch_fwd_e(const RecFwdArgs &a, hipStream_t st) {
+template <int E, int DT>
+static void launch_fwd_et(const RecFwdArgs &a, hipStream_t st) {
     dim3 grid(rec_num_row_blocks(a.Dv), a.Hv, a.B);
     if (a.gate == GATE_DECAY_VEC)
-        hipLaunchKernelGGL((rec_fwd_kernel<E, true>), grid, dim3(THREADS), 0, st, a);
+        hipLaunchKernelGGL((rec_fwd_kernel<E, true, DT>), grid, dim3(THREADS), 0, st, a);
     else
-        hipLaunchKernelGGL((rec_fwd_kernel<E, false>), grid, dim3(THREADS), 0, st, a);
+        hipLaunchKernelGGL((rec_fwd_kernel<E, false, DT>), grid, dim3(THREADS), 0, st, a);
+}
+
+template <int E>
+static void launch_fwd_e(const RecFwdArgs &a, hipStream_t st) {
+    if (a.in_dt == DT_BF16) launch_fwd_et<E, DT_BF16>(a, st);
+    else if (a.in_dt == DT_F16) launch_fwd_et<E, DT_F16>(a, st);
+    else launch_fwd_et<E, DT_F32>(a, st);
 }
 
 void launch_rec_fwd(const RecFwdArgs &a, hipStream_t st) {
