@@ -33,64 +33,12 @@ struct StageBuf {
     float m[TT];
 };
 
-// Stage tokens [t0, t0+n) of head (b, hv), rows [rb*16, rb*16+16) into LDS as fp32.  Slots past n and
-// channels past Dk are zero (decay 1), so padded lanes carry exact zeros through every step.
-template <int E, bool VEC, int TT, bool WITH_DY>
-__device__ __forceinline__ void stage_tokens(StageBuf<E, VEC, TT> &sb, const void *q, const void *k,
-                                             const void *v, const float *g, const float *beta,
-                                             const uint8_t *mask, const void *dy, int b, int hv, int hk,
-                                             int rb, int t0, int n, int T, int Hk, int Hv, int Dk, int Dv,
-                                             int in_dt, int dy_dt, int gate) {
-    constexpr int DKP = 16 * E;
-    const int tid = threadIdx.x;
-    for (int i = tid; i < TT * DKP; i += THREADS) {
-        const int tt = i / DKP, j = i - tt * DKP;
-        float kv = 0.f, qv = 0.f, gv = 1.f;
-        if (tt < n && j < Dk) {
-            const size_t idx = (((size_t)b * T + t0 + tt) * Hk + hk) * Dk + j;
-            kv = load_as_f32(k, idx, in_dt);
-            qv = load_as_f32(q, idx, in_dt);
-            if (VEC) gv = g[(((size_t)b * T + t0 + tt) * Hv + hv) * Dk + j];
-        }
-        sb.k[tt][j] = kv;
-        sb.q[tt][j] = qv;
-        if (VEC) sb.g[tt][j] = gv;
-    }
-    for (int i = tid; i < TT * ROWS; i += THREADS) {
-        const int tt = i / ROWS, r = i - tt * ROWS, rr = rb * ROWS + r;
-        float vv = 0.f, dd = 0.f;
-        if (tt < n && rr < Dv) {
-            const size_t idx = (((size_t)b * T + t0 + tt) * Hv + hv) * Dv + rr;
-            vv = load_as_f32(v, idx, in_dt);
-            if (WITH_DY) dd = load_as_f32(dy, idx, dy_dt);
-        }
-        sb.v[tt][r] = vv;
-        if (WITH_DY) sb.dy[tt][r] = dd;
-    }
-    if (tid < TT) {
-        const int tt = tid;
-        float bt = 0.f, gt = 1.f, mt = 1.f;
-        if (tt < n) {
-            const size_t gi = ((size_t)b * T + t0 + tt) * Hv + hv;
-            bt = beta[gi];
-            if (!VEC) {
-                gt = g[gi];
-                if (gate == GATE_LOG) gt = expf(gt);
-            }
-            if (mask) mt = mask[(size_t)b * T + t0 + tt] ? 1.f : 0.f;
-        }
-        sb.beta[tt] = bt;
-        if (!VEC) sb.g[tt][0] = gt;
-        sb.m[tt] = mt;
-    }
-}
-
 // One thread's share of a stage of TT tokens, in registers: stage_fetch issues every load of the stage at once,
 // stage_store moves them to LDS.  The loads take clamped indices (a token past T reads token T - 1, a channel or
 // row past Dk / Dv the last one) and sit under no branch, and the dtypes are template parameters: loads under a
 // branch or a dtype switch made the compiler wait for each one where the branches joined, so a stage's loads came
-// in one after another.  stage_store zeroes what lies past the tokens, channels and rows (decay 1), as
-// stage_tokens does.
+// in one after another.  stage_store zeroes what lies past the tokens, channels and rows (decay 1), so padded
+// lanes carry exact zeros through every step.
 template <int E, bool VEC, int TT, bool WITH_DY>
 struct TokRegs {
     static constexpr int DKP = 16 * E;
@@ -104,24 +52,25 @@ template <int E, bool VEC, int TT, bool WITH_DY, int DT, int DYT>
 __device__ __forceinline__ void stage_fetch(TokRegs<E, VEC, TT, WITH_DY> &r, const void *q, const void *k,
                                             const void *v, const float *g, const float *beta, const uint8_t *mask,
                                             const void *dy, int b, int hv, int hk, int rb, int t0, int T, int Hk,
-                                            int Hv, int Dk, int Dv) {
+                                            int Hv, int Dk, int Dv, int in_dt, int dy_dt) {
     using R = TokRegs<E, VEC, TT, WITH_DY>;
     const int tid = threadIdx.x;
+    const int xdt = DT >= 0 ? DT : in_dt, ydt = DYT >= 0 ? DYT : dy_dt;  // DT < 0: read from the arguments
 #pragma unroll
     for (int p = 0; p < R::NKQ; ++p) {
         const int i = tid + p * THREADS, tt = i / R::DKP, j = i - tt * R::DKP;
         const int t = min(t0 + tt, T - 1), jc = min(j, Dk - 1);
         const size_t idx = (((size_t)b * T + t) * Hk + hk) * Dk + jc;
-        r.k[p] = load_as_f32(k, idx, DT);
-        r.q[p] = load_as_f32(q, idx, DT);
+        r.k[p] = load_as_f32(k, idx, xdt);
+        r.q[p] = load_as_f32(q, idx, xdt);
         if constexpr (VEC) r.g[p] = g[(((size_t)b * T + t) * Hv + hv) * Dk + jc];
     }
 #pragma unroll
     for (int p = 0; p < R::NV; ++p) {
         const int i = tid + p * THREADS, tt = i / ROWS, rr = rb * ROWS + (i - tt * ROWS);
         const size_t idx = (((size_t)b * T + min(t0 + tt, T - 1)) * Hv + hv) * Dv + min(rr, Dv - 1);
-        r.v[p] = load_as_f32(v, idx, DT);
-        if constexpr (WITH_DY) r.dy[p] = load_as_f32(dy, idx, DYT);
+        r.v[p] = load_as_f32(v, idx, xdt);
+        if constexpr (WITH_DY) r.dy[p] = load_as_f32(dy, idx, ydt);
     }
     const int t = min(t0 + tid % TT, T - 1);
     const size_t gi = ((size_t)b * T + t) * Hv + hv;
@@ -233,14 +182,14 @@ __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
     // the next stage's tokens are loaded into registers while this one computes
     TokRegs<E, VEC, FWD_TT, false> tr;
     stage_fetch<E, VEC, FWD_TT, false, DT, DT>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb, 0, T,
-                                               a.Hk, a.Hv, Dk, Dv);
+                                               a.Hk, a.Hv, Dk, Dv, a.in_dt, 0);
     for (int t0 = 0; t0 < T; t0 += FWD_TT) {
         const int n = min(FWD_TT, T - t0);
         __syncthreads();
         stage_store<E, VEC, FWD_TT, false>(sb, tr, a.mask != nullptr, n, Dk, Dv, rb, a.gate);
         __syncthreads();
         stage_fetch<E, VEC, FWD_TT, false, DT, DT>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb,
-                                                   t0 + FWD_TT, T, a.Hk, a.Hv, Dk, Dv);
+                                                   t0 + FWD_TT, T, a.Hk, a.Hv, Dk, Dv, a.in_dt, 0);
         for (int tt = 0; tt < n; ++tt) {
             float cand[E], kk[E], qq[E], delta;
             row_step<E, VEC, FWD_TT>(sb, tt, grp, c, S, cand, kk, delta);
@@ -285,7 +234,7 @@ __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
 
 // ---------------------------------------------------------------------------------------------------- backward
 
-template <int E, bool VEC>
+template <int E, bool VEC, int DT>
 __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
     constexpr int CS = BWD_CS;
     constexpr int DKP = 16 * E;
@@ -311,9 +260,18 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
         dS[e] = (a.dstate_T && row_ok && j < Dk) ? a.dstate_T[row_off + j] : 0.f;
     }
     const int nch = (T + a.chunk - 1) / a.chunk;
+    // Stages in order: per chunk (last first), the replay sub-chunks 0 .. nsub-2, then the sub-chunks nsub-1 .. 0
+    // with dY.  Each stage's tokens are loaded into registers during the one before (its first token: next_t0).
+    TokRegs<E, VEC, CS, true> tr;
+    auto fetch = [&](int t0) {
+        stage_fetch<E, VEC, CS, true, DT, DT>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, a.dy, b, hv, hk, rb, t0, T,
+                                              a.Hk, Hv, Dk, Dv, a.in_dt, a.dy_dt);
+    };
+    fetch((nch - 1) * a.chunk);
     for (int ci = nch - 1; ci >= 0; --ci) {
         const int cs = ci * a.chunk, ce = min(T, cs + a.chunk);
         const int nsub = (ce - cs + CS - 1) / CS;
+        const int next_chunk_t0 = ci > 0 ? (ci - 1) * a.chunk : 0;  // the previous chunk's first stage
         const float *start = ci == 0 ? a.state0 : a.snaps + (size_t)(ci - 1) * state_elems;
         float S[E];
 #pragma unroll
@@ -324,9 +282,9 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
         // Replay the chunk once, recording the state at each sub-chunk start (1 .. nsub-1).
         for (int si = 0; si < nsub - 1; ++si) {
             __syncthreads();
-            stage_tokens<E, VEC, CS, false>(sb, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb,
-                                            cs + si * CS, CS, T, a.Hk, Hv, Dk, Dv, a.in_dt, 0, a.gate);
+            stage_store<E, VEC, CS, true>(sb, tr, a.mask != nullptr, CS, Dk, Dv, rb, a.gate);
             __syncthreads();
+            fetch(si + 1 < nsub - 1 ? cs + (si + 1) * CS : cs + (nsub - 1) * CS);
 #pragma unroll
             for (int s = 0; s < CS; ++s) {
                 float cand[E], kk[E], delta;
@@ -353,9 +311,9 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
                 for (int e = 0; e < E; ++e) S[e] = ws[(size_t)(si - 1) * ROWS * DKP + e];
             }
             __syncthreads();
-            stage_tokens<E, VEC, CS, true>(sb, a.q, a.k, a.v, a.g, a.beta, a.mask, a.dy, b, hv, hk, rb, ss, n,
-                                           T, a.Hk, Hv, Dk, Dv, a.in_dt, a.dy_dt, a.gate);
+            stage_store<E, VEC, CS, true>(sb, tr, a.mask != nullptr, n, Dk, Dv, rb, a.gate);
             __syncthreads();
+            fetch(si > 0 ? cs + (si - 1) * CS : next_chunk_t0);
             float hist[CS][E];
             float rh[CS];
 #pragma unroll
@@ -586,13 +544,22 @@ void launch_rec_fwd(const RecFwdArgs &a, hipStream_t st) {
     }
 }
 
-template <int E>
-static void launch_bwd_e(const RecBwdArgs &a, hipStream_t st) {
+template <int E, int DT>
+static void launch_bwd_et(const RecBwdArgs &a, hipStream_t st) {
     dim3 grid(rec_num_row_blocks(a.Dv), a.Hv, a.B);
     if (a.gate == GATE_DECAY_VEC)
-        hipLaunchKernelGGL((rec_bwd_kernel<E, true>), grid, dim3(THREADS), 0, st, a);
+        hipLaunchKernelGGL((rec_bwd_kernel<E, true, DT>), grid, dim3(THREADS), 0, st, a);
     else
-        hipLaunchKernelGGL((rec_bwd_kernel<E, false>), grid, dim3(THREADS), 0, st, a);
+        hipLaunchKernelGGL((rec_bwd_kernel<E, false, DT>), grid, dim3(THREADS), 0, st, a);
+}
+
+// inputs and cotangent of one dtype: fixed at compile time; mixed (e.g. a wider cotangent): read at run time
+template <int E>
+static void launch_bwd_e(const RecBwdArgs &a, hipStream_t st) {
+    if (a.in_dt != a.dy_dt) launch_bwd_et<E, -1>(a, st);
+    else if (a.in_dt == DT_BF16) launch_bwd_et<E, DT_BF16>(a, st);
+    else if (a.in_dt == DT_F16) launch_bwd_et<E, DT_F16>(a, st);
+    else launch_bwd_et<E, DT_F32>(a, st);
 }
 
 void launch_rec_bwd(const RecBwdArgs &a, hipStream_t st) {
