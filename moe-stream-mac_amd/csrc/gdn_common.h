@@ -113,4 +113,17 @@ __device__ __forceinline__ float lane_xor32(float x) {
     return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
+// Two sums over lane pairs l, l ^ 16 with one swap: lanes of even 16-lane rows get a + a(l ^ 16), lanes of odd
+// rows b + b(l ^ 16).  The swap leaves each lane holding the two addends it needs (a even lane keeps its a and
+// receives its partner's a; an odd lane keeps its b and receives its partner's b).
+__device__ __forceinline__ float pair_sum16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// The same over lane pairs l, l ^ 32: the lower half gets a + a(l ^ 32), the upper half b + b(l ^ 32).
+__device__ __forceinline__ float pair_sum32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 }  // namespace gdn

@@ -372,34 +372,39 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
                         s_row[s][grp][2] = dgl;
                     }
                     // Sum dq / dk over the 4 rows of this wave: halve the vector at each exchange so every
-                    // lane ends with E/2 fully reduced values.
-                    const int h = gw & 1;
+                    // lane ends with E/2 fully reduced values (even rows dq, odd rows dk; then the lower half
+                    // of the wave the first E/2 channels, the upper half the rest).
+                    const int h = gw & 1, h2 = gw >> 1;
                     float W[E];
 #pragma unroll
-                    for (int e = 0; e < E; ++e) {
-                        const float mine = h ? pk[e] : pq[e];
-                        const float other = h ? pq[e] : pk[e];
-                        W[e] = mine + lane_xor16(other);
-                    }
+                    for (int e = 0; e < E; ++e) W[e] = pair_sum16(pq[e], pk[e]);
                     if constexpr (E >= 2) {
                         constexpr int H = E / 2;
-                        const int h2 = gw >> 1;
 #pragma unroll
-                        for (int e = 0; e < H; ++e) {
-                            const float mine = h2 ? W[H + e] : W[e];
-                            const float other = h2 ? W[e] : W[H + e];
-                            s_red[s][wave][h * DKP + c * E + h2 * H + e] = mine + lane_xor32(other);
-                        }
+                        for (int e = 0; e < H; ++e)
+                            s_red[s][wave][h * DKP + c * E + h2 * H + e] = pair_sum32(W[e], W[H + e]);
                     } else {
                         const float x = W[0] + lane_xor32(W[0]);
-                        if ((gw >> 1) == 0) s_red[s][wave][h * DKP + c] = x;
+                        if (h2 == 0) s_red[s][wave][h * DKP + c] = x;
                     }
                     if constexpr (VEC) {
+                        // the same halving over one vector: lane (h, h2) ends with channels
+                        // c E + h E/2 + h2 E/4 + i, i < E/4, summed over the 4 rows
+                        if constexpr (E >= 4) {
+                            constexpr int H = E / 2, Q = E / 4;
+                            float P[H];
 #pragma unroll
-                        for (int e = 0; e < E; ++e) {
-                            float x = pg[e] + lane_xor16(pg[e]);
-                            x += lane_xor32(x);
-                            if (gw == 0) s_red[s][wave][2 * DKP + c * E + e] = x;
+                            for (int i = 0; i < H; ++i) P[i] = pair_sum16(pg[i], pg[H + i]);
+#pragma unroll
+                            for (int i = 0; i < Q; ++i)
+                                s_red[s][wave][2 * DKP + c * E + h * H + h2 * Q + i] = pair_sum32(P[i], P[Q + i]);
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < E; ++e) {
+                                float x = pg[e] + lane_xor16(pg[e]);
+                                x += lane_xor32(x);
+                                if (gw == 0) s_red[s][wave][2 * DKP + c * E + e] = x;
+                            }
                         }
                     }
                 }
