@@ -240,7 +240,7 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
     constexpr int DKP = 16 * E;
     constexpr int NQ = VEC ? 3 : 2;
     __shared__ __align__(16) StageBuf<E, VEC, CS> sb;
-    __shared__ float s_red[CS][4][NQ * DKP];  // per-wave sums over its 4 rows: dq | dk | (dg per channel)
+    __shared__ __align__(16) float s_red[CS][4][NQ * DKP];  // per-wave sums over its 4 rows: dq | dk | (dg per channel)
     __shared__ float s_row[CS][ROWS][3];      // per row: dv, dbeta, dg (scalar gate)
 
     const int rb = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
@@ -252,6 +252,9 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
     const size_t state_elems = (size_t)B * Hv * Dv * Dk;
     const size_t row_off = (((size_t)b * Hv + hv) * Dv + row) * Dk;
     float *ws = a.ws_sub + ((((size_t)b * Hv + hv) * a.nrb + rb) * a.max_sub) * ROWS * DKP + grp * DKP + c * E;
+    // rows of whole 16-byte pieces in the partial-sum buffers
+    const bool part_vec = (Dk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.part_qk) & 15) == 0 &&
+                          (!VEC || (reinterpret_cast<uintptr_t>(a.part_gv) & 15) == 0);
 
     float dS[E];
 #pragma unroll
@@ -410,14 +413,33 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
                 }
             }
             __syncthreads();
-            // Write this workgroup's partial sums for tokens [ss, ss+n).
-            for (int i = tid; i < n * NQ * Dk; i += THREADS) {
-                const int s = i / (NQ * Dk), rem = i - s * NQ * Dk, which = rem / Dk, j = rem - which * Dk;
-                const float sum = (s_red[s][0][which * DKP + j] + s_red[s][1][which * DKP + j]) +
-                                  (s_red[s][2][which * DKP + j] + s_red[s][3][which * DKP + j]);
-                const size_t tok = (((size_t)rb * B + b) * T + ss + s) * Hv + hv;
-                if (which < 2) a.part_qk[tok * 2 * Dk + which * Dk + j] = sum;
-                else a.part_gv[tok * Dk + j] = sum;
+            // Write this workgroup's partial sums for tokens [ss, ss+n), four channels per thread and step (the
+            // index split has compile-time divisors); 16-byte stores when the rows allow them.
+            {
+                constexpr int NJ4 = DKP / 4, PER_S = NQ * NJ4;
+                const size_t tok0 = (((size_t)rb * B + b) * T + ss) * Hv + hv;
+                for (int i = tid; i < CS * PER_S; i += THREADS) {
+                    const int s = i / PER_S, rem = i - s * PER_S, which = rem / NJ4, j = 4 * (rem - which * NJ4);
+                    if (s < n && j < Dk) {
+                        const int o = which * DKP + j;
+                        const float4 w0 = *reinterpret_cast<const float4 *>(&s_red[s][0][o]);
+                        const float4 w1 = *reinterpret_cast<const float4 *>(&s_red[s][1][o]);
+                        const float4 w2 = *reinterpret_cast<const float4 *>(&s_red[s][2][o]);
+                        const float4 w3 = *reinterpret_cast<const float4 *>(&s_red[s][3][o]);
+                        const float4 sum = make_float4((w0.x + w1.x) + (w2.x + w3.x), (w0.y + w1.y) + (w2.y + w3.y),
+                                                       (w0.z + w1.z) + (w2.z + w3.z), (w0.w + w1.w) + (w2.w + w3.w));
+                        const size_t tok = tok0 + (size_t)s * Hv;
+                        float *dst = which < 2 ? a.part_qk + tok * 2 * Dk + which * Dk + j : a.part_gv + tok * Dk + j;
+                        if (part_vec) {
+                            *reinterpret_cast<float4 *>(dst) = sum;
+                        } else {
+                            const float v4[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+                            for (int u = 0; u < 4; ++u)
+                                if (j + u < Dk) dst[u] = v4[u];
+                        }
+                    }
+                }
             }
             for (int i = tid; i < n * ROWS; i += THREADS) {
                 const int s = i / ROWS, r = i - s * ROWS, rr = rb * ROWS + r;
