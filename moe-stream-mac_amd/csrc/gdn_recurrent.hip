@@ -198,10 +198,9 @@ __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
 #pragma unroll
             for (int e = 0; e < E; ++e) y = fmaf(cand[e], qq[e], y);
             y = row16_allreduce(y);
-            if (sb.m[tt] != 0.f) {
+            const bool keep = sb.m[tt] != 0.f;  // a select, not a branch: no register shuffles around it
 #pragma unroll
-                for (int e = 0; e < E; ++e) S[e] = cand[e];
-            }
+            for (int e = 0; e < E; ++e) S[e] = keep ? cand[e] : S[e];
             if (c == 0) s_y[tt][grp] = y;
             if (--until_snap == 0) {
                 until_snap = a.chunk;
@@ -292,10 +291,9 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
             for (int s = 0; s < CS; ++s) {
                 float cand[E], kk[E], delta;
                 row_step<E, VEC, CS>(sb, s, grp, c, S, cand, kk, delta);
-                if (sb.m[s] != 0.f) {
+                const bool keep = sb.m[s] != 0.f;
 #pragma unroll
-                    for (int e = 0; e < E; ++e) S[e] = cand[e];
-                }
+                for (int e = 0; e < E; ++e) S[e] = keep ? cand[e] : S[e];
             }
 #pragma unroll
             for (int e = 0; e < E; ++e) ws[(size_t)si * ROWS * DKP + e] = S[e];
@@ -317,97 +315,94 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
             stage_store<E, VEC, CS, true>(sb, tr, a.mask != nullptr, n, Dk, Dv, rb, a.gate);
             __syncthreads();
             fetch(si > 0 ? cs + (si - 1) * CS : next_chunk_t0);
+            // All CS slots are stepped, also past n: stage_store gives those k = v = beta = 0, decay 1 and keep 1,
+            // so they leave S and dS unchanged, and their dq / dk / dg sums are never written out.
             float hist[CS][E];
             float rh[CS];
 #pragma unroll
             for (int s = 0; s < CS; ++s) {
-                if (s < n) {
-                    float cand[E], kk[E], delta;
+                float cand[E], kk[E], delta;
 #pragma unroll
-                    for (int e = 0; e < E; ++e) hist[s][e] = S[e];
-                    rh[s] = row_step<E, VEC, CS>(sb, s, grp, c, S, cand, kk, delta);
-                    if (sb.m[s] != 0.f) {
+                for (int e = 0; e < E; ++e) hist[s][e] = S[e];
+                rh[s] = row_step<E, VEC, CS>(sb, s, grp, c, S, cand, kk, delta);
+                const bool keep = sb.m[s] != 0.f;
 #pragma unroll
-                        for (int e = 0; e < E; ++e) S[e] = cand[e];
-                    }
-                }
+                for (int e = 0; e < E; ++e) S[e] = keep ? cand[e] : S[e];
             }
 #pragma unroll
             for (int s = CS - 1; s >= 0; --s) {
-                if (s < n) {
-                    float kk[E], qq[E], dec[E];
-                    lds_vec<E>(kk, &sb.k[s][c * E]);
-                    lds_vec<E>(qq, &sb.q[s][c * E]);
-                    if (VEC) {
-                        lds_vec<E>(dec, &sb.g[s][c * E]);
+                float kk[E], qq[E], dec[E];
+                lds_vec<E>(kk, &sb.k[s][c * E]);
+                lds_vec<E>(qq, &sb.q[s][c * E]);
+                if (VEC) {
+                    lds_vec<E>(dec, &sb.g[s][c * E]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < E; ++e) dec[e] = sb.g[s][0];
+                }
+                const float dyr = sb.dy[s][grp], bt = sb.beta[s], r = rh[s], delta = r * bt;
+                const bool keep = sb.m[s] != 0.f;
+                float dSc[E];
+                float u = 0.f;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    dSc[e] = fmaf(dyr, qq[e], keep ? dS[e] : 0.f);
+                    u = fmaf(dSc[e], kk[e], u);
+                }
+                u = row16_allreduce(u);
+                const float ev = bt * u;
+                float pq[E], pk[E], pg[E];
+                float dgl = 0.f;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const float A = hist[s][e] * dec[e];
+                    const float cand = fmaf(delta, kk[e], A);
+                    pq[e] = dyr * cand;
+                    pk[e] = fmaf(dSc[e], delta, -ev * A);
+                    const float dA = fmaf(-ev, kk[e], dSc[e]);
+                    if (VEC) pg[e] = dA * hist[s][e];
+                    else dgl = fmaf(dA, hist[s][e], dgl);
+                    dS[e] = fmaf(dA, dec[e], keep ? 0.f : dS[e]);
+                }
+                if (!VEC) dgl = row16_allreduce(dgl);
+                if (c == 0) {
+                    s_row[s][grp][0] = ev;
+                    s_row[s][grp][1] = u * r;
+                    s_row[s][grp][2] = dgl;
+                }
+                // Sum dq / dk over the 4 rows of this wave: halve the vector at each exchange so every
+                // lane ends with E/2 fully reduced values (even rows dq, odd rows dk; then the lower half
+                // of the wave the first E/2 channels, the upper half the rest).
+                const int h = gw & 1, h2 = gw >> 1;
+                float W[E];
+#pragma unroll
+                for (int e = 0; e < E; ++e) W[e] = pair_sum16(pq[e], pk[e]);
+                if constexpr (E >= 2) {
+                    constexpr int H = E / 2;
+#pragma unroll
+                    for (int e = 0; e < H; ++e)
+                        s_red[s][wave][h * DKP + c * E + h2 * H + e] = pair_sum32(W[e], W[H + e]);
+                } else {
+                    const float x = W[0] + lane_xor32(W[0]);
+                    if (h2 == 0) s_red[s][wave][h * DKP + c] = x;
+                }
+                if constexpr (VEC) {
+                    // the same halving over one vector: lane (h, h2) ends with channels
+                    // c E + h E/2 + h2 E/4 + i, i < E/4, summed over the 4 rows
+                    if constexpr (E >= 4) {
+                        constexpr int H = E / 2, Q = E / 4;
+                        float P[H];
+#pragma unroll
+                        for (int i = 0; i < H; ++i) P[i] = pair_sum16(pg[i], pg[H + i]);
+#pragma unroll
+                        for (int i = 0; i < Q; ++i)
+                            s_red[s][wave][2 * DKP + c * E + h * H + h2 * Q + i] = pair_sum32(P[i], P[Q + i]);
                     } else {
 #pragma unroll
-                        for (int e = 0; e < E; ++e) dec[e] = sb.g[s][0];
-                    }
-                    const float dyr = sb.dy[s][grp], bt = sb.beta[s], r = rh[s], delta = r * bt;
-                    const bool keep = sb.m[s] != 0.f;
-                    float dSc[E];
-                    float u = 0.f;
-#pragma unroll
-                    for (int e = 0; e < E; ++e) {
-                        dSc[e] = fmaf(dyr, qq[e], keep ? dS[e] : 0.f);
-                        u = fmaf(dSc[e], kk[e], u);
-                    }
-                    u = row16_allreduce(u);
-                    const float ev = bt * u;
-                    float pq[E], pk[E], pg[E];
-                    float dgl = 0.f;
-#pragma unroll
-                    for (int e = 0; e < E; ++e) {
-                        const float A = hist[s][e] * dec[e];
-                        const float cand = fmaf(delta, kk[e], A);
-                        pq[e] = dyr * cand;
-                        pk[e] = fmaf(dSc[e], delta, -ev * A);
-                        const float dA = fmaf(-ev, kk[e], dSc[e]);
-                        if (VEC) pg[e] = dA * hist[s][e];
-                        else dgl = fmaf(dA, hist[s][e], dgl);
-                        dS[e] = fmaf(dA, dec[e], keep ? 0.f : dS[e]);
-                    }
-                    if (!VEC) dgl = row16_allreduce(dgl);
-                    if (c == 0) {
-                        s_row[s][grp][0] = ev;
-                        s_row[s][grp][1] = u * r;
-                        s_row[s][grp][2] = dgl;
-                    }
-                    // Sum dq / dk over the 4 rows of this wave: halve the vector at each exchange so every
-                    // lane ends with E/2 fully reduced values (even rows dq, odd rows dk; then the lower half
-                    // of the wave the first E/2 channels, the upper half the rest).
-                    const int h = gw & 1, h2 = gw >> 1;
-                    float W[E];
-#pragma unroll
-                    for (int e = 0; e < E; ++e) W[e] = pair_sum16(pq[e], pk[e]);
-                    if constexpr (E >= 2) {
-                        constexpr int H = E / 2;
-#pragma unroll
-                        for (int e = 0; e < H; ++e)
-                            s_red[s][wave][h * DKP + c * E + h2 * H + e] = pair_sum32(W[e], W[H + e]);
-                    } else {
-                        const float x = W[0] + lane_xor32(W[0]);
-                        if (h2 == 0) s_red[s][wave][h * DKP + c] = x;
-                    }
-                    if constexpr (VEC) {
-                        // the same halving over one vector: lane (h, h2) ends with channels
-                        // c E + h E/2 + h2 E/4 + i, i < E/4, summed over the 4 rows
-                        if constexpr (E >= 4) {
-                            constexpr int H = E / 2, Q = E / 4;
-                            float P[H];
-#pragma unroll
-                            for (int i = 0; i < H; ++i) P[i] = pair_sum16(pg[i], pg[H + i]);
-#pragma unroll
-                            for (int i = 0; i < Q; ++i)
-                                s_red[s][wave][2 * DKP + c * E + h * H + h2 * Q + i] = pair_sum32(P[i], P[Q + i]);
-                        } else {
-#pragma unroll
-                            for (int e = 0; e < E; ++e) {
-                                float x = pg[e] + lane_xor16(pg[e]);
-                                x += lane_xor32(x);
-                                if (gw == 0) s_red[s][wave][2 * DKP + c * E + e] = x;
-                            }
+                        for (int e = 0; e < E; ++e) {
+                            float x = pg[e] + lane_xor16(pg[e]);
+                            x += lane_xor32(x);
+                            if (gw == 0) s_red[s][wave][2 * DKP + c * E + e] = x;
                         }
                     }
                 }
