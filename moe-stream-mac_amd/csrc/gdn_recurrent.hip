@@ -190,7 +190,7 @@ __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
         __syncthreads();
         stage_fetch<E, VEC, FWD_TT, false, DT, DT>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb,
                                                    t0 + FWD_TT, T, a.Hk, a.Hv, Dk, Dv, a.in_dt, 0);
-        for (int tt = 0; tt < n; ++tt) {
+        auto token = [&](const int tt) {
             float cand[E], kk[E], qq[E], delta;
             row_step<E, VEC, FWD_TT>(sb, tt, grp, c, S, cand, kk, delta);
             lds_vec<E>(qq, &sb.q[tt][c * E]);
@@ -214,6 +214,14 @@ __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
                     }
                 }
             }
+        };
+        // A full stage is unrolled, so each token's LDS reads are issued during the token before; a partial one
+        // (the last, or a decode step's single token) steps only its n tokens.
+        if (n == FWD_TT) {
+#pragma unroll
+            for (int tt = 0; tt < FWD_TT; ++tt) token(tt);
+        } else {
+            for (int tt = 0; tt < n; ++tt) token(tt);
         }
         __syncthreads();
         for (int i = tid; i < n * ROWS; i += THREADS) {
