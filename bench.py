@@ -15,6 +15,9 @@ Workloads (one GPU; the default is the T=4096 configuration the metric is quoted
   masked_bf16_b4_t4096
                   bf16_b4_t4096 with a mask (each sequence's last 10% masked, padding): two chunked
                   passes plus the masked tokens' fix-up
+  vgate_bf16_b4_t4096
+                  bf16_b4_t4096 with one decay per key channel (g [B, T, Hv, D], in decay space); runs the
+                  token-recurrent form
   stream_ops_bf16_b2_t8192
                   the streaming kernels around the recurrence on block-shaped bf16 inputs (B=2, T=8192, Hk=16,
                   Hv=32, D=128): fused conv + SiLU + split + q/k L2 norm, plain conv + SiLU (8192 channels), q/k L2
@@ -59,11 +62,13 @@ def algo_model(w, form="chunk"):
       (7 D^2 forward + 20 D^2 backward), priced at the fp32 peak.
     The recurrent form (masks, vector gates) computes the recurrence itself, 27 D^2 flops per head-token on fp32
     VALU, whatever the input dtype; its bytes follow the dtype as above.
+    Per-channel (vector) gates read g and write dg per key channel: 4 * 2 Hv D bytes in place of 4 * 2 Hv.
     The per-sequence state traffic (S0, S_T, dS_T, dS0) and snapshot traffic are not algorithmic."""
     Hk, Hv, D, C = w["Hk"], w["Hv"], w["D"], CK_C
     if form == "recurrent":
         b = 2 if w["dtype"] == "bf16" else 4
-        return b * (4 * Hk * D + 4 * Hv * D) + 4 * 4 * Hv, {"fp32": 27 * D * D * Hv}, PEAK_FP32_TFLOPS
+        gates = 4 * 2 * Hv * (D + 1) if w.get("vector_gate") else 4 * 4 * Hv
+        return b * (4 * Hk * D + 4 * Hv * D) + gates, {"fp32": 27 * D * D * Hv}, PEAK_FP32_TFLOPS
     if w["dtype"] == "bf16":
         nbytes = 2 * (4 * Hk * D + 4 * Hv * D) + 4 * 4 * Hv
         flops = {"bf16_intra_chunk": 3 * 10 * C * D * Hv, "bf16_state": 3 * 6 * D * D * Hv}
@@ -156,6 +161,8 @@ WORKLOADS = {
     "ckpt_b1_t16384": dict(B=1, T=16384, Hk=16, Hv=32, D=128, dtype="fp32", chunk=256, s0_std=0.0),
     "masked_bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
                                  masked_tail=0.1),
+    "vgate_bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
+                                vector_gate=True),
     "stream_ops_bf16_b2_t8192": dict(B=2, T=8192, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
                                      ops=True),
     "block_bf16_b2_t8192": dict(B=2, T=8192, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
@@ -181,11 +188,15 @@ def make_inputs(w, dev, seed=0):
     v = n(B, T, Hv, D)
     beta = torch.sigmoid(n(B, T, Hv))
     A_log = torch.empty(Hv, device=dev).uniform_(0.0, float(torch.log(torch.tensor(16.0))), generator=gen)
-    a = n(B, T, Hv)
-    g_log = -torch.exp(A_log) * torch.nn.functional.softplus(a)
+    if w.get("vector_gate"):
+        # one decay per key channel, [B, T, Hv, D]: the multiplicative decay itself (a per-channel gate is taken
+        # in decay space, tools/gdn_vjp.py:174-179), exp of the same log-decay distribution
+        g = torch.exp(-torch.exp(A_log)[:, None] * torch.nn.functional.softplus(n(B, T, Hv, D)))
+    else:
+        g = -torch.exp(A_log) * torch.nn.functional.softplus(n(B, T, Hv))  # log decay per head
     state = n(B, Hv, D, D) * w["s0_std"] if w["s0_std"] > 0 else torch.zeros(B, Hv, D, D, device=dev)
     dy = n(B, T, Hv, D)
-    return dict(q=q.to(dt), k=k.to(dt), v=v.to(dt), g_log=g_log.contiguous(), beta=beta.contiguous(),
+    return dict(q=q.to(dt), k=k.to(dt), v=v.to(dt), g=g.contiguous(), beta=beta.contiguous(),
                 state=state.contiguous(), dy=dy.to(dt))
 
 
@@ -367,15 +378,16 @@ def main():
     else:
         x = make_inputs(w, dev)
         out_dtype = x["q"].dtype
-        leaves = [x[n].requires_grad_(True) for n in ("q", "k", "v", "g_log", "beta", "state")]
+        leaves = [x[n].requires_grad_(True) for n in ("q", "k", "v", "g", "beta", "state")]
         mask = None
         if w.get("masked_tail"):
             mask = torch.ones(B, T, dtype=torch.bool, device=dev)
             mask[:, T - int(T * w["masked_tail"]):] = False
 
         def step():
-            y, S = gdn_engine.recurrence(x["q"], x["k"], x["v"], x["g_log"], x["beta"], x["state"], mask,
-                                         chunk=w["chunk"], log_gate=True, output_dtype=out_dtype)
+            y, S = gdn_engine.recurrence(x["q"], x["k"], x["v"], x["g"], x["beta"], x["state"], mask,
+                                         chunk=w["chunk"], log_gate=not w.get("vector_gate"),
+                                         output_dtype=out_dtype)
             return torch.autograd.grad([y], leaves, [x["dy"]])
 
     for i in range(args.warmup):

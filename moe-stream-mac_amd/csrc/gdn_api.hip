@@ -129,12 +129,12 @@ struct BwdLayout {
 };
 
 static BwdLayout bwd_layout(int B, int T, int Hv, int Dk, int Dv, int chunk, int gate) {
-    const size_t nrb = (size_t)rec_num_row_blocks(Dv);
+    const size_t nrb = (size_t)rec_bwd_row_blocks(B, Hv, Dk, Dv, gate);
     const size_t toks = (size_t)B * T * Hv;
     BwdLayout L;
     size_t off = 0;
     L.sub = off;
-    off += align256(rec_sub_floats(B, Hv, Dk, Dv, T, chunk) * sizeof(float));
+    off += align256(rec_sub_floats(B, Hv, Dk, Dv, T, chunk, gate) * sizeof(float));
     L.part_qk = off;
     off += align256(nrb * toks * 2 * Dk * sizeof(float));
     L.part_gb = off;
@@ -896,7 +896,7 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
     a.part_qk = reinterpret_cast<float *>(ws + L.part_qk);
     a.part_gb = reinterpret_cast<float *>(ws + L.part_gb);
     a.part_gv = reinterpret_cast<float *>(ws + L.part_gv);
-    a.nrb = rec_num_row_blocks(Dv);
+    a.nrb = rec_bwd_row_blocks(B, Hv, Dk, Dv, gate_kind);
     a.max_sub = rec_max_sub(T, chunk);
     {
         Timed tm("rec_bwd", st);

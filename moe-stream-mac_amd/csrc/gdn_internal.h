@@ -96,8 +96,10 @@ void launch_add2(float *dst, const float *x, const float *y, size_t n, hipStream
 
 int pick_lane_width(int Dk);
 int rec_num_row_blocks(int Dv);
+int rec_bwd_rows(int B, int Hv, int Dk, int Dv, int gate);
+int rec_bwd_row_blocks(int B, int Hv, int Dk, int Dv, int gate);
 int rec_max_sub(int T, int chunk);
-size_t rec_sub_floats(int B, int Hv, int Dk, int Dv, int T, int chunk);
+size_t rec_sub_floats(int B, int Hv, int Dk, int Dv, int T, int chunk, int gate);
 
 void launch_rec_fwd(const RecFwdArgs &a, hipStream_t st);
 void launch_rec_bwd(const RecBwdArgs &a, hipStream_t st);

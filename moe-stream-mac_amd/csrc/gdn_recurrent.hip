@@ -9,8 +9,9 @@
 // are never stored: for each chunk the workgroup reloads the chunk-start snapshot written by the forward,
 // replays the chunk once to write sub-chunk starts (every CS tokens) to a small workspace, then for each
 // sub-chunk in reverse replays CS steps keeping S_{t-1} of its rows in VGPRs (fully unrolled), and walks them
-// backward.  Cross-row sums (dq, dk, dg, dbeta) are reduced in-wave (xor shuffles), across the 4 waves in LDS,
-// and across row blocks and the GQA head group by a second, deterministic kernel — no atomics.
+// backward.  Backward workgroups hold 16 or 32 rows (4 or 8 waves; rec_bwd_rows).  Cross-row sums (dq, dk, dg,
+// dbeta) are reduced in-wave (lane swaps), across the waves in LDS, and across row blocks and the GQA head group by
+// a second, deterministic kernel — no atomics.
 #include "gdn_common.h"
 #include "gdn_internal.h"
 
@@ -21,14 +22,14 @@ constexpr int THREADS = 256;  // 4 wave64
 constexpr int FWD_TT = 16;    // tokens per LDS tile in the forward
 constexpr int BWD_CS = 8;     // tokens per register-resident sub-chunk in the backward
 
-template <int E, bool VEC, int TT>
+template <int E, bool VEC, int TT, int R>
 struct StageBuf {
     static constexpr int DKP = 16 * E;
     float k[TT][DKP];
     float q[TT][DKP];
     float g[TT][VEC ? DKP : 1];
-    float v[TT][ROWS];
-    float dy[TT][ROWS];
+    float v[TT][R];
+    float dy[TT][R];
     float beta[TT];
     float m[TT];
 };
@@ -39,26 +40,27 @@ struct StageBuf {
 // branch or a dtype switch made the compiler wait for each one where the branches joined, so a stage's loads came
 // in one after another.  stage_store zeroes what lies past the tokens, channels and rows (decay 1), so padded
 // lanes carry exact zeros through every step.
-template <int E, bool VEC, int TT, bool WITH_DY>
+// NT threads stage the tokens of a workgroup of R value rows.
+template <int E, bool VEC, int TT, bool WITH_DY, int NT, int R>
 struct TokRegs {
     static constexpr int DKP = 16 * E;
-    static constexpr int NKQ = (TT * DKP + THREADS - 1) / THREADS;
-    static constexpr int NV = (TT * ROWS + THREADS - 1) / THREADS;
+    static constexpr int NKQ = (TT * DKP + NT - 1) / NT;
+    static constexpr int NV = (TT * R + NT - 1) / NT;
     float k[NKQ], q[NKQ], g[VEC ? NKQ : 1], v[NV], dy[WITH_DY ? NV : 1];
     float bt, gt, mt;
 };
 
-template <int E, bool VEC, int TT, bool WITH_DY, int DT, int DYT>
-__device__ __forceinline__ void stage_fetch(TokRegs<E, VEC, TT, WITH_DY> &r, const void *q, const void *k,
+template <int E, bool VEC, int TT, bool WITH_DY, int DT, int DYT, int NT, int R>
+__device__ __forceinline__ void stage_fetch(TokRegs<E, VEC, TT, WITH_DY, NT, R> &r, const void *q, const void *k,
                                             const void *v, const float *g, const float *beta, const uint8_t *mask,
                                             const void *dy, int b, int hv, int hk, int rb, int t0, int T, int Hk,
                                             int Hv, int Dk, int Dv, int in_dt, int dy_dt) {
-    using R = TokRegs<E, VEC, TT, WITH_DY>;
+    using TR = TokRegs<E, VEC, TT, WITH_DY, NT, R>;
     const int tid = threadIdx.x;
     const int xdt = DT >= 0 ? DT : in_dt, ydt = DYT >= 0 ? DYT : dy_dt;  // DT < 0: read from the arguments
 #pragma unroll
-    for (int p = 0; p < R::NKQ; ++p) {
-        const int i = tid + p * THREADS, tt = i / R::DKP, j = i - tt * R::DKP;
+    for (int p = 0; p < TR::NKQ; ++p) {
+        const int i = tid + p * NT, tt = i / TR::DKP, j = i - tt * TR::DKP;
         const int t = min(t0 + tt, T - 1), jc = min(j, Dk - 1);
         const size_t idx = (((size_t)b * T + t) * Hk + hk) * Dk + jc;
         r.k[p] = load_as_f32(k, idx, xdt);
@@ -66,8 +68,8 @@ __device__ __forceinline__ void stage_fetch(TokRegs<E, VEC, TT, WITH_DY> &r, con
         if constexpr (VEC) r.g[p] = g[(((size_t)b * T + t) * Hv + hv) * Dk + jc];
     }
 #pragma unroll
-    for (int p = 0; p < R::NV; ++p) {
-        const int i = tid + p * THREADS, tt = i / ROWS, rr = rb * ROWS + (i - tt * ROWS);
+    for (int p = 0; p < TR::NV; ++p) {
+        const int i = tid + p * NT, tt = i / R, rr = rb * R + (i - tt * R);
         const size_t idx = (((size_t)b * T + min(t0 + tt, T - 1)) * Hv + hv) * Dv + min(rr, Dv - 1);
         r.v[p] = load_as_f32(v, idx, xdt);
         if constexpr (WITH_DY) r.dy[p] = load_as_f32(dy, idx, ydt);
@@ -81,15 +83,15 @@ __device__ __forceinline__ void stage_fetch(TokRegs<E, VEC, TT, WITH_DY> &r, con
     r.mt = *mp ? 1.f : 0.f;
 }
 
-template <int E, bool VEC, int TT, bool WITH_DY>
-__device__ __forceinline__ void stage_store(StageBuf<E, VEC, TT> &sb, const TokRegs<E, VEC, TT, WITH_DY> &r,
+template <int E, bool VEC, int TT, bool WITH_DY, int NT, int R>
+__device__ __forceinline__ void stage_store(StageBuf<E, VEC, TT, R> &sb, const TokRegs<E, VEC, TT, WITH_DY, NT, R> &r,
                                             bool masked, int n, int Dk, int Dv, int rb, int gate) {
-    using R = TokRegs<E, VEC, TT, WITH_DY>;
+    using TR = TokRegs<E, VEC, TT, WITH_DY, NT, R>;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int p = 0; p < R::NKQ; ++p) {
-        const int i = tid + p * THREADS, tt = i / R::DKP, j = i - tt * R::DKP;
-        if (i < TT * R::DKP) {
+    for (int p = 0; p < TR::NKQ; ++p) {
+        const int i = tid + p * NT, tt = i / TR::DKP, j = i - tt * TR::DKP;
+        if (i < TT * TR::DKP) {
             const bool ok = tt < n && j < Dk;
             sb.k[tt][j] = ok ? r.k[p] : 0.f;
             sb.q[tt][j] = ok ? r.q[p] : 0.f;
@@ -97,10 +99,10 @@ __device__ __forceinline__ void stage_store(StageBuf<E, VEC, TT> &sb, const TokR
         }
     }
 #pragma unroll
-    for (int p = 0; p < R::NV; ++p) {
-        const int i = tid + p * THREADS, tt = i / ROWS, rl = i - tt * ROWS;
-        if (i < TT * ROWS) {
-            const bool ok = tt < n && rb * ROWS + rl < Dv;
+    for (int p = 0; p < TR::NV; ++p) {
+        const int i = tid + p * NT, tt = i / R, rl = i - tt * R;
+        if (i < TT * R) {
+            const bool ok = tt < n && rb * R + rl < Dv;
             sb.v[tt][rl] = ok ? r.v[p] : 0.f;
             if constexpr (WITH_DY) sb.dy[tt][rl] = ok ? r.dy[p] : 0.f;
         }
@@ -129,8 +131,8 @@ __device__ __forceinline__ void lds_vec(float (&dst)[E], const float *src) {
 
 // One forward step of one state row held as E channels per lane.  Returns the residual r = v - A k and
 // leaves the candidate S~ in cand.
-template <int E, bool VEC, int TT>
-__device__ __forceinline__ float row_step(const StageBuf<E, VEC, TT> &sb, int tt, int grp, int c,
+template <int E, bool VEC, int TT, int R>
+__device__ __forceinline__ float row_step(const StageBuf<E, VEC, TT, R> &sb, int tt, int grp, int c,
                                           const float (&S)[E], float (&cand)[E], float (&kk)[E],
                                           float &delta) {
     float dec[E];
@@ -160,7 +162,7 @@ __device__ __forceinline__ float row_step(const StageBuf<E, VEC, TT> &sb, int tt
 
 template <int E, bool VEC, int DT>
 __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
-    __shared__ __align__(16) StageBuf<E, VEC, FWD_TT> sb;
+    __shared__ __align__(16) StageBuf<E, VEC, FWD_TT, ROWS> sb;
     __shared__ float s_y[FWD_TT][ROWS];
 
     const int rb = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
@@ -180,19 +182,19 @@ __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
     }
     int until_snap = a.chunk;  // tokens left before the next chunk boundary
     // the next stage's tokens are loaded into registers while this one computes
-    TokRegs<E, VEC, FWD_TT, false> tr;
-    stage_fetch<E, VEC, FWD_TT, false, DT, DT>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb, 0, T,
+    TokRegs<E, VEC, FWD_TT, false, THREADS, ROWS> tr;
+    stage_fetch<E, VEC, FWD_TT, false, DT, DT, THREADS, ROWS>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb, 0, T,
                                                a.Hk, a.Hv, Dk, Dv, a.in_dt, 0);
     for (int t0 = 0; t0 < T; t0 += FWD_TT) {
         const int n = min(FWD_TT, T - t0);
         __syncthreads();
-        stage_store<E, VEC, FWD_TT, false>(sb, tr, a.mask != nullptr, n, Dk, Dv, rb, a.gate);
+        stage_store<E, VEC, FWD_TT, false, THREADS, ROWS>(sb, tr, a.mask != nullptr, n, Dk, Dv, rb, a.gate);
         __syncthreads();
-        stage_fetch<E, VEC, FWD_TT, false, DT, DT>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb,
+        stage_fetch<E, VEC, FWD_TT, false, DT, DT, THREADS, ROWS>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb,
                                                    t0 + FWD_TT, T, a.Hk, a.Hv, Dk, Dv, a.in_dt, 0);
         auto token = [&](const int tt) {
             float cand[E], kk[E], qq[E], delta;
-            row_step<E, VEC, FWD_TT>(sb, tt, grp, c, S, cand, kk, delta);
+            row_step<E, VEC, FWD_TT, ROWS>(sb, tt, grp, c, S, cand, kk, delta);
             lds_vec<E>(qq, &sb.q[tt][c * E]);
             float y = 0.f;
 #pragma unroll
@@ -241,24 +243,26 @@ __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
 
 // ---------------------------------------------------------------------------------------------------- backward
 
-template <int E, bool VEC, int DT>
-__global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
+// NW waves per workgroup, 4 NW value rows (4 per wave).
+template <int E, bool VEC, int DT, int NW>
+__global__ __launch_bounds__(64 * NW) void rec_bwd_kernel(RecBwdArgs a) {
     constexpr int CS = BWD_CS;
     constexpr int DKP = 16 * E;
     constexpr int NQ = VEC ? 3 : 2;
-    __shared__ __align__(16) StageBuf<E, VEC, CS> sb;
-    __shared__ __align__(16) float s_red[CS][4][NQ * DKP];  // per-wave sums over its 4 rows: dq | dk | (dg per channel)
-    __shared__ float s_row[CS][ROWS][3];      // per row: dv, dbeta, dg (scalar gate)
+    constexpr int NT = 64 * NW, R = 4 * NW;
+    __shared__ __align__(16) StageBuf<E, VEC, CS, R> sb;
+    __shared__ __align__(16) float s_red[CS][NW][NQ * DKP];  // per-wave sums over its 4 rows: dq | dk | (dg per channel)
+    __shared__ float s_row[CS][R][3];                        // per row: dv, dbeta, dg (scalar gate)
 
     const int rb = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, grp = tid >> 4, c = tid & 15, wave = tid >> 6, gw = grp & 3;
-    const int row = rb * ROWS + grp;
+    const int row = rb * R + grp;
     const bool row_ok = row < a.Dv;
     const int hk = hv / (a.Hv / a.Hk);
     const int T = a.T, Dk = a.Dk, Dv = a.Dv, B = a.B, Hv = a.Hv;
     const size_t state_elems = (size_t)B * Hv * Dv * Dk;
     const size_t row_off = (((size_t)b * Hv + hv) * Dv + row) * Dk;
-    float *ws = a.ws_sub + ((((size_t)b * Hv + hv) * a.nrb + rb) * a.max_sub) * ROWS * DKP + grp * DKP + c * E;
+    float *ws = a.ws_sub + ((((size_t)b * Hv + hv) * a.nrb + rb) * a.max_sub) * R * DKP + grp * DKP + c * E;
     // rows of whole 16-byte pieces in the partial-sum buffers
     const bool part_vec = (Dk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.part_qk) & 15) == 0 &&
                           (!VEC || (reinterpret_cast<uintptr_t>(a.part_gv) & 15) == 0);
@@ -272,9 +276,9 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
     const int nch = (T + a.chunk - 1) / a.chunk;
     // Stages in order: per chunk (last first), the replay sub-chunks 0 .. nsub-2, then the sub-chunks nsub-1 .. 0
     // with dY.  Each stage's tokens are loaded into registers during the one before (its first token: next_t0).
-    TokRegs<E, VEC, CS, true> tr;
+    TokRegs<E, VEC, CS, true, NT, R> tr;
     auto fetch = [&](int t0) {
-        stage_fetch<E, VEC, CS, true, DT, DT>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, a.dy, b, hv, hk, rb, t0, T,
+        stage_fetch<E, VEC, CS, true, DT, DT, NT, R>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, a.dy, b, hv, hk, rb, t0, T,
                                               a.Hk, Hv, Dk, Dv, a.in_dt, a.dy_dt);
     };
     fetch((nch - 1) * a.chunk);
@@ -292,19 +296,19 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
         // Replay the chunk once, recording the state at each sub-chunk start (1 .. nsub-1).
         for (int si = 0; si < nsub - 1; ++si) {
             __syncthreads();
-            stage_store<E, VEC, CS, true>(sb, tr, a.mask != nullptr, CS, Dk, Dv, rb, a.gate);
+            stage_store<E, VEC, CS, true, NT, R>(sb, tr, a.mask != nullptr, CS, Dk, Dv, rb, a.gate);
             __syncthreads();
             fetch(si + 1 < nsub - 1 ? cs + (si + 1) * CS : cs + (nsub - 1) * CS);
 #pragma unroll
             for (int s = 0; s < CS; ++s) {
                 float cand[E], kk[E], delta;
-                row_step<E, VEC, CS>(sb, s, grp, c, S, cand, kk, delta);
+                row_step<E, VEC, CS, R>(sb, s, grp, c, S, cand, kk, delta);
                 const bool keep = sb.m[s] != 0.f;
 #pragma unroll
                 for (int e = 0; e < E; ++e) S[e] = keep ? cand[e] : S[e];
             }
 #pragma unroll
-            for (int e = 0; e < E; ++e) ws[(size_t)si * ROWS * DKP + e] = S[e];
+            for (int e = 0; e < E; ++e) ws[(size_t)si * R * DKP + e] = S[e];
         }
         // Sub-chunks in reverse.
         for (int si = nsub - 1; si >= 0; --si) {
@@ -317,10 +321,10 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
                 }
             } else {
 #pragma unroll
-                for (int e = 0; e < E; ++e) S[e] = ws[(size_t)(si - 1) * ROWS * DKP + e];
+                for (int e = 0; e < E; ++e) S[e] = ws[(size_t)(si - 1) * R * DKP + e];
             }
             __syncthreads();
-            stage_store<E, VEC, CS, true>(sb, tr, a.mask != nullptr, n, Dk, Dv, rb, a.gate);
+            stage_store<E, VEC, CS, true, NT, R>(sb, tr, a.mask != nullptr, n, Dk, Dv, rb, a.gate);
             __syncthreads();
             fetch(si > 0 ? cs + (si - 1) * CS : next_chunk_t0);
             // All CS slots are stepped, also past n: stage_store gives those k = v = beta = 0, decay 1 and keep 1,
@@ -332,7 +336,7 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
                 float cand[E], kk[E], delta;
 #pragma unroll
                 for (int e = 0; e < E; ++e) hist[s][e] = S[e];
-                rh[s] = row_step<E, VEC, CS>(sb, s, grp, c, S, cand, kk, delta);
+                rh[s] = row_step<E, VEC, CS, R>(sb, s, grp, c, S, cand, kk, delta);
                 const bool keep = sb.m[s] != 0.f;
 #pragma unroll
                 for (int e = 0; e < E; ++e) S[e] = keep ? cand[e] : S[e];
@@ -421,16 +425,21 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
             {
                 constexpr int NJ4 = DKP / 4, PER_S = NQ * NJ4;
                 const size_t tok0 = (((size_t)rb * B + b) * T + ss) * Hv + hv;
-                for (int i = tid; i < CS * PER_S; i += THREADS) {
+                for (int i = tid; i < CS * PER_S; i += NT) {
                     const int s = i / PER_S, rem = i - s * PER_S, which = rem / NJ4, j = 4 * (rem - which * NJ4);
                     if (s < n && j < Dk) {
                         const int o = which * DKP + j;
-                        const float4 w0 = *reinterpret_cast<const float4 *>(&s_red[s][0][o]);
-                        const float4 w1 = *reinterpret_cast<const float4 *>(&s_red[s][1][o]);
-                        const float4 w2 = *reinterpret_cast<const float4 *>(&s_red[s][2][o]);
-                        const float4 w3 = *reinterpret_cast<const float4 *>(&s_red[s][3][o]);
-                        const float4 sum = make_float4((w0.x + w1.x) + (w2.x + w3.x), (w0.y + w1.y) + (w2.y + w3.y),
-                                                       (w0.z + w1.z) + (w2.z + w3.z), (w0.w + w1.w) + (w2.w + w3.w));
+                        // the waves' sums, added pairwise in a fixed tree: ((w0 + w1) + (w2 + w3)) + ...
+                        float4 w[NW];
+#pragma unroll
+                        for (int u = 0; u < NW; ++u) w[u] = *reinterpret_cast<const float4 *>(&s_red[s][u][o]);
+#pragma unroll
+                        for (int h = 1; h < NW; h *= 2)
+#pragma unroll
+                            for (int u = 0; u < NW; u += 2 * h)
+                                w[u] = make_float4(w[u].x + w[u + h].x, w[u].y + w[u + h].y, w[u].z + w[u + h].z,
+                                                   w[u].w + w[u + h].w);
+                        const float4 sum = w[0];
                         const size_t tok = tok0 + (size_t)s * Hv;
                         float *dst = which < 2 ? a.part_qk + tok * 2 * Dk + which * Dk + j : a.part_gv + tok * Dk + j;
                         if (part_vec) {
@@ -444,8 +453,8 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
                     }
                 }
             }
-            for (int i = tid; i < n * ROWS; i += THREADS) {
-                const int s = i / ROWS, r = i - s * ROWS, rr = rb * ROWS + r;
+            for (int i = tid; i < n * R; i += NT) {
+                const int s = i / R, r = i - s * R, rr = rb * R + r;
                 if (rr < Dv)
                     store_from_f32(a.dv, (((size_t)b * T + ss + s) * Hv + hv) * Dv + rr, s_row[s][r][0],
                                    a.grad_dt);
@@ -454,7 +463,7 @@ __global__ __launch_bounds__(THREADS) void rec_bwd_kernel(RecBwdArgs a) {
                 const int s = tid;
                 float db = 0.f, dg = 0.f;
 #pragma unroll
-                for (int r = 0; r < ROWS; ++r) {
+                for (int r = 0; r < R; ++r) {
                     db += s_row[s][r][1];
                     dg += s_row[s][r][2];
                 }
@@ -537,15 +546,32 @@ int pick_lane_width(int Dk) {
 
 int rec_num_row_blocks(int Dv) { return (Dv + ROWS - 1) / ROWS; }
 
+// Value rows per backward workgroup.  32 (8 waves) halves the per-row-block partial sums that rec_bwd writes and
+// rec_bwd_reduce_* read back, but one 8-wave workgroup per CU leaves every SIMD waiting at its barriers where two
+// 4-wave ones overlap: at B=4, T=4096, Hv=32 it made rec_bwd 0.8 ms slower for 0.45 ms less reduction with scalar
+// gates, and 0.55 ms slower for 0.85 ms less with per-channel gates (whose dg partials double the traffic).  So 32
+// is taken for per-channel gates only, when the grid keeps at least 512 workgroups (two rounds of one per CU) and
+// up to Dk = 128 (the 8-wave LDS sums of wider rows would not fit); 16 (4 waves) otherwise.
+int rec_bwd_rows(int B, int Hv, int Dk, int Dv, int gate) {
+    if (gate != GATE_DECAY_VEC || pick_lane_width(Dk) > 8 || Dv <= ROWS) return ROWS;
+    return (int64_t)B * Hv * ((Dv + 2 * ROWS - 1) / (2 * ROWS)) >= 512 ? 2 * ROWS : ROWS;
+}
+
+int rec_bwd_row_blocks(int B, int Hv, int Dk, int Dv, int gate) {
+    const int r = rec_bwd_rows(B, Hv, Dk, Dv, gate);
+    return (Dv + r - 1) / r;
+}
+
 int rec_max_sub(int T, int chunk) {
     const int span = chunk < T ? chunk : T;
     const int ns = (span + BWD_CS - 1) / BWD_CS - 1;
     return ns > 0 ? ns : 0;
 }
 
-size_t rec_sub_floats(int B, int Hv, int Dk, int Dv, int T, int chunk) {
+size_t rec_sub_floats(int B, int Hv, int Dk, int Dv, int T, int chunk, int gate) {
     const int E = pick_lane_width(Dk);
-    return (size_t)B * Hv * rec_num_row_blocks(Dv) * rec_max_sub(T, chunk) * ROWS * 16 * E;
+    return (size_t)B * Hv * rec_bwd_row_blocks(B, Hv, Dk, Dv, gate) * rec_max_sub(T, chunk) *
+           rec_bwd_rows(B, Hv, Dk, Dv, gate) * 16 * E;
 }
 
 template <int E, int DT>
@@ -574,13 +600,21 @@ void launch_rec_fwd(const RecFwdArgs &a, hipStream_t st) {
     }
 }
 
+template <int E, int DT, int NW>
+static void launch_bwd_etw(const RecBwdArgs &a, hipStream_t st) {
+    const dim3 grid(a.nrb, a.Hv, a.B);
+    if (a.gate == GATE_DECAY_VEC)
+        hipLaunchKernelGGL((rec_bwd_kernel<E, true, DT, NW>), grid, dim3(64 * NW), 0, st, a);
+    else
+        hipLaunchKernelGGL((rec_bwd_kernel<E, false, DT, NW>), grid, dim3(64 * NW), 0, st, a);
+}
+
 template <int E, int DT>
 static void launch_bwd_et(const RecBwdArgs &a, hipStream_t st) {
-    dim3 grid(rec_num_row_blocks(a.Dv), a.Hv, a.B);
-    if (a.gate == GATE_DECAY_VEC)
-        hipLaunchKernelGGL((rec_bwd_kernel<E, true, DT>), grid, dim3(THREADS), 0, st, a);
-    else
-        hipLaunchKernelGGL((rec_bwd_kernel<E, false, DT>), grid, dim3(THREADS), 0, st, a);
+    if constexpr (E <= 8) {
+        if (rec_bwd_rows(a.B, a.Hv, a.Dk, a.Dv, a.gate) == 2 * ROWS) return launch_bwd_etw<E, DT, 8>(a, st);
+    }
+    launch_bwd_etw<E, DT, 4>(a, st);
 }
 
 // inputs and cotangent of one dtype: fixed at compile time; mixed (e.g. a wider cotangent): read at run time

@@ -212,6 +212,34 @@ def test_bf16_inputs_fp32_state(dev):
             assert nerr(a, b) <= 1e-2, (hk, n, nerr(a, b))
 
 
+@pytest.mark.parametrize("gate_ndim", [3, 4])
+def test_recurrent_wide_grid_against_oracle(dev, monkeypatch, gate_ndim):
+    """The recurrent form at B=4, Hk=16, Hv=32, D=128, T=80 (a partial second chunk and partial sub-chunks), a mask,
+    random dS_T, scalar or per-channel decay gates: with per-channel gates this grid takes the backward's 8-wave,
+    32-row workgroups (per-channel gates and B * Hv * Dv / 32 >= 512), with scalar gates the 16-row ones.  Two
+    key-head groups in two sequences against the fp64 oracle."""
+    monkeypatch.setenv("GDN_FORM", "recurrent")
+    rng = np.random.default_rng(77 + gate_ndim)
+    B, T, Hk, Hv, D = 4, 80, 16, 32, 128
+    q = O.l2norm(rng.standard_normal((B, T, Hk, D)), 1e-6, D ** -0.5).astype(np.float32)
+    k = O.l2norm(rng.standard_normal((B, T, Hk, D)), 1e-6, 1.0).astype(np.float32)
+    gshape = (B, T, Hv) + ((D,) if gate_ndim == 4 else ())
+    c = dict(q=q, k=k, v=rng.standard_normal((B, T, Hv, D)).astype(np.float32),
+             g=rng.uniform(0.9, 1.0, gshape).astype(np.float32),
+             beta=rng.uniform(0.05, 0.95, (B, T, Hv)).astype(np.float32),
+             state=(0.1 * rng.standard_normal((B, Hv, D, D))).astype(np.float32),
+             dy=rng.standard_normal((B, T, Hv, D)).astype(np.float32),
+             dstate=(0.1 * rng.standard_normal((B, Hv, D, D))).astype(np.float32),
+             mask=rng.random((B, T)) > 0.2)
+    got = run_gpu(c, dev, 64)
+    for bi, hk in ((0, 0), (3, 13)):
+        cb = {n: (x[bi:bi + 1] if isinstance(x, np.ndarray) else x) for n, x in c.items()}
+        want = oracle_vjp(dict(_slice_group(cb, hk), mask=cb["mask"]), 64)
+        gs = [x[bi:bi + 1] for x in _slice_out(got, hk)]
+        for n, a, b in zip(OUT_NAMES, gs, want):
+            assert nerr(a, b) <= 1e-4, (bi, hk, n, nerr(a, b))
+
+
 def test_chunk_invariance_long(dev, monkeypatch):
     """The recurrent form's snapshot interval is an implementation detail: chunk 64 vs 256 vs 1000 agree."""
     monkeypatch.setenv("GDN_FORM", "recurrent")
