@@ -52,7 +52,8 @@ __device__ __forceinline__ void mma_strip(f4 (&acc)[NTILES], const float *A, int
 }
 
 // Copy a [ROWS][COLS] tile (rows strided by src_stride elements, dtype dt) into LDS as fp32 with row stride
-// lds_stride, multiplying row r by scale[r] when scale is given.  Rows >= n are zero.  Every load is 16 bytes
+// lds_stride, multiplying row r by scale[r] when scale is given.  Rows >= n are zero (n >= 1: they load row n - 1
+// and select zero, so no load sits under a branch, where the compiler would wait for it).  Every load is 16 bytes
 // and all of a thread's loads are issued before the first LDS store, so the tile costs one memory latency.
 template <int ROWS, int COLS, int NTH = NT>
 __device__ __forceinline__ void load_tile(float *dst, int lds_stride, const void *src, size_t src_stride, int n,
@@ -69,8 +70,9 @@ __device__ __forceinline__ void load_tile(float *dst, int lds_stride, const void
 #pragma unroll
             for (int p = 0; p < NB; ++p) {
                 const int v = tid + (p0 + p) * NTH, r = v / VPR, c4 = (v - r * VPR) * 4;
-                buf[p] = r < n ? *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + r * src_stride + c4)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float4 x =
+                    *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + min(r, n - 1) * src_stride + c4);
+                buf[p] = r < n ? x : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (int p = 0; p < NB; ++p) {
@@ -91,8 +93,9 @@ __device__ __forceinline__ void load_tile(float *dst, int lds_stride, const void
 #pragma unroll
             for (int p = 0; p < NB; ++p) {
                 const int v = tid + (p0 + p) * NTH, r = v / VPR, c8 = (v - r * VPR) * 8;
-                buf[p] = r < n ? *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(src) + r * src_stride + c8)
-                               : make_uint4(0u, 0u, 0u, 0u);
+                const uint4 x =
+                    *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(src) + min(r, n - 1) * src_stride + c8);
+                buf[p] = r < n ? x : make_uint4(0u, 0u, 0u, 0u);
             }
 #pragma unroll
             for (int p = 0; p < NB; ++p) {
@@ -872,9 +875,8 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
     // ---- phase 0: gates, dY, h; TdD with dv = diag(beta) TdD and rowsum(V * TdD) from its loads
     if (tid < C) {
         sG[tid] = a.w.G[ci * C + tid];
-        float bt = 0.f;
-        if (tid < n) bt = a.beta[((size_t)b * a.Ts + t0 + tid) * a.Hv + hv];
-        sB[tid] = bt;
+        const float bt = a.beta[((size_t)b * a.Ts + t0 + min(tid, n - 1)) * a.Hv + hv];
+        sB[tid] = tid < n ? bt : 0.f;
     }
     load_tile<D, D, NTB>(R1, LD, Hc, D, D, DT_F32, nullptr, tid);
     load_tile<C, D, NTB>(R2, LD, elem_ptr(a.dy, v0, k_dy_dt), v_row, n, k_dy_dt, nullptr, tid);
@@ -887,9 +889,20 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
         for (int p = 0; p < PER; ++p) {
             const int v = tid + p * NTB, r = v / (D / 4), c4 = (v - r * (D / 4)) * 4;
             td[p] = *reinterpret_cast<const float4 *>(TDc + r * D + c4);
-            bt[p] = r < n ? a.beta[((size_t)b * a.Ts + t0 + r) * a.Hv + hv] : 0.f;
+            // rows past n read row n - 1 and are zeroed after: no load sits under a branch
+            const int rc = min(r, n - 1);
+            const float b4 = a.beta[((size_t)b * a.Ts + t0 + rc) * a.Hv + hv];
+            bt[p] = r < n ? b4 : 0.f;
+            if constexpr (AF32) {
+                const float4 x = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.v) + v0 +
+                                                                   (size_t)rc * v_row + c4);
+                vv[p][0] = x.x; vv[p][1] = x.y; vv[p][2] = x.z; vv[p][3] = x.w;
+            } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) vv[p][q] = r < n ? load_as_f32(a.v, v0 + (size_t)r * v_row + c4 + q, k_in_dt) : 0.f;
+                for (int q = 0; q < 4; ++q) vv[p][q] = load_as_f32(a.v, v0 + (size_t)rc * v_row + c4 + q, k_in_dt);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) vv[p][q] = r < n ? vv[p][q] : 0.f;
         }
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
@@ -977,6 +990,13 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
         for (int e = 0; e < 4; ++e) dK[t][e] *= sRc[r0 + 4 * lg + e];
     f4 dPG[2], Ep[2], dA[2];
     {
+        // this lane's P values, loaded before the products and with no branch (the C x C tile holds every (r, s))
+        float pw[2][4];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                pw[t][e] = a.w.P[ci * C * C + (r0 + 4 * lg + e) * C + 32 * ch + 16 * t + li];
         f4 dp[2] = {zero4(), zero4()};
         dA[0] = dA[1] = zero4();
         mma_strip<D, 2>(dp, R2 + r0 * LD, LD, 1, RX + 32 * ch * LD, 1, LD, 16 * LD, l);
@@ -992,7 +1012,7 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
             for (int e = 0; e < 4; ++e) {
                 const int r = r0 + 4 * lg + e, s2 = 32 * ch + 16 * t + li;
                 const float pv = s2 <= r ? dp[t][e] : 0.f;
-                Ep[t][e] = s2 < r ? pv * a.w.P[ci * C * C + r * C + s2] : 0.f;
+                Ep[t][e] = s2 < r ? pv * pw[t][e] : 0.f;
                 dPG[t][e] = s2 <= r ? pv * expf((float)(sG[r] - sG[s2])) : 0.f;
             }
     }
@@ -1081,8 +1101,11 @@ __device__ __forceinline__ void bwd_local_f32_head(const Args &a, int c, int hk,
         for (int p = 0; p < 4; ++p) {
             const int i = l + 64 * p, r = r0 + (i >> 4), c4 = 64 * ch + 4 * (i & 15);
             const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            prq[p] = r < n ? *reinterpret_cast<const float4 *>(sum_row + (size_t)r * park_row + c4) : z;
-            prk[p] = r < n ? *reinterpret_cast<const float4 *>(sum_row + (size_t)r * park_row + D + c4) : z;
+            const int rc = min(r, n - 1);  // rows past n read row n - 1, unused: no load under a branch
+            const float4 xq = *reinterpret_cast<const float4 *>(sum_row + (size_t)rc * park_row + c4);
+            const float4 xk = *reinterpret_cast<const float4 *>(sum_row + (size_t)rc * park_row + D + c4);
+            prq[p] = r < n ? xq : z;
+            prk[p] = r < n ? xk : z;
         }
     }
     chunk_dg_dbeta<NTB>(sE, sRow, sLast, 1.f, sScan, a, b, hv, t0, n, tid);
