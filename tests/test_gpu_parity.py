@@ -240,6 +240,23 @@ def test_recurrent_wide_grid_against_oracle(dev, monkeypatch, gate_ndim):
             assert nerr(a, b) <= 1e-4, (bi, hk, n, nerr(a, b))
 
 
+@pytest.mark.parametrize("form", ["recurrent", "chunk"])
+def test_fp16_inputs_fp32_state(dev, monkeypatch, form):
+    """fp16 q/k/v with fp32 state, gates and cotangent: the kernels that read the input dtype from their arguments
+    (the recurrent form's and the fp32 chunked set's run-time dtype variants), against the oracle fed the same
+    fp16-rounded inputs.  The arithmetic is fp32, so y, S_T, dg, dbeta and dS0 (fp32) meet the fp32 bar; dq, dk and
+    dv come out in the input dtype, within fp16's rounding (2^-11 of the largest value) of the oracle."""
+    monkeypatch.setenv("GDN_FORM", form)
+    c = _workload(200, B=1, seed=6, heads=(2, 4))
+    hf = lambda x: torch.tensor(x).half().float().numpy()
+    c = dict(c, q=hf(c["q"]), k=hf(c["k"]), v=hf(c["v"]), dstate=np.full_like(c["state"], 0.01))
+    got = run_gpu(c, dev, 64, dtype=torch.float16)
+    want = oracle_vjp(c, 64)
+    for n, a, b in zip(OUT_NAMES, got, want):
+        bar = 1e-3 if n in ("dq", "dk", "dv") else 1e-4
+        assert nerr(a, b) <= bar, (form, n, nerr(a, b))
+
+
 def test_chunk_invariance_long(dev, monkeypatch):
     """The recurrent form's snapshot interval is an implementation detail: chunk 64 vs 256 vs 1000 agree."""
     monkeypatch.setenv("GDN_FORM", "recurrent")
