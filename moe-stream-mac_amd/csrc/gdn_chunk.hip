@@ -70,8 +70,8 @@ __device__ __forceinline__ void load_tile(float *dst, int lds_stride, const void
 #pragma unroll
             for (int p = 0; p < NB; ++p) {
                 const int v = tid + (p0 + p) * NTH, r = v / VPR, c4 = (v - r * VPR) * 4;
-                const float4 x =
-                    *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + min(r, n - 1) * src_stride + c4);
+                const float *row = static_cast<const float *>(src) + min(r, n - 1) * src_stride;
+                const float4 x = *reinterpret_cast<const float4 *>(row + c4);
                 buf[p] = r < n ? x : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
@@ -93,8 +93,8 @@ __device__ __forceinline__ void load_tile(float *dst, int lds_stride, const void
 #pragma unroll
             for (int p = 0; p < NB; ++p) {
                 const int v = tid + (p0 + p) * NTH, r = v / VPR, c8 = (v - r * VPR) * 8;
-                const uint4 x =
-                    *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(src) + min(r, n - 1) * src_stride + c8);
+                const uint16_t *row = static_cast<const uint16_t *>(src) + min(r, n - 1) * src_stride;
+                const uint4 x = *reinterpret_cast<const uint4 *>(row + c8);
                 buf[p] = r < n ? x : make_uint4(0u, 0u, 0u, 0u);
             }
 #pragma unroll

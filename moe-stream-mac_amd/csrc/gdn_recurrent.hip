@@ -84,8 +84,9 @@ __device__ __forceinline__ void stage_fetch(TokRegs<E, VEC, TT, WITH_DY, NT, R> 
 }
 
 template <int E, bool VEC, int TT, bool WITH_DY, int NT, int R>
-__device__ __forceinline__ void stage_store(StageBuf<E, VEC, TT, R> &sb, const TokRegs<E, VEC, TT, WITH_DY, NT, R> &r,
-                                            bool masked, int n, int Dk, int Dv, int rb, int gate) {
+__device__ __forceinline__ void stage_store(StageBuf<E, VEC, TT, R> &sb,
+                                            const TokRegs<E, VEC, TT, WITH_DY, NT, R> &r, bool masked, int n, int Dk,
+                                            int Dv, int rb, int gate) {
     using TR = TokRegs<E, VEC, TT, WITH_DY, NT, R>;
     const int tid = threadIdx.x;
 #pragma unroll
@@ -184,15 +185,17 @@ __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
     int until_snap = a.chunk;  // tokens left before the next chunk boundary
     // the next stage's tokens are loaded into registers while this one computes
     TokRegs<E, VEC, FWD_TT, false, THREADS, ROWS> tr;
-    stage_fetch<E, VEC, FWD_TT, false, DT, DT, THREADS, ROWS>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb, 0, T,
-                                               a.Hk, a.Hv, Dk, Dv, a.in_dt, 0);
+    auto fetch = [&](int t0) {
+        stage_fetch<E, VEC, FWD_TT, false, DT, DT, THREADS, ROWS>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b,
+                                                                  hv, hk, rb, t0, T, a.Hk, a.Hv, Dk, Dv, a.in_dt, 0);
+    };
+    fetch(0);
     for (int t0 = 0; t0 < T; t0 += FWD_TT) {
         const int n = min(FWD_TT, T - t0);
         __syncthreads();
         stage_store<E, VEC, FWD_TT, false, THREADS, ROWS>(sb, tr, a.mask != nullptr, n, Dk, Dv, rb, a.gate);
         __syncthreads();
-        stage_fetch<E, VEC, FWD_TT, false, DT, DT, THREADS, ROWS>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, nullptr, b, hv, hk, rb,
-                                                   t0 + FWD_TT, T, a.Hk, a.Hv, Dk, Dv, a.in_dt, 0);
+        fetch(t0 + FWD_TT);
         auto token = [&](const int tt) {
             float cand[E], kk[E], qq[E], delta;
             row_step<E, VEC, FWD_TT, ROWS>(sb, tt, grp, c, S, cand, kk, delta);
@@ -252,7 +255,7 @@ __global__ __launch_bounds__(64 * NW) void rec_bwd_kernel(RecBwdArgs a) {
     constexpr int NQ = VEC ? 3 : 2;
     constexpr int NT = 64 * NW, R = 4 * NW;
     __shared__ __align__(16) StageBuf<E, VEC, CS, R> sb;
-    __shared__ __align__(16) float s_red[CS][NW][NQ * DKP];  // per-wave sums over its 4 rows: dq | dk | (dg per channel)
+    __shared__ __align__(16) float s_red[CS][NW][NQ * DKP];  // per wave, sums over its 4 rows: dq | dk | (dg / channel)
     __shared__ float s_row[CS][R][3];                        // per row: dv, dbeta, dg (scalar gate)
 
     const int rb = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
@@ -276,11 +279,11 @@ __global__ __launch_bounds__(64 * NW) void rec_bwd_kernel(RecBwdArgs a) {
     }
     const int nch = (T + a.chunk - 1) / a.chunk;
     // Stages in order: per chunk (last first), the replay sub-chunks 0 .. nsub-2, then the sub-chunks nsub-1 .. 0
-    // with dY.  Each stage's tokens are loaded into registers during the one before (its first token: next_t0).
+    // with dY.  Each stage's tokens are loaded into registers during the stage before.
     TokRegs<E, VEC, CS, true, NT, R> tr;
     auto fetch = [&](int t0) {
-        stage_fetch<E, VEC, CS, true, DT, DT, NT, R>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, a.dy, b, hv, hk, rb, t0, T,
-                                              a.Hk, Hv, Dk, Dv, a.in_dt, a.dy_dt);
+        stage_fetch<E, VEC, CS, true, DT, DT, NT, R>(tr, a.q, a.k, a.v, a.g, a.beta, a.mask, a.dy, b, hv, hk, rb, t0,
+                                                     T, a.Hk, Hv, Dk, Dv, a.in_dt, a.dy_dt);
     };
     fetch((nch - 1) * a.chunk);
     for (int ci = nch - 1; ci >= 0; --ci) {
@@ -671,8 +674,8 @@ void launch_rec_bwd_reduce(const RecBwdArgs &a, hipStream_t st) {
     const size_t ng = (size_t)a.B * a.T * a.Hv * (a.gate == GATE_DECAY_VEC ? a.Dk : 1);
     if (nqk) hipLaunchKernelGGL(rec_bwd_reduce_qk, dim3((unsigned)((nqk + 255) / 256)), dim3(256), 0, st, a);
     if (!ng) return;
-    const bool vec4 = a.gate == GATE_DECAY_VEC && (a.Dk & 3) == 0 &&
-                      (reinterpret_cast<uintptr_t>(a.part_gv) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.dg) & 15) == 0;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(a.part_gv) | reinterpret_cast<uintptr_t>(a.dg)) & 15) == 0;
+    const bool vec4 = a.gate == GATE_DECAY_VEC && (a.Dk & 3) == 0 && aligned;
     if (vec4) {
         const size_t N = (size_t)a.B * a.T * a.Hv;
         const int per = 256 / (a.Dk >> 2);
