@@ -18,6 +18,8 @@ Workloads (one GPU; the default is the T=4096 configuration the metric is quoted
   vgate_bf16_b4_t4096
                   bf16_b4_t4096 with one decay per key channel (g [B, T, Hv, D], in decay space); runs the
                   token-recurrent form
+  decode_bf16_b64 one decode step (gdn_decode_step: a token of each of 64 sequences, forward only, the fp32
+                  state [64, 32, 128, 128] read and written in place); bound by the state's HBM traffic
   stream_ops_bf16_b2_t8192
                   the streaming kernels around the recurrence on block-shaped bf16 inputs (B=2, T=8192, Hk=16,
                   Hv=32, D=128): fused conv + SiLU + split + q/k L2 norm, plain conv + SiLU (8192 channels), q/k L2
@@ -63,8 +65,14 @@ def algo_model(w, form="chunk"):
     The recurrent form (masks, vector gates) computes the recurrence itself, 27 D^2 flops per head-token on fp32
     VALU, whatever the input dtype; its bytes follow the dtype as above.
     Per-channel (vector) gates read g and write dg per key channel: 4 * 2 Hv D bytes in place of 4 * 2 Hv.
-    The per-sequence state traffic (S0, S_T, dS_T, dS0) and snapshot traffic are not algorithmic."""
+    The per-sequence state traffic (S0, S_T, dS_T, dS0) and snapshot traffic are not algorithmic, except in a decode
+    step (one token per sequence, forward only), where reading and writing the fp32 state is the work:
+    4 * 2 Hv D^2 + dtype * (2 Hk D + 2 Hv D) + 4 * 2 Hv bytes and 7 D^2 Hv flops per token."""
     Hk, Hv, D, C = w["Hk"], w["Hv"], w["D"], CK_C
+    if w.get("decode"):
+        b = 2 if w["dtype"] == "bf16" else 4
+        return (4 * 2 * Hv * D * D + b * (2 * Hk * D + 2 * Hv * D) + 4 * 2 * Hv, {"fp32": 7 * D * D * Hv},
+                PEAK_FP32_TFLOPS)
     if form == "recurrent":
         b = 2 if w["dtype"] == "bf16" else 4
         gates = 4 * 2 * Hv * (D + 1) if w.get("vector_gate") else 4 * 4 * Hv
@@ -151,6 +159,8 @@ def kernel_model(name, B, T, Hk, Hv, D, in_b):
         return 0, tokh * D * 3 * in_b
     if name == "grms_bwd":
         return 0, tokh * D * 5 * in_b
+    if name == "rec_decode":  # one token per sequence: the fp32 state read and written, q/k/v/y, the gates
+        return 7 * tokh * D * D, B * (2 * Hv * D * D * 4 + (2 * Hk * D + 2 * Hv * D) * in_b + 2 * Hv * 4)
     return 0, 0
 
 WORKLOADS = {
@@ -163,6 +173,7 @@ WORKLOADS = {
                                  masked_tail=0.1),
     "vgate_bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
                                 vector_gate=True),
+    "decode_bf16_b64": dict(B=64, T=1, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.02, decode=True),
     "stream_ops_bf16_b2_t8192": dict(B=2, T=8192, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
                                      ops=True),
     "block_bf16_b2_t8192": dict(B=2, T=8192, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
@@ -380,6 +391,12 @@ def main():
 
         def step():
             return torch.autograd.grad(outputs(), leaves, cot)
+    elif "decode" in w:
+        x = {n: t[:, 0].contiguous() if n not in ("state",) else t for n, t in make_inputs(w, dev).items()}
+
+        def step():  # one token of each sequence, the state updated in place
+            return gdn_engine.decode_step(x["q"], x["k"], x["v"], x["g"], x["beta"], x["state"], x["state"],
+                                          log_gate=True, out_dtype=x["q"].dtype)
     else:
         x = make_inputs(w, dev)
         out_dtype = x["q"].dtype

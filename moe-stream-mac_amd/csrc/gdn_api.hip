@@ -817,7 +817,7 @@ int gdn_decode_step(const void *q, const void *k, const void *v, const float *g,
                  B, 1, Hk, Hv, Dk, Dv, 1, in_dtype, out_dtype, gate_kind};
     {
         Timed tm("rec_decode", st);
-        launch_rec_fwd(a, st);
+        launch_rec_decode(a, st);
     }
     return check_launch(st, "gdn_decode_step");
 }

@@ -102,6 +102,7 @@ int rec_max_sub(int T, int chunk);
 size_t rec_sub_floats(int B, int Hv, int Dk, int Dv, int T, int chunk, int gate);
 
 void launch_rec_fwd(const RecFwdArgs &a, hipStream_t st);
+void launch_rec_decode(const RecFwdArgs &a, hipStream_t st);  // T = 1, no mask, no snapshots
 void launch_rec_bwd(const RecBwdArgs &a, hipStream_t st);
 void launch_rec_bwd_reduce(const RecBwdArgs &a, hipStream_t st);
 void launch_copy_or_zero(float *dst, const float *src, size_t n, hipStream_t st);

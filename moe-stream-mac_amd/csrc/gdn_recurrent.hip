@@ -245,6 +245,86 @@ __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------------- decode
+
+// One token of B sequences (gdn_decode_step, engine/src/gdn.c:63-108): the forward step with every input read
+// straight into registers, no LDS and no barrier, so the launch streams the state.  A lane loads its E channels of
+// k and q (clamped, zero past Dk), its row's v, the head's beta and decay, and its E state elements; it computes in
+// the forward kernel's order of operations (the same results) and writes the state back, which may be in place
+// (a lane reads its elements before writing them).  Without state0 the state is zero: state_T is read in its place
+// (in bounds, unused), so no load sits under a branch.
+template <int E, bool VEC, int DT>
+__global__ __launch_bounds__(THREADS) void rec_decode_kernel(RecFwdArgs a) {
+    const int rb = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, grp = tid >> 4, c = tid & 15;
+    const int Dk = a.Dk, Dv = a.Dv, row = rb * ROWS + grp, rowc = min(row, Dv - 1);
+    const bool row_ok = row < Dv, has0 = a.state0 != nullptr;
+    const int hk = hv / (a.Hv / a.Hk), xdt = DT >= 0 ? DT : a.in_dt;
+    const size_t head = (size_t)b * a.Hv + hv, kq0 = ((size_t)b * a.Hk + hk) * Dk;
+    const size_t row_off = (head * Dv + rowc) * Dk;
+    const float *s_in = has0 ? a.state0 : a.state_T;
+    // full rows of 16-byte pieces: E % 4 == 0, Dk = 16 E, both state rows aligned
+    const bool wide = E % 4 == 0 && Dk == 16 * E &&
+                      ((reinterpret_cast<uintptr_t>(s_in) | reinterpret_cast<uintptr_t>(a.state_T)) & 15) == 0;
+    float kk[E], qq[E], dec[E], S[E];
+    const float vr = load_as_f32(a.v, head * Dv + rowc, xdt), bt = a.beta[head];
+    const float gs = VEC ? 1.f : a.g[head];
+    const float dsc = a.gate == GATE_LOG ? expf(gs) : gs;
+    if (wide) {
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+            const float4 x = *reinterpret_cast<const float4 *>(s_in + row_off + c * E + e);
+            S[e] = x.x; S[e + 1] = x.y; S[e + 2] = x.z; S[e + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) S[e] = s_in[row_off + min(c * E + e, Dk - 1)];
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int j = c * E + e, jc = min(j, Dk - 1);
+        const bool ok = j < Dk;
+        const float kx = load_as_f32(a.k, kq0 + jc, xdt), qx = load_as_f32(a.q, kq0 + jc, xdt);
+        kk[e] = ok ? kx : 0.f;
+        qq[e] = ok ? qx : 0.f;
+        if constexpr (VEC) {
+            const float gx = a.g[head * Dk + jc];
+            dec[e] = ok ? gx : 1.f;
+        } else {
+            dec[e] = dsc;
+        }
+        S[e] = has0 && ok && row_ok ? S[e] : 0.f;
+    }
+    float A[E], kv = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        A[e] = S[e] * dec[e];
+        kv = fmaf(A[e], kk[e], kv);
+    }
+    kv = row16_allreduce(kv);
+    const float delta = ((row_ok ? vr : 0.f) - kv) * bt;
+    float y = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        S[e] = fmaf(delta, kk[e], A[e]);
+        y = fmaf(S[e], qq[e], y);
+    }
+    y = row16_allreduce(y);
+    if (row_ok) {
+        if (wide) {
+#pragma unroll
+            for (int e = 0; e < E; e += 4)
+                *reinterpret_cast<float4 *>(a.state_T + row_off + c * E + e) =
+                    make_float4(S[e], S[e + 1], S[e + 2], S[e + 3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                if (c * E + e < Dk) a.state_T[row_off + c * E + e] = S[e];
+        }
+        if (c == 0) store_from_f32(a.y, head * Dv + row, y, a.out_dt);
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------- backward
 
 // NW waves per workgroup, 4 NW value rows (4 per wave).  MASKED as in the forward.
@@ -616,6 +696,32 @@ static void launch_fwd_e(const RecFwdArgs &a, hipStream_t st) {
     if (a.in_dt == DT_BF16) launch_fwd_et<E, DT_BF16>(a, st);
     else if (a.in_dt == DT_F32) launch_fwd_et<E, DT_F32>(a, st);
     else launch_fwd_et<E, -1>(a, st);
+}
+
+template <int E>
+static void launch_decode_e(const RecFwdArgs &a, hipStream_t st) {
+    const dim3 grid(rec_num_row_blocks(a.Dv), a.Hv, a.B);
+    const bool vec = a.gate == GATE_DECAY_VEC;
+    if (a.in_dt == DT_BF16) {
+        if (vec) hipLaunchKernelGGL((rec_decode_kernel<E, true, DT_BF16>), grid, dim3(THREADS), 0, st, a);
+        else hipLaunchKernelGGL((rec_decode_kernel<E, false, DT_BF16>), grid, dim3(THREADS), 0, st, a);
+    } else if (a.in_dt == DT_F32) {
+        if (vec) hipLaunchKernelGGL((rec_decode_kernel<E, true, DT_F32>), grid, dim3(THREADS), 0, st, a);
+        else hipLaunchKernelGGL((rec_decode_kernel<E, false, DT_F32>), grid, dim3(THREADS), 0, st, a);
+    } else {
+        if (vec) hipLaunchKernelGGL((rec_decode_kernel<E, true, -1>), grid, dim3(THREADS), 0, st, a);
+        else hipLaunchKernelGGL((rec_decode_kernel<E, false, -1>), grid, dim3(THREADS), 0, st, a);
+    }
+}
+
+void launch_rec_decode(const RecFwdArgs &a, hipStream_t st) {
+    switch (pick_lane_width(a.Dk)) {
+        case 1: launch_decode_e<1>(a, st); break;
+        case 2: launch_decode_e<2>(a, st); break;
+        case 4: launch_decode_e<4>(a, st); break;
+        case 8: launch_decode_e<8>(a, st); break;
+        default: launch_decode_e<16>(a, st); break;
+    }
 }
 
 void launch_rec_fwd(const RecFwdArgs &a, hipStream_t st) {
