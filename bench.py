@@ -18,6 +18,9 @@ Workloads (one GPU; the default is the T=4096 configuration the metric is quoted
   vgate_bf16_b4_t4096
                   bf16_b4_t4096 with one decay per key channel (g [B, T, Hv, D], in decay space); runs the
                   token-recurrent form
+  fwd_bf16_b4_t4096
+                  the forward alone, as frozen layers and prefill run it (no autograd graph, no saved tiles),
+                  bf16_b4_t4096's shape
   decode_bf16_b64 one decode step (gdn_decode_step: a token of each of 64 sequences, forward only, the fp32
                   state [64, 32, 128, 128] read and written in place); bound by the state's HBM traffic
   stream_ops_bf16_b2_t8192
@@ -65,10 +68,18 @@ def algo_model(w, form="chunk"):
     The recurrent form (masks, vector gates) computes the recurrence itself, 27 D^2 flops per head-token on fp32
     VALU, whatever the input dtype; its bytes follow the dtype as above.
     Per-channel (vector) gates read g and write dg per key channel: 4 * 2 Hv D bytes in place of 4 * 2 Hv.
+    A forward-only call (no saved state) reads q, k, v, g, beta and writes y, with the forward's third of the
+    contractions (10 C D + 6 D^2 per head-token on the chunked form).
     The per-sequence state traffic (S0, S_T, dS_T, dS0) and snapshot traffic are not algorithmic, except in a decode
     step (one token per sequence, forward only), where reading and writing the fp32 state is the work:
     4 * 2 Hv D^2 + dtype * (2 Hk D + 2 Hv D) + 4 * 2 Hv bytes and 7 D^2 Hv flops per token."""
     Hk, Hv, D, C = w["Hk"], w["Hv"], w["D"], CK_C
+    if w.get("forward_only"):  # a forward with no saved state (frozen layers, prefill): reads q/k/v/g/beta, writes y
+        b = 2 if w["dtype"] == "bf16" else 4
+        nbytes = b * (2 * Hk * D + 2 * Hv * D) + 4 * 2 * Hv
+        if form == "chunk" and w["dtype"] == "bf16":
+            return nbytes, {"bf16_intra_chunk": 10 * C * D * Hv, "bf16_state": 6 * D * D * Hv}, PEAK_BF16_TFLOPS
+        return nbytes, {"fp32": 7 * D * D * Hv}, PEAK_FP32_TFLOPS
     if w.get("decode"):
         b = 2 if w["dtype"] == "bf16" else 4
         return (4 * 2 * Hv * D * D + b * (2 * Hk * D + 2 * Hv * D) + 4 * 2 * Hv, {"fp32": 7 * D * D * Hv},
@@ -173,6 +184,8 @@ WORKLOADS = {
                                  masked_tail=0.1),
     "vgate_bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
                                 vector_gate=True),
+    "fwd_bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
+                              forward_only=True),
     "decode_bf16_b64": dict(B=64, T=1, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.02, decode=True),
     "stream_ops_bf16_b2_t8192": dict(B=2, T=8192, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
                                      ops=True),
@@ -397,6 +410,12 @@ def main():
         def step():  # one token of each sequence, the state updated in place
             return gdn_engine.decode_step(x["q"], x["k"], x["v"], x["g"], x["beta"], x["state"], x["state"],
                                           log_gate=True, out_dtype=x["q"].dtype)
+    elif "forward_only" in w:
+        x = make_inputs(w, dev)
+
+        def step():  # no autograd graph, no saved tiles: y and the final state only
+            return gdn_engine.recurrence(x["q"], x["k"], x["v"], x["g"], x["beta"], x["state"], None,
+                                         chunk=w["chunk"], log_gate=True, output_dtype=x["q"].dtype, need_grad=False)
     else:
         x = make_inputs(w, dev)
         out_dtype = x["q"].dtype
