@@ -4,7 +4,7 @@
 A step is one forward of the delta-rule recurrence over a batch of synthetic input plus its full VJP (dq, dk,
 dv, dg, dbeta, dS0), with every input already resident in HBM.  Prints ONE JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--workload NAME] [--chunk N] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--batch B] [--chunk N] [--no-cpu-baseline]
 
 Workloads (one GPU; the default is the T=4096 configuration the metric is quoted on):
   bf16_b4_t4096   B=4, T=4096, Hk=16, Hv=32, D=128, bf16 q/k/v/dO, fp32 state and gates, chunk 64
@@ -341,6 +341,7 @@ def main():
     ap.add_argument("--workload", default="bf16_b4_t4096", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=1024)
+    ap.add_argument("--batch", type=int, default=0, help="override the workload's batch size B")
     ap.add_argument("--chunk", type=int, default=0,
                     help="override the workload's chunk (the snapshot interval of the recurrent form and of the "
                          "checkpointed chunked form)")
@@ -367,6 +368,8 @@ def main():
     w = dict(WORKLOADS[args.workload])
     if args.chunk:
         w["chunk"] = args.chunk
+    if args.batch:
+        w["B"] = args.batch
     dev = torch.device("cuda:0")
     gdn_lib.load()
     if args.copy_calibration:
