@@ -247,6 +247,33 @@ __global__ __launch_bounds__(THREADS) void rec_fwd_kernel(RecFwdArgs a) {
 
 // ---------------------------------------------------------------------------------------------------- decode
 
+// E consecutive elements from index i0 (16-byte aligned) as float: 16-byte loads when the dtype is fixed at compile
+// time (8 bf16 or 4 fp32 per load), element loads otherwise.
+template <int E, int DT>
+__device__ __forceinline__ void load_span(float (&dst)[E], const void *p, size_t i0, int dt) {
+    if constexpr (DT == DT_BF16 && E % 8 == 0) {
+#pragma unroll
+        for (int e = 0; e < E; e += 8) {
+            const uint4 x = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i0 + e);
+            const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                dst[e + 2 * u] = __uint_as_float(w[u] << 16);
+                dst[e + 2 * u + 1] = __uint_as_float(w[u] & 0xffff0000u);
+            }
+        }
+    } else if constexpr (DT == DT_F32 && E % 4 == 0) {
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+            const float4 x = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i0 + e);
+            dst[e] = x.x; dst[e + 1] = x.y; dst[e + 2] = x.z; dst[e + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) dst[e] = load_as_f32(p, i0 + e, dt);
+    }
+}
+
 // One token of B sequences (gdn_decode_step, engine/src/gdn.c:63-108): the forward step with every input read
 // straight into registers, no LDS and no barrier, so the launch streams the state.  A lane loads its E channels of
 // k and q (clamped, zero past Dk), its row's v, the head's beta and decay, and its E state elements; it computes in
@@ -264,29 +291,36 @@ __global__ __launch_bounds__(THREADS) void rec_decode_kernel(RecFwdArgs a) {
     const size_t row_off = (head * Dv + rowc) * Dk;
     const float *s_in = has0 ? a.state0 : a.state_T;
     // full rows of 16-byte pieces: E % 4 == 0, Dk = 16 E, both state rows aligned
-    const bool wide = E % 4 == 0 && Dk == 16 * E &&
-                      ((reinterpret_cast<uintptr_t>(s_in) | reinterpret_cast<uintptr_t>(a.state_T)) & 15) == 0;
+    const uintptr_t align = reinterpret_cast<uintptr_t>(s_in) | reinterpret_cast<uintptr_t>(a.state_T) |
+                            reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.q);
+    const bool wide = E % 4 == 0 && Dk == 16 * E && (align & 15) == 0;
     float kk[E], qq[E], dec[E], S[E];
     const float vr = load_as_f32(a.v, head * Dv + rowc, xdt), bt = a.beta[head];
     const float gs = VEC ? 1.f : a.g[head];
     const float dsc = a.gate == GATE_LOG ? expf(gs) : gs;
-    if (wide) {
+    if (wide) {  // 16-byte pieces of the state row and of k and q (every channel valid)
 #pragma unroll
         for (int e = 0; e < E; e += 4) {
             const float4 x = *reinterpret_cast<const float4 *>(s_in + row_off + c * E + e);
             S[e] = x.x; S[e + 1] = x.y; S[e + 2] = x.z; S[e + 3] = x.w;
         }
+        load_span<E, DT>(kk, a.k, kq0 + c * E, xdt);
+        load_span<E, DT>(qq, a.q, kq0 + c * E, xdt);
     } else {
 #pragma unroll
-        for (int e = 0; e < E; ++e) S[e] = s_in[row_off + min(c * E + e, Dk - 1)];
+        for (int e = 0; e < E; ++e) {
+            const int jc = min(c * E + e, Dk - 1);
+            S[e] = s_in[row_off + jc];
+            kk[e] = load_as_f32(a.k, kq0 + jc, xdt);
+            qq[e] = load_as_f32(a.q, kq0 + jc, xdt);
+        }
     }
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int j = c * E + e, jc = min(j, Dk - 1);
         const bool ok = j < Dk;
-        const float kx = load_as_f32(a.k, kq0 + jc, xdt), qx = load_as_f32(a.q, kq0 + jc, xdt);
-        kk[e] = ok ? kx : 0.f;
-        qq[e] = ok ? qx : 0.f;
+        kk[e] = ok ? kk[e] : 0.f;
+        qq[e] = ok ? qq[e] : 0.f;
         if constexpr (VEC) {
             const float gx = a.g[head * Dk + jc];
             dec[e] = ok ? gx : 1.f;
