@@ -39,6 +39,21 @@ __device__ __forceinline__ void store_from_f32(void *p, size_t i, float x, int d
     }
 }
 
+// Four consecutive elements from element i (i a multiple of 4, the buffer 16-byte aligned): one 16-byte store in
+// fp32, one 8-byte store of packed bf16, element stores in fp16.
+__device__ __forceinline__ void store4_from_f32(void *p, size_t i, float4 x, int dt) {
+    if (dt == DT_F32) {
+        *reinterpret_cast<float4 *>(static_cast<float *>(p) + i) = x;
+    } else if (dt == DT_BF16) {
+        const uint32_t lo = f32_to_bf16_cvt(x.x) | ((uint32_t)f32_to_bf16_cvt(x.y) << 16);
+        const uint32_t hi = f32_to_bf16_cvt(x.z) | ((uint32_t)f32_to_bf16_cvt(x.w) << 16);
+        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(p) + i) = make_uint2(lo, hi);
+    } else {
+        __half *h = static_cast<__half *>(p) + i;
+        h[0] = __float2half(x.x); h[1] = __float2half(x.y); h[2] = __float2half(x.z); h[3] = __float2half(x.w);
+    }
+}
+
 // DPP lane moves inside a row of 16 lanes.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float x) {

@@ -651,6 +651,29 @@ __global__ __launch_bounds__(256) void rec_bwd_reduce_gates(RecBwdArgs a) {
     a.dg[i] = dg;
 }
 
+// Dk % 4 == 0 and 16-byte aligned buffers: four channels per thread (float4 partial loads, the row blocks and value
+// heads summed in the same order as above), a workgroup over 256 / (Dk / 4) token rows of one key head (grid.y).
+__global__ __launch_bounds__(256) void rec_bwd_reduce_qk_vec4(RecBwdArgs a) {
+    const int Dk4 = a.Dk >> 2, per = 256 / Dk4, hk = blockIdx.y;
+    const int tl = threadIdx.x / Dk4, j4 = threadIdx.x - tl * Dk4;
+    const size_t BT = (size_t)a.B * a.T, bt = (size_t)blockIdx.x * per + tl;
+    if (tl >= per || bt >= BT) return;
+    const int rep = a.Hv / a.Hk;
+    float4 sq = make_float4(0.f, 0.f, 0.f, 0.f), sk = sq;
+    for (int rb = 0; rb < a.nrb; ++rb) {
+        for (int r = 0; r < rep; ++r) {
+            const size_t tok = ((size_t)rb * BT + bt) * a.Hv + hk * rep + r;
+            const float4 *p = reinterpret_cast<const float4 *>(a.part_qk + tok * 2 * a.Dk) + j4;
+            const float4 x = p[0], y = p[Dk4];
+            sq = make_float4(sq.x + x.x, sq.y + x.y, sq.z + x.z, sq.w + x.w);
+            sk = make_float4(sk.x + y.x, sk.y + y.y, sk.z + y.z, sk.w + y.w);
+        }
+    }
+    const size_t i = (bt * a.Hk + hk) * a.Dk + 4 * j4;
+    store4_from_f32(a.dq, i, sq, a.grad_dt);
+    store4_from_f32(a.dk, i, sk, a.grad_dt);
+}
+
 // Per-channel gates with Dk % 4 == 0 and 16-byte aligned rows: four channels per thread (float4 loads and
 // stores, the row blocks summed in the same order as above), a workgroup over 256 / (Dk / 4) token-heads.
 __global__ __launch_bounds__(256) void rec_bwd_reduce_gates_vec4(RecBwdArgs a) {
@@ -812,7 +835,16 @@ void launch_rec_bwd(const RecBwdArgs &a, hipStream_t st) {
 void launch_rec_bwd_reduce(const RecBwdArgs &a, hipStream_t st) {
     const size_t nqk = (size_t)a.B * a.T * a.Hk * a.Dk;
     const size_t ng = (size_t)a.B * a.T * a.Hv * (a.gate == GATE_DECAY_VEC ? a.Dk : 1);
-    if (nqk) hipLaunchKernelGGL(rec_bwd_reduce_qk, dim3((unsigned)((nqk + 255) / 256)), dim3(256), 0, st, a);
+    const bool qk4 = (a.Dk & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.part_qk) | reinterpret_cast<uintptr_t>(a.dq) |
+                                          reinterpret_cast<uintptr_t>(a.dk)) & 15) == 0;
+    if (nqk && qk4) {
+        const int per = 256 / (a.Dk >> 2);
+        const size_t BT = (size_t)a.B * a.T;
+        hipLaunchKernelGGL(rec_bwd_reduce_qk_vec4, dim3((unsigned)((BT + per - 1) / per), a.Hk), dim3(256), 0, st,
+                           a);
+    } else if (nqk) {
+        hipLaunchKernelGGL(rec_bwd_reduce_qk, dim3((unsigned)((nqk + 255) / 256)), dim3(256), 0, st, a);
+    }
     if (!ng) return;
     const bool aligned = ((reinterpret_cast<uintptr_t>(a.part_gv) | reinterpret_cast<uintptr_t>(a.dg)) & 15) == 0;
     const bool vec4 = a.gate == GATE_DECAY_VEC && (a.Dk & 3) == 0 && aligned;
