@@ -2066,12 +2066,14 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
     // V as 8-token x 2-channel blocks (one per thread) for the transposed tile, kept in registers until Q is dead
     static_assert((C / 8) * (D / 2) == NTP, "one V block per thread");
     const int vb = tid / (D / 2), vc = 2 * (tid - vb * (D / 2));
+    // rows past n read row n - 1 and are zeroed after: no load sits under a branch
     uint32_t vr[8];
 #pragma unroll
     for (int rr = 0; rr < 8; ++rr) {
         const int s2 = 8 * vb + rr;
-        vr[rr] = s2 < n ? *reinterpret_cast<const uint32_t *>(static_cast<const bfr *>(a.v) + v0 + s2 * v_row + vc)
-                        : 0u;
+        const uint32_t x =
+            *reinterpret_cast<const uint32_t *>(static_cast<const bfr *>(a.v) + v0 + min(s2, n - 1) * v_row + vc);
+        vr[rr] = s2 < n ? x : 0u;
     }
     // K and Q rows (16-byte pieces) and the gates: every load of the phase is issued before the first LDS store
     constexpr int KPER = C * (D / 8) / NTP;
@@ -2080,16 +2082,15 @@ __global__ __launch_bounds__(NTP, 2) void ck_prep_bf16_kernel(Args a) {
 #pragma unroll
     for (int p = 0; p < KPER; ++p) {
         const int pc = tid + p * NTP, r = pc / (D / 8), c8 = (pc - r * (D / 8)) * 8;
-        const size_t o = qk0 + (size_t)r * qk_row + c8;
-        kr[p] = r < n ? *reinterpret_cast<const uint4 *>(static_cast<const bfr *>(a.k) + o) : make_uint4(0u, 0u, 0u, 0u);
-        qr[p] = r < n ? *reinterpret_cast<const uint4 *>(static_cast<const bfr *>(a.q) + o) : make_uint4(0u, 0u, 0u, 0u);
+        const size_t o = qk0 + (size_t)min(r, n - 1) * qk_row + c8;
+        const uint4 xk = *reinterpret_cast<const uint4 *>(static_cast<const bfr *>(a.k) + o);
+        const uint4 xq = *reinterpret_cast<const uint4 *>(static_cast<const bfr *>(a.q) + o);
+        kr[p] = r < n ? xk : make_uint4(0u, 0u, 0u, 0u);
+        qr[p] = r < n ? xq : make_uint4(0u, 0u, 0u, 0u);
     }
-    float bt = 0.f, graw = 1.f;
-    if (tid < n) {
-        const size_t gi = ((size_t)b * a.Ts + t0 + tid) * a.Hv + hv;
-        bt = a.beta[gi];
-        graw = a.g[gi];
-    }
+    const size_t gi = ((size_t)b * a.Ts + t0 + min(tid, n - 1)) * a.Hv + hv;
+    const float b_ld = a.beta[gi], g_ld = a.g[gi];
+    const float bt = tid < n ? b_ld : 0.f, graw = tid < n ? g_ld : 1.f;
 #pragma unroll
     for (int p = 0; p < KPER; ++p) {
         const int pc = tid + p * NTP, r = pc / (D / 8), c8 = (pc - r * (D / 8)) * 8;
