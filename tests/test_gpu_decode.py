@@ -34,7 +34,7 @@ def nerr(a, b):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("Hk,Hv,D,gate", [(2, 4, 128, "log"), (2, 4, 128, "decay"), (1, 3, 32, "vector"),
-                                          (2, 2, 8, "decay")])
+                                          (2, 2, 8, "decay"), (2, 4, 100, "log"), (1, 2, 96, "vector")])
 def test_decode_steps_match_sequence_and_oracle(dev, dtype, Hk, Hv, D, gate):
     import gdn_engine
     B, T = 2, 20
