@@ -40,13 +40,27 @@ template <int K, int NTILES>
 __device__ __forceinline__ void mma_strip(f4 (&acc)[NTILES], const float *A, int asr, int asc, const float *B,
                                           int bsr, int bsc, int btile, int l = threadIdx.x & 63) {
     const int li = l & 15, lg = l >> 4;
+    if constexpr (NTILES == 1 && K % 8 == 0) {
+        // one tile: even and odd k-steps on two accumulators, so two products are in flight instead of one
+        // dependent chain of K / 4
+        f4 odd = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
-    for (int k0 = 0; k0 < K; k0 += 4) {
-        const float av = A[li * asr + (k0 + lg) * asc];
+        for (int k0 = 0; k0 < K; k0 += 8) {
+            const float a0 = A[li * asr + (k0 + lg) * asc], a1 = A[li * asr + (k0 + 4 + lg) * asc];
+            const float b0 = B[(k0 + lg) * bsr + li * bsc], b1 = B[(k0 + 4 + lg) * bsr + li * bsc];
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0], 0, 0, 0);
+            odd = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, odd, 0, 0, 0);
+        }
+        acc[0] += odd;
+    } else {
+#pragma unroll 4
+        for (int k0 = 0; k0 < K; k0 += 4) {
+            const float av = A[li * asr + (k0 + lg) * asc];
 #pragma unroll
-        for (int t = 0; t < NTILES; ++t) {
-            const float bv = B[t * btile + (k0 + lg) * bsr + li * bsc];
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[t], 0, 0, 0);
+            for (int t = 0; t < NTILES; ++t) {
+                const float bv = B[t * btile + (k0 + lg) * bsr + li * bsc];
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[t], 0, 0, 0);
+            }
         }
     }
 }
