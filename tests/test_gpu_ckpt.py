@@ -7,7 +7,8 @@ cotangent and the measured workload at its full length.
   T = 16384 through full-size properties (agreement with chunk = 64, finite gradients, peak memory);
 * forward-only calls (saved = NULL, frozen layers) against the oracle's forward, group by group;
 * the headline workload (B=4, T=4096, Hk=16, Hv=32, bf16 q/k/v/dO, fp32 state) against the fp64 oracle on two
-  key-head groups, with the errors printed at T = 600, 2048 and 4096.
+  key-head groups, with the errors printed at T = 600, 2048 and 4096;
+* fp32 at B=1, T=4096, Hk=16, Hv=32 on both forms against the fp64 oracle at 1e-4 (two key-head groups).
 """
 
 import numpy as np
@@ -45,14 +46,14 @@ def _inputs(B, T, Hk, Hv, seed, s0_std=0.02, bf16=False, dS_T=True):
     return d
 
 
-def _engine(d, dev, chunk, dtype=torch.float32, state_grad=True):
+def _engine(d, dev, chunk, dtype=torch.float32, state_grad=True, form="chunk"):
     """gdn_engine forward + VJP (log gates), grads of y (and of S_T when state_grad)."""
     import gdn_engine
     t = lambda x, dt=torch.float32: torch.tensor(np.asarray(x), device=dev, dtype=dt)
     q, k, v = (t(d[n], dtype).requires_grad_(True) for n in ("q", "k", "v"))
     g, beta, S0 = (t(d[n]).requires_grad_(True) for n in ("g_log", "beta", "state"))
     leaves = [q, k, v, g, beta, S0]
-    y, S = gdn_engine.recurrence(q, k, v, g, beta, S0, None, chunk, log_gate=True, output_dtype=dtype, form="chunk")
+    y, S = gdn_engine.recurrence(q, k, v, g, beta, S0, None, chunk, log_gate=True, output_dtype=dtype, form=form)
     if state_grad:
         grads = torch.autograd.grad([y, S], leaves, [t(d["dy"], dtype), t(d["dS_T"])])
     else:
@@ -304,3 +305,14 @@ def test_headline_config_against_oracle_full_length(dev):
         grow[T] = worst
         for n, e in worst.items():
             assert e <= 1e-2, (T, n, e)
+
+
+@pytest.mark.parametrize("form", ["chunk", "recurrent"])
+def test_fp32_b1_t4096_against_oracle(dev, form):
+    """fp32 throughout, B=1, T=4096, Hk=16, Hv=32, D=128 (32 value heads), S0 ~ N(0, 0.02) and a full exit-state
+    cotangent: two key-head groups of every output against the fp64 oracle, normalised error <= 1e-4, on the
+    chunked form (chunk 64) and on the token-recurrent form (snapshots every 64 tokens)."""
+    d = _inputs(1, 4096, 16, 32, seed=91)
+    print(f"fp32 B=1 T=4096 form={form}", flush=True)
+    got = _engine(d, dev, 64, torch.float32, state_grad=True, form=form)
+    _check_groups(got, d, ((0, 0), (0, 11)), 2, 1e-4, f"fp32 B=1 T=4096 {form}")
