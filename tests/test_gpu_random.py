@@ -1,11 +1,12 @@
 """GPU parity over seeded random combinations of the call's options, each against the fp64 oracle.
 
 Every case draws: the form (chunked, token-recurrent, or the default choice), the head size (128 on the chunked
-form; 32, 64 or 128 on the recurrent one), the input dtype (fp32, or bf16 with an fp32 state), B, T (1..300),
+form; 32, 64 or 128 on the recurrent one), the input dtype (fp32, or bf16 with an fp32 state), B (1..3), T (1..300),
 the GQA layout (Hk 1-2, Hv/Hk 1, 2 or 4), the gate (log or decay space per head, or one decay per key channel on
 the recurrent form), the mask (none, random, or a masked tail), the snapshot interval `chunk` (16, 64, 100, 256),
-a zero or random initial state and a zero or random exit-state cotangent.  Bars: normalised error
-max|gpu - oracle| / max|oracle| <= 1e-4 for fp32 inputs, <= 1e-2 for bf16 inputs, per output.
+a zero or random initial state and a zero or random exit-state cotangent.  Eight more draws run at B = 1,
+T = 1000..3000 (several checkpoint windows and groups).  Bars: normalised error max|gpu - oracle| / max|oracle|
+<= 1e-4 for fp32 inputs, <= 1e-2 for bf16 inputs, per output.
 """
 
 import numpy as np
@@ -18,6 +19,7 @@ pytestmark = pytest.mark.gpu
 
 NAMES = ("y", "S_T", "dq", "dk", "dv", "dg", "dbeta", "dS0")
 N_CASES = 32
+N_LONG = 8  # B = 1, T in 1000..3000: several checkpoint windows and groups
 
 
 @pytest.fixture(scope="module")
@@ -29,15 +31,15 @@ def dev():
     return torch.device("cuda:0")
 
 
-def draw(i):
-    rng = np.random.default_rng(5000 + i)
+def draw(i, long=False):
+    rng = np.random.default_rng((9000 if long else 5000) + i)
     form = ("chunk", "recurrent", "auto")[rng.integers(3)]
     vector = form != "chunk" and rng.random() < 0.3
     if vector:
         form = "recurrent" if form == "auto" else form
     D = 128 if form != "recurrent" else int(rng.choice([32, 64, 128]))
     bf16 = bool(rng.random() < 0.5)
-    B, T = int(rng.integers(1, 4)), int(rng.integers(1, 301))
+    B, T = (1, int(rng.integers(1000, 3001))) if long else (int(rng.integers(1, 4)), int(rng.integers(1, 301)))
     Hk = int(rng.integers(1, 3))
     Hv = Hk * int(rng.choice([1, 2, 4]))
     mask_kind = ("none", "random", "tail")[rng.integers(3)]
@@ -46,7 +48,7 @@ def draw(i):
     s0 = bool(rng.random() < 0.5)
     dS = bool(rng.random() < 0.5)
     return dict(form=form, vector=vector, D=D, bf16=bf16, B=B, T=T, Hk=Hk, Hv=Hv, mask=mask_kind, chunk=chunk,
-                log_gate=log_gate, s0=s0, dS=dS, seed=7000 + i)
+                log_gate=log_gate, s0=s0, dS=dS, seed=(8000 if long else 7000) + i)
 
 
 def inputs(c):
@@ -92,7 +94,15 @@ def nerr(a, b):
 
 @pytest.mark.parametrize("i", range(N_CASES))
 def test_random_combination_against_oracle(dev, i):
-    c = draw(i)
+    check(draw(i), dev, i)
+
+
+@pytest.mark.parametrize("i", range(N_LONG))
+def test_random_long_combination_against_oracle(dev, i):
+    check(draw(i, long=True), dev, i)
+
+
+def check(c, dev, i):
     print("case", i, c, flush=True)
     d = inputs(c)
     got = run_engine(c, d, dev)
