@@ -1918,7 +1918,9 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
     const int T = a.T, hk = hv / (a.Hv / a.Hk);
     const size_t head = (size_t)b * a.Hv + hv;
     const int mrow = 16 * (w & 3);
-    const bool cwave = NTN >= 2 || w < 4;
+    // with 16-wide slices (NTN == 1) waves 0-3 form Delta and waves 4-7 form y on the same row blocks; wider slices
+    // give every wave both
+    const bool dwave = NTN >= 2 || w < 4, ywave = NTN >= 2 || w >= 4;
     const int nt0 = NTN >= 2 ? (w >> 2) * DN : 0;
 
     f4 h[NTN];  // rows j = 16w + 4lg + e, columns i = i0 + 16t + li
@@ -1936,14 +1938,14 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
         const bfr *pb = a.w.Pb + ci * 2 * C * C + frag_off<C>(mrow, 0) + 8 * l;
         const bfr *kt = a.w.KTb + ci * D * C + frag_off<C>(16 * w, 0) + 8 * l;
         const bfr *qb = static_cast<const bfr *>(a.q) + (((size_t)b * a.Ts + t0 + r) * a.Hk + hk) * D + 8 * lg;
-        // W, Q and P only in the waves that form Delta and y (all of them when NTN >= 2; with 16-wide slices the
-        // other four waves only update their rows of h)
-        if (cwave) {
+        // W and U in the waves that form Delta, Q and P in the waves that form y
+        if (dwave) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                f.W[k] = ld_frag(wb + FRAG_BLOCK * k);
-                f.Q[k] = r < n ? ld_frag(qb + 32 * k) : zero_frag();
-            }
+            for (int k = 0; k < 4; ++k) f.W[k] = ld_frag(wb + FRAG_BLOCK * k);
+        }
+        if (ywave) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) f.Q[k] = r < n ? ld_frag(qb + 32 * k) : zero_frag();
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 f.P[k] = ld_frag(pb + FRAG_BLOCK * k);
@@ -1952,7 +1954,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
         }
 #pragma unroll
         for (int k = 0; k < 2; ++k) f.K[k] = ld_frag(kt + FRAG_BLOCK * k);
-        if (cwave) {
+        if (dwave) {
 #pragma unroll
             for (int t = 0; t < DN; ++t) {
                 const float4 x = *reinterpret_cast<const float4 *>(a.w.U + ci * C * D + acc_off(mrow + 4 * lg, i0 + 16 * (nt0 + t) + li));
@@ -1986,12 +1988,12 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
         f4 yi[DN];
 #pragma unroll
         for (int t = 0; t < DN; ++t) yi[t] = zero4();
-        if (cwave) {
-            f4 wh[DN];
+        f4 wh[DN];
 #pragma unroll
-            for (int t = 0; t < DN; ++t) wh[t] = zero4();
-            mmar<D, DN>(wh, cur.W, nullptr, sHh, nullptr, LH, 16 * nt0);
-            mmar<D, DN, false, true>(yi, cur.Q, nullptr, sHh, sHl, LH, 16 * nt0);
+        for (int t = 0; t < DN; ++t) wh[t] = zero4();
+        if (dwave) mmar<D, DN>(wh, cur.W, nullptr, sHh, nullptr, LH, 16 * nt0);
+        if (ywave) mmar<D, DN, false, true>(yi, cur.Q, nullptr, sHh, sHl, LH, 16 * nt0);
+        if (dwave) {
 #pragma unroll
             for (int t = 0; t < DN; ++t) {
                 f4 dl;
@@ -2006,7 +2008,7 @@ __global__ __launch_bounds__(NTS) void ck_fwd_bf16_kernel(Args a) {
             }
         }
         __syncthreads();
-        if (cwave && kOut) {
+        if (ywave && kOut) {
             // Y = diag(gamma) Q h + P Delta
 #pragma unroll
             for (int t = 0; t < DN; ++t)
