@@ -2350,6 +2350,8 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
     const size_t head = (size_t)b * a.Hv + hv;
     const int mrow = 16 * (w & 3);
     const bool cwave = NTN >= 2 || w < 4;
+    // with 16-wide slices waves 4-7 form the saved TdD after the barrier while waves 0-3 go on
+    const bool twave = NTN >= 2 || w >= 4;
     const int nt0 = NTN >= 2 ? (w >> 2) * DN : 0;
     // this thread's block of the dY slice: tokens 8 yb .. 8 yb + 7, slice columns yc, yc + 1
     const bool ythr = tid < NYB;
@@ -2485,7 +2487,7 @@ __global__ __launch_bounds__(NTS) void ck_bwd_seq_bf16_kernel(Args a) {
         }
         __syncthreads();
         if (c > 0) fetch_tt(c - 1);
-        if (cwave) {
+        if (twave) {
             // saved TdD = T^T dDelta (T^T and dDelta split): rows s = mrow + 4 lg + e, this slice's columns
             f4 tdd[DN];
 #pragma unroll
