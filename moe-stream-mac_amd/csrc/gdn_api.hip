@@ -104,19 +104,23 @@ static int check_shape(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, 
     return GDN_OK;
 }
 
-// Masked calls run the chunked form as two passes (gdn_mask.hip) and need no other condition.
-static bool chunk_eligible(int Dk, int Dv, int has_mask, int gate) {
-    (void)has_mask;
-    return Dk == 128 && Dv == 128 && (gate == GATE_DECAY || gate == GATE_LOG);
+// Masked calls run the chunked form as two passes (gdn_mask.hip), whose fix-up kernels hold per-head values of one
+// token in LDS: Hv <= mask_max_heads().
+static bool chunk_eligible(int Hv, int Dk, int Dv, int has_mask, int gate) {
+    return Dk == 128 && Dv == 128 && (gate == GATE_DECAY || gate == GATE_LOG) &&
+           (!has_mask || Hv <= mask_max_heads());
 }
 
 // The form a (shape, mask, gate, requested form) resolves to, or < 0 when a requested form cannot run.
-static int resolve_form(int Dk, int Dv, int has_mask, int gate, int form) {
+static int resolve_form(int Hv, int Dk, int Dv, int has_mask, int gate, int form) {
     if (form == GDN_FORM_RECURRENT) return GDN_FORM_RECURRENT;
-    const bool ok = chunk_eligible(Dk, Dv, has_mask, gate);
-    if (form == GDN_FORM_CHUNK)
-        return ok ? GDN_FORM_CHUNK
-                  : fail(GDN_ERR_UNSUPPORTED, "the chunked form needs Dk = Dv = 128 and a scalar gate");
+    const bool ok = chunk_eligible(Hv, Dk, Dv, has_mask, gate);
+    if (form == GDN_FORM_CHUNK) {
+        if (ok) return GDN_FORM_CHUNK;
+        if (has_mask && Hv > mask_max_heads() && Dk == 128 && Dv == 128 && gate != GATE_DECAY_VEC)
+            return fail(GDN_ERR_UNSUPPORTED, "masked calls of the chunked form take Hv <= %d", mask_max_heads());
+        return fail(GDN_ERR_UNSUPPORTED, "the chunked form needs Dk = Dv = 128 and a scalar gate");
+    }
     return ok ? GDN_FORM_CHUNK : GDN_FORM_RECURRENT;
 }
 
@@ -278,7 +282,7 @@ using namespace gdn;
 
 extern "C" {
 
-int gdn_version(void) { return (2 << 16) | 0; }
+int gdn_version(void) { return (3 << 16) | 0; }
 
 int gdn_profile_enable(int on) {
     g_prof_on.store(on != 0, std::memory_order_relaxed);
@@ -324,15 +328,15 @@ int64_t gdn_num_snapshots(int T, int chunk) {
     return (int64_t)((T + chunk - 1) / chunk) - 1;
 }
 
-int gdn_select_form(int Dk, int Dv, int has_mask, int gate_kind, int form) {
+int gdn_select_form(int Hv, int Dk, int Dv, int has_mask, int gate_kind, int form) {
     g_err[0] = 0;
-    return resolve_form(Dk, Dv, has_mask, gate_kind, form);
+    return resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form);
 }
 
 size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind, int has_mask,
                        int form, int in_dtype) {
     if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
-    const int f = resolve_form(Dk, Dv, has_mask, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form);
     if (f < 0 || B == 0 || T == 0) return 0;
     if (f == GDN_FORM_CHUNK) {
         const int W = ck_window(chunk);
@@ -346,7 +350,7 @@ size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, 
 size_t gdn_fwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind, int has_mask,
                                int form, int in_dtype, int with_saved) {
     if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
-    const int f = resolve_form(Dk, Dv, has_mask, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form);
     if (f != GDN_FORM_CHUNK || B == 0 || T == 0) return 0;
     const int W = ck_window(chunk);
     const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16};
@@ -731,7 +735,7 @@ int gdn_fwd_noalloc(const void *q, const void *k, const void *v, const float *g,
     if (mask && form == GDN_FORM_CHUNK)
         return fail(GDN_ERR_UNSUPPORTED, "gdn_fwd_noalloc runs masked calls in the recurrent form only");
     if (mask) form = GDN_FORM_RECURRENT;
-    const int f = resolve_form(Dk, Dv, mask != nullptr, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, mask != nullptr, gate_kind, form);
     if (f < 0) return f;
     void *ws = nullptr;
     size_t ws_bytes = 0;
@@ -759,7 +763,7 @@ int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const f
     int rc = check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form);
     if (rc) return rc;
     if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
-    const int f = resolve_form(Dk, Dv, mask != nullptr, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, mask != nullptr, gate_kind, form);
     if (f < 0) return f;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (B == 0) return GDN_OK;
@@ -776,11 +780,7 @@ int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const f
         cc.y = y; cc.state_T = state_T;
         cc.B = B; cc.T = T; cc.Ts = T; cc.Hk = Hk; cc.Hv = Hv; cc.in_dt = in_dtype; cc.out_dt = out_dtype;
         cc.gate = gate_kind;
-        if (mask) {
-            if (Hv > mask_max_heads())
-                return fail(GDN_ERR_UNSUPPORTED, "masked calls of the chunked form take Hv <= %d", mask_max_heads());
-            return ck_masked_forward(cc, mask, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
-        }
+        if (mask) return ck_masked_forward(cc, mask, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
         return ck_forward(cc, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
     }
     const size_t need = rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
@@ -825,7 +825,7 @@ int gdn_decode_step(const void *q, const void *k, const void *v, const float *g,
 size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind,
                                int has_mask, int form, int in_dtype) {
     if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
-    const int f = resolve_form(Dk, Dv, has_mask, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form);
     if (f < 0) return 0;
     if (f == GDN_FORM_CHUNK) {
         if (B == 0 || T == 0) return 0;
@@ -847,7 +847,7 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
     if (rc) return rc;
     if (!dtype_ok(in_dtype) || !dtype_ok(dy_dtype) || !dtype_ok(grad_dtype))
         return fail(GDN_ERR_INVALID, "unknown dtype code");
-    const int f = resolve_form(Dk, Dv, mask != nullptr, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, mask != nullptr, gate_kind, form);
     if (f < 0) return f;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (B == 0) return GDN_OK;
@@ -870,11 +870,7 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
         cc.dstate0 = dstate0;
         cc.B = B; cc.T = T; cc.Ts = T; cc.Hk = Hk; cc.Hv = Hv; cc.in_dt = in_dtype; cc.dy_dt = dy_dtype;
         cc.grad_dt = grad_dtype; cc.gate = gate_kind;
-        if (mask) {
-            if (Hv > mask_max_heads())
-                return fail(GDN_ERR_UNSUPPORTED, "masked calls of the chunked form take Hv <= %d", mask_max_heads());
-            return ck_masked_backward(cc, mask, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
-        }
+        if (mask) return ck_masked_backward(cc, mask, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
         return ck_backward(cc, chunk, saved, saved_bytes, workspace, workspace_bytes, st);
     }
     const size_t need_saved = rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);

@@ -44,7 +44,8 @@ def _saved_bytes(lib, B, T, Hk, Hv, Dk, Dv, chunk, gate, has_mask, form, in_code
 
 class _GDNRecurrence(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, g, beta, state, mask, chunk, log_gate, out_dtype, need_saved, form):
+    def forward(ctx, q, k, v, g, beta, state, mask, chunk, log_gate, out_dtype, need_saved, form,
+                backward_error=None):
         # an output that the loss does not use reaches backward as None instead of a zero tensor filled for it
         # (the library takes a NULL exit-state cotangent as zero)
         ctx.set_materialize_grads(False)
@@ -55,7 +56,7 @@ class _GDNRecurrence(torch.autograd.Function):
         gate = gate_kind_for(g, log_gate)
         lib = L.load()
         has_mask = int(mask is not None)
-        resolved = int(lib.gdn_select_form(Dk, Dv, has_mask, gate, form))
+        resolved = int(lib.gdn_select_form(Hv, Dk, Dv, has_mask, gate, form))
         if resolved < 0:
             L.check(resolved)
         y = torch.empty((B, T, Hv, Dv), device=dev, dtype=out_dtype)
@@ -75,10 +76,13 @@ class _GDNRecurrence(torch.autograd.Function):
         del ws
         ctx.save_for_backward(q, k, v, g, beta, state, mask, saved)
         ctx.meta = (chunk, gate, form)
+        ctx.backward_error = backward_error
         return y, state_T
 
     @staticmethod
     def backward(ctx, dy, dstate_T):
+        if ctx.backward_error is not None:
+            raise ValueError(ctx.backward_error)
         q, k, v, g, beta, state, mask, saved = ctx.saved_tensors
         chunk, gate, form = ctx.meta
         dev = q.device
@@ -110,7 +114,7 @@ class _GDNRecurrence(torch.autograd.Function):
                             L.ptr(dS0), L.ptr(ws), ws_bytes, B, T, Hk, Hv, Dk, Dv, chunk,
                             L.DTYPE_CODE[q.dtype], L.DTYPE_CODE[dy.dtype], L.DTYPE_CODE[grad_dtype], gate,
                             form, L.stream_handle(dev)))
-        return dq, dk, dv, dg, dbeta, dS0, None, None, None, None, None, None
+        return dq, dk, dv, dg, dbeta, dS0, None, None, None, None, None, None, None
 
 
 def _aligned(t: torch.Tensor) -> torch.Tensor:
@@ -164,13 +168,14 @@ def default_form() -> int:
 
 def recurrence(q, k, v, g, beta, state, mask=None, chunk: int = 64, log_gate: bool = False,
                output_dtype: Optional[torch.dtype] = None, need_grad: Optional[bool] = None,
-               form: Optional[str] = None):
+               form: Optional[str] = None, backward_error: Optional[str] = None):
     """(y, final_state) of the delta-rule recurrence with a HIP forward and VJP.
 
     ``g`` is the multiplicative decay ([B,T,Hv] or [B,T,Hv,Dk]) or, with ``log_gate``, the log decay.
     ``y`` defaults to the dtype the reference's arithmetic promotes to (fp32 with an fp32 state).
     ``need_grad=False`` runs the forward-only path (no autograd graph).  ``form`` is "auto" (default, or the
-    GDN_FORM environment variable), "recurrent" or "chunk".
+    GDN_FORM environment variable), "recurrent" or "chunk".  ``backward_error``, when given, is raised as a
+    ``ValueError`` by the backward (the forward runs).
     """
     if chunk <= 0:
         raise ValueError("chunk must be a positive integer")
@@ -199,7 +204,8 @@ def recurrence(q, k, v, g, beta, state, mask=None, chunk: int = 64, log_gate: bo
         with torch.no_grad():
             return _GDNRecurrence.forward(_NoCtx(), pq, pk, pv, pg, pb, ps, pm, chunk, log_gate, out_dtype,
                                           False, form_code)
-    y, state_T = _GDNRecurrence.apply(pq, pk, pv, pg, pb, ps, pm, chunk, log_gate, out_dtype, True, form_code)
+    y, state_T = _GDNRecurrence.apply(pq, pk, pv, pg, pb, ps, pm, chunk, log_gate, out_dtype, True, form_code,
+                                      backward_error)
     return y, state_T
 
 

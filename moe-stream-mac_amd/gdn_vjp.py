@@ -54,17 +54,20 @@ def gated_delta_chunked(
         raise ValueError("chunk must be a positive integer")
     if impl not in ("chunked", "staged", "kernel"):
         raise ValueError("impl must be 'chunked', 'staged', or 'kernel'")
+    backward_error = None
     if impl == "kernel":
-        # The reference's kernel impl accepts only these inputs (tools/gdn_vjp.py:391-394).
+        # The reference's kernel impl accepts only these inputs, and checks them when the backward runs
+        # (tools/gdn_vjp.py:391-394): a forward-only call with other inputs succeeds.
         if q.shape[-1] % 32:
-            raise ValueError("impl='kernel' requires key_dim divisible by 32")
-        if q.dtype != k.dtype or q.dtype != v.dtype:
-            raise ValueError("impl='kernel' requires q, k, and v to share a dtype")
+            backward_error = "impl='kernel' requires key_dim divisible by 32"
+        elif q.dtype != k.dtype or q.dtype != v.dtype:
+            backward_error = "impl='kernel' requires q, k, and v to share a dtype"
     batch, _, _, key_dim = q.shape
     value_heads, value_dim = v.shape[-2:]
     if state is None:
         state = torch.zeros((batch, value_heads, value_dim, key_dim), dtype=torch.float32, device=q.device)
-    return gdn_engine.recurrence(q, k, v, g, beta, state, mask, chunk, output_dtype=output_dtype)
+    return gdn_engine.recurrence(q, k, v, g, beta, state, mask, chunk, output_dtype=output_dtype,
+                                 backward_error=backward_error)
 
 
 def _vjp_update(
@@ -92,7 +95,8 @@ def _vjp_update(
             allow_neg_eigval=allow_neg_eigval
         )
     g, beta = gated_delta.gates(a, b, A_log, dt_bias, allow_neg_eigval, lower_bound)
-    impl = "kernel" if q.shape[-1] % 32 == 0 and q.dtype == k.dtype == v.dtype else "staged"
+    # the reference picks the kernel impl by key_dim alone (tools/gdn_vjp.py:562)
+    impl = "kernel" if q.shape[-1] % 32 == 0 else "staged"
     return gated_delta_chunked(q, k, v, g, beta, state, mask, impl=impl)
 
 

@@ -26,10 +26,23 @@ int main(void) {
     CHECK(gdn_version() > 0);
 
     /* forms */
-    CHECK(gdn_select_form(128, 128, 0, GDN_GATE_LOG, GDN_FORM_AUTO) == GDN_FORM_CHUNK);
-    CHECK(gdn_select_form(128, 128, 1, GDN_GATE_LOG, GDN_FORM_AUTO) == GDN_FORM_CHUNK);
-    CHECK(gdn_select_form(64, 128, 0, GDN_GATE_DECAY, GDN_FORM_AUTO) == GDN_FORM_RECURRENT);
-    CHECK(gdn_select_form(128, 128, 0, GDN_GATE_DECAY_VEC, GDN_FORM_CHUNK) == GDN_ERR_UNSUPPORTED);
+    CHECK(gdn_select_form(32, 128, 128, 0, GDN_GATE_LOG, GDN_FORM_AUTO) == GDN_FORM_CHUNK);
+    CHECK(gdn_select_form(32, 128, 128, 1, GDN_GATE_LOG, GDN_FORM_AUTO) == GDN_FORM_CHUNK);
+    CHECK(gdn_select_form(32, 64, 128, 0, GDN_GATE_DECAY, GDN_FORM_AUTO) == GDN_FORM_RECURRENT);
+    CHECK(gdn_select_form(32, 128, 128, 0, GDN_GATE_DECAY_VEC, GDN_FORM_CHUNK) == GDN_ERR_UNSUPPORTED);
+    /* masked calls above 256 value heads: AUTO resolves to the recurrent form, and the size queries follow it */
+    CHECK(gdn_select_form(260, 128, 128, 1, GDN_GATE_LOG, GDN_FORM_AUTO) == GDN_FORM_RECURRENT);
+    CHECK(gdn_select_form(260, 128, 128, 1, GDN_GATE_LOG, GDN_FORM_CHUNK) == GDN_ERR_UNSUPPORTED && err_has("Hv <= 256"));
+    CHECK(gdn_saved_bytes(1, 300, 130, 260, 128, 128, 64, GDN_GATE_LOG, 1, GDN_FORM_AUTO, GDN_BF16) ==
+          gdn_saved_bytes(1, 300, 130, 260, 128, 128, 64, GDN_GATE_LOG, 1, GDN_FORM_RECURRENT, GDN_BF16));
+    CHECK(gdn_bwd_workspace_bytes(1, 300, 130, 260, 128, 128, 64, GDN_GATE_LOG, 1, GDN_FORM_AUTO, GDN_BF16) ==
+          gdn_bwd_workspace_bytes(1, 300, 130, 260, 128, 128, 64, GDN_GATE_LOG, 1, GDN_FORM_RECURRENT, GDN_BF16));
+    CHECK(gdn_fwd_workspace_bytes(1, 300, 130, 260, 128, 128, 64, GDN_GATE_LOG, 1, GDN_FORM_AUTO, GDN_BF16, 1) == 0);
+    {   /* a masked chunked call above 256 value heads is refused before anything runs */
+        const int rc = gdn_fwd(fake, fake, fake, fake, fake, NULL, fake, fake, NULL, NULL, 0, NULL, 0, 1, 4, 130, 260,
+                               128, 128, 64, GDN_BF16, GDN_BF16, GDN_GATE_LOG, GDN_FORM_CHUNK, NULL);
+        CHECK(rc == GDN_ERR_UNSUPPORTED && err_has("Hv <= 256"));
+    }
 
     /* size queries over shapes, dtypes, masks, chunks and forms */
     const int Ts[] = {1, 63, 64, 65, 200, 4096, 16384};

@@ -16,7 +16,7 @@ def test_library_exports_every_declared_symbol():
             "gdn_profile_collect"} <= set(declared)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.gdn_version() >> 16 == 2
+    assert lib.gdn_version() >> 16 == 3
 
 
 def test_bindings_match_header_arities():
@@ -87,6 +87,20 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert dec([fake] * 8, 1, 1, 1, 8, 8, 0, 0, 9) == gdn_lib.GDN_ERR_INVALID
 
 
+def test_noalloc_refusals_without_launching():
+    """gdn_fwd_noalloc refuses, before any device call, a masked call that asks for the chunked form and a call whose
+    one 64-token group does not fit its fixed scratch."""
+    L = gdn_lib
+    lib = L.load()
+    fake = ctypes.c_void_p(256)   # never dereferenced: both calls fail their host-side checks first
+    rc = lib.gdn_fwd_noalloc(*([fake] * 6), fake, fake, fake, 2, 70, 2, 4, 128, 128, L.F32, L.F32, L.GATE_LOG,
+                             L.FORM_CHUNK, None)
+    assert rc == L.GDN_ERR_UNSUPPORTED and b"recurrent form only" in lib.gdn_last_error()
+    rc = lib.gdn_fwd_noalloc(*([fake] * 6), None, fake, fake, 16, 64, 16, 64, 128, 128, L.BF16, L.BF16, L.GATE_LOG,
+                             L.FORM_CHUNK, None)
+    assert rc == L.GDN_ERR_UNSUPPORTED and b"fixed scratch" in lib.gdn_last_error()
+
+
 def test_block_op_abi_rejects_bad_arguments_without_launching():
     lib = gdn_lib.load()
     L = gdn_lib
@@ -144,9 +158,21 @@ def test_saved_sizes_by_form():
     assert rec == 63 * 32 * 128 * 128 * 4
     ck = lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_AUTO, L.F32)
     assert ck == lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_CHUNK, L.F32) > rec
-    assert lib.gdn_select_form(128, 128, 0, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK
-    assert lib.gdn_select_form(128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK   # masks: two chunked passes
-    assert lib.gdn_select_form(8, 8, 0, L.GATE_DECAY, L.FORM_AUTO) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(32, 128, 128, 0, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK
+    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK   # masks: two chunked passes
+    assert lib.gdn_select_form(32, 8, 8, 0, L.GATE_DECAY, L.FORM_AUTO) == L.FORM_RECURRENT
+    # masked calls take the chunked form up to 256 value heads; above, AUTO falls back to the recurrent form and
+    # the size queries answer for that form
+    assert lib.gdn_select_form(256, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK
+    assert lib.gdn_select_form(260, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(260, 128, 128, 0, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK
+    assert lib.gdn_select_form(260, 128, 128, 1, L.GATE_LOG, L.FORM_CHUNK) == L.GDN_ERR_UNSUPPORTED
+    assert b"Hv <= 256" in lib.gdn_last_error()
+    for q in (lambda f: lib.gdn_saved_bytes(1, 300, 130, 260, 128, 128, 64, L.GATE_LOG, 1, f, L.BF16),
+              lambda f: lib.gdn_bwd_workspace_bytes(1, 300, 130, 260, 128, 128, 64, L.GATE_LOG, 1, f, L.BF16)):
+        assert q(L.FORM_AUTO) == q(L.FORM_RECURRENT) > 0
+    assert lib.gdn_fwd_workspace_bytes(1, 300, 130, 260, 128, 128, 64, L.GATE_LOG, 1, L.FORM_AUTO, L.BF16, 1) == 0
+    assert lib.gdn_fwd_workspace_bytes(1, 300, 130, 260, 128, 128, 64, L.GATE_LOG, 1, L.FORM_CHUNK, L.BF16, 0) == 0
 
 
 def _ck_tile_bytes_per_chunk_head(bf16: bool) -> int:

@@ -4,7 +4,8 @@ cotangent and the measured workload at its full length.
 * checkpointing (tools/gdn_checkpoint.py:39-50,81-95): the forward keeps ceil(T/W) - 1 fp32 window states and the
   backward rebuilds each group of windows from them; checked against the fp64 oracle (1e-4 fp32, 1e-2 bf16), against
   the chunk = 64 run of the same engine, with groups of one or two windows forced through a small workspace, and at
-  T = 16384 through full-size properties (agreement with chunk = 64, finite gradients, peak memory);
+  T = 16384 against the oracle on one key-head group and through full-size properties (agreement with chunk = 64,
+  finite gradients, peak memory);
 * forward-only calls (saved = NULL, frozen layers) against the oracle's forward, group by group;
 * the headline workload (B=4, T=4096, Hk=16, Hv=32, bf16 q/k/v/dO, fp32 state) against the fp64 oracle on two
   key-head groups, with the errors printed at T = 600, 2048 and 4096;
@@ -140,6 +141,24 @@ def test_checkpoint_fp32_measured_heads_against_oracle(dev):
     _check_groups(got, d, ((0, 0), (0, 11)), 2, 1e-4, "ckpt fp32")
     snaps = L.load().gdn_saved_bytes(1, 2048, 16, 32, D, D, 256, L.GATE_DECAY, 0, L.FORM_CHUNK, L.F32)
     assert snaps == 7 * 32 * D * D * 4
+
+
+def test_checkpoint_t16384_against_oracle(dev):
+    """The checkpoint configuration at its own length: fp32, B=1, T=16384, Hk=16, Hv=32, D=128, S0 ~ N(0, 0.02),
+    snapshots every 256 tokens (63 windows, several backward groups) through gated_delta_ops_checkpointed, with one
+    key-head group (two value heads) against the fp64 oracle at 1e-4."""
+    import gdn_checkpoint
+    d = _inputs(1, 16384, 16, 32, seed=41)
+    print("checkpoint fp32 B=1 T=16384 Hv=32 chunk=256 against the oracle (key head 5)", flush=True)
+    t = lambda x: torch.tensor(np.asarray(x), device=dev).requires_grad_(True)
+    leaves = [t(d[n]) for n in ("q", "k", "v", "decay", "beta", "state")]
+    y, S = gdn_checkpoint.gated_delta_ops_checkpointed(*leaves, None, 256)
+    grads = torch.autograd.grad([y, S], leaves, [t(d["dy"]), t(d["dS_T"])])
+    torch.cuda.synchronize()
+    got = [x.detach().cpu().numpy() for x in (y, S, *grads)]
+    del y, S, grads, leaves
+    got[5] = got[5] * d["decay"]   # d/d(decay) -> d/d(log decay), as the oracle group reports
+    _check_groups(got, d, ((0, 5),), 2, 1e-4, "ckpt fp32 T=16384")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

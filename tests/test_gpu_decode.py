@@ -2,7 +2,8 @@
 engine/include/gdn.h:27-38, engine/src/gdn.c:63-108), the conv and recurrent state caches of
 qwen3_5.GatedDeltaNet, and token-by-token decoding of the tiny model.
 
-* token-by-token decode equals the full-sequence forward and both match the fp64 oracle (1e-4 fp32, 1e-2 bf16);
+* token-by-token decode matches the fp64 oracle (1e-4 with fp32 or bf16 inputs: its arithmetic and y are fp32) and
+  equals the full-sequence forward (1e-2 where that runs the chunked form on bf16 inputs, else 1e-4);
 * a prefill of part of a sequence followed by one call per token, through the block's caches, equals the block's
   full-sequence forward, which the float64 block oracle pins (frozen / eval path at Dk = Dv = 128, chunked form);
 * the tiny model's logits decoded one token at a time equal its full forward.
@@ -63,11 +64,16 @@ def test_decode_steps_match_sequence_and_oracle(dev, dtype, Hk, Hv, D, gate):
     torch.cuda.synchronize()
     wy, wS = O.gated_delta_chunked(d["q"], d["k"], d["v"], d["decay"], d["beta"], d["state"], None, 64,
                                    dtype=np.float64)
-    tol = 1e-2 if dtype == torch.bfloat16 else 1e-4
-    assert nerr(y_dec.cpu().numpy(), wy) <= tol
-    assert nerr(state.cpu().numpy(), wS) <= tol
-    assert nerr(y_dec.cpu().numpy(), y_seq.cpu().numpy()) <= tol
-    assert nerr(state.cpu().numpy(), S_seq.cpu().numpy()) <= tol
+    # the decode step computes in fp32 from the same bf16-rounded inputs the oracle sees, and returns y in fp32: 1e-4
+    # with either input dtype.  The sequence forward runs the chunked form at D = 128, whose bf16 inputs enter bf16
+    # MFMA products: 1e-2 there.
+    seq_tol = 1e-2 if dtype == torch.bfloat16 and D == 128 and gate != "vector" else 1e-4
+    errs = dict(y=nerr(y_dec.cpu().numpy(), wy), S=nerr(state.cpu().numpy(), wS),
+                y_seq=nerr(y_dec.cpu().numpy(), y_seq.cpu().numpy()),
+                S_seq=nerr(state.cpu().numpy(), S_seq.cpu().numpy()))
+    print("  errors", {n: f"{e:.1e}" for n, e in errs.items()}, flush=True)
+    assert errs["y"] <= 1e-4 and errs["S"] <= 1e-4, errs
+    assert errs["y_seq"] <= seq_tol and errs["S_seq"] <= seq_tol, errs
 
 
 def test_decode_step_out_of_place_and_zero_state(dev):

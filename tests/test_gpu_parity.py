@@ -112,6 +112,27 @@ def test_forward_and_six_cotangents_match_oracle(dev, timesteps, chunk, masked, 
     assert_close(got, oracle_vjp(c, chunk))
 
 
+@pytest.mark.parametrize("gate_ndim", [3, 4])
+def test_kernel_impl_parity_case(dev, gate_ndim):
+    """Counterpart of tools/test_gdn_vjp.py:79-107: Dk=32, Dv=3, T=2, chunk=T, mask [[True, False]],
+    impl="kernel", against the float64 oracle at the reference's gradient atol 1e-4."""
+    rng = np.random.default_rng(777 + gate_ndim)
+    B, T, Hk, Hv, Dk, Dv = 1, 2, 1, 2, 32, 3
+    q = O.l2norm(rng.standard_normal((B, T, Hk, Dk)), 1e-6, Dk ** -0.5)
+    k = O.l2norm(rng.standard_normal((B, T, Hk, Dk)), 1e-6, 1.0)
+    gshape = (B, T, Hv) + ((Dk,) if gate_ndim == 4 else ())
+    c = dict(q=q, k=k, v=rng.standard_normal((B, T, Hv, Dv)), g=rng.uniform(0.7, 1.0, gshape),
+             beta=rng.uniform(0.05, 0.95, (B, T, Hv)), state=rng.standard_normal((B, Hv, Dv, Dk)),
+             dy=rng.standard_normal((B, T, Hv, Dv)), dstate=rng.standard_normal((B, Hv, Dv, Dk)))
+    c = {n: x.astype(np.float32) for n, x in c.items()}
+    c["mask"] = np.array([[True, False]])
+    got = run_gpu(c, dev, T, impl="kernel")
+    want = oracle_vjp(c, T)
+    for n, a, b in zip(OUT_NAMES, got, want):
+        assert a.shape == b.shape, n
+        assert float(np.abs(a - b).max()) <= 1e-4, (n, float(np.abs(a - b).max()))
+
+
 # ------------------------------------------------------------------------------ checkpoint matrix, real heads
 
 @pytest.mark.parametrize("timesteps", [1, 63, 64, 65, 200])
@@ -313,8 +334,29 @@ def test_errors_match_reference(dev):
         gdn_vjp.gated_delta_chunked(q, q, v, g, g, impl="fast")
     with pytest.raises(ValueError, match="head count must divide"):
         gdn_vjp.gated_delta_chunked(q, q, v, g, g)
+    # impl="kernel" checks key_dim and the shared dtype when the backward runs (tools/gdn_vjp.py:391-394):
+    # the forward succeeds, with and without a graph, and the backward raises
+    v2, g2 = torch.zeros(1, 4, 2, 8, device=dev), g[:, :, :2]
+    with torch.no_grad():
+        y, S = gdn_vjp.gated_delta_chunked(q, q, v2, g2, g2, impl="kernel")
+    assert y.shape == (1, 4, 2, 8) and S.shape == (1, 2, 8, 8)
+    qg = q.clone().requires_grad_(True)
+    y, S = gdn_vjp.gated_delta_chunked(qg, q, v2, g2, g2, impl="kernel")
     with pytest.raises(ValueError, match="key_dim divisible by 32"):
-        gdn_vjp.gated_delta_chunked(q, q, torch.zeros(1, 4, 2, 8, device=dev), g[:, :, :2], g[:, :, :2],
-                                    impl="kernel")
+        y.sum().backward()
+    q32 = torch.randn(1, 4, 2, 32, device=dev)
+    k32 = q32.to(torch.bfloat16)
+    v32 = torch.zeros(1, 4, 2, 32, device=dev)
+    with torch.no_grad():
+        gdn_vjp.gated_delta_chunked(q32, k32, v32, g2, g2, impl="kernel")
+    qg = q32.clone().requires_grad_(True)
+    y, S = gdn_vjp.gated_delta_chunked(qg, k32, v32, g2, g2, impl="kernel")
+    with pytest.raises(ValueError, match="share a dtype"):
+        y.sum().backward()
+    # the other impls take the same inputs through the backward
+    qg = q32.clone().requires_grad_(True)
+    y, S = gdn_vjp.gated_delta_chunked(qg, k32, v32, g2, g2, impl="staged")
+    y.sum().backward()
+    assert qg.grad is not None and bool(torch.isfinite(qg.grad).all())
     with pytest.raises(ValueError, match="Unsupported gating shape"):
         gdn_vjp.gated_delta_chunked(q, q, torch.zeros(1, 4, 2, 8, device=dev), g[:, :, 0], g[:, :, :2])

@@ -5,8 +5,10 @@ form; 32, 64 or 128 on the recurrent one), the input dtype (fp32, or bf16 with a
 the GQA layout (Hk 1-2, Hv/Hk 1, 2 or 4), the gate (log or decay space per head, or one decay per key channel on
 the recurrent form), the mask (none, random, or a masked tail), the snapshot interval `chunk` (16, 64, 100, 256),
 a zero or random initial state and a zero or random exit-state cotangent.  Eight more draws run at B = 1,
-T = 1000..3000 (several checkpoint windows and groups).  Bars: normalised error max|gpu - oracle| / max|oracle|
-<= 1e-4 for fp32 inputs, <= 1e-2 for bf16 inputs, per output.
+T = 1000..3000 (several checkpoint windows and groups).  Bars, as normalised error max|gpu - oracle| / max|oracle|
+per output, are set by each output's arithmetic (``bar``): 1e-4 for fp32 inputs and for the fp32 outputs of the
+token-recurrent form with bf16 inputs, 4e-3 for that form's bf16 dq / dk / dv, 1e-2 on the chunked form with bf16
+inputs.
 """
 
 import numpy as np
@@ -111,11 +113,23 @@ def check(c, dev, i):
     want = [y, S, *g]
     if c["log_gate"]:
         want[5] = want[5] * d["decay"]  # the oracle's d/d(decay) -> d/d(log decay), what the engine returns
-    tol = 1e-2 if c["bf16"] else 1e-4
     errs = {}
     for n, a, w in zip(NAMES, got, want):
         assert a.shape == w.shape, (n, a.shape, w.shape)
         errs[n] = nerr(a, w)
     print("  errors", {n: f"{e:.1e}" for n, e in errs.items()}, flush=True)
     for n, e in errs.items():
-        assert e <= tol, (i, n, e, c)
+        assert e <= bar(c, n), (i, n, e, bar(c, n), c)
+
+
+def bar(c, name):
+    """The bar each output's arithmetic sets.  fp32 inputs: 1e-4.  bf16 inputs on the token-recurrent form (the
+    oracle sees the same bf16-rounded inputs and the recurrence runs in fp32): 1e-4 for the fp32 outputs y, S_T, dg,
+    dbeta and dS0, and 4e-3 for dq, dk and dv, which come back rounded to bf16 (2^-9 of an element, plus the fp32
+    sums).  bf16 inputs on the chunked form, whose products take bf16 MFMA operands: 1e-2."""
+    if not c["bf16"]:
+        return 1e-4
+    recurrent = c["form"] == "recurrent" or c["vector"]
+    if not recurrent:
+        return 1e-2
+    return 4e-3 if name in ("dq", "dk", "dv") else 1e-4

@@ -71,9 +71,9 @@ def test_noalloc_forward_matches_gdn_fwd_twice(dev, dtype):
 
 
 def test_noalloc_recurrent_form_and_limits(dev):
-    """A masked call runs the recurrent form (no scratch), equal to gdn_fwd's recurrent form; a masked call that asks
-    for the chunked form, or whose one-chunk group exceeds the fixed scratch, is refused with a clear error before
-    anything runs."""
+    """A masked call runs the recurrent form (no scratch), equal to gdn_fwd's recurrent form.  The refusals (a masked
+    call that asks for the chunked form, a one-chunk group beyond the fixed scratch) are host-side checks, tested on
+    the CPU (tests/test_abi_cpu.py)."""
     import gdn_lib as L
     x = _inputs(2, 70, 2, 4, 128, torch.float32, dev, 3)
     mask = torch.ones(2, 70, dtype=torch.uint8, device=dev)
@@ -82,11 +82,32 @@ def test_noalloc_recurrent_form_and_limits(dev):
         y0, S0 = _run(x, dev, noalloc=False, mask=mask, form=L.FORM_RECURRENT)
         y1, S1 = _run(x, dev, noalloc=True, mask=mask)
         assert torch.equal(y0, y1) and torch.equal(S0, S1)
+
+
+def test_noalloc_forward_under_graph_capture(dev):
+    """gdn_fwd_noalloc recorded into a HIP graph (torch.cuda.graph capture) after one eager call on the device: each
+    replay, over new contents of the captured inputs and with eager work between replays, equals gdn_fwd."""
+    import gdn_lib as L
     lib = L.load()
-    fake = 256
-    rc = lib.gdn_fwd_noalloc(*([fake] * 6), fake, fake, fake, 2, 70, 2, 4, 128, 128, L.F32, L.F32, L.GATE_LOG,
-                             L.FORM_CHUNK, None)
-    assert rc == L.GDN_ERR_UNSUPPORTED and b"recurrent form only" in lib.gdn_last_error()
-    rc = lib.gdn_fwd_noalloc(*([fake] * 6), None, fake, fake, 16, 64, 16, 64, 128, 128, L.BF16, L.BF16, L.GATE_LOG,
-                             L.FORM_CHUNK, None)
-    assert rc == L.GDN_ERR_UNSUPPORTED and b"fixed scratch" in lib.gdn_last_error()
+    B, T, Hk, Hv, D = 2, 300, 16, 32, 128
+    x = _inputs(B, T, Hk, Hv, D, torch.bfloat16, dev, 11)
+    _run(x, dev, noalloc=True)   # the first call on the device looks up the scratch address
+    code = L.DTYPE_CODE[torch.bfloat16]
+    y = torch.empty((B, T, Hv, D), device=dev, dtype=torch.bfloat16)
+    S = torch.empty((B, Hv, D, D), device=dev)
+    ptrs = [x[n].data_ptr() for n in ("q", "k", "v", "g", "beta", "S0")]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.gdn_fwd_noalloc(*ptrs, None, y.data_ptr(), S.data_ptr(), B, T, Hk, Hv, D, D, code, code,
+                                 L.GATE_LOG, L.FORM_AUTO, L.stream_handle(dev))
+    L.check(rc)
+    for rep in range(3):
+        print(f"graph replay {rep}", flush=True)
+        new = _inputs(B, T, Hk, Hv, D, torch.bfloat16, dev, 20 + rep)
+        for n in new:
+            x[n].copy_(new[n])
+        y.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        y0, S0 = _run(x, dev, noalloc=False)
+        assert torch.equal(y0, y) and torch.equal(S0, S)
