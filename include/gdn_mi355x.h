@@ -75,9 +75,9 @@ int64_t gdn_num_snapshots(int T, int chunk);
 
 /* The form a call with these arguments runs in (GDN_FORM_RECURRENT or GDN_FORM_CHUNK), or < 0 when the
  * requested form cannot run them.  gdn_fwd, gdn_bwd and the size queries resolve the form the same way: GDN_FORM_AUTO
- * picks the chunked form for Dk = Dv = 128 with a scalar gate, and, with a mask, Hv <= 256; the recurrent form
- * otherwise. */
-int gdn_select_form(int Hv, int Dk, int Dv, int has_mask, int gate_kind, int form);
+ * picks the chunked form for Dk = Dv = 128 with a scalar gate (with a mask: Hv <= 256) or with one decay per key
+ * channel (GDN_GATE_DECAY_VEC: bf16 inputs, no mask); the recurrent form otherwise. */
+int gdn_select_form(int Hv, int Dk, int Dv, int has_mask, int gate_kind, int form, int in_dtype);
 
 /* What `chunk` means.
  *   Recurrent form: the forward keeps the state every `chunk` tokens (gdn_num_snapshots) and the backward replays

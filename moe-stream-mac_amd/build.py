@@ -1,6 +1,8 @@
 """Builds libgdn_mi355x.so (all HIP sources under csrc/) in place for gfx950 with hipcc.
 
     python moe-stream-mac_amd/build.py          # or __graft_entry__.build()
+
+Each source is compiled to an object in a temporary directory (in parallel), then the objects are linked.
 """
 
 from __future__ import annotations
@@ -9,12 +11,15 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libgdn_mi355x.so"
 ARCH = os.environ.get("GDN_OFFLOAD_ARCH", "gfx950")
+NOISE = "is not a recognized feature for this target"
 
 
 def hipcc() -> str:
@@ -28,24 +33,36 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every csrc/*.hip into one shared library; always recompiles."""
-    tmp = LIB.with_name(LIB.name + ".tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-shared", "-fPIC",
-           # packed-FP32 VALU forms stay off (plain fp32 FMA only)
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           "-Wall", "-Wno-unused-result", f"-I{HERE.parent / 'include'}",
-           *map(str, sources()), "-o", str(tmp)]
+def compile_flags() -> list[str]:
+    return [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+            # packed-FP32 VALU forms stay off (plain fp32 FMA only)
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            "-Wall", "-Wno-unused-result", f"-I{HERE.parent / 'include'}"]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    err = "\n".join(l for l in res.stderr.splitlines() if NOISE not in l)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
     if err.strip() and verbose:
         print(err, file=sys.stderr)
-    os.replace(tmp, LIB)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every csrc/*.hip into one shared library; always recompiles."""
+    hc, flags = hipcc(), compile_flags()
+    with tempfile.TemporaryDirectory(prefix="gdn_build_") as tmpdir:
+        objs = [str(Path(tmpdir) / (src.stem + ".o")) for src in sources()]
+        jobs = max(1, min(len(objs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+        with ThreadPoolExecutor(jobs) as ex:
+            list(ex.map(lambda so: _run([hc, *flags, "-c", str(so[0]), "-o", so[1]], verbose),
+                        zip(sources(), objs)))
+        tmp = LIB.with_name(LIB.name + ".tmp")
+        _run([hc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
+        os.replace(tmp, LIB)
     return LIB
 
 

@@ -105,21 +105,24 @@ static int check_shape(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, 
 }
 
 // Masked calls run the chunked form as two passes (gdn_mask.hip), whose fix-up kernels hold per-head values of one
-// token in LDS: Hv <= mask_max_heads().
-static bool chunk_eligible(int Hv, int Dk, int Dv, int has_mask, int gate) {
-    return Dk == 128 && Dv == 128 && (gate == GATE_DECAY || gate == GATE_LOG) &&
-           (!has_mask || Hv <= mask_max_heads());
+// token in LDS: Hv <= mask_max_heads().  Per-channel gates run on the chunked form with bf16 inputs and no mask
+// (gdn_chunk_vg.hip).
+static bool chunk_eligible(int Hv, int Dk, int Dv, int has_mask, int gate, int in_dt) {
+    if (Dk != 128 || Dv != 128) return false;
+    if (gate == GATE_DECAY_VEC) return !has_mask && chunk_vg_supported(in_dt);
+    return !has_mask || Hv <= mask_max_heads();
 }
 
-// The form a (shape, mask, gate, requested form) resolves to, or < 0 when a requested form cannot run.
-static int resolve_form(int Hv, int Dk, int Dv, int has_mask, int gate, int form) {
+// The form a (shape, mask, gate, requested form, input dtype) resolves to, or < 0 when a requested form cannot run.
+static int resolve_form(int Hv, int Dk, int Dv, int has_mask, int gate, int form, int in_dt) {
     if (form == GDN_FORM_RECURRENT) return GDN_FORM_RECURRENT;
-    const bool ok = chunk_eligible(Hv, Dk, Dv, has_mask, gate);
+    const bool ok = chunk_eligible(Hv, Dk, Dv, has_mask, gate, in_dt);
     if (form == GDN_FORM_CHUNK) {
         if (ok) return GDN_FORM_CHUNK;
-        if (has_mask && Hv > mask_max_heads() && Dk == 128 && Dv == 128 && gate != GATE_DECAY_VEC)
-            return fail(GDN_ERR_UNSUPPORTED, "masked calls of the chunked form take Hv <= %d", mask_max_heads());
-        return fail(GDN_ERR_UNSUPPORTED, "the chunked form needs Dk = Dv = 128 and a scalar gate");
+        if (Dk != 128 || Dv != 128) return fail(GDN_ERR_UNSUPPORTED, "the chunked form needs Dk = Dv = 128");
+        if (gate == GATE_DECAY_VEC)
+            return fail(GDN_ERR_UNSUPPORTED, "the chunked form takes per-channel gates with bf16 inputs and no mask");
+        return fail(GDN_ERR_UNSUPPORTED, "masked calls of the chunked form take Hv <= %d", mask_max_heads());
     }
     return ok ? GDN_FORM_CHUNK : GDN_FORM_RECURRENT;
 }
@@ -177,18 +180,18 @@ static size_t ck_snap_bytes(int B, int T, int Hv, int W) {
 
 struct CkShape {
     int B, T, Hk, Hv;
-    bool bf16;
+    bool bf16, vg;  // vg: one decay per key channel
 };
 
 // Forward group workspace: the forward tile set of Tg tokens, plus two carried states between groups when no
 // snapshots carry them.
 static size_t ck_fwd_group_bytes(const CkShape &s, int Tg, bool ckpt) {
-    return chunk_sizes(s.B, Tg, s.Hk, s.Hv, s.bf16, false).saved + (ckpt ? 0 : 2 * align256(ck_state_bytes(s.B, s.Hv)));
+    return chunk_sizes(s.B, Tg, s.Hk, s.Hv, s.bf16, false, s.vg).saved + (ckpt ? 0 : 2 * align256(ck_state_bytes(s.B, s.Hv)));
 }
 
 // Backward group workspace: two carried state adjoints, the whole tile set and the backward buffers of Tg tokens.
 static size_t ck_bwd_group_bytes(const CkShape &s, int Tg) {
-    const ChunkSizes cs = chunk_sizes(s.B, Tg, s.Hk, s.Hv, s.bf16, true);
+    const ChunkSizes cs = chunk_sizes(s.B, Tg, s.Hk, s.Hv, s.bf16, true, s.vg);
     return 2 * align256(ck_state_bytes(s.B, s.Hv)) + align256(cs.saved) + cs.work;
 }
 
@@ -225,7 +228,7 @@ struct MaskSaved {
 };
 static MaskSaved mask_saved(const CkShape &s, int chunk) {
     const int W = ck_window(chunk);
-    const size_t tiles = chunk_sizes(s.B, s.T, s.Hk, s.Hv, s.bf16, true).saved;
+    const size_t tiles = chunk_sizes(s.B, s.T, s.Hk, s.Hv, s.bf16, true, s.vg).saved;
     const size_t ng = (size_t)s.B * s.T * s.Hv * 4, nv = ng * kChunkD;
     MaskSaved m{};
     size_t off = 0;
@@ -247,7 +250,7 @@ struct MaskWork {
 static MaskWork mask_work(const CkShape &s, int chunk) {
     const int W = ck_window(chunk);
     MaskWork m{};
-    m.pass_bytes = W ? ck_bwd_target_bytes(s, W) : chunk_sizes(s.B, s.T, s.Hk, s.Hv, s.bf16, true).work;
+    m.pass_bytes = W ? ck_bwd_target_bytes(s, W) : chunk_sizes(s.B, s.T, s.Hk, s.Hv, s.bf16, true, s.vg).work;
     const size_t nqk = (size_t)s.B * s.T * s.Hk * kChunkD * 4, ng = (size_t)s.B * s.T * s.Hv * 4, nv = ng * kChunkD;
     const size_t nst = ck_state_bytes(s.B, s.Hv);
     const size_t sizes[6] = {nqk, nqk, nv, ng, ng, nst};
@@ -268,6 +271,9 @@ static size_t mask_fwd_only_head(const CkShape &s) {
 }
 
 static size_t dt_size(int dt) { return dt == DT_F32 ? 4 : 2; }
+
+// Gate values per (token, value head): one, or one per key channel.
+static size_t gate_width(int gate) { return gate == GATE_DECAY_VEC ? kChunkD : 1; }
 
 template <class P>
 static P *tok_offset(P *p, size_t elems, int dt) {
@@ -328,21 +334,21 @@ int64_t gdn_num_snapshots(int T, int chunk) {
     return (int64_t)((T + chunk - 1) / chunk) - 1;
 }
 
-int gdn_select_form(int Hv, int Dk, int Dv, int has_mask, int gate_kind, int form) {
+int gdn_select_form(int Hv, int Dk, int Dv, int has_mask, int gate_kind, int form, int in_dtype) {
     g_err[0] = 0;
-    return resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form);
+    return resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form, in_dtype);
 }
 
 size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind, int has_mask,
                        int form, int in_dtype) {
     if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
-    const int f = resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form, in_dtype);
     if (f < 0 || B == 0 || T == 0) return 0;
     if (f == GDN_FORM_CHUNK) {
         const int W = ck_window(chunk);
-        if (has_mask) return mask_saved({B, T, Hk, Hv, in_dtype == DT_BF16}, chunk).total;
+        if (has_mask) return mask_saved({B, T, Hk, Hv, in_dtype == DT_BF16, false}, chunk).total;
         if (W) return ck_snap_bytes(B, T, Hv, W);
-        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true).saved;
+        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true, gate_kind == GATE_DECAY_VEC).saved;
     }
     return rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
 }
@@ -350,10 +356,10 @@ size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, 
 size_t gdn_fwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind, int has_mask,
                                int form, int in_dtype, int with_saved) {
     if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
-    const int f = resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form, in_dtype);
     if (f != GDN_FORM_CHUNK || B == 0 || T == 0) return 0;
     const int W = ck_window(chunk);
-    const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16};
+    const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16, gate_kind == GATE_DECAY_VEC};
     if (has_mask) {
         // pass 2 runs forward-only when checkpointing; a forward-only call also holds g', beta' and z
         if (with_saved) return W ? std::max(ck_fwd_target_bytes(shp, W, true), ck_fwd_target_bytes(shp, W, false)) : 0;
@@ -371,11 +377,11 @@ namespace gdn {
 static int ck_forward(const ChunkCall &base, int chunk, void *saved, size_t saved_bytes, void *ws, size_t ws_bytes,
                       hipStream_t st) {
     const int B = base.B, T = base.T, Hk = base.Hk, Hv = base.Hv;
-    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16};
+    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16, base.gate == GATE_DECAY_VEC};
     const int W = ck_window(chunk);
     int rc;
     if (saved && !W) {  // the whole tile set, kept for the backward
-        const size_t need = chunk_sizes(B, T, Hk, Hv, shp.bf16, true).saved;
+        const size_t need = chunk_sizes(B, T, Hk, Hv, shp.bf16, true, shp.vg).saved;
         if (saved_bytes < need)
             return fail(GDN_ERR_WORKSPACE, "saved buffer of %zu bytes is smaller than the %zu bytes required",
                         saved_bytes, need);
@@ -420,7 +426,7 @@ static int ck_forward(const ChunkCall &base, int chunk, void *saved, size_t save
         cc.q = tok_offset(base.q, (size_t)ts * Hk * kChunkD, base.in_dt);
         cc.k = tok_offset(base.k, (size_t)ts * Hk * kChunkD, base.in_dt);
         cc.v = tok_offset(base.v, (size_t)ts * Hv * kChunkD, base.in_dt);
-        cc.g = base.g + (size_t)ts * Hv;
+        cc.g = base.g + (size_t)ts * Hv * gate_width(base.gate);
         cc.beta = base.beta + (size_t)ts * Hv;
         cc.y = tok_offset(base.y, (size_t)ts * Hv * kChunkD, base.out_dt);
         cc.T = Tg;
@@ -456,11 +462,11 @@ static int ck_forward(const ChunkCall &base, int chunk, void *saved, size_t save
 static int ck_backward(const ChunkCall &base, int chunk, const void *saved, size_t saved_bytes, void *ws,
                        size_t ws_bytes, hipStream_t st) {
     const int B = base.B, T = base.T, Hk = base.Hk, Hv = base.Hv;
-    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16};
+    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16, base.gate == GATE_DECAY_VEC};
     const int W = ck_window(chunk);
     int rc;
     if (!W) {
-        const ChunkSizes cs = chunk_sizes(B, T, Hk, Hv, shp.bf16, true);
+        const ChunkSizes cs = chunk_sizes(B, T, Hk, Hv, shp.bf16, true, shp.vg);
         if (!saved || saved_bytes < cs.saved)
             return fail(GDN_ERR_INVALID, "the saved buffer written by gdn_fwd (%zu bytes) is required", cs.saved);
         if (!ws || ws_bytes < cs.work)
@@ -492,7 +498,7 @@ static int ck_backward(const ChunkCall &base, int chunk, const void *saved, size
     const size_t sb = align256(ck_state_bytes(B, Hv));
     char *w8 = static_cast<char *>(ws);
     float *carry[2] = {reinterpret_cast<float *>(w8), reinterpret_cast<float *>(w8 + sb)};
-    const ChunkSizes full = chunk_sizes(B, std::min(Gt, T), Hk, Hv, shp.bf16, true);
+    const ChunkSizes full = chunk_sizes(B, std::min(Gt, T), Hk, Hv, shp.bf16, true, shp.vg);
     char *tiles = w8 + 2 * sb, *work = tiles + align256(full.saved);
     for (int g = ng - 1; g >= 0; --g) {
         const int ts = g * Gt, Tg = std::min(Gt, T - ts);
@@ -501,13 +507,13 @@ static int ck_backward(const ChunkCall &base, int chunk, const void *saved, size
         cc.q = tok_offset(base.q, qk, base.in_dt);
         cc.k = tok_offset(base.k, qk, base.in_dt);
         cc.v = tok_offset(base.v, vv, base.in_dt);
-        cc.g = base.g + (size_t)ts * Hv;
+        cc.g = base.g + (size_t)ts * Hv * gate_width(base.gate);
         cc.beta = base.beta + (size_t)ts * Hv;
         cc.dy = tok_offset(base.dy, vv, base.dy_dt);
         cc.dq = tok_offset(base.dq, qk, base.grad_dt);
         cc.dk = tok_offset(base.dk, qk, base.grad_dt);
         cc.dv = tok_offset(base.dv, vv, base.grad_dt);
-        cc.dg = base.dg + (size_t)ts * Hv;
+        cc.dg = base.dg + (size_t)ts * Hv * gate_width(base.gate);
         cc.dbeta = base.dbeta + (size_t)ts * Hv;
         cc.T = Tg;
         cc.Ts = T;
@@ -553,7 +559,7 @@ static char *at_off(void *base, size_t off) { return static_cast<char *>(base) +
 // beta, state0, y, state_T and shapes.
 static int ck_masked_forward(const ChunkCall &base, const uint8_t *mask, int chunk, void *saved, size_t saved_bytes,
                              void *ws, size_t ws_bytes, hipStream_t st) {
-    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16};
+    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16, base.gate == GATE_DECAY_VEC};
     const int W = ck_window(chunk);
     const size_t tokens = (size_t)base.B * base.T;
     float *g2, *b2, *Z, *Yp = nullptr;
@@ -624,7 +630,7 @@ static int ck_masked_forward(const ChunkCall &base, const uint8_t *mask, int chu
 // Masked chunked backward (resolved form GDN_FORM_CHUNK, arguments checked).
 static int ck_masked_backward(const ChunkCall &base, const uint8_t *mask, int chunk, const void *saved,
                               size_t saved_bytes, void *ws, size_t ws_bytes, hipStream_t st) {
-    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16};
+    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16, base.gate == GATE_DECAY_VEC};
     const int W = ck_window(chunk);
     const size_t tokens = (size_t)base.B * base.T;
     const MaskSaved m = mask_saved(shp, chunk);
@@ -735,12 +741,12 @@ int gdn_fwd_noalloc(const void *q, const void *k, const void *v, const float *g,
     if (mask && form == GDN_FORM_CHUNK)
         return fail(GDN_ERR_UNSUPPORTED, "gdn_fwd_noalloc runs masked calls in the recurrent form only");
     if (mask) form = GDN_FORM_RECURRENT;
-    const int f = resolve_form(Hv, Dk, Dv, mask != nullptr, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, mask != nullptr, gate_kind, form, in_dtype);
     if (f < 0) return f;
     void *ws = nullptr;
     size_t ws_bytes = 0;
     if (f == GDN_FORM_CHUNK && B > 0 && T > 0) {
-        const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16};
+        const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16, gate_kind == GATE_DECAY_VEC};
         const size_t one = ck_fwd_group_bytes(shp, std::min(kChunkC, T), false);
         if (one > kNoAllocScratchBytes)
             return fail(GDN_ERR_UNSUPPORTED,
@@ -763,7 +769,7 @@ int gdn_fwd(const void *q, const void *k, const void *v, const float *g, const f
     int rc = check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form);
     if (rc) return rc;
     if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(GDN_ERR_INVALID, "unknown dtype code");
-    const int f = resolve_form(Hv, Dk, Dv, mask != nullptr, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, mask != nullptr, gate_kind, form, in_dtype);
     if (f < 0) return f;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (B == 0) return GDN_OK;
@@ -825,14 +831,14 @@ int gdn_decode_step(const void *q, const void *k, const void *v, const float *g,
 size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, int gate_kind,
                                int has_mask, int form, int in_dtype) {
     if (check_shape(B, T, Hk, Hv, Dk, Dv, chunk, gate_kind, form)) return 0;
-    const int f = resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form, in_dtype);
     if (f < 0) return 0;
     if (f == GDN_FORM_CHUNK) {
         if (B == 0 || T == 0) return 0;
         const int W = ck_window(chunk);
-        if (has_mask) return mask_work({B, T, Hk, Hv, in_dtype == DT_BF16}, chunk).total;
-        if (W) return ck_bwd_target_bytes({B, T, Hk, Hv, in_dtype == DT_BF16}, W);
-        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true).work;
+        if (has_mask) return mask_work({B, T, Hk, Hv, in_dtype == DT_BF16, false}, chunk).total;
+        if (W) return ck_bwd_target_bytes({B, T, Hk, Hv, in_dtype == DT_BF16, gate_kind == GATE_DECAY_VEC}, W);
+        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true, gate_kind == GATE_DECAY_VEC).work;
     }
     return bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind).total;
 }
@@ -847,7 +853,7 @@ int gdn_bwd(const void *q, const void *k, const void *v, const float *g, const f
     if (rc) return rc;
     if (!dtype_ok(in_dtype) || !dtype_ok(dy_dtype) || !dtype_ok(grad_dtype))
         return fail(GDN_ERR_INVALID, "unknown dtype code");
-    const int f = resolve_form(Hv, Dk, Dv, mask != nullptr, gate_kind, form);
+    const int f = resolve_form(Hv, Dk, Dv, mask != nullptr, gate_kind, form, in_dtype);
     if (f < 0) return f;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (B == 0) return GDN_OK;

@@ -46,11 +46,13 @@ struct ChunkSizes {
     };
     Buf H, G, T, P, W, U, Dl;         // tile set
     Buf Wb, KTb, Pb, PTb, QTb, nWTb;  // bf16 operand tiles of the bf16 set
+    Buf Gv, QGb, KDb;                 // per-channel gates (bf16 set)
     size_t saved;                     // size of the tile set
     Buf dH, dDl, part;                // backward workspace
     size_t work;                      // its size
 };
-ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd);
+// vg: one decay per key channel (GATE_DECAY_VEC), bf16 set only.
+ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd, bool vg = false);
 
 // One launch of a chunked stage.  q, k, v, g, beta, y, dy, dq, dk, dv, dg and dbeta point at the launch's first
 // token; T is the launch's token count and Ts the token stride of a sequence (the full length).  tiles / work are
@@ -70,6 +72,8 @@ struct ChunkCall {
 // stage: "prep" | "fwd" (forward) or "seq" | "local" (backward; "local" walks the value heads of each key head
 // and writes dq and dk).  With recompute, "fwd" runs every window of the launch at once.
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st);
+// The chunked form takes per-channel gates (GATE_DECAY_VEC) for bf16 inputs (gdn_chunk_vg.hip).
+bool chunk_vg_supported(int in_dt);
 
 // Masked steps on the chunked form (gdn_mask.hip): tensors of B*T tokens, contiguous; q, k [tok][Hk][Dk], v, y, dy
 // [tok][Hv][Dv], g, beta [tok][Hv] (the raw gates), mask [tok]; Z, Yp, dy1, dz and the passes' parts fp32.

@@ -56,7 +56,7 @@ class _GDNRecurrence(torch.autograd.Function):
         gate = gate_kind_for(g, log_gate)
         lib = L.load()
         has_mask = int(mask is not None)
-        resolved = int(lib.gdn_select_form(Hv, Dk, Dv, has_mask, gate, form))
+        resolved = int(lib.gdn_select_form(Hv, Dk, Dv, has_mask, gate, form, L.DTYPE_CODE[in_dtype]))
         if resolved < 0:
             L.check(resolved)
         y = torch.empty((B, T, Hv, Dv), device=dev, dtype=out_dtype)

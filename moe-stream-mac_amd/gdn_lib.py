@@ -47,7 +47,7 @@ _SIGS = {
     "gdn_version": ([], _i),
     "gdn_last_error": ([], ctypes.c_char_p),
     "gdn_num_snapshots": ([_i, _i], ctypes.c_int64),
-    "gdn_select_form": ([_i] * 6, _i),
+    "gdn_select_form": ([_i] * 7, _i),
     "gdn_saved_bytes": ([_i] * 11, ctypes.c_size_t),
     "gdn_fwd_workspace_bytes": ([_i] * 12, ctypes.c_size_t),
     "gdn_fwd": ([_vp] * 10 + [_sz, _vp, _sz] + [_i] * 11 + [_vp], _i),

@@ -26,13 +26,20 @@ int main(void) {
     CHECK(gdn_version() > 0);
 
     /* forms */
-    CHECK(gdn_select_form(32, 128, 128, 0, GDN_GATE_LOG, GDN_FORM_AUTO) == GDN_FORM_CHUNK);
-    CHECK(gdn_select_form(32, 128, 128, 1, GDN_GATE_LOG, GDN_FORM_AUTO) == GDN_FORM_CHUNK);
-    CHECK(gdn_select_form(32, 64, 128, 0, GDN_GATE_DECAY, GDN_FORM_AUTO) == GDN_FORM_RECURRENT);
-    CHECK(gdn_select_form(32, 128, 128, 0, GDN_GATE_DECAY_VEC, GDN_FORM_CHUNK) == GDN_ERR_UNSUPPORTED);
+    CHECK(gdn_select_form(32, 128, 128, 0, GDN_GATE_LOG, GDN_FORM_AUTO, GDN_F32) == GDN_FORM_CHUNK);
+    CHECK(gdn_select_form(32, 128, 128, 1, GDN_GATE_LOG, GDN_FORM_AUTO, GDN_F32) == GDN_FORM_CHUNK);
+    CHECK(gdn_select_form(32, 64, 128, 0, GDN_GATE_DECAY, GDN_FORM_AUTO, GDN_F32) == GDN_FORM_RECURRENT);
+    CHECK(gdn_select_form(32, 128, 128, 0, GDN_GATE_DECAY_VEC, GDN_FORM_CHUNK, GDN_F32) == GDN_ERR_UNSUPPORTED);
+    /* per-channel gates: the chunked form for bf16 inputs without a mask */
+    CHECK(gdn_select_form(32, 128, 128, 0, GDN_GATE_DECAY_VEC, GDN_FORM_AUTO, GDN_BF16) == GDN_FORM_CHUNK);
+    CHECK(gdn_select_form(32, 128, 128, 1, GDN_GATE_DECAY_VEC, GDN_FORM_AUTO, GDN_BF16) == GDN_FORM_RECURRENT);
+    CHECK(gdn_saved_bytes(2, 300, 16, 32, 128, 128, 64, GDN_GATE_DECAY_VEC, 0, GDN_FORM_AUTO, GDN_BF16) >
+          gdn_saved_bytes(2, 300, 16, 32, 128, 128, 64, GDN_GATE_LOG, 0, GDN_FORM_AUTO, GDN_BF16));
+    CHECK(gdn_fwd_workspace_bytes(2, 300, 16, 32, 128, 128, 64, GDN_GATE_DECAY_VEC, 0, GDN_FORM_AUTO, GDN_BF16, 0) > 0);
+    CHECK(gdn_bwd_workspace_bytes(2, 300, 16, 32, 128, 128, 256, GDN_GATE_DECAY_VEC, 0, GDN_FORM_AUTO, GDN_BF16) > 0);
     /* masked calls above 256 value heads: AUTO resolves to the recurrent form, and the size queries follow it */
-    CHECK(gdn_select_form(260, 128, 128, 1, GDN_GATE_LOG, GDN_FORM_AUTO) == GDN_FORM_RECURRENT);
-    CHECK(gdn_select_form(260, 128, 128, 1, GDN_GATE_LOG, GDN_FORM_CHUNK) == GDN_ERR_UNSUPPORTED && err_has("Hv <= 256"));
+    CHECK(gdn_select_form(260, 128, 128, 1, GDN_GATE_LOG, GDN_FORM_AUTO, GDN_F32) == GDN_FORM_RECURRENT);
+    CHECK(gdn_select_form(260, 128, 128, 1, GDN_GATE_LOG, GDN_FORM_CHUNK, GDN_F32) == GDN_ERR_UNSUPPORTED && err_has("Hv <= 256"));
     CHECK(gdn_saved_bytes(1, 300, 130, 260, 128, 128, 64, GDN_GATE_LOG, 1, GDN_FORM_AUTO, GDN_BF16) ==
           gdn_saved_bytes(1, 300, 130, 260, 128, 128, 64, GDN_GATE_LOG, 1, GDN_FORM_RECURRENT, GDN_BF16));
     CHECK(gdn_bwd_workspace_bytes(1, 300, 130, 260, 128, 128, 64, GDN_GATE_LOG, 1, GDN_FORM_AUTO, GDN_BF16) ==

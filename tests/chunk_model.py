@@ -182,3 +182,167 @@ def run(q, k, v, g_log, beta, S0, dY, dS_T, C=64, z_form=False):
         dh = dh_prev
     n = T_len
     return y[:n], S_T, dq[:n], dk[:n], dv[:n], dg[:n], db[:n], dh.T
+
+
+# ------------------------------------------------------------------------------------------ per-channel gates
+#
+# With one log decay per key channel (g_log [C, Dk]) the cumulative decay is G [C, Dk] and every decay factor
+# depends on the channel, exp(G_rj - G_sj):
+#
+#   A_rs = beta_r sum_j k_rj k_sj exp(G_rj - G_sj)  (s < r)      T = (I + A)^-1
+#   P_rs = sum_j q_rj k_sj exp(G_rj - G_sj)  (s <= r)
+#   W = T diag(beta) (K * exp(G))    U = T diag(beta) V    Delta = U - W h
+#   Y = (Q * exp(G)) h + P Delta     h' = diag(exp(G_C)) h + (K * exp(G_C - G))^T Delta
+#
+# The pair sums cannot be one product of K exp(G) and K exp(-G) (exp(-G_s) overflows over a chunk), so they are
+# formed per 16-token block pair: below the diagonal blocks through the last token b of the block before R,
+# M_RS = (X_R * exp(G_R - G_b)) (Y_S * exp(G_b - G_S))^T with both factors <= 1, and elementwise on the diagonal
+# blocks.  Their VJP uses the same split.
+
+SUB = 16
+
+
+def pair_direct(X, Y, G, incl):
+    """M_rs = sum_j X_rj Y_sj exp(G_rj - G_sj) for s < r (s <= r with incl), zero above."""
+    C = X.shape[0]
+    M = np.zeros((C, C))
+    for r in range(C):
+        for s in range(r + 1 if incl else r):
+            M[r, s] = (X[r] * Y[s] * np.exp(G[r] - G[s])).sum()
+    return M
+
+
+def pair_blocked(X, Y, G, incl):
+    """pair_direct through 16-token blocks: products of factors <= 1 below the diagonal blocks."""
+    C = X.shape[0]
+    M = np.zeros((C, C))
+    for R in range(C // SUB):
+        rs = slice(SUB * R, SUB * R + SUB)
+        if R:
+            b = SUB * R - 1
+            xl = X[rs] * np.exp(G[rs] - G[b])
+            ys = Y[:SUB * R] * np.exp(G[b] - G[:SUB * R])
+            M[rs, :SUB * R] = xl @ ys.T
+        for r in range(SUB * R, SUB * R + SUB):
+            for s in range(SUB * R, r + 1 if incl else r):
+                M[r, s] = (X[r] * Y[s] * np.exp(G[r] - G[s])).sum()
+    return M
+
+
+def pair_vjp(X, Y, G, dM):
+    """Cotangents of M = pair(X, Y, G) (dM already masked): dX, dY and dG (the +G_r role minus the -G_s role)."""
+    C = X.shape[0]
+    dX, dY = np.zeros_like(X), np.zeros_like(Y)
+    for R in range(C // SUB):
+        rs = slice(SUB * R, SUB * R + SUB)
+        if R:
+            b = SUB * R - 1
+            el = np.exp(G[rs] - G[b])
+            es = np.exp(G[b] - G[:SUB * R])
+            dX[rs] += (dM[rs, :SUB * R] @ (Y[:SUB * R] * es)) * el
+            dY[:SUB * R] += (dM[rs, :SUB * R].T @ (X[rs] * el)) * es
+        for r in range(SUB * R, SUB * R + SUB):
+            for s in range(SUB * R, SUB * R + SUB):
+                if dM[r, s]:
+                    e = np.exp(G[r] - G[s])
+                    dX[r] += dM[r, s] * Y[s] * e
+                    dY[s] += dM[r, s] * X[r] * e
+    return dX, dY, X * dX - Y * dY
+
+
+def vg_prep(k, v, q, g_log, beta):
+    """Per chunk: (G, T, W, U, P, Ahat) for one head with per-channel log decays g_log [C, Dk]."""
+    C = k.shape[0]
+    G = np.cumsum(g_log.astype(np.float64), axis=0)
+    Ahat = pair_blocked(k, k, G, incl=False)
+    A = beta[:, None] * Ahat
+    T = np.linalg.inv(np.eye(C) + A)
+    W = T @ (beta[:, None] * k * np.exp(G))
+    U = T @ (beta[:, None] * v)
+    P = pair_blocked(q, k, G, incl=True)
+    return G, T, W, U, P, Ahat
+
+
+def vg_fwd_chunk(h, q, k, G, W, U, P):
+    Delta = U - W @ h
+    Y = (q * np.exp(G)) @ h + P @ Delta
+    gC = G[-1]
+    h_next = np.exp(gC)[:, None] * h + (k * np.exp(gC - G)).T @ Delta
+    return Delta, Y, h_next
+
+
+def vg_bwd_state_chunk(dh_next, q, k, G, W, P, dY):
+    gC = G[-1]
+    dDelta = (k * np.exp(gC - G)) @ dh_next + P.T @ dY
+    dh = np.exp(gC)[:, None] * dh_next + (q * np.exp(G)).T @ dY - W.T @ dDelta
+    return dDelta, dh
+
+
+def vg_bwd_local_chunk(q, k, v, beta, G, P, Ahat, h, dh_next, Delta, TdD, dY):
+    """dq, dk, dv, dbeta, dg_log [C, Dk] for one chunk of one head, from TdD = T^T dDelta."""
+    gC = G[-1]
+    eG, eD = np.exp(G), np.exp(gC - G)
+    Qg, Kg, Kd = q * eG, k * eG, k * eD
+    dQg = dY @ h.T
+    dq = dQg * eG
+    dG = Qg * dQg
+    dKd = Delta @ dh_next.T
+    dk = dKd * eD
+    dG -= Kd * dKd
+    dgC = (Kd * dKd).sum(0) + np.exp(gC) * (dh_next * h).sum(1)
+    # through Z = diag(beta) V - diag(beta) (K * exp(G)) h
+    Y2 = TdD @ h.T
+    dKg = -beta[:, None] * Y2
+    dk += dKg * eG
+    dG += Kg * dKg
+    dv = beta[:, None] * TdD
+    dbeta = (v * TdD).sum(1) - (Kg * Y2).sum(1)
+    # P and A
+    dP = np.tril(dY @ Delta.T)
+    dXq, dYk, dGp = pair_vjp(q, k, G, dP)
+    dq += dXq
+    dk += dYk
+    dG += dGp
+    dA = -np.tril(TdD @ Delta.T, -1)
+    dbeta += (dA * Ahat).sum(1)
+    dXk, dYk2, dGa = pair_vjp(k, k, G, beta[:, None] * dA)
+    dk += dXk + dYk2
+    dG += dGa
+    dg_log = np.cumsum(dG[::-1], axis=0)[::-1] + dgC
+    return dq, dk, dv, dbeta, dg_log
+
+
+def vg_run(q, k, v, g_log, beta, S0, dY, dS_T, C=64):
+    """Whole-sequence forward + VJP for one batch element and one value head with per-channel log decays
+    g_log [T, Dk].  Returns (y, S_T, dq, dk, dv, dg_log, dbeta, dS0), the states in [Dv, Dk] layout."""
+    T_len, Dk = q.shape
+    Dv = v.shape[1]
+    nc = -(-T_len // C)
+    pad = nc * C - T_len
+    padf = lambda x: np.concatenate([x, np.zeros((pad,) + x.shape[1:], x.dtype)]) if pad else x
+    q, k, v, g_log, beta, dY = (padf(np.asarray(x, np.float64)) for x in (q, k, v, g_log, beta, dY))
+    h = np.asarray(S0, np.float64).T.copy()
+    preps, hs, Ds = [], [], []
+    y = np.zeros((nc * C, Dv))
+    for c in range(nc):
+        sl = slice(c * C, (c + 1) * C)
+        pr = vg_prep(k[sl], v[sl], q[sl], g_log[sl], beta[sl])
+        preps.append(pr)
+        hs.append(h)
+        G, T, W, U, P, _ = pr
+        Delta, Y, h = vg_fwd_chunk(h, q[sl], k[sl], G, W, U, P)
+        Ds.append(Delta)
+        y[sl] = Y
+    S_T = h.T
+    dh = np.asarray(dS_T, np.float64).T.copy()
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    dg, db = np.zeros((nc * C, Dk)), np.zeros(nc * C)
+    for c in range(nc - 1, -1, -1):
+        sl = slice(c * C, (c + 1) * C)
+        G, T, W, U, P, Ahat = preps[c]
+        dDelta, dh_prev = vg_bwd_state_chunk(dh, q[sl], k[sl], G, W, P, dY[sl])
+        out = vg_bwd_local_chunk(q[sl], k[sl], v[sl], beta[sl], G, P, Ahat, hs[c], dh, Ds[c], T.T @ dDelta, dY[sl])
+        dq[sl], dk[sl], dv[sl], db[sl], dg[sl] = out
+        dh = dh_prev
+    n = T_len
+    return y[:n], S_T, dq[:n], dk[:n], dv[:n], dg[:n], db[:n], dh.T

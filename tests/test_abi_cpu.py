@@ -158,16 +158,23 @@ def test_saved_sizes_by_form():
     assert rec == 63 * 32 * 128 * 128 * 4
     ck = lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_AUTO, L.F32)
     assert ck == lib.gdn_saved_bytes(1, 4096, 16, 32, 128, 128, 64, L.GATE_LOG, 0, L.FORM_CHUNK, L.F32) > rec
-    assert lib.gdn_select_form(32, 128, 128, 0, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK
-    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK   # masks: two chunked passes
-    assert lib.gdn_select_form(32, 8, 8, 0, L.GATE_DECAY, L.FORM_AUTO) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(32, 128, 128, 0, L.GATE_LOG, L.FORM_AUTO, L.F32) == L.FORM_CHUNK
+    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO, L.F32) == L.FORM_CHUNK   # masks: two chunked passes
+    assert lib.gdn_select_form(32, 8, 8, 0, L.GATE_DECAY, L.FORM_AUTO, L.F32) == L.FORM_RECURRENT
     # masked calls take the chunked form up to 256 value heads; above, AUTO falls back to the recurrent form and
     # the size queries answer for that form
-    assert lib.gdn_select_form(256, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK
-    assert lib.gdn_select_form(260, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_RECURRENT
-    assert lib.gdn_select_form(260, 128, 128, 0, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK
-    assert lib.gdn_select_form(260, 128, 128, 1, L.GATE_LOG, L.FORM_CHUNK) == L.GDN_ERR_UNSUPPORTED
+    assert lib.gdn_select_form(256, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO, L.F32) == L.FORM_CHUNK
+    assert lib.gdn_select_form(260, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO, L.F32) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(260, 128, 128, 0, L.GATE_LOG, L.FORM_AUTO, L.F32) == L.FORM_CHUNK
+    assert lib.gdn_select_form(260, 128, 128, 1, L.GATE_LOG, L.FORM_CHUNK, L.F32) == L.GDN_ERR_UNSUPPORTED
     assert b"Hv <= 256" in lib.gdn_last_error()
+    # per-channel gates: the chunked form with bf16 inputs and no mask, the recurrent form otherwise
+    assert lib.gdn_select_form(32, 128, 128, 0, L.GATE_DECAY_VEC, L.FORM_AUTO, L.BF16) == L.FORM_CHUNK
+    assert lib.gdn_select_form(32, 128, 128, 0, L.GATE_DECAY_VEC, L.FORM_AUTO, L.F32) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_DECAY_VEC, L.FORM_AUTO, L.BF16) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(32, 64, 64, 0, L.GATE_DECAY_VEC, L.FORM_AUTO, L.BF16) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_DECAY_VEC, L.FORM_CHUNK, L.BF16) == L.GDN_ERR_UNSUPPORTED
+    assert b"per-channel gates" in lib.gdn_last_error()
     for q in (lambda f: lib.gdn_saved_bytes(1, 300, 130, 260, 128, 128, 64, L.GATE_LOG, 1, f, L.BF16),
               lambda f: lib.gdn_bwd_workspace_bytes(1, 300, 130, 260, 128, 128, 64, L.GATE_LOG, 1, f, L.BF16)):
         assert q(L.FORM_AUTO) == q(L.FORM_RECURRENT) > 0

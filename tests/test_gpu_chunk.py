@@ -232,8 +232,8 @@ def test_chunk_matches_recurrent_wide_slices(dev, B):
 def test_auto_form_selection(dev):
     import gdn_lib as L
     lib = L.load()
-    assert lib.gdn_select_form(32, 128, 128, 0, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK
-    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK   # masks: two chunked passes
-    assert lib.gdn_select_form(32, 64, 128, 0, L.GATE_DECAY, L.FORM_AUTO) == L.FORM_RECURRENT
-    assert lib.gdn_select_form(32, 128, 128, 0, L.GATE_DECAY_VEC, L.FORM_AUTO) == L.FORM_RECURRENT
-    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_DECAY_VEC, L.FORM_CHUNK) == L.GDN_ERR_UNSUPPORTED
+    assert lib.gdn_select_form(32, 128, 128, 0, L.GATE_LOG, L.FORM_AUTO, L.F32) == L.FORM_CHUNK
+    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO, L.F32) == L.FORM_CHUNK   # masks: two chunked passes
+    assert lib.gdn_select_form(32, 64, 128, 0, L.GATE_DECAY, L.FORM_AUTO, L.F32) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(32, 128, 128, 0, L.GATE_DECAY_VEC, L.FORM_AUTO, L.F32) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_DECAY_VEC, L.FORM_CHUNK, L.F32) == L.GDN_ERR_UNSUPPORTED

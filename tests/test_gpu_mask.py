@@ -93,8 +93,8 @@ def _check(got, d, groups, rep, tol, label, **kw):
 def test_masked_calls_select_the_chunked_form(dev):
     import gdn_lib as L
     lib = L.load()
-    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_CHUNK
-    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_DECAY_VEC, L.FORM_AUTO) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO, L.F32) == L.FORM_CHUNK
+    assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_DECAY_VEC, L.FORM_AUTO, L.F32) == L.FORM_RECURRENT
 
 
 def test_masked_call_above_256_value_heads_runs_recurrent(dev):
@@ -102,7 +102,7 @@ def test_masked_call_above_256_value_heads_runs_recurrent(dev):
     256 heads of a token), and the result matches the oracle on two key-head groups."""
     import gdn_lib as L
     lib = L.load()
-    assert lib.gdn_select_form(260, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(260, 128, 128, 1, L.GATE_LOG, L.FORM_AUTO, L.F32) == L.FORM_RECURRENT
     d = _inputs(1, 40, 130, 260, seed=260)
     print("masked Hv=260 T=40 fp32, auto form", flush=True)
     got = _gpu(d, dev)

@@ -1,0 +1,162 @@
+"""GPU parity of per-channel (vector) gates, one decay per key channel [B,T,Hv,Dk] (tools/gdn_vjp.py:174-179,
+311-314), against the fp64 oracle.
+
+With bf16 inputs, Dk = Dv = 128 and no mask they run on the chunked form (gdn_chunk_vg.hip: the decay factors of
+the pair sums formed per 16-token block pair through a boundary token, so that no factor exceeds 1); fp32 inputs and
+masked calls run on the token-recurrent form.  Bars (normalised error max|gpu - oracle| / max|oracle| per output):
+1e-2 on the chunked form with bf16 inputs; on the recurrent form 1e-4 for fp32 inputs and for the fp32 outputs with
+bf16 inputs, 4e-3 for its bf16 dq / dk / dv.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+NAMES = ("y", "S_T", "dq", "dk", "dv", "dg", "dbeta", "dS0")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import gdn_lib
+    gdn_lib.load()
+    return torch.device("cuda:0")
+
+
+def nerr(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max()) / max(float(np.abs(b).max()), 1e-30)
+
+
+def _inputs(B, T, Hk, Hv, seed, decay=(0.7, 1.0), log_decay=None, masked=False, bf16=True):
+    """The reference's matrix distributions (tools/test_gdn_vjp.py:21-55) at Dk = Dv = 128: q, k L2-normalised (q
+    times Dk^-1/2), decays U(0.7, 1) per channel (or exp(-U(log_decay))), beta U(0.05, 0.95), S0, dy, dS_T normal."""
+    rng = np.random.default_rng(seed)
+    q = O.l2norm(rng.standard_normal((B, T, Hk, D)), 1e-6, D ** -0.5)
+    k = O.l2norm(rng.standard_normal((B, T, Hk, D)), 1e-6, 1.0)
+    if log_decay is None:
+        dec = rng.uniform(decay[0], decay[1], (B, T, Hv, D))
+    else:
+        dec = np.exp(-rng.uniform(log_decay[0], log_decay[1], (B, T, Hv, D)))
+    d = dict(q=q, k=k, v=rng.standard_normal((B, T, Hv, D)), decay=dec, beta=rng.uniform(0.05, 0.95, (B, T, Hv)),
+             state=rng.standard_normal((B, Hv, D, D)) * 0.1, dy=rng.standard_normal((B, T, Hv, D)),
+             dS_T=rng.standard_normal((B, Hv, D, D)) * 0.1)
+    d = {n: x.astype(np.float32) for n, x in d.items()}
+    d["mask"] = (np.random.default_rng(seed + 1).random((B, T)) > 0.2) if masked else None
+    if bf16:
+        bf = lambda x: torch.tensor(x).bfloat16().float().numpy()
+        d = dict(d, q=bf(d["q"]), k=bf(d["k"]), v=bf(d["v"]), dy=bf(d["dy"]))
+    return d
+
+
+def _gpu(d, dev, dtype, chunk=64, form=None):
+    import gdn_engine
+    t = lambda x, dt=torch.float32: torch.tensor(np.asarray(x), device=dev, dtype=dt)
+    q, k, v = (t(d[n], dtype).requires_grad_(True) for n in ("q", "k", "v"))
+    g, beta, S0 = (t(d[n]).requires_grad_(True) for n in ("decay", "beta", "state"))
+    mask = None if d["mask"] is None else torch.tensor(d["mask"], device=dev)
+    y, S = gdn_engine.recurrence(q, k, v, g, beta, S0, mask, chunk, form=form)
+    grads = torch.autograd.grad([y, S], [q, k, v, g, beta, S0], [t(d["dy"], y.dtype), t(d["dS_T"])])
+    torch.cuda.synchronize()
+    return [x.detach().float().cpu().numpy() for x in (y, S, *grads)]
+
+
+def _oracle(d, chunk=64):
+    (y, S), g = O.gated_delta_chunked_vjp(d["q"], d["k"], d["v"], d["decay"], d["beta"], d["state"], d["mask"],
+                                          d["dy"], d["dS_T"], chunk=chunk, dtype=np.float64)
+    return [y, S, *g]
+
+
+def _bar(name, chunked, bf16):
+    if chunked:
+        return 1e-2
+    if bf16 and name in ("dq", "dk", "dv"):
+        return 4e-3
+    return 1e-4
+
+
+def _check(got, want, chunked, bf16, label):
+    errs = {n: nerr(a, w) for n, a, w in zip(NAMES, got, want)}
+    print(label, {n: f"{e:.1e}" for n, e in errs.items()}, flush=True)
+    for n, e in errs.items():
+        assert e <= _bar(n, chunked, bf16), (label, n, e)
+
+
+def test_vector_gates_select_the_chunked_form_for_bf16(dev):
+    import gdn_lib as L
+    lib = L.load()
+    assert lib.gdn_select_form(4, D, D, 0, L.GATE_DECAY_VEC, L.FORM_AUTO, L.BF16) == L.FORM_CHUNK
+    assert lib.gdn_select_form(4, D, D, 0, L.GATE_DECAY_VEC, L.FORM_AUTO, L.F32) == L.FORM_RECURRENT
+    assert lib.gdn_select_form(4, D, D, 1, L.GATE_DECAY_VEC, L.FORM_AUTO, L.BF16) == L.FORM_RECURRENT
+
+
+@pytest.mark.parametrize("T", [1, 63, 64, 65, 200])
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_reference_vector_gate_matrix_at_d128(dev, T, masked, dtype):
+    """The reference's lengths with and without a mask, bf16 (chunked form without a mask) and fp32 (recurrent)."""
+    bf16 = dtype == torch.bfloat16
+    d = _inputs(2, T, 2, 4, seed=300 + T + 7 * masked, masked=masked, bf16=bf16)
+    print(f"vector gates {dtype} T={T} masked={masked}", flush=True)
+    _check(_gpu(d, dev, dtype), _oracle(d), bf16 and not masked, bf16, f"T={T} masked={masked} {dtype}")
+
+
+@pytest.mark.parametrize("log_decay", [(0.0, 1.5), (0.0, 6.0)])
+def test_strong_decays_on_the_chunked_form(dev, log_decay):
+    """Decays down to exp(-6) per token: over a chunk exp(-G) reaches exp(380), beyond fp32, while every factor the
+    chunked form forms stays <= 1."""
+    d = _inputs(2, 200, 2, 4, seed=11, log_decay=log_decay)
+    print(f"vector gates bf16 T=200 log decays {log_decay}", flush=True)
+    _check(_gpu(d, dev, torch.bfloat16), _oracle(d), True, True, f"log decay {log_decay}")
+
+
+def test_checkpointed_and_forward_only(dev):
+    """chunk = 256 (window snapshots, each group of windows rebuilt in backward) against the oracle; a forward-only
+    call (no graph) equals the training forward."""
+    import gdn_engine
+    d = _inputs(1, 1000, 2, 4, seed=21, log_decay=(0.0, 1.5))
+    print("vector gates bf16 T=1000 chunk=256", flush=True)
+    got = _gpu(d, dev, torch.bfloat16, chunk=256)
+    _check(got, _oracle(d), True, True, "ckpt 256")
+    t = lambda x, dt=torch.float32: torch.tensor(np.asarray(x), device=dev, dtype=dt)
+    with torch.no_grad():
+        y, S = gdn_engine.recurrence(t(d["q"], torch.bfloat16), t(d["k"], torch.bfloat16), t(d["v"], torch.bfloat16),
+                                     t(d["decay"]), t(d["beta"]), t(d["state"]), None, 64)
+    torch.cuda.synchronize()
+    assert nerr(y.float().cpu().numpy(), got[0]) <= 2e-3
+    assert nerr(S.cpu().numpy(), got[1]) <= 2e-3
+
+
+def test_measured_workload_chunked_against_recurrent(dev):
+    """B=4, T=4096, Hk=16, Hv=32, D=128, bf16, decays exp(-U(0, 1.5)) per channel (the measured vector-gate
+    workload): the chunked form against the recurrent form, every output."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    B, T, Hk, Hv = 4, 4096, 16, 32
+    n = lambda *s: torch.randn(*s, device=dev, generator=g)
+    q = (torch.nn.functional.normalize(n(B, T, Hk, D), dim=-1) * D ** -0.5).bfloat16()
+    k = torch.nn.functional.normalize(n(B, T, Hk, D), dim=-1).bfloat16()
+    v = n(B, T, Hv, D).bfloat16()
+    dec = torch.exp(-1.5 * torch.rand(B, T, Hv, D, device=dev, generator=g))
+    beta = torch.sigmoid(n(B, T, Hv))
+    dy = n(B, T, Hv, D).bfloat16()
+    print("vector gates bf16 B=4 T=4096 Hv=32: chunked against recurrent", flush=True)
+    res = {}
+    import gdn_engine
+    for form in ("chunk", "recurrent"):
+        xs = [x.detach().clone().requires_grad_(True) for x in (q, k, v, dec, beta)]
+        S0 = torch.zeros(B, Hv, D, D, device=dev, requires_grad=True)
+        y, S = gdn_engine.recurrence(*xs, S0, None, 64, form=form, output_dtype=torch.bfloat16)
+        grads = torch.autograd.grad([y], [*xs, S0], [dy])
+        torch.cuda.synchronize()
+        res[form] = [x.detach().float() for x in (y, S, *grads)]
+    for name, a, b in zip(NAMES, res["chunk"], res["recurrent"]):
+        e = float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+        print(f"  {name} {e:.1e}", flush=True)
+        assert e <= 1e-2, (name, e)
