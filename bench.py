@@ -16,8 +16,9 @@ Workloads (one GPU; the default is the T=4096 configuration the metric is quoted
                   bf16_b4_t4096 with a mask (each sequence's last 10% masked, padding): two chunked
                   passes plus the masked tokens' fix-up
   vgate_bf16_b4_t4096
-                  bf16_b4_t4096 with one decay per key channel (g [B, T, Hv, D], in decay space); runs the
-                  token-recurrent form
+                  bf16_b4_t4096 with one decay per key channel (g [B, T, Hv, D], in decay space); the chunked
+                  form with the per-channel-gate prep and local kernels (GDN_FORM=recurrent: the token-recurrent
+                  form)
   fwd_bf16_b4_t4096
                   the forward alone, as frozen layers and prefill run it (no autograd graph, no saved tiles),
                   bf16_b4_t4096's shape
@@ -65,8 +66,9 @@ def algo_model(w, form="chunk"):
       bf16 hi / lo pairs), so both are priced at the bf16 dense peak.
     fp32 (recurrent arithmetic): bytes 4 * (4 Hk D + 4 Hv D + 4 Hv) (= 98,816 B); flops 27 D^2 per head-token
       (7 D^2 forward + 20 D^2 backward), priced at the fp32 peak.
-    The recurrent form (masks, vector gates) computes the recurrence itself, 27 D^2 flops per head-token on fp32
-    VALU, whatever the input dtype; its bytes follow the dtype as above.
+    The recurrent form (head sizes other than 128; per-channel gates with fp32 inputs or a mask) computes the
+    recurrence itself, 27 D^2 flops per head-token on fp32 VALU, whatever the input dtype; its bytes follow the
+    dtype as above.
     Per-channel (vector) gates read g and write dg per key channel: 4 * 2 Hv D bytes in place of 4 * 2 Hv.
     A forward-only call (no saved state) reads q, k, v, g, beta and writes y, with the forward's third of the
     contractions (10 C D + 6 D^2 per head-token on the chunked form).
@@ -89,7 +91,8 @@ def algo_model(w, form="chunk"):
         gates = 4 * 2 * Hv * (D + 1) if w.get("vector_gate") else 4 * 4 * Hv
         return b * (4 * Hk * D + 4 * Hv * D) + gates, {"fp32": 27 * D * D * Hv}, PEAK_FP32_TFLOPS
     if w["dtype"] == "bf16":
-        nbytes = 2 * (4 * Hk * D + 4 * Hv * D) + 4 * 4 * Hv
+        gates = 4 * 2 * Hv * (D + 1) if w.get("vector_gate") else 4 * 4 * Hv
+        nbytes = 2 * (4 * Hk * D + 4 * Hv * D) + gates
         flops = {"bf16_intra_chunk": 3 * 10 * C * D * Hv, "bf16_state": 3 * 6 * D * D * Hv}
         return nbytes, flops, PEAK_BF16_TFLOPS
     nbytes = 4 * (4 * Hk * D + 4 * Hv * D + 4 * Hv)
