@@ -2,10 +2,11 @@
 
 Every case draws: the form (chunked, token-recurrent, or the default choice), the head size (128 on the chunked
 form; 32, 64 or 128 on the recurrent one), the input dtype (fp32, or bf16 with an fp32 state), B (1..3), T (1..300),
-the GQA layout (Hk 1-2, Hv/Hk 1, 2 or 4), the gate (log or decay space per head, or one decay per key channel on
-the recurrent form), the mask (none, random, or a masked tail), the snapshot interval `chunk` (16, 64, 100, 256),
+the GQA layout (Hk 1-2, Hv/Hk 1, 2 or 4), the gate (log or decay space per head, or one decay per key channel: on the
+chunked form with bf16 inputs and no mask, else on the recurrent form), the mask (none, random, or a masked tail), the snapshot interval `chunk` (16, 64, 100, 256),
 a zero or random initial state and a zero or random exit-state cotangent.  Eight more draws run at B = 1,
-T = 1000..3000 (several checkpoint windows and groups).  Bars, as normalised error max|gpu - oracle| / max|oracle|
+T = 1000..3000 (several checkpoint windows and groups), and twelve put per-channel gates on the chunked form (bf16,
+no mask) with the layout, B, T up to 1500, chunk and states drawn.  Bars, as normalised error max|gpu - oracle| / max|oracle|
 per output, are set by each output's arithmetic (``bar``): 1e-4 for fp32 inputs and for the fp32 outputs of the
 token-recurrent form with bf16 inputs, 4e-3 for that form's bf16 dq / dk / dv, 1e-2 on the chunked form with bf16
 inputs.
@@ -22,6 +23,7 @@ pytestmark = pytest.mark.gpu
 NAMES = ("y", "S_T", "dq", "dk", "dv", "dg", "dbeta", "dS0")
 N_CASES = 32
 N_LONG = 8  # B = 1, T in 1000..3000: several checkpoint windows and groups
+N_VEC = 12  # per-channel gates on the chunked form
 
 
 @pytest.fixture(scope="module")
@@ -36,21 +38,45 @@ def dev():
 def draw(i, long=False):
     rng = np.random.default_rng((9000 if long else 5000) + i)
     form = ("chunk", "recurrent", "auto")[rng.integers(3)]
-    vector = form != "chunk" and rng.random() < 0.3
-    if vector:
-        form = "recurrent" if form == "auto" else form
+    vector = bool(rng.random() < 0.3)
     D = 128 if form != "recurrent" else int(rng.choice([32, 64, 128]))
     bf16 = bool(rng.random() < 0.5)
     B, T = (1, int(rng.integers(1000, 3001))) if long else (int(rng.integers(1, 4)), int(rng.integers(1, 301)))
     Hk = int(rng.integers(1, 3))
     Hv = Hk * int(rng.choice([1, 2, 4]))
     mask_kind = ("none", "random", "tail")[rng.integers(3)]
+    if vector and form == "chunk" and not (bf16 and mask_kind == "none"):
+        form = "auto"  # the chunked form takes per-channel gates with bf16 inputs and no mask only
     chunk = int(rng.choice([16, 64, 100, 256]))
     log_gate = (not vector) and bool(rng.random() < 0.5)
     s0 = bool(rng.random() < 0.5)
     dS = bool(rng.random() < 0.5)
     return dict(form=form, vector=vector, D=D, bf16=bf16, B=B, T=T, Hk=Hk, Hv=Hv, mask=mask_kind, chunk=chunk,
                 log_gate=log_gate, s0=s0, dS=dS, seed=(8000 if long else 7000) + i)
+
+
+def draw_vector_chunked(i):
+    """One decay per key channel on the chunked form (bf16, no mask, D = 128): GQA layout, B, T (up to 1500, so
+    several checkpoint windows and groups), chunk, S0 and the exit cotangent drawn."""
+    rng = np.random.default_rng(6000 + i)
+    form = ("chunk", "auto")[rng.integers(2)]
+    B, T = int(rng.integers(1, 4)), int(rng.integers(1, 1501))
+    Hk = int(rng.integers(1, 3))
+    Hv = Hk * int(rng.choice([1, 2, 4]))
+    chunk = int(rng.choice([16, 64, 100, 256]))
+    s0 = bool(rng.random() < 0.5)
+    dS = bool(rng.random() < 0.5)
+    return dict(form=form, vector=True, D=128, bf16=True, B=B, T=T, Hk=Hk, Hv=Hv, mask="none", chunk=chunk,
+                log_gate=False, s0=s0, dS=dS, seed=7500 + i)
+
+
+def chunked(c):
+    """Whether the case runs on the chunked form (what gdn_select_form picks for it)."""
+    if c["form"] == "recurrent" or c["D"] != 128:
+        return False
+    if c["vector"]:
+        return c["bf16"] and c["mask"] == "none"
+    return True
 
 
 def inputs(c):
@@ -104,6 +130,13 @@ def test_random_long_combination_against_oracle(dev, i):
     check(draw(i, long=True), dev, i)
 
 
+@pytest.mark.parametrize("i", range(N_VEC))
+def test_random_vector_gate_chunked_against_oracle(dev, i):
+    c = draw_vector_chunked(i)
+    assert chunked(c)
+    check(c, dev, i)
+
+
 def check(c, dev, i):
     print("case", i, c, flush=True)
     d = inputs(c)
@@ -129,7 +162,6 @@ def bar(c, name):
     sums).  bf16 inputs on the chunked form, whose products take bf16 MFMA operands: 1e-2."""
     if not c["bf16"]:
         return 1e-4
-    recurrent = c["form"] == "recurrent" or c["vector"]
-    if not recurrent:
+    if chunked(c):
         return 1e-2
     return 4e-3 if name in ("dq", "dk", "dv") else 1e-4
