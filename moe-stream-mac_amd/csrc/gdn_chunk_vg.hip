@@ -734,19 +734,27 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
             bf8 ph, pl, zh, zl;
             split8(xp, ph, pl);
             split8(xa, zh, zl);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int pj = 64 * ch + 4 * li + t;  // column 64 ch + 16 t + li
-                const float gb = sGp[bt * VLGp + pj];
-                float y[8];
+            // the factors of this lane's four columns (contiguous in the permuted tiles), one token at a time
+            float y4[4][8];
+            {
+                const float4 gb4 = *reinterpret_cast<const float4 *>(sGp + bt * VLGp + pc0);
+                const float gb[4] = {gb4.x, gb4.y, gb4.z, gb4.w};
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const int s2 = min(s0 + i, C - 1);
-                    const float ks = bf2f(sKp[s2 * VLP + pj]);
-                    y[i] = s0 + i < 16 * R ? ks * ex2(gb - sGp[s2 * VLGp + pj]) : 0.f;
+                    const bool ok = s0 + i < 16 * R;
+                    const float4 g4 = *reinterpret_cast<const float4 *>(sGp + s2 * VLGp + pc0);
+                    const uint2 kk = *reinterpret_cast<const uint2 *>(sKp + s2 * VLP + pc0);
+                    const float gs4[4] = {g4.x, g4.y, g4.z, g4.w};
+                    const float ks4[4] = {bf2f(kk.x & 0xffffu), bf2f(kk.x >> 16), bf2f(kk.y & 0xffffu), bf2f(kk.y >> 16)};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) y4[t][i] = ok ? ks4[t] * ex2(gb[t] - gs4[t]) : 0.f;
                 }
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
                 bf8 yh, yl;
-                split8(y, yh, yl);
+                split8(y4[t], yh, yl);
                 aq[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, yh, aq[t], 0, 0, 0);
                 aq[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, yh, aq[t], 0, 0, 0);
                 aq[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, yl, aq[t], 0, 0, 0);
@@ -848,10 +856,11 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const bool at = sl == 4 * lg + e;
+                // E is zero before this lane's row and becomes 1 on it: E d + [s == r] is exact in both cases
+                const float at = sl == 4 * lg + e ? 1.f : 0.f;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    E[e][t] = at ? 1.f : E[e][t] * dn[t];
+                    E[e][t] = fmaf(E[e][t], dn[t], at);
                     const float kE = ks4[t] * E[e][t];
                     X1[t][e] = fmaf(pe[e], kE, X1[t][e]);
                     Z[t][e] = fmaf(ae[e], kE, Z[t][e]);
@@ -886,11 +895,11 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const bool at = rl == 4 * lg + e;
+                const float at = rl == 4 * lg + e ? 1.f : 0.f;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    E[e][t] = at ? 1.f : E[e][t] * dr[t];
-                    X2[t][e] = fmaf(pe[e] * qr4[t] + ae[e] * kr4[t], E[e][t], X2[t][e]);
+                    E[e][t] = fmaf(E[e][t], dr[t], at);
+                    X2[t][e] = fmaf(fmaf(ae[e], kr4[t], pe[e] * qr4[t]), E[e][t], X2[t][e]);
                 }
             }
         }
@@ -965,27 +974,59 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
         const int i = tid + p * NTB, r = i / D, j = i - r * D;
         if (r < n) a.dg[(((size_t)b * a.Ts + t0 + r) * a.Hv + hv) * D + j] = sDG[r * VLGp + j] / dec[p];
     }
-    // ---- dq | dk: this value head's parts summed over the key head's value heads (this lane's elements)
+    // ---- dq | dk: this value head's parts summed over the key head's value heads.  They leave through an fp32
+    // staging tile [64][dq 128 | dk 128] over the permuted K, Q, G tiles (dead since the diagonal loops), so that
+    // each thread moves 8-element row pieces: the running sum (part rows, the same [dq | dk] layout) is read and
+    // written, or the gradient stored, 16 bytes at a time.  A thread takes the same pieces for every value head and
+    // reads back only what it wrote itself.
+    {
+        constexpr int LSQ = 2 * D + 4;
+        static_assert(VO_K + C * LSQ * 4 <= VARENA && VO_K >= VO_DG + C * VLGp * 4, "dq | dk staging fits, clear of dG");
+        float *const sQK = F32(VO_K);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int r = r0 + 4 * lg + e;
-        if (r >= n) continue;
+        for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int j = 64 * ch + 16 * t + li;
-            float vq = X1[t][e], vk = Y2[t][e] + X2[t][e];
-            float *pr = part_row + (size_t)r * part_rs + j;
+            for (int t = 0; t < 4; ++t) {
+                const int r = r0 + 4 * lg + e, j = 64 * ch + 16 * t + li;
+                sQK[r * LSQ + j] = X1[t][e];
+                sQK[r * LSQ + D + j] = Y2[t][e] + X2[t][e];
+            }
+        __syncthreads();
+        constexpr int QPER = C * (2 * D / 8) / NTB;
+        static_assert(QPER * NTB == C * (2 * D / 8), "even split");
+#pragma unroll
+        for (int p = 0; p < QPER; ++p) {
+            const int pc = tid + p * NTB, r = pc / (2 * D / 8), c8 = (pc - r * (2 * D / 8)) * 8;
+            if (r >= n) continue;
+            float v[8];
+            {
+                const float4 x0 = *reinterpret_cast<const float4 *>(sQK + r * LSQ + c8);
+                const float4 x1 = *reinterpret_cast<const float4 *>(sQK + r * LSQ + c8 + 4);
+                v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+            }
+            float *pr = part_row + (size_t)r * part_rs + c8;
             if (!first) {
-                vq += pr[0];
-                vk += pr[D];
+                const float4 y0 = *reinterpret_cast<const float4 *>(pr), y1 = *reinterpret_cast<const float4 *>(pr + 4);
+                v[0] += y0.x; v[1] += y0.y; v[2] += y0.z; v[3] += y0.w;
+                v[4] += y1.x; v[5] += y1.y; v[6] += y1.z; v[7] += y1.w;
             }
             if (!last) {
-                pr[0] = vq;
-                pr[D] = vk;
+                *reinterpret_cast<float4 *>(pr) = make_float4(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<float4 *>(pr + 4) = make_float4(v[4], v[5], v[6], v[7]);
             } else {
-                const size_t o = qk_out + (size_t)r * a.Hk * D + j;
-                store_from_f32(a.dq, o, vq, a.grad_dt);
-                store_from_f32(a.dk, o, vk, a.grad_dt);
+                void *dst = c8 < D ? a.dq : a.dk;
+                const size_t o = qk_out + (size_t)r * a.Hk * D + (c8 & (D - 1));
+                if (a.grad_dt == DT_BF16) {
+                    *reinterpret_cast<uint4 *>(static_cast<bfr *>(dst) + o) =
+                        make_uint4(pk(v[0], v[1]), pk(v[2], v[3]), pk(v[4], v[5]), pk(v[6], v[7]));
+                } else if (a.grad_dt == DT_F32) {
+                    float *dp4 = static_cast<float *>(dst) + o;
+                    *reinterpret_cast<float4 *>(dp4) = make_float4(v[0], v[1], v[2], v[3]);
+                    *reinterpret_cast<float4 *>(dp4 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) store_from_f32(dst, o + q, v[q], a.grad_dt);
+                }
             }
         }
     }
