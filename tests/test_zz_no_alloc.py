@@ -22,14 +22,18 @@ def dev():
     return torch.device("cuda:0")
 
 
-def _inputs(B, T, Hk, Hv, D, dtype, dev, seed):
+def _inputs(B, T, Hk, Hv, D, dtype, dev, seed, vector=False):
+    """q, k L2-normalised (q times D^-1/2), v and S0 normal; the gate a log decay -U(0, 1) per value head, or with
+    vector=True a decay exp(-U(0, 1.5)) per key channel [B, T, Hv, D]."""
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     n = lambda *s: torch.randn(*s, device=dev, generator=g)
     q = torch.nn.functional.normalize(n(B, T, Hk, D), dim=-1) * D ** -0.5
     k = torch.nn.functional.normalize(n(B, T, Hk, D), dim=-1)
-    return dict(q=q.to(dtype), k=k.to(dtype), v=n(B, T, Hv, D).to(dtype), g=-torch.rand(B, T, Hv, device=dev,
-                generator=g), beta=torch.rand(B, T, Hv, device=dev, generator=g),
+    v = n(B, T, Hv, D).to(dtype)
+    gate = (torch.exp(-1.5 * torch.rand(B, T, Hv, D, device=dev, generator=g)) if vector
+            else -torch.rand(B, T, Hv, device=dev, generator=g))
+    return dict(q=q.to(dtype), k=k.to(dtype), v=v, g=gate, beta=torch.rand(B, T, Hv, device=dev, generator=g),
                 S0=n(B, Hv, D, D) * 0.02)
 
 
@@ -39,20 +43,21 @@ def _run(x, dev, noalloc, mask=None, form=None):
     B, T, Hk, D = x["q"].shape
     Hv = x["v"].shape[2]
     code = L.DTYPE_CODE[x["q"].dtype]
+    gate = L.GATE_DECAY_VEC if x["g"].dim() == 4 else L.GATE_LOG
     y = torch.full((B, T, Hv, D), float("nan"), device=dev, dtype=x["q"].dtype)
     S = torch.full((B, Hv, D, D), float("nan"), device=dev)
     ptrs = [x[n].data_ptr() for n in ("q", "k", "v", "g", "beta", "S0")]
     m = None if mask is None else mask.data_ptr()
     form = L.FORM_AUTO if form is None else form
     if noalloc:
-        rc = lib.gdn_fwd_noalloc(*ptrs, m, y.data_ptr(), S.data_ptr(), B, T, Hk, Hv, D, D, code, code, L.GATE_LOG,
+        rc = lib.gdn_fwd_noalloc(*ptrs, m, y.data_ptr(), S.data_ptr(), B, T, Hk, Hv, D, D, code, code, gate,
                                  form, None)
     else:
-        n_ws = lib.gdn_fwd_workspace_bytes(B, T, Hk, Hv, D, D, 64, L.GATE_LOG, int(mask is not None), form,
+        n_ws = lib.gdn_fwd_workspace_bytes(B, T, Hk, Hv, D, D, 64, gate, int(mask is not None), form,
                                            code, 0)
         ws = torch.empty(max(n_ws, 1), device=dev, dtype=torch.uint8)
         rc = lib.gdn_fwd(*ptrs, m, y.data_ptr(), S.data_ptr(), None, 0, ws.data_ptr(), n_ws, B, T, Hk, Hv, D, D, 64,
-                         code, code, L.GATE_LOG, form, None)
+                         code, code, gate, form, None)
     L.check(rc)
     torch.cuda.synchronize()
     return y, S
@@ -64,6 +69,21 @@ def test_noalloc_forward_matches_gdn_fwd_twice(dev, dtype):
     for B, T, seed in ((4, 1000, 1), (2, 300, 2)):
         print(f"gdn_fwd_noalloc {dtype} B={B} T={T} Hk=16 Hv=32 D=128", flush=True)
         x = _inputs(B, T, 16, 32, 128, dtype, dev, seed)
+        y0, S0 = _run(x, dev, noalloc=False)
+        y1, S1 = _run(x, dev, noalloc=True)
+        assert torch.isfinite(y1.float()).all() and torch.isfinite(S1).all()
+        assert torch.equal(y0, y1) and torch.equal(S0, S1)
+
+
+def test_noalloc_vector_gates_on_the_chunked_form_twice(dev):
+    """Per-channel gates with bf16 inputs run the chunked form's vector-gate kernels, whose per-chunk decay tiles
+    take their share of the fixed scratch: equal to gdn_fwd bit for bit on two calls, the second smaller."""
+    import gdn_lib as L
+    lib = L.load()
+    assert lib.gdn_select_form(32, 128, 128, 0, L.GATE_DECAY_VEC, L.FORM_AUTO, L.BF16) == L.FORM_CHUNK
+    for B, T, seed in ((4, 700, 4), (1, 130, 5)):
+        print(f"gdn_fwd_noalloc bf16 vector gates B={B} T={T} Hk=16 Hv=32 D=128", flush=True)
+        x = _inputs(B, T, 16, 32, 128, torch.bfloat16, dev, seed, vector=True)
         y0, S0 = _run(x, dev, noalloc=False)
         y1, S1 = _run(x, dev, noalloc=True)
         assert torch.isfinite(y1.float()).all() and torch.isfinite(S1).all()
