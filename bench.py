@@ -16,9 +16,10 @@ Workloads (one GPU; the default is the T=4096 configuration the metric is quoted
                   bf16_b4_t4096 with a mask (each sequence's last 10% masked, padding): two chunked
                   passes plus the masked tokens' fix-up
   vgate_bf16_b4_t4096
-                  bf16_b4_t4096 with one decay per key channel (g [B, T, Hv, D], in decay space); the chunked
-                  form with the per-channel-gate prep and local kernels (GDN_FORM=recurrent: the token-recurrent
-                  form)
+                  bf16_b4_t4096 with one log decay per key channel (g [B, T, Hv, D], the headline's gate
+                  distribution per channel, taken as log decays as the headline takes its per-head gates); the
+                  chunked form with the per-channel-gate prep and local kernels (GDN_FORM=recurrent: the
+                  token-recurrent form)
   fwd_bf16_b4_t4096
                   the forward alone, as frozen layers and prefill run it (no autograd graph, no saved tiles),
                   bf16_b4_t4096's shape
@@ -216,9 +217,10 @@ def make_inputs(w, dev, seed=0):
     beta = torch.sigmoid(n(B, T, Hv))
     A_log = torch.empty(Hv, device=dev).uniform_(0.0, float(torch.log(torch.tensor(16.0))), generator=gen)
     if w.get("vector_gate"):
-        # one decay per key channel, [B, T, Hv, D]: the multiplicative decay itself (a per-channel gate is taken
-        # in decay space, tools/gdn_vjp.py:174-179), exp of the same log-decay distribution
-        g = torch.exp(-torch.exp(A_log)[:, None] * torch.nn.functional.softplus(n(B, T, Hv, D)))
+        # one log decay per key channel, [B, T, Hv, D], from the same distribution.  Many of its decays are far
+        # below 1e-4, where a decay-space gate (the reference's convention for per-channel gates,
+        # tools/gdn_vjp.py:174-179) takes the token-recurrent form for an accurate d/d(decay)
+        g = -torch.exp(A_log)[:, None] * torch.nn.functional.softplus(n(B, T, Hv, D))
     else:
         g = -torch.exp(A_log) * torch.nn.functional.softplus(n(B, T, Hv))  # log decay per head
     state = n(B, Hv, D, D) * w["s0_std"] if w["s0_std"] > 0 else torch.zeros(B, Hv, D, D, device=dev)
@@ -433,8 +435,7 @@ def main():
 
         def step():
             y, S = gdn_engine.recurrence(x["q"], x["k"], x["v"], x["g"], x["beta"], x["state"], mask,
-                                         chunk=w["chunk"], log_gate=not w.get("vector_gate"),
-                                         output_dtype=out_dtype)
+                                         chunk=w["chunk"], log_gate=True, output_dtype=out_dtype)
             return torch.autograd.grad([y], leaves, [x["dy"]])
 
     for i in range(args.warmup):

@@ -9,7 +9,7 @@
  * Layouts (all row-major, contiguous):
  *   q, k    [B][T][Hk][Dk]          dtype in_dtype (GDN_F32 / GDN_BF16 / GDN_F16)
  *   v       [B][T][Hv][Dv]          dtype in_dtype
- *   g       [B][T][Hv]   (GDN_GATE_DECAY, GDN_GATE_LOG)   or [B][T][Hv][Dk] (GDN_GATE_DECAY_VEC), fp32
+ *   g       [B][T][Hv]   (GDN_GATE_DECAY, GDN_GATE_LOG)   or [B][T][Hv][Dk] (GDN_GATE_DECAY_VEC, _LOG_VEC), fp32
  *   beta    [B][T][Hv]              fp32
  *   state   [B][Hv][Dv][Dk]         fp32 (initial state S0; NULL means zeros)
  *   mask    [B][T]                  uint8, nonzero keeps the candidate state; NULL means all ones
@@ -44,7 +44,11 @@ enum gdn_dtype { GDN_F32 = 0, GDN_BF16 = 1, GDN_F16 = 2 };
 enum gdn_gate {
     GDN_GATE_DECAY = 0,      /* g is the multiplicative decay, [B][T][Hv] (reference convention) */
     GDN_GATE_DECAY_VEC = 1,  /* g is a decay per key channel, [B][T][Hv][Dk] (tools/gdn_vjp.py:174-179) */
-    GDN_GATE_LOG = 2         /* g is the log decay, [B][T][Hv]; dg is returned w.r.t. the log decay */
+    GDN_GATE_LOG = 2,        /* g is the log decay, [B][T][Hv]; dg is returned w.r.t. the log decay */
+    GDN_GATE_LOG_VEC = 3     /* g is a log decay per key channel, [B][T][Hv][Dk]; dg w.r.t. the log decay.  No
+                              * counterpart in the reference (which takes per-channel gates as decays): the
+                              * chunked form forms dg for the log decay from suffix sums, so its d/d(decay) =
+                              * dg / decay loses accuracy below decays of about 1e-5, and its log gradient does not */
 };
 
 enum gdn_form {
@@ -75,8 +79,11 @@ int64_t gdn_num_snapshots(int T, int chunk);
 
 /* The form a call with these arguments runs in (GDN_FORM_RECURRENT or GDN_FORM_CHUNK), or < 0 when the
  * requested form cannot run them.  gdn_fwd, gdn_bwd and the size queries resolve the form the same way: GDN_FORM_AUTO
- * picks the chunked form for Dk = Dv = 128 with a scalar gate (with a mask: Hv <= 256) or with one decay per key
- * channel (GDN_GATE_DECAY_VEC: bf16 inputs, no mask); the recurrent form otherwise. */
+ * picks the chunked form for Dk = Dv = 128 with a scalar gate (with a mask: Hv <= 256) or with one gate per key
+ * channel (GDN_GATE_DECAY_VEC or GDN_GATE_LOG_VEC: bf16 inputs, no mask); the recurrent form otherwise.  For
+ * training calls with GDN_GATE_DECAY_VEC the chunked form's dg holds to the bf16 bar for decays down to about 1e-4
+ * (suffix sums of the log gradient divided by the decay): callers with smaller decays pin GDN_FORM_RECURRENT or
+ * pass the log decays (GDN_GATE_LOG_VEC). */
 int gdn_select_form(int Hv, int Dk, int Dv, int has_mask, int gate_kind, int form, int in_dtype);
 
 /* What `chunk` means.
@@ -133,7 +140,7 @@ int gdn_fwd_noalloc(const void *q, const void *k, const void *v, const float *g,
 /* One decode step: the recurrence over a single token of B sequences, replacing gdn_recurrent_step
  * (engine/include/gdn.h:27-38, engine/src/gdn.c:63-108) batched over sequences.
  *   q, k [B][Hk][Dk], v [B][Hv][Dv] (in_dtype); g, beta [B][Hv] (g as gate_kind: GDN_GATE_DECAY, GDN_GATE_LOG,
- *   or [B][Hv][Dk] for GDN_GATE_DECAY_VEC) fp32; y [B][Hv][Dv] (out_dtype);
+ *   or [B][Hv][Dk] for GDN_GATE_DECAY_VEC, GDN_GATE_LOG_VEC) fp32; y [B][Hv][Dv] (out_dtype);
  *   state_in, state_out [B][Hv][Dv][Dk] fp32: state_out may be state_in (updated in place, as gdn_recurrent_step
  *   does); state_in NULL means zeros.
  * Forward only; any Dk <= 256 and Dv. */
@@ -151,7 +158,7 @@ size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int
  * the states inside each chunk, and writes
  *   dq, dk [B][T][Hk][Dk] (grad_dtype; summed over the value heads of each key head, tools/gdn_vjp.py:266-270)
  *   dv     [B][T][Hv][Dv] (grad_dtype)
- *   dg     shaped like g, fp32 (w.r.t. the log decay for GDN_GATE_LOG)
+ *   dg     shaped like g, fp32 (w.r.t. the log decay for GDN_GATE_LOG and GDN_GATE_LOG_VEC)
  *   dbeta  [B][T][Hv] fp32
  *   dstate0 [B][Hv][Dv][Dk] fp32 (may be NULL)
  * dy has dy_dtype; dstate_T may be NULL (zero cotangent).  Results are deterministic (no atomics).

@@ -95,7 +95,7 @@ static int check_shape(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, 
     if (Hk <= 0 || Hv <= 0 || Dk <= 0 || Dv <= 0)
         return fail(GDN_ERR_INVALID, "head counts and head dims must be positive");
     if (Hv % Hk != 0) return fail(GDN_ERR_INVALID, "q/k head count must divide the value head count");
-    if (gate != GATE_DECAY && gate != GATE_DECAY_VEC && gate != GATE_LOG)
+    if (gate != GATE_DECAY && gate != GATE_DECAY_VEC && gate != GATE_LOG && gate != GATE_LOG_VEC)
         return fail(GDN_ERR_INVALID, "Unsupported gating kind %d", gate);
     if (form != GDN_FORM_AUTO && form != GDN_FORM_RECURRENT && form != GDN_FORM_CHUNK)
         return fail(GDN_ERR_INVALID, "unknown form %d", form);
@@ -109,7 +109,7 @@ static int check_shape(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, 
 // (gdn_chunk_vg.hip).
 static bool chunk_eligible(int Hv, int Dk, int Dv, int has_mask, int gate, int in_dt) {
     if (Dk != 128 || Dv != 128) return false;
-    if (gate == GATE_DECAY_VEC) return !has_mask && chunk_vg_supported(in_dt);
+    if (gate_vec(gate)) return !has_mask && chunk_vg_supported(in_dt);
     return !has_mask || Hv <= mask_max_heads();
 }
 
@@ -120,7 +120,7 @@ static int resolve_form(int Hv, int Dk, int Dv, int has_mask, int gate, int form
     if (form == GDN_FORM_CHUNK) {
         if (ok) return GDN_FORM_CHUNK;
         if (Dk != 128 || Dv != 128) return fail(GDN_ERR_UNSUPPORTED, "the chunked form needs Dk = Dv = 128");
-        if (gate == GATE_DECAY_VEC)
+        if (gate_vec(gate))
             return fail(GDN_ERR_UNSUPPORTED, "the chunked form takes per-channel gates with bf16 inputs and no mask");
         return fail(GDN_ERR_UNSUPPORTED, "masked calls of the chunked form take Hv <= %d", mask_max_heads());
     }
@@ -147,7 +147,7 @@ static BwdLayout bwd_layout(int B, int T, int Hv, int Dk, int Dv, int chunk, int
     L.part_gb = off;
     off += align256(nrb * toks * 2 * sizeof(float));
     L.part_gv = off;
-    if (gate == GATE_DECAY_VEC) off += align256(nrb * toks * Dk * sizeof(float));
+    if (gate_vec(gate)) off += align256(nrb * toks * Dk * sizeof(float));
     L.total = off;
     return L;
 }
@@ -273,7 +273,7 @@ static size_t mask_fwd_only_head(const CkShape &s) {
 static size_t dt_size(int dt) { return dt == DT_F32 ? 4 : 2; }
 
 // Gate values per (token, value head): one, or one per key channel.
-static size_t gate_width(int gate) { return gate == GATE_DECAY_VEC ? kChunkD : 1; }
+static size_t gate_width(int gate) { return gate_vec(gate) ? kChunkD : 1; }
 
 template <class P>
 static P *tok_offset(P *p, size_t elems, int dt) {
@@ -336,6 +336,10 @@ int64_t gdn_num_snapshots(int T, int chunk) {
 
 int gdn_select_form(int Hv, int Dk, int Dv, int has_mask, int gate_kind, int form, int in_dtype) {
     g_err[0] = 0;
+    if (gate_kind != GATE_DECAY && gate_kind != GATE_DECAY_VEC && gate_kind != GATE_LOG && gate_kind != GATE_LOG_VEC)
+        return fail(GDN_ERR_INVALID, "Unsupported gating kind %d", gate_kind);
+    if (form != GDN_FORM_AUTO && form != GDN_FORM_RECURRENT && form != GDN_FORM_CHUNK)
+        return fail(GDN_ERR_INVALID, "unknown form %d", form);
     return resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form, in_dtype);
 }
 
@@ -348,7 +352,7 @@ size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, 
         const int W = ck_window(chunk);
         if (has_mask) return mask_saved({B, T, Hk, Hv, in_dtype == DT_BF16, false}, chunk).total;
         if (W) return ck_snap_bytes(B, T, Hv, W);
-        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true, gate_kind == GATE_DECAY_VEC).saved;
+        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true, gate_vec(gate_kind)).saved;
     }
     return rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
 }
@@ -359,7 +363,7 @@ size_t gdn_fwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int
     const int f = resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form, in_dtype);
     if (f != GDN_FORM_CHUNK || B == 0 || T == 0) return 0;
     const int W = ck_window(chunk);
-    const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16, gate_kind == GATE_DECAY_VEC};
+    const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16, gate_vec(gate_kind)};
     if (has_mask) {
         // pass 2 runs forward-only when checkpointing; a forward-only call also holds g', beta' and z
         if (with_saved) return W ? std::max(ck_fwd_target_bytes(shp, W, true), ck_fwd_target_bytes(shp, W, false)) : 0;
@@ -377,7 +381,7 @@ namespace gdn {
 static int ck_forward(const ChunkCall &base, int chunk, void *saved, size_t saved_bytes, void *ws, size_t ws_bytes,
                       hipStream_t st) {
     const int B = base.B, T = base.T, Hk = base.Hk, Hv = base.Hv;
-    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16, base.gate == GATE_DECAY_VEC};
+    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16, gate_vec(base.gate)};
     const int W = ck_window(chunk);
     int rc;
     if (saved && !W) {  // the whole tile set, kept for the backward
@@ -462,7 +466,7 @@ static int ck_forward(const ChunkCall &base, int chunk, void *saved, size_t save
 static int ck_backward(const ChunkCall &base, int chunk, const void *saved, size_t saved_bytes, void *ws,
                        size_t ws_bytes, hipStream_t st) {
     const int B = base.B, T = base.T, Hk = base.Hk, Hv = base.Hv;
-    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16, base.gate == GATE_DECAY_VEC};
+    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16, gate_vec(base.gate)};
     const int W = ck_window(chunk);
     int rc;
     if (!W) {
@@ -559,7 +563,7 @@ static char *at_off(void *base, size_t off) { return static_cast<char *>(base) +
 // beta, state0, y, state_T and shapes.
 static int ck_masked_forward(const ChunkCall &base, const uint8_t *mask, int chunk, void *saved, size_t saved_bytes,
                              void *ws, size_t ws_bytes, hipStream_t st) {
-    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16, base.gate == GATE_DECAY_VEC};
+    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16, gate_vec(base.gate)};
     const int W = ck_window(chunk);
     const size_t tokens = (size_t)base.B * base.T;
     float *g2, *b2, *Z, *Yp = nullptr;
@@ -630,7 +634,7 @@ static int ck_masked_forward(const ChunkCall &base, const uint8_t *mask, int chu
 // Masked chunked backward (resolved form GDN_FORM_CHUNK, arguments checked).
 static int ck_masked_backward(const ChunkCall &base, const uint8_t *mask, int chunk, const void *saved,
                               size_t saved_bytes, void *ws, size_t ws_bytes, hipStream_t st) {
-    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16, base.gate == GATE_DECAY_VEC};
+    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16, gate_vec(base.gate)};
     const int W = ck_window(chunk);
     const size_t tokens = (size_t)base.B * base.T;
     const MaskSaved m = mask_saved(shp, chunk);
@@ -746,7 +750,7 @@ int gdn_fwd_noalloc(const void *q, const void *k, const void *v, const float *g,
     void *ws = nullptr;
     size_t ws_bytes = 0;
     if (f == GDN_FORM_CHUNK && B > 0 && T > 0) {
-        const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16, gate_kind == GATE_DECAY_VEC};
+        const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16, gate_vec(gate_kind)};
         const size_t one = ck_fwd_group_bytes(shp, std::min(kChunkC, T), false);
         if (one > kNoAllocScratchBytes)
             return fail(GDN_ERR_UNSUPPORTED,
@@ -837,8 +841,8 @@ size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int
         if (B == 0 || T == 0) return 0;
         const int W = ck_window(chunk);
         if (has_mask) return mask_work({B, T, Hk, Hv, in_dtype == DT_BF16, false}, chunk).total;
-        if (W) return ck_bwd_target_bytes({B, T, Hk, Hv, in_dtype == DT_BF16, gate_kind == GATE_DECAY_VEC}, W);
-        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true, gate_kind == GATE_DECAY_VEC).work;
+        if (W) return ck_bwd_target_bytes({B, T, Hk, Hv, in_dtype == DT_BF16, gate_vec(gate_kind)}, W);
+        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true, gate_vec(gate_kind)).work;
     }
     return bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind).total;
 }

@@ -453,10 +453,7 @@ __device__ __forceinline__ void chunk_dg_dbeta(float *sE, const float (*sRow)[2]
         if (k == 0 && u < n) {
             const size_t gi = g0 + (size_t)u * a.Hv;
             float dgv = acc + sScan[0][u] + sScan[1][u];
-            if (a.gate == GATE_DECAY) {
-                const float dec = a.g[gi];
-                dgv = dec > 1e-30f ? dgv / dec : 0.f;
-            }
+            if (a.gate == GATE_DECAY) dgv = dg_per_decay(dgv, a.g[gi]);
             a.dg[gi] = dgv;
         }
     }
@@ -1964,7 +1961,7 @@ static ck::Args make_args(const ChunkCall &cc) {
     a.state_T = cc.state_T;
     a.dg = cc.dg; a.dbeta = cc.dbeta; a.dstate0 = cc.dstate0;
     const bool bf16 = cc.in_dt == DT_BF16;
-    const ChunkSizes s = chunk_sizes(cc.B, cc.T, cc.Hk, cc.Hv, bf16, !cc.fwd_only, cc.gate == GATE_DECAY_VEC);
+    const ChunkSizes s = chunk_sizes(cc.B, cc.T, cc.Hk, cc.Hv, bf16, !cc.fwd_only, gate_vec(cc.gate));
     char *sv = static_cast<char *>(cc.tiles);
     auto at = [&](const ChunkSizes::Buf &bf) -> void * { return bf.size ? sv + bf.off : nullptr; };
     a.w.H = static_cast<float *>(at(s.H));
@@ -2076,7 +2073,7 @@ static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) 
         hipLaunchKernelGGL(ck::ck_bwd_local_kernel<false>, dim3(a.NC, a.Hk, a.B), dim3(ck::NTB), 0, st, a);
 }
 
-static int kernel_set(int in_dt, int gate) { return in_dt == DT_BF16 ? (gate == GATE_DECAY_VEC ? 2 : 1) : 0; }
+static int kernel_set(int in_dt, int gate) { return in_dt == DT_BF16 ? (gate_vec(gate) ? 2 : 1) : 0; }
 
 bool chunk_vg_supported(int in_dt) { return in_dt == DT_BF16; }
 

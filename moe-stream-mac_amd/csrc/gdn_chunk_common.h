@@ -212,11 +212,24 @@ __device__ __forceinline__ void store_state_slice(float *dst, const float *sH, i
 
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
 
+// The smallest decay the chunked form takes in the decay conventions: a smaller one, zero included, runs as 2^-64.
+// The state then keeps 2^-64 of itself where a zero decay keeps none (far below the fp32 rounding of the other terms),
+// and every pair term that straddles such a token carries that factor, so dg = dg_log / 2^-64 is the derivative
+// with respect to the decay there instead of 0 / 0.
+constexpr float kMinDecay = 5.42101086242752217e-20f;  // 2^-64
+constexpr float kLogMinDecay = -44.3614195558365f;     // ln 2^-64
+
+// The per-token log decay the chunked form accumulates.  A log decay of -inf (a zero decay) is taken as -1e4, whose
+// exponential is exactly 0, so that differences of cumulative sums stay finite; NaN passes through.  No branch: a
+// conditional logf made the compiler wait for every load in flight before each one.
 __device__ __forceinline__ float gate_log(float g, int gate) {
-    if (gate == GATE_LOG) return g;
-    // decay -> log decay; exp(-1e4) is exactly 0, and fp64 prefix sums stay exact at that magnitude
-    return g > 0.f ? fmaxf(logf(g), -1e4f) : -1e4f;
+    if (gate_in_log(gate)) return g < -1e4f ? -1e4f : g;
+    const float l = logf(fmaxf(g, kMinDecay));  // logf(2^-64) = kLogMinDecay
+    return g == g ? l : g;
 }
+
+// d/d(decay) from d/d(log decay) at the decay the chunked form ran with
+__device__ __forceinline__ float dg_per_decay(float dg_log, float d) { return dg_log / fmaxf(d, kMinDecay); }
 
 struct Bufs {
     float *H;    // [B][Hv][NC][D][D] chunk-entry states h = S^T, element (j, i) at [j][i] (bf16 bits in the bf16 path)

@@ -1,5 +1,5 @@
 // Per-channel (vector) gates on the chunked form, bf16 inputs: one decay d_tj per key channel j (GATE_DECAY_VEC,
-// tools/gdn_vjp.py:174-179 with a [B,T,Hv,Dk] gate).  Per 64-token chunk of one value head, with G_rj the cumulative
+// tools/gdn_vjp.py:174-179 with a [B,T,Hv,Dk] gate; or its log, GATE_LOG_VEC, with dg returned for the log).  Per 64-token chunk of one value head, with G_rj the cumulative
 // log decay of channel j up to token r (G_C its last row) and E_rsj = exp(G_rj - G_sj):
 //   A_rs = beta_r sum_j k_rj k_sj E_rsj (s < r),   P_rs = sum_j q_rj k_sj E_rsj (s <= r),   T = (I + A)^-1
 //   W = T diag(beta) (K * exp(G)),   U = T diag(beta) V,   Delta = U - W h
@@ -80,6 +80,8 @@ static_assert(2 * C * C * 2 <= C * LDC * 4, "P hi / lo staging fits the T region
 static_assert(VP_END + 3 * 256 * 4 + 4 * D * 8 + C * 4 <= 160 * 1024, "LDS");
 static_assert(C * VLG * 4 <= 2 * D * VLT * 2, "the linear decays fit the (K exp(G))^T region");
 
+// LOGG: the gates are log decays (GATE_LOG_VEC) rather than decays (GATE_DECAY_VEC)
+template <bool LOGG>
 __global__ __launch_bounds__(NTP) void ck_prep_vg_kernel(Args a) {
     __shared__ __align__(16) unsigned char pa[VP_END];
     __shared__ float scratch[3 * 256];
@@ -132,8 +134,12 @@ __global__ __launch_bounds__(NTP) void ck_prep_vg_kernel(Args a) {
     for (int rr = 0; rr < SB; ++rr) {
         const int r = SB * gs + rr;
         const float x = a.g[(((size_t)b * a.Ts + t0 + min(r, n - 1)) * a.Hv + hv) * D + gj];
-        gl[rr] = r < n ? gate_log(x, GATE_DECAY_VEC) : 0.f;
-        dl[rr] = r < n ? fmaxf(x, 0.f) : 1.f;
+        // rows past the sequence by a 0 / 1 factor rather than a select: the compiler turned the select into a branch
+        // around the gate's load, and waited there for every load in flight
+        const float in = r < n ? 1.f : 0.f;
+        const float l = gate_log(x, LOGG ? GATE_LOG_VEC : GATE_DECAY_VEC);
+        gl[rr] = in * l;
+        dl[rr] = in * (LOGG ? ex2(l * 1.4426950408889634f) : fmaxf(x, kMinDecay)) + (1.f - in);
     }
     const float b_ld = a.beta[((size_t)b * a.Ts + t0 + min(tid, n - 1)) * a.Hv + hv];
 #pragma unroll
@@ -436,7 +442,8 @@ __global__ __launch_bounds__(NTP) void ck_prep_vg_kernel(Args a) {
 }
 
 void launch_vg_prep(const Args &a, hipStream_t st) {
-    hipLaunchKernelGGL(ck_prep_vg_kernel, dim3(a.NC, a.Hv, a.B), dim3(NTP), 0, st, a);
+    if (gate_in_log(a.gate)) hipLaunchKernelGGL(ck_prep_vg_kernel<true>, dim3(a.NC, a.Hv, a.B), dim3(NTP), 0, st, a);
+    else hipLaunchKernelGGL(ck_prep_vg_kernel<false>, dim3(a.NC, a.Hv, a.B), dim3(NTP), 0, st, a);
 }
 
 // ---------------------------------------------------------------------------------------------- ck_bwd_local_vg
@@ -968,11 +975,13 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
         if (r < n) a.dbeta[((size_t)b * a.Ts + t0 + r) * a.Hv + hv] = sVT[r] + sRow[0][r] + sRow[1][r];
     }
     __syncthreads();
-    // d/d(decay) = dg_log / d, coalesced over the channels
+    // d/d(decay) = dg_log / d (or dg_log itself for log gates), coalesced over the channels
+    const bool in_log = a.gate == GATE_LOG_VEC;
 #pragma unroll
     for (int p = 0; p < GPER; ++p) {
         const int i = tid + p * NTB, r = i / D, j = i - r * D;
-        if (r < n) a.dg[(((size_t)b * a.Ts + t0 + r) * a.Hv + hv) * D + j] = sDG[r * VLGp + j] / dec[p];
+        const float x = sDG[r * VLGp + j];
+        if (r < n) a.dg[(((size_t)b * a.Ts + t0 + r) * a.Hv + hv) * D + j] = in_log ? x : dg_per_decay(x, dec[p]);
     }
     // ---- dq | dk: this value head's parts summed over the key head's value heads.  They leave through an fp32
     // staging tile [64][dq 128 | dk 128] over the permuted K, Q, G tiles (dead since the diagonal loops), so that

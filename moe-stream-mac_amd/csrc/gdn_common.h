@@ -8,7 +8,10 @@
 namespace gdn {
 
 enum : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
-enum : int { GATE_DECAY = 0, GATE_DECAY_VEC = 1, GATE_LOG = 2 };
+enum : int { GATE_DECAY = 0, GATE_DECAY_VEC = 1, GATE_LOG = 2, GATE_LOG_VEC = 3 };
+// one gate value per key channel ([B][T][Hv][Dk]) rather than per head; the gate given as the log decay
+__host__ __device__ constexpr bool gate_vec(int gate) { return gate == GATE_DECAY_VEC || gate == GATE_LOG_VEC; }
+__host__ __device__ constexpr bool gate_in_log(int gate) { return gate == GATE_LOG || gate == GATE_LOG_VEC; }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 

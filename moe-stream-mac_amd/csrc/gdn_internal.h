@@ -51,7 +51,7 @@ struct ChunkSizes {
     Buf dH, dDl, part;                // backward workspace
     size_t work;                      // its size
 };
-// vg: one decay per key channel (GATE_DECAY_VEC), bf16 set only.
+// vg: one decay per key channel (GATE_DECAY_VEC or GATE_LOG_VEC), bf16 set only.
 ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd, bool vg = false);
 
 // One launch of a chunked stage.  q, k, v, g, beta, y, dy, dq, dk, dv, dg and dbeta point at the launch's first
@@ -72,7 +72,7 @@ struct ChunkCall {
 // stage: "prep" | "fwd" (forward) or "seq" | "local" (backward; "local" walks the value heads of each key head
 // and writes dq and dk).  With recompute, "fwd" runs every window of the launch at once.
 void launch_chunk_stage(const ChunkCall &cc, const char *stage, hipStream_t st);
-// The chunked form takes per-channel gates (GATE_DECAY_VEC) for bf16 inputs (gdn_chunk_vg.hip).
+// The chunked form takes per-channel gates (GATE_DECAY_VEC, GATE_LOG_VEC) for bf16 inputs (gdn_chunk_vg.hip).
 bool chunk_vg_supported(int in_dt);
 
 // Masked steps on the chunked form (gdn_mask.hip): tensors of B*T tokens, contiguous; q, k [tok][Hk][Dk], v, y, dy

@@ -96,7 +96,7 @@ __device__ __forceinline__ void stage_store(StageBuf<E, VEC, TT, R> &sb,
             const bool ok = tt < n && j < Dk;
             sb.k[tt][j] = ok ? r.k[p] : 0.f;
             sb.q[tt][j] = ok ? r.q[p] : 0.f;
-            if constexpr (VEC) sb.g[tt][j] = ok ? r.g[p] : 1.f;
+            if constexpr (VEC) sb.g[tt][j] = ok ? (gate == GATE_LOG_VEC ? expf(r.g[p]) : r.g[p]) : 1.f;
         }
     }
 #pragma unroll
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(THREADS) void rec_decode_kernel(RecFwdArgs a) {
         qq[e] = ok ? qq[e] : 0.f;
         if constexpr (VEC) {
             const float gx = a.g[head * Dk + jc];
-            dec[e] = ok ? gx : 1.f;
+            dec[e] = ok ? (a.gate == GATE_LOG_VEC ? expf(gx) : gx) : 1.f;
         } else {
             dec[e] = dsc;
         }
@@ -625,13 +625,13 @@ __global__ __launch_bounds__(256) void rec_bwd_reduce_qk(RecBwdArgs a) {
 
 __global__ __launch_bounds__(256) void rec_bwd_reduce_gates(RecBwdArgs a) {
     const size_t BT = (size_t)a.B * a.T;
-    const size_t total = BT * a.Hv * (a.gate == GATE_DECAY_VEC ? a.Dk : 1);
+    const size_t total = BT * a.Hv * (gate_vec(a.gate) ? a.Dk : 1);
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= total) return;
-    if (a.gate == GATE_DECAY_VEC) {
+    if (gate_vec(a.gate)) {
         float s = 0.f;
         for (int rb = 0; rb < a.nrb; ++rb) s += a.part_gv[(size_t)rb * BT * a.Hv * a.Dk + i];
-        a.dg[i] = s;
+        a.dg[i] = a.gate == GATE_LOG_VEC ? s * expf(a.g[i]) : s;
         if (i % a.Dk == 0) {
             const size_t tok = i / a.Dk;
             float db = 0.f;
@@ -688,6 +688,10 @@ __global__ __launch_bounds__(256) void rec_bwd_reduce_gates_vec4(RecBwdArgs a) {
         const float4 p = src[(size_t)rb * plane4];
         s = make_float4(s.x + p.x, s.y + p.y, s.z + p.z, s.w + p.w);
     }
+    if (a.gate == GATE_LOG_VEC) {  // d/d(log decay) = d/d(decay) * decay
+        const float4 g = reinterpret_cast<const float4 *>(a.g)[th * Dk4 + j4];
+        s = make_float4(s.x * expf(g.x), s.y * expf(g.y), s.z * expf(g.z), s.w * expf(g.w));
+    }
     reinterpret_cast<float4 *>(a.dg)[th * Dk4 + j4] = s;
     if (j4 == 0) {
         float db = 0.f;
@@ -716,7 +720,7 @@ int rec_num_row_blocks(int Dv) { return (Dv + ROWS - 1) / ROWS; }
 // is taken for per-channel gates only, when the grid keeps at least 512 workgroups (two rounds of one per CU) and
 // up to Dk = 128 (the 8-wave LDS sums of wider rows would not fit); 16 (4 waves) otherwise.
 int rec_bwd_rows(int B, int Hv, int Dk, int Dv, int gate) {
-    if (gate != GATE_DECAY_VEC || pick_lane_width(Dk) > 8 || Dv <= ROWS) return ROWS;
+    if (!gate_vec(gate) || pick_lane_width(Dk) > 8 || Dv <= ROWS) return ROWS;
     return (int64_t)B * Hv * ((Dv + 2 * ROWS - 1) / (2 * ROWS)) >= 512 ? 2 * ROWS : ROWS;
 }
 
@@ -740,7 +744,7 @@ size_t rec_sub_floats(int B, int Hv, int Dk, int Dv, int T, int chunk, int gate)
 template <int E, int DT>
 static void launch_fwd_et(const RecFwdArgs &a, hipStream_t st) {
     dim3 grid(rec_num_row_blocks(a.Dv), a.Hv, a.B);
-    const bool vec = a.gate == GATE_DECAY_VEC, masked = a.mask != nullptr;
+    const bool vec = gate_vec(a.gate), masked = a.mask != nullptr;
     if (vec && masked) hipLaunchKernelGGL((rec_fwd_kernel<E, true, DT, true>), grid, dim3(THREADS), 0, st, a);
     else if (vec) hipLaunchKernelGGL((rec_fwd_kernel<E, true, DT, false>), grid, dim3(THREADS), 0, st, a);
     else if (masked) hipLaunchKernelGGL((rec_fwd_kernel<E, false, DT, true>), grid, dim3(THREADS), 0, st, a);
@@ -758,7 +762,7 @@ static void launch_fwd_e(const RecFwdArgs &a, hipStream_t st) {
 template <int E>
 static void launch_decode_e(const RecFwdArgs &a, hipStream_t st) {
     const dim3 grid(rec_num_row_blocks(a.Dv), a.Hv, a.B);
-    const bool vec = a.gate == GATE_DECAY_VEC;
+    const bool vec = gate_vec(a.gate);
     if (a.in_dt == DT_BF16) {
         if (vec) hipLaunchKernelGGL((rec_decode_kernel<E, true, DT_BF16>), grid, dim3(THREADS), 0, st, a);
         else hipLaunchKernelGGL((rec_decode_kernel<E, false, DT_BF16>), grid, dim3(THREADS), 0, st, a);
@@ -797,7 +801,7 @@ static void launch_bwd_etw(const RecBwdArgs &a, hipStream_t st) {
     // Per-channel gates keep the mask selects even without a mask (every token then keeps its candidate): built
     // without them, that backward measured slower (11.30 against 11.02 ms at B=4, T=4096, Hv=32) although it issues
     // 12% fewer instructions.
-    if (a.gate == GATE_DECAY_VEC)
+    if (gate_vec(a.gate))
         hipLaunchKernelGGL((rec_bwd_kernel<E, true, DT, NW, true>), grid, block, 0, st, a);
     else if (a.mask)
         hipLaunchKernelGGL((rec_bwd_kernel<E, false, DT, NW, true>), grid, block, 0, st, a);
@@ -834,7 +838,7 @@ void launch_rec_bwd(const RecBwdArgs &a, hipStream_t st) {
 
 void launch_rec_bwd_reduce(const RecBwdArgs &a, hipStream_t st) {
     const size_t nqk = (size_t)a.B * a.T * a.Hk * a.Dk;
-    const size_t ng = (size_t)a.B * a.T * a.Hv * (a.gate == GATE_DECAY_VEC ? a.Dk : 1);
+    const size_t ng = (size_t)a.B * a.T * a.Hv * (gate_vec(a.gate) ? a.Dk : 1);
     const bool qk4 = (a.Dk & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.part_qk) | reinterpret_cast<uintptr_t>(a.dq) |
                                           reinterpret_cast<uintptr_t>(a.dk)) & 15) == 0;
     if (nqk && qk4) {
@@ -846,8 +850,9 @@ void launch_rec_bwd_reduce(const RecBwdArgs &a, hipStream_t st) {
         hipLaunchKernelGGL(rec_bwd_reduce_qk, dim3((unsigned)((nqk + 255) / 256)), dim3(256), 0, st, a);
     }
     if (!ng) return;
-    const bool aligned = ((reinterpret_cast<uintptr_t>(a.part_gv) | reinterpret_cast<uintptr_t>(a.dg)) & 15) == 0;
-    const bool vec4 = a.gate == GATE_DECAY_VEC && (a.Dk & 3) == 0 && aligned;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(a.part_gv) | reinterpret_cast<uintptr_t>(a.dg) |
+                           reinterpret_cast<uintptr_t>(a.g)) & 15) == 0;
+    const bool vec4 = gate_vec(a.gate) && (a.Dk & 3) == 0 && aligned;
     if (vec4) {
         const size_t N = (size_t)a.B * a.T * a.Hv;
         const int per = 256 / (a.Dk >> 2);

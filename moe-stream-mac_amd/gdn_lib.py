@@ -19,7 +19,7 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "gdn_mi355x.h"
 
 GDN_OK, GDN_ERR_INVALID, GDN_ERR_UNSUPPORTED, GDN_ERR_WORKSPACE, GDN_ERR_LAUNCH = 0, -1, -2, -3, -4
 F32, BF16, F16 = 0, 1, 2
-GATE_DECAY, GATE_DECAY_VEC, GATE_LOG = 0, 1, 2
+GATE_DECAY, GATE_DECAY_VEC, GATE_LOG, GATE_LOG_VEC = 0, 1, 2, 3
 FORM_AUTO, FORM_RECURRENT, FORM_CHUNK = 0, 1, 2
 FORMS = {"auto": FORM_AUTO, "recurrent": FORM_RECURRENT, "chunk": FORM_CHUNK}
 

@@ -107,10 +107,11 @@ def test_reference_vector_gate_matrix_at_d128(dev, T, masked, dtype):
     _check(_gpu(d, dev, dtype), _oracle(d), bf16 and not masked, bf16, f"T={T} masked={masked} {dtype}")
 
 
-@pytest.mark.parametrize("log_decay", [(0.0, 1.5), (0.0, 6.0)])
+@pytest.mark.parametrize("log_decay", [(0.0, 1.5), (0.0, 6.0), (0.0, 9.0)])
 def test_strong_decays_on_the_chunked_form(dev, log_decay):
-    """Decays down to exp(-6) per token: over a chunk exp(-G) reaches exp(380), beyond fp32, while every factor the
-    chunked form forms stays <= 1."""
+    """Decays down to exp(-9) per token: over a chunk exp(-G) reaches exp(570), beyond fp32, while every factor the
+    chunked form forms stays <= 1.  exp(-9) = 1.2e-4 is just above the smallest decay that the automatic choice
+    leaves on the chunked form for training calls (gdn_engine.VG_CHUNK_MIN_DECAY)."""
     d = _inputs(2, 200, 2, 4, seed=11, log_decay=log_decay)
     print(f"vector gates bf16 T=200 log decays {log_decay}", flush=True)
     _check(_gpu(d, dev, torch.bfloat16), _oracle(d), True, True, f"log decay {log_decay}")
@@ -160,3 +161,31 @@ def test_measured_workload_chunked_against_recurrent(dev):
         e = float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
         print(f"  {name} {e:.1e}", flush=True)
         assert e <= 1e-2, (name, e)
+
+
+@pytest.mark.parametrize("T", [1, 65, 200])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_log_vector_gates_at_any_decay_size(dev, T, dtype):
+    """Per-channel log decays (log_gate=True, [B,T,Hv,Dk]): -U(0, 20) with about 2% of them -inf, so decays from 1
+    down to 2e-9 and exact zeros.  bf16 runs the chunked form, whose gradient for the log decay is its suffix sums
+    with no division by the decay; fp32 the recurrent one.  dg against the oracle's d/d(decay) times the decay."""
+    import gdn_engine
+    bf16 = dtype == torch.bfloat16
+    d = _inputs(2, T, 2, 4, seed=700 + T, bf16=bf16)
+    rng = np.random.default_rng(710 + T)
+    gl = -rng.uniform(0.0, 20.0, (2, T, 4, D))
+    gl[rng.random(gl.shape) < 0.02] = -np.inf
+    d["decay"] = np.exp(gl).astype(np.float32)
+    t = lambda x, dt=torch.float32: torch.tensor(np.asarray(x), device=dev, dtype=dt)
+    q, k, v = (t(d[n], dtype).requires_grad_(True) for n in ("q", "k", "v"))
+    g = t(gl.astype(np.float32)).requires_grad_(True)
+    beta, S0 = (t(d[n]).requires_grad_(True) for n in ("beta", "state"))
+    print(f"log vector gates {dtype} T={T}", flush=True)
+    y, S = gdn_engine.recurrence(q, k, v, g, beta, S0, None, 64, log_gate=True)
+    grads = torch.autograd.grad([y, S], [q, k, v, g, beta, S0], [t(d["dy"], y.dtype), t(d["dS_T"])])
+    torch.cuda.synchronize()
+    got = [x.detach().float().cpu().numpy() for x in (y, S, *grads)]
+    want = _oracle(d)
+    want[5] = want[5] * d["decay"]
+    assert all(np.isfinite(x).all() for x in got)
+    _check(got, want, bf16, bf16, f"log gates T={T} {dtype}")
