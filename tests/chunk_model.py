@@ -278,8 +278,9 @@ def vg_bwd_state_chunk(dh_next, q, k, G, W, P, dY):
     return dDelta, dh
 
 
-def vg_bwd_local_chunk(q, k, v, beta, G, P, Ahat, h, dh_next, Delta, TdD, dY):
-    """dq, dk, dv, dbeta, dg_log [C, Dk] for one chunk of one head, from TdD = T^T dDelta."""
+def vg_bwd_local_chunk(q, k, v, beta, G, P, Ahat, h, dh_next, Delta, TdD, dY, decay_grad=False):
+    """dq, dk, dv, dbeta, dg_log [C, Dk] for one chunk of one head, from TdD = T^T dDelta (with decay_grad,
+    d/d(decay) from vg_dg_decay in place of dg_log)."""
     gC = G[-1]
     eG, eD = np.exp(G), np.exp(gC - G)
     Qg, Kg, Kd = q * eG, k * eG, k * eD
@@ -309,12 +310,72 @@ def vg_bwd_local_chunk(q, k, v, beta, G, P, Ahat, h, dh_next, Delta, TdD, dY):
     dk += dXk + dYk2
     dG += dGa
     dg_log = np.cumsum(dG[::-1], axis=0)[::-1] + dgC
+    if decay_grad:
+        hdot = (dh_next * h).sum(1)
+        return dq, dk, dv, dbeta, vg_dg_decay(q, k, beta, G, dQg, Y2, dKd, hdot, dP, dA)
     return dq, dk, dv, dbeta, dg_log
 
 
-def vg_run(q, k, v, g_log, beta, S0, dY, dS_T, C=64):
+def vg_dg_decay(q, k, beta, G, dQg, Y2, dKd, hdot, dP, dA):
+    """d/d(decay) [C, Dk] of one chunk, formed only from factors <= 1 (no division by the decay).
+
+    Every term of d/d(log decay)_u is a pair term E[r][s'] (s' = -1 the chunk start, r = C the chunk end) whose
+    span straddles u (s' < u <= r) and which carries the factor exp(G_r - G_s'); d/d(decay)_u = that sum / d_u,
+    and exp(G_r - G_s') / d_u = exp(G_r - G_u) exp(G_{u-1} - G_s').  Per 16-token block U (rows a..b2, bt = a - 1):
+      X_u = L_u Srow_u + R_u Scol_u + L_u R_u K_U + D4_u,  L_u = exp(G_{u-1} - G_bt),  R_u = exp(G_b2 - G_u),
+      Srow_u = sum_{r in U, r >= u} exp(G_r - G_u) (exp(G_bt) rho0_r + rho1_r)
+      Scol_u = sum_{s in U, s < u} exp(G_{u-1} - G_s) (exp(G_C - G_b2) sig0_s + sig1_s)
+      K_U = M_U + exp(G_bt) T0 + exp(G_C - G_b2) T0' + exp(G_bt + G_C - G_b2) hdot
+    with rho0 = q dQg - beta k Y2 (pairs (r, -1)), sig0 = k dKd (pairs (C, s)), hdot (pair (C, -1)),
+    rho1_r = sum_{s < a} e'_rs exp(G_bt - G_s), sig1_s = sum_{r > b2} e'_rs exp(G_r - G_b2) (the row and column
+    roles through the block boundaries), T0 = sum_{r > b2} exp(G_r - G_b2) rho0_r, T0' = sum_{s <= bt}
+    exp(G_bt - G_s) sig0_s, M_U = sum_{r > b2, s <= bt} exp(G_r - G_b2) exp(G_bt - G_s) e'_rs, and D4 the pairs
+    inside U; e'_rs = dP_rs q_r k_s + beta_r dA_rs k_r k_s.  G is the cumulative log decay [C, Dk] (G_{-1} = 0)."""
+    C, Dk = G.shape
+    E = lambda x: np.exp(x)
+    gC = G[-1]
+    Gm1 = np.vstack([np.zeros((1, Dk)), G[:-1]])
+    rho0 = q * dQg - beta[:, None] * k * Y2
+    sig0 = k * dKd
+    ep = lambda r, s: dP[r, s] * q[r] * k[s] + beta[r] * dA[r, s] * k[r] * k[s]  # e'_rs, per channel
+    X = np.zeros((C, Dk))
+    for U in range(C // SUB):
+        a, b2 = SUB * U, SUB * U + SUB - 1
+        bt = a - 1
+        Gbt = G[bt] if bt >= 0 else np.zeros(Dk)
+        Gb2 = G[b2]
+        rho1 = np.zeros((SUB, Dk))
+        sig1 = np.zeros((SUB, Dk))
+        for i, r in enumerate(range(a, b2 + 1)):
+            for s_ in range(a):
+                rho1[i] += ep(r, s_) * E(Gbt - G[s_])
+            for r2 in range(b2 + 1, C):
+                sig1[i] += ep(r2, r) * E(G[r2] - Gb2)
+        rho = E(Gbt) * rho0[a:b2 + 1] + rho1
+        sig = E(gC - Gb2) * sig0[a:b2 + 1] + sig1
+        T0 = sum((E(G[r] - Gb2) * rho0[r] for r in range(b2 + 1, C)), np.zeros(Dk))
+        T0p = sum((E(Gbt - G[s_]) * sig0[s_] for s_ in range(a)), np.zeros(Dk))
+        M = np.zeros(Dk)
+        for r in range(b2 + 1, C):
+            for s_ in range(a):
+                M += E(G[r] - Gb2) * E(Gbt - G[s_]) * ep(r, s_)
+        K = M + E(Gbt) * T0 + E(gC - Gb2) * T0p + E(Gbt + gC - Gb2) * hdot
+        for u in range(a, b2 + 1):
+            L, R = E(Gm1[u] - Gbt), E(Gb2 - G[u])
+            srow = sum((E(G[r] - G[u]) * rho[r - a] for r in range(u, b2 + 1)), np.zeros(Dk))
+            scol = sum((E(Gm1[u] - G[s_]) * sig[s_ - a] for s_ in range(a, u)), np.zeros(Dk))
+            d4 = np.zeros(Dk)
+            for r in range(u, b2 + 1):
+                for s_ in range(a, u):
+                    d4 += E(G[r] - G[u]) * E(Gm1[u] - G[s_]) * ep(r, s_)
+            X[u] = L * srow + R * scol + L * R * K + d4
+    return X
+
+
+def vg_run(q, k, v, g_log, beta, S0, dY, dS_T, C=64, decay_grad=False):
     """Whole-sequence forward + VJP for one batch element and one value head with per-channel log decays
-    g_log [T, Dk].  Returns (y, S_T, dq, dk, dv, dg_log, dbeta, dS0), the states in [Dv, Dk] layout."""
+    g_log [T, Dk].  Returns (y, S_T, dq, dk, dv, dg_log, dbeta, dS0), the states in [Dv, Dk] layout; with
+    decay_grad, d/d(decay) (vg_dg_decay) in place of dg_log."""
     T_len, Dk = q.shape
     Dv = v.shape[1]
     nc = -(-T_len // C)
@@ -341,7 +402,8 @@ def vg_run(q, k, v, g_log, beta, S0, dY, dS_T, C=64):
         sl = slice(c * C, (c + 1) * C)
         G, T, W, U, P, Ahat = preps[c]
         dDelta, dh_prev = vg_bwd_state_chunk(dh, q[sl], k[sl], G, W, P, dY[sl])
-        out = vg_bwd_local_chunk(q[sl], k[sl], v[sl], beta[sl], G, P, Ahat, hs[c], dh, Ds[c], T.T @ dDelta, dY[sl])
+        out = vg_bwd_local_chunk(q[sl], k[sl], v[sl], beta[sl], G, P, Ahat, hs[c], dh, Ds[c], T.T @ dDelta, dY[sl],
+                                 decay_grad)
         dq[sl], dk[sl], dv[sl], db[sl], dg[sl] = out
         dh = dh_prev
     n = T_len

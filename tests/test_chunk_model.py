@@ -81,3 +81,28 @@ def test_vector_gate_chunk_model_matches_oracle(T, s0):
                 np.testing.assert_allclose(a, b, atol=1e-9, rtol=1e-7, err_msg=name)
     np.testing.assert_allclose(outs[0][2] + outs[1][2], dq[0, :, 0], atol=1e-9, rtol=1e-7)
     np.testing.assert_allclose(outs[0][3] + outs[1][3], dk[0, :, 0], atol=1e-9, rtol=1e-7)
+
+
+@pytest.mark.parametrize("T,zeros,top", [(64, 0.0, 1.5), (100, 0.0, 1.5), (100, 0.05, 1.5), (130, 0.02, 0.05)])
+def test_vector_gate_decay_gradient_without_division(T, zeros, top):
+    """vg_dg_decay forms d/d(decay) from factors <= 1: it equals d/d(log decay) / decay where both are defined, and
+    at zero decays (a log decay of -1e4, whose exponential is exactly 0) it equals the oracle's per-channel
+    recurrence, which differentiates the decay directly (S * decay, tools/gdn_vjp.py:174-179).  float64, two
+    value heads, decays exp(-U(0, top)) with a fraction set to zero; top = 0.05 keeps the terms that span whole
+    blocks (M_U, T0, the exit pair) large enough that leaving any one out fails the check."""
+    d = O.make_inputs(1, T, 1, 2, 16, seed=T + 7, s0_std=0.5, dtype=np.float64)
+    rng = np.random.default_rng(T + 3)
+    decay = np.exp(-rng.uniform(0.0, top, (1, T, 2, 16)))
+    decay[rng.random(decay.shape) < zeros] = 0.0
+    g_log = np.where(decay > 0, np.log(np.where(decay > 0, decay, 1.0)), -1e4)
+    dS_T = rng.standard_normal(d["state"].shape) * 0.3
+    (_, _), (_, _, _, dg, _, _) = O.gated_delta_chunked_vjp(
+        d["q"], d["k"], d["v"], decay, d["beta"], d["state"], None, d["dy"], dS_T, chunk=64, dtype=np.float64)
+    for h in range(2):
+        args = (d["q"][0, :, 0], d["k"][0, :, 0], d["v"][0, :, h], g_log[0, :, h], d["beta"][0, :, h],
+                d["state"][0, h], d["dy"][0, :, h], dS_T[0, h])
+        x = chunk_model.vg_run(*args, decay_grad=True)[5]
+        np.testing.assert_allclose(x, dg[0, :, h], atol=1e-9, rtol=1e-7)
+        if not zeros:
+            dgl = chunk_model.vg_run(*args)[5]
+            np.testing.assert_allclose(x * decay[0, :, h], dgl, atol=1e-9, rtol=1e-7)
