@@ -180,7 +180,8 @@ static size_t ck_snap_bytes(int B, int T, int Hv, int W) {
 
 struct CkShape {
     int B, T, Hk, Hv;
-    bool bf16, vg;  // vg: one decay per key channel
+    bool bf16;
+    int vg;  // vg_kind of the gate: 0 one decay per head, 1 per-channel log decays, 2 per-channel decays
 };
 
 // Forward group workspace: the forward tile set of Tg tokens, plus two carried states between groups when no
@@ -352,7 +353,7 @@ size_t gdn_saved_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int chunk, 
         const int W = ck_window(chunk);
         if (has_mask) return mask_saved({B, T, Hk, Hv, in_dtype == DT_BF16, false}, chunk).total;
         if (W) return ck_snap_bytes(B, T, Hv, W);
-        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true, gate_vec(gate_kind)).saved;
+        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true, vg_kind(gate_kind)).saved;
     }
     return rec_saved_bytes(B, T, Hv, Dk, Dv, chunk);
 }
@@ -363,7 +364,7 @@ size_t gdn_fwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int
     const int f = resolve_form(Hv, Dk, Dv, has_mask, gate_kind, form, in_dtype);
     if (f != GDN_FORM_CHUNK || B == 0 || T == 0) return 0;
     const int W = ck_window(chunk);
-    const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16, gate_vec(gate_kind)};
+    const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16, vg_kind(gate_kind)};
     if (has_mask) {
         // pass 2 runs forward-only when checkpointing; a forward-only call also holds g', beta' and z
         if (with_saved) return W ? std::max(ck_fwd_target_bytes(shp, W, true), ck_fwd_target_bytes(shp, W, false)) : 0;
@@ -381,7 +382,7 @@ namespace gdn {
 static int ck_forward(const ChunkCall &base, int chunk, void *saved, size_t saved_bytes, void *ws, size_t ws_bytes,
                       hipStream_t st) {
     const int B = base.B, T = base.T, Hk = base.Hk, Hv = base.Hv;
-    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16, gate_vec(base.gate)};
+    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16, vg_kind(base.gate)};
     const int W = ck_window(chunk);
     int rc;
     if (saved && !W) {  // the whole tile set, kept for the backward
@@ -466,7 +467,7 @@ static int ck_forward(const ChunkCall &base, int chunk, void *saved, size_t save
 static int ck_backward(const ChunkCall &base, int chunk, const void *saved, size_t saved_bytes, void *ws,
                        size_t ws_bytes, hipStream_t st) {
     const int B = base.B, T = base.T, Hk = base.Hk, Hv = base.Hv;
-    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16, gate_vec(base.gate)};
+    const CkShape shp{B, T, Hk, Hv, base.in_dt == DT_BF16, vg_kind(base.gate)};
     const int W = ck_window(chunk);
     int rc;
     if (!W) {
@@ -563,7 +564,7 @@ static char *at_off(void *base, size_t off) { return static_cast<char *>(base) +
 // beta, state0, y, state_T and shapes.
 static int ck_masked_forward(const ChunkCall &base, const uint8_t *mask, int chunk, void *saved, size_t saved_bytes,
                              void *ws, size_t ws_bytes, hipStream_t st) {
-    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16, gate_vec(base.gate)};
+    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16, vg_kind(base.gate)};
     const int W = ck_window(chunk);
     const size_t tokens = (size_t)base.B * base.T;
     float *g2, *b2, *Z, *Yp = nullptr;
@@ -634,7 +635,7 @@ static int ck_masked_forward(const ChunkCall &base, const uint8_t *mask, int chu
 // Masked chunked backward (resolved form GDN_FORM_CHUNK, arguments checked).
 static int ck_masked_backward(const ChunkCall &base, const uint8_t *mask, int chunk, const void *saved,
                               size_t saved_bytes, void *ws, size_t ws_bytes, hipStream_t st) {
-    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16, gate_vec(base.gate)};
+    const CkShape shp{base.B, base.T, base.Hk, base.Hv, base.in_dt == DT_BF16, vg_kind(base.gate)};
     const int W = ck_window(chunk);
     const size_t tokens = (size_t)base.B * base.T;
     const MaskSaved m = mask_saved(shp, chunk);
@@ -750,7 +751,7 @@ int gdn_fwd_noalloc(const void *q, const void *k, const void *v, const float *g,
     void *ws = nullptr;
     size_t ws_bytes = 0;
     if (f == GDN_FORM_CHUNK && B > 0 && T > 0) {
-        const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16, gate_vec(gate_kind)};
+        const CkShape shp{B, T, Hk, Hv, in_dtype == DT_BF16, vg_kind(gate_kind)};
         const size_t one = ck_fwd_group_bytes(shp, std::min(kChunkC, T), false);
         if (one > kNoAllocScratchBytes)
             return fail(GDN_ERR_UNSUPPORTED,
@@ -841,8 +842,8 @@ size_t gdn_bwd_workspace_bytes(int B, int T, int Hk, int Hv, int Dk, int Dv, int
         if (B == 0 || T == 0) return 0;
         const int W = ck_window(chunk);
         if (has_mask) return mask_work({B, T, Hk, Hv, in_dtype == DT_BF16, false}, chunk).total;
-        if (W) return ck_bwd_target_bytes({B, T, Hk, Hv, in_dtype == DT_BF16, gate_vec(gate_kind)}, W);
-        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true, gate_vec(gate_kind)).work;
+        if (W) return ck_bwd_target_bytes({B, T, Hk, Hv, in_dtype == DT_BF16, vg_kind(gate_kind)}, W);
+        return chunk_sizes(B, T, Hk, Hv, in_dtype == DT_BF16, true, vg_kind(gate_kind)).work;
     }
     return bwd_layout(B, T, Hv, Dk, Dv, chunk, gate_kind).total;
 }

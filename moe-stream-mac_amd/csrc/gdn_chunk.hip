@@ -1916,7 +1916,7 @@ constexpr int CK_D = ck::D;
 
 static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd, bool vg) {
+ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd, int vgk) {
     static_assert(CK_C == kChunkC && CK_D == kChunkD, "chunk geometry");
     ChunkSizes s{};
     const size_t NC = (size_t)(T + CK_C - 1) / CK_C;
@@ -1928,7 +1928,7 @@ ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd, bool v
         bf.size = bytes;
         off += al256(bytes);
     };
-    vg = vg && bf16;
+    const bool vg = vgk && bf16, vgd = vgk == 2 && bf16;
     put(s.G, vg ? 0 : n * CK_C * 8);
     put(s.U, n * cd * 4);
     put(s.H, bwd ? n * dd * (bf16 ? 2 : 4) : 0);
@@ -1950,6 +1950,7 @@ ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd, bool v
     put(s.dH, n * dd * (bf16 ? 2 : 4));
     put(s.dDl, n * cd * 4);                    // fp32 dDelta, or TdD = T^T dDelta (bf16 set)
     put(s.part, (size_t)B * T * (bf16 ? Hk : Hv) * 2 * CK_D * 4);
+    put(s.vgd, vgd ? n * ck::VGD_FLOATS * 4 : 0);
     s.work = off;
     return s;
 }
@@ -1961,7 +1962,7 @@ static ck::Args make_args(const ChunkCall &cc) {
     a.state_T = cc.state_T;
     a.dg = cc.dg; a.dbeta = cc.dbeta; a.dstate0 = cc.dstate0;
     const bool bf16 = cc.in_dt == DT_BF16;
-    const ChunkSizes s = chunk_sizes(cc.B, cc.T, cc.Hk, cc.Hv, bf16, !cc.fwd_only, gate_vec(cc.gate));
+    const ChunkSizes s = chunk_sizes(cc.B, cc.T, cc.Hk, cc.Hv, bf16, !cc.fwd_only, vg_kind(cc.gate));
     char *sv = static_cast<char *>(cc.tiles);
     auto at = [&](const ChunkSizes::Buf &bf) -> void * { return bf.size ? sv + bf.off : nullptr; };
     a.w.H = static_cast<float *>(at(s.H));
@@ -1985,6 +1986,7 @@ static ck::Args make_args(const ChunkCall &cc) {
         a.w.dH = reinterpret_cast<float *>(wk + s.dH.off);
         a.w.dDl = reinterpret_cast<float *>(wk + s.dDl.off);
         a.w.part = reinterpret_cast<float *>(wk + s.part.off);
+        a.w.vgd = s.vgd.size ? reinterpret_cast<float *>(wk + s.vgd.off) : nullptr;
     }
     a.B = cc.B; a.T = cc.T; a.Ts = cc.Ts; a.Hk = cc.Hk; a.Hv = cc.Hv; a.NC = (cc.T + CK_C - 1) / CK_C;
     a.in_dt = cc.in_dt; a.out_dt = cc.out_dt; a.dy_dt = cc.dy_dt; a.grad_dt = cc.grad_dt; a.gate = cc.gate;

@@ -258,7 +258,17 @@ struct Bufs {
     float *Gv;            // [B][Hv][NC][C][D]     G_rj log2(e), G_rj = sum_{u<=r} log d_uj within the chunk; row C-1: G_C
     unsigned short *QGb;  // [B][Hv][NC][C][D]     Q * exp(G), fragment order (the forward's A operand of Y)
     unsigned short *KDb;  // [B][Hv][NC][C][D]     K * exp(G_C - G), fragment order (ck_bwd_seq's A operand of dDelta)
+    // per-channel decays (not log decays): what ck_bwd_local_vg leaves for ck_vg_dg, VGD_FLOATS per chunk-head
+    float *vgd;
 };
+
+// The vgd buffer of one chunk-head (fp32): the pair terms through the chunk's entry state rho0 = q * dQg -
+// beta k * Y2 and through its exit state sig0 = k * dKd, the row role through the token before the row's 16-token
+// block rho1 and the column role through the block's last token sig1 (all [C][D], before any decay factor), the
+// pair cotangents dP and dA [C][C] (only the four diagonal blocks and the blocks (2, 0), (3, 0), (3, 1) are
+// written), and <dh', h> per state row [D].
+constexpr int VGD_R0 = 0, VGD_R1 = VGD_R0 + C * D, VGD_S0 = VGD_R1 + C * D, VGD_S1 = VGD_S0 + C * D;
+constexpr int VGD_DP = VGD_S1 + C * D, VGD_DA = VGD_DP + C * C, VGD_HD = VGD_DA + C * C, VGD_FLOATS = VGD_HD + D;
 
 struct Args {
     const void *q, *k, *v;

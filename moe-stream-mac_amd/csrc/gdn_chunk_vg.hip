@@ -480,7 +480,10 @@ static_assert(C * VLGp * 4 <= 2 * C * LDC * 4, "dG fits the transposed pair tile
 // that lane (ch, li) owns are contiguous.
 __device__ __forceinline__ int pcol(int j) { return (j & ~63) + (j & 15) * 4 + ((j >> 4) & 3); }
 
-template <bool DYF32>
+// DEC: per-channel decays.  Their gradient d/d(decay) = dg_log / d loses every digit where d is small (dg_log is a
+// suffix sum of terms that each carry the factor d), so this head writes no dg: it leaves the pieces of the pair
+// terms, before their decay factors, in the vgd buffer, and ck_vg_dg forms d/d(decay) from them with factors <= 1.
+template <bool DYF32, bool DEC>
 __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, int b, int rr, int rep) {
     __shared__ __align__(16) unsigned char arena[VARENA];
     __shared__ float sB[C], sVT[C], sHdot[D], sGCp[D];
@@ -501,6 +504,7 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
     const int w = tid >> 6, l = tid & 63, li = l & 15, lg = l >> 4;
     const int R = w & 3, r0 = 16 * R, ch = w >> 2;
     const size_t ci = chunk_index(a, b, hv, c);
+    float *const vgd = DEC ? a.w.vgd + ci * VGD_FLOATS : nullptr;
     const bfr *Hc = reinterpret_cast<const bfr *>(a.w.H) + ci * D * D;
     const bfr *dHc = reinterpret_cast<const bfr *>(a.w.dH) + ci * D * D;
     const float *Dc = a.w.Dl + ci * C * D;
@@ -561,7 +565,10 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
                 dot += bf2f(hw[q] & 0xffffu) * bf2f(dw[q] & 0xffffu) + bf2f(hw[q] >> 16) * bf2f(dw[q] >> 16);
             // the 16 pieces of state row r are the 16 lanes of one DPP row
             dot = row16_allreduce(dot);
-            if ((tid & 15) == 0) sHdot[r] = dot;
+            if ((tid & 15) == 0) {
+                sHdot[r] = dot;
+                if constexpr (DEC) vgd[VGD_HD + r] = dot;
+            }
         }
         auto f = [](uint32_t x) { return __uint_as_float(x); };
 #pragma unroll
@@ -660,6 +667,14 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
             sDA[r * LDC + s2] = av;
             sDPt[s2 * LDC + r] = pv;
             sDAt[s2 * LDC + r] = av;
+            if constexpr (DEC) {
+                // the blocks ck_vg_dg reads: the diagonal ones and those with a whole block between row and column
+                const int S = 2 * ch + t;
+                if (S == R || R - S >= 2) {
+                    vgd[VGD_DP + r * C + s2] = pv;
+                    vgd[VGD_DA + r * C + s2] = av;
+                }
+            }
         }
     {
         constexpr int PPER = C * (D / 8) / NTB;
@@ -710,6 +725,11 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const float eG = ex2(Gr[e][t]), eD = ex2(gc[t] - Gr[e][t]);
+            if constexpr (DEC) {
+                const int o = (r0 + 4 * lg + e) * D + 64 * ch + 16 * t + li;
+                vgd[VGD_R0 + o] = qv[e][t] * X1[t][e] - be * kv[e][t] * Y2[t][e];
+                vgd[VGD_S0 + o] = kv[e][t] * X2[t][e];
+            }
             bp[e] -= kv[e][t] * eG * Y2[t][e];
             X1[t][e] *= eG;
             Y2[t][e] *= -be * eG;
@@ -776,6 +796,9 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float eL = ex2(Gr[e][t] - gb);
+                if constexpr (DEC)
+                    vgd[VGD_R1 + (r0 + 4 * lg + e) * D + 64 * ch + 16 * t + li] =
+                        qv[e][t] * aq[t][e] + sB[r0 + 4 * lg + e] * kv[e][t] * az[t][e];
                 X1[t][e] += aq[t][e] * eL;
                 Z[t][e] = az[t][e] * eL;
             }
@@ -828,7 +851,10 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
         for (int t = 0; t < 4; ++t) {
             const float gb = sGp[b2 * VLGp + pc0 + t];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) X2[t][e] += am[t][e] * ex2(gb - Gr[e][t]);
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (DEC) vgd[VGD_S1 + (r0 + 4 * lg + e) * D + 64 * ch + 16 * t + li] = kv[e][t] * am[t][e];
+                X2[t][e] += am[t][e] * ex2(gb - Gr[e][t]);
+            }
         }
     }
     // ---- the diagonal block R, elementwise, along running products of the decays E_rs = prod_{s<u<=r} d_u (four
@@ -925,35 +951,30 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
     }
     __syncthreads();  // the transposed pair tiles are read: dG takes their space
     float *const sDG = F32(VO_DG);
+    if constexpr (!DEC) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
+        for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) sDG[(r0 + 4 * lg + e) * VLGp + 64 * ch + 16 * t + li] = dGv[e][t];
+            for (int t = 0; t < 4; ++t) sDG[(r0 + 4 * lg + e) * VLGp + 64 * ch + 16 * t + li] = dGv[e][t];
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const float rb = row16_allreduce(bp[e]);
         if (li == 0) sRow[ch][r0 + 4 * lg + e] = rb;
     }
+    if constexpr (!DEC) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        float x = gp[t];
-        x += lane_xor16(x);
-        x += lane_xor32(x);
-        if (lg == 0) sDgc[R][64 * ch + 16 * t + li] = x;
-    }
-    // the decays of this thread's part of the dg output, in flight during the scan
-    constexpr int GPER = C * D / NTB;
-    static_assert(GPER * NTB == C * D, "even split");
-    float dec[GPER];
-#pragma unroll
-    for (int p = 0; p < GPER; ++p) {
-        const int i = tid + p * NTB, r = i / D, j = i - r * D;
-        dec[p] = a.g[(((size_t)b * a.Ts + t0 + min(r, n - 1)) * a.Hv + hv) * D + j];
+        for (int t = 0; t < 4; ++t) {
+            float x = gp[t];
+            x += lane_xor16(x);
+            x += lane_xor32(x);
+            if (lg == 0) sDgc[R][64 * ch + 16 * t + li] = x;
+        }
     }
     __syncthreads();
     // dg_log_u = sum_{r >= u} dG_r + dG_C (every token's log decay adds to G_C), in place: thread (segment gs of 16
     // rows, channel j) sums its segment, then adds the later segments' totals and dG_C while it writes the suffix sums
-    {
+    if constexpr (!DEC) {
         const int j = tid & (D - 1), gs = tid >> 7;
         float tot = 0.f;
 #pragma unroll
@@ -974,14 +995,16 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
         const int r = tid;
         if (r < n) a.dbeta[((size_t)b * a.Ts + t0 + r) * a.Hv + hv] = sVT[r] + sRow[0][r] + sRow[1][r];
     }
-    __syncthreads();
-    // d/d(decay) = dg_log / d (or dg_log itself for log gates), coalesced over the channels
-    const bool in_log = a.gate == GATE_LOG_VEC;
+    if constexpr (!DEC) {
+        __syncthreads();
+        // d/d(log decay), coalesced over the channels
+        constexpr int GPER = C * D / NTB;
+        static_assert(GPER * NTB == C * D, "even split");
 #pragma unroll
-    for (int p = 0; p < GPER; ++p) {
-        const int i = tid + p * NTB, r = i / D, j = i - r * D;
-        const float x = sDG[r * VLGp + j];
-        if (r < n) a.dg[(((size_t)b * a.Ts + t0 + r) * a.Hv + hv) * D + j] = in_log ? x : dg_per_decay(x, dec[p]);
+        for (int p = 0; p < GPER; ++p) {
+            const int i = tid + p * NTB, r = i / D, j = i - r * D;
+            if (r < n) a.dg[(((size_t)b * a.Ts + t0 + r) * a.Hv + hv) * D + j] = sDG[r * VLGp + j];
+        }
     }
     // ---- dq | dk: this value head's parts summed over the key head's value heads.  They leave through an fp32
     // staging tile [64][dq 128 | dk 128] over the permuted K, Q, G tiles (dead since the diagonal loops), so that
@@ -1042,7 +1065,7 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
     __syncthreads();  // the arena is reused by the next value head
 }
 
-template <bool DYF32>
+template <bool DYF32, bool DEC>
 __global__ __launch_bounds__(NTB) void ck_bwd_local_vg_kernel(Args a) {
     typedef const __attribute__((address_space(4))) Args *KArgs;
     const int rep = a.Hv / a.Hk;
@@ -1050,15 +1073,200 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_vg_kernel(Args a) {
         // the arguments are read anew for each value head instead of being held in scalar registers across it
         KArgs ap = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
         asm volatile("" : "+s"(ap));
-        bwd_local_vg_head<DYF32>(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep);
+        bwd_local_vg_head<DYF32, DEC>(*(const Args *)ap, blockIdx.x, blockIdx.y, blockIdx.z, rr, rep);
     }
 }
 
+// ---------------------------------------------------------------------------------------------- ck_vg_dg
+//
+// d/d(decay) of per-channel decays, one workgroup per (chunk, value head), thread (block U = tid / 128, channel j)
+// for the 16 tokens u of block U (rows a..b2, bt = a - 1, G_-1 = 0, G the cumulative log decay of the chunk).
+// Every term of d/d(log decay)_u is a pair term whose span s' < u <= r straddles u and which carries the factor
+// exp(G_r - G_s'); d/d(decay)_u is that sum divided by d_u, and exp(G_r - G_s') / d_u = exp(G_r - G_u)
+// exp(G_{u-1} - G_s'), two factors <= 1.  Grouped by where r and s' lie:
+//   X_u = L_u Srow_u + R_u Scol_u + L_u R_u K_U + D4_u,  L_u = exp(G_{u-1} - G_bt),  R_u = exp(G_b2 - G_u)
+//   Srow_u = sum_{r in U, r >= u} exp(G_r - G_u) RHO_r,  RHO = exp(G_bt) rho0 + rho1  (s' before the block)
+//   Scol_u = sum_{s in U, s < u} exp(G_{u-1} - G_s) SIG_s,  SIG = exp(G_C - G_b2) sig0 + sig1  (r after it)
+//   K_U = M_U + exp(G_bt) T0 + exp(G_C - G_b2) T0' + exp(G_bt + G_C - G_b2) <dh', h>  (both outside)
+//   D4_u = sum_{r in U, r >= u} sum_{s in U, s < u} exp(G_r - G_u) exp(G_{u-1} - G_s) e'_rs  (both inside)
+// with e'_rs = dP_rs q_r k_s + beta_r dA_rs k_r k_s, T0 = sum_{r > b2} exp(G_r - G_b2) rho0_r and T0' =
+// sum_{s <= bt} exp(G_bt - G_s) sig0_s from the block sums B0_R = sum_{r in R} exp(G_r - G_bt(R)) rho0_r and
+// B0'_S = sum_{s in S} exp(G_b2(S) - G_s) sig0_s, and M_U = sum_{r > b2, s <= bt} exp(G_r - G_b2) exp(G_bt - G_s)
+// e'_rs from the transfers Q_RS = sum_{r in R, s in S} exp(G_r - G_bt(R)) exp(G_b2(S) - G_s) e'_rs of the block
+// pairs (2, 0), (3, 0), (3, 1), which threads of blocks 0, 3 and 1 form.  Srow and Scol are scans along the block
+// (S_u = RHO_u + d_{u+1} S_{u+1}; Scol_{u+1} = d_u Scol_u + SIG_u); D4 keeps c_r(u) = sum_{s in U, s < u}
+// exp(G_{u-1} - G_s) e'_rs for the rows r of the block (c_r(u + 1) = d_u c_r(u) + e'_ru) and reads D4_u out of
+// them by Horner steps.  Decays below 2^-64 count as 2^-64 (the cumulative log decays are formed that way).
+__global__ __launch_bounds__(NTB) void ck_vg_dg_kernel(Args a) {
+    __shared__ float sP[C][C + 1], sA[C][C + 1];
+    __shared__ float sBt[C];
+    __shared__ float sB0[4][D], sB0p[4][D], sQ[4][D];
+    const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+    const int hk = hv / (a.Hv / a.Hk);
+    const int t0 = c * C, n = min(C, a.T - t0);
+    const size_t ci = chunk_index(a, b, hv, c);
+    const float *const vgd = a.w.vgd + ci * VGD_FLOATS;
+    const float *const Gc = a.w.Gv + ci * C * D;  // log2 units
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int U = tid >> 7, j = tid & (D - 1), a0 = 16 * U;
+    const size_t qk0 = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D + j, qk_row = (size_t)a.Hk * D;
+    const bfr *const qsrc = static_cast<const bfr *>(a.q) + qk0, *const ksrc = static_cast<const bfr *>(a.k) + qk0;
+    // the blocks of dP and dA in use: (0,0) (1,1) (2,2) (3,3) (2,0) (3,0) (3,1)
+    for (int i = tid; i < 7 * 256; i += NTB) {
+        const int blk = i >> 8, e = i & 255;
+        const int R = blk < 4 ? blk : blk == 6 ? 3 : blk - 2, S = blk < 4 ? blk : blk == 6 ? 1 : 0;
+        const int r = 16 * R + (e >> 4), s = 16 * S + (e & 15);
+        sP[r][s] = vgd[VGD_DP + r * C + s];
+        sA[r][s] = vgd[VGD_DA + r * C + s];
+    }
+    if (tid < C) {
+        const float xb = a.beta[((size_t)b * a.Ts + t0 + min(tid, n - 1)) * a.Hv + hv];
+        sBt[tid] = tid < n ? xb : 0.f;
+    }
+    // G at the last row of each block; this block's rows
+    float gB[4], G[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gB[i] = Gc[(16 * i + 15) * D + j];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) G[i] = Gc[(a0 + i) * D + j];
+    const float gbt = U == 0 ? 0.f : U == 1 ? gB[0] : U == 2 ? gB[1] : gB[2];
+    const float gb2 = U == 0 ? gB[0] : U == 1 ? gB[1] : U == 2 ? gB[2] : gB[3];
+    const float gC = gB[3];
+    // RHO, SIG of this block, and its block sums B0, B0'
+    float RHO[16], SIG[16];
+    {
+        const float fb = ex2(gbt), fc = ex2(gC - gb2);
+        float b0 = 0.f, b0p = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int o = (a0 + i) * D + j;
+            const float x0 = vgd[VGD_R0 + o], y0 = vgd[VGD_S0 + o];
+            b0 = fmaf(ex2(G[i] - gbt), x0, b0);
+            b0p = fmaf(ex2(gb2 - G[i]), y0, b0p);
+            RHO[i] = fb * x0;
+            SIG[i] = fc * y0;
+        }
+        sB0[U][j] = b0;
+        sB0p[U][j] = b0p;
+        // the row role of block 0 and the column role of block 3 are empty
+        if (U > 0) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) RHO[i] += vgd[VGD_R1 + (a0 + i) * D + j];
+        }
+        if (U < 3) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) SIG[i] += vgd[VGD_S1 + (a0 + i) * D + j];
+        }
+    }
+    __syncthreads();  // dP, dA, beta staged
+    // the transfer of block pair (R, S): threads of block 0 take (2, 0), of block 3 (3, 0), of block 1 (3, 1)
+    if (U != 2) {
+        const int R = U == 0 ? 2 : 3, S = U == 1 ? 1 : 0;
+        const float gtR = R == 2 ? gB[1] : gB[2], gbS = S == 0 ? gB[0] : gB[1];
+        float kap[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int s = 16 * S + i;
+            const float ks = bf2f(ksrc[(size_t)min(s, n - 1) * qk_row]);
+            kap[i] = s < n ? ks * ex2(gbS - Gc[s * D + j]) : 0.f;
+        }
+        float acc = 0.f;
+        for (int ii = 0; ii < 16; ++ii) {
+            const int r = 16 * R + ii, rc = min(r, n - 1);
+            const float qr = bf2f(qsrc[(size_t)rc * qk_row]), kr = bf2f(ksrc[(size_t)rc * qk_row]);
+            float pp = 0.f, pa = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                pp = fmaf(sP[r][16 * S + i], kap[i], pp);
+                pa = fmaf(sA[r][16 * S + i], kap[i], pa);
+            }
+            const float x = ex2(Gc[r * D + j] - gtR) * fmaf(qr, pp, sBt[r] * kr * pa);
+            acc += r < n ? x : 0.f;
+        }
+        sQ[U][j] = acc;
+    }
+    // q, k of this block's rows (zero past the sequence)
+    float qv[16], kv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = a0 + i, rc = min(r, n - 1);
+        const float xq = bf2f(qsrc[(size_t)rc * qk_row]), xk = bf2f(ksrc[(size_t)rc * qk_row]);
+        qv[i] = r < n ? xq : 0.f;
+        kv[i] = r < n ? xk : 0.f;
+    }
+    const float hdot = vgd[VGD_HD + j];
+    __syncthreads();  // block sums and transfers
+    // opaque copies of the block's boundary values: the factors below are formed anew rather than kept in registers
+    // from the block sums above
+    float gbt_ = gbt, gb2_ = gb2;
+    asm volatile("" : "+v"(gbt_), "+v"(gb2_));
+    float K;
+    {
+        float T0 = 0.f, T0p = 0.f;
+#pragma unroll
+        for (int R = 1; R < 4; ++R)
+            if (R > U) T0 = fmaf(ex2(gB[R - 1] - gb2_), sB0[R][j], T0);
+#pragma unroll
+        for (int S = 0; S < 3; ++S)
+            if (S < U) T0p = fmaf(ex2(gbt_ - gB[S]), sB0p[S][j], T0p);
+        const float M = U == 1 ? sQ[0][j] + ex2(gB[2] - gB[1]) * sQ[3][j]
+                        : U == 2 ? ex2(gB[1] - gB[0]) * sQ[3][j] + sQ[1][j] : 0.f;
+        K = M + ex2(gbt_) * T0 + ex2(gC - gb2_) * T0p + ex2(gbt_ + gC - gb2_) * hdot;
+    }
+    // the decays d[i] = 2^(G_i - G_{i-1}) along the block, L and R
+    float d[16], X[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) d[i] = ex2(G[i] - (i ? G[i - 1] : gbt_));
+    {
+        float S = 0.f;
+#pragma unroll
+        for (int i = 15; i >= 0; --i) {
+            S = i < 15 ? fmaf(d[i + 1], S, RHO[i]) : RHO[i];
+            const float L = ex2((i ? G[i - 1] : gbt_) - gbt_), Rf = ex2(gb2_ - G[i]);
+            X[i] = L * fmaf(Rf, K, S);
+        }
+        float Sc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            X[i] = fmaf(ex2(gb2_ - G[i]), Sc, X[i]);
+            Sc = fmaf(d[i], Sc, SIG[i]);
+        }
+    }
+    // D4, one row r of the block at a time: c = c_r(u) = sum_{s in U, s < u} exp(G_{u-1} - G_s) e'_rs runs along
+    // u (c_r(u + 1) = d_u c_r(u) + e'_ru) and adds exp(G_r - G_u) c_r(u) to X_u for u <= r
+#pragma unroll 1
+    for (int r = 1; r < 16; ++r) {
+        const int rr = a0 + r, rc = min(rr, n - 1);
+        const float gr = Gc[rr * D + j];
+        const float xq = bf2f(qsrc[(size_t)rc * qk_row]), xk = bf2f(ksrc[(size_t)rc * qk_row]);
+        const float qr = rr < n ? xq : 0.f, bkr = rr < n ? sBt[rr] * xk : 0.f;
+        const float *const prow = &sP[rr][a0], *const arow = &sA[rr][a0];
+        float cc = 0.f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const float xu = ex2(gr - G[u]) * cc;  // past the row (u > r) the factor may overflow: not taken
+            X[u] += u <= r ? xu : 0.f;
+            const float ep = kv[u] * fmaf(prow[u], qr, bkr * arow[u]);
+            cc = fmaf(d[u], cc, u < r ? ep : 0.f);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if (a0 + i < n) a.dg[(((size_t)b * a.Ts + t0 + a0 + i) * a.Hv + hv) * D + j] = X[i];
+}
+
 void launch_vg_local(const Args &a, hipStream_t st) {
-    if (a.dy_dt == DT_F32)
-        hipLaunchKernelGGL(ck_bwd_local_vg_kernel<true>, dim3(a.NC, a.Hk, a.B), dim3(NTB), 0, st, a);
-    else
-        hipLaunchKernelGGL(ck_bwd_local_vg_kernel<false>, dim3(a.NC, a.Hk, a.B), dim3(NTB), 0, st, a);
+    const bool dec = a.gate == GATE_DECAY_VEC;
+    const dim3 grid(a.NC, a.Hk, a.B);
+    if (a.dy_dt == DT_F32) {
+        if (dec) hipLaunchKernelGGL((ck_bwd_local_vg_kernel<true, true>), grid, dim3(NTB), 0, st, a);
+        else hipLaunchKernelGGL((ck_bwd_local_vg_kernel<true, false>), grid, dim3(NTB), 0, st, a);
+    } else {
+        if (dec) hipLaunchKernelGGL((ck_bwd_local_vg_kernel<false, true>), grid, dim3(NTB), 0, st, a);
+        else hipLaunchKernelGGL((ck_bwd_local_vg_kernel<false, false>), grid, dim3(NTB), 0, st, a);
+    }
+    if (dec) hipLaunchKernelGGL(ck_vg_dg_kernel, dim3(a.NC, a.Hv, a.B), dim3(NTB), 0, st, a);
 }
 
 }  // namespace ck

@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "gdn_common.h"
+
 namespace gdn {
 
 struct RecFwdArgs {
@@ -48,11 +50,14 @@ struct ChunkSizes {
     Buf Wb, KTb, Pb, PTb, QTb, nWTb;  // bf16 operand tiles of the bf16 set
     Buf Gv, QGb, KDb;                 // per-channel gates (bf16 set)
     size_t saved;                     // size of the tile set
-    Buf dH, dDl, part;                // backward workspace
+    Buf dH, dDl, part, vgd;           // backward workspace
     size_t work;                      // its size
 };
-// vg: one decay per key channel (GATE_DECAY_VEC or GATE_LOG_VEC), bf16 set only.
-ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd, bool vg = false);
+// vg: the per-channel gate kind (vg_kind), bf16 set only.
+ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd, int vg = 0);
+// The per-channel gate kind of a gate: 0 one decay per head, 1 per-channel log decays, 2 per-channel decays (whose
+// backward also keeps the pieces ck_vg_dg forms d/d(decay) from, in the vgd buffer).
+inline int vg_kind(int gate) { return gate == GATE_LOG_VEC ? 1 : gate == GATE_DECAY_VEC ? 2 : 0; }
 
 // One launch of a chunked stage.  q, k, v, g, beta, y, dy, dq, dk, dv, dg and dbeta point at the launch's first
 // token; T is the launch's token count and Ts the token stride of a sequence (the full length).  tiles / work are

@@ -312,7 +312,8 @@ def vg_bwd_local_chunk(q, k, v, beta, G, P, Ahat, h, dh_next, Delta, TdD, dY, de
     dg_log = np.cumsum(dG[::-1], axis=0)[::-1] + dgC
     if decay_grad:
         hdot = (dh_next * h).sum(1)
-        return dq, dk, dv, dbeta, vg_dg_decay(q, k, beta, G, dQg, Y2, dKd, hdot, dP, dA)
+        f = vg_dg_decay_blocked if decay_grad == "blocked" else vg_dg_decay
+        return dq, dk, dv, dbeta, f(q, k, beta, G, dQg, Y2, dKd, hdot, dP, dA)
     return dq, dk, dv, dbeta, dg_log
 
 
@@ -372,10 +373,78 @@ def vg_dg_decay(q, k, beta, G, dQg, Y2, dKd, hdot, dP, dA):
     return X
 
 
+def vg_dg_decay_blocked(q, k, beta, G, dQg, Y2, dKd, hdot, dP, dA):
+    """vg_dg_decay in the order of ck_vg_dg (gdn_chunk_vg.hip), one (block U, channel) pair per thread: the
+    whole-block spans from block sums B0_R = sum_{r in R} exp(G_r - G_bt(R)) rho0_r and B0'_S = sum_{s in S}
+    exp(G_b2(S) - G_s) sig0_s, M_U from the transfers Q_RS = sum_{r in R, s in S} exp(G_r - G_bt(R))
+    exp(G_b2(S) - G_s) e'_rs of the block pairs (2, 0), (3, 0), (3, 1) (the only ones with a block between them),
+    Srow and Scol as scans along the block, D4 from running sums c_r(u) = sum_{s in U, s < u} exp(G_{u-1} - G_s)
+    e'_rs (c_r(u + 1) = d_u c_r(u) + e'_ru) read out by Horner steps.  Every factor is exp of a difference <= 0."""
+    C, Dk = G.shape
+    nb = C // SUB
+    E = np.exp
+    rho0 = q * dQg - beta[:, None] * k * Y2
+    sig0 = k * dKd
+    Gb = [G[SUB * i + SUB - 1] for i in range(nb)]  # G at the last row of each block
+    gbt = lambda U: Gb[U - 1] if U else np.zeros(Dk)
+    gC = G[-1]
+    B0 = [sum(E(G[r] - gbt(R)) * rho0[r] for r in range(SUB * R, SUB * R + SUB)) for R in range(nb)]
+    B0p = [sum(E(Gb[S] - G[s]) * sig0[s] for s in range(SUB * S, SUB * S + SUB)) for S in range(nb)]
+
+    def transfer(R, S):
+        kap = [k[s] * E(Gb[S] - G[s]) for s in range(SUB * S, SUB * S + SUB)]
+        acc = np.zeros(Dk)
+        for r in range(SUB * R, SUB * R + SUB):
+            p = sum(dP[r, SUB * S + i] * kap[i] for i in range(SUB))
+            a = sum(dA[r, SUB * S + i] * kap[i] for i in range(SUB))
+            acc += E(G[r] - gbt(R)) * (q[r] * p + beta[r] * k[r] * a)
+        return acc
+    Q20, Q30, Q31 = transfer(2, 0), transfer(3, 0), transfer(3, 1)
+    M = [np.zeros(Dk), Q20 + E(Gb[2] - Gb[1]) * Q30, E(Gb[1] - Gb[0]) * Q30 + Q31, np.zeros(Dk)]
+    X = np.zeros((C, Dk))
+    for U in range(nb):
+        a0 = SUB * U
+        rows = range(a0, a0 + SUB)
+        gb2 = Gb[U]
+        T0 = sum((E(gbt(R) - gb2) * B0[R] for R in range(U + 1, nb)), np.zeros(Dk))
+        T0p = sum((E(gbt(U) - Gb[S]) * B0p[S] for S in range(U)), np.zeros(Dk))
+        K = M[U] + E(gbt(U)) * T0 + E(gC - gb2) * T0p + E(gbt(U) + gC - gb2) * hdot
+        rho1 = np.zeros((SUB, Dk))
+        sig1 = np.zeros((SUB, Dk))
+        ep = lambda r, s: dP[r, s] * q[r] * k[s] + beta[r] * dA[r, s] * k[r] * k[s]
+        for i, r in enumerate(rows):
+            for s in range(a0):
+                rho1[i] += ep(r, s) * E(gbt(U) - G[s])
+            for r2 in range(a0 + SUB, C):
+                sig1[i] += ep(r2, r) * E(G[r2] - gb2)
+        RHO = E(gbt(U)) * rho0[a0:a0 + SUB] + rho1
+        SIG = E(gC - gb2) * sig0[a0:a0 + SUB] + sig1
+        Gm = [gbt(U)] + [G[r] for r in rows]  # G_{u-1}, G_u for local u at Gm[u], Gm[u + 1]
+        d = [E(Gm[i + 1] - Gm[i]) for i in range(SUB)]
+        L = [E(Gm[i] - gbt(U)) for i in range(SUB)]
+        Rf = [E(gb2 - Gm[i + 1]) for i in range(SUB)]
+        srow = [None] * SUB
+        acc = np.zeros(Dk)
+        for i in range(SUB - 1, -1, -1):
+            acc = RHO[i] + (d[i + 1] * acc if i + 1 < SUB else 0.0)
+            srow[i] = acc
+        scol = np.zeros(Dk)
+        cr = [np.zeros(Dk) for _ in range(SUB)]
+        for i in range(SUB):
+            d4 = cr[SUB - 1].copy()
+            for r in range(SUB - 2, i - 1, -1):
+                d4 = cr[r] + d[r + 1] * d4
+            X[a0 + i] = L[i] * srow[i] + Rf[i] * scol + L[i] * Rf[i] * K + d4
+            scol = d[i] * scol + SIG[i]
+            for r in range(i + 1, SUB):
+                cr[r] = d[i] * cr[r] + ep(a0 + r, a0 + i)
+    return X
+
+
 def vg_run(q, k, v, g_log, beta, S0, dY, dS_T, C=64, decay_grad=False):
     """Whole-sequence forward + VJP for one batch element and one value head with per-channel log decays
     g_log [T, Dk].  Returns (y, S_T, dq, dk, dv, dg_log, dbeta, dS0), the states in [Dv, Dk] layout; with
-    decay_grad, d/d(decay) (vg_dg_decay) in place of dg_log."""
+    decay_grad, d/d(decay) (vg_dg_decay, or vg_dg_decay_blocked for decay_grad="blocked") in place of dg_log."""
     T_len, Dk = q.shape
     Dv = v.shape[1]
     nc = -(-T_len // C)

@@ -175,13 +175,18 @@ def test_saved_sizes_by_form():
     assert lib.gdn_select_form(32, 64, 64, 0, L.GATE_DECAY_VEC, L.FORM_AUTO, L.BF16) == L.FORM_RECURRENT
     assert lib.gdn_select_form(32, 128, 128, 1, L.GATE_DECAY_VEC, L.FORM_CHUNK, L.BF16) == L.GDN_ERR_UNSUPPORTED
     assert b"per-channel gates" in lib.gdn_last_error()
-    # per-channel log decays resolve like per-channel decays, and size the same buffers
+    # per-channel log decays resolve like per-channel decays and save the same tiles; on the chunked form the
+    # backward of decays (not log decays) also keeps, per (value head, 64-token chunk), the pieces d/d(decay) is
+    # formed from: four fp32 [64][128] tiles, dP and dA fp32 [64][64] and one fp32 [128] row (2 x 4 heads x 5 chunks)
+    vgd = 2 * 4 * 5 * (4 * 64 * 128 + 2 * 64 * 64 + 128) * 4
     for m, dt in ((0, L.BF16), (0, L.F32), (1, L.BF16)):
         assert (lib.gdn_select_form(32, 128, 128, m, L.GATE_LOG_VEC, L.FORM_AUTO, dt)
                 == lib.gdn_select_form(32, 128, 128, m, L.GATE_DECAY_VEC, L.FORM_AUTO, dt))
-        for gate_sizes in (lambda gk: lib.gdn_saved_bytes(2, 300, 2, 4, 128, 128, 64, gk, m, L.FORM_AUTO, dt),
-                           lambda gk: lib.gdn_bwd_workspace_bytes(2, 300, 2, 4, 128, 128, 64, gk, m, L.FORM_AUTO, dt)):
-            assert gate_sizes(L.GATE_LOG_VEC) == gate_sizes(L.GATE_DECAY_VEC) > 0
+        saved = lambda gk: lib.gdn_saved_bytes(2, 300, 2, 4, 128, 128, 64, gk, m, L.FORM_AUTO, dt)
+        assert saved(L.GATE_LOG_VEC) == saved(L.GATE_DECAY_VEC) > 0
+        work = lambda gk: lib.gdn_bwd_workspace_bytes(2, 300, 2, 4, 128, 128, 64, gk, m, L.FORM_AUTO, dt)
+        extra = vgd if (m, dt) == (0, L.BF16) else 0
+        assert work(L.GATE_LOG_VEC) + extra == work(L.GATE_DECAY_VEC) > 0
     assert lib.gdn_select_form(32, 128, 128, 0, 4, L.FORM_AUTO, L.BF16) == L.GDN_ERR_INVALID
     for q in (lambda f: lib.gdn_saved_bytes(1, 300, 130, 260, 128, 128, 64, L.GATE_LOG, 1, f, L.BF16),
               lambda f: lib.gdn_bwd_workspace_bytes(1, 300, 130, 260, 128, 128, 64, L.GATE_LOG, 1, f, L.BF16)):

@@ -89,7 +89,8 @@ def test_vector_gate_decay_gradient_without_division(T, zeros, top):
     at zero decays (a log decay of -1e4, whose exponential is exactly 0) it equals the oracle's per-channel
     recurrence, which differentiates the decay directly (S * decay, tools/gdn_vjp.py:174-179).  float64, two
     value heads, decays exp(-U(0, top)) with a fraction set to zero; top = 0.05 keeps the terms that span whole
-    blocks (M_U, T0, the exit pair) large enough that leaving any one out fails the check."""
+    blocks (M_U, T0, the exit pair) large enough that leaving any one out fails the check.  The blocked
+    restatement (the order of the GPU kernel) is held to the same bar."""
     d = O.make_inputs(1, T, 1, 2, 16, seed=T + 7, s0_std=0.5, dtype=np.float64)
     rng = np.random.default_rng(T + 3)
     decay = np.exp(-rng.uniform(0.0, top, (1, T, 2, 16)))
@@ -103,6 +104,8 @@ def test_vector_gate_decay_gradient_without_division(T, zeros, top):
                 d["state"][0, h], d["dy"][0, :, h], dS_T[0, h])
         x = chunk_model.vg_run(*args, decay_grad=True)[5]
         np.testing.assert_allclose(x, dg[0, :, h], atol=1e-9, rtol=1e-7)
+        xb = chunk_model.vg_run(*args, decay_grad="blocked")[5]
+        np.testing.assert_allclose(xb, dg[0, :, h], atol=1e-9, rtol=1e-7)
         if not zeros:
             dgl = chunk_model.vg_run(*args)[5]
             np.testing.assert_allclose(x * decay[0, :, h], dgl, atol=1e-9, rtol=1e-7)

@@ -189,3 +189,19 @@ def test_log_vector_gates_at_any_decay_size(dev, T, dtype):
     want[5] = want[5] * d["decay"]
     assert all(np.isfinite(x).all() for x in got)
     _check(got, want, bf16, bf16, f"log gates T={T} {dtype}")
+
+
+@pytest.mark.parametrize("T, chunk", [(1, 64), (65, 64), (200, 64), (700, 256)])
+def test_decays_of_any_size_on_the_chunked_form(dev, T, chunk):
+    """Per-channel decays exp(-U(0, 20)) with about 2% exact zeros, on the chunked form (pinned): d/d(decay) is formed
+    by ck_vg_dg from factors <= 1 (no division by the decay), so it holds the chunked bar against the oracle's
+    recurrence, which differentiates the decay itself, down to decays of 2e-9 and at the zeros (taken as 2^-64:
+    the gradient there differs from the one at zero by terms of that size).  chunk = 256 rebuilds each group of
+    windows in backward."""
+    d = _inputs(2, T, 2, 4, seed=800 + T, log_decay=(0.0, 20.0))
+    rng = np.random.default_rng(810 + T)
+    d["decay"] = np.where(rng.random(d["decay"].shape) < 0.02, 0.0, d["decay"]).astype(np.float32)
+    print(f"vector decays of any size bf16 T={T} chunk={chunk}, chunked form", flush=True)
+    got = _gpu(d, dev, torch.bfloat16, chunk=chunk, form="chunk")
+    assert all(np.isfinite(x).all() for x in got)
+    _check(got, _oracle(d, chunk), True, True, f"decays of any size T={T} chunk={chunk}")
