@@ -217,9 +217,9 @@ def make_inputs(w, dev, seed=0):
     beta = torch.sigmoid(n(B, T, Hv))
     A_log = torch.empty(Hv, device=dev).uniform_(0.0, float(torch.log(torch.tensor(16.0))), generator=gen)
     if w.get("vector_gate"):
-        # one log decay per key channel, [B, T, Hv, D], from the same distribution.  Many of its decays are far
-        # below 1e-4, where a decay-space gate (the reference's convention for per-channel gates,
-        # tools/gdn_vjp.py:174-179) takes the token-recurrent form for an accurate d/d(decay)
+        # one log decay per key channel, [B, T, Hv, D], from the same distribution (as decays, the reference's
+        # convention for per-channel gates, tools/gdn_vjp.py:174-179, the backward adds the pass that forms
+        # d/d(decay))
         g = -torch.exp(A_log)[:, None] * torch.nn.functional.softplus(n(B, T, Hv, D))
     else:
         g = -torch.exp(A_log) * torch.nn.functional.softplus(n(B, T, Hv))  # log decay per head

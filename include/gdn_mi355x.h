@@ -47,8 +47,8 @@ enum gdn_gate {
     GDN_GATE_LOG = 2,        /* g is the log decay, [B][T][Hv]; dg is returned w.r.t. the log decay */
     GDN_GATE_LOG_VEC = 3     /* g is a log decay per key channel, [B][T][Hv][Dk]; dg w.r.t. the log decay.  No
                               * counterpart in the reference (which takes per-channel gates as decays): the
-                              * chunked form forms dg for the log decay from suffix sums, so its d/d(decay) =
-                              * dg / decay loses accuracy below decays of about 1e-5, and its log gradient does not */
+                              * chunked form's backward is cheaper with it (dg from suffix sums, without the pass
+                              * that forms d/d(decay) for GDN_GATE_DECAY_VEC) */
 };
 
 enum gdn_form {
@@ -80,10 +80,9 @@ int64_t gdn_num_snapshots(int T, int chunk);
 /* The form a call with these arguments runs in (GDN_FORM_RECURRENT or GDN_FORM_CHUNK), or < 0 when the
  * requested form cannot run them.  gdn_fwd, gdn_bwd and the size queries resolve the form the same way: GDN_FORM_AUTO
  * picks the chunked form for Dk = Dv = 128 with a scalar gate (with a mask: Hv <= 256) or with one gate per key
- * channel (GDN_GATE_DECAY_VEC or GDN_GATE_LOG_VEC: bf16 inputs, no mask); the recurrent form otherwise.  For
- * training calls with GDN_GATE_DECAY_VEC the chunked form's dg holds to the bf16 bar for decays down to about 1e-4
- * (suffix sums of the log gradient divided by the decay): callers with smaller decays pin GDN_FORM_RECURRENT or
- * pass the log decays (GDN_GATE_LOG_VEC). */
+ * channel (GDN_GATE_DECAY_VEC or GDN_GATE_LOG_VEC: bf16 inputs, no mask); the recurrent form otherwise.  Decays
+ * of any size, zeros included, hold the same bars on both forms (the chunked form takes decays below 2^-64 as
+ * 2^-64). */
 int gdn_select_form(int Hv, int Dk, int Dv, int has_mask, int gate_kind, int form, int in_dtype);
 
 /* What `chunk` means.

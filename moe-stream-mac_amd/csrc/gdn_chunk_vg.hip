@@ -461,9 +461,10 @@ void launch_vg_prep(const Args &a, hipStream_t st) {
 //   dG_C = sum_r Kd * X2 exp... (the Kd term) + exp(G_C) rowsum(dh' * h)
 // The pair terms go through the same 16-token blocks as ck_prep_vg: below the diagonal blocks on MFMA (row role of
 // block R through the token before it, column role of block S through its last token, so both factors are <= 1;
-// every wave contracts 48 tokens in all), on the diagonal blocks elementwise.  The decay-space gradient is
-// dg_log / d.  dq | dk of the key head are summed over its value heads in the part rows (fp32), each thread reading
-// back only the elements it wrote; the last value head writes them in the gradient dtype.
+// every wave contracts 48 tokens in all), on the diagonal blocks elementwise.  With decays (not log decays) the
+// kernel leaves the pieces of d/d(decay) to ck_vg_dg instead of writing dg.  dq | dk of the key head are summed over
+// its value heads in the part rows (fp32), each thread reading back only the elements it wrote; the last value head
+// writes them in the gradient dtype.
 constexpr int VSA = C * LA * 2, VSB = D * LA * 2;  // [64][136], [128][136] bf16
 constexpr int VO_TD = 0, VO_DHH = VO_TD + VSA, VO_H = VO_DHH + VSB, VO_DLH = VO_H + VSB, VO_DLL = VO_DLH + VSA;
 constexpr int VO_DY = VO_DLL + VSA, VARENA = VO_DY + VSA;
@@ -1079,8 +1080,9 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_vg_kernel(Args a) {
 
 // ---------------------------------------------------------------------------------------------- ck_vg_dg
 //
-// d/d(decay) of per-channel decays, one workgroup per (chunk, value head), thread (block U = tid / 128, channel j)
-// for the 16 tokens u of block U (rows a..b2, bt = a - 1, G_-1 = 0, G the cumulative log decay of the chunk).
+// d/d(decay) of per-channel decays, two workgroups per (chunk, value head), each for 64 channels: thread (block
+// U = its wave, channel j) for the 16 tokens u of block U (rows a..b2, bt = a - 1, G_-1 = 0, G the cumulative log
+// decay of the chunk).
 // Every term of d/d(log decay)_u is a pair term whose span s' < u <= r straddles u and which carries the factor
 // exp(G_r - G_s'); d/d(decay)_u is that sum divided by d_u, and exp(G_r - G_s') / d_u = exp(G_r - G_u)
 // exp(G_{u-1} - G_s'), two factors <= 1.  Grouped by where r and s' lie:
@@ -1094,14 +1096,16 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_vg_kernel(Args a) {
 // B0'_S = sum_{s in S} exp(G_b2(S) - G_s) sig0_s, and M_U = sum_{r > b2, s <= bt} exp(G_r - G_b2) exp(G_bt - G_s)
 // e'_rs from the transfers Q_RS = sum_{r in R, s in S} exp(G_r - G_bt(R)) exp(G_b2(S) - G_s) e'_rs of the block
 // pairs (2, 0), (3, 0), (3, 1), which threads of blocks 0, 3 and 1 form.  Srow and Scol are scans along the block
-// (S_u = RHO_u + d_{u+1} S_{u+1}; Scol_{u+1} = d_u Scol_u + SIG_u); D4 keeps c_r(u) = sum_{s in U, s < u}
-// exp(G_{u-1} - G_s) e'_rs for the rows r of the block (c_r(u + 1) = d_u c_r(u) + e'_ru) and reads D4_u out of
-// them by Horner steps.  Decays below 2^-64 count as 2^-64 (the cumulative log decays are formed that way).
-__global__ __launch_bounds__(NTB) void ck_vg_dg_kernel(Args a) {
-    __shared__ float sP[C][C + 1], sA[C][C + 1];
+// (S_u = RHO_u + d_{u+1} S_{u+1}; Scol_{u+1} = d_u Scol_u + SIG_u), L and R running products of the decays, and D4
+// runs row by row (below).  Decays below 2^-64 count as 2^-64 (the cumulative log decays are formed that way).
+constexpr int VDW = 64, NTV = 4 * VDW;  // channels per workgroup (two workgroups per chunk-head), threads
+
+__global__ __launch_bounds__(NTV) void ck_vg_dg_kernel(Args a) {
+    constexpr int LP = C + 4;  // 16-byte rows
+    __shared__ __align__(16) float sP[C][LP], sA[C][LP];
     __shared__ float sBt[C];
-    __shared__ float sB0[4][D], sB0p[4][D], sQ[4][D];
-    const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+    __shared__ float sB0[4][VDW], sB0p[4][VDW], sQ[4][VDW];
+    const int c = blockIdx.x >> 1, hv = blockIdx.y, b = blockIdx.z;
     const int hk = hv / (a.Hv / a.Hk);
     const int t0 = c * C, n = min(C, a.T - t0);
     const size_t ci = chunk_index(a, b, hv, c);
@@ -1109,11 +1113,22 @@ __global__ __launch_bounds__(NTB) void ck_vg_dg_kernel(Args a) {
     const float *const Gc = a.w.Gv + ci * C * D;  // log2 units
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
-    const int U = tid >> 7, j = tid & (D - 1), a0 = 16 * U;
-    const size_t qk0 = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D + j, qk_row = (size_t)a.Hk * D;
+    // the block index is uniform over a wave: row offsets stay in scalar registers and every load is a scalar base
+    // plus the channel
+    const int U = __builtin_amdgcn_readfirstlane(tid / VDW), a0 = 16 * U;
+    const int jl = tid & (VDW - 1);
+    const unsigned j = (blockIdx.x & 1) * VDW + jl;
+    const size_t qk0 = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
     const bfr *const qsrc = static_cast<const bfr *>(a.q) + qk0, *const ksrc = static_cast<const bfr *>(a.k) + qk0;
+    // row r of a [C][D] fp32 tile of this chunk-head, at this channel
+    auto tile = [&](const float *base, int r) { return (base + (size_t)r * D)[j]; };
+    // q or k of row r of this channel, zero past the sequence
+    auto ld_qk = [&](const bfr *src, int r) {
+        const float x = bf2f((src + (size_t)min(r, n - 1) * qk_row)[j]);
+        return r < n ? x : 0.f;
+    };
     // the blocks of dP and dA in use: (0,0) (1,1) (2,2) (3,3) (2,0) (3,0) (3,1)
-    for (int i = tid; i < 7 * 256; i += NTB) {
+    for (int i = tid; i < 7 * 256; i += NTV) {
         const int blk = i >> 8, e = i & 255;
         const int R = blk < 4 ? blk : blk == 6 ? 3 : blk - 2, S = blk < 4 ? blk : blk == 6 ? 1 : 0;
         const int r = 16 * R + (e >> 4), s = 16 * S + (e & 15);
@@ -1124,136 +1139,167 @@ __global__ __launch_bounds__(NTB) void ck_vg_dg_kernel(Args a) {
         const float xb = a.beta[((size_t)b * a.Ts + t0 + min(tid, n - 1)) * a.Hv + hv];
         sBt[tid] = tid < n ? xb : 0.f;
     }
-    // G at the last row of each block; this block's rows
-    float gB[4], G[16];
+    // G at the last row of each block; this block's rows and decays d_i = 2^(G_i - G_{i-1})
+    float gB[4], G[16], d[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) gB[i] = Gc[(16 * i + 15) * D + j];
+    for (int i = 0; i < 4; ++i) gB[i] = tile(Gc, 16 * i + 15);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) G[i] = Gc[(a0 + i) * D + j];
+    for (int i = 0; i < 16; ++i) G[i] = tile(Gc, a0 + i);
     const float gbt = U == 0 ? 0.f : U == 1 ? gB[0] : U == 2 ? gB[1] : gB[2];
     const float gb2 = U == 0 ? gB[0] : U == 1 ? gB[1] : U == 2 ? gB[2] : gB[3];
     const float gC = gB[3];
-    // RHO, SIG of this block, and its block sums B0, B0'
-    float RHO[16], SIG[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) d[i] = ex2(G[i] - (i ? G[i - 1] : gbt));
+    // RHO, SIG of this block and its block sums B0, B0'; X = L Srow + R Scol (the K term waits for the transfers)
+    float X[16];
     {
+        float RHO[16], SIG[16];
         const float fb = ex2(gbt), fc = ex2(gC - gb2);
         float b0 = 0.f, b0p = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int o = (a0 + i) * D + j;
-            const float x0 = vgd[VGD_R0 + o], y0 = vgd[VGD_S0 + o];
+            const float x0 = tile(vgd + VGD_R0, a0 + i), y0 = tile(vgd + VGD_S0, a0 + i);
             b0 = fmaf(ex2(G[i] - gbt), x0, b0);
             b0p = fmaf(ex2(gb2 - G[i]), y0, b0p);
             RHO[i] = fb * x0;
             SIG[i] = fc * y0;
         }
-        sB0[U][j] = b0;
-        sB0p[U][j] = b0p;
+        sB0[U][jl] = b0;
+        sB0p[U][jl] = b0p;
         // the row role of block 0 and the column role of block 3 are empty
         if (U > 0) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) RHO[i] += vgd[VGD_R1 + (a0 + i) * D + j];
+            for (int i = 0; i < 16; ++i) RHO[i] += tile(vgd + VGD_R1, a0 + i);
         }
         if (U < 3) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) SIG[i] += vgd[VGD_S1 + (a0 + i) * D + j];
+            for (int i = 0; i < 16; ++i) SIG[i] += tile(vgd + VGD_S1, a0 + i);
         }
-    }
-    __syncthreads();  // dP, dA, beta staged
-    // the transfer of block pair (R, S): threads of block 0 take (2, 0), of block 3 (3, 0), of block 1 (3, 1)
-    if (U != 2) {
-        const int R = U == 0 ? 2 : 3, S = U == 1 ? 1 : 0;
-        const float gtR = R == 2 ? gB[1] : gB[2], gbS = S == 0 ? gB[0] : gB[1];
-        float kap[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int s = 16 * S + i;
-            const float ks = bf2f(ksrc[(size_t)min(s, n - 1) * qk_row]);
-            kap[i] = s < n ? ks * ex2(gbS - Gc[s * D + j]) : 0.f;
-        }
-        float acc = 0.f;
-        for (int ii = 0; ii < 16; ++ii) {
-            const int r = 16 * R + ii, rc = min(r, n - 1);
-            const float qr = bf2f(qsrc[(size_t)rc * qk_row]), kr = bf2f(ksrc[(size_t)rc * qk_row]);
-            float pp = 0.f, pa = 0.f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                pp = fmaf(sP[r][16 * S + i], kap[i], pp);
-                pa = fmaf(sA[r][16 * S + i], kap[i], pa);
-            }
-            const float x = ex2(Gc[r * D + j] - gtR) * fmaf(qr, pp, sBt[r] * kr * pa);
-            acc += r < n ? x : 0.f;
-        }
-        sQ[U][j] = acc;
-    }
-    // q, k of this block's rows (zero past the sequence)
-    float qv[16], kv[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int r = a0 + i, rc = min(r, n - 1);
-        const float xq = bf2f(qsrc[(size_t)rc * qk_row]), xk = bf2f(ksrc[(size_t)rc * qk_row]);
-        qv[i] = r < n ? xq : 0.f;
-        kv[i] = r < n ? xk : 0.f;
-    }
-    const float hdot = vgd[VGD_HD + j];
-    __syncthreads();  // block sums and transfers
-    // opaque copies of the block's boundary values: the factors below are formed anew rather than kept in registers
-    // from the block sums above
-    float gbt_ = gbt, gb2_ = gb2;
-    asm volatile("" : "+v"(gbt_), "+v"(gb2_));
-    float K;
-    {
-        float T0 = 0.f, T0p = 0.f;
-#pragma unroll
-        for (int R = 1; R < 4; ++R)
-            if (R > U) T0 = fmaf(ex2(gB[R - 1] - gb2_), sB0[R][j], T0);
-#pragma unroll
-        for (int S = 0; S < 3; ++S)
-            if (S < U) T0p = fmaf(ex2(gbt_ - gB[S]), sB0p[S][j], T0p);
-        const float M = U == 1 ? sQ[0][j] + ex2(gB[2] - gB[1]) * sQ[3][j]
-                        : U == 2 ? ex2(gB[1] - gB[0]) * sQ[3][j] + sQ[1][j] : 0.f;
-        K = M + ex2(gbt_) * T0 + ex2(gC - gb2_) * T0p + ex2(gbt_ + gC - gb2_) * hdot;
-    }
-    // the decays d[i] = 2^(G_i - G_{i-1}) along the block, L and R
-    float d[16], X[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) d[i] = ex2(G[i] - (i ? G[i - 1] : gbt_));
-    {
+        // Srow (a scan from the block's end) times L_i = exp(G_{i-1} - G_bt), then R_i Scol_i with R_i = exp(G_b2 -
+        // G_i); L and R as running products of the decays
         float S = 0.f;
 #pragma unroll
         for (int i = 15; i >= 0; --i) {
             S = i < 15 ? fmaf(d[i + 1], S, RHO[i]) : RHO[i];
-            const float L = ex2((i ? G[i - 1] : gbt_) - gbt_), Rf = ex2(gb2_ - G[i]);
-            X[i] = L * fmaf(Rf, K, S);
+            X[i] = S;
+        }
+        float L = 1.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            X[i] *= L;
+            L *= d[i];
+        }
+        float rr[16], Rf = 1.f;
+#pragma unroll
+        for (int i = 15; i >= 0; --i) {
+            rr[i] = Rf;
+            Rf *= d[i];
         }
         float Sc = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            X[i] = fmaf(ex2(gb2_ - G[i]), Sc, X[i]);
+            X[i] = fmaf(rr[i], Sc, X[i]);
             Sc = fmaf(d[i], Sc, SIG[i]);
         }
     }
-    // D4, one row r of the block at a time: c = c_r(u) = sum_{s in U, s < u} exp(G_{u-1} - G_s) e'_rs runs along
-    // u (c_r(u + 1) = d_u c_r(u) + e'_ru) and adds exp(G_r - G_u) c_r(u) to X_u for u <= r
-#pragma unroll 1
-    for (int r = 1; r < 16; ++r) {
-        const int rr = a0 + r, rc = min(rr, n - 1);
-        const float gr = Gc[rr * D + j];
-        const float xq = bf2f(qsrc[(size_t)rc * qk_row]), xk = bf2f(ksrc[(size_t)rc * qk_row]);
-        const float qr = rr < n ? xq : 0.f, bkr = rr < n ? sBt[rr] * xk : 0.f;
-        const float *const prow = &sP[rr][a0], *const arow = &sA[rr][a0];
-        float cc = 0.f;
+    const float hdot = (vgd + VGD_HD)[j];
+    __syncthreads();  // dP, dA, beta, block sums
+    // the transfer of block pair (R, S): threads of block 0 take (2, 0), of block 3 (3, 0), of block 1 (3, 1)
+    if (U != 2) {
+        const int R = U == 0 ? 2 : 3, S = U == 1 ? 1 : 0;
+        const float gtR = R == 2 ? gB[1] : gB[2], gbS = S == 0 ? gB[0] : gB[1];
+        float kap[16], qr[16], kr[16], er[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const float xu = ex2(gr - G[u]) * cc;  // past the row (u > r) the factor may overflow: not taken
-            X[u] += u <= r ? xu : 0.f;
-            const float ep = kv[u] * fmaf(prow[u], qr, bkr * arow[u]);
-            cc = fmaf(d[u], cc, u < r ? ep : 0.f);
+        for (int i = 0; i < 16; ++i) {
+            const int s = 16 * S + i, r = 16 * R + i;
+            kap[i] = ld_qk(ksrc, s) * ex2(gbS - tile(Gc, s));
+            qr[i] = ld_qk(qsrc, r);
+            kr[i] = ld_qk(ksrc, r) * sBt[r];
+            er[i] = ex2(tile(Gc, r) - gtR);
+        }
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = 16 * R + i;
+            float pp = 0.f, pa = 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                pp = fmaf(sP[r][16 * S + e], kap[e], pp);
+                pa = fmaf(sA[r][16 * S + e], kap[e], pa);
+            }
+            acc = fmaf(er[i], fmaf(qr[i], pp, kr[i] * pa), acc);
+        }
+        sQ[U][jl] = acc;
+    }
+    __syncthreads();  // transfers
+    {
+        float T0 = 0.f, T0p = 0.f;
+#pragma unroll
+        for (int R = 1; R < 4; ++R)
+            if (R > U) T0 = fmaf(ex2(gB[R - 1] - gb2), sB0[R][jl], T0);
+#pragma unroll
+        for (int S = 0; S < 3; ++S)
+            if (S < U) T0p = fmaf(ex2(gbt - gB[S]), sB0p[S][jl], T0p);
+        const float M = U == 1 ? sQ[0][jl] + ex2(gB[2] - gB[1]) * sQ[3][jl]
+                        : U == 2 ? ex2(gB[1] - gB[0]) * sQ[3][jl] + sQ[1][jl] : 0.f;
+        const float K = M + ex2(gbt) * T0 + ex2(gC - gb2) * T0p + ex2(gbt + gC - gb2) * hdot;
+        // L_i R_i = prod of the block's decays other than d_i
+        float L = 1.f, rr[16], Rf = 1.f;
+#pragma unroll
+        for (int i = 15; i >= 0; --i) {
+            rr[i] = Rf;
+            Rf *= d[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            X[i] = fmaf(L * rr[i], K, X[i]);
+            L *= d[i];
         }
     }
+    // D4, one row r of the block at a time: cs[u] = c_r(u) = sum_{s in U, s < u} exp(G_{u-1} - G_s) e'_rs
+    // (c_r(u + 1) = d_u c_r(u) + e'_ru), then X_u += exp(G_r - G_u) c_r(u) for u <= r, the factor a running product
+    // from u = r down.  Each row's LDS reads go through an address that depends on the previous row's result: the
+    // compiler would otherwise hoist the reads of every row to the start and spill.
+    {
+        float qv[16], kv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            qv[i] = ld_qk(qsrc, a0 + i);
+            kv[i] = ld_qk(ksrc, a0 + i);
+        }
+        float link = 0.f;
+#pragma unroll
+        for (int r = 1; r < 16; ++r) {
+            int ro = (a0 + r) * LP + a0;
+            asm volatile("" : "+v"(ro) : "v"(link));
+            const float *const prow = &sP[0][0] + ro, *const arow = &sA[0][0] + ro;
+            const float qr = qv[r], bkr = sBt[a0 + r] * kv[r];
+            float cs[16];
+            float cc = 0.f;
+#pragma unroll
+            for (int u = 0; u < r; ++u) {
+                const float ep = kv[u] * fmaf(prow[u], qr, bkr * arow[u]);
+                cc = fmaf(d[u], cc, ep);
+                cs[u + 1] = cc;
+            }
+            float E = 1.f;
+#pragma unroll
+            for (int u = r; u >= 1; --u) {
+                X[u] = fmaf(E, cs[u], X[u]);
+                E *= d[u];
+            }
+            link = cc;
+        }
+    }
+    // X is complete here: without this the compiler sinks the row updates into the conditional stores below and
+    // keeps every term live until then
+#pragma unroll
+    for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(X[i]));
+    float *const dgb = a.dg + (((size_t)b * a.Ts + t0 + a0) * a.Hv + hv) * D;
+    const size_t drow = (size_t)a.Hv * D;
 #pragma unroll
     for (int i = 0; i < 16; ++i)
-        if (a0 + i < n) a.dg[(((size_t)b * a.Ts + t0 + a0 + i) * a.Hv + hv) * D + j] = X[i];
+        if (a0 + i < n) (dgb + i * drow)[j] = X[i];
 }
 
 void launch_vg_local(const Args &a, hipStream_t st) {
@@ -1266,7 +1312,7 @@ void launch_vg_local(const Args &a, hipStream_t st) {
         if (dec) hipLaunchKernelGGL((ck_bwd_local_vg_kernel<false, true>), grid, dim3(NTB), 0, st, a);
         else hipLaunchKernelGGL((ck_bwd_local_vg_kernel<false, false>), grid, dim3(NTB), 0, st, a);
     }
-    if (dec) hipLaunchKernelGGL(ck_vg_dg_kernel, dim3(a.NC, a.Hv, a.B), dim3(NTB), 0, st, a);
+    if (dec) hipLaunchKernelGGL(ck_vg_dg_kernel, dim3(2 * a.NC, a.Hv, a.B), dim3(NTV), 0, st, a);
 }
 
 }  // namespace ck

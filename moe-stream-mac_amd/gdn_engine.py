@@ -156,27 +156,6 @@ def check_shapes(q, k, v, g, beta, state, mask) -> None:
         raise ValueError("mask must be [B, T]")
 
 
-# Per-channel gates on the chunked form return d/d(decay) as d/d(log decay) / decay, where d/d(log decay) comes from
-# suffix sums whose fp32 rounding is absolute: below about 1e-5 the division amplifies it past the bf16 bar (measured:
-# normalised dg error 4e-3 with decays down to 4.5e-5, 0.3 at 8e-7, inf at 0).  Training calls with decays (not log
-# decays) whose smallest decay is below this bound run the token-recurrent form, which works in decay space.  Log
-# decays (log_gate=True) need no such check: their gradient is the suffix sums themselves.
-VG_CHUNK_MIN_DECAY = 1e-4
-
-
-def _vector_decays_too_small(q, v, g, mask, log_gate) -> bool:
-    """Whether a training call that the automatic choice would put on the chunked form carries per-channel decays
-    below VG_CHUNK_MIN_DECAY (one reduction over g and a device sync, for per-channel decays only)."""
-    if g.dim() != 4 or log_gate or g.numel() == 0:
-        return False
-    lib = L.load()
-    B, T, Hk, Dk = q.shape
-    if lib.gdn_select_form(v.shape[2], Dk, v.shape[3], int(mask is not None), L.GATE_DECAY_VEC, L.FORM_AUTO,
-                           L.DTYPE_CODE[q.dtype]) != L.FORM_CHUNK:
-        return False
-    return bool(g.amin() < VG_CHUNK_MIN_DECAY)
-
-
 def default_form() -> int:
     """Form requested by default: GDN_FORM=auto|recurrent|chunk in the environment, else auto."""
     name = os.environ.get("GDN_FORM", "auto").strip().lower()
@@ -213,8 +192,6 @@ def recurrence(q, k, v, g, beta, state, mask=None, chunk: int = 64, log_gate: bo
         need_grad = grads_wanted
     form_code = default_form() if form is None else L.FORMS[form]
     pq, pk, pv, pg, pb, ps, pm = _prep(q, k, v, g, beta, state, mask)
-    if need_grad and grads_wanted and form_code == L.FORM_AUTO and _vector_decays_too_small(pq, pv, pg, pm, log_gate):
-        form_code = L.FORM_RECURRENT
     if not (need_grad and grads_wanted) and q.shape[1] == 1 and pm is None:
         # one token, no gradient: the decode step (gdn_recurrent_step's counterpart)
         with torch.no_grad():

@@ -110,8 +110,7 @@ def test_reference_vector_gate_matrix_at_d128(dev, T, masked, dtype):
 @pytest.mark.parametrize("log_decay", [(0.0, 1.5), (0.0, 6.0), (0.0, 9.0)])
 def test_strong_decays_on_the_chunked_form(dev, log_decay):
     """Decays down to exp(-9) per token: over a chunk exp(-G) reaches exp(570), beyond fp32, while every factor the
-    chunked form forms stays <= 1.  exp(-9) = 1.2e-4 is just above the smallest decay that the automatic choice
-    leaves on the chunked form for training calls (gdn_engine.VG_CHUNK_MIN_DECAY)."""
+    chunked form forms stays <= 1."""
     d = _inputs(2, 200, 2, 4, seed=11, log_decay=log_decay)
     print(f"vector gates bf16 T=200 log decays {log_decay}", flush=True)
     _check(_gpu(d, dev, torch.bfloat16), _oracle(d), True, True, f"log decay {log_decay}")
