@@ -262,13 +262,16 @@ struct Bufs {
     float *vgd;
 };
 
-// The vgd buffer of one chunk-head (fp32): the pair terms through the chunk's entry state rho0 = q * dQg -
-// beta k * Y2 and through its exit state sig0 = k * dKd, the row role through the token before the row's 16-token
-// block rho1 and the column role through the block's last token sig1 (all [C][D], before any decay factor), the
-// pair cotangents dP and dA [C][C] (only the four diagonal blocks and the blocks (2, 0), (3, 0), (3, 1) are
-// written), and <dh', h> per state row [D].
-constexpr int VGD_R0 = 0, VGD_R1 = VGD_R0 + C * D, VGD_S0 = VGD_R1 + C * D, VGD_S1 = VGD_S0 + C * D;
-constexpr int VGD_DP = VGD_S1 + C * D, VGD_DA = VGD_DP + C * C, VGD_HD = VGD_DA + C * C, VGD_FLOATS = VGD_HD + D;
+// The vgd buffer of one chunk-head (fp32), by 16-token block R (rows 16R..16R+15, bt = 16R - 1, b2 = 16R + 15):
+//   RHO [C][D]  exp(G_bt) rho0 + rho1: the pair terms through the chunk's entry state rho0 = q * dQg - beta k * Y2
+//               and the row role through the token before the row's block rho1, before their decay factors
+//   SIG [C][D]  exp(G_C - G_b2) sig0 + sig1: through the exit state sig0 = k * dKd and the column role through
+//               the block's last token sig1
+//   B0, B0P [4][D]  the block sums sum_{r in R} exp(G_r - G_bt) rho0_r and sum_{s in R} exp(G_b2 - G_s) sig0_s
+//   dP, dA [C][C]   the pair cotangents (only the four diagonal blocks and the blocks (2, 0), (3, 0), (3, 1))
+//   HD [D]      <dh', h> per state row
+constexpr int VGD_RHO = 0, VGD_SIG = VGD_RHO + C * D, VGD_B0 = VGD_SIG + C * D, VGD_B0P = VGD_B0 + 4 * D;
+constexpr int VGD_DP = VGD_B0P + 4 * D, VGD_DA = VGD_DP + C * C, VGD_HD = VGD_DA + C * C, VGD_FLOATS = VGD_HD + D;
 
 struct Args {
     const void *q, *k, *v;

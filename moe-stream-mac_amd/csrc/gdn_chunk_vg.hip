@@ -720,6 +720,16 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
     // ---- the terms through the entry state and the exit-state adjoint: dq = X1 exp(G) (in X1), dk+ =
     // -beta Y2 exp(G) (in Y2), dk- = X2 exp(G_C - G) (in X2); dbeta -= Kg . Y2; dG_C's Kd term sum_r K * dk-
     float bp[4] = {0.f, 0.f, 0.f, 0.f}, gp[4] = {0.f, 0.f, 0.f, 0.f};
+    // decays: this block's boundary values of G per channel, and the block sums of rho0 and sig0
+    float gbt[4], gb2[4], b0[4], b0p[4];
+    if constexpr (DEC) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            gbt[t] = R ? sGp[(r0 - 1) * VLGp + pc0 + t] : 0.f;
+            gb2[t] = sGp[(r0 + 15) * VLGp + pc0 + t];
+            b0[t] = b0p[t] = 0.f;
+        }
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const float be = sB[r0 + 4 * lg + e];
@@ -728,14 +738,32 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
             const float eG = ex2(Gr[e][t]), eD = ex2(gc[t] - Gr[e][t]);
             if constexpr (DEC) {
                 const int o = (r0 + 4 * lg + e) * D + 64 * ch + 16 * t + li;
-                vgd[VGD_R0 + o] = qv[e][t] * X1[t][e] - be * kv[e][t] * Y2[t][e];
-                vgd[VGD_S0 + o] = kv[e][t] * X2[t][e];
+                const float rho0 = qv[e][t] * X1[t][e] - be * kv[e][t] * Y2[t][e], sig0 = kv[e][t] * X2[t][e];
+                // the row and column roles add rho1 and sig1 to these (the same lane reads back what it wrote)
+                vgd[VGD_RHO + o] = ex2(gbt[t]) * rho0;
+                vgd[VGD_SIG + o] = ex2(gc[t] - gb2[t]) * sig0;
+                b0[t] = fmaf(ex2(Gr[e][t] - gbt[t]), rho0, b0[t]);
+                b0p[t] = fmaf(ex2(gb2[t] - Gr[e][t]), sig0, b0p[t]);
             }
             bp[e] -= kv[e][t] * eG * Y2[t][e];
             X1[t][e] *= eG;
             Y2[t][e] *= -be * eG;
             X2[t][e] *= eD;
             gp[t] += kv[e][t] * X2[t][e];
+        }
+    }
+    if constexpr (DEC) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float x = b0[t], y = b0p[t];
+            x += lane_xor16(x);
+            x += lane_xor32(x);
+            y += lane_xor16(y);
+            y += lane_xor32(y);
+            if (lg == 0) {
+                vgd[VGD_B0 + R * D + 64 * ch + 16 * t + li] = x;
+                vgd[VGD_B0P + R * D + 64 * ch + 16 * t + li] = y;
+            }
         }
     }
     f4 Z[4];
@@ -798,7 +826,7 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
             for (int e = 0; e < 4; ++e) {
                 const float eL = ex2(Gr[e][t] - gb);
                 if constexpr (DEC)
-                    vgd[VGD_R1 + (r0 + 4 * lg + e) * D + 64 * ch + 16 * t + li] =
+                    vgd[VGD_RHO + (r0 + 4 * lg + e) * D + 64 * ch + 16 * t + li] +=
                         qv[e][t] * aq[t][e] + sB[r0 + 4 * lg + e] * kv[e][t] * az[t][e];
                 X1[t][e] += aq[t][e] * eL;
                 Z[t][e] = az[t][e] * eL;
@@ -853,7 +881,7 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
             const float gb = sGp[b2 * VLGp + pc0 + t];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                if constexpr (DEC) vgd[VGD_S1 + (r0 + 4 * lg + e) * D + 64 * ch + 16 * t + li] = kv[e][t] * am[t][e];
+                if constexpr (DEC) vgd[VGD_SIG + (r0 + 4 * lg + e) * D + 64 * ch + 16 * t + li] += kv[e][t] * am[t][e];
                 X2[t][e] += am[t][e] * ex2(gb - Gr[e][t]);
             }
         }
@@ -1104,7 +1132,7 @@ __global__ __launch_bounds__(NTV) void ck_vg_dg_kernel(Args a) {
     constexpr int LP = C + 4;  // 16-byte rows
     __shared__ __align__(16) float sP[C][LP], sA[C][LP];
     __shared__ float sBt[C];
-    __shared__ float sB0[4][VDW], sB0p[4][VDW], sQ[4][VDW];
+    __shared__ float sQ[4][VDW];
     const int c = blockIdx.x >> 1, hv = blockIdx.y, b = blockIdx.z;
     const int hk = hv / (a.Hv / a.Hk);
     const int t0 = c * C, n = min(C, a.T - t0);
@@ -1150,30 +1178,14 @@ __global__ __launch_bounds__(NTV) void ck_vg_dg_kernel(Args a) {
     const float gC = gB[3];
 #pragma unroll
     for (int i = 0; i < 16; ++i) d[i] = ex2(G[i] - (i ? G[i - 1] : gbt));
-    // RHO, SIG of this block and its block sums B0, B0'; X = L Srow + R Scol (the K term waits for the transfers)
+    // X = L Srow + R Scol (the K term waits for the transfers)
     float X[16];
     {
         float RHO[16], SIG[16];
-        const float fb = ex2(gbt), fc = ex2(gC - gb2);
-        float b0 = 0.f, b0p = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float x0 = tile(vgd + VGD_R0, a0 + i), y0 = tile(vgd + VGD_S0, a0 + i);
-            b0 = fmaf(ex2(G[i] - gbt), x0, b0);
-            b0p = fmaf(ex2(gb2 - G[i]), y0, b0p);
-            RHO[i] = fb * x0;
-            SIG[i] = fc * y0;
-        }
-        sB0[U][jl] = b0;
-        sB0p[U][jl] = b0p;
-        // the row role of block 0 and the column role of block 3 are empty
-        if (U > 0) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) RHO[i] += tile(vgd + VGD_R1, a0 + i);
-        }
-        if (U < 3) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) SIG[i] += tile(vgd + VGD_S1, a0 + i);
+            RHO[i] = tile(vgd + VGD_RHO, a0 + i);
+            SIG[i] = tile(vgd + VGD_SIG, a0 + i);
         }
         // Srow (a scan from the block's end) times L_i = exp(G_{i-1} - G_bt), then R_i Scol_i with R_i = exp(G_b2 -
         // G_i); L and R as running products of the decays
@@ -1203,7 +1215,7 @@ __global__ __launch_bounds__(NTV) void ck_vg_dg_kernel(Args a) {
         }
     }
     const float hdot = (vgd + VGD_HD)[j];
-    __syncthreads();  // dP, dA, beta, block sums
+    __syncthreads();  // dP, dA, beta
     // the transfer of block pair (R, S): threads of block 0 take (2, 0), of block 3 (3, 0), of block 1 (3, 1)
     if (U != 2) {
         const int R = U == 0 ? 2 : 3, S = U == 1 ? 1 : 0;
@@ -1236,10 +1248,10 @@ __global__ __launch_bounds__(NTV) void ck_vg_dg_kernel(Args a) {
         float T0 = 0.f, T0p = 0.f;
 #pragma unroll
         for (int R = 1; R < 4; ++R)
-            if (R > U) T0 = fmaf(ex2(gB[R - 1] - gb2), sB0[R][jl], T0);
+            if (R > U) T0 = fmaf(ex2(gB[R - 1] - gb2), tile(vgd + VGD_B0, R), T0);
 #pragma unroll
         for (int S = 0; S < 3; ++S)
-            if (S < U) T0p = fmaf(ex2(gbt - gB[S]), sB0p[S][jl], T0p);
+            if (S < U) T0p = fmaf(ex2(gbt - gB[S]), tile(vgd + VGD_B0P, S), T0p);
         const float M = U == 1 ? sQ[0][jl] + ex2(gB[2] - gB[1]) * sQ[3][jl]
                         : U == 2 ? ex2(gB[1] - gB[0]) * sQ[3][jl] + sQ[1][jl] : 0.f;
         const float K = M + ex2(gbt) * T0 + ex2(gC - gb2) * T0p + ex2(gbt + gC - gb2) * hdot;

@@ -177,8 +177,9 @@ def test_saved_sizes_by_form():
     assert b"per-channel gates" in lib.gdn_last_error()
     # per-channel log decays resolve like per-channel decays and save the same tiles; on the chunked form the
     # backward of decays (not log decays) also keeps, per (value head, 64-token chunk), the pieces d/d(decay) is
-    # formed from: four fp32 [64][128] tiles, dP and dA fp32 [64][64] and one fp32 [128] row (2 x 4 heads x 5 chunks)
-    vgd = 2 * 4 * 5 * (4 * 64 * 128 + 2 * 64 * 64 + 128) * 4
+    # formed from: two fp32 [64][128] tiles, two fp32 [4][128] block sums, dP and dA fp32 [64][64] and one fp32
+    # [128] row (2 x 4 heads x 5 chunks)
+    vgd = 2 * 4 * 5 * (2 * 64 * 128 + 2 * 4 * 128 + 2 * 64 * 64 + 128) * 4
     for m, dt in ((0, L.BF16), (0, L.F32), (1, L.BF16)):
         assert (lib.gdn_select_form(32, 128, 128, m, L.GATE_LOG_VEC, L.FORM_AUTO, dt)
                 == lib.gdn_select_form(32, 128, 128, m, L.GATE_DECAY_VEC, L.FORM_AUTO, dt))
