@@ -20,6 +20,9 @@ Workloads (one GPU; the default is the T=4096 configuration the metric is quoted
                   distribution per channel, taken as log decays as the headline takes its per-head gates); the
                   chunked form with the per-channel-gate prep and local kernels (GDN_FORM=recurrent: the
                   token-recurrent form)
+  vgate_decay_bf16_b4_t4096
+                  the same gates given as decays (exp of those log decays), the reference's convention for
+                  per-channel gates: d/d(decay) adds the ck_vg_dg pass
   fwd_bf16_b4_t4096
                   the forward alone, as frozen layers and prefill run it (no autograd graph, no saved tiles),
                   bf16_b4_t4096's shape
@@ -152,6 +155,9 @@ def kernel_model(name, B, T, Hk, Hv, D, in_b):
         by = ch * (2 * dd * 4 + 2 * cd * 4 + cc * 4 + C * 8 + 4 * cd * in_b + C * 4
                    + 2 * cd * 4 + cd * in_b + 2 * C * 4)
         return f, by
+    if name == "ck_vg_dg":  # per-channel decays: reads RHO, SIG, G (fp32), the block sums, the 7 dP / dA blocks in
+        #                    use, q and k (bf16), beta and <dh', h>; writes dg (VALU work, not counted)
+        return 0, ch * (3 * cd * 4 + 8 * D * 4 + 2 * 7 * 256 * 4 + 2 * cd * 2 + C * 4 + D * 4 + cd * 4)
     if name == "rec_fwd":
         return 7 * tokh * D * D, B * T * (2 * Hk * D * in_b + Hv * D * in_b * 2 + 2 * Hv * 4)
     if name == "rec_bwd":
@@ -188,6 +194,8 @@ WORKLOADS = {
                                  masked_tail=0.1),
     "vgate_bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
                                 vector_gate=True),
+    "vgate_decay_bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
+                                      vector_gate=True, decay_gate=True),
     "fwd_bf16_b4_t4096": dict(B=4, T=4096, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.0,
                               forward_only=True),
     "decode_bf16_b64": dict(B=64, T=1, Hk=16, Hv=32, D=128, dtype="bf16", chunk=64, s0_std=0.02, decode=True),
@@ -217,10 +225,11 @@ def make_inputs(w, dev, seed=0):
     beta = torch.sigmoid(n(B, T, Hv))
     A_log = torch.empty(Hv, device=dev).uniform_(0.0, float(torch.log(torch.tensor(16.0))), generator=gen)
     if w.get("vector_gate"):
-        # one log decay per key channel, [B, T, Hv, D], from the same distribution (as decays, the reference's
-        # convention for per-channel gates, tools/gdn_vjp.py:174-179, the backward adds the pass that forms
-        # d/d(decay))
+        # one log decay per key channel, [B, T, Hv, D], from the same distribution; decay_gate: given as decays
+        # (the reference's convention for per-channel gates, tools/gdn_vjp.py:174-179)
         g = -torch.exp(A_log)[:, None] * torch.nn.functional.softplus(n(B, T, Hv, D))
+        if w.get("decay_gate"):
+            g = torch.exp(g)
     else:
         g = -torch.exp(A_log) * torch.nn.functional.softplus(n(B, T, Hv))  # log decay per head
     state = n(B, Hv, D, D) * w["s0_std"] if w["s0_std"] > 0 else torch.zeros(B, Hv, D, D, device=dev)
@@ -433,9 +442,11 @@ def main():
             mask = torch.ones(B, T, dtype=torch.bool, device=dev)
             mask[:, T - int(T * w["masked_tail"]):] = False
 
+        log_gate = not w.get("decay_gate")
+
         def step():
             y, S = gdn_engine.recurrence(x["q"], x["k"], x["v"], x["g"], x["beta"], x["state"], mask,
-                                         chunk=w["chunk"], log_gate=True, output_dtype=out_dtype)
+                                         chunk=w["chunk"], log_gate=log_gate, output_dtype=out_dtype)
             return torch.autograd.grad([y], leaves, [x["dy"]])
 
     for i in range(args.warmup):

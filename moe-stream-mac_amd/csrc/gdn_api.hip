@@ -490,7 +490,12 @@ static int ck_backward(const ChunkCall &base, int chunk, const void *saved, size
             Timed tm("ck_bwd_local", st);
             launch_chunk_stage(cc, "local", st);
         }
-        return check_launch(st, "gdn_bwd(ck_bwd_local)");
+        if ((rc = check_launch(st, "gdn_bwd(ck_bwd_local)"))) return rc;
+        if (shp.vg == 2) {
+            Timed tm("ck_vg_dg", st);
+            launch_chunk_stage(cc, "dg", st);
+        }
+        return check_launch(st, "gdn_bwd(ck_vg_dg)");
     }
     const size_t need_snap = ck_snap_bytes(B, T, Hv, W);
     if (need_snap && (!saved || saved_bytes < need_snap))
@@ -554,6 +559,11 @@ static int ck_backward(const ChunkCall &base, int chunk, const void *saved, size
             launch_chunk_stage(cc, "local", st);
         }
         if ((rc = check_launch(st, "gdn_bwd(ck_bwd_local)"))) return rc;
+        if (shp.vg == 2) {
+            Timed tm("ck_vg_dg", st);
+            launch_chunk_stage(cc, "dg", st);
+            if ((rc = check_launch(st, "gdn_bwd(ck_vg_dg)"))) return rc;
+        }
     }
     return GDN_OK;
 }

@@ -2061,6 +2061,8 @@ template <int MT>
 static void ck_bwd_launch(const ck::Args &a, hipStream_t st, const char *stage) {
     if (stage[0] == 's') {
         seq_dispatch<MT>(a, st, false);
+    } else if (stage[0] == 'd') {
+        if constexpr (MT == 2) ck::launch_vg_dg(a, st);
     } else if constexpr (MT == 2) {
         ck::launch_vg_local(a, st);
     } else if constexpr (MT == 1) {

@@ -722,6 +722,7 @@ __device__ __forceinline__ void mmar(f4 (&acc)[NTL], const bf8 *ah, const bf8 *a
 // Per-channel-gate stages of the bf16 set (gdn_chunk_vg.hip).
 void launch_vg_prep(const Args &a, hipStream_t st);
 void launch_vg_local(const Args &a, hipStream_t st);
+void launch_vg_dg(const Args &a, hipStream_t st);  // per-channel decays only: d/d(decay) after launch_vg_local
 
 }  // namespace ck
 }  // namespace gdn

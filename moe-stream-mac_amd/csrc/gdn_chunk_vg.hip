@@ -1324,7 +1324,10 @@ void launch_vg_local(const Args &a, hipStream_t st) {
         if (dec) hipLaunchKernelGGL((ck_bwd_local_vg_kernel<false, true>), grid, dim3(NTB), 0, st, a);
         else hipLaunchKernelGGL((ck_bwd_local_vg_kernel<false, false>), grid, dim3(NTB), 0, st, a);
     }
-    if (dec) hipLaunchKernelGGL(ck_vg_dg_kernel, dim3(2 * a.NC, a.Hv, a.B), dim3(NTV), 0, st, a);
+}
+
+void launch_vg_dg(const Args &a, hipStream_t st) {
+    if (a.gate == GATE_DECAY_VEC) hipLaunchKernelGGL(ck_vg_dg_kernel, dim3(2 * a.NC, a.Hv, a.B), dim3(NTV), 0, st, a);
 }
 
 }  // namespace ck
