@@ -204,3 +204,15 @@ def test_decays_of_any_size_on_the_chunked_form(dev, T, chunk):
     got = _gpu(d, dev, torch.bfloat16, chunk=chunk, form="chunk")
     assert all(np.isfinite(x).all() for x in got)
     _check(got, _oracle(d, chunk), True, True, f"decays of any size T={T} chunk={chunk}")
+
+
+@pytest.mark.parametrize("Hk, Hv", [(4, 4), (1, 4)])
+def test_decays_on_the_chunked_form_across_head_groupings(dev, Hk, Hv):
+    """Per-channel decays with 2% zeros on the chunked form at one and four value heads per key head: ck_vg_dg reads
+    q and k through the key head of each value head, and ck_bwd_local_vg sums dq and dk over a key head's value
+    heads."""
+    d = _inputs(2, 130, Hk, Hv, seed=830 + Hk, log_decay=(0.0, 6.0))
+    rng = np.random.default_rng(840 + Hk)
+    d["decay"] = np.where(rng.random(d["decay"].shape) < 0.02, 0.0, d["decay"]).astype(np.float32)
+    print(f"vector decays bf16 T=130 Hk={Hk} Hv={Hv}, chunked form", flush=True)
+    _check(_gpu(d, dev, torch.bfloat16, form="chunk"), _oracle(d), True, True, f"decays Hk={Hk} Hv={Hv}")
