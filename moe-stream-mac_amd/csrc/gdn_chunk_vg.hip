@@ -1108,7 +1108,8 @@ __global__ __launch_bounds__(NTB) void ck_bwd_local_vg_kernel(Args a) {
 
 // ---------------------------------------------------------------------------------------------- ck_vg_dg
 //
-// d/d(decay) of per-channel decays, two workgroups per (chunk, value head), each for 64 channels: thread (block
+// d/d(decay) of per-channel decays (the vector dg of tools/gdn_vjp.py:311-314, for the decay S * d of :174-179),
+// two workgroups per (chunk, value head), each for 64 channels: thread (block
 // U = its wave, channel j) for the 16 tokens u of block U (rows a..b2, bt = a - 1, G_-1 = 0, G the cumulative log
 // decay of the chunk).
 // Every term of d/d(log decay)_u is a pair term whose span s' < u <= r straddles u and which carries the factor
