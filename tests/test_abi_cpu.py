@@ -71,6 +71,14 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert need > 0 and lib.gdn_bwd_workspace_bytes(1, 4, 1, 1, 8, 8, 0, 0, 0, 0, 0) == 0
     rc = lib.gdn_bwd(*([fake] * 8), 0, *([fake] * 9), need - 1, 1, 4, 1, 1, 8, 8, 64, 0, 0, 0, 0, 0, null)
     assert rc == gdn_lib.GDN_ERR_WORKSPACE
+    # per-channel decays on the chunked form need the d/d(decay) buffers beyond what log decays need
+    L = gdn_lib
+    ws_log = lib.gdn_bwd_workspace_bytes(2, 300, 2, 4, 128, 128, 64, L.GATE_LOG_VEC, 0, L.FORM_CHUNK, L.BF16)
+    ws_dec = lib.gdn_bwd_workspace_bytes(2, 300, 2, 4, 128, 128, 64, L.GATE_DECAY_VEC, 0, L.FORM_CHUNK, L.BF16)
+    assert ws_dec > ws_log > 0
+    rc = lib.gdn_bwd(*([fake] * 6), null, fake, 1 << 40, fake, null, *([fake] * 6), fake, ws_log, 2, 300, 2, 4, 128,
+                     128, 64, L.BF16, L.BF16, L.BF16, L.GATE_DECAY_VEC, L.FORM_CHUNK, null)
+    assert rc == L.GDN_ERR_WORKSPACE and b"workspace of" in lib.gdn_last_error()
     # bf16 inputs with an fp16 cotangent cannot run on the chunked form (its kernels read bf16 or fp32 dy)
     rc = lib.gdn_bwd(*([fake] * 6), null, fake, 1 << 40, *([fake] * 9), 1 << 40, 1, 4, 1, 1, 128, 128, 64, 1, 2,
                      1, 2, gdn_lib.FORM_CHUNK, null)
