@@ -1179,6 +1179,17 @@ __global__ __launch_bounds__(NTV) void ck_vg_dg_kernel(Args a) {
     const float gC = gB[3];
 #pragma unroll
     for (int i = 0; i < 16; ++i) d[i] = ex2(G[i] - (i ? G[i - 1] : gbt));
+    float qv[16], kv[16], B0[4], B0P[4];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        qv[i] = ld_qk(qsrc, a0 + i);
+        kv[i] = ld_qk(ksrc, a0 + i);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        B0[i] = tile(vgd + VGD_B0, i);
+        B0P[i] = tile(vgd + VGD_B0P, i);
+    }
     // X = L Srow + R Scol (the K term waits for the transfers)
     float X[16];
     {
@@ -1249,10 +1260,10 @@ __global__ __launch_bounds__(NTV) void ck_vg_dg_kernel(Args a) {
         float T0 = 0.f, T0p = 0.f;
 #pragma unroll
         for (int R = 1; R < 4; ++R)
-            if (R > U) T0 = fmaf(ex2(gB[R - 1] - gb2), tile(vgd + VGD_B0, R), T0);
+            if (R > U) T0 = fmaf(ex2(gB[R - 1] - gb2), B0[R], T0);
 #pragma unroll
         for (int S = 0; S < 3; ++S)
-            if (S < U) T0p = fmaf(ex2(gbt - gB[S]), tile(vgd + VGD_B0P, S), T0p);
+            if (S < U) T0p = fmaf(ex2(gbt - gB[S]), B0P[S], T0p);
         const float M = U == 1 ? sQ[0][jl] + ex2(gB[2] - gB[1]) * sQ[3][jl]
                         : U == 2 ? ex2(gB[1] - gB[0]) * sQ[3][jl] + sQ[1][jl] : 0.f;
         const float K = M + ex2(gbt) * T0 + ex2(gC - gb2) * T0p + ex2(gbt + gC - gb2) * hdot;
@@ -1274,12 +1285,6 @@ __global__ __launch_bounds__(NTV) void ck_vg_dg_kernel(Args a) {
     // from u = r down.  Each row's LDS reads go through an address that depends on the previous row's result: the
     // compiler would otherwise hoist the reads of every row to the start and spill.
     {
-        float qv[16], kv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            qv[i] = ld_qk(qsrc, a0 + i);
-            kv[i] = ld_qk(ksrc, a0 + i);
-        }
         float link = 0.f;
 #pragma unroll
         for (int r = 1; r < 16; ++r) {
