@@ -216,3 +216,52 @@ def test_decays_on_the_chunked_form_across_head_groupings(dev, Hk, Hv):
     d["decay"] = np.where(rng.random(d["decay"].shape) < 0.02, 0.0, d["decay"]).astype(np.float32)
     print(f"vector decays bf16 T=130 Hk={Hk} Hv={Hv}, chunked form", flush=True)
     _check(_gpu(d, dev, torch.bfloat16, form="chunk"), _oracle(d), True, True, f"decays Hk={Hk} Hv={Hv}")
+
+
+def _abi_vg(d, dev, chunk, fwd_ws_T=None, bwd_ws_T=None):
+    """Forward + backward of per-channel decays (bf16) through the C ABI, with the forward / backward workspaces
+    sized for fwd_ws_T / bwd_ws_T tokens (fewer tokens than T force smaller groups of windows)."""
+    import gdn_lib as L
+    lib = L.load()
+    B, T, Hk = d["q"].shape[:3]
+    Hv = d["v"].shape[2]
+    t = lambda x, dt=torch.float32: torch.tensor(np.asarray(x), device=dev, dtype=dt).contiguous()
+    q, k, v, dy = (t(d[n], torch.bfloat16) for n in ("q", "k", "v", "dy"))
+    g, beta, S0, dS_T = (t(d[n]) for n in ("decay", "beta", "state", "dS_T"))
+    y = torch.empty((B, T, Hv, D), device=dev, dtype=torch.bfloat16)
+    ST = torch.empty((B, Hv, D, D), device=dev)
+    common = (D, D, chunk, L.GATE_DECAY_VEC, 0, L.FORM_CHUNK, L.BF16)
+    n_saved = lib.gdn_saved_bytes(B, T, Hk, Hv, *common)
+    saved = torch.empty(max(n_saved, 1), device=dev, dtype=torch.uint8)
+    n_fws = lib.gdn_fwd_workspace_bytes(B, fwd_ws_T or T, Hk, Hv, *common, 1)
+    fws = torch.empty(max(n_fws, 1), device=dev, dtype=torch.uint8)
+    L.check(lib.gdn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), S0.data_ptr(),
+                        None, y.data_ptr(), ST.data_ptr(), saved.data_ptr(), n_saved, fws.data_ptr(), n_fws,
+                        B, T, Hk, Hv, D, D, chunk, L.BF16, L.BF16, L.GATE_DECAY_VEC, L.FORM_CHUNK, None))
+    outs = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), torch.empty_like(g),
+            torch.empty_like(beta), torch.empty_like(S0)]
+    n_bws = lib.gdn_bwd_workspace_bytes(B, bwd_ws_T or T, Hk, Hv, *common)
+    bws = torch.empty(max(n_bws, 1), device=dev, dtype=torch.uint8)
+    L.check(lib.gdn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), S0.data_ptr(),
+                        None, saved.data_ptr(), n_saved, dy.data_ptr(), dS_T.data_ptr(),
+                        *(o.data_ptr() for o in outs), bws.data_ptr(), n_bws, B, T, Hk, Hv, D, D, chunk,
+                        L.BF16, L.BF16, L.BF16, L.GATE_DECAY_VEC, L.FORM_CHUNK, None))
+    torch.cuda.synchronize()
+    return [x.float().cpu().numpy() for x in (y, ST, *outs)]
+
+
+def test_decays_checkpointed_in_groups_of_windows(dev):
+    """Per-channel decays with 2% zeros, chunk = 100 (windows of 128 tokens) over T = 700, through the C ABI: the
+    backward in groups of one and of three windows (forced by small workspaces, each group with its own d/d(decay)
+    buffers) gives the same results as one group, and that matches the fp64 oracle."""
+    d = _inputs(2, 700, 2, 4, seed=850, log_decay=(0.0, 6.0))
+    rng = np.random.default_rng(851)
+    d["decay"] = np.where(rng.random(d["decay"].shape) < 0.02, 0.0, d["decay"]).astype(np.float32)
+    print("vector decays bf16 T=700 chunk=100, groups of windows", flush=True)
+    one = _abi_vg(d, dev, 100)
+    for fT, bT in ((128, 128), (256, 384)):
+        print(f"  forward groups of {fT} tokens, backward groups of {bT}", flush=True)
+        got = _abi_vg(d, dev, 100, fwd_ws_T=fT, bwd_ws_T=bT)
+        for n, a, w in zip(NAMES, got, one):
+            assert nerr(a, w) <= 1e-6, (fT, bT, n, nerr(a, w))
+    _check(one, _oracle(d, 100), True, True, "decays ckpt groups")
