@@ -504,6 +504,16 @@ def main():
         # every kernel's modelled bytes per launch over its own average launch time
         "kernels_gbs": {n: round(kernel_model(n, B, T, Hk, Hv, D, in_b)[1] / (v[0] / v[1] * 1e-3) / 1e9, 1)
                         for n, v in kt.items() if kernel_model(n, B, T, Hk, Hv, D, in_b)[1]}})
+    # each kernel's own share of the step's algorithmic flops (split in proportion to the implementation model's
+    # flops of the kernels) over that kernel's own time, against the same flop peak; `frac` above charges the
+    # whole step's work to the dominant kernel alone
+    kf = {n: kernel_model(n, B, T, Hk, Hv, D, in_b)[0] for n in kt}
+    kf_sum = sum(kf.values())
+    if kf_sum and "block" not in w and "ops" not in w:
+        algo_step = sum(a_flops.values()) * tokens
+        roofline["kernels_own_share_flop_frac"] = {
+            n: round(algo_step * f / kf_sum / (kt[n][0] / args.steps * 1e-3) / (a_peak * 1e12), 4)
+            for n, f in kf.items() if f}
     if "block" in w:
         lib_ms = sum(v[0] for v in kt.values()) / args.steps
         roofline["outside_library_ms_per_step"] = round(elapsed / args.steps * 1e3 - lib_ms, 4)
