@@ -270,6 +270,8 @@ struct Bufs {
 //   B0, B0P [4][D]  the block sums sum_{r in R} exp(G_r - G_bt) rho0_r and sum_{s in R} exp(G_b2 - G_s) sig0_s
 //   dP, dA [C][C]   the pair cotangents (only the four diagonal blocks and the blocks (2, 0), (3, 0), (3, 1))
 //   HD [D]      <dh', h> per state row
+// The columns of RHO, SIG, B0 and B0P are in the permuted order of ck_bwd_local_vg's lanes: channel j at column
+// (j & ~63) + 4 (j & 15) + ((j >> 4) & 3), so that each lane's four channels are one 16-byte piece.
 constexpr int VGD_RHO = 0, VGD_SIG = VGD_RHO + C * D, VGD_B0 = VGD_SIG + C * D, VGD_B0P = VGD_B0 + 4 * D;
 constexpr int VGD_DP = VGD_B0P + 4 * D, VGD_DA = VGD_DP + C * C, VGD_HD = VGD_DA + C * C, VGD_FLOATS = VGD_HD + D;
 

@@ -733,15 +733,14 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const float be = sB[r0 + 4 * lg + e];
+        float rv[4], sv[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const float eG = ex2(Gr[e][t]), eD = ex2(gc[t] - Gr[e][t]);
             if constexpr (DEC) {
-                const int o = (r0 + 4 * lg + e) * D + 64 * ch + 16 * t + li;
                 const float rho0 = qv[e][t] * X1[t][e] - be * kv[e][t] * Y2[t][e], sig0 = kv[e][t] * X2[t][e];
-                // the row and column roles add rho1 and sig1 to these (the same lane reads back what it wrote)
-                vgd[VGD_RHO + o] = ex2(gbt[t]) * rho0;
-                vgd[VGD_SIG + o] = ex2(gc[t] - gb2[t]) * sig0;
+                rv[t] = ex2(gbt[t]) * rho0;
+                sv[t] = ex2(gc[t] - gb2[t]) * sig0;
                 b0[t] = fmaf(ex2(Gr[e][t] - gbt[t]), rho0, b0[t]);
                 b0p[t] = fmaf(ex2(gb2[t] - Gr[e][t]), sig0, b0p[t]);
             }
@@ -750,6 +749,13 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
             Y2[t][e] *= -be * eG;
             X2[t][e] *= eD;
             gp[t] += kv[e][t] * X2[t][e];
+        }
+        if constexpr (DEC) {
+            // the lane's four channels, in the permuted column order of the vgd tiles; the row and column roles add
+            // rho1 and sig1 to these (the same lane reads back what it wrote)
+            const int o = (r0 + 4 * lg + e) * D + pc0;
+            *reinterpret_cast<float4 *>(vgd + VGD_RHO + o) = make_float4(rv[0], rv[1], rv[2], rv[3]);
+            *reinterpret_cast<float4 *>(vgd + VGD_SIG + o) = make_float4(sv[0], sv[1], sv[2], sv[3]);
         }
     }
     if constexpr (DEC) {
@@ -760,10 +766,12 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
             x += lane_xor32(x);
             y += lane_xor16(y);
             y += lane_xor32(y);
-            if (lg == 0) {
-                vgd[VGD_B0 + R * D + 64 * ch + 16 * t + li] = x;
-                vgd[VGD_B0P + R * D + 64 * ch + 16 * t + li] = y;
-            }
+            b0[t] = x;
+            b0p[t] = y;
+        }
+        if (lg == 0) {
+            *reinterpret_cast<float4 *>(vgd + VGD_B0 + R * D + pc0) = make_float4(b0[0], b0[1], b0[2], b0[3]);
+            *reinterpret_cast<float4 *>(vgd + VGD_B0P + R * D + pc0) = make_float4(b0p[0], b0p[1], b0p[2], b0p[3]);
         }
     }
     f4 Z[4];
@@ -819,15 +827,25 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
                 az[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(zh, yl, az[t], 0, 0, 0);
             }
         }
+        if constexpr (DEC) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float be = sB[r0 + 4 * lg + e];
+                float4 *const p4 = reinterpret_cast<float4 *>(vgd + VGD_RHO + (r0 + 4 * lg + e) * D + pc0);
+                float4 x = *p4;
+                x.x += qv[e][0] * aq[0][e] + be * kv[e][0] * az[0][e];
+                x.y += qv[e][1] * aq[1][e] + be * kv[e][1] * az[1][e];
+                x.z += qv[e][2] * aq[2][e] + be * kv[e][2] * az[2][e];
+                x.w += qv[e][3] * aq[3][e] + be * kv[e][3] * az[3][e];
+                *p4 = x;
+            }
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const float gb = sGp[bt * VLGp + pc0 + t];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float eL = ex2(Gr[e][t] - gb);
-                if constexpr (DEC)
-                    vgd[VGD_RHO + (r0 + 4 * lg + e) * D + 64 * ch + 16 * t + li] +=
-                        qv[e][t] * aq[t][e] + sB[r0 + 4 * lg + e] * kv[e][t] * az[t][e];
                 X1[t][e] += aq[t][e] * eL;
                 Z[t][e] = az[t][e] * eL;
             }
@@ -876,12 +894,23 @@ __device__ __forceinline__ void bwd_local_vg_head(const Args &a, int c, int hk, 
                 am[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(zh, kl, am[t], 0, 0, 0);
             }
         }
+        if constexpr (DEC) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float4 *const p4 = reinterpret_cast<float4 *>(vgd + VGD_SIG + (r0 + 4 * lg + e) * D + pc0);
+                float4 x = *p4;
+                x.x += kv[e][0] * am[0][e];
+                x.y += kv[e][1] * am[1][e];
+                x.z += kv[e][2] * am[2][e];
+                x.w += kv[e][3] * am[3][e];
+                *p4 = x;
+            }
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const float gb = sGp[b2 * VLGp + pc0 + t];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                if constexpr (DEC) vgd[VGD_SIG + (r0 + 4 * lg + e) * D + 64 * ch + 16 * t + li] += kv[e][t] * am[t][e];
                 X2[t][e] += am[t][e] * ex2(gb - Gr[e][t]);
             }
         }
@@ -1149,8 +1178,11 @@ __global__ __launch_bounds__(NTV) void ck_vg_dg_kernel(Args a) {
     const unsigned j = (blockIdx.x & 1) * VDW + jl;
     const size_t qk0 = (((size_t)b * a.Ts + t0) * a.Hk + hk) * D, qk_row = (size_t)a.Hk * D;
     const bfr *const qsrc = static_cast<const bfr *>(a.q) + qk0, *const ksrc = static_cast<const bfr *>(a.k) + qk0;
-    // row r of a [C][D] fp32 tile of this chunk-head, at this channel
+    // row r of a [C][D] fp32 tile of this chunk-head, at this channel; tile_p: of the vgd tiles, whose columns are
+    // in the permuted order of ck_bwd_local_vg's lanes (pcol)
     auto tile = [&](const float *base, int r) { return (base + (size_t)r * D)[j]; };
+    const unsigned jp = pcol(j);
+    auto tile_p = [&](const float *base, int r) { return (base + (size_t)r * D)[jp]; };
     // q or k of row r of this channel, zero past the sequence
     auto ld_qk = [&](const bfr *src, int r) {
         const float x = bf2f((src + (size_t)min(r, n - 1) * qk_row)[j]);
@@ -1187,8 +1219,8 @@ __global__ __launch_bounds__(NTV) void ck_vg_dg_kernel(Args a) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        B0[i] = tile(vgd + VGD_B0, i);
-        B0P[i] = tile(vgd + VGD_B0P, i);
+        B0[i] = tile_p(vgd + VGD_B0, i);
+        B0P[i] = tile_p(vgd + VGD_B0P, i);
     }
     // X = L Srow + R Scol (the K term waits for the transfers)
     float X[16];
@@ -1196,8 +1228,8 @@ __global__ __launch_bounds__(NTV) void ck_vg_dg_kernel(Args a) {
         float RHO[16], SIG[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            RHO[i] = tile(vgd + VGD_RHO, a0 + i);
-            SIG[i] = tile(vgd + VGD_SIG, a0 + i);
+            RHO[i] = tile_p(vgd + VGD_RHO, a0 + i);
+            SIG[i] = tile_p(vgd + VGD_SIG, a0 + i);
         }
         // Srow (a scan from the block's end) times L_i = exp(G_{i-1} - G_bt), then R_i Scol_i with R_i = exp(G_b2 -
         // G_i); L and R as running products of the decays
