@@ -817,11 +817,11 @@ static_assert(O_STQ + 8 * 16 * LQ * 4 <= ARENA, "dq staging fits");
 static_assert(O_SM + C * LDC * 4 <= ARENA && O_MT + SZ_D <= O_QT, "S6 tiles fit, clear of K^T");
 static_assert(C * (D + 4) * 4 <= O_KT, "dk staging below K^T and the pair matrix");
 
-constexpr int NQR = 2;  // dq row pieces per thread whose running sum stays in registers (of four)
+constexpr int NQR = 4;  // dq row pieces per thread whose running sum stays in registers (of four: all of them)
 
 // One value head hv = hk * rep + rr of key head hk.  dq | dk of the key head: the value heads' fp32 parts are summed
 // in order (rr = 0, 1, ...) at the 16-byte row pieces each thread writes out: dk (ck) and the first NQR dq pieces
-// (cq) in registers, the other dq pieces in the part rows of the key head (each thread reading back only the
+// (cq) in registers, any other dq pieces in the part rows of the key head (each thread reading back only the
 // elements it wrote itself); the last value head writes dq and dk in the gradient dtype.
 template <bool DYF32>
 __device__ __forceinline__ void bwd_local_bf16_head(const Args &a, int c, int hk, int b, int rr, int rep,
@@ -1200,7 +1200,7 @@ template <bool DYF32>
 __global__ __launch_bounds__(NTB) void ck_bwd_local_bf16_kernel(Args a) {
     typedef const __attribute__((address_space(4))) Args *KArgs;  // the kernel arguments (constant memory)
     const int rep = a.Hv / a.Hk;
-    float4 ck[4], cq[NQR];  // the running dk sum and part of the running dq sum of the value heads done so far
+    float4 ck[4], cq[NQR];  // the running dk and dq sums of the value heads done so far
     static_assert(C * D / 4 / NTB == 4, "four dk row pieces per thread");
     for (int rr = 0; rr < rep; ++rr) {
         // the arguments are read anew for each value head instead of being held in scalar registers across it
@@ -1949,7 +1949,8 @@ ChunkSizes chunk_sizes(int B, int T, int Hk, int Hv, bool bf16, bool bwd, int vg
     off = 0;
     put(s.dH, n * dd * (bf16 ? 2 : 4));
     put(s.dDl, n * cd * 4);                    // fp32 dDelta, or TdD = T^T dDelta (bf16 set)
-    put(s.part, (size_t)B * T * (bf16 ? Hk : Hv) * 2 * CK_D * 4);
+    // the bf16 set with one gate per head keeps its whole running dq | dk sum in registers (NQR of four pieces)
+    put(s.part, bf16 && !vg && ck::NQR == 4 ? 0 : (size_t)B * T * (bf16 ? Hk : Hv) * 2 * CK_D * 4);
     put(s.vgd, vgd ? n * ck::VGD_FLOATS * 4 : 0);
     s.work = off;
     return s;

@@ -241,9 +241,10 @@ struct Bufs {
     float *Dl;   // [B][Hv][NC][C][D]  Delta
     float *dH;   // [B][Hv][NC][D][D]  adjoint of each chunk's exit state, [j][i] like H (bf16 in the bf16 path)
     float *dDl;  // [B][Hv][NC][C][D]  dDelta (bf16 path: TdD = T^T dDelta, fp32)
-    float *part; // [B][T][Hv][2][D]   ck_bwd_local scratch: the running dq | dk sum of a key head (bf16 set: in the
-                 // rows [B][T][Hk][2][D]; fp32 set: in the slot of the key head's first value head, the other slots
-                 // parking each value head's dW)
+    float *part; // [B][T][Hv][2][D]   ck_bwd_local scratch: the running dq | dk sum of a key head (per-channel
+                 // gates: in the rows [B][T][Hk][2][D]; fp32 set: in the slot of the key head's first value head, the
+                 // other slots parking each value head's dW; the bf16 set with one gate per head keeps the sum in
+                 // registers and has no part buffer)
     // bf16 operand tiles written by ck_prep for the bf16 sequential kernels (raw bf16 bits), each [M][K] tile in
     // fragment order (frag_off<K>); the bf16 set keeps U in accumulator order (acc_off)
     unsigned short *Wb;   // [B][Hv][NC][C][D]     W
