@@ -115,7 +115,7 @@ def roof(nbytes, flops, peak_tflops, seconds):
             "frac": round(f_fl, 4), "other_roof_frac": round(f_hbm, 4)}
 
 
-def kernel_model(name, B, T, Hk, Hv, D, in_b):
+def kernel_model(name, B, T, Hk, Hv, D, in_b, fwd_only=False):
     """Implementation model of one launch of a kernel: (flops, HBM bytes) from what this implementation's kernel
     reads and writes, saved tiles included (recompute and padding excluded).  Chunk kernels: per (head, 64-token
     chunk); recurrent kernels: per head-token state element.  Reported beside the roofline, never as it."""
@@ -130,15 +130,20 @@ def kernel_model(name, B, T, Hk, Hv, D, in_b):
         if bf:  # reads q, k (per key head), v, g, beta; writes G, T (fp32), P and P^T (hi / lo), W, -W^T, K~^T, U
             #     (fp32) and Q^T (per key head)
             kv = Hk / Hv
-            return f, ch * (2 * cd * 2 * kv + cd * 2 + 2 * C * 4 + C * 8 + cc * 4 + 4 * cc * 2 + 3 * cd * 2
-                            + cd * 2 * kv + cd * 4)
-        return f, ch * (3 * cd * in_b + 2 * C * 4 + 2 * cd * 4 + 2 * cc * 4 + C * 8)
+            by = ch * (2 * cd * 2 * kv + cd * 2 + 2 * C * 4 + C * 8 + cc * 4 + 4 * cc * 2 + 3 * cd * 2
+                       + cd * 2 * kv + cd * 4)
+            # a forward-only call writes none of the backward's tiles: T, P^T, -W^T, Q^T
+            return f, by - (ch * (cc * 4 + 2 * cc * 2 + cd * 2 + cd * 2 * kv) if fwd_only else 0)
+        return f, ch * (3 * cd * in_b + 2 * C * 4 + 2 * cd * 4 + 2 * cc * 4 + C * 8) - (ch * cc * 4 if fwd_only else 0)
     if name in ("ck_fwd", "ck_bwd_seq"):
         f = ch * (3 * 2 * cd * D + 2 * cc * D)
         if name == "ck_fwd":
+            # a forward-only call saves neither h nor Delta
             if bf:  # reads W, Q, K~^T, P (hi / lo), U, G; writes h (bf16), Delta (fp32), y
-                return f, ch * (3 * cd * 2 + 2 * cc * 2 + cd * 4 + C * 8 + dd * 2 + cd * 4 + cd * 2)
-            return f, ch * (2 * cd * 4 + cc * 4 + 2 * cd * in_b + C * 8 + dd * 4 + cd * 4 + cd * in_b)
+                saved = 0 if fwd_only else dd * 2 + cd * 4
+                return f, ch * (3 * cd * 2 + 2 * cc * 2 + cd * 4 + C * 8 + saved + cd * 2)
+            saved = 0 if fwd_only else dd * 4 + cd * 4
+            return f, ch * (2 * cd * 4 + cc * 4 + 2 * cd * in_b + C * 8 + saved + cd * in_b)
         f += ch * 2 * cc * D  # TdD = T^T dDelta
         if bf:  # reads K, P^T (hi / lo), Q^T, -W^T, T^T (hi / lo), dY, G; writes dh' (bf16), TdD (fp32)
             return f, ch * (cd * 2 + 2 * cc * 2 + 2 * cd * 2 + 2 * cc * 2 + cd * 2 + C * 8 + dd * 2 + cd * 4)
@@ -472,6 +477,7 @@ def main():
     ms, cnt = kt[dom]
     avg_ms = ms / cnt
     in_b = 2 if w["dtype"] == "bf16" else 4
+    km = lambda n: kernel_model(n, B, T, Hk, Hv, D, in_b, fwd_only=bool(w.get("forward_only")))
     step_s = elapsed / args.steps
     form = "chunk" if any(n.startswith("ck_") for n in kt) else "recurrent"
     a_bytes, a_flops, a_peak = algo_model(w, form)
@@ -480,7 +486,7 @@ def main():
     launch_tokens = tokens * args.steps / cnt
     if "ops" in w:
         # streaming kernels: the bytes the launch must read and write, against the HBM roof
-        a_bytes, a_flops = kernel_model(dom, B, T, Hk, Hv, D, in_b)[1] / tokens, {"none": 0}
+        a_bytes, a_flops = km(dom)[1] / tokens, {"none": 0}
     roofline = roof(a_bytes * launch_tokens, sum(a_flops.values()) * launch_tokens, a_peak, avg_ms * 1e-3)
     traffic = None
     tj = ROOT / "profiles" / "traffic.json"
@@ -488,7 +494,10 @@ def main():
         rec = json.loads(tj.read_text()).get(args.workload, {}).get(dom)
         if rec:
             traffic = rec["read_bytes"] + rec["write_bytes"]
-    i_flops, i_bytes = kernel_model(dom, B, T, Hk, Hv, D, in_b)
+    # the implementation model of a chunk kernel covers the whole batch once; a call that runs group-wise launches
+    # it several times per step, each launch over its share (a masked call's two passes each cover the whole batch)
+    per_step = lambda n: kt[n][1] / args.steps / (2 if w.get("masked_tail") else 1) if n.startswith("ck_") else 1
+    i_flops, i_bytes = (int(x / per_step(dom)) for x in km(dom))
     roofline.update({
         "traffic": traffic, "traffic_source": "profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE)"
         if traffic else None, "kernel": dom, "avg_launch_ms": round(avg_ms, 4),
@@ -502,12 +511,12 @@ def main():
                                  "hbm_frac": round(i_bytes / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
         "kernels_ms_per_step": {n: round(v[0] / args.steps, 4) for n, v in kt.items()},
         # every kernel's modelled bytes per launch over its own average launch time
-        "kernels_gbs": {n: round(kernel_model(n, B, T, Hk, Hv, D, in_b)[1] / (v[0] / v[1] * 1e-3) / 1e9, 1)
-                        for n, v in kt.items() if kernel_model(n, B, T, Hk, Hv, D, in_b)[1]}})
+        "kernels_gbs": {n: round(km(n)[1] / per_step(n) / (v[0] / v[1] * 1e-3) / 1e9, 1)
+                        for n, v in kt.items() if km(n)[1]}})
     # each kernel's own share of the step's algorithmic flops (split in proportion to the implementation model's
     # flops of the kernels) over that kernel's own time, against the same flop peak; `frac` above charges the
     # whole step's work to the dominant kernel alone
-    kf = {n: kernel_model(n, B, T, Hk, Hv, D, in_b)[0] for n in kt}
+    kf = {n: km(n)[0] for n in kt}
     kf_sum = sum(kf.values())
     if kf_sum and "block" not in w and "ops" not in w:
         algo_step = sum(a_flops.values()) * tokens
